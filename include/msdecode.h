@@ -1,0 +1,93 @@
+/* C ABI of the MI355X fused whole-model decode step (libmsdecode.so, gfx950).
+ *
+ * Every entry point takes plain device pointers and sizes, runs on the caller's
+ * HIP stream and returns 0 on success or a negative MSD_E* code.  Nothing here
+ * allocates device memory: buffers are sized with the msd_*_bytes/elems
+ * queries and owned by the caller.
+ *
+ * Reference interfaces replaced (zahlmann/transformer):
+ *   msd_decode_step       <- kernels/multi_sm_decode.py:369-432
+ *                            multi_sm_decode_nlayer(w, config, token_id, pos, kv_packed)
+ *                            and its launch jt.triton_call(_multi_sm_decode, ...) at :402-430
+ *   msd_packed_weight_elems, msd_workspace_bytes
+ *                         <- the packed_w size implied by kernels/fused_decode_nlayer.py:250-270
+ *                            and the workspace layout of kernels/multi_sm_decode.py:390-400
+ */
+#ifndef MSDECODE_H
+#define MSDECODE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Model shape; same keys as the reference config dict (model.py:37-47). */
+typedef struct msd_config {
+  int32_t vocab_size;
+  int32_t d_model;
+  int32_t n_heads;
+  int32_t n_kv_heads;
+  int32_t n_layers;
+  int32_t d_head;
+  int32_t d_ff;
+  int32_t context_len;
+} msd_config;
+
+enum {
+  MSD_OK = 0,
+  MSD_E_CONFIG = -1,      /* unsupported or inconsistent shape */
+  MSD_E_ARG = -2,         /* null pointer, misaligned buffer, token/pos out of range */
+  MSD_E_HIP = -3,         /* a HIP runtime call failed */
+  MSD_E_TIMEOUT = -4,     /* a cross-workgroup wait exceeded its spin bound (reported by msd_check_status) */
+};
+
+/* Number of bf16 elements of the packed per-layer weight buffer (kernel layout). */
+int64_t msd_packed_weight_elems(const msd_config* cfg);
+
+/* Bytes of device workspace a decode step needs for n_workgroups workgroups.
+ * The workspace must be zero-filled once before first use; it is reused across steps. */
+int64_t msd_workspace_bytes(const msd_config* cfg, int32_t n_workgroups);
+
+/* Workgroups a step launches on device `device` (one per compute unit). */
+int32_t msd_default_workgroups(int32_t device);
+
+/* One fused decode step: embedding of the token, all layers (RMSNorm, QKV, RoPE, KV write
+ * at `pos`, GQA attention over rows 0..pos, O projection, SwiGLU FFN, residuals), final
+ * RMSNorm, tied logits over the vocabulary and argmax.
+ *
+ *   token_emb   bf16 (vocab_size, d_model)
+ *   packed_w    bf16, msd_packed_weight_elems(cfg) elements (kernel layout)
+ *   lnf_s       bf16 (d_model) final RMSNorm scale
+ *   rope        f32 (context_len, d_head): [cos(0..d_head/2) | sin(0..d_head/2)] per position
+ *   token_id    input token, used when token_dev is NULL
+ *   token_dev   optional device int32 holding the input token (e.g. the previous step's
+ *               next_token), read by the kernel instead of token_id
+ *   pos         position of the input token, 0 <= pos < context_len
+ *   kv          bf16 KV cache [layer][K,V][kv_head][context_len][d_head], updated in place at pos
+ *   workspace   msd_workspace_bytes(cfg, n_workgroups) bytes
+ *   epoch       strictly increasing per call on one workspace (starts at 1)
+ *   logits      f32 (vocab_size) output
+ *   next_token  device int32[2] output: [0] argmax of logits (lowest index on ties),
+ *               [1] the workspace status word at the end of the step (0 = ok; bit 0 = a
+ *               cross-workgroup wait ran out, bit 1 = token_dev held an out-of-range id)
+ *
+ * Supported shapes: d_head 64, d_model 256 or 1024, d_ff a multiple of 16 up to 4096,
+ * context_len up to 1024, n_workgroups >= 16 * n_kv_heads.  Returns MSD_E_CONFIG otherwise.
+ * Calls that share a workspace must be ordered on one stream.
+ */
+int32_t msd_decode_step(const msd_config* cfg, const void* token_emb, const void* packed_w,
+                        const void* lnf_s, const float* rope, int32_t token_id,
+                        const int32_t* token_dev, int32_t pos, void* kv, void* workspace,
+                        uint32_t epoch, float* logits, int32_t* next_token,
+                        int32_t n_workgroups, void* stream);
+
+/* Reads and clears the device status word of a workspace (synchronous on `stream`).
+ * Returns MSD_OK, MSD_E_TIMEOUT when a wait of an earlier step ran out, or MSD_E_HIP. */
+int32_t msd_check_status(void* workspace, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MSDECODE_H */

@@ -1,0 +1,117 @@
+"""Parity of the HIP decode step against the oracle (GPU)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import model as om
+from transformer_amd.configs import TINY
+from transformer_amd.fused_decode_nlayer import prepare_decode_weights_nlayer, unpack_kv_caches
+from transformer_amd.multi_sm_decode import Decoder, multi_sm_decode_nlayer
+from transformer_amd.synthetic import make_params, make_prompt
+
+pytestmark = pytest.mark.gpu
+
+# logits tolerance stated by the task: 2e-2 abs / 1e-2 rel against the reference maths
+ATOL, RTOL = 2e-2, 1e-2
+
+
+@pytest.fixture(scope="module")
+def tiny():
+    params = make_params(TINY, seed=0)
+    prompt = make_prompt(16, TINY["vocab_size"], seed=1)
+    w = prepare_decode_weights_nlayer(params, TINY)
+    return params, prompt, w
+
+
+def _gpu_generate(w, cfg, prompt, n_new):
+    dec = Decoder(w, cfg)
+    for p, t in enumerate(prompt):
+        tok, lg = dec.step(int(t), p)
+    toks, logs = [tok], [lg.cpu().numpy().copy()]
+    for i in range(n_new - 1):
+        tok, lg = dec.step(toks[-1], len(prompt) + i)
+        toks.append(tok)
+        logs.append(lg.cpu().numpy().copy())
+    return toks, logs, dec
+
+
+def test_tiny_first_step_logits(tiny):
+    params, prompt, w = tiny
+    dec = Decoder(w, TINY)
+    tok, lg = dec.step(int(prompt[0]), 0)
+    kc, vc = om.new_kv_cache(TINY)
+    ref, rtok = om.decode_step(params, TINY, int(prompt[0]), 0, kc, vc)
+    got = lg.cpu().numpy()
+    print("max |diff| at pos 0:", np.abs(got - ref).max())
+    np.testing.assert_allclose(got, ref, atol=1e-4, rtol=1e-4)
+    assert tok == rtok
+
+
+def test_tiny_greedy_token_exact(tiny):
+    """Config 1: 16-token prompt, 48 greedy tokens; tokens bit-exact, logits within tolerance."""
+    params, prompt, w = tiny
+    toks, logs, dec = _gpu_generate(w, TINY, prompt, 48)
+    rtoks, rlogs = om.greedy_generate(params, TINY, prompt, 48, prefill="step", return_logits=True)
+    diffs = [float(np.abs(a - b).max()) for a, b in zip(logs, rlogs)]
+    print("max |logit diff| per step:", max(diffs))
+    assert toks == rtoks
+    for a, b in zip(logs, rlogs):
+        np.testing.assert_allclose(a, b, atol=ATOL, rtol=RTOL)
+    # KV cache rows 0..P+47-1 match the oracle's bf16 cache (one bf16 ulp of rounding slack)
+    kc, vc = unpack_kv_caches(dec.kv, TINY["n_layers"], TINY["n_kv_heads"], TINY["context_len"], 64)
+    okc, ovc = om.new_kv_cache(TINY)
+    seq = list(prompt) + rtoks[:-1]
+    for p, t in enumerate(seq):
+        om.decode_step(params, TINY, t, p, okc, ovc)
+    n = len(seq)
+    for l in range(TINY["n_layers"]):
+        np.testing.assert_allclose(kc[l][:, :n].float().cpu().numpy(), okc[l][:, :n], rtol=1e-2, atol=1e-3)
+        np.testing.assert_allclose(vc[l][:, :n].float().cpu().numpy(), ovc[l][:, :n], rtol=1e-2, atol=1e-3)
+
+
+def test_tiny_logits_close_to_full_forward(tiny):
+    """Against the literal model.py forward (f32, un-rounded K/V) over the whole sequence."""
+    params, prompt, w = tiny
+    toks, logs, _ = _gpu_generate(w, TINY, prompt, 16)
+    seq = np.array(list(prompt) + toks[:-1])
+    full = om.forward(params, TINY, seq)
+    for i, lg in enumerate(logs):
+        np.testing.assert_allclose(lg, full[len(prompt) - 1 + i], atol=ATOL, rtol=RTOL)
+
+
+def test_tiny_replay_is_bitwise_deterministic(tiny):
+    params, prompt, w = tiny
+    a, la, _ = _gpu_generate(w, TINY, prompt, 8)
+    b, lb, _ = _gpu_generate(w, TINY, prompt, 8)
+    assert a == b
+    for x, y in zip(la, lb):
+        assert np.array_equal(x, y)
+
+
+def test_reference_signature_dropin(tiny):
+    params, prompt, w = tiny
+    from transformer_amd.fused_decode_nlayer import new_kv_packed
+    kv = new_kv_packed(TINY)
+    for p, t in enumerate(prompt):
+        nt, logits, kv2 = multi_sm_decode_nlayer(w, TINY, int(t), p, kv)
+        assert kv2 is kv
+    kc, vc = om.new_kv_cache(TINY)
+    for p, t in enumerate(prompt):
+        ref, rt = om.decode_step(params, TINY, int(t), p, kc, vc)
+    assert int(nt) == rt and logits.shape == (TINY["vocab_size"],)
+    np.testing.assert_allclose(logits.cpu().numpy(), ref, atol=1e-4, rtol=1e-4)
+
+
+def test_device_token_chaining(tiny):
+    """The input token can be the previous step's device output (no host round trip)."""
+    params, prompt, w = tiny
+    dec = Decoder(w, TINY)
+    for p, t in enumerate(prompt):
+        dec.launch(int(t), p)
+    toks = []
+    for i in range(8):
+        out = dec.launch(dec.out[0:1], len(prompt) + i)
+        toks.append(out[0:1].clone())
+    got = [int(t) for t in toks]
+    ref = om.greedy_generate(params, TINY, prompt, 9, prefill="step")
+    assert got == ref[1:]

@@ -1,0 +1,72 @@
+"""Packing layout contract (CPU): kernel-layout rows equal the reference matrices' columns."""
+import ctypes
+
+import numpy as np
+import torch
+
+from transformer_amd import _lib
+from transformer_amd.configs import TINY
+from transformer_amd.fused_decode_nlayer import (pack_kv_caches, pack_layer, precompute_rope_table,
+                                                 unpack_kv_caches)
+from transformer_amd.synthetic import make_params
+
+
+def test_library_exports_every_declared_symbol():
+    L = _lib.lib()
+    hdr = open(_lib.os.path.join(_lib.HERE, "..", "include", "msdecode.h")).read()
+    import re
+    declared = set(re.findall(r"\b(msd_[a-z_]+)\s*\(", hdr))
+    assert declared == set(_lib.EXPORTS)
+    for name in declared:
+        assert getattr(L, name) is not None
+
+
+def test_packed_layer_layout(tiny_params):
+    cfg = TINY
+    d, H, KV, ff, dh = cfg["d_model"], cfg["n_heads"], cfg["n_kv_heads"], cfg["d_ff"], 64
+    blk = pack_layer(tiny_params, cfg, 1, device="cpu").float().numpy()
+    n = _lib.lib().msd_packed_weight_elems(ctypes.byref(_lib.MsdConfig.from_dict(cfg)))
+    assert blk.size * cfg["n_layers"] == n
+    p = "layer1"
+    o = 0
+    np.testing.assert_array_equal(blk[o:o + d], tiny_params[f"{p}.ln1.scale"]); o += d
+    np.testing.assert_array_equal(blk[o:o + d], tiny_params[f"{p}.ln2.scale"]); o += d
+    qkv = blk[o:o + (H + 2 * KV) * dh * d].reshape(-1, d); o += qkv.size
+    for h in range(H):
+        for r in range(dh):
+            orig = r // 2 if r % 2 == 0 else 32 + r // 2
+            np.testing.assert_array_equal(qkv[h * dh + r], tiny_params[f"{p}.attn.q"][:, h * dh + orig])
+    for g in range(KV):
+        for r in range(dh):
+            orig = r // 2 if r % 2 == 0 else 32 + r // 2
+            np.testing.assert_array_equal(qkv[(H + g) * dh + r], tiny_params[f"{p}.attn.k"][:, g * dh + orig])
+            np.testing.assert_array_equal(qkv[(H + KV + g) * dh + r], tiny_params[f"{p}.attn.v"][:, g * dh + r])
+    wo = blk[o:o + d * d].reshape(d, d); o += d * d
+    np.testing.assert_array_equal(wo, tiny_params[f"{p}.attn.o"].T)
+    gu = blk[o:o + 2 * ff * d].reshape(2 * ff, d); o += 2 * ff * d
+    np.testing.assert_array_equal(gu[0::2], tiny_params[f"{p}.ffn.gate"].T)
+    np.testing.assert_array_equal(gu[1::2], tiny_params[f"{p}.ffn.up"].T)
+    dn = blk[o:o + d * ff].reshape(d, ff); o += d * ff
+    np.testing.assert_array_equal(dn, tiny_params[f"{p}.ffn.down"].T)
+    assert o == blk.size
+
+
+def test_kv_pack_roundtrip():
+    rng = np.random.default_rng(0)
+    ks = [rng.standard_normal((2, 16, 64)).astype(np.float32) for _ in range(3)]
+    vs = [rng.standard_normal((2, 16, 64)).astype(np.float32) for _ in range(3)]
+    flat = pack_kv_caches(ks, vs, device="cpu")
+    assert flat.dtype == torch.bfloat16 and flat.numel() == 3 * 2 * 2 * 16 * 64
+    k2, v2 = unpack_kv_caches(flat, 3, 2, 16, 64)
+    for a, b in zip(ks + vs, k2 + v2):
+        np.testing.assert_array_equal(torch.from_numpy(a).to(torch.bfloat16).float().numpy(), b.float().numpy())
+    # layer 1 K starts after layer 0's K and V
+    assert torch.equal(flat[2 * 2 * 16 * 64:3 * 2 * 16 * 64].view(2, 16, 64), k2[1])
+
+
+def test_rope_table_matches_reference_formula():
+    c, s = precompute_rope_table(512, 64)
+    f = np.float32(10000.0) ** (-np.arange(32, dtype=np.float32) * np.float32(2.0) / np.float32(64))
+    ang = np.arange(512, dtype=np.float32)[:, None] * f[None, :]
+    np.testing.assert_array_equal(c, np.cos(ang))
+    np.testing.assert_array_equal(s, np.sin(ang))

@@ -1,0 +1,74 @@
+"""ctypes binding of libmsdecode.so (C ABI in include/msdecode.h).
+
+torch is imported first so that the library's HIP runtime dependency resolves to the
+runtime torch already loaded (one runtime per process, shared device pointers/streams).
+There is no fallback: a missing library raises.
+"""
+import ctypes
+import os
+
+import torch  # noqa: F401  (load torch's HIP runtime before the library)
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libmsdecode.so")
+
+MSD_OK = 0
+MSD_E_CONFIG = -1
+MSD_E_ARG = -2
+MSD_E_HIP = -3
+MSD_E_TIMEOUT = -4
+_ERRNAMES = {MSD_E_CONFIG: "unsupported config", MSD_E_ARG: "invalid argument",
+             MSD_E_HIP: "HIP runtime error", MSD_E_TIMEOUT: "cross-workgroup wait timed out"}
+
+EXPORTS = ("msd_packed_weight_elems", "msd_workspace_bytes", "msd_default_workgroups",
+           "msd_decode_step", "msd_check_status")
+
+
+class MsdConfig(ctypes.Structure):
+    _fields_ = [(k, ctypes.c_int32) for k in ("vocab_size", "d_model", "n_heads", "n_kv_heads",
+                                              "n_layers", "d_head", "d_ff", "context_len")]
+
+    @classmethod
+    def from_dict(cls, c):
+        return cls(c["vocab_size"], c["d_model"], c["n_heads"], c["n_kv_heads"], c["n_layers"],
+                   c.get("d_head", c["d_model"] // c["n_heads"]), c["d_ff"], c["context_len"])
+
+
+class MsdError(RuntimeError):
+    def __init__(self, code, what):
+        super().__init__(f"{what}: {_ERRNAMES.get(code, 'error')} ({code})")
+        self.code = code
+
+
+_lib = None
+
+
+def lib():
+    """Load libmsdecode.so once; raises if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(f"{LIB_PATH} is missing: build it with `python -m transformer_amd.build` "
+                           "(or __graft_entry__.build())")
+    L = ctypes.CDLL(LIB_PATH)
+    P, I32, I64, U32 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_uint32
+    CP = ctypes.POINTER(MsdConfig)
+    L.msd_packed_weight_elems.argtypes = [CP]
+    L.msd_packed_weight_elems.restype = I64
+    L.msd_workspace_bytes.argtypes = [CP, I32]
+    L.msd_workspace_bytes.restype = I64
+    L.msd_default_workgroups.argtypes = [I32]
+    L.msd_default_workgroups.restype = I32
+    L.msd_decode_step.argtypes = [CP, P, P, P, P, I32, P, I32, P, P, U32, P, P, I32, P]
+    L.msd_decode_step.restype = I32
+    L.msd_check_status.argtypes = [P, P]
+    L.msd_check_status.restype = I32
+    _lib = L
+    return L
+
+
+def check(code, what):
+    if code < 0:
+        raise MsdError(code, what)
+    return code

@@ -1,0 +1,116 @@
+"""Fused whole-model decode step (drop-in for the reference's multi_sm_decode module).
+
+``multi_sm_decode_nlayer(w, config, token_id, pos, kv_packed)`` keeps the reference
+signature and return triple (kernels/multi_sm_decode.py:369-432); ``Decoder`` is the
+stateful form with ``step(token, pos) -> (next_token, logits)`` that owns the workspace.
+
+Differences from the reference call, by design:
+  * the KV cache is updated in place at ``pos`` (the returned kv is the same tensor); a
+    step writes ``pos`` before reading it and never reads rows > pos, so replaying from
+    the same start position (profile_kernels.py:54-63) gives the same results;
+  * the workspace is allocated once per decoder and never re-zeroed: exchange words are
+    tagged with a per-call epoch instead (multi_sm_decode.py:400 zero-fills per call).
+"""
+import ctypes
+
+import torch
+
+from . import _lib
+
+
+class Decoder:
+    """One decode stream: weights dict, packed KV buffer, workspace and output buffers."""
+
+    def __init__(self, w, config, kv_packed=None, device=None, n_workgroups=None):
+        from .fused_decode_nlayer import new_kv_packed
+        self.w = w
+        self.config = dict(config)
+        self.device = torch.device(device) if device is not None else w["packed_w"].device
+        self._cfg = _lib.MsdConfig.from_dict(self.config)
+        L = _lib.lib()
+        if n_workgroups is None:
+            idx = self.device.index if self.device.index is not None else torch.cuda.current_device()
+            n_workgroups = _lib.check(L.msd_default_workgroups(idx), "msd_default_workgroups")
+        self.n_workgroups = int(n_workgroups)
+        nbytes = _lib.check(L.msd_workspace_bytes(ctypes.byref(self._cfg), self.n_workgroups),
+                            "msd_workspace_bytes")
+        self.workspace = torch.zeros(nbytes, dtype=torch.uint8, device=self.device)
+        self.kv = kv_packed if kv_packed is not None else new_kv_packed(self.config, self.device)
+        self.logits = torch.empty(self.config["vocab_size"], dtype=torch.float32, device=self.device)
+        self.out = torch.zeros(2, dtype=torch.int32, device=self.device)   # [token, status]
+        self._host = torch.zeros(2, dtype=torch.int32).pin_memory()
+        self.epoch = 0
+        self._check_kv(self.kv)
+
+    def _check_kv(self, kv):
+        c = self.config
+        n = c["n_layers"] * 2 * c["n_kv_heads"] * c["context_len"] * c.get("d_head", c["d_model"] // c["n_heads"])
+        if kv.dtype != torch.bfloat16 or kv.numel() != n or not kv.is_contiguous() or kv.device != self.device:
+            raise ValueError("kv_packed must be a contiguous bf16 tensor of "
+                             f"{n} elements on {self.device}")
+
+    def launch(self, token, pos, stream=None, out=None):
+        """Enqueue one step; ``token`` is an int or a device int32 tensor (read on device).
+
+        Returns the device int32[2] output (token, status) without synchronising.
+        """
+        c = self.config
+        pos = int(pos)
+        if not 0 <= pos < c["context_len"]:
+            raise ValueError(f"pos {pos} outside [0, {c['context_len']})")
+        tok_dev = None
+        tok = 0
+        if isinstance(token, torch.Tensor) and token.is_cuda:
+            if token.dtype != torch.int32:
+                raise ValueError("device token must be int32")
+            tok_dev = token.data_ptr()
+        else:
+            tok = int(token)
+            if not 0 <= tok < c["vocab_size"]:
+                raise ValueError(f"token {tok} outside [0, {c['vocab_size']})")
+        out = self.out if out is None else out
+        self.epoch = (self.epoch % 0xFFFFFFFE) + 1
+        s = stream if stream is not None else torch.cuda.current_stream(self.device)
+        w = self.w
+        rc = _lib.lib().msd_decode_step(
+            ctypes.byref(self._cfg), w["token_emb"].data_ptr(), w["packed_w"].data_ptr(),
+            w["lnf_s"].data_ptr(), w["rope"].data_ptr(), tok, tok_dev, pos, self.kv.data_ptr(),
+            self.workspace.data_ptr(), self.epoch, self.logits.data_ptr(), out.data_ptr(),
+            self.n_workgroups, ctypes.c_void_p(s.cuda_stream))
+        _lib.check(rc, "msd_decode_step")
+        return out
+
+    def step(self, token, pos):
+        """Run one step and return (next_token: int, logits: (V,) f32 device tensor).
+
+        The logits tensor is this decoder's buffer and is overwritten by the next step.
+        """
+        out = self.launch(token, pos)
+        self._host.copy_(out, non_blocking=True)
+        torch.cuda.current_stream(self.device).synchronize()
+        tok, status = int(self._host[0]), int(self._host[1])
+        if status != 0:
+            _lib.lib().msd_check_status(self.workspace.data_ptr(),
+                                        ctypes.c_void_p(torch.cuda.current_stream(self.device).cuda_stream))
+            raise _lib.MsdError(_lib.MSD_E_TIMEOUT if status & 1 else _lib.MSD_E_ARG,
+                                f"decode step at pos {pos} (status {status:#x})")
+        return tok, self.logits
+
+
+_decoders = {}
+
+
+def multi_sm_decode_nlayer(w, config, token_id, pos, kv_packed, kv_splits=1):
+    """Reference signature (multi_sm_decode.py:369): returns (next_token, logits[:V] f32, kv).
+
+    next_token is a device int32 scalar tensor, logits a fresh (V,) f32 tensor, kv the
+    same ``kv_packed`` tensor updated in place.  ``kv_splits`` is accepted for signature
+    compatibility; the kernel chooses its own split of the attention work.
+    """
+    key = (id(w), kv_packed.data_ptr())
+    dec = _decoders.get(key)
+    if dec is None:
+        dec = Decoder(w, config, kv_packed)
+        _decoders[key] = dec
+    out = dec.launch(token_id, pos)
+    return out[0].clone(), dec.logits.clone(), kv_packed
