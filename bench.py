@@ -1,0 +1,170 @@
+"""Benchmark: batch-1 greedy decode of the 306M config on one MI355X.
+
+Workload (one "step" = one fused decode step = one token): 306M GQA decoder (d 1024,
+16 heads, 4 KV heads, 24 layers, d_ff 2816, vocab 32000, ctx 512), random-init bf16
+weights (N(0, 0.02), residual projections 0.02/sqrt(48), seed 0), a 32-token uniform
+random prompt (seed 1) fed step by step, then greedy decode at positions 32..510.  The
+timed region runs K steps starting at position 32 (wrapping back to 32 after 510); each
+step reads the previous step's token on the device, so no host round trip sits between
+steps.  The KV cache is updated in place, so the warmup and timed passes replay the same
+positions with the same inputs.
+
+Prints one JSON line.  value = decoded tokens per second; roofline.achieved = algorithmic
+bytes per step (weights + KV rows read + KV row written, averaged over the timed
+positions) / measured average step time; cpu_baseline = the numpy oracle's cached decode
+step on the host (a bounded sample of positions).
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "decode tok/s @batch1 306M on 1 MI355X; % of HBM roofline"
+PEAK_HBM_GBS = 8000.0
+
+
+def positions(start, stop, k):
+    span = stop - start
+    return [start + (i % span) for i in range(k)]
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=479)
+    ap.add_argument("--warmup", type=int, default=32)
+    ap.add_argument("--cpu-sample", type=int, default=4, help="oracle steps timed for cpu_baseline (0 = skip)")
+    ap.add_argument("--synced-steps", type=int, default=128, help="host-synced steps for the secondary figure")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported "
+              "(the decode step runs on a single MI355X; see DESIGN.md for how it would shard)",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    from transformer_amd.configs import M306, bytes_per_token
+    from transformer_amd.fused_decode_nlayer import prepare_decode_weights_nlayer
+    from transformer_amd.multi_sm_decode import Decoder
+    from transformer_amd.synthetic import make_params, make_prompt
+
+    cfg = dict(M306)
+    prompt_len = 32
+    t0 = time.time()
+    params = make_params(cfg, seed=0, resid_scaled=True)
+    prompt = make_prompt(prompt_len, cfg["vocab_size"], seed=1)
+    w = prepare_decode_weights_nlayer(params, cfg, device="cuda")
+    dec = Decoder(w, cfg)
+    print(f"[bench] weights ready in {time.time() - t0:.1f}s; workgroups={dec.n_workgroups}",
+          file=sys.stderr, flush=True)
+
+    # prompt ingest (not timed): one step per prompt token
+    for p, t in enumerate(prompt):
+        first, _ = dec.step(int(t), p)
+    stream = torch.cuda.current_stream()
+    start, stop = prompt_len, cfg["context_len"] - 1   # positions 32..510
+
+    def run(ps):
+        # ring[i] = (token, status) written by step i-1; step i reads ring[i][0] on device
+        ring = torch.zeros((len(ps) + 1, 2), dtype=torch.int32, device="cuda")
+        ring[0, 0] = first
+        for i, p in enumerate(ps):
+            dec.launch(ring[i, 0:1], p, out=ring[i + 1])
+        return ring
+
+    warm = positions(start, stop, args.warmup)
+    if warm:
+        run(warm)
+    torch.cuda.synchronize()
+    ps = positions(start, stop, args.steps)
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    ring = run(ps)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1)
+    status = int(ring[1:, 1].abs().max())
+    if status != 0:
+        raise RuntimeError(f"decode status {status:#x} during the timed run")
+    ms_per_step = ms / args.steps
+    tok_s = args.steps / (ms / 1e3)
+    avg_bytes = float(np.mean([bytes_per_token(cfg, p) for p in ps]))
+    achieved = avg_bytes / (ms_per_step * 1e-3) / 1e9
+    print(f"[bench] timed {args.steps} steps: {ms_per_step * 1e3:.1f} us/step, {tok_s:.0f} tok/s, "
+          f"{achieved:.0f} GB/s", file=sys.stderr, flush=True)
+
+    # secondary: host-synchronised loop (token read back after every step, as generate.py does)
+    synced = None
+    if args.synced_steps > 0:
+        sp = positions(start, stop, args.synced_steps)
+        tok = first
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        for p in sp:
+            tok, _ = dec.step(tok, p)
+        synced = len(sp) / (time.perf_counter() - t1)
+
+    # CPU baseline: the oracle's cached decode step on the host, bounded sample
+    cpu = None
+    if args.cpu_sample > 0:
+        from oracle import model as om
+        try:
+            from threadpoolctl import threadpool_info
+            cores = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+        except Exception:
+            cores = os.cpu_count()
+        kc, vc = om.new_kv_cache(cfg)
+        rope = om.precompute_rope_table(cfg["context_len"], cfg["d_head"])
+        n = args.cpu_sample
+        # cache rows come from the GPU run (bf16 values), so the sample attends over a full prompt
+        from transformer_amd.fused_decode_nlayer import unpack_kv_caches
+        gk, gv = unpack_kv_caches(dec.kv, cfg["n_layers"], cfg["n_kv_heads"], cfg["context_len"], cfg["d_head"])
+        for l in range(cfg["n_layers"]):
+            kc[l][:, :start] = gk[l][:, :start].float().cpu().numpy()
+            vc[l][:, :start] = gv[l][:, :start].float().cpu().numpy()
+        om.decode_step(params, cfg, int(first), start, kc, vc, rope=rope)   # warm
+        tc = time.perf_counter()
+        tk = int(first)
+        for i in range(n):
+            _, tk = om.decode_step(params, cfg, tk, start + i, kc, vc, rope=rope)
+        cpu_s = time.perf_counter() - tc
+        cpu = {"value": round(n / cpu_s, 3), "unit": "tok/s", "cores": int(cores), "kind": "port",
+               "sample": f"{n} cached decode steps of the numpy oracle (f32 on bf16-valued 306M "
+                         f"weights) at positions {start}..{start + n - 1}, {cpu_s:.1f}s"}
+
+    line = {
+        "metric": METRIC,
+        "value": round(tok_s, 1),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (random-init weights N(0,0.02), seeded uniform prompt)",
+        "config": {"workload": "306M batch-1 greedy decode, 32-token prompt, positions 32..510",
+                   "d_model": cfg["d_model"], "n_layers": cfg["n_layers"], "n_heads": cfg["n_heads"],
+                   "n_kv_heads": cfg["n_kv_heads"], "d_ff": cfg["d_ff"], "vocab": cfg["vocab_size"],
+                   "context_len": cfg["context_len"], "batch": 1},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
+                     "bytes_per_step": round(avg_bytes)},
+        "cpu_baseline": cpu,
+        "host_synced_tok_s": None if synced is None else round(synced, 1),
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

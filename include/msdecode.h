@@ -42,7 +42,11 @@ enum {
   MSD_E_TIMEOUT = -4,     /* a cross-workgroup wait exceeded its spin bound (reported by msd_check_status) */
 };
 
-/* Number of bf16 elements of the packed per-layer weight buffer (kernel layout). */
+/* Kernel row layout: every row of K bf16 inputs is cut into blocks of 512 (the last block
+ * holds the remaining S = 8*m values); within block b the value stored at offset
+ * 512*b + 8*l + k (l < m, k < 8) is input element 512*b + k*m + l of the row.
+ *
+ * Number of bf16 elements of the packed per-layer weight buffer (kernel layout). */
 int64_t msd_packed_weight_elems(const msd_config* cfg);
 
 /* Bytes of device workspace a decode step needs for n_workgroups workgroups.
@@ -56,7 +60,9 @@ int32_t msd_default_workgroups(int32_t device);
  * at `pos`, GQA attention over rows 0..pos, O projection, SwiGLU FFN, residuals), final
  * RMSNorm, tied logits over the vocabulary and argmax.
  *
- *   token_emb   bf16 (vocab_size, d_model)
+ *   token_emb   bf16 (vocab_size, d_model), natural layout (embedding gather)
+ *   output_proj bf16 (vocab_size, d_model): token_emb with every row in the kernel row layout
+ *               (tied output projection; replaces the reference's output_proj_padded)
  *   packed_w    bf16, msd_packed_weight_elems(cfg) elements (kernel layout)
  *   lnf_s       bf16 (d_model) final RMSNorm scale
  *   rope        f32 (context_len, d_head): [cos(0..d_head/2) | sin(0..d_head/2)] per position
@@ -76,7 +82,8 @@ int32_t msd_default_workgroups(int32_t device);
  * context_len up to 1024, n_workgroups >= 16 * n_kv_heads.  Returns MSD_E_CONFIG otherwise.
  * Calls that share a workspace must be ordered on one stream.
  */
-int32_t msd_decode_step(const msd_config* cfg, const void* token_emb, const void* packed_w,
+int32_t msd_decode_step(const msd_config* cfg, const void* token_emb, const void* output_proj,
+                        const void* packed_w,
                         const void* lnf_s, const float* rope, int32_t token_id,
                         const int32_t* token_dev, int32_t pos, void* kv, void* workspace,
                         uint32_t epoch, float* logits, int32_t* next_token,

@@ -6,8 +6,8 @@ import torch
 
 from transformer_amd import _lib
 from transformer_amd.configs import TINY
-from transformer_amd.fused_decode_nlayer import (pack_kv_caches, pack_layer, precompute_rope_table,
-                                                 unpack_kv_caches)
+from transformer_amd.fused_decode_nlayer import (kernel_perm, pack_kv_caches, pack_layer,
+                                                 precompute_rope_table, unpack_kv_caches)
 from transformer_amd.synthetic import make_params
 
 
@@ -31,7 +31,10 @@ def test_packed_layer_layout(tiny_params):
     o = 0
     np.testing.assert_array_equal(blk[o:o + d], tiny_params[f"{p}.ln1.scale"]); o += d
     np.testing.assert_array_equal(blk[o:o + d], tiny_params[f"{p}.ln2.scale"]); o += d
-    qkv = blk[o:o + (H + 2 * KV) * dh * d].reshape(-1, d); o += qkv.size
+    # undo the in-dimension permutation of the kernel row layout
+    inv_d = np.argsort(kernel_perm(d).numpy())
+    inv_f = np.argsort(kernel_perm(ff).numpy())
+    qkv = blk[o:o + (H + 2 * KV) * dh * d].reshape(-1, d)[:, inv_d]; o += (H + 2 * KV) * dh * d
     for h in range(H):
         for r in range(dh):
             orig = r // 2 if r % 2 == 0 else 32 + r // 2
@@ -41,12 +44,12 @@ def test_packed_layer_layout(tiny_params):
             orig = r // 2 if r % 2 == 0 else 32 + r // 2
             np.testing.assert_array_equal(qkv[(H + g) * dh + r], tiny_params[f"{p}.attn.k"][:, g * dh + orig])
             np.testing.assert_array_equal(qkv[(H + KV + g) * dh + r], tiny_params[f"{p}.attn.v"][:, g * dh + r])
-    wo = blk[o:o + d * d].reshape(d, d); o += d * d
+    wo = blk[o:o + d * d].reshape(d, d)[:, inv_d]; o += d * d
     np.testing.assert_array_equal(wo, tiny_params[f"{p}.attn.o"].T)
-    gu = blk[o:o + 2 * ff * d].reshape(2 * ff, d); o += 2 * ff * d
+    gu = blk[o:o + 2 * ff * d].reshape(2 * ff, d)[:, inv_d]; o += 2 * ff * d
     np.testing.assert_array_equal(gu[0::2], tiny_params[f"{p}.ffn.gate"].T)
     np.testing.assert_array_equal(gu[1::2], tiny_params[f"{p}.ffn.up"].T)
-    dn = blk[o:o + d * ff].reshape(d, ff); o += d * ff
+    dn = blk[o:o + d * ff].reshape(d, ff)[:, inv_f]; o += d * ff
     np.testing.assert_array_equal(dn, tiny_params[f"{p}.ffn.down"].T)
     assert o == blk.size
 
@@ -70,3 +73,15 @@ def test_rope_table_matches_reference_formula():
     ang = np.arange(512, dtype=np.float32)[:, None] * f[None, :]
     np.testing.assert_array_equal(c, np.cos(ang))
     np.testing.assert_array_equal(s, np.sin(ang))
+
+
+def test_kernel_perm_layout():
+    """Block b, lane l, value q of the packed row is input 512*b + q*m + l (m lanes in the block)."""
+    for k in (256, 1024, 704, 2816):
+        p = kernel_perm(k).numpy()
+        assert sorted(p.tolist()) == list(range(k))
+        for b in range(0, k, 512):
+            m = min(512, k - b) // 8
+            for lane in (0, m - 1):
+                for q in (0, 7):
+                    assert p[b + 8 * lane + q] == b + q * m + lane

@@ -60,7 +60,7 @@ def lib():
     L.msd_workspace_bytes.restype = I64
     L.msd_default_workgroups.argtypes = [I32]
     L.msd_default_workgroups.restype = I32
-    L.msd_decode_step.argtypes = [CP, P, P, P, P, I32, P, I32, P, P, U32, P, P, I32, P]
+    L.msd_decode_step.argtypes = [CP, P, P, P, P, P, I32, P, I32, P, P, U32, P, P, I32, P]
     L.msd_decode_step.restype = I32
     L.msd_check_status.argtypes = [P, P]
     L.msd_check_status.restype = I32

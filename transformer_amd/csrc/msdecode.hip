@@ -37,12 +37,30 @@
 
 namespace msd {
 
-constexpr int kThreads = 256;
-constexpr int kWaves = kThreads / 64;
+// Optional phase timestamps for profiling builds (-DMSD_TRACE): lane 0 of the first exchange
+// wave and of compute wave 0 record s_memrealtime (100 MHz) at phase boundaries of one layer
+// into msd_trace_buffer[workgroup][slot].  Compiled out otherwise.
+#ifdef MSD_TRACE
+__device__ uint64_t msd_trace_buffer[4096 * 32];
+#define MSD_TRACE_POINT(cond, slot)                                                        \
+  do {                                                                                    \
+    if ((cond) && l == MSD_TRACE_LAYER && c.lane == 0)                                    \
+      msd_trace_buffer[c.wg * 32 + (slot)] = __builtin_amdgcn_s_memrealtime();           \
+  } while (0)
+#else
+#define MSD_TRACE_POINT(cond, slot) \
+  do {                              \
+  } while (0)
+#endif
+
 constexpr int kDh = 64;          // head dimension (fixed)
-constexpr int kChunks = 16;      // attention position chunks per KV head
+constexpr int kChunkMax = 64;    // attention positions per chunk (one per lane of a wave)
 constexpr int kPartStride = 66;  // per (chunk, head): m, l, o[64]
+constexpr int kKPad = kDh + 1;   // LDS row stride of cached K rows (floats)
 constexpr uint32_t kSpinLimit = 1u << 20;
+
+constexpr int kWavesC = 4;      // compute waves per workgroup
+constexpr int kWavesX = 4;      // exchange waves per workgroup
 
 constexpr uint32_t kStatusTimeout = 1u;
 constexpr uint32_t kStatusBadToken = 2u;
@@ -58,7 +76,10 @@ struct Layout {
 
 __host__ __device__ inline int64_t align64(int64_t v) { return (v + 63) & ~int64_t(63); }
 
-__host__ __device__ inline Layout make_layout(int d, int H, int KV, int ff) {
+// attention chunks per KV head: enough that a chunk of the full context fits a wave
+__host__ __device__ inline int n_chunks(int ctx) { return (ctx + kChunkMax - 1) / kChunkMax; }
+
+__host__ __device__ inline Layout make_layout(int d, int H, int KV, int ff, int ctx) {
   Layout t;
   const int64_t nqkv = int64_t(H + 2 * KV) * kDh;
   t.off_ln1 = 0;
@@ -71,7 +92,7 @@ __host__ __device__ inline Layout make_layout(int d, int H, int KV, int ff) {
   const int GQ = H / KV;
   t.x_qkv = 0;
   t.x_part = t.x_qkv + align64(nqkv);
-  t.x_attn = t.x_part + align64(int64_t(KV) * kChunks * GQ * kPartStride);
+  t.x_attn = t.x_part + align64(int64_t(KV) * n_chunks(ctx) * GQ * kPartStride);
   t.x_hd1 = t.x_attn + align64(d);
   t.x_act = t.x_hd1 + align64(d);
   t.x_hd2 = t.x_act + align64(ff);
@@ -82,6 +103,7 @@ __host__ __device__ inline Layout make_layout(int d, int H, int KV, int ff) {
 
 struct Args {
   const uint16_t* emb;
+  const uint16_t* outp;   // tied output projection: token_emb rows in the kernel row layout
   const uint16_t* w;
   const uint16_t* lnf;
   const float* rope;
@@ -93,7 +115,7 @@ struct Args {
   uint64_t* xw;     // exchange words, n_layers * x_layer
   int token, pos;
   uint32_t epoch;
-  int H, KV, L, ff, V, ctx;
+  int H, KV, L, ff, V, ctx, nch;
   Layout lay;
 };
 
@@ -106,15 +128,50 @@ __device__ __forceinline__ uint16_t f2bf(float f) {  // round to nearest even
   return uint16_t((u + (((u >> 16) & 1u) + 0x7fffu)) >> 16);
 }
 
+// Wave64 reductions with DPP (no LDS traffic): rows of 16 lanes are scanned with
+// row_shr 1/2/4/8, then row_bcast 15/31 carry the row totals into lane 63, which is read
+// back as a wave-uniform value.  The addition order is fixed, so every call is
+// deterministic.
+__device__ __forceinline__ float dpp_f(float v, int ctrl, int row_mask) {
+  switch (ctrl) {   // the control word must be a compile-time constant
+    case 0x111: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x111, 0xf, 0xf, true));
+    case 0x112: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x112, 0xf, 0xf, true));
+    case 0x114: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x114, 0xf, 0xf, true));
+    case 0x118: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x118, 0xf, 0xf, true));
+    case 0x142: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x142, 0xa, 0xf, true));
+    default: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x143, 0xc, 0xf, true));
+  }
+  (void)row_mask;
+}
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
+  v += dpp_f(v, 0x111, 0xf);
+  v += dpp_f(v, 0x112, 0xf);
+  v += dpp_f(v, 0x114, 0xf);
+  v += dpp_f(v, 0x118, 0xf);
+  v += dpp_f(v, 0x142, 0xa);
+  v += dpp_f(v, 0x143, 0xc);
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+// max over the wave; -inf fills lanes without a DPP source
+__device__ __forceinline__ float dppm_f(float v, int ctrl) {
+  const int ninf = __float_as_int(-INFINITY);
+  switch (ctrl) {
+    case 0x111: return __int_as_float(__builtin_amdgcn_update_dpp(ninf, __float_as_int(v), 0x111, 0xf, 0xf, false));
+    case 0x112: return __int_as_float(__builtin_amdgcn_update_dpp(ninf, __float_as_int(v), 0x112, 0xf, 0xf, false));
+    case 0x114: return __int_as_float(__builtin_amdgcn_update_dpp(ninf, __float_as_int(v), 0x114, 0xf, 0xf, false));
+    case 0x118: return __int_as_float(__builtin_amdgcn_update_dpp(ninf, __float_as_int(v), 0x118, 0xf, 0xf, false));
+    case 0x142: return __int_as_float(__builtin_amdgcn_update_dpp(ninf, __float_as_int(v), 0x142, 0xa, 0xf, false));
+    default: return __int_as_float(__builtin_amdgcn_update_dpp(ninf, __float_as_int(v), 0x143, 0xc, 0xf, false));
+  }
 }
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
+  v = fmaxf(v, dppm_f(v, 0x111));
+  v = fmaxf(v, dppm_f(v, 0x112));
+  v = fmaxf(v, dppm_f(v, 0x114));
+  v = fmaxf(v, dppm_f(v, 0x118));
+  v = fmaxf(v, dppm_f(v, 0x142));
+  v = fmaxf(v, dppm_f(v, 0x143));
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
 __device__ __forceinline__ void st_tag(uint64_t* p, float v, uint32_t tag) {
@@ -128,103 +185,111 @@ __device__ __forceinline__ uint32_t ld_status(uint32_t* ctrl) {
   return __hip_atomic_load(ctrl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Gather n tagged words into LDS floats; all threads of the workgroup participate.
-// `bad` (workgroup-uniform after the call) records a timeout or an abort seen in the status.
-__device__ void gather(const uint64_t* src, int n, float* dst, uint32_t tag, uint32_t* ctrl,
-                       int* sh_flag, bool& bad) {
-  constexpr int PT = 8;
-  const int tid = threadIdx.x;
-  for (int base = 0; base < n; base += kThreads * PT) {
-    uint64_t w[PT];
+// Poll NW tagged words per lane (word k of lane at src[idx(k)]) until every tag equals
+// `tag`.  A bounded spin: after kSpinLimit rounds, or when another workgroup has reported a
+// timeout in the status word, the wave stops waiting and `bad` is set.
+constexpr int kXW = 12;   // words per lane per exchange wave and batch (3072 words per batch)
+
+// The exchange waves share a gather: 64-word blocks are dealt round-robin to the
+// kWavesX waves (block b -> wave b % kWavesX), so wave ew, lane j handles words
+// 64 * (kWavesX * k + ew) + j.
+__device__ __forceinline__ int xidx(int k, int ew, int lane) { return 64 * (kWavesX * k + ew) + lane; }
+
+__device__ void gather_x(const uint64_t* src, int n, float* dst, uint32_t tag, uint32_t* ctrl,
+                         int ew, int lane, bool& bad) {
+  for (int base = 0; base < n; base += 64 * kWavesX * kXW) {
+    uint64_t w[kXW];
 #pragma unroll
-    for (int j = 0; j < PT; ++j) {
-      const int i = base + tid + j * kThreads;
-      w[j] = (i < n) ? ld_tag(src + i) : (uint64_t(tag) << 32);
+    for (int k = 0; k < kXW; ++k) {
+      const int i = base + xidx(k, ew, lane);
+      w[k] = (i < n) ? ld_tag(src + i) : (uint64_t(tag) << 32);
     }
     uint32_t spins = 0;
-    bool mybad = bad;
-    while (!mybad) {
+    while (!bad) {
       bool ok = true;
 #pragma unroll
-      for (int j = 0; j < PT; ++j) {
-        if (uint32_t(w[j] >> 32) != tag) {
+      for (int k = 0; k < kXW; ++k) {
+        if (uint32_t(w[k] >> 32) != tag) {
           ok = false;
-          w[j] = ld_tag(src + base + tid + j * kThreads);
+          w[k] = ld_tag(src + base + xidx(k, ew, lane));
         }
       }
-      if (ok) break;
+      if (__all(ok)) break;
       ++spins;
-      if ((spins & 255u) == 0 && (ld_status(ctrl) & kStatusTimeout)) mybad = true;
+      if ((spins & 255u) == 0 && (ld_status(ctrl) & kStatusTimeout)) bad = true;
       if (spins > kSpinLimit) {
-        atomicOr(ctrl, kStatusTimeout);
-        mybad = true;
+        if (lane == 0) atomicOr(ctrl, kStatusTimeout);
+        bad = true;
       }
     }
 #pragma unroll
-    for (int j = 0; j < PT; ++j) {
-      const int i = base + tid + j * kThreads;
-      if (i < n) dst[i] = __uint_as_float(uint32_t(w[j]));
+    for (int k = 0; k < kXW; ++k) {
+      const int i = base + xidx(k, ew, lane);
+      if (i < n) dst[i] = __uint_as_float(uint32_t(w[k]));
     }
-    if (mybad) *sh_flag = 1;
   }
-  __syncthreads();
-  bad = bad || (*sh_flag != 0);
 }
 
-// x = scale * (h / sqrt(mean(h^2) + 1e-5))   (model.py:94-98), all threads
-__device__ void rmsnorm(const float* h, const uint16_t* scale, float* x, int d, float* red) {
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  float ss = 0.f;
-  for (int i = tid; i < d; i += kThreads) ss += h[i] * h[i];
-  ss = wave_sum(ss);
-  if (lane == 0) red[wv] = ss;
-  __syncthreads();
-  float tot = 0.f;
-#pragma unroll
-  for (int w = 0; w < kWaves; ++w) tot += red[w];
-  const float r = sqrtf(tot / float(d) + 1e-5f);
-  for (int i = tid; i < d; i += kThreads) x[i] = bf2f(scale[i]) * (h[i] / r);
-  __syncthreads();
+// Synchronise the exchange waves only (the compute waves are not involved): every wave
+// bumps an LDS counter and waits for the other waves' bumps.  `phase` counts calls.
+__device__ __forceinline__ void xsync(int* ctr, int& phase, int lane) {
+  phase += kWavesX;
+  __builtin_amdgcn_s_waitcnt(0xc07f);   // this wave's LDS writes are done (lgkmcnt(0))
+  if (lane == 0) __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+  while (__hip_atomic_load(ctr, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < phase) __builtin_amdgcn_s_sleep(1);
 }
 
-// One row of K bf16 held as NL 16-byte pieces per lane (piece j covers elements
-// [(j*64 + lane)*8, +8)); dot with x (LDS floats), reduced over the wave.
+// Row layout for the matrix-vector products.  A row of K bf16 values is cut into blocks of
+// 512 (the last block may be shorter: S = 8*m values, m lanes); in block b, lane l holds the
+// 16 bytes at packed offset 512*b + 8*l, and its k-th value (k < 8) multiplies input element
+// 512*b + k*m + l.  The packer applies that in-dimension permutation to every row, so the
+// lane's 8 inputs are x[512*b + k*m + l]: consecutive lanes read consecutive LDS words
+// (no bank conflicts) and each lane keeps its inputs in registers for all rows of a phase.
 template <int NL>
 struct Row {
   uint4 v[NL];
 };
+template <int NL>
+struct XV {
+  float v[NL][8];
+};
+
+__device__ __forceinline__ int block_lanes(int k, int b) {
+  const int rem = k - 512 * b;
+  return rem >= 512 ? 64 : (rem > 0 ? rem / 8 : 0);
+}
 
 template <int NL>
 __device__ __forceinline__ void load_row(Row<NL>& r, const uint16_t* row, int k, int lane) {
   const uint4* p = reinterpret_cast<const uint4*>(row);
-  const int n16 = k >> 3;
+#pragma unroll
+  for (int j = 0; j < NL; ++j) r.v[j] = (lane < block_lanes(k, j)) ? p[j * 64 + lane] : make_uint4(0, 0, 0, 0);
+}
+
+template <int NL>
+__device__ __forceinline__ void load_x(XV<NL>& xv, const float* x, int k, int lane) {
 #pragma unroll
   for (int j = 0; j < NL; ++j) {
-    const int i = j * 64 + lane;
-    r.v[j] = (i < n16) ? p[i] : make_uint4(0, 0, 0, 0);
+    const int m = block_lanes(k, j);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) xv.v[j][q] = (lane < m) ? x[512 * j + q * m + lane] : 0.f;
   }
 }
 
 template <int NL>
-__device__ __forceinline__ float dot_row(const Row<NL>& r, const float* x, int k, int lane) {
-  const int n16 = k >> 3;
+__device__ __forceinline__ float dot_row(const Row<NL>& r, const XV<NL>& xv) {
   float acc = 0.f;
 #pragma unroll
   for (int j = 0; j < NL; ++j) {
-    const int i = j * 64 + lane;
-    if (i < n16) {
-      const float4 a = *reinterpret_cast<const float4*>(x + i * 8);
-      const float4 b = *reinterpret_cast<const float4*>(x + i * 8 + 4);
-      const uint4 w = r.v[j];
-      acc += bf_lo(w.x) * a.x;
-      acc += bf_hi(w.x) * a.y;
-      acc += bf_lo(w.y) * a.z;
-      acc += bf_hi(w.y) * a.w;
-      acc += bf_lo(w.z) * b.x;
-      acc += bf_hi(w.z) * b.y;
-      acc += bf_lo(w.w) * b.z;
-      acc += bf_hi(w.w) * b.w;
-    }
+    const uint4 w = r.v[j];
+    acc += bf_lo(w.x) * xv.v[j][0];
+    acc += bf_hi(w.x) * xv.v[j][1];
+    acc += bf_lo(w.y) * xv.v[j][2];
+    acc += bf_hi(w.y) * xv.v[j][3];
+    acc += bf_lo(w.z) * xv.v[j][4];
+    acc += bf_hi(w.z) * xv.v[j][5];
+    acc += bf_lo(w.w) * xv.v[j][6];
+    acc += bf_hi(w.w) * xv.v[j][7];
   }
   return wave_sum(acc);
 }
@@ -241,348 +306,545 @@ __device__ __forceinline__ uint64_t argmax_key(float v, int idx) {
 }
 
 // ---------------------------------------------------------------- kernel
-// D = d_model (compile time), FFL = 16-byte pieces per lane for a d_ff-long row.
-template <int D, int FFL>
-__global__ __launch_bounds__(kThreads, 1) void decode_step_kernel(Args a) {
-  constexpr int NLD = (D + 511) / 512;  // pieces per lane for a d-long row
-  extern __shared__ float smem[];
-  const int G = gridDim.x, wg = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int H = a.H, KV = a.KV, GQ = H / KV, ff = a.ff;
-  const Layout& lay = a.lay;
-  const int ch_max = (a.ctx + kChunks - 1) / kChunks;
+// Workgroup = 4 compute waves + 1 exchange wave.
+//   compute waves: own fixed output rows of every projection; the weights of a phase for
+//     layer l+1 are loaded into registers right after the phase of layer l used them, so
+//     weight streaming runs a whole layer ahead of the dependency chain.
+//   exchange wave: waits for the inputs of the next phase (tagged words), keeps the
+//     residual stream h in its registers, applies the residual adds and RMSNorms, and
+//     writes the next phase's input vector into one of two LDS buffers (alternating).
+// Phases per layer (all waves meet at a workgroup barrier between phases):
+//   B0: x0 = rmsnorm1(h)         | compute: QKV rows (+RoPE, KV write)   | exch: q/k/v of the head group (attention WGs)
+//   B1:                          | compute: attention chunk (attention WGs) | exch: merge (merger WGs), attn -> x1
+//   B2: x1 = attention output    | compute: O rows -> hd1                | exch: h += hd1, x0 = rmsnorm2(h)
+//   B3: x0                       | compute: gate/up rows -> act          | exch: act -> x1
+//   B4: x1 = act                 | compute: down rows -> hd2             | exch: h += hd2, x0 = rmsnorm1'(h)
+constexpr int kThreadsWG = (kWavesC + kWavesX) * 64;
 
-  // LDS carve-up
-  float* sh_h = smem;                                      // D
-  float* sh_x = sh_h + D;                                  // xmax
-  const int xmax = max(max(D, ff), kChunks * GQ * kPartStride);
-  float* sh_k = sh_x + xmax;                               // ch_max * 64
-  float* sh_v = sh_k + ch_max * kDh;                       // ch_max * 64
-  float* sh_q = sh_v + ch_max * kDh;                       // GQ*64 + 128 (q, k_new, v_new)
-  float* sh_e = sh_q + GQ * kDh + 2 * kDh;                 // kWaves * 64
-  float* sh_red = sh_e + kWaves * 64;                      // 64
-  int* sh_flag = reinterpret_cast<int*>(sh_red + 64);      // 1
+// Shared per-step quantities of one workgroup.
+struct Ctx {
+  int G, wg, lane, wv;
+  int H, KV, GQ, ff, L, nch, npart, nqkv;
+  int pos;
+  uint32_t tag;
+  bool att, merger;
+  int ag, ac, q0, q1, P, ncached;
+  float* sh_x0;
+  float* sh_x1;
+  float* sh_k;
+  float* sh_v;
+  float* sh_q;
+  float* sh_e;
+  float* sh_red;
+  int* sh_sync;
+};
 
-  if (tid == 0) *sh_flag = 0;
+__device__ __forceinline__ uint64_t* layer_x(const Args& a, int l) { return a.xw + int64_t(l) * a.lay.x_layer; }
+__device__ __forceinline__ const uint16_t* layer_w(const Args& a, int l) { return a.w + int64_t(l) * a.lay.layer_elems; }
+__device__ __forceinline__ uint16_t* layer_k(const Args& a, int l) { return a.kv + int64_t(l) * 2 * a.KV * a.ctx * kDh; }
+
+// ---------------------------------------------------------------- exchange waves
+// kWavesX waves: gather the inputs of each phase in parallel (gather_x), keep the residual
+// stream h (element xidx(k, ew, lane)), apply the residual adds and the RMSNorms.
+template <int D>
+__device__ void exchange_role(const Args& a, const Ctx& c, int token) {
+  constexpr int HPW = D / (64 * kWavesX);   // residual elements per lane of each exchange wave
+  const int lane = c.lane, ew = c.wv - kWavesC;
   bool bad = false;
-  const uint32_t tag = a.epoch;
-  const int pos = a.pos;
-
-  int token = a.token_dev ? *a.token_dev : a.token;
-  if (token < 0 || token >= a.V) {
-    if (wg == 0 && tid == 0) atomicOr(a.ctrl, kStatusBadToken);
-    token = token < 0 ? 0 : a.V - 1;
-  }
-  // embedding gather (multi_sm_decode.py:88)
-  for (int i = tid; i < D; i += kThreads) sh_h[i] = bf2f(a.emb[int64_t(token) * D + i]);
-  __syncthreads();
-
-  const int nqkv = (H + 2 * KV) * kDh;
-  const float* rope = a.rope + int64_t(pos) * kDh;
-
-  for (int l = 0; l < a.L; ++l) {
-    const uint16_t* W = a.w + int64_t(l) * lay.layer_elems;
-    uint64_t* X = a.xw + int64_t(l) * lay.x_layer;
-    uint16_t* kcache = a.kv + int64_t(l) * 2 * KV * a.ctx * kDh;
-    uint16_t* vcache = kcache + int64_t(KV) * a.ctx * kDh;
-
-    // ---------------- QKV rows, RoPE, KV write (multi_sm_decode.py:121-180)
-    {
-      int p0, p1;
-      split(nqkv / 2, G, wg, p0, p1);
-      const int npairs = p1 - p0;
-      // prefetch this wave's first pair before the norm
-      Row<NLD> r0, r1;
-      const int pf = p0 + wv;
-      if (pf < p1) {
-        load_row(r0, W + lay.off_qkv + int64_t(2 * pf) * D, D, lane);
-        load_row(r1, W + lay.off_qkv + int64_t(2 * pf + 1) * D, D, lane);
+  int sphase = 0;
+  float* ss_slot = c.sh_red + 32;           // per-wave partial sums of squares
+  float h[HPW];
+  float sc[HPW];                            // prefetched RMSNorm scale
+#pragma unroll
+  for (int k = 0; k < HPW; ++k) h[k] = bf2f(a.emb[int64_t(token) * D + xidx(k, ew, lane)]);
+  auto load_scale = [&](const uint16_t* scale) {
+#pragma unroll
+    for (int k = 0; k < HPW; ++k) sc[k] = bf2f(scale[xidx(k, ew, lane)]);
+  };
+  // x = scale * (h / sqrt(mean(h^2) + eps)) into LDS (model.py:94-98)
+  auto norm_to = [&](float* x) {
+    float ss = 0.f;
+#pragma unroll
+    for (int k = 0; k < HPW; ++k) ss += h[k] * h[k];
+    ss = wave_sum(ss);
+    if (lane == 0) ss_slot[(sphase / kWavesX) % 2 * kWavesX + ew] = ss;
+    const int slot = (sphase / kWavesX) % 2;
+    xsync(c.sh_sync, sphase, lane);
+    float tot = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWavesX; ++w) tot += ss_slot[slot * kWavesX + w];
+    const float r = sqrtf(tot / float(D) + 1e-5f);
+#pragma unroll
+    for (int k = 0; k < HPW; ++k) x[xidx(k, ew, lane)] = sc[k] * (h[k] / r);
+  };
+  auto add_h = [&](const uint64_t* src) {
+    uint64_t wd[HPW];
+#pragma unroll
+    for (int k = 0; k < HPW; ++k) wd[k] = ld_tag(src + xidx(k, ew, lane));
+    uint32_t spins = 0;
+    while (!bad) {
+      bool ok = true;
+#pragma unroll
+      for (int k = 0; k < HPW; ++k) {
+        if (uint32_t(wd[k] >> 32) != c.tag) {
+          ok = false;
+          wd[k] = ld_tag(src + xidx(k, ew, lane));
+        }
       }
-      rmsnorm(sh_h, W + lay.off_ln1, sh_x, D, sh_red);
-      for (int p = pf; p < p1; p += kWaves) {
-        if (p != pf) {
-          load_row(r0, W + lay.off_qkv + int64_t(2 * p) * D, D, lane);
-          load_row(r1, W + lay.off_qkv + int64_t(2 * p + 1) * D, D, lane);
-        }
-        const float s0 = dot_row(r0, sh_x, D, lane);
-        const float s1 = dot_row(r1, sh_x, D, lane);
-        const int row = 2 * p;
-        const int head = row / kDh, rr = row % kDh;
-        int i0, i1;
-        float o0, o1;
-        if (head < H + KV) {  // q or k: packed rows (i, i+32), rotate-half (model.py:110-117)
-          const int i = rr / 2;
-          const float c = rope[i], s = rope[kDh / 2 + i];
-          o0 = s0 * c - s1 * s;
-          o1 = s0 * s + s1 * c;
-          i0 = head * kDh + i;
-          i1 = i0 + kDh / 2;
-        } else {
-          o0 = s0;
-          o1 = s1;
-          i0 = head * kDh + rr;
-          i1 = i0 + 1;
-        }
-        if (lane == 0) {
-          st_tag(X + lay.x_qkv + i0, o0, tag);
-          st_tag(X + lay.x_qkv + i1, o1, tag);
-          if (head >= H) {  // K (post-RoPE) or V row of the cache at pos, bf16 (:179-180)
-            const bool isv = head >= H + KV;
-            const int kvh = isv ? head - H - KV : head - H;
-            uint16_t* c = (isv ? vcache : kcache) + (int64_t(kvh) * a.ctx + pos) * kDh;
-            c[i0 - head * kDh] = f2bf(o0);
-            c[i1 - head * kDh] = f2bf(o1);
+      if (__all(ok)) break;
+      ++spins;
+      if ((spins & 255u) == 0 && (ld_status(a.ctrl) & kStatusTimeout)) bad = true;
+      if (spins > kSpinLimit) {
+        if (lane == 0) atomicOr(a.ctrl, kStatusTimeout);
+        bad = true;
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < HPW; ++k) h[k] = h[k] + __uint_as_float(uint32_t(wd[k]));
+  };
+  load_scale(a.w + a.lay.off_ln1);
+  norm_to(c.sh_x0);
+  __syncthreads();
+  for (int l = 0; l < c.L; ++l) {
+    const Layout& lay = a.lay;
+    uint64_t* X = layer_x(a, l);
+    load_scale(layer_w(a, l) + lay.off_ln2);
+    // B0 .. B1: q of the head group and the new k, v for the attention chunk
+    if (c.att) {
+      gather_x(X + lay.x_qkv + int64_t(c.ag) * c.GQ * kDh, c.GQ * kDh, c.sh_q, c.tag, a.ctrl, ew, lane, bad);
+      if (c.pos >= c.q0 && c.pos < c.q1 && ew < 2) {   // current position: un-rounded K/V (multi_sm_decode.py:197,205)
+        const int prow = c.pos - c.q0;
+        const int hh = ew == 0 ? c.H + c.ag : c.H + c.KV + c.ag;
+        float* dst = ew == 0 ? c.sh_k + prow * kKPad : c.sh_v + prow * kDh;
+        uint64_t w = ld_tag(X + lay.x_qkv + int64_t(hh) * kDh + lane);
+        uint32_t spins = 0;
+        while (!bad && uint32_t(w >> 32) != c.tag) {
+          w = ld_tag(X + lay.x_qkv + int64_t(hh) * kDh + lane);
+          if (++spins > kSpinLimit) {
+            if (lane == 0) atomicOr(a.ctrl, kStatusTimeout);
+            bad = true;
           }
         }
-      }
-      (void)npairs;
-    }
-
-    // ---------------- attention over a chunk of positions for one KV head (:182-221)
-    const int n_att = KV * kChunks;
-    if (wg < n_att) {
-      const int g = wg / kChunks, c = wg % kChunks;
-      const int npos = pos + 1;
-      const int cs = (npos + kChunks - 1) / kChunks;
-      const int q0 = c * cs, q1 = min(q0 + cs, npos);
-      const int P = max(0, q1 - q0);
-      // cached rows [q0, min(q1, pos)) -> LDS f32 (these do not depend on this step)
-      const int nc = max(0, min(q1, pos) - q0);
-      for (int t = tid; t < nc * 16; t += kThreads) {
-        const int prow = t >> 4, piece = t & 15;   // 8 pieces of K, 8 of V per row
-        const bool isv = piece >= 8;
-        const uint16_t* src = (isv ? vcache : kcache) + (int64_t(g) * a.ctx + q0 + prow) * kDh + (piece & 7) * 8;
-        const uint4 u = *reinterpret_cast<const uint4*>(src);
-        float* dst = (isv ? sh_v : sh_k) + prow * kDh + (piece & 7) * 8;
-        dst[0] = bf_lo(u.x); dst[1] = bf_hi(u.x); dst[2] = bf_lo(u.y); dst[3] = bf_hi(u.y);
-        dst[4] = bf_lo(u.z); dst[5] = bf_hi(u.z); dst[6] = bf_lo(u.w); dst[7] = bf_hi(u.w);
-      }
-      // q for the GQ heads of group g, and the new k, v (f32, un-rounded: :197, :205)
-      gather(X + lay.x_qkv + int64_t(g) * GQ * kDh, GQ * kDh, sh_q, tag, a.ctrl, sh_flag, bad);
-      gather(X + lay.x_qkv + int64_t(H + g) * kDh, kDh, sh_q + GQ * kDh, tag, a.ctrl, sh_flag, bad);
-      gather(X + lay.x_qkv + int64_t(H + KV + g) * kDh, kDh, sh_q + GQ * kDh + kDh, tag, a.ctrl, sh_flag, bad);
-      if (pos >= q0 && pos < q1) {
-        const int prow = pos - q0;
-        for (int j = tid; j < kDh; j += kThreads) {
-          sh_k[prow * kDh + j] = sh_q[GQ * kDh + j];
-          sh_v[prow * kDh + j] = sh_q[GQ * kDh + kDh + j];
-        }
-      }
-      __syncthreads();
-      for (int n = wv; n < GQ; n += kWaves) {
-        const float* q = sh_q + n * kDh;
-        float s = -INFINITY;
-        if (lane < P) {
-          float acc = 0.f;
-          const float* kr = sh_k + lane * kDh;
-#pragma unroll 16
-          for (int j = 0; j < kDh; ++j) acc += q[j] * kr[j];
-          s = acc * 0.125f;
-        }
-        const float m = wave_max(s);
-        const float e = (lane < P) ? expf(s - m) : 0.f;
-        const float lsum = wave_sum(e);
-        sh_e[wv * 64 + lane] = e;
-        __builtin_amdgcn_wave_barrier();
-        float o = 0.f;
-        for (int p = 0; p < P; ++p) o += sh_e[wv * 64 + p] * sh_v[p * kDh + lane];
-        uint64_t* part = X + lay.x_part + (int64_t(g * kChunks + c) * GQ + n) * kPartStride;
-        if (lane == 0) {
-          st_tag(part + 0, P > 0 ? m : -INFINITY, tag);
-          st_tag(part + 1, lsum, tag);
-        }
-        st_tag(part + 2 + lane, o, tag);
-        __builtin_amdgcn_wave_barrier();
+        dst[lane] = __uint_as_float(uint32_t(w));
       }
     }
-
-    // ---------------- merge the chunks of one KV head (:243-259 LSE merge)
-    if (wg < n_att && (wg % kChunks) == 0) {
-      const int g = wg / kChunks;
-      gather(X + lay.x_part + int64_t(g) * kChunks * GQ * kPartStride, kChunks * GQ * kPartStride,
-             sh_x, tag, a.ctrl, sh_flag, bad);
-      for (int n = wv; n < GQ; n += kWaves) {
+    MSD_TRACE_POINT(ew == 0, 0);
+    __syncthreads();  // B1
+    MSD_TRACE_POINT(ew == 0, 1);
+    // B1 .. B2: merge the chunks of a KV head (multi_sm_decode.py:243-259), attention vector -> x1
+    if (c.merger) {
+      gather_x(X + lay.x_part + int64_t(c.ag) * c.npart, c.npart, c.sh_x1, c.tag, a.ctrl, ew, lane, bad);
+      xsync(c.sh_sync, sphase, lane);
+      for (int n = ew; n < c.GQ; n += kWavesX) {
         float M = -INFINITY;
-        for (int c = 0; c < kChunks; ++c) {
-          const float* pc = sh_x + (c * GQ + n) * kPartStride;
+        for (int ch = 0; ch < c.nch; ++ch) {
+          const float* pc = c.sh_x1 + (ch * c.GQ + n) * kPartStride;
           if (pc[1] > 0.f) M = fmaxf(M, pc[0]);
         }
         float num = 0.f, den = 0.f;
-        for (int c = 0; c < kChunks; ++c) {
-          const float* pc = sh_x + (c * GQ + n) * kPartStride;
+        for (int ch = 0; ch < c.nch; ++ch) {
+          const float* pc = c.sh_x1 + (ch * c.GQ + n) * kPartStride;
           if (pc[1] > 0.f) {
             const float wgt = expf(pc[0] - M);
             num += wgt * pc[2 + lane];
             den += wgt * pc[1];
           }
         }
-        st_tag(X + lay.x_attn + (g * GQ + n) * kDh + lane, num / den, tag);
+        st_tag(X + lay.x_attn + (c.ag * c.GQ + n) * kDh + lane, num / den, c.tag);
       }
-      __syncthreads();
+      xsync(c.sh_sync, sphase, lane);   // the partials in x1 are no longer read
+      MSD_TRACE_POINT(ew == 0, 2);
     }
+    gather_x(X + lay.x_attn, D, c.sh_x1, c.tag, a.ctrl, ew, lane, bad);
+    MSD_TRACE_POINT(ew == 0, 3);
+    __syncthreads();  // B2
+    MSD_TRACE_POINT(ew == 0, 4);
+    // B2 .. B3: h += O output, x0 = rmsnorm2(h)
+    add_h(X + lay.x_hd1);
+    MSD_TRACE_POINT(ew == 0, 5);
+    norm_to(c.sh_x0);
+    MSD_TRACE_POINT(ew == 0, 6);
+    load_scale(l + 1 < c.L ? layer_w(a, l + 1) + lay.off_ln1 : a.lnf);
+    __syncthreads();  // B3
+    MSD_TRACE_POINT(ew == 0, 7);
+    // B3 .. B4: act -> x1
+    gather_x(X + lay.x_act, c.ff, c.sh_x1, c.tag, a.ctrl, ew, lane, bad);
+    MSD_TRACE_POINT(ew == 0, 8);
+    __syncthreads();  // B4
+    MSD_TRACE_POINT(ew == 0, 9);
+    // B4 .. B0': h += down output, x0 = rmsnorm1 of the next layer (or the final norm)
+    add_h(X + lay.x_hd2);
+    MSD_TRACE_POINT(ew == 0, 10);
+    norm_to(c.sh_x0);
+    __syncthreads();  // B0'
+    MSD_TRACE_POINT(ew == 0, 11);
+  }
+  __syncthreads();  // logits done
+}
 
-    // ---------------- O projection rows + residual (:223-232, :244-260)
-    {
-      int r0, r1;
-      split(D, G, wg, r0, r1);
-      Row<NLD> rw;
-      const int rf = r0 + wv;
-      if (rf < r1) load_row(rw, W + lay.off_o + int64_t(rf) * D, D, lane);
-      gather(X + lay.x_attn, D, sh_x, tag, a.ctrl, sh_flag, bad);
-      for (int r = rf; r < r1; r += kWaves) {
-        if (r != rf) load_row(rw, W + lay.off_o + int64_t(r) * D, D, lane);
-        const float y = dot_row(rw, sh_x, D, lane);
-        if (lane == 0) st_tag(X + lay.x_hd1 + r, y, tag);
-      }
-      gather(X + lay.x_hd1, D, sh_x, tag, a.ctrl, sh_flag, bad);
-      for (int i = tid; i < D; i += kThreads) sh_h[i] = sh_h[i] + sh_x[i];
-      __syncthreads();
+// ---------------------------------------------------------------- compute waves
+template <int D, int FFL, int FRW>
+__device__ void compute_role(const Args& a, const Ctx& c) {
+  constexpr int NLD = (D + 511) / 512;
+  const int lane = c.lane, wv = c.wv, ff = c.ff;
+  const Layout& lay = a.lay;
+  const int tidc = wv * 64 + lane;   // index among the compute threads
+  int qp0, qp1, or0, or1, f0, f1;
+  split(c.nqkv / 2, c.G, c.wg, qp0, qp1);
+  split(D, c.G, c.wg, or0, or1);
+  split(ff, c.G, c.wg, f0, f1);
+  const int myqp = qp0 + wv, myor = or0 + wv;
+  const bool has_qp = myqp < qp1, has_or = myor < or1;
+  const float* rope = a.rope + int64_t(c.pos) * kDh;
+  const int nkv16 = c.att ? c.ncached * 16 : 0;   // 16-byte pieces of cached K/V: 8 of K, 8 of V per row
+
+  // Weights are loaded one phase ahead: right after a phase's dot products, the rows of
+  // the next phase are requested, so the loads overlap the exchange that precedes it.
+  Row<NLD> qb0, qb1, ob, gbg[FRW], gbu[FRW];
+  Row<FFL> db;
+  uint4 kvr[4];
+  auto load_qkv = [&](int l) {
+    if (has_qp) {
+      load_row(qb0, layer_w(a, l) + lay.off_qkv + int64_t(2 * myqp) * D, D, lane);
+      load_row(qb1, layer_w(a, l) + lay.off_qkv + int64_t(2 * myqp + 1) * D, D, lane);
     }
-
-    // ---------------- gate/up rows + SwiGLU (:262-289, model.py:159)
-    {
-      int f0, f1;
-      split(ff, G, wg, f0, f1);
-      Row<NLD> rg, ru;
-      const int ffirst = f0 + wv;
-      if (ffirst < f1) {
-        load_row(rg, W + lay.off_gu + int64_t(2 * ffirst) * D, D, lane);
-        load_row(ru, W + lay.off_gu + int64_t(2 * ffirst + 1) * D, D, lane);
+    // cached K/V rows of this workgroup's attention chunk (rows < pos of layer l)
+    uint16_t* kc = layer_k(a, l);
+    uint16_t* vc = kc + int64_t(c.KV) * a.ctx * kDh;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int t = tidc + j * (kWavesC * 64);
+      if (t < nkv16) {
+        const int prow = t >> 4, piece = t & 15;
+        const uint16_t* src = ((piece >= 8) ? vc : kc) + (int64_t(c.ag) * a.ctx + c.q0 + prow) * kDh + (piece & 7) * 8;
+        kvr[j] = *reinterpret_cast<const uint4*>(src);
       }
-      rmsnorm(sh_h, W + lay.off_ln2, sh_x, D, sh_red);
-      for (int f = ffirst; f < f1; f += kWaves) {
-        if (f != ffirst) {
-          load_row(rg, W + lay.off_gu + int64_t(2 * f) * D, D, lane);
-          load_row(ru, W + lay.off_gu + int64_t(2 * f + 1) * D, D, lane);
+    }
+  };
+  auto load_o = [&](int l) { if (has_or) load_row(ob, layer_w(a, l) + lay.off_o + int64_t(myor) * D, D, lane); };
+  auto load_gu = [&](int l) {
+#pragma unroll
+    for (int j = 0; j < FRW; ++j) {
+      const int f = f0 + wv + kWavesC * j;
+      if (f < f1) {
+        load_row(gbg[j], layer_w(a, l) + lay.off_gu + int64_t(2 * f) * D, D, lane);
+        load_row(gbu[j], layer_w(a, l) + lay.off_gu + int64_t(2 * f + 1) * D, D, lane);
+      }
+    }
+  };
+  auto load_dn = [&](int l) { if (has_or) load_row(db, layer_w(a, l) + lay.off_dn + int64_t(myor) * ff, ff, lane); };
+
+  load_qkv(0);
+  __syncthreads();
+  for (int l = 0; l < c.L; ++l) {
+    uint64_t* X = layer_x(a, l);
+    uint16_t* kcache = layer_k(a, l);
+    uint16_t* vcache = kcache + int64_t(c.KV) * a.ctx * kDh;
+
+    // ---- B0 .. B1: QKV rows, RoPE, KV write (multi_sm_decode.py:121-180)
+    MSD_TRACE_POINT(wv == 0, 16);
+    // Stores share the in-order vmcnt counter with loads, so every phase computes its dot
+    // products first, then requests the next phase's weights, and publishes last: later
+    // waits for those weights never wait behind a store.
+    int i0 = 0, i1 = 0, head = 0;
+    float o0 = 0.f, o1 = 0.f;
+    if (has_qp) {
+      XV<NLD> xv;
+      load_x(xv, c.sh_x0, D, lane);
+      const float s0 = dot_row(qb0, xv);
+      const float s1 = dot_row(qb1, xv);
+      const int row = 2 * myqp;
+      head = row / kDh;
+      const int rr = row % kDh;
+      if (head < c.H + c.KV) {  // q or k rows (i, i+32): rotate-half RoPE (model.py:110-117)
+        const int i = rr / 2;
+        const float cs = rope[i], sn = rope[kDh / 2 + i];
+        o0 = s0 * cs - s1 * sn;
+        o1 = s0 * sn + s1 * cs;
+        i0 = head * kDh + i;
+        i1 = i0 + kDh / 2;
+      } else {
+        o0 = s0;
+        o1 = s1;
+        i0 = head * kDh + rr;
+        i1 = i0 + 1;
+      }
+    }
+    MSD_TRACE_POINT(wv == 0, 17);
+    load_o(l);
+    if (has_qp && lane == 0) {
+      st_tag(X + lay.x_qkv + i0, o0, c.tag);
+      st_tag(X + lay.x_qkv + i1, o1, c.tag);
+      if (head >= c.H) {  // K (post-RoPE) or V row of the cache at pos, bf16 (multi_sm_decode.py:179-180)
+        const bool isv = head >= c.H + c.KV;
+        const int kvh = isv ? head - c.H - c.KV : head - c.H;
+        uint16_t* cp = (isv ? vcache : kcache) + (int64_t(kvh) * a.ctx + c.pos) * kDh;
+        cp[i0 - head * kDh] = f2bf(o0);
+        cp[i1 - head * kDh] = f2bf(o1);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int t = tidc + j * (kWavesC * 64);
+      if (t < nkv16) {   // K rows padded to kKPad floats so lanes of the score loop hit distinct banks
+        const int prow = t >> 4, piece = t & 15;
+        float* dst = (piece >= 8) ? c.sh_v + prow * kDh + (piece & 7) * 8 : c.sh_k + prow * kKPad + (piece & 7) * 8;
+        const uint4 u = kvr[j];
+        dst[0] = bf_lo(u.x); dst[1] = bf_hi(u.x); dst[2] = bf_lo(u.y); dst[3] = bf_hi(u.y);
+        dst[4] = bf_lo(u.z); dst[5] = bf_hi(u.z); dst[6] = bf_lo(u.w); dst[7] = bf_hi(u.w);
+      }
+    }
+    __syncthreads();  // B1
+    MSD_TRACE_POINT(wv == 0, 18);
+
+    // ---- B1 .. B2: attention over this chunk, one head per compute wave (multi_sm_decode.py:182-221)
+    if (c.att) {
+      for (int n = wv; n < c.GQ; n += kWavesC) {
+        const float* q = c.sh_q + n * kDh;
+        float s = -INFINITY;
+        if (lane < c.P) {
+          float acc = 0.f;
+          const float* kr = c.sh_k + lane * kKPad;
+#pragma unroll 16
+          for (int j = 0; j < kDh; ++j) acc += q[j] * kr[j];
+          s = acc * 0.125f;
         }
-        const float gt = dot_row(rg, sh_x, D, lane);
-        const float up = dot_row(ru, sh_x, D, lane);
-        const float act = (gt * (1.f / (1.f + expf(-gt)))) * up;
-        if (lane == 0) st_tag(X + lay.x_act + f, act, tag);
+        const float m = wave_max(s);
+        const float e = (lane < c.P) ? expf(s - m) : 0.f;
+        const float lsum = wave_sum(e);
+        c.sh_e[wv * 64 + lane] = e;
+        __builtin_amdgcn_wave_barrier();
+        float o = 0.f;
+        for (int p = 0; p < c.P; ++p) o += c.sh_e[wv * 64 + p] * c.sh_v[p * kDh + lane];
+        uint64_t* part = X + lay.x_part + (int64_t(c.ag * c.nch + c.ac) * c.GQ + n) * kPartStride;
+        if (lane == 0) {
+          st_tag(part + 0, c.P > 0 ? m : -INFINITY, c.tag);
+          st_tag(part + 1, lsum, c.tag);
+        }
+        st_tag(part + 2 + lane, o, c.tag);
+        __builtin_amdgcn_wave_barrier();
+      }
+      MSD_TRACE_POINT(wv == 0, 19);
+    }
+    __syncthreads();  // B2
+    MSD_TRACE_POINT(wv == 0, 20);
+
+    // ---- B2 .. B3: O rows (multi_sm_decode.py:223-232)
+    float yo = 0.f;
+    if (has_or) {
+      XV<NLD> xv;
+      load_x(xv, c.sh_x1, D, lane);
+      yo = dot_row(ob, xv);
+    }
+    MSD_TRACE_POINT(wv == 0, 21);
+    load_gu(l);
+    if (has_or && lane == 0) st_tag(X + lay.x_hd1 + myor, yo, c.tag);
+    __syncthreads();  // B3
+    MSD_TRACE_POINT(wv == 0, 22);
+
+    // ---- B3 .. B4: gate/up rows + SwiGLU (multi_sm_decode.py:262-289, model.py:159)
+    XV<NLD> xg;
+    if (f0 + wv < f1) load_x(xg, c.sh_x0, D, lane);
+    float act[FRW];
+#pragma unroll
+    for (int j = 0; j < FRW; ++j) {
+      const int f = f0 + wv + kWavesC * j;
+      act[j] = 0.f;
+      if (f < f1) {
+        const float gt = dot_row(gbg[j], xg);
+        const float up = dot_row(gbu[j], xg);
+        act[j] = (gt * (1.f / (1.f + expf(-gt)))) * up;
       }
     }
+    MSD_TRACE_POINT(wv == 0, 23);
+    load_dn(l);
+#pragma unroll
+    for (int j = 0; j < FRW; ++j) {
+      const int f = f0 + wv + kWavesC * j;
+      if (f < f1 && lane == 0) st_tag(X + lay.x_act + f, act[j], c.tag);
+    }
+    __syncthreads();  // B4
+    MSD_TRACE_POINT(wv == 0, 24);
 
-    // ---------------- down rows + residual (:273-305)
-    {
-      int r0, r1;
-      split(D, G, wg, r0, r1);
-      Row<FFL> rw;
-      const int rf = r0 + wv;
-      if (rf < r1) load_row(rw, W + lay.off_dn + int64_t(rf) * ff, ff, lane);
-      gather(X + lay.x_act, ff, sh_x, tag, a.ctrl, sh_flag, bad);
-      for (int r = rf; r < r1; r += kWaves) {
-        if (r != rf) load_row(rw, W + lay.off_dn + int64_t(r) * ff, ff, lane);
-        const float y = dot_row(rw, sh_x, ff, lane);
-        if (lane == 0) st_tag(X + lay.x_hd2 + r, y, tag);
+    // ---- B4 .. B0': down rows (multi_sm_decode.py:273-291)
+    float yd = 0.f;
+    if (has_or) {
+      XV<FFL> xv;
+      load_x(xv, c.sh_x1, ff, lane);
+      yd = dot_row(db, xv);
+    }
+    MSD_TRACE_POINT(wv == 0, 25);
+    if (l + 1 < c.L) load_qkv(l + 1);
+    if (has_or && lane == 0) st_tag(X + lay.x_hd2 + myor, yd, c.tag);
+    __syncthreads();  // B0'
+    MSD_TRACE_POINT(wv == 0, 26);
+  }
+  // ---- tied logits over this workgroup's vocabulary rows (multi_sm_decode.py:314-337)
+  int v0, v1;
+  split(a.V, c.G, c.wg, v0, v1);
+  float best = -INFINITY;
+  int besti = 0x7fffffff;
+  constexpr int B = 4;
+  XV<NLD> xv;
+  load_x(xv, c.sh_x0, D, lane);
+  for (int base = v0 + wv * B; base < v1; base += kWavesC * B) {
+    Row<NLD> rr[B];
+#pragma unroll
+    for (int j = 0; j < B; ++j)
+      if (base + j < v1) load_row(rr[j], a.outp + int64_t(base + j) * D, D, lane);
+#pragma unroll
+    for (int j = 0; j < B; ++j) {
+      if (base + j < v1) {
+        const float y = dot_row(rr[j], xv);
+        if (lane == 0) a.logits[base + j] = y;
+        if (y > best) { best = y; besti = base + j; }
       }
-      gather(X + lay.x_hd2, D, sh_x, tag, a.ctrl, sh_flag, bad);
-      for (int i = tid; i < D; i += kThreads) sh_h[i] = sh_h[i] + sh_x[i];
-      __syncthreads();
     }
   }
-
-  // ---------------- final RMSNorm, tied logits, argmax (:314-357, model.py:185-191)
-  rmsnorm(sh_h, a.lnf, sh_x, D, sh_red);
-  {
-    int v0, v1;
-    split(a.V, G, wg, v0, v1);
-    float best = -INFINITY;
-    int besti = 0x7fffffff;
-    constexpr int B = 4;
-    for (int base = v0 + wv * B; base < v1; base += kWaves * B) {
-      Row<NLD> rr[B];
-#pragma unroll
-      for (int j = 0; j < B; ++j)
-        if (base + j < v1) load_row(rr[j], a.emb + int64_t(base + j) * D, D, lane);
-#pragma unroll
-      for (int j = 0; j < B; ++j) {
-        if (base + j < v1) {
-          const float y = dot_row(rr[j], sh_x, D, lane);
-          if (lane == 0) a.logits[base + j] = y;
-          if (y > best) { best = y; besti = base + j; }
-        }
-      }
+  if (lane == 0) {
+    c.sh_red[wv] = best;
+    reinterpret_cast<int*>(c.sh_red)[8 + wv] = besti;
+  }
+  __syncthreads();  // logits done
+  if (wv == 0 && lane == 0) {   // argmax: larger value wins, ties -> lower index (np.argmax)
+    float bv = c.sh_red[0];
+    int bi = reinterpret_cast<int*>(c.sh_red)[8];
+    for (int w = 1; w < kWavesC; ++w) {
+      const float v = c.sh_red[w];
+      const int i = reinterpret_cast<int*>(c.sh_red)[8 + w];
+      if (v > bv || (v == bv && i < bi)) { bv = v; bi = i; }
     }
-    // combine waves: larger value wins, ties -> lower index
-    if (lane == 0) {
-      sh_red[wv] = best;
-      reinterpret_cast<int*>(sh_red)[8 + wv] = besti;
-    }
-    __syncthreads();
-    if (tid == 0) {
-      float bv = sh_red[0];
-      int bi = reinterpret_cast<int*>(sh_red)[8];
-      for (int w = 1; w < kWaves; ++w) {
-        const float v = sh_red[w];
-        const int i = reinterpret_cast<int*>(sh_red)[8 + w];
-        if (v > bv || (v == bv && i < bi)) { bv = v; bi = i; }
-      }
-      uint64_t* keyp = reinterpret_cast<uint64_t*>(a.ctrl + 2);
-      if (bi != 0x7fffffff)
-        __hip_atomic_fetch_max(keyp, argmax_key(bv, bi), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      // the max above returns before the arrival below is issued
-      __builtin_amdgcn_s_waitcnt(0);
-      const uint32_t old = __hip_atomic_fetch_add(a.ctrl + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if ((old % uint32_t(G)) == uint32_t(G - 1)) {   // last arriver publishes the token
-        const uint64_t key = __hip_atomic_load(keyp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        a.next_token[0] = int32_t(0xffffffffu - uint32_t(key & 0xffffffffu));
-        a.next_token[1] = int32_t(ld_status(a.ctrl));
-        __hip_atomic_store(keyp, uint64_t(0), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
+    uint64_t* keyp = reinterpret_cast<uint64_t*>(a.ctrl + 2);
+    if (bi != 0x7fffffff)
+      __hip_atomic_fetch_max(keyp, argmax_key(bv, bi), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // the max above completes before the arrival below is issued
+    __builtin_amdgcn_s_waitcnt(0);
+    const uint32_t old = __hip_atomic_fetch_add(a.ctrl + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if ((old % uint32_t(c.G)) == uint32_t(c.G - 1)) {   // last arriver publishes the token
+      const uint64_t key = __hip_atomic_load(keyp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      a.next_token[0] = int32_t(0xffffffffu - uint32_t(key & 0xffffffffu));
+      a.next_token[1] = int32_t(ld_status(a.ctrl));
+      __hip_atomic_store(keyp, uint64_t(0), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
-  (void)bad;
+}
+
+template <int D, int FFL, int FRW>
+__global__ __launch_bounds__(kThreadsWG, 1) void decode_step_kernel(Args a) {
+  extern __shared__ float smem[];
+  Ctx c;
+  c.G = gridDim.x;
+  c.wg = blockIdx.x;
+  c.lane = threadIdx.x & 63;
+  c.wv = threadIdx.x >> 6;
+  c.H = a.H;
+  c.KV = a.KV;
+  c.GQ = a.H / a.KV;
+  c.ff = a.ff;
+  c.L = a.L;
+  c.nch = a.nch;
+  c.npart = c.nch * c.GQ * kPartStride;
+  c.nqkv = (a.H + 2 * a.KV) * kDh;
+  c.pos = a.pos;
+  c.tag = a.epoch;
+  const int ch_max = (a.ctx + c.nch - 1) / c.nch;
+  // attention: workgroup i < KV*nch handles KV head i / nch, position chunk i % nch
+  c.att = c.wg < c.KV * c.nch;
+  c.ag = c.wg / c.nch;
+  c.ac = c.wg % c.nch;
+  c.merger = c.att && c.ac == 0;
+  const int npos = c.pos + 1;
+  const int cs = (npos + c.nch - 1) / c.nch;
+  c.q0 = min(c.ac * cs, npos);
+  c.q1 = min(c.q0 + cs, npos);
+  c.P = c.q1 - c.q0;
+  c.ncached = max(0, min(c.q1, c.pos) - c.q0);
+  const int xmax = max(max(D, c.ff), c.npart);
+  c.sh_x0 = smem;
+  c.sh_x1 = c.sh_x0 + D;
+  c.sh_k = c.sh_x1 + xmax;
+  c.sh_v = c.sh_k + ch_max * kKPad;
+  c.sh_q = c.sh_v + ch_max * kDh;
+  c.sh_e = c.sh_q + c.GQ * kDh;
+  c.sh_red = c.sh_e + kWavesC * 64;
+  c.sh_sync = reinterpret_cast<int*>(c.sh_red + 64);
+  if (threadIdx.x == 0) *c.sh_sync = 0;
+  __syncthreads();
+
+  int token = a.token_dev ? *a.token_dev : a.token;
+  if (token < 0 || token >= a.V) {
+    if (c.wg == 0 && threadIdx.x == 0) atomicOr(a.ctrl, kStatusBadToken);
+    token = token < 0 ? 0 : a.V - 1;
+  }
+  if (c.wv >= kWavesC) exchange_role<D>(a, c, token);
+  else compute_role<D, FFL, FRW>(a, c);
 }
 
 // ---------------------------------------------------------------- host side
+struct Plan {   // per-config launch parameters
+  int frw;      // gate/up rows per compute wave
+  int ffl;      // 16-byte pieces per lane of a d_ff row
+  size_t lds;
+};
+
 static bool config_ok(const msd_config* c) {
   if (!c) return false;
   if (c->d_head != kDh || c->n_heads <= 0 || c->n_kv_heads <= 0 || c->n_layers <= 0) return false;
   if (c->n_heads * kDh != c->d_model || c->n_heads % c->n_kv_heads != 0) return false;
   if (c->d_ff <= 0 || c->d_ff % 16 != 0 || c->vocab_size <= 0 || c->context_len <= 0) return false;
-  if ((c->context_len + kChunks - 1) / kChunks > 64) return false;   // chunk fits a wave
+  if (c->context_len > 1024) return false;
   if (c->d_model != 256 && c->d_model != 1024) return false;
-  if ((c->d_ff + 511) / 512 > 8) return false;
   return true;
 }
 
-static size_t lds_bytes(const msd_config* c) {
+static int cdiv(int a, int b) { return (a + b - 1) / b; }
+
+// Shapes the kernel instantiations cover for n_workgroups workgroups; false if unsupported.
+static bool make_plan(const msd_config* c, int G, Plan* p) {
+  if (!config_ok(c) || G <= 0) return false;
+  const int nqkv = (c->n_heads + 2 * c->n_kv_heads) * kDh;
+  if (cdiv(nqkv / 2, G) > kWavesC || cdiv(c->d_model, G) > kWavesC) return false;
+  if (c->n_kv_heads * n_chunks(c->context_len) > G) return false;
+  p->frw = cdiv(cdiv(c->d_ff, G), kWavesC);
+  p->ffl = cdiv(c->d_ff, 512);
   const int GQ = c->n_heads / c->n_kv_heads;
-  const int ch_max = (c->context_len + kChunks - 1) / kChunks;
-  const int xmax = std::max(std::max(c->d_model, c->d_ff), kChunks * GQ * kPartStride);
-  const size_t floats = size_t(c->d_model) + xmax + 2 * ch_max * kDh + GQ * kDh + 2 * kDh + kWaves * 64 + 64 + 4;
-  return floats * 4;
+  const int nch = n_chunks(c->context_len);
+  const int ch_max = cdiv(c->context_len, nch);
+  const int xmax = std::max(std::max(c->d_model, c->d_ff), nch * GQ * kPartStride);
+  const size_t floats = size_t(c->d_model) + xmax + ch_max * (kKPad + kDh) + GQ * kDh + kWavesC * 64 + 64 + 4;
+  p->lds = floats * 4;
+  return true;
 }
 
 // At least this much LDS per workgroup, so that no two workgroups of a step share a
 // compute unit (160 KB per CU): the grid then spreads over every CU.
 constexpr size_t kMinLds = 84 * 1024;
 
-template <int D, int FFL>
+template <int D, int FFL, int FRW>
 static hipError_t launch_t(const Args& a, int grid, size_t lds, hipStream_t s) {
   static bool attr_set = false;
   if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&decode_step_kernel<D, FFL>),
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&decode_step_kernel<D, FFL, FRW>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
     if (e != hipSuccess) return e;
     attr_set = true;
   }
-  hipLaunchKernelGGL((decode_step_kernel<D, FFL>), dim3(grid), dim3(kThreads), lds, s, a);
+  hipLaunchKernelGGL((decode_step_kernel<D, FFL, FRW>), dim3(grid), dim3(kThreadsWG), lds, s, a);
   return hipGetLastError();
 }
 
-template <int D>
-static hipError_t launch_ff(const Args& a, int grid, size_t lds, hipStream_t s) {
-  switch ((a.ff + 511) / 512) {
-    case 1: return launch_t<D, 1>(a, grid, lds, s);
-    case 2: return launch_t<D, 2>(a, grid, lds, s);
-    case 3: return launch_t<D, 3>(a, grid, lds, s);
-    case 4: return launch_t<D, 4>(a, grid, lds, s);
-    case 5: return launch_t<D, 5>(a, grid, lds, s);
-    case 6: return launch_t<D, 6>(a, grid, lds, s);
-    case 7: return launch_t<D, 7>(a, grid, lds, s);
-    case 8: return launch_t<D, 8>(a, grid, lds, s);
-  }
+// Instantiated shapes: (d_model, ceil(d_ff/512), gate/up rows per wave).
+static hipError_t launch(const Args& a, const Plan& p, int d, int grid, size_t lds, hipStream_t s) {
+  if (d == 256 && p.ffl == 2 && p.frw == 1) return launch_t<256, 2, 1>(a, grid, lds, s);
+  if (d == 1024 && p.ffl == 6 && p.frw == 3) return launch_t<1024, 6, 3>(a, grid, lds, s);
+  if (d == 1024 && p.ffl == 6 && p.frw == 1) return launch_t<1024, 6, 1>(a, grid, lds, s);
+  if (d == 256 && p.ffl == 2 && p.frw == 3) return launch_t<256, 2, 3>(a, grid, lds, s);
   return hipErrorInvalidValue;
+}
+
+static bool plan_instantiated(const msd_config* c, const Plan& p) {
+  return (c->d_model == 256 && p.ffl == 2 && (p.frw == 1 || p.frw == 3)) ||
+         (c->d_model == 1024 && p.ffl == 6 && (p.frw == 1 || p.frw == 3));
 }
 
 }  // namespace msd
@@ -591,13 +853,15 @@ using namespace msd;
 
 extern "C" int64_t msd_packed_weight_elems(const msd_config* cfg) {
   if (!config_ok(cfg)) return MSD_E_CONFIG;
-  return make_layout(cfg->d_model, cfg->n_heads, cfg->n_kv_heads, cfg->d_ff).layer_elems * cfg->n_layers;
+  return make_layout(cfg->d_model, cfg->n_heads, cfg->n_kv_heads, cfg->d_ff, cfg->context_len).layer_elems *
+         cfg->n_layers;
 }
 
 extern "C" int64_t msd_workspace_bytes(const msd_config* cfg, int32_t n_workgroups) {
+  Plan p;
   if (!config_ok(cfg)) return MSD_E_CONFIG;
-  if (n_workgroups < cfg->n_kv_heads * kChunks) return MSD_E_ARG;
-  const Layout t = make_layout(cfg->d_model, cfg->n_heads, cfg->n_kv_heads, cfg->d_ff);
+  if (!make_plan(cfg, n_workgroups, &p) || !plan_instantiated(cfg, p)) return MSD_E_CONFIG;
+  const Layout t = make_layout(cfg->d_model, cfg->n_heads, cfg->n_kv_heads, cfg->d_ff, cfg->context_len);
   return t.ctrl_bytes + t.x_layer * cfg->n_layers * int64_t(sizeof(uint64_t));
 }
 
@@ -607,22 +871,27 @@ extern "C" int32_t msd_default_workgroups(int32_t device) {
   return n;
 }
 
-extern "C" int32_t msd_decode_step(const msd_config* cfg, const void* token_emb, const void* packed_w,
-                                   const void* lnf_s, const float* rope, int32_t token_id,
+extern "C" int32_t msd_decode_step(const msd_config* cfg, const void* token_emb, const void* output_proj,
+                                   const void* packed_w, const void* lnf_s, const float* rope, int32_t token_id,
                                    const int32_t* token_dev, int32_t pos, void* kv, void* workspace,
                                    uint32_t epoch, float* logits, int32_t* next_token,
                                    int32_t n_workgroups, void* stream) {
+  Plan p;
   if (!config_ok(cfg)) return MSD_E_CONFIG;
-  if (!token_emb || !packed_w || !lnf_s || !rope || !kv || !workspace || !logits || !next_token) return MSD_E_ARG;
+  if (n_workgroups <= 0 || n_workgroups > 4096) return MSD_E_ARG;
+  if (!make_plan(cfg, n_workgroups, &p) || !plan_instantiated(cfg, p)) return MSD_E_CONFIG;
+  if (!token_emb || !output_proj || !packed_w || !lnf_s || !rope || !kv || !workspace || !logits || !next_token)
+    return MSD_E_ARG;
   if (pos < 0 || pos >= cfg->context_len) return MSD_E_ARG;
   if (!token_dev && (token_id < 0 || token_id >= cfg->vocab_size)) return MSD_E_ARG;
-  if (n_workgroups < cfg->n_kv_heads * kChunks || n_workgroups > 4096) return MSD_E_ARG;
   if (epoch == 0) return MSD_E_ARG;
   const uintptr_t al = reinterpret_cast<uintptr_t>(token_emb) | reinterpret_cast<uintptr_t>(packed_w) |
+                       reinterpret_cast<uintptr_t>(output_proj) |
                        reinterpret_cast<uintptr_t>(kv) | reinterpret_cast<uintptr_t>(workspace);
   if (al & 15) return MSD_E_ARG;
   Args a;
   a.emb = static_cast<const uint16_t*>(token_emb);
+  a.outp = static_cast<const uint16_t*>(output_proj);
   a.w = static_cast<const uint16_t*>(packed_w);
   a.lnf = static_cast<const uint16_t*>(lnf_s);
   a.rope = rope;
@@ -631,7 +900,7 @@ extern "C" int32_t msd_decode_step(const msd_config* cfg, const void* token_emb,
   a.next_token = next_token;
   a.token_dev = token_dev;
   a.ctrl = static_cast<uint32_t*>(workspace);
-  a.lay = make_layout(cfg->d_model, cfg->n_heads, cfg->n_kv_heads, cfg->d_ff);
+  a.lay = make_layout(cfg->d_model, cfg->n_heads, cfg->n_kv_heads, cfg->d_ff, cfg->context_len);
   a.xw = reinterpret_cast<uint64_t*>(static_cast<char*>(workspace) + a.lay.ctrl_bytes);
   a.token = token_id;
   a.pos = pos;
@@ -642,14 +911,9 @@ extern "C" int32_t msd_decode_step(const msd_config* cfg, const void* token_emb,
   a.ff = cfg->d_ff;
   a.V = cfg->vocab_size;
   a.ctx = cfg->context_len;
-  const size_t lds = std::max(lds_bytes(cfg), kMinLds);
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  hipError_t e;
-  switch (cfg->d_model) {
-    case 256: e = launch_ff<256>(a, n_workgroups, lds, s); break;
-    case 1024: e = launch_ff<1024>(a, n_workgroups, lds, s); break;
-    default: return MSD_E_CONFIG;
-  }
+  a.nch = n_chunks(cfg->context_len);
+  const size_t lds = std::max(p.lds, kMinLds);
+  const hipError_t e = launch(a, p, cfg->d_model, n_workgroups, lds, static_cast<hipStream_t>(stream));
   return e == hipSuccess ? MSD_OK : MSD_E_HIP;
 }
 
@@ -666,3 +930,9 @@ extern "C" int32_t msd_check_status(void* workspace, void* stream) {
   if (st & kStatusTimeout) return MSD_E_TIMEOUT;
   return MSD_E_ARG;
 }
+
+#ifdef MSD_TRACE
+extern "C" int msd_trace_copy(void* host) {
+  return hipMemcpyFromSymbol(host, HIP_SYMBOL(msd::msd_trace_buffer), sizeof(uint64_t) * 4096 * 32) == hipSuccess ? 0 : -1;
+}
+#endif

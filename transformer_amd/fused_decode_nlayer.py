@@ -13,12 +13,15 @@ Every output element of a projection is one contiguous row (the transpose of the
 reference's (in, out) matrices, fused_decode_nlayer.py:260-268), so the kernel reads
 each output's weights as one run of 128-bit loads.  Within each q and k head the rows
 are ordered (0, 32, 1, 33, ..., 31, 63) so a rotate-half RoPE pair (model.py:110-117)
-is two adjacent rows.
+is two adjacent rows.  Within every row the input dimension is permuted by
+``kernel_perm`` (blocks of 512; in block b, position 8*l + k holds input 512*b + k*m + l,
+m = lanes of the block), so each lane of a wave multiplies its 8 loaded weights with
+inputs that consecutive lanes read from consecutive LDS words.
 
-The reference also builds ``output_proj_padded`` (the transposed, padded embedding,
-fused_decode_nlayer.py:312-319); the kernel reads ``token_emb`` rows directly for the
-tied logits, so that copy is not made.  ``vocab_pad`` is still reported as the reference
-computes it.  RoPE tables stay float32 (model.py:101-107) instead of the reference's bf16
+The reference's ``output_proj_padded`` (the transposed, padded embedding,
+fused_decode_nlayer.py:312-319) becomes ``output_proj``: the (V, d) embedding with every
+row in the kernel row layout (no transpose, no padding).  ``vocab_pad`` is still
+reported as the reference computes it.  RoPE tables stay float32 (model.py:101-107) instead of the reference's bf16
 copies (fused_decode_nlayer.py:317-318); ``rope`` holds them as one (ctx, d_head) table.
 """
 import numpy as np
@@ -35,6 +38,19 @@ def _bf16(a, device):
     if isinstance(a, torch.Tensor):
         return a.to(device=device, dtype=torch.bfloat16)
     return torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(torch.bfloat16).to(device)
+
+
+def kernel_perm(k):
+    """Index array p with packed_row = row[p] for the kernel row layout of a k-long row."""
+    assert k % 8 == 0
+    p = np.empty(k, dtype=np.int64)
+    for b in range(0, k, 512):
+        s = min(512, k - b)
+        m = s // 8
+        lanes = np.arange(m)
+        for q in range(8):
+            p[b + 8 * lanes + q] = b + q * m + lanes
+    return torch.from_numpy(p)
 
 
 def _rope_perm(dh=64):
@@ -58,14 +74,16 @@ def pack_layer(params, config, i, device=None):
     dh = config.get("d_head", d // H)
     p = f"layer{i}"
     perm = _rope_perm(dh).to(dev)
-    wq = _bf16(params[f"{p}.attn.q"], dev).t().reshape(H, dh, d)[:, perm].reshape(H * dh, d)
-    wk = _bf16(params[f"{p}.attn.k"], dev).t().reshape(KV, dh, d)[:, perm].reshape(KV * dh, d)
-    wv = _bf16(params[f"{p}.attn.v"], dev).t()
-    wo = _bf16(params[f"{p}.attn.o"], dev).t()
-    g = _bf16(params[f"{p}.ffn.gate"], dev).t()
-    u = _bf16(params[f"{p}.ffn.up"], dev).t()
+    kd = kernel_perm(d).to(dev)
+    kf = kernel_perm(config["d_ff"]).to(dev)
+    wq = _bf16(params[f"{p}.attn.q"], dev).t().reshape(H, dh, d)[:, perm].reshape(H * dh, d)[:, kd]
+    wk = _bf16(params[f"{p}.attn.k"], dev).t().reshape(KV, dh, d)[:, perm].reshape(KV * dh, d)[:, kd]
+    wv = _bf16(params[f"{p}.attn.v"], dev).t()[:, kd]
+    wo = _bf16(params[f"{p}.attn.o"], dev).t()[:, kd]
+    g = _bf16(params[f"{p}.ffn.gate"], dev).t()[:, kd]
+    u = _bf16(params[f"{p}.ffn.up"], dev).t()[:, kd]
     gu = torch.stack([g, u], dim=1).reshape(-1, d)
-    dn = _bf16(params[f"{p}.ffn.down"], dev).t()
+    dn = _bf16(params[f"{p}.ffn.down"], dev).t()[:, kf]
     parts = [_bf16(params[f"{p}.ln1.scale"], dev).reshape(-1), _bf16(params[f"{p}.ln2.scale"], dev).reshape(-1),
              wq, wk, wv, wo, gu, dn]
     return torch.cat([t.contiguous().reshape(-1) for t in parts])
@@ -117,8 +135,9 @@ def new_kv_packed(config, device=None):
 def prepare_decode_weights_nlayer(params, config, kv_splits=1, device=None):
     """Decode weight dict (reference: fused_decode_nlayer.py:299-321).
 
-    Keys: token_emb (V, d) bf16, packed_w (kernel layout), lnf_s (d) bf16, cos/sin
-    (ctx, d_head/2) f32, rope (ctx, d_head) f32 = [cos | sin], vocab_pad (reference value).
+    Keys: token_emb (V, d) bf16, output_proj (V, d) bf16 in the kernel row layout,
+    packed_w (kernel layout), lnf_s (d) bf16, cos/sin (ctx, d_head/2) f32,
+    rope (ctx, d_head) f32 = [cos | sin], vocab_pad (reference value).
     """
     from .configs import check_config
     dh = check_config(config)
@@ -128,8 +147,10 @@ def prepare_decode_weights_nlayer(params, config, kv_splits=1, device=None):
     vocab_pad = ((vocab + align - 1) // align) * align
     cos, sin = precompute_rope_table(config["context_len"], dh)
     rope = np.concatenate([cos, sin], axis=1)
+    emb = _bf16(params["token_emb"], dev).contiguous()
     return {
-        "token_emb": _bf16(params["token_emb"], dev).contiguous(),
+        "token_emb": emb,
+        "output_proj": emb[:, kernel_perm(config["d_model"]).to(dev)].contiguous(),
         "packed_w": pack_weights(params, config, dev),
         "lnf_s": _bf16(params["ln_final.scale"], dev).contiguous(),
         "cos": torch.from_numpy(cos).to(dev),

@@ -73,7 +73,8 @@ class Decoder:
         s = stream if stream is not None else torch.cuda.current_stream(self.device)
         w = self.w
         rc = _lib.lib().msd_decode_step(
-            ctypes.byref(self._cfg), w["token_emb"].data_ptr(), w["packed_w"].data_ptr(),
+            ctypes.byref(self._cfg), w["token_emb"].data_ptr(), w["output_proj"].data_ptr(),
+            w["packed_w"].data_ptr(),
             w["lnf_s"].data_ptr(), w["rope"].data_ptr(), tok, tok_dev, pos, self.kv.data_ptr(),
             self.workspace.data_ptr(), self.epoch, self.logits.data_ptr(), out.data_ptr(),
             self.n_workgroups, ctypes.c_void_p(s.cuda_stream))
