@@ -72,14 +72,19 @@ struct Layout {
   // exchange words per layer (uint64)
   int64_t x_qkv, x_part, x_attn, x_hd1, x_act, x_hd2, x_layer;
   int64_t ctrl_bytes;
+  // producer flags: flags[(layer * kNumEx + exchange) * G + producer_workgroup] (uint32)
+  int64_t flag_words;   // uint32 flags per layer
 };
+
+// exchanges of a layer (index into the flag arrays)
+enum { kExQkv = 0, kExPart = 1, kExAttn = 2, kExHd1 = 3, kExAct = 4, kExHd2 = 5, kNumEx = 6 };
 
 __host__ __device__ inline int64_t align64(int64_t v) { return (v + 63) & ~int64_t(63); }
 
 // attention chunks per KV head: enough that a chunk of the full context fits a wave
 __host__ __device__ inline int n_chunks(int ctx) { return (ctx + kChunkMax - 1) / kChunkMax; }
 
-__host__ __device__ inline Layout make_layout(int d, int H, int KV, int ff, int ctx) {
+__host__ __device__ inline Layout make_layout(int d, int H, int KV, int ff, int ctx, int G = 0) {
   Layout t;
   const int64_t nqkv = int64_t(H + 2 * KV) * kDh;
   t.off_ln1 = 0;
@@ -98,6 +103,7 @@ __host__ __device__ inline Layout make_layout(int d, int H, int KV, int ff, int 
   t.x_hd2 = t.x_act + align64(ff);
   t.x_layer = t.x_hd2 + align64(d);
   t.ctrl_bytes = 256;
+  t.flag_words = int64_t(kNumEx) * G;
   return t;
 }
 
@@ -113,6 +119,7 @@ struct Args {
   const int32_t* token_dev;
   uint32_t* ctrl;   // [0] status, [1] arrival counter, [2..3] argmax key (u64)
   uint64_t* xw;     // exchange words, n_layers * x_layer
+  uint32_t* flags;  // producer flags, n_layers * flag_words
   int token, pos;
   uint32_t epoch;
   int H, KV, L, ff, V, ctx, nch;
@@ -181,6 +188,12 @@ __device__ __forceinline__ void st_tag(uint64_t* p, float v, uint32_t tag) {
 __device__ __forceinline__ uint64_t ld_tag(const uint64_t* p) {
   return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+__device__ __forceinline__ void st_flag(uint32_t* p, uint32_t tag) {
+  __hip_atomic_store(p, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t ld_flag(const uint32_t* p) {
+  return __hip_atomic_load(const_cast<uint32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 __device__ __forceinline__ uint32_t ld_status(uint32_t* ctrl) {
   return __hip_atomic_load(ctrl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -228,6 +241,57 @@ __device__ void gather_x(const uint64_t* src, int n, float* dst, uint32_t tag, u
       if (i < n) dst[i] = __uint_as_float(uint32_t(w[k]));
     }
   }
+}
+
+// Producer-flag gating of gathers.  With MSD_FLAG_POLL defined, consumers first wait for the
+// producers' flags and then read the data; otherwise they poll the tagged data words
+// directly (one round trip less; the flags are still raised).
+#ifdef MSD_FLAG_POLL
+constexpr bool kFlagPoll = true;
+#else
+constexpr bool kFlagPoll = false;
+#endif
+
+// Wait until the producer flags f[0..n) all equal `tag` (one wave; bounded spin).  A
+// producer raises its flag after issuing its tagged data words, so a consumer polls n
+// 4-byte flags instead of all data words; the data words are still validated by their tags.
+__device__ void poll_flags(const uint32_t* f, int n, uint32_t tag, uint32_t* ctrl, int lane, bool& bad) {
+  if (!kFlagPoll) return;
+  for (int base = 0; base < n; base += 64 * 4) {
+    uint32_t v[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int i = base + lane + 64 * k;
+      v[k] = (i < n) ? ld_flag(f + i) : tag;
+    }
+    uint32_t spins = 0;
+    while (!bad) {
+      bool ok = true;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        if (v[k] != tag) {
+          ok = false;
+          v[k] = ld_flag(f + base + lane + 64 * k);
+        }
+      }
+      if (__all(ok)) break;
+      ++spins;
+      if ((spins & 255u) == 0 && (ld_status(ctrl) & kStatusTimeout)) bad = true;
+      if (spins > kSpinLimit) {
+        if (lane == 0) atomicOr(ctrl, kStatusTimeout);
+        bad = true;
+      }
+    }
+  }
+}
+
+// LDS spin-wait until *ctr >= target (intra-workgroup hand-off between wave roles).
+__device__ __forceinline__ void lds_wait(int* ctr, int target) {
+  while (__hip_atomic_load(ctr, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < target) __builtin_amdgcn_s_sleep(1);
+}
+__device__ __forceinline__ void lds_bump(int* ctr, int lane) {
+  __builtin_amdgcn_s_waitcnt(0xc07f);   // this wave's LDS writes are done (lgkmcnt(0))
+  if (lane == 0) __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
 // Synchronise the exchange waves only (the compute waves are not involved): every wave
@@ -294,6 +358,29 @@ __device__ __forceinline__ float dot_row(const Row<NL>& r, const XV<NL>& xv) {
   return wave_sum(acc);
 }
 
+// Same as dot_row, with the lane's inputs read from LDS block by block (single-row phases).
+template <int NL>
+__device__ __forceinline__ float dot_row_lds(const Row<NL>& r, const float* x, int k, int lane) {
+  float acc = 0.f;
+#pragma unroll
+  for (int j = 0; j < NL; ++j) {
+    const int m = block_lanes(k, j);
+    float xv[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) xv[q] = (lane < m) ? x[512 * j + q * m + lane] : 0.f;
+    const uint4 w = r.v[j];
+    acc += bf_lo(w.x) * xv[0];
+    acc += bf_hi(w.x) * xv[1];
+    acc += bf_lo(w.y) * xv[2];
+    acc += bf_hi(w.y) * xv[3];
+    acc += bf_lo(w.z) * xv[4];
+    acc += bf_hi(w.z) * xv[5];
+    acc += bf_lo(w.w) * xv[6];
+    acc += bf_hi(w.w) * xv[7];
+  }
+  return wave_sum(acc);
+}
+
 __device__ __forceinline__ void split(int total, int parts, int idx, int& lo, int& hi) {
   lo = int((int64_t(total) * idx) / parts);
   hi = int((int64_t(total) * (idx + 1)) / parts);
@@ -337,26 +424,38 @@ struct Ctx {
   float* sh_e;
   float* sh_red;
   int* sh_sync;
+  // mailbox from compute waves to the publishing exchange wave
+  float* mb_val;   // kWavesC * kMbox values
+  int* mb_idx;     // word index in the layer's exchange words, -1 = unused
+  int* mb_out;     // compute waves: outputs written (bumped once per wave and phase)
+  int* mb_pub;     // exchange wave 0: outputs published (bumped once per phase)
 };
+
+constexpr int kMbox = 4;   // outputs per compute wave and phase
 
 __device__ __forceinline__ uint64_t* layer_x(const Args& a, int l) { return a.xw + int64_t(l) * a.lay.x_layer; }
 __device__ __forceinline__ const uint16_t* layer_w(const Args& a, int l) { return a.w + int64_t(l) * a.lay.layer_elems; }
 __device__ __forceinline__ uint16_t* layer_k(const Args& a, int l) { return a.kv + int64_t(l) * 2 * a.KV * a.ctx * kDh; }
 
 // ---------------------------------------------------------------- exchange waves
-// kWavesX waves: gather the inputs of each phase in parallel (gather_x), keep the residual
-// stream h (element xidx(k, ew, lane)), apply the residual adds and the RMSNorms.
+// kWavesX waves.  Per phase they first publish this workgroup's outputs (exchange wave 0
+// takes them from the compute waves' LDS mailbox, stores the tagged words, then raises the
+// workgroup's flag), then wait for the producer flags of the next input and gather it in
+// parallel (gather_x).  They keep the residual stream h (element xidx(k, ew, lane)) and
+// apply the residual adds and the RMSNorms.
 template <int D>
 __device__ void exchange_role(const Args& a, const Ctx& c, int token) {
   constexpr int HPW = D / (64 * kWavesX);   // residual elements per lane of each exchange wave
   const int lane = c.lane, ew = c.wv - kWavesC;
+  const int G = c.G;
   bool bad = false;
-  int sphase = 0;
+  int sphase = 0, pphase = 0, aphase = 0;
   float* ss_slot = c.sh_red + 32;           // per-wave partial sums of squares
   float h[HPW];
   float sc[HPW];                            // prefetched RMSNorm scale
 #pragma unroll
   for (int k = 0; k < HPW; ++k) h[k] = bf2f(a.emb[int64_t(token) * D + xidx(k, ew, lane)]);
+  auto flagp = [&](int l, int ex) { return a.flags + (int64_t(l) * kNumEx + ex) * G; };
   auto load_scale = [&](const uint16_t* scale) {
 #pragma unroll
     for (int k = 0; k < HPW; ++k) sc[k] = bf2f(scale[xidx(k, ew, lane)]);
@@ -367,8 +466,8 @@ __device__ void exchange_role(const Args& a, const Ctx& c, int token) {
 #pragma unroll
     for (int k = 0; k < HPW; ++k) ss += h[k] * h[k];
     ss = wave_sum(ss);
-    if (lane == 0) ss_slot[(sphase / kWavesX) % 2 * kWavesX + ew] = ss;
     const int slot = (sphase / kWavesX) % 2;
+    if (lane == 0) ss_slot[slot * kWavesX + ew] = ss;
     xsync(c.sh_sync, sphase, lane);
     float tot = 0.f;
 #pragma unroll
@@ -402,6 +501,18 @@ __device__ void exchange_role(const Args& a, const Ctx& c, int token) {
 #pragma unroll
     for (int k = 0; k < HPW; ++k) h[k] = h[k] + __uint_as_float(uint32_t(wd[k]));
   };
+  // exchange wave 0: publish the compute waves' outputs of this phase, then the flag
+  auto publish = [&](uint64_t* X, uint32_t* flag) {
+    ++pphase;
+    if (ew != 0) return;
+    lds_wait(c.mb_out, kWavesC * pphase);
+    if (lane < kWavesC * kMbox) {
+      const int idx = c.mb_idx[lane];
+      if (idx >= 0) st_tag(X + idx, c.mb_val[lane], c.tag);
+    }
+    if (lane == 0) st_flag(flag, c.tag);
+    lds_bump(c.mb_pub, lane);
+  };
   load_scale(a.w + a.lay.off_ln1);
   norm_to(c.sh_x0);
   __syncthreads();
@@ -409,8 +520,10 @@ __device__ void exchange_role(const Args& a, const Ctx& c, int token) {
     const Layout& lay = a.lay;
     uint64_t* X = layer_x(a, l);
     load_scale(layer_w(a, l) + lay.off_ln2);
-    // B0 .. B1: q of the head group and the new k, v for the attention chunk
+    // B0 .. B1: publish q/k/v rows; attention workgroups gather q of their head group and the new k, v
+    publish(X, flagp(l, kExQkv) + c.wg);
     if (c.att) {
+      poll_flags(flagp(l, kExQkv), G, c.tag, a.ctrl, lane, bad);
       gather_x(X + lay.x_qkv + int64_t(c.ag) * c.GQ * kDh, c.GQ * kDh, c.sh_q, c.tag, a.ctrl, ew, lane, bad);
       if (c.pos >= c.q0 && c.pos < c.q1 && ew < 2) {   // current position: un-rounded K/V (multi_sm_decode.py:197,205)
         const int prow = c.pos - c.q0;
@@ -431,8 +544,17 @@ __device__ void exchange_role(const Args& a, const Ctx& c, int token) {
     MSD_TRACE_POINT(ew == 0, 0);
     __syncthreads();  // B1
     MSD_TRACE_POINT(ew == 0, 1);
-    // B1 .. B2: merge the chunks of a KV head (multi_sm_decode.py:243-259), attention vector -> x1
+    // B1 .. B2: flag of this chunk's partials; merge the chunks of a KV head
+    // (multi_sm_decode.py:243-259); everyone gathers the attention vector -> x1
+    if (c.att) {
+      ++aphase;
+      if (ew == 0) {
+        lds_wait(c.mb_out + 2, kWavesC * aphase);   // the compute waves issued their partials
+        if (lane == 0) st_flag(flagp(l, kExPart) + c.wg, c.tag);
+      }
+    }
     if (c.merger) {
+      poll_flags(flagp(l, kExPart) + c.ag * c.nch, c.nch, c.tag, a.ctrl, lane, bad);
       gather_x(X + lay.x_part + int64_t(c.ag) * c.npart, c.npart, c.sh_x1, c.tag, a.ctrl, ew, lane, bad);
       xsync(c.sh_sync, sphase, lane);
       for (int n = ew; n < c.GQ; n += kWavesX) {
@@ -452,14 +574,18 @@ __device__ void exchange_role(const Args& a, const Ctx& c, int token) {
         }
         st_tag(X + lay.x_attn + (c.ag * c.GQ + n) * kDh + lane, num / den, c.tag);
       }
-      xsync(c.sh_sync, sphase, lane);   // the partials in x1 are no longer read
+      xsync(c.sh_sync, sphase, lane);   // every head's words are issued, the partials in x1 are no longer read
+      if (ew == 0 && lane == 0) st_flag(flagp(l, kExAttn) + c.ag, c.tag);
       MSD_TRACE_POINT(ew == 0, 2);
     }
+    poll_flags(flagp(l, kExAttn), c.KV, c.tag, a.ctrl, lane, bad);
     gather_x(X + lay.x_attn, D, c.sh_x1, c.tag, a.ctrl, ew, lane, bad);
     MSD_TRACE_POINT(ew == 0, 3);
     __syncthreads();  // B2
     MSD_TRACE_POINT(ew == 0, 4);
-    // B2 .. B3: h += O output, x0 = rmsnorm2(h)
+    // B2 .. B3: publish O rows; h += O output, x0 = rmsnorm2(h)
+    publish(X, flagp(l, kExHd1) + c.wg);
+    poll_flags(flagp(l, kExHd1), G, c.tag, a.ctrl, lane, bad);
     add_h(X + lay.x_hd1);
     MSD_TRACE_POINT(ew == 0, 5);
     norm_to(c.sh_x0);
@@ -467,12 +593,16 @@ __device__ void exchange_role(const Args& a, const Ctx& c, int token) {
     load_scale(l + 1 < c.L ? layer_w(a, l + 1) + lay.off_ln1 : a.lnf);
     __syncthreads();  // B3
     MSD_TRACE_POINT(ew == 0, 7);
-    // B3 .. B4: act -> x1
+    // B3 .. B4: publish gate/up outputs; act -> x1
+    publish(X, flagp(l, kExAct) + c.wg);
+    poll_flags(flagp(l, kExAct), G, c.tag, a.ctrl, lane, bad);
     gather_x(X + lay.x_act, c.ff, c.sh_x1, c.tag, a.ctrl, ew, lane, bad);
     MSD_TRACE_POINT(ew == 0, 8);
     __syncthreads();  // B4
     MSD_TRACE_POINT(ew == 0, 9);
-    // B4 .. B0': h += down output, x0 = rmsnorm1 of the next layer (or the final norm)
+    // B4 .. B0': publish down rows; h += down output, x0 = rmsnorm1 of the next layer (or the final norm)
+    publish(X, flagp(l, kExHd2) + c.wg);
+    poll_flags(flagp(l, kExHd2), G, c.tag, a.ctrl, lane, bad);
     add_h(X + lay.x_hd2);
     MSD_TRACE_POINT(ew == 0, 10);
     norm_to(c.sh_x0);
@@ -483,10 +613,12 @@ __device__ void exchange_role(const Args& a, const Ctx& c, int token) {
 }
 
 // ---------------------------------------------------------------- compute waves
-template <int D, int FFL, int FRW>
+template <int D, int FF, int FRW>
 __device__ void compute_role(const Args& a, const Ctx& c) {
   constexpr int NLD = (D + 511) / 512;
-  const int lane = c.lane, wv = c.wv, ff = c.ff;
+  constexpr int FFL = (FF + 511) / 512;
+  constexpr int ff = FF;
+  const int lane = c.lane, wv = c.wv;
   const Layout& lay = a.lay;
   const int tidc = wv * 64 + lane;   // index among the compute threads
   int qp0, qp1, or0, or1, f0, f1;
@@ -525,7 +657,7 @@ __device__ void compute_role(const Args& a, const Ctx& c) {
   auto load_gu = [&](int l) {
 #pragma unroll
     for (int j = 0; j < FRW; ++j) {
-      const int f = f0 + wv + kWavesC * j;
+      const int f = f0 + wv * FRW + j;   // contiguous gate/up pairs per wave
       if (f < f1) {
         load_row(gbg[j], layer_w(a, l) + lay.off_gu + int64_t(2 * f) * D, D, lane);
         load_row(gbu[j], layer_w(a, l) + lay.off_gu + int64_t(2 * f + 1) * D, D, lane);
@@ -533,6 +665,22 @@ __device__ void compute_role(const Args& a, const Ctx& c) {
     }
   };
   auto load_dn = [&](int l) { if (has_or) load_row(db, layer_w(a, l) + lay.off_dn + int64_t(myor) * ff, ff, lane); };
+
+  // Outputs go through the LDS mailbox to exchange wave 0, which stores them; the compute
+  // waves request the next phase's weights only after the outputs are published, so the
+  // latency-critical stores leave this CU ahead of the bulk loads.
+  int cphase = 0;
+  auto post = [&](int j, int idx, float v) {
+    if (lane == 0) {
+      c.mb_idx[wv * kMbox + j] = idx;
+      c.mb_val[wv * kMbox + j] = v;
+    }
+  };
+  auto handoff = [&]() {
+    ++cphase;
+    lds_bump(c.mb_out, lane);
+    lds_wait(c.mb_pub, cphase);
+  };
 
   load_qkv(0);
   __syncthreads();
@@ -571,10 +719,13 @@ __device__ void compute_role(const Args& a, const Ctx& c) {
       }
     }
     MSD_TRACE_POINT(wv == 0, 17);
+    post(0, has_qp ? int(lay.x_qkv) + i0 : -1, o0);
+    post(1, has_qp ? int(lay.x_qkv) + i1 : -1, o1);
+#pragma unroll
+    for (int j = 2; j < kMbox; ++j) post(j, -1, 0.f);
+    handoff();
     load_o(l);
     if (has_qp && lane == 0) {
-      st_tag(X + lay.x_qkv + i0, o0, c.tag);
-      st_tag(X + lay.x_qkv + i1, o1, c.tag);
       if (head >= c.H) {  // K (post-RoPE) or V row of the cache at pos, bf16 (multi_sm_decode.py:179-180)
         const bool isv = head >= c.H + c.KV;
         const int kvh = isv ? head - c.H - c.KV : head - c.H;
@@ -624,6 +775,7 @@ __device__ void compute_role(const Args& a, const Ctx& c) {
         st_tag(part + 2 + lane, o, c.tag);
         __builtin_amdgcn_wave_barrier();
       }
+      lds_bump(c.mb_out + 2, lane);   // exchange wave 0 raises the chunk's flag after all heads
       MSD_TRACE_POINT(wv == 0, 19);
     }
     __syncthreads();  // B2
@@ -637,18 +789,21 @@ __device__ void compute_role(const Args& a, const Ctx& c) {
       yo = dot_row(ob, xv);
     }
     MSD_TRACE_POINT(wv == 0, 21);
+    post(0, has_or ? int(lay.x_hd1) + myor : -1, yo);
+#pragma unroll
+    for (int j = 1; j < kMbox; ++j) post(j, -1, 0.f);
+    handoff();
     load_gu(l);
-    if (has_or && lane == 0) st_tag(X + lay.x_hd1 + myor, yo, c.tag);
     __syncthreads();  // B3
     MSD_TRACE_POINT(wv == 0, 22);
 
     // ---- B3 .. B4: gate/up rows + SwiGLU (multi_sm_decode.py:262-289, model.py:159)
     XV<NLD> xg;
-    if (f0 + wv < f1) load_x(xg, c.sh_x0, D, lane);
+    if (f0 + wv * FRW < f1) load_x(xg, c.sh_x0, D, lane);
     float act[FRW];
 #pragma unroll
     for (int j = 0; j < FRW; ++j) {
-      const int f = f0 + wv + kWavesC * j;
+      const int f = f0 + wv * FRW + j;   // contiguous gate/up pairs per wave
       act[j] = 0.f;
       if (f < f1) {
         const float gt = dot_row(gbg[j], xg);
@@ -657,25 +812,25 @@ __device__ void compute_role(const Args& a, const Ctx& c) {
       }
     }
     MSD_TRACE_POINT(wv == 0, 23);
-    load_dn(l);
 #pragma unroll
-    for (int j = 0; j < FRW; ++j) {
-      const int f = f0 + wv + kWavesC * j;
-      if (f < f1 && lane == 0) st_tag(X + lay.x_act + f, act[j], c.tag);
+    for (int j = 0; j < kMbox; ++j) {
+      const int f = f0 + wv * FRW + j;   // contiguous gate/up pairs per wave
+      post(j, (j < FRW && f < f1) ? int(lay.x_act) + f : -1, j < FRW ? act[j < FRW ? j : 0] : 0.f);
     }
+    handoff();
+    load_dn(l);
     __syncthreads();  // B4
     MSD_TRACE_POINT(wv == 0, 24);
 
     // ---- B4 .. B0': down rows (multi_sm_decode.py:273-291)
     float yd = 0.f;
-    if (has_or) {
-      XV<FFL> xv;
-      load_x(xv, c.sh_x1, ff, lane);
-      yd = dot_row(db, xv);
-    }
+    if (has_or) yd = dot_row_lds(db, c.sh_x1, ff, lane);
     MSD_TRACE_POINT(wv == 0, 25);
+    post(0, has_or ? int(lay.x_hd2) + myor : -1, yd);
+#pragma unroll
+    for (int j = 1; j < kMbox; ++j) post(j, -1, 0.f);
+    handoff();
     if (l + 1 < c.L) load_qkv(l + 1);
-    if (has_or && lane == 0) st_tag(X + lay.x_hd2 + myor, yd, c.tag);
     __syncthreads();  // B0'
     MSD_TRACE_POINT(wv == 0, 26);
   }
@@ -729,14 +884,14 @@ __device__ void compute_role(const Args& a, const Ctx& c) {
   }
 }
 
-template <int D, int FFL, int FRW>
+template <int D, int FF, int FRW>
 __global__ __launch_bounds__(kThreadsWG, 1) void decode_step_kernel(Args a) {
   extern __shared__ float smem[];
   Ctx c;
   c.G = gridDim.x;
   c.wg = blockIdx.x;
   c.lane = threadIdx.x & 63;
-  c.wv = threadIdx.x >> 6;
+  c.wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform (scalar register)
   c.H = a.H;
   c.KV = a.KV;
   c.GQ = a.H / a.KV;
@@ -768,7 +923,16 @@ __global__ __launch_bounds__(kThreadsWG, 1) void decode_step_kernel(Args a) {
   c.sh_e = c.sh_q + c.GQ * kDh;
   c.sh_red = c.sh_e + kWavesC * 64;
   c.sh_sync = reinterpret_cast<int*>(c.sh_red + 64);
-  if (threadIdx.x == 0) *c.sh_sync = 0;
+  c.mb_val = c.sh_red + 64 + 4;
+  c.mb_idx = reinterpret_cast<int*>(c.mb_val + kWavesC * kMbox);
+  c.mb_out = c.mb_idx + kWavesC * kMbox;   // [0] outputs written, [2] attention partials issued
+  c.mb_pub = c.mb_out + 1;
+  if (threadIdx.x == 0) {
+    *c.sh_sync = 0;
+    c.mb_out[0] = 0;
+    c.mb_out[1] = 0;
+    c.mb_out[2] = 0;
+  }
   __syncthreads();
 
   int token = a.token_dev ? *a.token_dev : a.token;
@@ -777,7 +941,7 @@ __global__ __launch_bounds__(kThreadsWG, 1) void decode_step_kernel(Args a) {
     token = token < 0 ? 0 : a.V - 1;
   }
   if (c.wv >= kWavesC) exchange_role<D>(a, c, token);
-  else compute_role<D, FFL, FRW>(a, c);
+  else compute_role<D, FF, FRW>(a, c);
 }
 
 // ---------------------------------------------------------------- host side
@@ -811,7 +975,8 @@ static bool make_plan(const msd_config* c, int G, Plan* p) {
   const int nch = n_chunks(c->context_len);
   const int ch_max = cdiv(c->context_len, nch);
   const int xmax = std::max(std::max(c->d_model, c->d_ff), nch * GQ * kPartStride);
-  const size_t floats = size_t(c->d_model) + xmax + ch_max * (kKPad + kDh) + GQ * kDh + kWavesC * 64 + 64 + 4;
+  const size_t floats = size_t(c->d_model) + xmax + ch_max * (kKPad + kDh) + GQ * kDh + kWavesC * 64 + 64 + 4 +
+                        2 * kWavesC * kMbox + 8;
   p->lds = floats * 4;
   return true;
 }
@@ -820,31 +985,30 @@ static bool make_plan(const msd_config* c, int G, Plan* p) {
 // compute unit (160 KB per CU): the grid then spreads over every CU.
 constexpr size_t kMinLds = 84 * 1024;
 
-template <int D, int FFL, int FRW>
+template <int D, int FF, int FRW>
 static hipError_t launch_t(const Args& a, int grid, size_t lds, hipStream_t s) {
   static bool attr_set = false;
   if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&decode_step_kernel<D, FFL, FRW>),
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&decode_step_kernel<D, FF, FRW>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
     if (e != hipSuccess) return e;
     attr_set = true;
   }
-  hipLaunchKernelGGL((decode_step_kernel<D, FFL, FRW>), dim3(grid), dim3(kThreadsWG), lds, s, a);
+  hipLaunchKernelGGL((decode_step_kernel<D, FF, FRW>), dim3(grid), dim3(kThreadsWG), lds, s, a);
   return hipGetLastError();
 }
 
-// Instantiated shapes: (d_model, ceil(d_ff/512), gate/up rows per wave).
-static hipError_t launch(const Args& a, const Plan& p, int d, int grid, size_t lds, hipStream_t s) {
-  if (d == 256 && p.ffl == 2 && p.frw == 1) return launch_t<256, 2, 1>(a, grid, lds, s);
-  if (d == 1024 && p.ffl == 6 && p.frw == 3) return launch_t<1024, 6, 3>(a, grid, lds, s);
-  if (d == 1024 && p.ffl == 6 && p.frw == 1) return launch_t<1024, 6, 1>(a, grid, lds, s);
-  if (d == 256 && p.ffl == 2 && p.frw == 3) return launch_t<256, 2, 3>(a, grid, lds, s);
+// Instantiated shapes (d_model, d_ff, gate/up rows per compute wave): the tiny and the
+// 306M configurations on 256 workgroups, and the same shapes on fewer workgroups.
+static hipError_t launch(const Args& a, const Plan& p, int d, int ff, int grid, size_t lds, hipStream_t s) {
+  if (d == 256 && ff == 704 && p.frw == 1) return launch_t<256, 704, 1>(a, grid, lds, s);
+  if (d == 1024 && ff == 2816 && p.frw == 3) return launch_t<1024, 2816, 3>(a, grid, lds, s);
   return hipErrorInvalidValue;
 }
 
 static bool plan_instantiated(const msd_config* c, const Plan& p) {
-  return (c->d_model == 256 && p.ffl == 2 && (p.frw == 1 || p.frw == 3)) ||
-         (c->d_model == 1024 && p.ffl == 6 && (p.frw == 1 || p.frw == 3));
+  return (c->d_model == 256 && c->d_ff == 704 && p.frw == 1) ||
+         (c->d_model == 1024 && c->d_ff == 2816 && p.frw == 3);
 }
 
 }  // namespace msd
@@ -861,8 +1025,9 @@ extern "C" int64_t msd_workspace_bytes(const msd_config* cfg, int32_t n_workgrou
   Plan p;
   if (!config_ok(cfg)) return MSD_E_CONFIG;
   if (!make_plan(cfg, n_workgroups, &p) || !plan_instantiated(cfg, p)) return MSD_E_CONFIG;
-  const Layout t = make_layout(cfg->d_model, cfg->n_heads, cfg->n_kv_heads, cfg->d_ff, cfg->context_len);
-  return t.ctrl_bytes + t.x_layer * cfg->n_layers * int64_t(sizeof(uint64_t));
+  const Layout t = make_layout(cfg->d_model, cfg->n_heads, cfg->n_kv_heads, cfg->d_ff, cfg->context_len, n_workgroups);
+  return t.ctrl_bytes + t.x_layer * cfg->n_layers * int64_t(sizeof(uint64_t)) +
+         t.flag_words * cfg->n_layers * int64_t(sizeof(uint32_t));
 }
 
 extern "C" int32_t msd_default_workgroups(int32_t device) {
@@ -900,8 +1065,9 @@ extern "C" int32_t msd_decode_step(const msd_config* cfg, const void* token_emb,
   a.next_token = next_token;
   a.token_dev = token_dev;
   a.ctrl = static_cast<uint32_t*>(workspace);
-  a.lay = make_layout(cfg->d_model, cfg->n_heads, cfg->n_kv_heads, cfg->d_ff, cfg->context_len);
+  a.lay = make_layout(cfg->d_model, cfg->n_heads, cfg->n_kv_heads, cfg->d_ff, cfg->context_len, n_workgroups);
   a.xw = reinterpret_cast<uint64_t*>(static_cast<char*>(workspace) + a.lay.ctrl_bytes);
+  a.flags = reinterpret_cast<uint32_t*>(a.xw + a.lay.x_layer * cfg->n_layers);
   a.token = token_id;
   a.pos = pos;
   a.epoch = epoch;
@@ -913,7 +1079,7 @@ extern "C" int32_t msd_decode_step(const msd_config* cfg, const void* token_emb,
   a.ctx = cfg->context_len;
   a.nch = n_chunks(cfg->context_len);
   const size_t lds = std::max(p.lds, kMinLds);
-  const hipError_t e = launch(a, p, cfg->d_model, n_workgroups, lds, static_cast<hipStream_t>(stream));
+  const hipError_t e = launch(a, p, cfg->d_model, cfg->d_ff, n_workgroups, lds, static_cast<hipStream_t>(stream));
   return e == hipSuccess ? MSD_OK : MSD_E_HIP;
 }
 
