@@ -24,6 +24,17 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 METRIC = "decode tok/s @batch1 306M on 1 MI355X; % of HBM roofline"
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_step_306m_hbm_traffic.json")
+
+
+def measured_traffic():
+    """HBM bytes per decode step from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            t = json.load(f)
+        return float(t["fetch_bytes"]) + float(t["write_bytes"])
+    except (OSError, KeyError, ValueError):
+        return None
 PEAK_HBM_GBS = 8000.0
 
 
@@ -37,8 +48,12 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=479)
     ap.add_argument("--warmup", type=int, default=32)
-    ap.add_argument("--cpu-sample", type=int, default=4, help="oracle steps timed for cpu_baseline (0 = skip)")
+    ap.add_argument("--cpu-sample", type=int, default=479,
+                    help="oracle decode steps timed for cpu_baseline, from position 32 (0 = skip)")
     ap.add_argument("--synced-steps", type=int, default=128, help="host-synced steps for the secondary figure")
+    ap.add_argument("--copy-calibration-mb", type=int, default=0,
+                    help="run one device-to-device copy of this many MiB before decoding (reference "
+                         "kernel for scaling HBM byte counters; not timed)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported "
@@ -63,6 +78,14 @@ def main():
     dec = Decoder(w, cfg)
     print(f"[bench] weights ready in {time.time() - t0:.1f}s; workgroups={dec.n_workgroups}",
           file=sys.stderr, flush=True)
+
+    if args.copy_calibration_mb > 0:
+        n = args.copy_calibration_mb << 20
+        src = torch.ones(n // 4, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     # prompt ingest (not timed): one step per prompt token
     for p, t in enumerate(prompt):
@@ -133,12 +156,12 @@ def main():
         om.decode_step(params, cfg, int(first), start, kc, vc, rope=rope)   # warm
         tc = time.perf_counter()
         tk = int(first)
-        for i in range(n):
-            _, tk = om.decode_step(params, cfg, tk, start + i, kc, vc, rope=rope)
+        for p in positions(start, stop, n):
+            _, tk = om.decode_step(params, cfg, tk, p, kc, vc, rope=rope)
         cpu_s = time.perf_counter() - tc
         cpu = {"value": round(n / cpu_s, 3), "unit": "tok/s", "cores": int(cores), "kind": "port",
-               "sample": f"{n} cached decode steps of the numpy oracle (f32 on bf16-valued 306M "
-                         f"weights) at positions {start}..{start + n - 1}, {cpu_s:.1f}s"}
+               "sample": f"{n} greedy cached decode steps of the numpy oracle (f32 on bf16-valued 306M "
+                         f"weights) from position {start}, {cpu_s:.1f}s"}
 
     line = {
         "metric": METRIC,
@@ -158,7 +181,7 @@ def main():
                    "n_kv_heads": cfg["n_kv_heads"], "d_ff": cfg["d_ff"], "vocab": cfg["vocab_size"],
                    "context_len": cfg["context_len"], "batch": 1},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
-                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": measured_traffic(),
                      "bytes_per_step": round(avg_bytes)},
         "cpu_baseline": cpu,
         "host_synced_tok_s": None if synced is None else round(synced, 1),

@@ -4,7 +4,10 @@ import pytest
 import torch
 
 from oracle import model as om
-from transformer_amd.configs import TINY
+import json
+import os
+
+from transformer_amd.configs import M306, TINY
 from transformer_amd.fused_decode_nlayer import prepare_decode_weights_nlayer, unpack_kv_caches
 from transformer_amd.multi_sm_decode import Decoder, multi_sm_decode_nlayer
 from transformer_amd.synthetic import make_params, make_prompt
@@ -115,3 +118,69 @@ def test_device_token_chaining(tiny):
     got = [int(t) for t in toks]
     ref = om.greedy_generate(params, TINY, prompt, 9, prefill="step")
     assert got == ref[1:]
+
+
+def test_tiny_matches_golden_fixture(tiny):
+    params, prompt, w = tiny
+    with open(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "tiny_greedy.json")) as f:
+        g = json.load(f)
+    toks, logs, _ = _gpu_generate(w, TINY, np.array(g["prompt"]), 48)
+    assert toks == g["greedy_tokens_step_prefill"]
+    for st, lg in zip(g["steps"], logs):
+        np.testing.assert_allclose(lg[:8], st["logits_0_8"], atol=1e-4, rtol=1e-4)
+
+
+def _teacher_forced(params, w, cfg, seq):
+    """Feed a fixed token stream; compare every position's logits and argmax with the oracle."""
+    dec = Decoder(w, cfg)
+    kc, vc = om.new_kv_cache(cfg)
+    rope = om.precompute_rope_table(cfg["context_len"], cfg["d_head"])
+    worst, flips = 0.0, []
+    for p, t in enumerate(seq):
+        tok, lg = dec.step(int(t), p)
+        ref, rtok = om.decode_step(params, cfg, int(t), p, kc, vc, rope=rope)
+        got = lg.cpu().numpy()
+        worst = max(worst, float(np.abs(got - ref).max()))
+        np.testing.assert_allclose(got, ref, atol=ATOL, rtol=RTOL)
+        if tok != rtok:
+            top = np.sort(ref)[-2:]
+            flips.append((p, tok, rtok, float(top[1] - top[0])))
+    return worst, flips
+
+
+def test_tiny_teacher_forced_all_positions(tiny):
+    """Random token stream over the whole 128-token context: argmax exact at every position."""
+    params, prompt, w = tiny
+    seq = make_prompt(TINY["context_len"], TINY["vocab_size"], seed=5)
+    worst, flips = _teacher_forced(params, w, TINY, seq)
+    print("tiny teacher-forced max |logit diff|:", worst)
+    assert not flips, flips
+
+
+@pytest.fixture(scope="module")
+def m306():
+    params = make_params(M306, seed=0, resid_scaled=True)
+    w = prepare_decode_weights_nlayer(params, M306)
+    return params, w
+
+
+def test_306m_teacher_forced(m306):
+    """306M: a random token stream over the whole 512-token context, every position checked."""
+    params, w = m306
+    seq = make_prompt(M306["context_len"], M306["vocab_size"], seed=6)
+    worst, flips = _teacher_forced(params, w, M306, seq)
+    print("306M teacher-forced max |logit diff|:", worst)
+    assert not flips, flips
+
+
+def test_306m_greedy_full_generation_token_exact(m306):
+    """Config 2: 32-token prompt, 480 greedy tokens (prompt fed step by step, positions 32..510)."""
+    params, w = m306
+    prompt = make_prompt(32, M306["vocab_size"], seed=1)
+    toks, logs, _ = _gpu_generate(w, M306, prompt, 480)
+    rtoks, rlogs = om.greedy_generate(params, M306, prompt, 480, prefill="step", return_logits=True)
+    diffs = [float(np.abs(a - b).max()) for a, b in zip(logs, rlogs)]
+    print("306M greedy: max |logit diff|", max(diffs), "distinct tokens", len(set(toks)))
+    assert toks == rtoks
+    for a, b in zip(logs[::40], rlogs[::40]):
+        np.testing.assert_allclose(a, b, atol=ATOL, rtol=RTOL)
