@@ -12,6 +12,11 @@
  *   msd_packed_weight_elems, msd_workspace_bytes
  *                         <- the packed_w size implied by kernels/fused_decode_nlayer.py:250-270
  *                            and the workspace layout of kernels/multi_sm_decode.py:390-400
+ *   msd_sample_token      <- generate.py:28-65 sample_token(logits, temperature, top_p,
+ *                            rep_penalty, generated_ids), with the np.random.choice draw
+ *                            (generate.py:63,65) taken from a supplied uniform
+ *   msd_sample_workspace_bytes
+ *                         <- the host numpy temporaries of generate.py:28-65
  */
 #ifndef MSDECODE_H
 #define MSDECODE_H
@@ -92,6 +97,38 @@ int32_t msd_decode_step(const msd_config* cfg, const void* token_emb, const void
 /* Reads and clears the device status word of a workspace (synchronous on `stream`).
  * Returns MSD_OK, MSD_E_TIMEOUT when a wait of an earlier step ran out, or MSD_E_HIP. */
 int32_t msd_check_status(void* workspace, void* stream);
+
+/* Bytes of device workspace msd_sample_token needs for a vocabulary of `vocab` ids
+ * (vocab <= 32768; MSD_E_CONFIG otherwise).  No initialisation is needed. */
+int64_t msd_sample_workspace_bytes(int32_t vocab);
+
+/* Draws the next token from f32 logits on the device, with numpy's arithmetic of the host
+ * sampler reproduced (float32 penalty/temperature/softmax, numpy's pairwise sums, the
+ * sequential float32 cumsum of the descending probabilities, a float64 inverse CDF):
+ *
+ *   temperature == 0      argmax of the penalised logits (lowest id on ties); no draw
+ *   top_p >= 1            inverse CDF of the full softmax in id order
+ *   top_p < 1             nucleus: ids sorted by descending probability (equal values in
+ *                         ascending id order), kept up to and including the first whose
+ *                         running float32 sum reaches top_p, renormalised, inverse CDF
+ *
+ *   seen         device uint8 (vocab): 1 for ids generated earlier in this sequence; the
+ *                penalty (l / rep_penalty if l > 0 else l * rep_penalty) applies to them when
+ *                rep_penalty != 1.  The drawn id is set to 1 on return.
+ *   uniform      device float64: the draw u in [0, 1) (RandomState.random_sample()); may be
+ *                NULL when temperature == 0
+ *   token_out    device int32 output (can be the token input of the next msd_decode_step)
+ *   probs_out    optional device f32 (vocab): the normalised probabilities in id order
+ *                (temperature > 0)
+ *   kept_out     optional device int32: number of ids the nucleus kept (top_p < 1)
+ *   workspace    msd_sample_workspace_bytes(vocab) bytes, 256-byte aligned
+ *
+ * The exponential is the correctly rounded float32 value (numpy's float32 exp differs by up to
+ * 2 ulp).  Calls sharing a workspace or `seen` must be ordered on one stream. */
+int32_t msd_sample_token(const float* logits, int32_t vocab, double temperature, double top_p,
+                         double rep_penalty, uint8_t* seen, const double* uniform,
+                         int32_t* token_out, float* probs_out, int32_t* kept_out,
+                         void* workspace, void* stream);
 
 #ifdef __cplusplus
 }

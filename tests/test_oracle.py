@@ -5,6 +5,7 @@ import torch
 
 from oracle import model as om
 from oracle.numerics import bf16_round
+from oracle import sampling as osm
 from oracle.sampling import sample_token, _choice
 from transformer_amd.configs import TINY
 from transformer_amd.synthetic import bf16_round_np, make_params, make_prompt
@@ -212,6 +213,73 @@ def test_sample_token_closed_forms():
         assert sample_token(logits, 1.0, 1.0, 1.0, [], u) == int(np.searchsorted(np.cumsum(p.astype(np.float64)) / p.astype(np.float64).sum(), u, side="right"))
     # tiny top_p keeps only the argmax
     assert sample_token(logits, 0.7, 1e-6, 1.0, [], 0.99) == int(np.argmax(logits))
+
+
+def test_nucleus_compares_top_p_in_float64():
+    # cumsum[0] = float32(0.95) = 0.94999998... < 0.95: numpy's searchsorted compares in
+    # float64, so the cutoff moves one further (a float32 comparison would keep one id)
+    probs = np.array([0.95, 0.05], np.float32)
+    keep, filt = osm.nucleus(probs, 0.95)
+    assert list(keep) == [0, 1]
+    keep, _ = osm.nucleus(probs, float(np.float32(0.95)))
+    assert list(keep) == [0]
+
+
+def test_nucleus_cutoff_against_exact_sums():
+    """Cutoff = one past the first sorted position whose running sum reaches top_p, checked
+    with exact rational sums of the float32 probabilities (skipping near-ties)."""
+    from fractions import Fraction
+    rng = np.random.default_rng(21)
+    checked = 0
+    for trial in range(300):
+        n = int(rng.integers(1, 60))
+        p = (rng.random(n) ** 3).astype(np.float32)
+        p /= p.sum()
+        top_p = float(rng.random())
+        order = np.argsort(-p, kind="stable")
+        acc, first = Fraction(0), None
+        near = False
+        for i, j in enumerate(order):
+            acc += Fraction(float(p[j]))
+            if abs(float(acc) - top_p) < 1e-6:
+                near = True
+            if first is None and acc >= Fraction(top_p):
+                first = i
+        if near:
+            continue
+        keep, filt = osm.nucleus(p, top_p)
+        expect = n if first is None else first + 1
+        assert len(keep) == expect
+        assert list(keep) == list(order[:expect])
+        np.testing.assert_allclose(filt.sum(dtype=np.float64), 1.0, atol=1e-6)
+        checked += 1
+    assert checked > 250
+
+
+def test_nucleus_equal_probabilities_closed_form():
+    n = 1024
+    p = np.full(n, 1.0 / n, np.float32)   # exact: sums of powers of two
+    for top_p in (0.25, 0.5, 0.75, 0.999):
+        keep, filt = osm.nucleus(p, top_p)
+        assert list(keep) == list(range(int(np.ceil(top_p * n))))
+        assert np.all(filt == np.float32(1.0 / len(keep)))
+
+
+def test_numpy_exp_versus_rounded_exp():
+    """numpy's float32 exp differs from the correctly rounded value by <= 2 ulp; the drawn
+    tokens of the two oracle modes agree except where a draw lands within that noise."""
+    rng = np.random.default_rng(22)
+    same = total = 0
+    for trial in range(60):
+        lg = (rng.standard_normal(32000) * rng.choice([0.3, 1.0, 4.0])).astype(np.float32)
+        a = osm.softmax_probs(lg, 0.7, exp="numpy")
+        b = osm.softmax_probs(lg, 0.7, exp="rounded")
+        assert np.max(np.abs(a.view(np.int32) - b.view(np.int32))) <= 8   # exp ulps + the sum's
+        for u in rng.random(5):
+            total += 1
+            same += osm.sample_token(lg, 0.7, 0.95, 1.0, [], u, exp="numpy") == \
+                osm.sample_token(lg, 0.7, 0.95, 1.0, [], u, exp="rounded")
+    assert same >= 0.97 * total, (same, total)
 
 
 def test_synthetic_generator_is_seeded():

@@ -21,7 +21,7 @@ _ERRNAMES = {MSD_E_CONFIG: "unsupported config", MSD_E_ARG: "invalid argument",
              MSD_E_HIP: "HIP runtime error", MSD_E_TIMEOUT: "cross-workgroup wait timed out"}
 
 EXPORTS = ("msd_packed_weight_elems", "msd_workspace_bytes", "msd_default_workgroups",
-           "msd_decode_step", "msd_check_status")
+           "msd_decode_step", "msd_check_status", "msd_sample_workspace_bytes", "msd_sample_token")
 
 
 class MsdConfig(ctypes.Structure):
@@ -64,6 +64,11 @@ def lib():
     L.msd_decode_step.restype = I32
     L.msd_check_status.argtypes = [P, P]
     L.msd_check_status.restype = I32
+    D = ctypes.c_double
+    L.msd_sample_workspace_bytes.argtypes = [I32]
+    L.msd_sample_workspace_bytes.restype = I64
+    L.msd_sample_token.argtypes = [P, I32, D, D, D, P, P, P, P, P, P, P]
+    L.msd_sample_token.restype = I32
     _lib = L
     return L
 

@@ -1,0 +1,612 @@
+// Sampling tail of token generation on one MI355X (gfx950): repetition penalty, temperature,
+// softmax, top-p (nucleus) filtering and the inverse-CDF draw of one token.
+//
+// Follows generate.py:28-65 (sample_token) with numpy's float arithmetic reproduced step by
+// step, so that the drawn token matches the host code on the same logits and uniform:
+//   * penalty and temperature in float32 (generate.py:33-46; NEP 50 casts the Python floats
+//     to float32), applied once per distinct previously generated id (a 0/1 byte per id);
+//   * max shift, exp, and normalisation by numpy's float32 `sum` (generate.py:48-51), whose
+//     reduction order is reproduced exactly: buffers of 8192 entries summed in turn, each by
+//     numpy's pairwise recursion (blocks of <= 128 entries with 8 interleaved accumulators);
+//     exp is the correctly rounded float32 value, computed in float64;
+//   * the descending sort of the probabilities with equal values in ascending id order
+//     (generate.py:55), the float32 sequential `cumsum` of the sorted values and
+//     `searchsorted(cumsum, top_p)` compared in float64 (generate.py:56-58), the pairwise
+//     float32 sum of the kept values and their float32 renormalisation (generate.py:59-61);
+//   * RandomState.choice(keep, p=filtered) on a supplied uniform u (generate.py:62-65):
+//     searchsorted(cdf / cdf[-1], u, 'right') with cdf the float64 cumulative sum.
+//
+// Kernels, all on the caller's stream:
+//   sample_prep_kernel     1 workgroup x 1024: penalty, temperature, argmax (temperature 0),
+//                          softmax, full-vocabulary draw (top_p >= 1), or the sort keys and the
+//                          first radix histogram (top_p < 1)
+//   sample_radix_kernel    4 stable LSD passes of 8 bits over (probability bits, id), tiles of
+//                          512 entries per workgroup; each pass counts the next pass's digits
+//   sample_nucleus_kernel  1 workgroup x 1024: the cumsum cutoff walk, renormalisation and draw
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <math.h>
+
+#include <algorithm>
+
+#include "../../include/msdecode.h"
+
+// Every float operation below is a separately rounded IEEE operation (no contraction).
+#pragma clang fp contract(off)
+
+namespace mss {
+
+constexpr int kT = 1024;                    // threads of the single-workgroup kernels
+constexpr int kWaves = kT / 64;
+constexpr int kVMax = 32768;                // largest vocabulary: 32 entries per thread
+constexpr int kPer = kVMax / kT;
+constexpr int kTile = 512;                  // radix tile: entries per scatter workgroup
+constexpr int kTileThreads = 256;
+constexpr int kRounds = kTile / kTileThreads;
+constexpr int kMaxTiles = kVMax / kTile;
+constexpr int kHistWords = kMaxTiles * 256;  // one pass's [tile][digit] counts
+constexpr int kPasses = 4;
+constexpr int kRedChunk = 8192;             // numpy's reduction buffer (np.getbufsize())
+constexpr int kPwBlock = 128;               // numpy's pairwise-sum block
+constexpr int kSlots = 255;                 // heap slots of one buffer's pairwise tree (depth <= 7)
+// Large LDS arrays keep entry j at j + j/32: a thread's 32 consecutive entries then start on
+// a different bank from its neighbours'.
+constexpr size_t kLdsBig = size_t(kVMax + kVMax / 32) * sizeof(float);
+
+enum Mode { kGreedy = 0, kFull = 1, kNucleus = 2 };
+
+struct SArgs {
+  const float* logits;
+  uint8_t* seen;          // [V] 1 = generated before (penalised); the drawn id is marked
+  const double* u;        // one uniform draw in [0, 1)
+  int32_t* token_out;
+  float* probs_out;       // optional [V]: normalised probabilities in id order
+  int32_t* kept_out;      // optional: number of ids kept by the nucleus
+  uint32_t* keys[2];      // radix ping-pong: float bits of the probabilities
+  uint32_t* ids[2];
+  uint32_t* hist;         // [kPasses][kMaxTiles][256]
+  int V;
+  int mode;
+  int use_pen;
+  float pen;
+  int scale;              // temperature != 1
+  float temp;
+  float t32;              // smallest float32 >= top_p
+};
+
+// ---------------------------------------------------------------- wave/block helpers
+__device__ inline int lane_id() { return threadIdx.x & 63; }
+
+// Inclusive prefix sum over the 64 lanes (row shifts within rows of 16, then row broadcasts).
+__device__ inline int wave_incl_scan(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false);   // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false);   // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false);   // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false);   // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);   // row_bcast:15 -> rows 1, 3
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false);   // row_bcast:31 -> rows 2, 3
+  return v;
+}
+
+__device__ inline int readlane_i(int v, int l) { return __builtin_amdgcn_readlane(v, l); }
+__device__ inline float readlane_f(float v, int l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+
+__device__ inline float wave_max(float v) {
+  for (int o = 32; o; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  return v;
+}
+
+__device__ inline int wave_sum_i(int v) {
+  for (int o = 32; o; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+__device__ inline uint64_t wave_max_u64(uint64_t v) {
+  for (int o = 32; o; o >>= 1) {
+    const uint64_t w = __shfl_xor(v, o);
+    v = w > v ? w : v;
+  }
+  return v;
+}
+
+// float -> unsigned with the same order
+__device__ inline uint32_t ordered(float f) {
+  const uint32_t b = __float_as_uint(f);
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+__device__ inline int pad(int j) { return j + (j >> 5); }
+
+__device__ inline int binade(float s) { return int((__float_as_uint(s) >> 23) & 0xffu) - 127; }
+
+struct BlockScratch {   // small shared scratch of the 1024-thread kernels
+  float vals[kT];       // pairwise-tree node sums
+  double dw[kWaves];
+  float fw[kWaves];
+  int iw[kWaves];
+  uint64_t kw[kWaves];
+  double dtot;
+  int i0;
+};
+
+__device__ float block_max(float v, BlockScratch& b) {
+  v = wave_max(v);
+  if (lane_id() == 0) b.fw[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float m = b.fw[0];
+  for (int i = 1; i < kWaves; ++i) m = fmaxf(m, b.fw[i]);
+  __syncthreads();
+  return m;
+}
+
+__device__ int block_sum_i(int v, BlockScratch& b) {
+  v = wave_sum_i(v);
+  if (lane_id() == 0) b.iw[threadIdx.x >> 6] = v;
+  __syncthreads();
+  int s = 0;
+  for (int i = 0; i < kWaves; ++i) s += b.iw[i];
+  __syncthreads();
+  return s;
+}
+
+__device__ uint64_t block_max_u64(uint64_t v, BlockScratch& b) {
+  v = wave_max_u64(v);
+  if (lane_id() == 0) b.kw[threadIdx.x >> 6] = v;
+  __syncthreads();
+  uint64_t m = b.kw[0];
+  for (int i = 1; i < kWaves; ++i) m = b.kw[i] > m ? b.kw[i] : m;
+  __syncthreads();
+  return m;
+}
+
+// Sum of the float64 values of all threads with lower index (thread order).
+__device__ double block_excl_scan_f64(double v, BlockScratch& b) {
+  const int lane = lane_id(), w = threadIdx.x >> 6;
+  double incl = v;
+  for (int o = 1; o < 64; o <<= 1) {
+    const double t = __shfl_up(incl, o);
+    if (lane >= o) incl += t;
+  }
+  double excl = __shfl_up(incl, 1);
+  if (lane == 0) excl = 0.0;
+  if (lane == 63) b.dw[w] = incl;
+  __syncthreads();
+  double off = 0.0;
+  for (int i = 0; i < w; ++i) off += b.dw[i];
+  __syncthreads();
+  return w == 0 ? excl : (lane == 0 ? off : off + excl);
+}
+
+// ---------------------------------------------------------------- numpy's float32 sum
+// Node (start, len) of heap slot `slot` of numpy's pairwise recursion over n entries: a node of
+// more than 128 entries splits into n2 = n/2 rounded down to a multiple of 8, and n - n2.
+__device__ bool pw_node(int n, int slot, int& start, int& len) {
+  const int id = slot + 1;
+  const int depth = 31 - __clz(id);
+  start = 0;
+  len = n;
+  for (int b = depth - 1; b >= 0; --b) {
+    if (len <= kPwBlock) return false;
+    int n2 = len / 2;
+    n2 -= n2 % 8;
+    if ((id >> b) & 1) {
+      start += n2;
+      len -= n2;
+    } else {
+      len = n2;
+    }
+  }
+  return true;
+}
+
+// numpy's pairwise leaf: < 8 entries summed in order from 0; otherwise 8 interleaved
+// accumulators over the multiple-of-8 prefix, combined as ((r0+r1)+(r2+r3))+((r4+r5)+(r6+r7)),
+// then the remaining entries added in order.
+__device__ float pw_leaf(const float* a, int start, int n) {
+  if (n < 8) {
+    float r = 0.f;
+    for (int i = 0; i < n; ++i) r += a[pad(start + i)];
+    return r;
+  }
+  float r0 = a[pad(start)], r1 = a[pad(start + 1)], r2 = a[pad(start + 2)], r3 = a[pad(start + 3)];
+  float r4 = a[pad(start + 4)], r5 = a[pad(start + 5)], r6 = a[pad(start + 6)], r7 = a[pad(start + 7)];
+  const int lim = n - (n % 8);
+  int i = 8;
+  for (; i < lim; i += 8) {
+    const int j = start + i;
+    r0 += a[pad(j)];
+    r1 += a[pad(j + 1)];
+    r2 += a[pad(j + 2)];
+    r3 += a[pad(j + 3)];
+    r4 += a[pad(j + 4)];
+    r5 += a[pad(j + 5)];
+    r6 += a[pad(j + 6)];
+    r7 += a[pad(j + 7)];
+  }
+  float res = ((r0 + r1) + (r2 + r3)) + ((r4 + r5) + (r6 + r7));
+  for (; i < n; ++i) res += a[pad(start + i)];
+  return res;
+}
+
+// numpy's float32 sum of a[0..n) (n <= 32768, padded LDS layout); every thread gets the result.
+// Buffers of 8192 entries are reduced by the pairwise recursion (thread 256*k + slot evaluates
+// heap slot `slot` of buffer k; leaves first, then inner nodes by decreasing depth) and their
+// results added in buffer order to 0.
+__device__ float np_sum(const float* a, int n, BlockScratch& b) {
+  const int t = threadIdx.x, k = t >> 8, slot = t & 255;
+  const int nbuf = (n + kRedChunk - 1) / kRedChunk;
+  const int bn = k < nbuf ? min(kRedChunk, n - k * kRedChunk) : 0;
+  int start = 0, len = 0;
+  const bool valid = k < nbuf && slot < kSlots && pw_node(bn, slot, start, len);
+  const bool leaf = valid && len <= kPwBlock;
+  if (leaf) b.vals[t] = pw_leaf(a, k * kRedChunk + start, len);
+  __syncthreads();
+  const int depth = 31 - __clz(slot + 1);
+  for (int d = 6; d >= 0; --d) {
+    if (valid && !leaf && depth == d) b.vals[t] = b.vals[(k << 8) + 2 * slot + 1] + b.vals[(k << 8) + 2 * slot + 2];
+    __syncthreads();
+  }
+  float s = 0.f;
+  for (int i = 0; i < nbuf; ++i) s += b.vals[i << 8];
+  __syncthreads();
+  return s;
+}
+
+// ---------------------------------------------------------------- inverse CDF draw
+// RandomState.choice on one uniform: the number of i < n with cdf[i] / cdf[n-1] <= u, where
+// cdf is the float64 running sum of w[i] = (divide ? v[i] / div : v[i]) (float32 values,
+// padded LDS layout).  Thread t adds entries [32t, 32t+32) in order on top of the sum of all
+// earlier entries, so every partial sum equals the sequential one whenever the float64 sums
+// are exact (float32 terms spanning fewer than 29 binades below the total).
+__device__ int inverse_cdf(const float* v, int n, bool divide, float div, double u, BlockScratch& b) {
+  const int t = threadIdx.x, base = t * kPer;
+  double tot = 0.0;
+  for (int i = 0; i < kPer; ++i) {
+    const int j = base + i;
+    if (j < n) tot += double(divide ? v[pad(j)] / div : v[pad(j)]);
+  }
+  const double excl = block_excl_scan_f64(tot, b);
+  if (base <= n - 1 && n - 1 < base + kPer) {   // cdf[n-1] as accumulated by its owner
+    double r = excl;
+    for (int i = 0; i < kPer; ++i) {
+      const int j = base + i;
+      if (j < n) r += double(divide ? v[pad(j)] / div : v[pad(j)]);
+    }
+    b.dtot = r;
+  }
+  __syncthreads();
+  const double total = b.dtot;
+  double r = excl;
+  int cnt = 0;
+  for (int i = 0; i < kPer; ++i) {
+    const int j = base + i;
+    if (j < n) {
+      r += double(divide ? v[pad(j)] / div : v[pad(j)]);
+      if (r / total <= u) ++cnt;
+    }
+  }
+  const int c = block_sum_i(cnt, b);
+  return min(c, n - 1);
+}
+
+// ---------------------------------------------------------------- nucleus cutoff
+// One wave: with cumsum the float32 running sum of the descending probabilities p[0..n),
+// returns searchsorted(cumsum, top_p) + 1 -- one past the first i with cumsum[i] >= top_p
+// (n + 1 when there is none).  t32 is the smallest float32 >= top_p, so cumsum[i] >= top_p
+// (compared in float64) exactly when cumsum[i] >= t32.
+//
+// Adding x to a float32 running sum s that stays in the binade [2^E, 2^(E+1)) adds
+// round-half-even(x / ulp) ulps, ulp = 2^(E-23), whatever s is, unless x / ulp has fraction
+// exactly 1/2 (then the parity of s decides).  64 entries at a time become integer ulp counts
+// whose exact prefix sums give every running sum, up to the first entry where the sum would
+// leave the binade, the fraction is 1/2, or top_p is reached; that entry is added with an
+// ordinary float32 addition and the walk resumes after it.  (p is sorted descending, so every
+// later x <= s and x / ulp < 2^24.)
+__device__ int nucleus_cutoff(const float* p, int n, float t32) {
+  const int lane = lane_id();
+  float s = p[pad(0)];
+  if (s >= t32) return 1;
+  const int te = binade(t32);
+  int k = 1;
+  float x = (k + lane < n) ? p[pad(k + lane)] : 0.f;
+  while (k < n) {
+    const int jn = k + 64 + lane;
+    const float xn = jn < n ? p[pad(jn)] : 0.f;   // next block, used when this one has no special entry
+    const int E = binade(s);
+    const bool valid = k + lane < n;
+    const float y = ldexpf(x, 23 - E);
+    const bool tie = (y - floorf(y)) == 0.5f;
+    const int q = int(rintf(y));
+    const int S = int(ldexpf(s, 23 - E));
+    const int P = wave_incl_scan(q);
+    const int lim = te == E ? int(ldexpf(t32, 23 - E)) : (1 << 24);
+    const uint64_t m = __ballot(!valid || tie || S + P >= lim);
+    if (m == 0) {
+      s = ldexpf(float(S + readlane_i(P, 63)), E - 23);
+      k += 64;
+      x = xn;
+      continue;
+    }
+    const int f = __ffsll(static_cast<unsigned long long>(m)) - 1;
+    const int jf = k + f;
+    if (jf >= n) return n + 1;
+    const float sp = f == 0 ? s : ldexpf(float(S + readlane_i(P, f - 1)), E - 23);
+    const float sn = sp + readlane_f(x, f);
+    if (sn >= t32) return jf + 1;
+    s = sn;
+    k = jf + 1;
+    x = (k + lane < n) ? p[pad(k + lane)] : 0.f;
+  }
+  return n + 1;
+}
+
+// ---------------------------------------------------------------- kernels
+__device__ void finish(const SArgs& a, int token) {
+  if (threadIdx.x == 0) {
+    a.token_out[0] = token;
+    a.seen[token] = 1;
+  }
+}
+
+__global__ __launch_bounds__(kT) void sample_prep_kernel(SArgs a) {
+  extern __shared__ float sh_e[];   // kVMax entries, padded layout
+  __shared__ BlockScratch b;
+  const int t = threadIdx.x, V = a.V;
+  float l[kPer];
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int j = t + kT * i;
+    float v = -INFINITY;
+    if (j < V) {
+      v = a.logits[j];
+      if (a.use_pen && a.seen[j]) v = v > 0.f ? v / a.pen : v * a.pen;
+    }
+    l[i] = v;
+  }
+  if (a.mode == kGreedy) {   // argmax, lowest id on ties
+    uint64_t best = 0;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int j = t + kT * i;
+      if (j < V) {
+        const uint64_t key = (uint64_t(ordered(l[i])) << 32) | uint32_t(0xffffffffu - uint32_t(j));
+        best = key > best ? key : best;
+      }
+    }
+    best = block_max_u64(best, b);
+    finish(a, int(0xffffffffu - uint32_t(best & 0xffffffffu)));
+    return;
+  }
+  // scaled logits to LDS; exp and normalisation run from LDS one entry at a time
+  float m = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int j = t + kT * i;
+    if (j < V) {
+      if (a.scale) l[i] = l[i] / a.temp;
+      sh_e[pad(j)] = l[i];
+      m = fmaxf(m, l[i]);
+    }
+  }
+  m = block_max(m, b);
+  for (int j = t; j < V; j += kT) sh_e[pad(j)] = float(exp(double(sh_e[pad(j)] - m)));
+  __syncthreads();
+  const float sum = np_sum(sh_e, V, b);
+  for (int j = t; j < V; j += kT) {
+    const float pj = sh_e[pad(j)] / sum;
+    sh_e[pad(j)] = pj;
+    if (a.probs_out) a.probs_out[j] = pj;
+  }
+  __syncthreads();
+  if (a.mode == kFull) {
+    const int tok = inverse_cdf(sh_e, V, false, 1.f, a.u[0], b);
+    finish(a, tok);
+    return;
+  }
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int j = t + kT * i;
+    l[i] = j < V ? sh_e[pad(j)] : 0.f;
+  }
+  __syncthreads();
+  // top_p < 1: radix keys in id order and the first pass's per-tile digit counts
+  const int ntiles = (V + kTile - 1) / kTile;
+  uint32_t* hl = reinterpret_cast<uint32_t*>(sh_e);
+  for (int i = t; i < ntiles * 256; i += kT) hl[i] = 0;
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int j = t + kT * i;
+    if (j < V) {
+      const uint32_t key = __float_as_uint(l[i]);
+      a.keys[0][j] = key;
+      a.ids[0][j] = uint32_t(j);
+      atomicAdd(&hl[(j / kTile) * 256 + (255u - (key & 255u))], 1u);
+    }
+  }
+  __syncthreads();
+  for (int i = t; i < ntiles * 256; i += kT) {
+    a.hist[i] = hl[i];
+    for (int p = 1; p < kPasses; ++p) a.hist[p * kHistWords + i] = 0;
+  }
+}
+
+// One stable LSD pass over digit `pass` (bits 8*pass..8*pass+7, descending order) from
+// keys/ids[pass & 1] to keys/ids[(pass + 1) & 1].  Workgroup w moves entries
+// [512w, 512w+512) in order: an entry's destination is the number of entries with a larger
+// digit, plus those with the same digit in earlier tiles, earlier rounds of this tile, earlier
+// waves of this round and lower lanes of this wave.
+__global__ __launch_bounds__(kTileThreads) void sample_radix_kernel(SArgs a, int pass) {
+  __shared__ uint32_t base[256], run[256], wcnt[kTileThreads / 64][256], wtot[kTileThreads / 64];
+  const int t = threadIdx.x, w = blockIdx.x, wv = t >> 6, lane = lane_id();
+  const int V = a.V, ntiles = (V + kTile - 1) / kTile;
+  const uint32_t* H = a.hist + pass * kHistWords;
+  uint32_t tot = 0, part = 0;
+#pragma unroll
+  for (int i = 0; i < kMaxTiles; ++i) {
+    const uint32_t h = i < ntiles ? H[i * 256 + t] : 0u;
+    tot += h;
+    if (i < w) part += h;
+  }
+  const int inc = wave_incl_scan(int(tot));
+  if (lane == 63) wtot[wv] = uint32_t(inc);
+  __syncthreads();
+  uint32_t off = 0;
+  for (int i = 0; i < wv; ++i) off += wtot[i];
+  base[t] = off + uint32_t(inc) - tot + part;
+  run[t] = 0;
+  const uint32_t* kin = a.keys[pass & 1];
+  const uint32_t* iin = a.ids[pass & 1];
+  uint32_t* kout = a.keys[(pass + 1) & 1];
+  uint32_t* iout = a.ids[(pass + 1) & 1];
+  const int shift = 8 * pass;
+  const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+  for (int r = 0; r < kRounds; ++r) {
+    for (int i = 0; i < kTileThreads / 64; ++i) wcnt[i][t] = 0;
+    __syncthreads();
+    const int e = w * kTile + r * kTileThreads + t;
+    const bool valid = e < V;
+    const uint32_t key = valid ? kin[e] : 0u;
+    const uint32_t id = valid ? iin[e] : 0u;
+    const uint32_t dig = 255u - ((key >> shift) & 255u);
+    uint64_t peers = __ballot(valid);
+    for (int bit = 0; bit < 8; ++bit) {
+      const bool on = (dig >> bit) & 1u;
+      const uint64_t bb = __ballot(on);
+      peers &= on ? bb : ~bb;
+    }
+    const int rk = __popcll(peers & below);
+    if (valid && rk == 0) wcnt[wv][dig] = uint32_t(__popcll(peers));
+    __syncthreads();
+    uint32_t acc = 0;
+    for (int i = 0; i < kTileThreads / 64; ++i) {   // exclusive prefix over waves, digit t
+      const uint32_t c = wcnt[i][t];
+      wcnt[i][t] = acc;
+      acc += c;
+    }
+    __syncthreads();
+    const uint32_t pos = base[dig] + run[dig] + wcnt[wv][dig] + uint32_t(rk);
+    if (valid && pos < uint32_t(V)) {   // always true when the counts are consistent
+      kout[pos] = key;
+      iout[pos] = id;
+      if (pass + 1 < kPasses) {
+        const uint32_t nd = 255u - ((key >> (shift + 8)) & 255u);
+        atomicAdd(&a.hist[(pass + 1) * kHistWords + (pos / kTile) * 256 + nd], 1u);
+      }
+    }
+    __syncthreads();
+    run[t] += acc;
+  }
+}
+
+__global__ __launch_bounds__(kT) void sample_nucleus_kernel(SArgs a) {
+  extern __shared__ float sh_p[];   // sorted probabilities, padded layout
+  __shared__ BlockScratch b;
+  const int t = threadIdx.x, V = a.V;
+  const uint32_t* ks = a.keys[kPasses & 1];
+  for (int j = t; j < V; j += kT) sh_p[pad(j)] = __uint_as_float(ks[j]);
+  __syncthreads();
+  if (t < 64) {
+    const int c = nucleus_cutoff(sh_p, V, a.t32);
+    if (t == 0) b.i0 = c;
+  }
+  __syncthreads();
+  const int kept = min(b.i0, V);
+  const float fsum = np_sum(sh_p, kept, b);
+  const int pos = inverse_cdf(sh_p, kept, true, fsum, a.u[0], b);
+  if (t == 0 && a.kept_out) a.kept_out[0] = kept;
+  finish(a, int(a.ids[kPasses & 1][pos]));
+}
+
+// ---------------------------------------------------------------- host side
+struct SLayout {
+  size_t keys0, keys1, ids0, ids1, hist, bytes;
+};
+
+static size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+static SLayout slayout(int V) {
+  SLayout s;
+  const size_t arr = align256(size_t(V) * sizeof(uint32_t));
+  s.keys0 = 0;
+  s.keys1 = arr;
+  s.ids0 = 2 * arr;
+  s.ids1 = 3 * arr;
+  s.hist = 4 * arr;
+  s.bytes = s.hist + align256(size_t(kPasses) * kHistWords * sizeof(uint32_t));
+  return s;
+}
+
+static hipError_t set_lds_once() {
+  static bool done = false;
+  if (done) return hipSuccess;
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&sample_prep_kernel),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, int(kLdsBig));
+  if (e != hipSuccess) return e;
+  e = hipFuncSetAttribute(reinterpret_cast<const void*>(&sample_nucleus_kernel),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, int(kLdsBig));
+  if (e != hipSuccess) return e;
+  done = true;
+  return hipSuccess;
+}
+
+}  // namespace mss
+
+using namespace mss;
+
+extern "C" int64_t msd_sample_workspace_bytes(int32_t vocab) {
+  if (vocab <= 0 || vocab > kVMax) return MSD_E_CONFIG;
+  return int64_t(slayout(vocab).bytes);
+}
+
+extern "C" int32_t msd_sample_token(const float* logits, int32_t vocab, double temperature, double top_p,
+                                    double rep_penalty, uint8_t* seen, const double* uniform,
+                                    int32_t* token_out, float* probs_out, int32_t* kept_out,
+                                    void* workspace, void* stream) {
+  if (vocab <= 0 || vocab > kVMax) return MSD_E_CONFIG;
+  if (!logits || !seen || !token_out || !workspace) return MSD_E_ARG;
+  if (!(temperature >= 0.0) || !isfinite(temperature) || !isfinite(rep_penalty) || rep_penalty == 0.0 ||
+      isnan(top_p))
+    return MSD_E_ARG;
+  if (reinterpret_cast<uintptr_t>(workspace) & 255) return MSD_E_ARG;
+  SArgs a;
+  a.mode = temperature == 0.0 ? kGreedy : (top_p < 1.0 ? kNucleus : kFull);
+  if (a.mode != kGreedy && !uniform) return MSD_E_ARG;
+  const SLayout L = slayout(vocab);
+  char* ws = static_cast<char*>(workspace);
+  a.logits = logits;
+  a.seen = seen;
+  a.u = uniform;
+  a.token_out = token_out;
+  a.probs_out = probs_out;
+  a.kept_out = kept_out;
+  a.keys[0] = reinterpret_cast<uint32_t*>(ws + L.keys0);
+  a.keys[1] = reinterpret_cast<uint32_t*>(ws + L.keys1);
+  a.ids[0] = reinterpret_cast<uint32_t*>(ws + L.ids0);
+  a.ids[1] = reinterpret_cast<uint32_t*>(ws + L.ids1);
+  a.hist = reinterpret_cast<uint32_t*>(ws + L.hist);
+  a.V = vocab;
+  a.use_pen = rep_penalty != 1.0;
+  a.pen = float(rep_penalty);
+  a.scale = temperature != 1.0;
+  a.temp = float(temperature);
+  float t32 = float(top_p);
+  if (double(t32) < top_p) t32 = nextafterf(t32, INFINITY);
+  a.t32 = t32;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (set_lds_once() != hipSuccess) return MSD_E_HIP;
+  hipLaunchKernelGGL(sample_prep_kernel, dim3(1), dim3(kT), kLdsBig, s, a);
+  if (hipGetLastError() != hipSuccess) return MSD_E_HIP;
+  if (a.mode == kNucleus) {
+    const int ntiles = (vocab + kTile - 1) / kTile;
+    for (int p = 0; p < kPasses; ++p) {
+      hipLaunchKernelGGL(sample_radix_kernel, dim3(ntiles), dim3(kTileThreads), 0, s, a, p);
+      if (hipGetLastError() != hipSuccess) return MSD_E_HIP;
+    }
+    hipLaunchKernelGGL(sample_nucleus_kernel, dim3(1), dim3(kT), kLdsBig, s, a);
+    if (hipGetLastError() != hipSuccess) return MSD_E_HIP;
+  }
+  return MSD_OK;
+}

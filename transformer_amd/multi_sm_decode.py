@@ -26,6 +26,8 @@ class Decoder:
         self.w = w
         self.config = dict(config)
         self.device = torch.device(device) if device is not None else w["packed_w"].device
+        if self.device.type == "cuda" and self.device.index is None:
+            self.device = torch.device("cuda", torch.cuda.current_device())
         self._cfg = _lib.MsdConfig.from_dict(self.config)
         L = _lib.lib()
         if n_workgroups is None:
