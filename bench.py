@@ -13,6 +13,13 @@ Prints one JSON line.  value = decoded tokens per second; roofline.achieved = al
 bytes per step (weights + KV rows read + KV row written, averaged over the timed
 positions) / measured average step time; cpu_baseline = the numpy oracle's cached decode
 step on the host (a bounded sample of positions).
+
+Secondary figures on the same weights (not the headline value):
+  prefill_128     matrix-core prefill of a 128-token prompt (ms, median of runs), then 128
+                  greedy decode steps after it (tok/s)
+  sampled_decode  64-token prompt, then 256 tokens with temperature 0.7, top-p 0.95 and
+                  repetition penalty 1.2 drawn on the device (decode + sampler chained, tok/s),
+                  and the sampler alone per token (us)
 """
 import argparse
 import json
@@ -43,6 +50,77 @@ def positions(start, stop, k):
     return [start + (i % span) for i in range(k)]
 
 
+def _events_ms(fn, reps):
+    import torch
+    s = torch.cuda.current_stream()
+    times = []
+    for _ in range(reps):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record(s)
+        fn()
+        e1.record(s)
+        torch.cuda.synchronize()
+        times.append(e0.elapsed_time(e1))
+    times.sort()
+    return times[len(times) // 2]
+
+
+def secondary(w, cfg, dec):
+    """Prefill (128 tokens) and sampled-decode figures, on the decoder's weights and KV."""
+    import numpy as np
+    import torch
+
+    from transformer_amd.generate import Sampler
+    from transformer_amd.prefill import Prefiller
+    from transformer_amd.synthetic import make_prompt
+
+    out = {}
+    # prefill of a 128-token prompt, then 128 greedy steps chained on the device
+    prompt = make_prompt(128, cfg["vocab_size"], seed=2)
+    pf = Prefiller(w, cfg, max_tokens=128)
+    tok_dev = torch.as_tensor(np.asarray(prompt, dtype=np.int32)).cuda()
+    ring = torch.zeros((129, 2), dtype=torch.int32, device="cuda")
+    pf.launch(tok_dev, dec.kv, out=ring[0])
+    ms = _events_ms(lambda: pf.launch(tok_dev, dec.kv, out=ring[0]), 7)
+
+    def steps():
+        for i in range(128):
+            dec.launch(ring[i, 0:1], 128 + i, out=ring[i + 1])
+    steps()
+    dms = _events_ms(steps, 3)
+    if int(ring[:, 1].abs().max()) != 0:
+        raise RuntimeError("decode status set after prefill")
+    out["prefill_128"] = {"prefill_ms": round(ms, 4), "prefill_tok_s": round(128 / (ms / 1e3), 1),
+                          "decode_after_tok_s": round(128 / (dms / 1e3), 1),
+                          "workload": "306M, 128-token prompt prefilled in one call, then 128 greedy steps"}
+    # sampled decode: 64-token prompt, 256 tokens, temperature 0.7 / top-p 0.95 / penalty 1.2
+    prompt = make_prompt(64, cfg["vocab_size"], seed=1)
+    pf64 = Prefiller(w, cfg, max_tokens=64)
+    smp = Sampler(cfg["vocab_size"])
+    u = torch.as_tensor(np.random.RandomState(11).random_sample(256)).cuda()
+    toks = torch.zeros(256, dtype=torch.int32, device="cuda")
+    st = torch.zeros((256, 2), dtype=torch.int32, device="cuda")
+    tok_dev = torch.as_tensor(np.asarray(prompt, dtype=np.int32)).cuda()
+
+    def sampled():
+        smp.reset()
+        pf64.launch(tok_dev, dec.kv, out=st[0])
+        smp.launch(pf64.logits, 0.7, 0.95, 1.2, u=u[0:1], out=toks[0:1])
+        for i in range(1, 256):
+            dec.launch(toks[i - 1:i], 63 + i, out=st[i])
+            smp.launch(dec.logits, 0.7, 0.95, 1.2, u=u[i:i + 1], out=toks[i:i + 1])
+    sampled()
+    sms = _events_ms(sampled, 3)
+    if int(st[:, 1].abs().max()) != 0:
+        raise RuntimeError("decode status set in the sampled run")
+    one = _events_ms(lambda: [smp.launch(dec.logits, 0.7, 0.95, 1.2, u=u[0:1], out=toks[0:1]) for _ in range(50)], 3)
+    out["sampled_decode"] = {"tok_s": round(256 / (sms / 1e3), 1), "sampler_us_per_token": round(one / 50 * 1e3, 2),
+                             "workload": "306M, 64-token prompt, 256 tokens, temp 0.7 top-p 0.95 rep-penalty 1.2"}
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -51,6 +129,7 @@ def main():
     ap.add_argument("--cpu-sample", type=int, default=479,
                     help="oracle decode steps timed for cpu_baseline, from position 32 (0 = skip)")
     ap.add_argument("--synced-steps", type=int, default=128, help="host-synced steps for the secondary figure")
+    ap.add_argument("--secondary", type=int, default=1, help="also time the prefill and sampled-decode workloads")
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
                     help="run one device-to-device copy of this many MiB before decoding (reference "
                          "kernel for scaling HBM byte counters; not timed)")
@@ -163,6 +242,10 @@ def main():
                "sample": f"{n} greedy cached decode steps of the numpy oracle (f32 on bf16-valued 306M "
                          f"weights) from position {start}, {cpu_s:.1f}s"}
 
+    extra = {}
+    if args.secondary:
+        extra = secondary(w, cfg, dec)
+
     line = {
         "metric": METRIC,
         "value": round(tok_s, 1),
@@ -186,6 +269,7 @@ def main():
         "cpu_baseline": cpu,
         "host_synced_tok_s": None if synced is None else round(synced, 1),
     }
+    line.update(extra)
     print(json.dumps(line), flush=True)
 
 

@@ -17,6 +17,10 @@
  *                            (generate.py:63,65) taken from a supplied uniform
  *   msd_sample_workspace_bytes
  *                         <- the host numpy temporaries of generate.py:28-65
+ *   msd_prefill           <- model.py:194-231 prefill_with_kv(params, config, x) as used by
+ *                            generate.py:70-90 (_prefill)
+ *   msd_prefill_workspace_bytes
+ *                         <- the activations XLA allocates for prefill_with_kv
  */
 #ifndef MSDECODE_H
 #define MSDECODE_H
@@ -129,6 +133,23 @@ int32_t msd_sample_token(const float* logits, int32_t vocab, double temperature,
                          double rep_penalty, uint8_t* seen, const double* uniform,
                          int32_t* token_out, float* probs_out, int32_t* kept_out,
                          void* workspace, void* stream);
+
+/* Bytes of device workspace msd_prefill needs for a prompt of n_tokens tokens. */
+int64_t msd_prefill_workspace_bytes(const msd_config* cfg, int32_t n_tokens);
+
+/* Forward pass over a prompt: tokens[0..n_tokens) at positions 0..n_tokens-1 (device int32).
+ * Writes the KV cache rows 0..n_tokens-1 of every layer (bf16, post-RoPE K) and the f32
+ * logits of the last position; with logits_all != NULL also the logits of every position
+ * (n_tokens x vocab_size, row-major).  next_token (device int32[2]) receives the argmax of the
+ * last position's logits (lowest index on ties) and a status word (bit 1 = a token id was out
+ * of range).  Every projection is a bf16 x bf16 matrix-core product accumulated in f32 with the
+ * activations rounded to bf16 on entry; residual stream, RoPE, softmax and SwiGLU are f32.
+ * Weight arguments as for msd_decode_step.  Requires d_model, 2*d_ff and vocab_size to be
+ * multiples of 64, d_ff a multiple of 32 and n_tokens <= context_len. */
+int32_t msd_prefill(const msd_config* cfg, const void* token_emb, const void* output_proj,
+                    const void* packed_w, const void* lnf_s, const float* rope,
+                    const int32_t* tokens, int32_t n_tokens, void* kv, void* workspace,
+                    float* logits_last, float* logits_all, int32_t* next_token, void* stream);
 
 #ifdef __cplusplus
 }

@@ -202,10 +202,11 @@ def decode_step(params, config, token, pos, k_caches, v_caches, act_round=None, 
 
 
 def greedy_generate(params, config, prompt, n_new, prefill="step", act_round=None,
-                    return_logits=False):
+                    return_logits=False, prefill_act_round="same"):
     """Greedy generation following generate.py:92-123.
 
-    prefill="full": the prompt goes through ``prefill_with_kv`` (the reference pipeline);
+    prefill="full": the prompt goes through ``prefill_with_kv`` (the reference pipeline),
+    with ``prefill_act_round`` (default: the same as ``act_round``);
     prefill="step": the prompt is fed through ``decode_step`` at positions 0..P-1.
     The first new token is the argmax at position P-1; step i then runs at pos P+i on
     the previous token.  Returns the list of n_new tokens (and per-token logits).
@@ -213,7 +214,8 @@ def greedy_generate(params, config, prompt, n_new, prefill="step", act_round=Non
     P = len(prompt)
     rope = precompute_rope_table(config["context_len"], config["d_head"], dtype=params["token_emb"].dtype)
     if prefill == "full":
-        logits_all, kc, vc = prefill_with_kv(params, config, prompt, act_round)
+        par = act_round if prefill_act_round == "same" else prefill_act_round
+        logits_all, kc, vc = prefill_with_kv(params, config, prompt, par)
         last = logits_all[P - 1]
     else:
         kc, vc = new_kv_cache(config, params["token_emb"].dtype)

@@ -1,0 +1,128 @@
+"""Parity of the matrix-core prefill (msd_prefill) with the oracle (GPU).
+
+The prefill rounds every projection input to bf16 and accumulates in f32, so the oracle
+is ``prefill_with_kv(..., act_round="bf16")`` (model.py:194-231 with those rounding points);
+logits are compared to 2e-2 abs / 1e-2 rel, the bf16 KV cache rows to the same bound.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import model as om
+from transformer_amd.configs import M306, TINY
+from transformer_amd.fused_decode_nlayer import (new_kv_packed, prepare_decode_weights_nlayer,
+                                                 unpack_kv_caches)
+from transformer_amd.multi_sm_decode import Decoder
+from transformer_amd.prefill import Prefiller, prefill_with_kv
+from transformer_amd.synthetic import make_params, make_prompt
+
+pytestmark = pytest.mark.gpu
+
+ATOL, RTOL = 2e-2, 1e-2
+SENTINEL = 7.0
+
+
+@pytest.fixture(scope="module")
+def tiny():
+    params = make_params(TINY, seed=0)
+    return params, prepare_decode_weights_nlayer(params, TINY)
+
+
+@pytest.fixture(scope="module")
+def m306():
+    params = make_params(M306, seed=0, resid_scaled=True)
+    return params, prepare_decode_weights_nlayer(params, M306)
+
+
+def _run(w, cfg, toks, all_logits=True):
+    T = len(toks)
+    pf = Prefiller(w, cfg, max_tokens=T)
+    kv = new_kv_packed(cfg).fill_(SENTINEL)
+    la = torch.empty((T, cfg["vocab_size"]), dtype=torch.float32, device="cuda") if all_logits else None
+    out = pf.launch(toks, kv, logits_all=la)
+    torch.cuda.synchronize()
+    return (None if la is None else la.cpu().numpy()), pf.logits.cpu().numpy(), out.cpu().numpy(), kv
+
+
+def _check_kv(kv, cfg, T, kc, vc):
+    ks, vs = unpack_kv_caches(kv, cfg["n_layers"], cfg["n_kv_heads"], cfg["context_len"], cfg["d_head"])
+    for l in range(cfg["n_layers"]):
+        k = ks[l].float().cpu().numpy()
+        v = vs[l].float().cpu().numpy()
+        np.testing.assert_allclose(k[:, :T], kc[l][:, :T], atol=ATOL, rtol=RTOL)
+        np.testing.assert_allclose(v[:, :T], vc[l][:, :T], atol=ATOL, rtol=RTOL)
+        assert np.all(k[:, T:] == SENTINEL) and np.all(v[:, T:] == SENTINEL), "rows >= T were written"
+
+
+@pytest.mark.parametrize("T", [1, 16, 77, 128])
+def test_tiny_prefill_matches_oracle(tiny, T):
+    params, w = tiny
+    toks = make_prompt(T, TINY["vocab_size"], seed=100 + T)
+    la, last, out, kv = _run(w, TINY, toks)
+    ref, kc, vc = om.prefill_with_kv(params, TINY, toks, act_round="bf16")
+    np.testing.assert_allclose(la, ref, atol=ATOL, rtol=RTOL)
+    assert np.array_equal(last, la[-1])
+    assert out[0] == int(np.argmax(la[-1])) and out[1] == 0
+    _check_kv(kv, TINY, T, kc, vc)
+    # the last-position-only path computes the same row bitwise
+    _, last2, out2, _ = _run(w, TINY, toks, all_logits=False)
+    assert np.array_equal(last2, last) and out2[0] == out[0]
+
+
+def test_306m_prefill_128_matches_oracle(m306):
+    """The prefill of a 128-token prompt on the 306M configuration."""
+    params, w = m306
+    toks = make_prompt(128, M306["vocab_size"], seed=3)
+    la, last, out, kv = _run(w, M306, toks)
+    ref, kc, vc = om.prefill_with_kv(params, M306, toks, act_round="bf16")
+    print("306M prefill max |logit diff|:", float(np.max(np.abs(la - ref))))
+    np.testing.assert_allclose(la, ref, atol=ATOL, rtol=RTOL)
+    _check_kv(kv, M306, 128, kc, vc)
+
+
+def _gpu_greedy_after_prefill(w, cfg, prompt, n):
+    dec = Decoder(w, cfg)
+    pf = Prefiller(w, cfg, max_tokens=len(prompt))
+    out = pf.launch(prompt, dec.kv)
+    toks = [int(out[0])]
+    for i in range(n - 1):
+        t, _ = dec.step(toks[-1], len(prompt) + i)
+        toks.append(t)
+    return toks
+
+
+@pytest.mark.parametrize("cfgname", ["tiny", "m306"])
+def test_prefill_then_decode_token_exact(cfgname, request):
+    """The reference pipeline: prefill the prompt, then decode greedily (generate.py:70-123)."""
+    params, w = request.getfixturevalue(cfgname)
+    cfg = TINY if cfgname == "tiny" else M306
+    prompt = make_prompt(48 if cfgname == "tiny" else 128, cfg["vocab_size"], seed=9)
+    n = 48 if cfgname == "tiny" else 96
+    got = _gpu_greedy_after_prefill(w, cfg, prompt, n)
+    ref = om.greedy_generate(params, cfg, prompt, n, prefill="full", act_round=None, prefill_act_round="bf16")
+    assert got == ref
+
+
+def test_reference_signature_prefill_with_kv(tiny):
+    params, w = tiny
+    toks = make_prompt(20, TINY["vocab_size"], seed=4)
+    logits, ks, vs = prefill_with_kv(params, TINY, toks)
+    ref, kc, vc = om.prefill_with_kv(params, TINY, toks, act_round="bf16")
+    assert tuple(logits.shape) == (20, TINY["vocab_size"])
+    np.testing.assert_allclose(logits.cpu().numpy(), ref, atol=ATOL, rtol=RTOL)
+    assert len(ks) == TINY["n_layers"] and tuple(ks[0].shape) == (1, 128, 64)
+    np.testing.assert_allclose(ks[2][:, :20].float().cpu().numpy(), kc[2][:, :20], atol=ATOL, rtol=RTOL)
+
+
+def test_prefill_rejects_bad_input(tiny):
+    params, w = tiny
+    pf = Prefiller(w, TINY, max_tokens=8)
+    kv = new_kv_packed(TINY)
+    with pytest.raises(ValueError):
+        pf.launch([1, 2, 40000], kv)
+    with pytest.raises(ValueError):
+        pf.launch(list(range(9)), kv)
+    bad = torch.tensor([1, 2, 99999], dtype=torch.int32, device="cuda")   # device ids: reported in the status
+    out = pf.launch(bad, kv)
+    torch.cuda.synchronize()
+    assert int(out[1]) & 2

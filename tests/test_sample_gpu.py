@@ -137,16 +137,15 @@ def _teacher_forced_sampled(params, cfg, prompt, n, temperature, top_p, pen, see
     rec = rec.cpu().numpy()
     for i in range(n):
         assert osm.sample_token(rec[i], temperature, top_p, pen, toks[:i], us[i], exp="rounded") == toks[i], i
-    kc, vc = om.new_kv_cache(cfg)
+    # oracle: prefill with bf16 projection inputs (as the matrix-core prefill), then f32 steps
+    first, kc, vc = om.prefill_with_kv(params, cfg, prompt, act_round="bf16")
     rope = om.precompute_rope_table(cfg["context_len"], cfg["d_head"])
-    for p, t in enumerate(prompt[:-1]):
-        om.decode_step(params, cfg, int(t), p, kc, vc, rope=rope)
-    seq = [int(prompt[-1])] + toks[:-1]
-    worst = 0.0
-    for i, t in enumerate(seq):
-        lg, _ = om.decode_step(params, cfg, t, len(prompt) - 1 + i, kc, vc, rope=rope)
-        np.testing.assert_allclose(rec[i], lg, atol=ATOL, rtol=RTOL)
-        worst = max(worst, float(np.max(np.abs(rec[i] - lg))))
+    np.testing.assert_allclose(rec[0], first[-1], atol=ATOL, rtol=RTOL)
+    worst = float(np.max(np.abs(rec[0] - first[-1])))
+    for i, t in enumerate(toks[:-1]):
+        lg, _ = om.decode_step(params, cfg, t, len(prompt) + i, kc, vc, rope=rope)
+        np.testing.assert_allclose(rec[i + 1], lg, atol=ATOL, rtol=RTOL)
+        worst = max(worst, float(np.max(np.abs(rec[i + 1] - lg))))
     return toks, worst
 
 
@@ -174,6 +173,9 @@ def test_stream_and_generate_agree():
     b = generate_tokens(params, TINY, prompt, 40, temperature=0.8, top_p=0.9, rep_penalty=1.1, seed=3)
     assert a == b
     g = generate_tokens(params, TINY, prompt, 40)
-    assert g == om.greedy_generate(params, TINY, prompt, 40, prefill="step")
+    assert g == om.greedy_generate(params, TINY, prompt, 40, prefill="full", prefill_act_round="bf16")
+    dec = Decoder(prepare_decode_weights_nlayer(params, TINY), TINY)
+    st = list(run_generation(dec, list(prompt), 40, prefill="step"))
+    assert st == om.greedy_generate(params, TINY, prompt, 40, prefill="step")
     p = generate_tokens(params, TINY, prompt, 20, temperature=0.0, rep_penalty=1.3)
     assert len(p) == 20

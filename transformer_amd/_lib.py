@@ -21,7 +21,8 @@ _ERRNAMES = {MSD_E_CONFIG: "unsupported config", MSD_E_ARG: "invalid argument",
              MSD_E_HIP: "HIP runtime error", MSD_E_TIMEOUT: "cross-workgroup wait timed out"}
 
 EXPORTS = ("msd_packed_weight_elems", "msd_workspace_bytes", "msd_default_workgroups",
-           "msd_decode_step", "msd_check_status", "msd_sample_workspace_bytes", "msd_sample_token")
+           "msd_decode_step", "msd_check_status", "msd_sample_workspace_bytes", "msd_sample_token",
+           "msd_prefill_workspace_bytes", "msd_prefill")
 
 
 class MsdConfig(ctypes.Structure):
@@ -69,6 +70,10 @@ def lib():
     L.msd_sample_workspace_bytes.restype = I64
     L.msd_sample_token.argtypes = [P, I32, D, D, D, P, P, P, P, P, P, P]
     L.msd_sample_token.restype = I32
+    L.msd_prefill_workspace_bytes.argtypes = [CP, I32]
+    L.msd_prefill_workspace_bytes.restype = I64
+    L.msd_prefill.argtypes = [CP, P, P, P, P, P, P, I32, P, P, P, P, P, P]
+    L.msd_prefill.restype = I32
     _lib = L
     return L
 

@@ -56,7 +56,9 @@ __device__ uint64_t msd_trace_buffer[4096 * 32];
 constexpr int kDh = 64;          // head dimension (fixed)
 constexpr int kChunkMax = 64;    // attention positions per chunk (one per lane of a wave)
 constexpr int kPartStride = 66;  // per (chunk, head): m, l, o[64]
-constexpr int kKPad = kDh + 1;   // LDS row stride of cached K rows (floats)
+// LDS row stride of cached K rows (floats): 16-byte aligned rows whose 128-bit reads by 16
+// consecutive lanes (one LDS pass) start 4 banks apart, so they never conflict.
+constexpr int kKPad = kDh + 4;
 constexpr uint32_t kSpinLimit = 1u << 20;
 
 constexpr int kWavesC = 4;      // compute waves per workgroup
@@ -71,10 +73,15 @@ struct Layout {
   int64_t off_ln1, off_ln2, off_qkv, off_o, off_gu, off_dn, layer_elems;
   // exchange words per layer (uint64)
   int64_t x_qkv, x_part, x_attn, x_hd1, x_act, x_hd2, x_layer;
+  int64_t x_rep;   // word stride between the replicas of the all-gathered vectors
   int64_t ctrl_bytes;
   // producer flags: flags[(layer * kNumEx + exchange) * G + producer_workgroup] (uint32)
   int64_t flag_words;   // uint32 flags per layer
 };
+
+// Replicas of every exchange vector that all workgroups gather (workgroup w reads replica
+// w % kRep, its XCD under the round-robin dispatch of workgroups to XCDs).
+constexpr int kRep = 8;
 
 // exchanges of a layer (index into the flag arrays)
 enum { kExQkv = 0, kExPart = 1, kExAttn = 2, kExHd1 = 3, kExAct = 4, kExHd2 = 5, kNumEx = 6 };
@@ -101,7 +108,11 @@ __host__ __device__ inline Layout make_layout(int d, int H, int KV, int ff, int 
   t.x_hd1 = t.x_attn + align64(d);
   t.x_act = t.x_hd1 + align64(d);
   t.x_hd2 = t.x_act + align64(ff);
-  t.x_layer = t.x_hd2 + align64(d);
+  // attn, hd1, act and hd2 are read by every workgroup: kRep replicas (at a stride that is
+  // not a multiple of 4 KB) spread those reads over the memory channels
+  const int64_t rep_words = t.x_hd2 + align64(d) - t.x_attn;
+  t.x_rep = ((rep_words + 511) & ~int64_t(511)) + 32;
+  t.x_layer = t.x_attn + kRep * t.x_rep;
   t.ctrl_bytes = 256;
   t.flag_words = int64_t(kNumEx) * G;
   return t;
@@ -502,17 +513,24 @@ __device__ void exchange_role(const Args& a, const Ctx& c, int token) {
     for (int k = 0; k < HPW; ++k) h[k] = h[k] + __uint_as_float(uint32_t(wd[k]));
   };
   // exchange wave 0: publish the compute waves' outputs of this phase, then the flag
-  auto publish = [&](uint64_t* X, uint32_t* flag) {
+  auto publish = [&](uint64_t* X, uint32_t* flag, bool replicated) {
     ++pphase;
     if (ew != 0) return;
     lds_wait(c.mb_out, kWavesC * pphase);
-    if (lane < kWavesC * kMbox) {
-      const int idx = c.mb_idx[lane];
-      if (idx >= 0) st_tag(X + idx, c.mb_val[lane], c.tag);
+    constexpr int E = kWavesC * kMbox;   // mailbox entries; 64 / E replicas per pass
+    const int e = lane % E;
+    const int idx = c.mb_idx[e];
+    const float v = c.mb_val[e];
+    if (replicated) {
+      for (int r = lane / E; r < kRep; r += 64 / E)
+        if (idx >= 0) st_tag(X + idx + r * a.lay.x_rep, v, c.tag);
+    } else if (lane < E && idx >= 0) {
+      st_tag(X + idx, v, c.tag);
     }
     if (lane == 0) st_flag(flag, c.tag);
     lds_bump(c.mb_pub, lane);
   };
+  const int64_t myrep = int64_t(c.wg % kRep) * a.lay.x_rep;
   load_scale(a.w + a.lay.off_ln1);
   norm_to(c.sh_x0);
   __syncthreads();
@@ -521,7 +539,7 @@ __device__ void exchange_role(const Args& a, const Ctx& c, int token) {
     uint64_t* X = layer_x(a, l);
     load_scale(layer_w(a, l) + lay.off_ln2);
     // B0 .. B1: publish q/k/v rows; attention workgroups gather q of their head group and the new k, v
-    publish(X, flagp(l, kExQkv) + c.wg);
+    publish(X, flagp(l, kExQkv) + c.wg, false);
     if (c.att) {
       poll_flags(flagp(l, kExQkv), G, c.tag, a.ctrl, lane, bad);
       gather_x(X + lay.x_qkv + int64_t(c.ag) * c.GQ * kDh, c.GQ * kDh, c.sh_q, c.tag, a.ctrl, ew, lane, bad);
@@ -572,21 +590,22 @@ __device__ void exchange_role(const Args& a, const Ctx& c, int token) {
             den += wgt * pc[1];
           }
         }
-        st_tag(X + lay.x_attn + (c.ag * c.GQ + n) * kDh + lane, num / den, c.tag);
+        for (int r = 0; r < kRep; ++r)
+          st_tag(X + lay.x_attn + r * lay.x_rep + (c.ag * c.GQ + n) * kDh + lane, num / den, c.tag);
       }
       xsync(c.sh_sync, sphase, lane);   // every head's words are issued, the partials in x1 are no longer read
       if (ew == 0 && lane == 0) st_flag(flagp(l, kExAttn) + c.ag, c.tag);
       MSD_TRACE_POINT(ew == 0, 2);
     }
     poll_flags(flagp(l, kExAttn), c.KV, c.tag, a.ctrl, lane, bad);
-    gather_x(X + lay.x_attn, D, c.sh_x1, c.tag, a.ctrl, ew, lane, bad);
+    gather_x(X + lay.x_attn + myrep, D, c.sh_x1, c.tag, a.ctrl, ew, lane, bad);
     MSD_TRACE_POINT(ew == 0, 3);
     __syncthreads();  // B2
     MSD_TRACE_POINT(ew == 0, 4);
     // B2 .. B3: publish O rows; h += O output, x0 = rmsnorm2(h)
-    publish(X, flagp(l, kExHd1) + c.wg);
+    publish(X, flagp(l, kExHd1) + c.wg, true);
     poll_flags(flagp(l, kExHd1), G, c.tag, a.ctrl, lane, bad);
-    add_h(X + lay.x_hd1);
+    add_h(X + lay.x_hd1 + myrep);
     MSD_TRACE_POINT(ew == 0, 5);
     norm_to(c.sh_x0);
     MSD_TRACE_POINT(ew == 0, 6);
@@ -594,16 +613,16 @@ __device__ void exchange_role(const Args& a, const Ctx& c, int token) {
     __syncthreads();  // B3
     MSD_TRACE_POINT(ew == 0, 7);
     // B3 .. B4: publish gate/up outputs; act -> x1
-    publish(X, flagp(l, kExAct) + c.wg);
+    publish(X, flagp(l, kExAct) + c.wg, true);
     poll_flags(flagp(l, kExAct), G, c.tag, a.ctrl, lane, bad);
-    gather_x(X + lay.x_act, c.ff, c.sh_x1, c.tag, a.ctrl, ew, lane, bad);
+    gather_x(X + lay.x_act + myrep, c.ff, c.sh_x1, c.tag, a.ctrl, ew, lane, bad);
     MSD_TRACE_POINT(ew == 0, 8);
     __syncthreads();  // B4
     MSD_TRACE_POINT(ew == 0, 9);
     // B4 .. B0': publish down rows; h += down output, x0 = rmsnorm1 of the next layer (or the final norm)
-    publish(X, flagp(l, kExHd2) + c.wg);
+    publish(X, flagp(l, kExHd2) + c.wg, true);
     poll_flags(flagp(l, kExHd2), G, c.tag, a.ctrl, lane, bad);
-    add_h(X + lay.x_hd2);
+    add_h(X + lay.x_hd2 + myrep);
     MSD_TRACE_POINT(ew == 0, 10);
     norm_to(c.sh_x0);
     __syncthreads();  // B0'
@@ -737,7 +756,7 @@ __device__ void compute_role(const Args& a, const Ctx& c) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int t = tidc + j * (kWavesC * 64);
-      if (t < nkv16) {   // K rows padded to kKPad floats so lanes of the score loop hit distinct banks
+      if (t < nkv16) {   // K rows padded to kKPad floats (conflict-free 128-bit reads in the score loop)
         const int prow = t >> 4, piece = t & 15;
         float* dst = (piece >= 8) ? c.sh_v + prow * kDh + (piece & 7) * 8 : c.sh_k + prow * kKPad + (piece & 7) * 8;
         const uint4 u = kvr[j];
@@ -751,22 +770,43 @@ __device__ void compute_role(const Args& a, const Ctx& c) {
     // ---- B1 .. B2: attention over this chunk, one head per compute wave (multi_sm_decode.py:182-221)
     if (c.att) {
       for (int n = wv; n < c.GQ; n += kWavesC) {
-        const float* q = c.sh_q + n * kDh;
+        // scores: lane = position; q (same for every lane) in registers, the lane's K row
+        // read as 16 independent 128-bit LDS loads
+        const float4* q4 = reinterpret_cast<const float4*>(c.sh_q + n * kDh);
         float s = -INFINITY;
         if (lane < c.P) {
-          float acc = 0.f;
-          const float* kr = c.sh_k + lane * kKPad;
-#pragma unroll 16
-          for (int j = 0; j < kDh; ++j) acc += q[j] * kr[j];
-          s = acc * 0.125f;
+          const float4* kr = reinterpret_cast<const float4*>(c.sh_k + lane * kKPad);
+          float4 kk[kDh / 4];
+#pragma unroll
+          for (int j = 0; j < kDh / 4; ++j) kk[j] = kr[j];
+          float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+#pragma unroll
+          for (int j = 0; j < kDh / 4; ++j) {
+            const float4 qq = q4[j];
+            a0 += qq.x * kk[j].x;
+            a1 += qq.y * kk[j].y;
+            a2 += qq.z * kk[j].z;
+            a3 += qq.w * kk[j].w;
+          }
+          s = ((a0 + a1) + (a2 + a3)) * 0.125f;
         }
         const float m = wave_max(s);
         const float e = (lane < c.P) ? expf(s - m) : 0.f;
         const float lsum = wave_sum(e);
-        c.sh_e[wv * 64 + lane] = e;
-        __builtin_amdgcn_wave_barrier();
-        float o = 0.f;
-        for (int p = 0; p < c.P; ++p) o += c.sh_e[wv * 64 + p] * c.sh_v[p * kDh + lane];
+        // o[lane = dim] = sum_p e[p] * V[p][lane]: V entries read 16 positions ahead, the
+        // weights e[p] taken from lane p as wave-uniform values
+        float o4[4] = {0.f, 0.f, 0.f, 0.f};
+        for (int p0 = 0; p0 < c.P; p0 += 16) {
+          float vv[16];
+#pragma unroll
+          for (int k = 0; k < 16; ++k) vv[k] = (p0 + k < c.P) ? c.sh_v[(p0 + k) * kDh + lane] : 0.f;
+#pragma unroll
+          for (int k = 0; k < 16; ++k) {
+            const float ek = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), p0 + k));
+            o4[k & 3] += ek * vv[k];
+          }
+        }
+        const float o = (o4[0] + o4[1]) + (o4[2] + o4[3]);
         uint64_t* part = X + lay.x_part + (int64_t(c.ag * c.nch + c.ac) * c.GQ + n) * kPartStride;
         if (lane == 0) {
           st_tag(part + 0, c.P > 0 ? m : -INFINITY, c.tag);
@@ -914,7 +954,7 @@ __global__ __launch_bounds__(kThreadsWG, 1) void decode_step_kernel(Args a) {
   c.q1 = min(c.q0 + cs, npos);
   c.P = c.q1 - c.q0;
   c.ncached = max(0, min(c.q1, c.pos) - c.q0);
-  const int xmax = max(max(D, c.ff), c.npart);
+  const int xmax = (max(max(D, c.ff), c.npart) + 3) & ~3;   // keeps sh_k 16-byte aligned
   c.sh_x0 = smem;
   c.sh_x1 = c.sh_x0 + D;
   c.sh_k = c.sh_x1 + xmax;
@@ -974,7 +1014,7 @@ static bool make_plan(const msd_config* c, int G, Plan* p) {
   const int GQ = c->n_heads / c->n_kv_heads;
   const int nch = n_chunks(c->context_len);
   const int ch_max = cdiv(c->context_len, nch);
-  const int xmax = std::max(std::max(c->d_model, c->d_ff), nch * GQ * kPartStride);
+  const int xmax = (std::max(std::max(c->d_model, c->d_ff), nch * GQ * kPartStride) + 3) & ~3;
   const size_t floats = size_t(c->d_model) + xmax + ch_max * (kKPad + kDh) + GQ * kDh + kWavesC * 64 + 64 + 4 +
                         2 * kWavesC * kMbox + 8;
   p->lds = floats * 4;

@@ -11,9 +11,12 @@ token comes from numpy's global RandomState, one ``random_sample()`` per sampled
 is the draw ``np.random.choice`` makes in the reference (generate.py:63,65), so a seeded run
 consumes the same uniform sequence.
 
-Prompt ingestion runs the decode step once per prompt token (positions 0..P-1); the logits
-of the last one are the reference's ``first_logits`` (generate.py:82), and the KV rows
-0..P-1 are those prefill_with_kv writes (rows >= P are never read before they are written).
+The prompt goes through the matrix-core prefill (``Prefiller``, model.py:194-231 as called
+by generate.py:75-82): it writes the KV rows 0..P-1 and its last-position logits are the
+reference's ``first_logits``.  The reference pads the prompt to the context length first
+(generate.py:75); rows >= P are never read before a decode step writes them, so only the P
+prompt tokens are processed.  ``prefill="step"`` feeds the prompt through the decode step
+one token at a time instead.
 """
 import ctypes
 
@@ -116,7 +119,8 @@ def _check_status(st, what):
 
 
 def run_generation(dec, prompt_ids, max_tokens, temperature=0.0, top_p=1.0, rep_penalty=1.0,
-                   uniforms=None, sampler=None, record_logits=None, sync_each=False):
+                   uniforms=None, sampler=None, record_logits=None, sync_each=False, prefill="kernel",
+                   prefiller=None):
     """Generate ``max_tokens`` tokens after ``prompt_ids`` with decoder ``dec``.
 
     Yields token ids.  With ``sync_each`` every token is read back as soon as it is drawn
@@ -147,17 +151,28 @@ def run_generation(dec, prompt_ids, max_tokens, temperature=0.0, top_p=1.0, rep_
     toks = dec_out[:, 0] if greedy else torch.zeros(max_tokens, dtype=torch.int32, device=dev)
     host = torch.zeros(2, dtype=torch.int32).pin_memory()
     pre = torch.zeros(2, dtype=torch.int32, device=dev)
-    for p, t in enumerate(prompt_ids[:-1]):
-        dec.launch(int(t), p, out=pre)
+    if prefill == "kernel":
+        from .prefill import Prefiller
+        pf = prefiller if prefiller is not None else Prefiller(dec.w, c, max_tokens=P, device=dev)
+    elif prefill == "step":
+        for p, t in enumerate(prompt_ids[:-1]):
+            dec.launch(int(t), p, out=pre)
+    else:
+        raise ValueError(prefill)
     for i in range(max_tokens):
-        if i == 0:
+        if i == 0 and prefill == "kernel":
+            pf.launch(prompt_ids, dec.kv, out=dec_out[0])
+            logits = pf.logits
+        elif i == 0:
             dec.launch(int(prompt_ids[-1]), P - 1, out=dec_out[0])
+            logits = dec.logits
         else:
             dec.launch(toks[i - 1:i], P - 1 + i, out=dec_out[i])
+            logits = dec.logits
         if record_logits is not None:
-            record_logits[i].copy_(dec.logits)
+            record_logits[i].copy_(logits)
         if not greedy:
-            sampler.launch(dec.logits, temperature, top_p, rep_penalty,
+            sampler.launch(logits, temperature, top_p, rep_penalty,
                            u=None if temperature == 0.0 else u_dev[i:i + 1], out=toks[i:i + 1])
         if sync_each:
             host[0:1].copy_(toks[i:i + 1], non_blocking=True)
