@@ -118,6 +118,35 @@ def secondary(w, cfg, dec):
     one = _events_ms(lambda: [smp.launch(dec.logits, 0.7, 0.95, 1.2, u=u[0:1], out=toks[0:1]) for _ in range(50)], 3)
     out["sampled_decode"] = {"tok_s": round(256 / (sms / 1e3), 1), "sampler_us_per_token": round(one / 50 * 1e3, 2),
                              "workload": "306M, 64-token prompt, 256 tokens, temp 0.7 top-p 0.95 rep-penalty 1.2"}
+    # batched paged decode: 8 sequences, prompts U[16, 256], 16-token pages from a shuffled pool
+    from transformer_amd.paged import PAGE, PagedBatchDecoder, PagePool
+    B, steps = 8, 128
+    rng = np.random.default_rng(4)
+    lens = [int(x) for x in rng.integers(16, 257, B)]
+    pool = PagePool(cfg, 256)
+    bd = PagedBatchDecoder(w, cfg, pool, B)
+    free = list(rng.permutation(256))
+    first = []
+    for b in range(B):
+        pages = [int(free.pop()) for _ in range(-(-(lens[b] + steps) // PAGE))]
+        first.append(int(bd.prefill(b, make_prompt(lens[b], cfg["vocab_size"], seed=50 + b), pages)[0]))
+    ring = torch.zeros((steps + 1, 2 * B), dtype=torch.int32, device="cuda")
+    ring[0, 0::2] = torch.tensor(first, dtype=torch.int32, device="cuda")
+    posr = torch.tensor([[lens[b] + i for b in range(B)] for i in range(steps)], dtype=torch.int32, device="cuda")
+    toks = torch.zeros((steps + 1, B), dtype=torch.int32, device="cuda")
+
+    def batched():
+        toks[0] = ring[0, 0::2]
+        for i in range(steps):
+            bd.launch(toks[i], posr[i], out=ring[i + 1])
+            toks[i + 1] = ring[i + 1, 0::2]
+    batched()
+    bms = _events_ms(batched, 3)
+    if int(ring[1:, 1::2].abs().max()) != 0:
+        raise RuntimeError("status set in the batched run")
+    out["batched_paged_decode"] = {"tok_s": round(B * steps / (bms / 1e3), 1), "ms_per_step": round(bms / steps, 4),
+                                   "workload": "306M, 8 sequences (prompts U[16,256]) x 128 steps, 16-token "
+                                               "pages from a shuffled pool, all 8 stepped per call"}
     return out
 
 

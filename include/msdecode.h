@@ -21,6 +21,11 @@
  *                            generate.py:70-90 (_prefill)
  *   msd_prefill_workspace_bytes
  *                         <- the activations XLA allocates for prefill_with_kv
+ *   msd_prefill_paged, msd_batch_decode_step, msd_batch_workspace_bytes
+ *                         <- the batched decode over a paged KV cache that the reference
+ *                            describes (PagePool with in-kernel page tables, batched decode
+ *                            kernels: knowledge/program.md:214-216, 245-250); no code of it is
+ *                            in the reference snapshot, so the interface is this library's own
  */
 #ifndef MSDECODE_H
 #define MSDECODE_H
@@ -150,6 +155,38 @@ int32_t msd_prefill(const msd_config* cfg, const void* token_emb, const void* ou
                     const void* packed_w, const void* lnf_s, const float* rope,
                     const int32_t* tokens, int32_t n_tokens, void* kv, void* workspace,
                     float* logits_last, float* logits_all, int32_t* next_token, void* stream);
+
+/* Paged KV cache (used by msd_prefill_paged and msd_batch_decode_step): a pool of pages of 16
+ * positions, bf16, laid out [layer][K, V][kv_head][pool_pages * 16][d_head].  A sequence's
+ * position p is stored at page page_table[p / 16], slot p % 16.  (The contiguous cache of
+ * msd_decode_step is the pool of context_len / 16 pages with the identity table.)
+ * Entries outside [0, pool_pages) and positions outside [0, context_len) or past a table are
+ * replaced by 0 and reported in the status word (bit 2); the call itself never leaves the pool. */
+
+/* msd_prefill into a paged cache: page_table is a device int32 array of max_pages entries
+ * (max_pages * 16 >= n_tokens, max_pages <= ceil(context_len / 16)) for this sequence. */
+int32_t msd_prefill_paged(const msd_config* cfg, const void* token_emb, const void* output_proj,
+                          const void* packed_w, const void* lnf_s, const float* rope,
+                          const int32_t* tokens, int32_t n_tokens, const int32_t* page_table,
+                          int32_t max_pages, void* kv_pool, int32_t pool_pages, void* workspace,
+                          float* logits_last, int32_t* next_token, void* stream);
+
+/* Bytes of device workspace msd_batch_decode_step needs for `batch` sequences. */
+int64_t msd_batch_workspace_bytes(const msd_config* cfg, int32_t batch);
+
+/* One decode step of `batch` independent sequences: sequence b feeds tokens[b] at position
+ * positions[b] (device int32 arrays), reads its cached rows 0..positions[b]-1 through
+ * page_tables[b * max_pages ...] and writes its K/V row at positions[b].  Outputs logits
+ * (batch x vocab_size f32) and next_tokens (device int32[2 * batch]: argmax of row b at 2b,
+ * the step's status word at 2b+1; bit 1 = token out of range, bit 2 = position or page out of
+ * range).  Same numerics as msd_prefill (bf16 projection inputs on the matrix cores); the
+ * current position attends with its un-rounded K/V. */
+int32_t msd_batch_decode_step(const msd_config* cfg, const void* token_emb, const void* output_proj,
+                              const void* packed_w, const void* lnf_s, const float* rope,
+                              const int32_t* tokens, const int32_t* positions, int32_t batch,
+                              const int32_t* page_tables, int32_t max_pages, void* kv_pool,
+                              int32_t pool_pages, void* workspace, float* logits,
+                              int32_t* next_tokens, void* stream);
 
 #ifdef __cplusplus
 }

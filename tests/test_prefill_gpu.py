@@ -126,3 +126,16 @@ def test_prefill_rejects_bad_input(tiny):
     out = pf.launch(bad, kv)
     torch.cuda.synchronize()
     assert int(out[1]) & 2
+
+
+def test_306m_prefill_full_context(m306):
+    """A prompt filling the whole 512-token context (projections large enough to run unsplit)."""
+    params, w = m306
+    toks = make_prompt(512, M306["vocab_size"], seed=8)
+    _, last, out, kv = _run(w, M306, toks, all_logits=False)
+    ref, kc, vc = om.prefill_with_kv(params, M306, toks, act_round="bf16")
+    np.testing.assert_allclose(last, ref[-1], atol=ATOL, rtol=RTOL)
+    ks, vs = unpack_kv_caches(kv, M306["n_layers"], M306["n_kv_heads"], M306["context_len"], M306["d_head"])
+    for l in (0, 11, 23):
+        np.testing.assert_allclose(ks[l].float().cpu().numpy(), kc[l], atol=ATOL, rtol=RTOL)
+        np.testing.assert_allclose(vs[l].float().cpu().numpy(), vc[l], atol=ATOL, rtol=RTOL)

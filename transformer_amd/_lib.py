@@ -22,7 +22,8 @@ _ERRNAMES = {MSD_E_CONFIG: "unsupported config", MSD_E_ARG: "invalid argument",
 
 EXPORTS = ("msd_packed_weight_elems", "msd_workspace_bytes", "msd_default_workgroups",
            "msd_decode_step", "msd_check_status", "msd_sample_workspace_bytes", "msd_sample_token",
-           "msd_prefill_workspace_bytes", "msd_prefill")
+           "msd_prefill_workspace_bytes", "msd_prefill", "msd_prefill_paged", "msd_batch_workspace_bytes",
+           "msd_batch_decode_step")
 
 
 class MsdConfig(ctypes.Structure):
@@ -74,6 +75,12 @@ def lib():
     L.msd_prefill_workspace_bytes.restype = I64
     L.msd_prefill.argtypes = [CP, P, P, P, P, P, P, I32, P, P, P, P, P, P]
     L.msd_prefill.restype = I32
+    L.msd_prefill_paged.argtypes = [CP, P, P, P, P, P, P, I32, P, I32, P, I32, P, P, P, P]
+    L.msd_prefill_paged.restype = I32
+    L.msd_batch_workspace_bytes.argtypes = [CP, I32]
+    L.msd_batch_workspace_bytes.restype = I64
+    L.msd_batch_decode_step.argtypes = [CP, P, P, P, P, P, P, P, I32, P, I32, P, I32, P, P, P, P]
+    L.msd_batch_decode_step.restype = I32
     _lib = L
     return L
 

@@ -1,30 +1,44 @@
-// Multi-token prefill on one MI355X (gfx950): the full forward over a prompt of M tokens,
-// writing the KV cache rows 0..M-1 and the logits of the last position (optionally of all
-// positions), with every projection on the matrix cores.
+// Matrix-core forward passes on one MI355X (gfx950) over M token rows at once:
+//   * prefill  — the M tokens of one prompt at positions 0..M-1 (model.py:194-231,
+//                prefill_with_kv, as called by generate.py:70-90)
+//   * batched decode — one token of each of M independent sequences, each at its own
+//                position, over a paged KV cache (the reference's described batched paged
+//                decode; kernels/multi_sm_decode.py:77-357 semantics per sequence)
+// writing the KV cache rows of every layer and the logits, with every projection on the
+// matrix cores.
 //
-// Reference: model.py:194-231 (prefill_with_kv), called by generate.py:70-90 (_prefill).
-// The maths is model.py:94-191 with the activations entering each projection rounded to
-// bf16 (RMSNorm outputs, attention output, SwiGLU output, final norm), the projections as
+// Numerics: model.py:94-191 with the activations entering each projection rounded to bf16
+// (RMSNorm outputs, attention output, SwiGLU output, final norm) — the rounding points of the
+// reference decode kernel (multi_sm_decode.py:143,229,268,289,320) — the projections as
 // bf16 x bf16 products accumulated in f32 (v_mfma_f32_16x16x32_bf16), the residual stream,
-// RoPE, softmax attention and SwiGLU in f32, and K/V stored to the cache as bf16 after RoPE
-// (model.py:212-215).
+// RoPE, softmax attention and SwiGLU in f32, K/V stored to the cache as bf16 after RoPE
+// (model.py:212-215).  In batched decode the current position attends with its un-rounded
+// K/V (multi_sm_decode.py:197,205).
+//
+// KV cache: [layer][K, V][kv_head][pool positions][64] bf16 with pool positions = 16 * pages.
+// A row's position p lives at page table[p / 16] * 16 + p % 16; without a table the page is
+// p / 16 (the contiguous cache of one sequence is the pool with the identity table).
 //
 // Kernels per layer, on the caller's stream:
-//   pf_norm        residual += split-K partials of the previous projection (in split order),
+//   mx_norm        residual += split-K partials of the previous projection (in split order),
 //                  then RMSNorm -> bf16 activations in the weights' permuted input order
-//   pf_gemm<QKV>   q/k/v projection; RoPE on q/k pairs, f32 q/k/v, bf16 K/V cache rows
-//   pf_attention   causal GQA attention, f32, online softmax over key chunks of 64
-//   pf_gemm<PART>  O projection, split-K partials
-//   pf_norm        (as above) -> ln2 activations
-//   pf_gemm<SWIGLU> gate/up projection; silu(gate) * up -> bf16 in down's input order
-//   pf_gemm<PART>  down projection, split-K partials
-// then pf_norm with the final scale, pf_gemm<LOGITS> against the tied embedding, pf_argmax.
+//   mx_gemm        q/k/v projection, split-K partials
+//   mx_qkv_fin     sum of the partials, RoPE on q/k, f32 q/k/v, bf16 K/V cache rows
+//   attention      prefill: causal GQA over the prompt; batched decode: each sequence over
+//                  its cached rows plus its current K/V
+//   mx_gemm        O projection, split-K partials
+//   mx_norm        (as above) -> ln2 activations
+//   mx_gemm        gate/up projection, split-K partials
+//   mx_swiglu_fin  silu(gate) * up -> bf16 in the down projection's input order
+//   mx_gemm        down projection, split-K partials
+// then mx_norm with the final scale, mx_gemm against the tied embedding, mx_argmax per row.
 //
 // GEMM: C[M x N] = A[M x K] * W[N x K]^T with A (activations) and W (packed weight rows)
-// both K-contiguous.  Workgroup tile 64 x 64, four waves as 2 x 2 blocks of 32 x 32, each
-// four 16 x 16 MFMA tiles; every operand fragment is one 16-byte run along K loaded
-// straight from memory (A from L2, W streamed once).  K is split across grid.z where the
-// consumer sums the partials.
+// both K-contiguous.  A workgroup of four waves covers 64 columns and BM rows; each wave
+// holds RB x CB 16 x 16 MFMA tiles, every operand fragment one 16-byte run along K loaded
+// straight from memory (W streamed once per row tile, A from L2).  K is split across grid.z
+// into enough workgroups to keep every compute unit streaming; partials are summed in split
+// order by the consuming kernel.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -38,22 +52,45 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kDh = 64;
-constexpr int kBM = 64;       // GEMM tile rows (tokens)
-constexpr int kBN = 64;       // GEMM tile columns (output features)
+constexpr int kPage = 16;     // positions per KV page
+constexpr int kBN = 64;       // GEMM tile columns
 constexpr int kBK = 32;       // K per MFMA step
-constexpr int kSplitO = 4;    // K splits of the O projection
-constexpr int kSplitDn = 8;   // K splits of the down projection
-constexpr int kMaxSplit = 8;
 constexpr int kNormThreads = 256;
-constexpr int kAttnQ = 64;    // queries per attention workgroup (16 per wave)
+constexpr int kAttnQ = 16;    // queries per prefill attention workgroup (4 per wave)
+constexpr int kQW = kAttnQ / 4;
+constexpr int kMaxSplitK = 16;  // largest K split (partials summed by the consumers)
 constexpr int kKStride = kDh + 4;
-
-enum Epi { kEpiQkv = 0, kEpiPart = 1, kEpiSwiglu = 2, kEpiLogits = 3 };
+constexpr int kMaxRows = 1024;
 
 __device__ __forceinline__ float bf2f(uint16_t b) { return __uint_as_float(uint32_t(b) << 16); }
 __device__ __forceinline__ uint16_t f2bf(float f) {   // round to nearest even
   const uint32_t u = __float_as_uint(f);
   return uint16_t((u + (((u >> 16) & 1u) + 0x7fffu)) >> 16);
+}
+
+// Wave64 reductions with DPP row shifts and row broadcasts (fixed order, no LDS traffic);
+// the result is read from lane 63 as a wave-uniform value.
+template <int CTRL, int ROWMASK>
+__device__ __forceinline__ float dpp(float v, float fill) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(fill), __float_as_int(v), CTRL, ROWMASK, 0xf, false));
+}
+__device__ __forceinline__ float wave_sum(float v) {
+  v += dpp<0x111, 0xf>(v, 0.f);
+  v += dpp<0x112, 0xf>(v, 0.f);
+  v += dpp<0x114, 0xf>(v, 0.f);
+  v += dpp<0x118, 0xf>(v, 0.f);
+  v += dpp<0x142, 0xa>(v, 0.f);
+  v += dpp<0x143, 0xc>(v, 0.f);
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+__device__ __forceinline__ float wave_max(float v) {
+  v = fmaxf(v, dpp<0x111, 0xf>(v, -INFINITY));
+  v = fmaxf(v, dpp<0x112, 0xf>(v, -INFINITY));
+  v = fmaxf(v, dpp<0x114, 0xf>(v, -INFINITY));
+  v = fmaxf(v, dpp<0x118, 0xf>(v, -INFINITY));
+  v = fmaxf(v, dpp<0x142, 0xa>(v, -INFINITY));
+  v = fmaxf(v, dpp<0x143, 0xc>(v, -INFINITY));
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
 // Position of input element i in a row of K under the packed row layout: blocks of 512
@@ -73,143 +110,107 @@ __device__ __forceinline__ int perm_elem(int j, int K) {
   return (b << 9) + (o & 7) * m + (o >> 3);
 }
 
+// Rows of a pass: row m is sequence seq(m) at position pos(m).
+struct Rows {
+  int M;
+  const int32_t* pos;     // NULL: pos(m) = m (prefill)
+  int batched;            // seq(m) = m; else every row is sequence 0
+  const int32_t* pages;   // [seq][max_pages] page table, NULL = identity
+  int max_pages;
+  int pool;               // pool positions (16 * pages)
+};
+__device__ __forceinline__ int row_pos(const Rows& r, int m) { return r.pos ? r.pos[m] : m; }
+__device__ __forceinline__ int64_t cache_row(const Rows& r, int m, int p) {
+  const int seq = r.batched ? m : 0;
+  const int page = r.pages ? r.pages[int64_t(seq) * r.max_pages + p / kPage] : p / kPage;
+  return int64_t(page) * kPage + p % kPage;
+}
+
 struct GemmArgs {
-  const uint16_t* A;   // [M][K] bf16
+  const uint16_t* A;   // [M][lda] bf16
   const uint16_t* W;   // [N][K] bf16
-  int M, N, K, lda;
-  int splits;
-  // epilogue targets
-  float* out;          // QKV: [M][N] f32 natural order; PART: [splits][M][N]; LOGITS: [M][N]
-  int ldo;
-  uint16_t* act;       // SWIGLU: [M][N/2] bf16 in the down projection's input order
-  uint16_t* kcache;    // QKV: this layer's K cache [KV][ctx][64]
-  uint16_t* vcache;
-  const float* rope;   // [ctx][64]: cos | sin
-  int H, KV, ctx;
+  float* out;          // partials [splits][M][N] f32, or [M][ldo] (single split)
+  int M, N, K, lda, ldo, splits;
 };
 
 __device__ __forceinline__ bf16x8 as_bf16x8(uint4 u) { return __builtin_bit_cast(bf16x8, u); }
 
-template <int EPI>
-__global__ __launch_bounds__(256) void pf_gemm(GemmArgs g) {
+// Four waves as WM x (4 / WM); a wave covers RB 16-row blocks and (WM) 16-column blocks.
+template <int RB, int WM>
+__global__ __launch_bounds__(256) void mx_gemm(GemmArgs g) {
+  constexpr int WN = 4 / WM, CB = 4 / WN, BM = 16 * RB * WM;
+  constexpr int U = RB * CB <= 2 ? 8 : 4;   // K steps with loads in flight
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const int wm = wv >> 1, wn = wv & 1;
-  const int m0 = blockIdx.y * kBM + 32 * wm, n0 = blockIdx.x * kBN + 32 * wn;
+  const int wm = wv / WN, wn = wv % WN;
+  const int m0 = blockIdx.y * BM + 16 * RB * wm, n0 = blockIdx.x * kBN + 16 * CB * wn;
   const int nchunks = g.K / kBK;
   const int c0 = (nchunks * int(blockIdx.z)) / g.splits, c1 = (nchunks * (int(blockIdx.z) + 1)) / g.splits;
   const int kq = 8 * (lane >> 4);   // this lane's 8-element K run within a 32 chunk
   const int r16 = lane & 15;
-  const uint16_t* arow[2];
-  bool aval[2];
+  const uint16_t* arow[RB];
+  bool aval[RB];
 #pragma unroll
-  for (int rb = 0; rb < 2; ++rb) {
+  for (int rb = 0; rb < RB; ++rb) {
     const int m = m0 + 16 * rb + r16;
     aval[rb] = m < g.M;
     arow[rb] = g.A + int64_t(aval[rb] ? m : 0) * g.lda + kq;
   }
-  const uint16_t* wrow[2];
+  const uint16_t* wrow[CB];
 #pragma unroll
-  for (int cb = 0; cb < 2; ++cb) wrow[cb] = g.W + int64_t(n0 + 16 * cb + r16) * g.K + kq;
-  f32x4 acc[2][2];
+  for (int cb = 0; cb < CB; ++cb) wrow[cb] = g.W + int64_t(n0 + 16 * cb + r16) * g.K + kq;
+  f32x4 acc[RB][CB];
 #pragma unroll
-  for (int rb = 0; rb < 2; ++rb)
+  for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-    for (int cb = 0; cb < 2; ++cb) acc[rb][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
-  constexpr int U = 4;   // chunks in flight
+    for (int cb = 0; cb < CB; ++cb) acc[rb][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  auto step = [&](const uint4* a, const uint4* w) {
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+      for (int cb = 0; cb < CB; ++cb)
+        acc[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a[rb]), as_bf16x8(w[cb]), acc[rb][cb], 0, 0, 0);
+  };
   int c = c0;
   for (; c + U <= c1; c += U) {
-    uint4 a[U][2], w[U][2];
+    uint4 a[U][RB], w[U][CB];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int k = (c + u) * kBK;
 #pragma unroll
-      for (int rb = 0; rb < 2; ++rb)
+      for (int rb = 0; rb < RB; ++rb)
         a[u][rb] = aval[rb] ? *reinterpret_cast<const uint4*>(arow[rb] + k) : make_uint4(0, 0, 0, 0);
 #pragma unroll
-      for (int cb = 0; cb < 2; ++cb) w[u][cb] = *reinterpret_cast<const uint4*>(wrow[cb] + k);
+      for (int cb = 0; cb < CB; ++cb) w[u][cb] = *reinterpret_cast<const uint4*>(wrow[cb] + k);
     }
 #pragma unroll
-    for (int u = 0; u < U; ++u)
-#pragma unroll
-      for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-        for (int cb = 0; cb < 2; ++cb)
-          acc[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a[u][rb]), as_bf16x8(w[u][cb]),
-                                                                acc[rb][cb], 0, 0, 0);
+    for (int u = 0; u < U; ++u) step(a[u], w[u]);
   }
   for (; c < c1; ++c) {
     const int k = c * kBK;
-    uint4 a[2], w[2];
+    uint4 a[RB], w[CB];
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb)
+    for (int rb = 0; rb < RB; ++rb)
       a[rb] = aval[rb] ? *reinterpret_cast<const uint4*>(arow[rb] + k) : make_uint4(0, 0, 0, 0);
 #pragma unroll
-    for (int cb = 0; cb < 2; ++cb) w[cb] = *reinterpret_cast<const uint4*>(wrow[cb] + k);
-#pragma unroll
-    for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-      for (int cb = 0; cb < 2; ++cb)
-        acc[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a[rb]), as_bf16x8(w[cb]), acc[rb][cb], 0, 0, 0);
+    for (int cb = 0; cb < CB; ++cb) w[cb] = *reinterpret_cast<const uint4*>(wrow[cb] + k);
+    step(a, w);
   }
   // D layout of a 16 x 16 tile: lane holds rows 4*(lane/16) + r (r < 4) of column lane % 16
+  float* out = g.splits > 1 ? g.out + int64_t(blockIdx.z) * g.M * g.N : g.out;
+  const int ldo = g.splits > 1 ? g.N : g.ldo;
 #pragma unroll
-  for (int rb = 0; rb < 2; ++rb) {
+  for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-    for (int cb = 0; cb < 2; ++cb) {
-      const int col = n0 + 16 * cb + r16;
+    for (int cb = 0; cb < CB; ++cb)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int row = m0 + 16 * rb + 4 * (lane >> 4) + r;
-        const float v = acc[rb][cb][r];
-        if (EPI == kEpiPart) {
-          if (row < g.M) g.out[(int64_t(blockIdx.z) * g.M + row) * g.ldo + col] = v;
-        } else if (EPI == kEpiLogits) {
-          if (row < g.M) g.out[int64_t(row) * g.ldo + col] = v;
-        } else if (EPI == kEpiSwiglu) {
-          // columns (2f, 2f+1) are gate and up of d_ff index f, held by lanes l, l^1
-          const float up = __shfl_xor(v, 1);
-          if (row < g.M && (col & 1) == 0) {
-            const float gt = v;
-            const float a = (gt * (1.f / (1.f + expf(-gt)))) * up;
-            const int f = col >> 1, F = g.N >> 1;
-            g.act[int64_t(row) * F + perm_pos(f, F)] = f2bf(a);
-          }
-        } else {   // kEpiQkv
-          const float other = __shfl_xor(v, 1);
-          if (row < g.M) {
-            const int head = col / kDh, rr = col % kDh;
-            float o;
-            int dim;
-            if (head < g.H + g.KV) {   // rotate-half RoPE on the pair (i, i + 32) (model.py:110-117)
-              const int i = rr >> 1;
-              const float cs = g.rope[int64_t(row) * kDh + i], sn = g.rope[int64_t(row) * kDh + kDh / 2 + i];
-              if ((rr & 1) == 0) {
-                o = v * cs - other * sn;
-                dim = i;
-              } else {
-                o = other * sn + v * cs;
-                dim = i + kDh / 2;
-              }
-            } else {
-              o = v;
-              dim = rr;
-            }
-            g.out[int64_t(row) * g.ldo + head * kDh + dim] = o;
-            if (head >= g.H) {
-              const bool isv = head >= g.H + g.KV;
-              const int kvh = isv ? head - g.H - g.KV : head - g.H;
-              uint16_t* cp = (isv ? g.vcache : g.kcache) + (int64_t(kvh) * g.ctx + row) * kDh + dim;
-              *cp = f2bf(o);
-            }
-          }
-        }
+        if (row < g.M) out[int64_t(row) * ldo + n0 + 16 * cb + r16] = acc[rb][cb][r];
       }
-    }
-  }
 }
 
 __device__ __forceinline__ float block_sum256(float v, float* red) {
-  for (int o = 32; o; o >>= 1) v += __shfl_xor(v, o);
+  v = wave_sum(v);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
   __syncthreads();
   const float s = (red[0] + red[1]) + (red[2] + red[3]);
@@ -217,31 +218,59 @@ __device__ __forceinline__ float block_sum256(float v, float* red) {
   return s;
 }
 
-// One row m per workgroup: h[m] += sum_z part[z][m] (z in order), then
-// xn[m][j] = bf16(scale[i] * (h[m][i] / sqrt(mean(h[m]^2) + 1e-5))) with i the input element
-// at position j of the packed row layout (model.py:94-98).
-__global__ __launch_bounds__(kNormThreads) void pf_norm(float* h, const float* part, int splits, int M, int d,
+// Row blockIdx.x + row0: h += sum_z part[z] (z in order), then
+// xn[j] = bf16(scale[i] * (h[i] / sqrt(mean(h^2) + 1e-5))) with i the input element at
+// position j of the packed row layout (model.py:94-98).  Every partial is requested before
+// the first is added, so the sum costs one memory round trip.
+__global__ __launch_bounds__(kNormThreads) void mx_norm(float* h, const float* part, int splits, int M, int d,
                                                         const uint16_t* scale, uint16_t* xn, int row0) {
+  constexpr int NE = kMaxRows / kNormThreads;
   __shared__ float red[4];
+  __shared__ float hs[kMaxRows];
   const int m = blockIdx.x + row0;
   float* hr = h + int64_t(m) * d;
+  float v[NE];
+#pragma unroll
+  for (int i = 0; i < NE; ++i) {
+    const int n = threadIdx.x + kNormThreads * i;
+    v[i] = n < d ? hr[n] : 0.f;
+  }
+  if (splits > 0) {
+    float pv[kMaxSplitK][NE];
+#pragma unroll
+    for (int z = 0; z < kMaxSplitK; ++z) {
+      const int zc = min(z, splits - 1);
+#pragma unroll
+      for (int i = 0; i < NE; ++i) {
+        const int n = min(threadIdx.x + kNormThreads * i, d - 1);
+        pv[z][i] = part[(int64_t(zc) * M + m) * d + n];
+      }
+    }
+#pragma unroll
+    for (int z = 0; z < kMaxSplitK; ++z)
+#pragma unroll
+      for (int i = 0; i < NE; ++i)
+        if (z < splits) v[i] += pv[z][i];
+  }
   float ss = 0.f;
-  for (int n = threadIdx.x; n < d; n += kNormThreads) {
-    float v = hr[n];
-    for (int z = 0; z < splits; ++z) v += part[(int64_t(z) * M + m) * d + n];
-    if (splits) hr[n] = v;
-    ss += v * v;
+#pragma unroll
+  for (int i = 0; i < NE; ++i) {
+    const int n = threadIdx.x + kNormThreads * i;
+    if (n < d) {
+      if (splits) hr[n] = v[i];
+      hs[n] = v[i];
+      ss += v[i] * v[i];
+    }
   }
   ss = block_sum256(ss, red);
   const float r = sqrtf(ss / float(d) + 1e-5f);
-  __syncthreads();   // the h writes above are visible to the whole workgroup
   for (int j = threadIdx.x; j < d; j += kNormThreads) {
     const int i = perm_elem(j, d);
-    xn[int64_t(blockIdx.x) * d + j] = f2bf(bf2f(scale[i]) * (hr[i] / r));
+    xn[int64_t(blockIdx.x) * d + j] = f2bf(bf2f(scale[i]) * (hs[i] / r));
   }
 }
 
-__global__ __launch_bounds__(256) void pf_embed(const uint16_t* emb, const int32_t* tokens, int d, float* h,
+__global__ __launch_bounds__(256) void mx_embed(const uint16_t* emb, const int32_t* tokens, int d, float* h,
                                                 int32_t* status, int V) {
   const int m = blockIdx.x;
   int t = tokens[m];
@@ -252,14 +281,78 @@ __global__ __launch_bounds__(256) void pf_embed(const uint16_t* emb, const int32
   for (int n = threadIdx.x; n < d; n += 256) h[int64_t(m) * d + n] = bf2f(emb[int64_t(t) * d + n]);
 }
 
-// Causal GQA attention of query block blockIdx.y (64 rows) for head blockIdx.x.  Each wave
-// owns 16 queries; key chunks of 64 rows go through LDS, with an online softmax per query
-// (scores: lane = key; output: lane = dimension).  Scale 1/sqrt(64) (model.py:98).
-__global__ __launch_bounds__(256) void pf_attention(const float* qkv, int M, int H, int KV, uint16_t* att) {
+// Row blockIdx.x: q/k/v = sum_z part[z] (z in order) over the packed q/k/v rows; RoPE on the
+// q and k pairs (packed rows 2i, 2i+1 = dims i, i+32; model.py:110-117) at the row's
+// position; f32 q/k/v in natural head-dim order to qkv; bf16 K/V to the cache.
+__global__ __launch_bounds__(256) void mx_qkv_fin(const float* part, int splits, int M, int H, int KV,
+                                                  const float* rope, Rows rows, uint16_t* kc, uint16_t* vc,
+                                                  float* qkv) {
+  const int m = blockIdx.x, nq = (H + 2 * KV) * kDh;
+  const int t = blockIdx.y * 256 + threadIdx.x;
+  if (t >= nq / 2) return;
+  const int p = row_pos(rows, m);
+  const int col = 2 * t;
+  float2 pv[kMaxSplitK];
+#pragma unroll
+  for (int z = 0; z < kMaxSplitK; ++z)
+    pv[z] = *reinterpret_cast<const float2*>(part + (int64_t(min(z, splits - 1)) * M + m) * nq + col);
+  float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+  for (int z = 0; z < kMaxSplitK; ++z)
+    if (z < splits) {
+      s0 += pv[z].x;
+      s1 += pv[z].y;
+    }
+  const int head = col / kDh, rr = col % kDh;
+  float o0 = s0, o1 = s1;
+  int d0 = rr, d1 = rr + 1;
+  if (head < H + KV) {
+    const int i = rr >> 1;
+    const float cs = rope[int64_t(p) * kDh + i], sn = rope[int64_t(p) * kDh + kDh / 2 + i];
+    o0 = s0 * cs - s1 * sn;
+    o1 = s0 * sn + s1 * cs;
+    d0 = i;
+    d1 = i + kDh / 2;
+  }
+  float* q = qkv + int64_t(m) * nq + head * kDh;
+  q[d0] = o0;
+  q[d1] = o1;
+  if (head >= H) {
+    const bool isv = head >= H + KV;
+    const int g = isv ? head - H - KV : head - H;
+    uint16_t* cp = (isv ? vc : kc) + (int64_t(g) * rows.pool + cache_row(rows, m, p)) * kDh;
+    cp[d0] = f2bf(o0);
+    cp[d1] = f2bf(o1);
+  }
+}
+
+// Row blockIdx.x: act_f = silu(gate_f) * up_f over the summed partials (gate/up are the packed
+// rows 2f, 2f+1; model.py:159), bf16 at the down projection's input position of f.
+__global__ __launch_bounds__(256) void mx_swiglu_fin(const float* part, int splits, int M, int F, uint16_t* act) {
+  const int m = blockIdx.x, f = blockIdx.y * 256 + threadIdx.x;
+  if (f >= F) return;
+  float2 pv[kMaxSplitK];
+#pragma unroll
+  for (int z = 0; z < kMaxSplitK; ++z)
+    pv[z] = *reinterpret_cast<const float2*>(part + (int64_t(min(z, splits - 1)) * M + m) * (2 * F) + 2 * f);
+  float gt = 0.f, up = 0.f;
+#pragma unroll
+  for (int z = 0; z < kMaxSplitK; ++z)
+    if (z < splits) {
+      gt += pv[z].x;
+      up += pv[z].y;
+    }
+  act[int64_t(m) * F + perm_pos(f, F)] = f2bf((gt * (1.f / (1.f + expf(-gt)))) * up);
+}
+
+// Prefill: causal GQA attention of query block blockIdx.y (16 rows) for head blockIdx.x.
+// Each wave owns 4 queries; key chunks of 64 rows go through LDS, with an online softmax per
+// query (scores: lane = key; output: lane = dimension).  Scale 1/sqrt(64) (model.py:98).
+__global__ __launch_bounds__(256) void mx_attention_prefill(const float* qkv, int M, int H, int KV, uint16_t* att) {
   __shared__ float sk[64 * kKStride];
   __shared__ float sv[64 * kDh];
   __shared__ float sq[kAttnQ * kDh];
-  __shared__ float sp[4][16][64];
+  __shared__ float sp[4][kQW][64];
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int h = blockIdx.x, g = h / (H / KV);
   const int nqkv = (H + 2 * KV) * kDh, d = H * kDh;
@@ -268,9 +361,9 @@ __global__ __launch_bounds__(256) void pf_attention(const float* qkv, int M, int
     const int i = q0 + t / kDh;
     sq[t] = i < M ? qkv[int64_t(i) * nqkv + h * kDh + (t % kDh)] : 0.f;
   }
-  float mx[16], ls[16], o[16];
+  float mx[kQW], ls[kQW], o[kQW];
 #pragma unroll
-  for (int t = 0; t < 16; ++t) {
+  for (int t = 0; t < kQW; ++t) {
     mx[t] = -INFINITY;
     ls[t] = 0.f;
     o[t] = 0.f;
@@ -286,29 +379,26 @@ __global__ __launch_bounds__(256) void pf_attention(const float* qkv, int M, int
     }
     __syncthreads();
     const int j = 64 * c + lane;
-    float s[16];
+    float s[kQW];
 #pragma unroll
-    for (int t = 0; t < 16; ++t) s[t] = 0.f;
+    for (int t = 0; t < kQW; ++t) s[t] = 0.f;
     const float4* kr = reinterpret_cast<const float4*>(sk + lane * kKStride);
-#pragma unroll 4
+#pragma unroll
     for (int e4 = 0; e4 < kDh / 4; ++e4) {
       const float4 kk = kr[e4];
 #pragma unroll
-      for (int t = 0; t < 16; ++t) {
-        const float4 qq = *reinterpret_cast<const float4*>(sq + (16 * wv + t) * kDh + 4 * e4);
+      for (int t = 0; t < kQW; ++t) {
+        const float4 qq = *reinterpret_cast<const float4*>(sq + (kQW * wv + t) * kDh + 4 * e4);
         s[t] += qq.x * kk.x + qq.y * kk.y + qq.z * kk.z + qq.w * kk.w;
       }
     }
 #pragma unroll
-    for (int t = 0; t < 16; ++t) {
-      const int i = q0 + 16 * wv + t;
-      float sc = (j <= i && j < M) ? s[t] * 0.125f : -INFINITY;
-      float cm = sc;
-      for (int off = 32; off; off >>= 1) cm = fmaxf(cm, __shfl_xor(cm, off));
-      const float mn = fmaxf(mx[t], cm);
+    for (int t = 0; t < kQW; ++t) {
+      const int i = q0 + kQW * wv + t;
+      const float sc = (j <= i && j < M) ? s[t] * 0.125f : -INFINITY;
+      const float mn = fmaxf(mx[t], wave_max(sc));
       const float p = (mn == -INFINITY) ? 0.f : expf(sc - mn);
-      float ps = p;
-      for (int off = 32; off; off >>= 1) ps += __shfl_xor(ps, off);
+      const float ps = wave_sum(p);
       const float alpha = (mx[t] == -INFINITY) ? 0.f : expf(mx[t] - mn);
       ls[t] = ls[t] * alpha + ps;
       o[t] *= alpha;
@@ -316,26 +406,127 @@ __global__ __launch_bounds__(256) void pf_attention(const float* qkv, int M, int
       sp[wv][t][lane] = p;
     }
     __builtin_amdgcn_wave_barrier();
+#pragma unroll 8
     for (int jj = 0; jj < 64; ++jj) {
       const float vv = sv[jj * kDh + lane];
 #pragma unroll
-      for (int t = 0; t < 16; ++t) o[t] += sp[wv][t][jj] * vv;
+      for (int t = 0; t < kQW; ++t) o[t] += sp[wv][t][jj] * vv;
     }
     __builtin_amdgcn_wave_barrier();
   }
 #pragma unroll
-  for (int t = 0; t < 16; ++t) {
-    const int i = q0 + 16 * wv + t;
+  for (int t = 0; t < kQW; ++t) {
+    const int i = q0 + kQW * wv + t;
     if (i < M) att[int64_t(i) * d + perm_pos(h * kDh + lane, d)] = f2bf(o[t] / ls[t]);
   }
 }
 
-// argmax over one row of logits (lowest index on ties), one workgroup of 1024 threads
-__global__ __launch_bounds__(1024) void pf_argmax(const float* logits, int V, int32_t* out, const int32_t* status) {
+// Batched decode: row m (one sequence at position p = pos(m)) and head blockIdx.y attend over
+// the cached rows 0..p-1 of the sequence (bf16, through its page table) and the row's
+// current, un-rounded K/V (multi_sm_decode.py:182-221).  Wave w takes the positions
+// 64*(w + 4*i) + lane (scores: lane = position) with its own running max and sum; each lane
+// looks its position's cache row up once and leaves it in LDS for the value loads, which are
+// issued 16 positions at a time; the four waves' states are merged in LDS at the end
+// (output: lane = dimension).
+__global__ __launch_bounds__(256) void mx_attention_decode(const float* qkv, Rows rows, int H, int KV,
+                                                           const uint16_t* kc, const uint16_t* vc, uint16_t* att) {
+  __shared__ float sq[kDh];
+  __shared__ float sp[4][64];
+  __shared__ int srow[4][64];
+  __shared__ float so[4][kDh];
+  __shared__ float sml[4][2];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int m = blockIdx.x, h = blockIdx.y, g = h / (H / KV);
+  const int nqkv = (H + 2 * KV) * kDh, d = H * kDh;
+  const int p = row_pos(rows, m);
+  const float* qr = qkv + int64_t(m) * nqkv;
+  if (threadIdx.x < kDh) sq[threadIdx.x] = qr[h * kDh + threadIdx.x];
+  __syncthreads();
+  const uint16_t* kg = kc + int64_t(g) * rows.pool * kDh;
+  const uint16_t* vg = vc + int64_t(g) * rows.pool * kDh;
+  const float vcur = qr[(H + KV + g) * kDh + lane];
+  float mx = -INFINITY, ls = 0.f, o = 0.f;
+  for (int j0 = 64 * wv; j0 <= p; j0 += 256) {
+    const int j = j0 + lane;
+    const int64_t crow = j < p ? cache_row(rows, m, j) : 0;
+    srow[wv][lane] = int(crow);
+    float s = -INFINITY;
+    if (j < p) {   // cached row: bf16
+      const uint4* kr = reinterpret_cast<const uint4*>(kg + crow * kDh);
+      uint4 ku[kDh / 8];
+#pragma unroll
+      for (int e8 = 0; e8 < kDh / 8; ++e8) ku[e8] = kr[e8];
+      float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+      for (int e8 = 0; e8 < kDh / 8; ++e8) {
+        const uint32_t wds[4] = {ku[e8].x, ku[e8].y, ku[e8].z, ku[e8].w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          a0 += sq[8 * e8 + 2 * q] * __uint_as_float(wds[q] << 16);
+          a1 += sq[8 * e8 + 2 * q + 1] * __uint_as_float(wds[q] & 0xffff0000u);
+        }
+      }
+      s = (a0 + a1) * 0.125f;
+    } else if (j == p) {   // current position: f32 K from this row's projection
+      const float* kr = qr + (H + g) * kDh;
+      float a0 = 0.f, a1 = 0.f;
+      for (int e = 0; e < kDh; e += 2) {
+        a0 += sq[e] * kr[e];
+        a1 += sq[e + 1] * kr[e + 1];
+      }
+      s = (a0 + a1) * 0.125f;
+    }
+    const float mn = fmaxf(mx, wave_max(s));
+    const float e = (s == -INFINITY) ? 0.f : expf(s - mn);
+    const float es = wave_sum(e);
+    const float alpha = (mx == -INFINITY) ? 0.f : expf(mx - mn);
+    ls = ls * alpha + es;
+    o *= alpha;
+    mx = mn;
+    sp[wv][lane] = e;
+    __builtin_amdgcn_wave_barrier();
+    const int nj = min(64, p + 1 - j0);
+    for (int jb = 0; jb < nj; jb += 16) {
+      float vv[16];
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        const int jj = jb + k;
+        vv[k] = jj < nj ? (j0 + jj < p ? bf2f(vg[int64_t(srow[wv][jj]) * kDh + lane]) : vcur) : 0.f;
+      }
+#pragma unroll
+      for (int k = 0; k < 16; ++k)
+        if (jb + k < nj) o += sp[wv][jb + k] * vv[k];
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+  so[wv][lane] = o;
+  if (lane == 0) {
+    sml[wv][0] = mx;
+    sml[wv][1] = ls;
+  }
+  __syncthreads();
+  if (wv == 0) {
+    float M = -INFINITY;
+    for (int w = 0; w < 4; ++w) M = fmaxf(M, sml[w][0]);
+    float num = 0.f, den = 0.f;
+    for (int w = 0; w < 4; ++w) {
+      if (sml[w][0] == -INFINITY) continue;
+      const float a = expf(sml[w][0] - M);
+      num += a * so[w][lane];
+      den += a * sml[w][1];
+    }
+    att[int64_t(m) * d + perm_pos(h * kDh + lane, d)] = f2bf(num / den);
+  }
+}
+
+// argmax of each row of logits (lowest index on ties): out[2*row] = index, out[2*row+1] = status
+__global__ __launch_bounds__(1024) void mx_argmax(const float* logits, int V, int ld, int32_t* out,
+                                                  const int32_t* status) {
   __shared__ uint64_t red[16];
+  const float* lr = logits + int64_t(blockIdx.x) * ld;
   uint64_t best = 0;
   for (int j = threadIdx.x; j < V; j += 1024) {
-    uint32_t u = __float_as_uint(logits[j]);
+    uint32_t u = __float_as_uint(lr[j]);
     u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
     const uint64_t key = (uint64_t(u) << 32) | uint64_t(0xffffffffu - uint32_t(j));
     best = key > best ? key : best;
@@ -349,132 +540,272 @@ __global__ __launch_bounds__(1024) void pf_argmax(const float* logits, int V, in
   if (threadIdx.x == 0) {
     uint64_t b = red[0];
     for (int i = 1; i < 16; ++i) b = red[i] > b ? red[i] : b;
-    out[0] = int32_t(0xffffffffu - uint32_t(b & 0xffffffffu));
-    out[1] = *status;
+    out[2 * blockIdx.x] = int32_t(0xffffffffu - uint32_t(b & 0xffffffffu));
+    out[2 * blockIdx.x + 1] = *status;
   }
 }
 
+// Copies the rows' positions and page tables into the workspace, which is what every later
+// kernel addresses the cache with: a position outside [0, ctx) or past the table, and a table
+// entry outside the pool, is replaced by 0 (status bit 2), so no access leaves the pool.
+// pos == NULL: every row is at fixed_pos (the last position of a prefill).
+__global__ void mx_sanitize_rows(const int32_t* pos, int fixed_pos, const int32_t* pages, int M, int max_pages,
+                                 int ctx, int pool_pages, int32_t* pos_out, int32_t* pages_out, int32_t* status) {
+  const int m = blockIdx.x * blockDim.x + threadIdx.x;
+  if (m >= M) return;
+  int p = pos ? pos[m] : fixed_pos;
+  bool bad = p < 0 || p >= ctx || p / kPage >= max_pages;
+  if (bad) p = 0;
+  for (int i = 0; i < max_pages; ++i) {
+    int pg = pages[int64_t(m) * max_pages + i];
+    if (pg < 0 || pg >= pool_pages) {
+      if (i <= p / kPage) bad = true;
+      pg = 0;
+    }
+    pages_out[int64_t(m) * max_pages + i] = pg;
+  }
+  if (pos_out) pos_out[m] = p;
+  if (bad) atomicOr(status, 4);
+}
+
 // ---------------------------------------------------------------- host side
-struct PfLayout {
-  size_t h, xn, qkv, att, act, part, status, bytes;
+struct Layout {
+  size_t h, xn, qkv, att, act, part, status, rowpos, pages, bytes;
 };
 
 static size_t al256(size_t x) { return (x + 255) & ~size_t(255); }
 
-static PfLayout pf_layout(const msd_config* c, int M) {
+// K splits of a projection: enough workgroups to occupy every compute unit, at least 4 K steps each
+static int splits_for(int M, int N, int K, int bm) {
+  const int tiles = (N / kBN) * ((M + bm - 1) / bm);
+  int s = 1;
+  while (tiles * s < 256 && (K / kBK) / (2 * s) >= 4 && 2 * s <= kMaxSplitK) s *= 2;
+  return s;
+}
+
+static int bm_for(int M) { return M <= 16 ? 16 : (M <= 64 ? 64 : 128); }
+
+static size_t part_floats(const msd_config* c, int M) {
   const int d = c->d_model, ff = c->d_ff, nqkv = (c->n_heads + 2 * c->n_kv_heads) * kDh;
-  PfLayout L;
+  const int bm = bm_for(M);
+  size_t mx = 0;
+  mx = std::max(mx, size_t(splits_for(M, nqkv, d, bm)) * nqkv);
+  mx = std::max(mx, size_t(splits_for(M, d, d, bm)) * d);
+  mx = std::max(mx, size_t(splits_for(M, 2 * ff, d, bm)) * 2 * ff);
+  mx = std::max(mx, size_t(splits_for(M, d, ff, bm)) * d);
+  return mx * M;
+}
+
+static Layout layout(const msd_config* c, int M) {
+  const int d = c->d_model, ff = c->d_ff, nqkv = (c->n_heads + 2 * c->n_kv_heads) * kDh;
+  Layout L;
   size_t o = 0;
   L.h = o;      o += al256(size_t(M) * d * 4);
   L.xn = o;     o += al256(size_t(M) * d * 2);
   L.qkv = o;    o += al256(size_t(M) * nqkv * 4);
   L.att = o;    o += al256(size_t(M) * d * 2);
   L.act = o;    o += al256(size_t(M) * ff * 2);
-  L.part = o;   o += al256(size_t(kMaxSplit) * M * d * 4);
+  L.part = o;   o += al256(part_floats(c, M) * 4);
   L.status = o; o += 256;
+  L.rowpos = o; o += al256(size_t(M) * 4);
+  L.pages = o;  o += al256(size_t(M) * ((c->context_len + kPage - 1) / kPage) * 4);
   L.bytes = o;
   return L;
 }
 
-static bool pf_config_ok(const msd_config* c) {
+static bool mx_config_ok(const msd_config* c) {
   if (!c || c->d_head != kDh || c->n_heads <= 0 || c->n_kv_heads <= 0 || c->n_layers <= 0) return false;
   if (c->n_heads * kDh != c->d_model || c->n_heads % c->n_kv_heads) return false;
   if (c->d_model % kBN || (2 * c->d_ff) % kBN || c->vocab_size % kBN || c->d_ff % 8) return false;
-  if (c->d_model % kBK || c->d_ff % kBK || c->context_len <= 0) return false;
+  if (c->d_model % kBK || c->d_ff % kBK || c->context_len <= 0 || c->d_model > kMaxRows) return false;
   return true;
 }
 
-template <int EPI>
-static hipError_t gemm(const GemmArgs& g, hipStream_t s) {
-  const dim3 grid(g.N / kBN, (g.M + kBM - 1) / kBM, g.splits);
-  hipLaunchKernelGGL(pf_gemm<EPI>, grid, dim3(256), 0, s, g);
+// C = A W^T split over K: partials [splits][M][N] (pass ldo = N), or with splits == 1 rows
+// of stride ldo
+static hipError_t gemm(const uint16_t* A, int lda, const uint16_t* W, int M, int N, int K, float* out, int ldo,
+                       int splits, hipStream_t s) {
+  GemmArgs g{A, W, out, M, N, K, lda, ldo, splits};
+  const int bm = bm_for(M);
+  const dim3 grid(N / kBN, (M + bm - 1) / bm, splits);
+  if (bm == 16) hipLaunchKernelGGL((mx_gemm<1, 1>), grid, dim3(256), 0, s, g);
+  else if (bm == 64) hipLaunchKernelGGL((mx_gemm<2, 2>), grid, dim3(256), 0, s, g);
+  else hipLaunchKernelGGL((mx_gemm<4, 2>), grid, dim3(256), 0, s, g);
   return hipGetLastError();
 }
+
+struct Weights {
+  const uint16_t* emb;
+  const uint16_t* outp;
+  const uint16_t* w;
+  const uint16_t* lnf;
+  const float* rope;
+};
+
+// The layer stack over M rows whose residual stream is already in h; leaves the last
+// projection's partials pending (returned split count).
+static int run_layers(const msd_config* cfg, const Weights& wt, const Rows& rows, uint16_t* kv, const Layout& L,
+                      char* ws, bool prefill, hipStream_t s, hipError_t& err) {
+  const int M = rows.M, d = cfg->d_model, ff = cfg->d_ff, H = cfg->n_heads, KV = cfg->n_kv_heads;
+  const int nqkv = (H + 2 * KV) * kDh;
+  float* h = reinterpret_cast<float*>(ws + L.h);
+  uint16_t* xn = reinterpret_cast<uint16_t*>(ws + L.xn);
+  float* qkv = reinterpret_cast<float*>(ws + L.qkv);
+  uint16_t* att = reinterpret_cast<uint16_t*>(ws + L.att);
+  uint16_t* act = reinterpret_cast<uint16_t*>(ws + L.act);
+  float* part = reinterpret_cast<float*>(ws + L.part);
+  const int64_t off_ln2 = d, off_qkv = 2 * int64_t(d), off_o = off_qkv + int64_t(nqkv) * d,
+                off_gu = off_o + int64_t(d) * d, off_dn = off_gu + 2 * int64_t(ff) * d,
+                layer = off_dn + int64_t(d) * ff;
+  const int bm = bm_for(M);
+  const int sq = splits_for(M, nqkv, d, bm), so = splits_for(M, d, d, bm), sg = splits_for(M, 2 * ff, d, bm),
+            sd = splits_for(M, d, ff, bm);
+  int pending = 0;
+  err = hipSuccess;
+  for (int l = 0; l < cfg->n_layers && err == hipSuccess; ++l) {
+    const uint16_t* Wl = wt.w + int64_t(l) * layer;
+    uint16_t* kc = kv + int64_t(l) * 2 * KV * rows.pool * kDh;
+    uint16_t* vc = kc + int64_t(KV) * rows.pool * kDh;
+    hipLaunchKernelGGL(mx_norm, dim3(M), dim3(kNormThreads), 0, s, h, part, pending, M, d, Wl, xn, 0);
+    if ((err = gemm(xn, d, Wl + off_qkv, M, nqkv, d, part, nqkv, sq, s)) != hipSuccess) break;
+    hipLaunchKernelGGL(mx_qkv_fin, dim3(M, (nqkv / 2 + 255) / 256), dim3(256), 0, s, part, sq, M, H, KV, wt.rope, rows,
+                       kc, vc, qkv);
+    if (prefill)
+      hipLaunchKernelGGL(mx_attention_prefill, dim3(H, (M + kAttnQ - 1) / kAttnQ), dim3(256), 0, s, qkv, M, H, KV,
+                         att);
+    else
+      hipLaunchKernelGGL(mx_attention_decode, dim3(M, H), dim3(256), 0, s, qkv, rows, H, KV, kc, vc, att);
+    if ((err = gemm(att, d, Wl + off_o, M, d, d, part, d, so, s)) != hipSuccess) break;
+    hipLaunchKernelGGL(mx_norm, dim3(M), dim3(kNormThreads), 0, s, h, part, so, M, d, Wl + off_ln2, xn, 0);
+    if ((err = gemm(xn, d, Wl + off_gu, M, 2 * ff, d, part, 2 * ff, sg, s)) != hipSuccess) break;
+    hipLaunchKernelGGL(mx_swiglu_fin, dim3(M, (ff + 255) / 256), dim3(256), 0, s, part, sg, M, ff, act);
+    if ((err = gemm(act, ff, Wl + off_dn, M, d, ff, part, d, sd, s)) != hipSuccess) break;
+    pending = sd;
+  }
+  if (err == hipSuccess) err = hipGetLastError();
+  return pending;
+}
+
+static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 }  // namespace mpf
 
 using namespace mpf;
 
 extern "C" int64_t msd_prefill_workspace_bytes(const msd_config* cfg, int32_t n_tokens) {
-  if (!pf_config_ok(cfg)) return MSD_E_CONFIG;
+  if (!mx_config_ok(cfg)) return MSD_E_CONFIG;
   if (n_tokens <= 0 || n_tokens > cfg->context_len) return MSD_E_ARG;
-  return int64_t(pf_layout(cfg, n_tokens).bytes);
+  return int64_t(layout(cfg, n_tokens).bytes);
+}
+
+static int32_t prefill_impl(const msd_config* cfg, const Weights& wt, const int32_t* tokens, int32_t n_tokens,
+                            const int32_t* page_table, int32_t max_pages, int32_t pool_pages, void* kv,
+                            void* workspace, float* logits_last, float* logits_all, int32_t* next_token,
+                            hipStream_t s) {
+  if (!mx_config_ok(cfg)) return MSD_E_CONFIG;
+  const int M = n_tokens;
+  if (M <= 0 || M > cfg->context_len) return MSD_E_ARG;
+  if (!wt.emb || !wt.outp || !wt.w || !wt.lnf || !wt.rope || !tokens || !kv || !workspace || !logits_last ||
+      !next_token)
+    return MSD_E_ARG;
+  if (!aligned16(wt.emb) || !aligned16(wt.outp) || !aligned16(wt.w) || !aligned16(kv) || !aligned16(workspace))
+    return MSD_E_ARG;
+  if (page_table && (max_pages * kPage < M || max_pages > (cfg->context_len + kPage - 1) / kPage || pool_pages <= 0))
+    return MSD_E_ARG;
+  const int d = cfg->d_model, V = cfg->vocab_size;
+  const Layout L = layout(cfg, M);
+  char* ws = static_cast<char*>(workspace);
+  float* h = reinterpret_cast<float*>(ws + L.h);
+  uint16_t* xn = reinterpret_cast<uint16_t*>(ws + L.xn);
+  float* part = reinterpret_cast<float*>(ws + L.part);
+  int32_t* status = reinterpret_cast<int32_t*>(ws + L.status);
+  int32_t* pages = reinterpret_cast<int32_t*>(ws + L.pages);
+  if (hipMemsetAsync(status, 0, 4, s) != hipSuccess) return MSD_E_HIP;
+  if (page_table)
+    hipLaunchKernelGGL(mx_sanitize_rows, dim3(1), dim3(64), 0, s, nullptr, M - 1, page_table, 1, max_pages,
+                       cfg->context_len, pool_pages, nullptr, pages, status);
+  Rows rows{M, nullptr, 0, page_table ? pages : nullptr, max_pages, page_table ? pool_pages * kPage : cfg->context_len};
+  hipLaunchKernelGGL(mx_embed, dim3(M), dim3(256), 0, s, wt.emb, tokens, d, h, status, V);
+  hipError_t err;
+  const int pending = run_layers(cfg, wt, rows, static_cast<uint16_t*>(kv), L, ws, true, s, err);
+  if (err != hipSuccess) return MSD_E_HIP;
+  // final norm of the rows whose logits are wanted, then the tied output projection
+  const int r0 = logits_all ? 0 : M - 1, nr = M - r0;
+  hipLaunchKernelGGL(mx_norm, dim3(nr), dim3(kNormThreads), 0, s, h, part, pending, M, d, wt.lnf, xn, r0);
+  if (gemm(xn, d, wt.outp, nr, V, d, logits_all ? logits_all : logits_last, V, 1, s) != hipSuccess) return MSD_E_HIP;
+  const float* last = logits_all ? logits_all + int64_t(M - 1) * V : logits_last;
+  if (logits_all && hipMemcpyAsync(logits_last, last, size_t(V) * 4, hipMemcpyDeviceToDevice, s) != hipSuccess)
+    return MSD_E_HIP;
+  hipLaunchKernelGGL(mx_argmax, dim3(1), dim3(1024), 0, s, logits_last, V, V, next_token, status);
+  return hipGetLastError() == hipSuccess ? MSD_OK : MSD_E_HIP;
 }
 
 extern "C" int32_t msd_prefill(const msd_config* cfg, const void* token_emb, const void* output_proj,
                                const void* packed_w, const void* lnf_s, const float* rope, const int32_t* tokens,
                                int32_t n_tokens, void* kv, void* workspace, float* logits_last,
                                float* logits_all, int32_t* next_token, void* stream) {
-  if (!pf_config_ok(cfg)) return MSD_E_CONFIG;
-  const int M = n_tokens;
-  if (M <= 0 || M > cfg->context_len) return MSD_E_ARG;
-  if (!token_emb || !output_proj || !packed_w || !lnf_s || !rope || !tokens || !kv || !workspace || !logits_last ||
-      !next_token)
+  const Weights wt{static_cast<const uint16_t*>(token_emb), static_cast<const uint16_t*>(output_proj),
+                   static_cast<const uint16_t*>(packed_w), static_cast<const uint16_t*>(lnf_s), rope};
+  return prefill_impl(cfg, wt, tokens, n_tokens, nullptr, 0, 0, kv, workspace, logits_last, logits_all, next_token,
+                      static_cast<hipStream_t>(stream));
+}
+
+extern "C" int32_t msd_prefill_paged(const msd_config* cfg, const void* token_emb, const void* output_proj,
+                                     const void* packed_w, const void* lnf_s, const float* rope,
+                                     const int32_t* tokens, int32_t n_tokens, const int32_t* page_table,
+                                     int32_t max_pages, void* kv_pool, int32_t pool_pages, void* workspace,
+                                     float* logits_last, int32_t* next_token, void* stream) {
+  if (!page_table) return MSD_E_ARG;
+  const Weights wt{static_cast<const uint16_t*>(token_emb), static_cast<const uint16_t*>(output_proj),
+                   static_cast<const uint16_t*>(packed_w), static_cast<const uint16_t*>(lnf_s), rope};
+  return prefill_impl(cfg, wt, tokens, n_tokens, page_table, max_pages, pool_pages, kv_pool, workspace, logits_last,
+                      nullptr, next_token, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int64_t msd_batch_workspace_bytes(const msd_config* cfg, int32_t batch) {
+  if (!mx_config_ok(cfg)) return MSD_E_CONFIG;
+  if (batch <= 0 || batch > kMaxRows) return MSD_E_ARG;
+  return int64_t(layout(cfg, batch).bytes);
+}
+
+extern "C" int32_t msd_batch_decode_step(const msd_config* cfg, const void* token_emb, const void* output_proj,
+                                         const void* packed_w, const void* lnf_s, const float* rope,
+                                         const int32_t* tokens, const int32_t* positions, int32_t batch,
+                                         const int32_t* page_tables, int32_t max_pages, void* kv_pool,
+                                         int32_t pool_pages, void* workspace, float* logits,
+                                         int32_t* next_tokens, void* stream) {
+  if (!mx_config_ok(cfg)) return MSD_E_CONFIG;
+  const int M = batch;
+  if (M <= 0 || M > kMaxRows) return MSD_E_ARG;
+  if (!token_emb || !output_proj || !packed_w || !lnf_s || !rope || !tokens || !positions || !page_tables ||
+      !kv_pool || !workspace || !logits || !next_tokens)
     return MSD_E_ARG;
-  const uintptr_t al = reinterpret_cast<uintptr_t>(token_emb) | reinterpret_cast<uintptr_t>(output_proj) |
-                       reinterpret_cast<uintptr_t>(packed_w) | reinterpret_cast<uintptr_t>(kv) |
-                       reinterpret_cast<uintptr_t>(workspace);
-  if (al & 15) return MSD_E_ARG;
+  if (!aligned16(token_emb) || !aligned16(output_proj) || !aligned16(packed_w) || !aligned16(kv_pool) ||
+      !aligned16(workspace))
+    return MSD_E_ARG;
+  if (max_pages <= 0 || max_pages > (cfg->context_len + kPage - 1) / kPage || pool_pages <= 0) return MSD_E_ARG;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const int d = cfg->d_model, ff = cfg->d_ff, H = cfg->n_heads, KV = cfg->n_kv_heads, ctx = cfg->context_len;
-  const int nqkv = (H + 2 * KV) * kDh, V = cfg->vocab_size;
-  const PfLayout L = pf_layout(cfg, M);
+  const Weights wt{static_cast<const uint16_t*>(token_emb), static_cast<const uint16_t*>(output_proj),
+                   static_cast<const uint16_t*>(packed_w), static_cast<const uint16_t*>(lnf_s), rope};
+  const int d = cfg->d_model, V = cfg->vocab_size;
+  const Layout L = layout(cfg, M);
   char* ws = static_cast<char*>(workspace);
-  float* hbuf = reinterpret_cast<float*>(ws + L.h);
+  float* h = reinterpret_cast<float*>(ws + L.h);
   uint16_t* xn = reinterpret_cast<uint16_t*>(ws + L.xn);
-  float* qkv = reinterpret_cast<float*>(ws + L.qkv);
-  uint16_t* att = reinterpret_cast<uint16_t*>(ws + L.att);
-  uint16_t* act = reinterpret_cast<uint16_t*>(ws + L.act);
   float* part = reinterpret_cast<float*>(ws + L.part);
   int32_t* status = reinterpret_cast<int32_t*>(ws + L.status);
-  // per-layer packed offsets (same layout as the decode step)
-  const int64_t off_ln2 = d, off_qkv = 2 * int64_t(d), off_o = off_qkv + int64_t(nqkv) * d,
-                off_gu = off_o + int64_t(d) * d, off_dn = off_gu + 2 * int64_t(ff) * d,
-                layer = off_dn + int64_t(d) * ff;
-  const uint16_t* W = static_cast<const uint16_t*>(packed_w);
-  uint16_t* kvb = static_cast<uint16_t*>(kv);
+  int32_t* rowpos = reinterpret_cast<int32_t*>(ws + L.rowpos);
+  int32_t* pages = reinterpret_cast<int32_t*>(ws + L.pages);
   if (hipMemsetAsync(status, 0, 4, s) != hipSuccess) return MSD_E_HIP;
-  hipLaunchKernelGGL(pf_embed, dim3(M), dim3(256), 0, s, static_cast<const uint16_t*>(token_emb), tokens, d, hbuf,
-                     status, V);
-  int splits = 0;   // partials pending in `part` for the next norm
-  for (int l = 0; l < cfg->n_layers; ++l) {
-    const uint16_t* Wl = W + int64_t(l) * layer;
-    uint16_t* kc = kvb + int64_t(l) * 2 * KV * ctx * kDh;
-    uint16_t* vc = kc + int64_t(KV) * ctx * kDh;
-    hipLaunchKernelGGL(pf_norm, dim3(M), dim3(kNormThreads), 0, s, hbuf, part, splits, M, d, Wl, xn, 0);
-    GemmArgs g{};
-    g.A = xn; g.lda = d; g.M = M; g.K = d; g.splits = 1;
-    g.W = Wl + off_qkv; g.N = nqkv; g.out = qkv; g.ldo = nqkv;
-    g.kcache = kc; g.vcache = vc; g.rope = rope; g.H = H; g.KV = KV; g.ctx = ctx;
-    if (gemm<kEpiQkv>(g, s) != hipSuccess) return MSD_E_HIP;
-    hipLaunchKernelGGL(pf_attention, dim3(H, (M + kAttnQ - 1) / kAttnQ), dim3(256), 0, s, qkv, M, H, KV, att);
-    GemmArgs go{};
-    go.A = att; go.lda = d; go.M = M; go.K = d; go.splits = kSplitO;
-    go.W = Wl + off_o; go.N = d; go.out = part; go.ldo = d;
-    if (gemm<kEpiPart>(go, s) != hipSuccess) return MSD_E_HIP;
-    hipLaunchKernelGGL(pf_norm, dim3(M), dim3(kNormThreads), 0, s, hbuf, part, kSplitO, M, d, Wl + off_ln2, xn, 0);
-    GemmArgs gg{};
-    gg.A = xn; gg.lda = d; gg.M = M; gg.K = d; gg.splits = 1;
-    gg.W = Wl + off_gu; gg.N = 2 * ff; gg.act = act;
-    if (gemm<kEpiSwiglu>(gg, s) != hipSuccess) return MSD_E_HIP;
-    GemmArgs gd{};
-    gd.A = act; gd.lda = ff; gd.M = M; gd.K = ff; gd.splits = std::min(kSplitDn, ff / kBK);
-    gd.W = Wl + off_dn; gd.N = d; gd.out = part; gd.ldo = d;
-    if (gemm<kEpiPart>(gd, s) != hipSuccess) return MSD_E_HIP;
-    splits = gd.splits;
-  }
-  // final norm of the rows whose logits are wanted, then the tied output projection
-  const int r0 = logits_all ? 0 : M - 1, nr = M - r0;
-  hipLaunchKernelGGL(pf_norm, dim3(nr), dim3(kNormThreads), 0, s, hbuf, part, splits, M, d,
-                     static_cast<const uint16_t*>(lnf_s), xn, r0);
-  GemmArgs gl{};
-  gl.A = xn; gl.lda = d; gl.M = nr; gl.K = d; gl.splits = 1;
-  gl.W = static_cast<const uint16_t*>(output_proj); gl.N = V;
-  gl.out = logits_all ? logits_all : logits_last; gl.ldo = V;
-  if (gemm<kEpiLogits>(gl, s) != hipSuccess) return MSD_E_HIP;
-  const float* last = logits_all ? logits_all + int64_t(M - 1) * V : logits_last;
-  if (logits_all && hipMemcpyAsync(logits_last, last, size_t(V) * 4, hipMemcpyDeviceToDevice, s) != hipSuccess)
-    return MSD_E_HIP;
-  hipLaunchKernelGGL(pf_argmax, dim3(1), dim3(1024), 0, s, logits_last, V, next_token, status);
+  hipLaunchKernelGGL(mx_sanitize_rows, dim3((M + 255) / 256), dim3(256), 0, s, positions, 0, page_tables, M, max_pages,
+                     cfg->context_len, pool_pages, rowpos, pages, status);
+  Rows rows{M, rowpos, 1, pages, max_pages, pool_pages * kPage};
+  hipLaunchKernelGGL(mx_embed, dim3(M), dim3(256), 0, s, wt.emb, tokens, d, h, status, V);
+  hipError_t err;
+  const int pending = run_layers(cfg, wt, rows, static_cast<uint16_t*>(kv_pool), L, ws, false, s, err);
+  if (err != hipSuccess) return MSD_E_HIP;
+  hipLaunchKernelGGL(mx_norm, dim3(M), dim3(kNormThreads), 0, s, h, part, pending, M, d, wt.lnf, xn, 0);
+  if (gemm(xn, d, wt.outp, M, V, d, logits, V, 1, s) != hipSuccess) return MSD_E_HIP;
+  hipLaunchKernelGGL(mx_argmax, dim3(M), dim3(1024), 0, s, logits, V, V, next_tokens, status);
   return hipGetLastError() == hipSuccess ? MSD_OK : MSD_E_HIP;
 }

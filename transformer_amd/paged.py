@@ -1,0 +1,116 @@
+"""Batched decode of independent sequences over a paged KV cache (GPU).
+
+The reference describes this path without shipping it (a PagePool with in-kernel page
+tables and batched decode kernels, knowledge/program.md:214-216, 245-250); here it is built
+on the matrix-core passes of ``msd_prefill_paged`` / ``msd_batch_decode_step``:
+
+  pool = PagePool(config, n_pages)                 # [layer][K, V][kv_head][pages * 16][d_head] bf16
+  bd = PagedBatchDecoder(w, config, pool, batch=8)
+  first = bd.prefill(b, prompt, pages)             # one sequence's prompt into its pages
+  toks, logits = bd.step(tokens, positions)        # one token of every sequence per call
+
+Page tables are int32 (batch, max_pages); sequence b's position p lives in page
+``tables[b, p // 16]``, slot ``p % 16``.  Numerics are those of the prefill (bf16 projection
+inputs, f32 accumulation); the current position attends with its un-rounded K/V.
+"""
+import ctypes
+
+import numpy as np
+import torch
+
+from . import _lib
+
+PAGE = 16
+
+
+class PagePool:
+    """KV pages for every layer: bf16 [layer][K, V][kv_head][n_pages * 16][d_head]."""
+
+    def __init__(self, config, n_pages, device=None):
+        self.config = dict(config)
+        self.n_pages = int(n_pages)
+        dh = config.get("d_head", config["d_model"] // config["n_heads"])
+        n = config["n_layers"] * 2 * config["n_kv_heads"] * self.n_pages * PAGE * dh
+        self.data = torch.zeros(n, dtype=torch.bfloat16, device=device if device is not None else "cuda")
+
+    def view(self):
+        """(layers, 2, kv_heads, pool positions, d_head) view of the pages."""
+        c = self.config
+        return self.data.view(c["n_layers"], 2, c["n_kv_heads"], self.n_pages * PAGE, c["d_head"])
+
+    def gather(self, table, n_pos):
+        """Per-layer (K, V) of one sequence, (kv_heads, n_pos, d_head) each, read through ``table``."""
+        t = torch.as_tensor(np.asarray(table), dtype=torch.long, device=self.data.device)
+        p = torch.arange(n_pos, device=self.data.device)
+        rows = t[p // PAGE] * PAGE + p % PAGE
+        v = self.view()
+        return [(v[l, 0][:, rows], v[l, 1][:, rows]) for l in range(self.config["n_layers"])]
+
+
+class PagedBatchDecoder:
+    def __init__(self, w, config, pool, batch, max_pages=None, device=None):
+        self.w = w
+        self.config = dict(config)
+        self.pool = pool
+        self.batch = int(batch)
+        self.device = pool.data.device
+        self.max_pages = int(max_pages or -(-config["context_len"] // PAGE))
+        self._cfg = _lib.MsdConfig.from_dict(self.config)
+        L = _lib.lib()
+        nb = _lib.check(L.msd_batch_workspace_bytes(ctypes.byref(self._cfg), self.batch), "msd_batch_workspace_bytes")
+        npf = _lib.check(L.msd_prefill_workspace_bytes(ctypes.byref(self._cfg), config["context_len"]),
+                         "msd_prefill_workspace_bytes")
+        self.workspace = torch.empty(max(nb, npf), dtype=torch.uint8, device=self.device)
+        self.tables = torch.zeros((self.batch, self.max_pages), dtype=torch.int32, device=self.device)
+        self.logits = torch.empty((self.batch, config["vocab_size"]), dtype=torch.float32, device=self.device)
+        self.out = torch.zeros(2 * self.batch, dtype=torch.int32, device=self.device)
+        self.last = torch.empty(config["vocab_size"], dtype=torch.float32, device=self.device)
+        self.pf_out = torch.zeros(2, dtype=torch.int32, device=self.device)
+
+    def _w(self):
+        w = self.w
+        return (w["token_emb"].data_ptr(), w["output_proj"].data_ptr(), w["packed_w"].data_ptr(),
+                w["lnf_s"].data_ptr(), w["rope"].data_ptr())
+
+    def set_pages(self, b, pages):
+        pages = np.asarray(pages, dtype=np.int32)
+        if pages.size > self.max_pages or (pages.size and (pages.min() < 0 or pages.max() >= self.pool.n_pages)):
+            raise ValueError("page table entries outside the pool or too many pages")
+        row = np.zeros(self.max_pages, np.int32)
+        row[:pages.size] = pages
+        self.tables[b].copy_(torch.from_numpy(row))
+
+    def prefill(self, b, prompt, pages=None, stream=None):
+        """Prefill sequence b's prompt into its pages; returns the device int32[2] (argmax, status)."""
+        if pages is not None:
+            self.set_pages(b, pages)
+        toks = torch.as_tensor(np.asarray(prompt, dtype=np.int32)).to(self.device)
+        s = stream if stream is not None else torch.cuda.current_stream(self.device)
+        rc = _lib.lib().msd_prefill_paged(
+            ctypes.byref(self._cfg), *self._w(), toks.data_ptr(), toks.numel(), self.tables[b].data_ptr(),
+            self.max_pages, self.pool.data.data_ptr(), self.pool.n_pages, self.workspace.data_ptr(),
+            self.last.data_ptr(), self.pf_out.data_ptr(), ctypes.c_void_p(s.cuda_stream))
+        _lib.check(rc, "msd_prefill_paged")
+        self._keep = toks
+        return self.pf_out
+
+    def launch(self, tokens, positions, out=None, stream=None):
+        """Enqueue one step of all sequences (device int32 tensors of ``batch``); returns out."""
+        out = self.out if out is None else out
+        s = stream if stream is not None else torch.cuda.current_stream(self.device)
+        rc = _lib.lib().msd_batch_decode_step(
+            ctypes.byref(self._cfg), *self._w(), tokens.data_ptr(), positions.data_ptr(), self.batch,
+            self.tables.data_ptr(), self.max_pages, self.pool.data.data_ptr(), self.pool.n_pages,
+            self.workspace.data_ptr(), self.logits.data_ptr(), out.data_ptr(), ctypes.c_void_p(s.cuda_stream))
+        _lib.check(rc, "msd_batch_decode_step")
+        return out
+
+    def step(self, tokens, positions):
+        """One step from host lists; returns (next tokens (batch,) list, logits (batch, V) tensor)."""
+        t = torch.as_tensor(np.asarray(tokens, dtype=np.int32)).to(self.device)
+        p = torch.as_tensor(np.asarray(positions, dtype=np.int32)).to(self.device)
+        out = self.launch(t, p).cpu().numpy()
+        st = int(np.bitwise_or.reduce(out[1::2]))
+        if st:
+            raise _lib.MsdError(_lib.MSD_E_ARG, f"batched decode step (status {st:#x})")
+        return [int(x) for x in out[0::2]], self.logits
