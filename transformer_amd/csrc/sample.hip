@@ -17,12 +17,16 @@
 //     searchsorted(cdf / cdf[-1], u, 'right') with cdf the float64 cumulative sum.
 //
 // Kernels, all on the caller's stream:
-//   sample_prep_kernel     1 workgroup x 1024: penalty, temperature, argmax (temperature 0),
-//                          softmax, full-vocabulary draw (top_p >= 1), or the sort keys and the
-//                          first radix histogram (top_p < 1)
+//   sample_greedy_kernel   temperature 0: argmax of the penalised logits (1 workgroup)
+//   sample_softmax_kernel  one workgroup per 8192-id numpy reduction buffer: maximum, correctly
+//                          rounded exponentials and the buffer's pairwise sum
+//   sample_norm_kernel     512 ids per workgroup: normalisation, radix keys, first digit counts
+//   sample_full_kernel     top_p >= 1: inverse CDF over all ids (1 workgroup)
 //   sample_radix_kernel    4 stable LSD passes of 8 bits over (probability bits, id), tiles of
 //                          512 entries per workgroup; each pass counts the next pass's digits
-//   sample_nucleus_kernel  1 workgroup x 1024: the cumsum cutoff walk, renormalisation and draw
+//   sample_table_kernel    per 64-entry chunk of the sorted probabilities: exact ulp totals for
+//                          the cumsum walk
+//   sample_nucleus_kernel  1 workgroup: the cumsum cutoff walk, renormalisation and draw
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <math.h>
@@ -52,6 +56,7 @@ constexpr int kSlots = 255;                 // heap slots of one buffer's pairwi
 // Large LDS arrays keep entry j at j + j/32: a thread's 32 consecutive entries then start on
 // a different bank from its neighbours'.
 constexpr size_t kLdsBig = size_t(kVMax + kVMax / 32) * sizeof(float);
+constexpr size_t kLdsBuf = size_t(kRedChunk + kRedChunk / 32) * sizeof(float);
 
 enum Mode { kGreedy = 0, kFull = 1, kNucleus = 2 };
 
@@ -65,6 +70,8 @@ struct SArgs {
   uint32_t* keys[2];      // radix ping-pong: float bits of the probabilities
   uint32_t* ids[2];
   uint32_t* hist;         // [kPasses][kMaxTiles][256]
+  int* table;             // [3][kVMax / 64]: chunk totals, binades, odd-start changes
+  float* bsum;            // [kVMax / 8192]: numpy's per-buffer sums of the exponentials
   int V;
   int mode;
   int use_pen;
@@ -257,87 +264,150 @@ __device__ float np_sum(const float* a, int n, BlockScratch& b) {
 // ---------------------------------------------------------------- inverse CDF draw
 // RandomState.choice on one uniform: the number of i < n with cdf[i] / cdf[n-1] <= u, where
 // cdf is the float64 running sum of w[i] = (divide ? v[i] / div : v[i]) (float32 values,
-// padded LDS layout).  Thread t adds entries [32t, 32t+32) in order on top of the sum of all
-// earlier entries, so every partial sum equals the sequential one whenever the float64 sums
-// are exact (float32 terms spanning fewer than 29 binades below the total).
-__device__ int inverse_cdf(const float* v, int n, bool divide, float div, double u, BlockScratch& b) {
+// padded LDS layout; with divide the entries are replaced by w).  Thread t adds entries
+// [32t, 32t+32) in order on top of the sum of all earlier entries, so every partial sum equals
+// the sequential one whenever the float64 sums are exact (float32 terms spanning fewer than 29
+// binades below the total).  cdf / total is nondecreasing, so each thread tests its last entry
+// and only the thread whose range crosses u tests its entries one by one.
+__device__ int inverse_cdf(float* v, int n, bool divide, float div, double u, BlockScratch& b) {
+  __shared__ uint8_t flag[kT];
   const int t = threadIdx.x, base = t * kPer;
+  const int cnt = max(0, min(kPer, n - base));
+  if (divide) {
+#pragma unroll 8
+    for (int i = 0; i < kPer; ++i)
+      if (i < cnt) v[pad(base + i)] = v[pad(base + i)] / div;
+  }
   double tot = 0.0;
-  for (int i = 0; i < kPer; ++i) {
-    const int j = base + i;
-    if (j < n) tot += double(divide ? v[pad(j)] / div : v[pad(j)]);
-  }
+#pragma unroll 8
+  for (int i = 0; i < kPer; ++i)
+    if (i < cnt) tot += double(v[pad(base + i)]);
   const double excl = block_excl_scan_f64(tot, b);
-  if (base <= n - 1 && n - 1 < base + kPer) {   // cdf[n-1] as accumulated by its owner
-    double r = excl;
-    for (int i = 0; i < kPer; ++i) {
-      const int j = base + i;
-      if (j < n) r += double(divide ? v[pad(j)] / div : v[pad(j)]);
-    }
-    b.dtot = r;
-  }
+  double r = excl;
+#pragma unroll 8
+  for (int i = 0; i < kPer; ++i)
+    if (i < cnt) r += double(v[pad(base + i)]);
+  if (cnt > 0 && base + cnt == n) b.dtot = r;   // cdf[n-1] as accumulated by its owner
   __syncthreads();
   const double total = b.dtot;
-  double r = excl;
-  int cnt = 0;
-  for (int i = 0; i < kPer; ++i) {
-    const int j = base + i;
-    if (j < n) {
-      r += double(divide ? v[pad(j)] / div : v[pad(j)]);
-      if (r / total <= u) ++cnt;
+  const bool below = cnt > 0 && r / total <= u;
+  flag[t] = below;
+  __syncthreads();
+  int c = below ? cnt : 0;
+  if (cnt > 0 && !below && (t == 0 || flag[t - 1])) {   // the range that crosses u
+    double rr = excl;
+    for (int i = 0; i < cnt; ++i) {
+      rr += double(v[pad(base + i)]);
+      if (rr / total <= u) ++c;
     }
   }
-  const int c = block_sum_i(cnt, b);
-  return min(c, n - 1);
+  const int cs = block_sum_i(c, b);
+  return min(cs, n - 1);
 }
 
 // ---------------------------------------------------------------- nucleus cutoff
-// One wave: with cumsum the float32 running sum of the descending probabilities p[0..n),
-// returns searchsorted(cumsum, top_p) + 1 -- one past the first i with cumsum[i] >= top_p
-// (n + 1 when there is none).  t32 is the smallest float32 >= top_p, so cumsum[i] >= top_p
-// (compared in float64) exactly when cumsum[i] >= t32.
-//
 // Adding x to a float32 running sum s that stays in the binade [2^E, 2^(E+1)) adds
-// round-half-even(x / ulp) ulps, ulp = 2^(E-23), whatever s is, unless x / ulp has fraction
-// exactly 1/2 (then the parity of s decides).  64 entries at a time become integer ulp counts
-// whose exact prefix sums give every running sum, up to the first entry where the sum would
-// leave the binade, the fraction is 1/2, or top_p is reached; that entry is added with an
-// ordinary float32 addition and the walk resumes after it.  (p is sorted descending, so every
-// later x <= s and x / ulp < 2^24.)
-__device__ int nucleus_cutoff(const float* p, int n, float t32) {
+// round-half-even(x / ulp) ulps, ulp = 2^(E-23).  With y = x / ulp: y - floor(y) != 1/2 adds
+// rint(y) whatever s is; at a tie the addition adds floor(y) plus 1 when the sum so far plus
+// floor(y) is odd.  Over a run of entries that stays in the binade, let b_i be the parity of
+// the start value plus all entries' base counts (rint or floor) up to tie i: the cumulative
+// parity of the tie adjustments after tie i equals b_i, so tie i adds b_i XOR b_(previous tie).
+// Every running sum of a 64-entry chunk is therefore an exact integer prefix, computed in
+// parallel across the wave.
+
+constexpr int kChunks = kVMax / 64;
+
+// Inclusive prefix (in ulps of binade E) of the exact increments of this wave's 64 entries
+// added to start value S; tm / bm: masks of the tie lanes and of their parities b.
+__device__ int chunk_prefix(float x, bool valid, int S, int E, uint64_t& tm, uint64_t& bm) {
+  const int lane = lane_id();
+  const float y = ldexpf(x, 23 - E);
+  const float fl = floorf(y);
+  const bool tie = valid && (y - fl) == 0.5f;
+  const int base = valid ? (tie ? int(fl) : int(rintf(y))) : 0;
+  const int pb = wave_incl_scan(base);
+  const bool b = tie && ((S + pb) & 1);
+  tm = __ballot(tie);
+  bm = __ballot(b);
+  const uint64_t prev = tm & ((1ull << lane) - 1);
+  const bool bprev = prev ? ((bm >> (63 - __clzll(prev))) & 1ull) != 0 : false;
+  const uint64_t am = __ballot(tie && (b != bprev));
+  return pb + __popcll(am & ((2ull << lane) - 1));
+}
+
+// One wave: with cumsum the float32 running sum of the descending probabilities p[0..n),
+// padded LDS layout, returns searchsorted(cumsum, top_p) + 1 -- one past the first i with
+// cumsum[i] >= top_p (n + 1 when there is none).  t32 is the smallest float32 >= top_p, so
+// cumsum[i] >= top_p (compared in float64) exactly when cumsum[i] >= t32.
+// Whole chunks come from the table while the sum stays in the table's binade and below top_p;
+// otherwise the current chunk's exact prefixes are formed in parallel up to the first entry
+// where the sum would leave the binade or reach top_p, which is added with an ordinary float32
+// addition before the walk resumes after it.  (p is sorted descending, so every later x <= s
+// and x / ulp < 2^24.)
+__device__ int nucleus_cutoff(const float* p, int n, float t32, const int* ttot, const int* tex, const int* tdl) {
   const int lane = lane_id();
   float s = p[pad(0)];
   if (s >= t32) return 1;
   const int te = binade(t32);
   int k = 1;
-  float x = (k + lane < n) ? p[pad(k + lane)] : 0.f;
   while (k < n) {
-    const int jn = k + 64 + lane;
-    const float xn = jn < n ? p[pad(jn)] : 0.f;   // next block, used when this one has no special entry
     const int E = binade(s);
-    const bool valid = k + lane < n;
-    const float y = ldexpf(x, 23 - E);
-    const bool tie = (y - floorf(y)) == 0.5f;
-    const int q = int(rintf(y));
     const int S = int(ldexpf(s, 23 - E));
-    const int P = wave_incl_scan(q);
     const int lim = te == E ? int(ldexpf(t32, 23 - E)) : (1 << 24);
-    const uint64_t m = __ballot(!valid || tie || S + P >= lim);
+    if ((k & 63) == 0) {
+      // up to 64 whole chunks at once, lane = chunk k/64 + lane.  A chunk with ties leaves the
+      // sum's parity at the parity of its even-start total whatever it started with; one
+      // without ties flips it by that parity.  So each lane's start parity follows from the
+      // chunks since the last chunk with ties, and an inclusive scan of the totals gives the
+      // sum after every chunk; the run stops before the first chunk outside the table's
+      // binade or whose sum would reach the binade's end or top_p.
+      const int cc = (k >> 6) + lane;
+      const bool in = (cc + 1) * 64 <= n;
+      const int tv = in ? ttot[cc] : -1;
+      const bool good = tv >= 0 && tex[cc] == E;
+      const int dv = good ? tdl[cc] : 0;
+      const uint64_t gm = __ballot(good);
+      const int ngood = ~gm == 0 ? 64 : __ffsll(static_cast<unsigned long long>(~gm)) - 1;
+      if (ngood > 0) {
+        const uint64_t pe = __ballot(good && (tv & 1)), pd = __ballot(good && dv != 0);
+        const uint64_t lt = (1ull << lane) - 1;
+        const uint64_t pdl = pd & lt;
+        int pb;
+        if (pdl) {
+          const int j0 = 63 - __clzll(pdl);
+          pb = __popcll(pe & lt & ~((1ull << j0) - 1)) & 1;
+        } else {
+          pb = (S & 1) ^ (__popcll(pe & lt) & 1);
+        }
+        const int tot = good ? min(tv + (pb ? dv : 0), 1 << 24) : (1 << 24);
+        const int P = wave_incl_scan(tot);
+        const uint64_t stop = __ballot(lane >= ngood || S + P >= lim);
+        const int nadv = stop ? __ffsll(static_cast<unsigned long long>(stop)) - 1 : 64;
+        if (nadv > 0) {
+          s = ldexpf(float(S + readlane_i(P, nadv - 1)), E - 23);
+          k += 64 * nadv;
+          continue;
+        }
+      }
+    }
+    const int end = min(n, (k & ~63) + 64);   // the rest of the current chunk
+    const bool valid = k + lane < end;
+    const float x = valid ? p[pad(k + lane)] : 0.f;
+    uint64_t tm, bm;
+    const int pi = chunk_prefix(x, valid, S, E, tm, bm);
+    const uint64_t m = __ballot(valid && S + pi >= lim);
     if (m == 0) {
-      s = ldexpf(float(S + readlane_i(P, 63)), E - 23);
-      k += 64;
-      x = xn;
+      s = ldexpf(float(S + readlane_i(pi, 63)), E - 23);
+      k = end;
       continue;
     }
     const int f = __ffsll(static_cast<unsigned long long>(m)) - 1;
     const int jf = k + f;
-    if (jf >= n) return n + 1;
-    const float sp = f == 0 ? s : ldexpf(float(S + readlane_i(P, f - 1)), E - 23);
+    const float sp = f == 0 ? s : ldexpf(float(S + readlane_i(pi, f - 1)), E - 23);
     const float sn = sp + readlane_f(x, f);
     if (sn >= t32) return jf + 1;
     s = sn;
     k = jf + 1;
-    x = (k + lane < n) ? p[pad(k + lane)] : 0.f;
   }
   return n + 1;
 }
@@ -350,86 +420,158 @@ __device__ void finish(const SArgs& a, int token) {
   }
 }
 
-__global__ __launch_bounds__(kT) void sample_prep_kernel(SArgs a) {
-  extern __shared__ float sh_e[];   // kVMax entries, padded layout
+// Penalised logit of id j (generate.py:33-39), divided by the temperature when scaled
+// (generate.py:45-46); float32 operations as numpy performs them.
+__device__ __forceinline__ float penalised(const SArgs& a, int j, bool scaled) {
+  float v = a.logits[j];
+  if (a.use_pen && a.seen[j]) v = v > 0.f ? v / a.pen : v * a.pen;
+  if (scaled && a.scale) v = v / a.temp;
+  return v;
+}
+
+// temperature == 0: argmax of the penalised logits, lowest id on ties (generate.py:41-42)
+__global__ __launch_bounds__(kT) void sample_greedy_kernel(SArgs a) {
+  __shared__ BlockScratch b;
+  const int t = threadIdx.x;
+  float l[kPer];
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) l[i] = t + kT * i < a.V ? penalised(a, t + kT * i, false) : 0.f;
+  uint64_t best = 0;
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int j = t + kT * i;
+    if (j < a.V) {
+      const uint64_t key = (uint64_t(ordered(l[i])) << 32) | uint32_t(0xffffffffu - uint32_t(j));
+      best = key > best ? key : best;
+    }
+  }
+  best = block_max_u64(best, b);
+  finish(a, int(0xffffffffu - uint32_t(best & 0xffffffffu)));
+}
+
+// Softmax numerator (generate.py:48-50), one workgroup per numpy reduction buffer of 8192 ids:
+// every workgroup forms the maximum of all penalised, scaled logits (identically), then the
+// correctly rounded exp(l - max) of its buffer (to keys[1]) and numpy's pairwise sum of the
+// buffer (to bsum[buffer]).
+__global__ __launch_bounds__(kT) void sample_softmax_kernel(SArgs a) {
+  extern __shared__ float sh_e[];   // one buffer, padded layout
   __shared__ BlockScratch b;
   const int t = threadIdx.x, V = a.V;
   float l[kPer];
 #pragma unroll
-  for (int i = 0; i < kPer; ++i) {
-    const int j = t + kT * i;
-    float v = -INFINITY;
-    if (j < V) {
-      v = a.logits[j];
-      if (a.use_pen && a.seen[j]) v = v > 0.f ? v / a.pen : v * a.pen;
-    }
-    l[i] = v;
-  }
-  if (a.mode == kGreedy) {   // argmax, lowest id on ties
-    uint64_t best = 0;
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-      const int j = t + kT * i;
-      if (j < V) {
-        const uint64_t key = (uint64_t(ordered(l[i])) << 32) | uint32_t(0xffffffffu - uint32_t(j));
-        best = key > best ? key : best;
-      }
-    }
-    best = block_max_u64(best, b);
-    finish(a, int(0xffffffffu - uint32_t(best & 0xffffffffu)));
-    return;
-  }
-  // scaled logits to LDS; exp and normalisation run from LDS one entry at a time
+  for (int i = 0; i < kPer; ++i) l[i] = t + kT * i < V ? penalised(a, t + kT * i, true) : -INFINITY;
   float m = -INFINITY;
 #pragma unroll
-  for (int i = 0; i < kPer; ++i) {
-    const int j = t + kT * i;
-    if (j < V) {
-      if (a.scale) l[i] = l[i] / a.temp;
-      sh_e[pad(j)] = l[i];
-      m = fmaxf(m, l[i]);
-    }
-  }
+  for (int i = 0; i < kPer; ++i) m = fmaxf(m, l[i]);
   m = block_max(m, b);
-  for (int j = t; j < V; j += kT) sh_e[pad(j)] = float(exp(double(sh_e[pad(j)] - m)));
-  __syncthreads();
-  const float sum = np_sum(sh_e, V, b);
-  for (int j = t; j < V; j += kT) {
-    const float pj = sh_e[pad(j)] / sum;
-    sh_e[pad(j)] = pj;
-    if (a.probs_out) a.probs_out[j] = pj;
-  }
-  __syncthreads();
-  if (a.mode == kFull) {
-    const int tok = inverse_cdf(sh_e, V, false, 1.f, a.u[0], b);
-    finish(a, tok);
-    return;
-  }
+  const int b0 = blockIdx.x * kRedChunk, bn = min(kRedChunk, V - b0);
+  float* eo = reinterpret_cast<float*>(a.keys[1]);
 #pragma unroll
-  for (int i = 0; i < kPer; ++i) {
-    const int j = t + kT * i;
-    l[i] = j < V ? sh_e[pad(j)] : 0.f;
-  }
-  __syncthreads();
-  // top_p < 1: radix keys in id order and the first pass's per-tile digit counts
-  const int ntiles = (V + kTile - 1) / kTile;
-  uint32_t* hl = reinterpret_cast<uint32_t*>(sh_e);
-  for (int i = t; i < ntiles * 256; i += kT) hl[i] = 0;
-  __syncthreads();
-#pragma unroll
-  for (int i = 0; i < kPer; ++i) {
-    const int j = t + kT * i;
-    if (j < V) {
-      const uint32_t key = __float_as_uint(l[i]);
-      a.keys[0][j] = key;
-      a.ids[0][j] = uint32_t(j);
-      atomicAdd(&hl[(j / kTile) * 256 + (255u - (key & 255u))], 1u);
+  for (int i = 0; i < kRedChunk / kT; ++i) {
+    const int jl = t + kT * i;
+    if (jl < bn) {
+      const float e = float(exp(double(penalised(a, b0 + jl, true) - m)));
+      sh_e[pad(jl)] = e;
+      eo[b0 + jl] = e;
     }
   }
   __syncthreads();
-  for (int i = t; i < ntiles * 256; i += kT) {
-    a.hist[i] = hl[i];
-    for (int p = 1; p < kPasses; ++p) a.hist[p * kHistWords + i] = 0;
+  const float sb = np_sum(sh_e, bn, b);
+  if (t == 0) a.bsum[blockIdx.x] = sb;
+}
+
+// Normalisation (generate.py:51): p = e / sum with numpy's sum = the buffer sums added in order
+// to 0.  Workgroup w takes ids [512w, 512w+512): probabilities (optionally to probs_out), and for
+// top_p < 1 the radix keys in id order with this tile's counts of the first digit.
+__global__ __launch_bounds__(kTile) void sample_norm_kernel(SArgs a) {
+  __shared__ uint32_t hl[256];
+  const int t = threadIdx.x, w = blockIdx.x, V = a.V, j = w * kTile + t;
+  const int nbuf = (V + kRedChunk - 1) / kRedChunk;
+  float total = 0.f;
+  for (int q = 0; q < nbuf; ++q) total += a.bsum[q];
+  if (t < 256) hl[t] = 0;
+  __syncthreads();
+  if (j < V) {
+    const float pj = reinterpret_cast<const float*>(a.keys[1])[j] / total;
+    if (a.probs_out) a.probs_out[j] = pj;
+    const uint32_t key = __float_as_uint(pj);
+    a.keys[0][j] = key;
+    a.ids[0][j] = uint32_t(j);
+    if (a.mode == kNucleus) atomicAdd(&hl[255u - (key & 255u)], 1u);
+  }
+  __syncthreads();
+  if (a.mode == kNucleus && t < 256) {
+    a.hist[w * 256 + t] = hl[t];
+    for (int p = 1; p < kPasses; ++p) a.hist[p * kHistWords + w * 256 + t] = 0;
+  }
+}
+
+// top_p >= 1: RandomState.choice over all ids in id order (generate.py:65)
+__global__ __launch_bounds__(kT) void sample_full_kernel(SArgs a) {
+  extern __shared__ float sh_p[];   // probabilities in id order, padded layout
+  __shared__ BlockScratch b;
+  const int t = threadIdx.x, V = a.V;
+  uint32_t kv[kPer];
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) kv[i] = t + kT * i < V ? a.keys[0][t + kT * i] : 0u;
+#pragma unroll
+  for (int i = 0; i < kPer; ++i)
+    if (t + kT * i < V) sh_p[pad(t + kT * i)] = __uint_as_float(kv[i]);
+  __syncthreads();
+  finish(a, inverse_cdf(sh_p, V, false, 1.f, a.u[0], b));
+}
+
+// Table for whole chunks c (entries [64c, 64c+64)) of the sorted probabilities whose float32
+// running sum is certain to stay in one binade E: the float64 sums before and after the chunk
+// lie inside [2^E, 2^(E+1)) with a margin of 4e-3 relative (more than 32768 float32 roundings
+// can move a sum).  table[c] = the chunk's increment in ulps for an even start value (-1: take
+// it entry by entry), table[kChunks + c] = E, table[2 kChunks + c] = the change for an odd
+// start value (only the first tie's adjustment flips).  Workgroup w takes chunks
+// [16w, 16w + 16), one wave per chunk.
+constexpr int kTabChunks = kWaves;   // one chunk per wave
+
+__global__ __launch_bounds__(kT) void sample_table_kernel(SArgs a) {
+  __shared__ double red[kWaves];
+  __shared__ double csum[kTabChunks];
+  const int t = threadIdx.x, lane = lane_id(), wv = t >> 6;
+  const int n = a.V, nch = n / 64;
+  const int c0 = blockIdx.x * kTabChunks;
+  if (c0 >= nch) return;
+  const float* p = reinterpret_cast<const float*>(a.keys[kPasses & 1]);
+  // float64 sum of the entries before this workgroup's chunks (at most 31 per thread, all
+  // requested at once; the order is irrelevant: only the binade with its margin is used)
+  float pv[kPer];
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) pv[i] = t + kT * i < 64 * c0 ? p[t + kT * i] : 0.f;
+  double pre = 0.0;
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) pre += double(pv[i]);
+  for (int o = 32; o; o >>= 1) pre += __shfl_xor(pre, o);
+  if (lane == 0) red[wv] = pre;
+  const int c = c0 + wv;
+  const float x = c < nch ? p[64 * c + lane] : 0.f;
+  double v = x;
+  for (int o = 32; o; o >>= 1) v += __shfl_xor(v, o);
+  if (lane == 0) csum[wv] = v;
+  __syncthreads();
+  if (c >= nch) return;
+  double ps = 0.0;
+  for (int q = 0; q < kWaves; ++q) ps += red[q];
+  for (int q = 0; q < wv; ++q) ps += csum[q];
+  const double pe = ps + csum[wv];
+  const int E = ps > 0.0 ? ilogb(ps) : 0;
+  const bool ok = ps > 0.0 && ps >= ldexp(1.0, E) * (1.0 + 4e-3) && pe <= ldexp(1.0, E + 1) * (1.0 - 4e-3);
+  int tv = -1, dv = 0;
+  if (ok && __ballot(!(ldexpf(x, 23 - E) < 16777216.f)) == 0) {
+    uint64_t tm, bm;
+    const int pi = chunk_prefix(x, true, 0, E, tm, bm);
+    tv = readlane_i(pi, 63);
+    if (tm) dv = 1 - 2 * int((bm >> (__ffsll(static_cast<unsigned long long>(tm)) - 1)) & 1ull);
+  }
+  if (lane == 0) {
+    a.table[c] = tv;
+    a.table[kChunks + c] = E;
+    a.table[2 * kChunks + c] = dv;
   }
 }
 
@@ -504,12 +646,23 @@ __global__ __launch_bounds__(kTileThreads) void sample_radix_kernel(SArgs a, int
 __global__ __launch_bounds__(kT) void sample_nucleus_kernel(SArgs a) {
   extern __shared__ float sh_p[];   // sorted probabilities, padded layout
   __shared__ BlockScratch b;
+  __shared__ int ttot[kChunks], tex[kChunks], tdl[kChunks];
   const int t = threadIdx.x, V = a.V;
   const uint32_t* ks = a.keys[kPasses & 1];
-  for (int j = t; j < V; j += kT) sh_p[pad(j)] = __uint_as_float(ks[j]);
+  uint32_t kv[kPer];   // every load issued before the first LDS store
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) kv[i] = t + kT * i < V ? ks[t + kT * i] : 0u;
+  for (int c = t; c < V / 64; c += kT) {
+    ttot[c] = a.table[c];
+    tex[c] = a.table[kChunks + c];
+    tdl[c] = a.table[2 * kChunks + c];
+  }
+#pragma unroll
+  for (int i = 0; i < kPer; ++i)
+    if (t + kT * i < V) sh_p[pad(t + kT * i)] = __uint_as_float(kv[i]);
   __syncthreads();
   if (t < 64) {
-    const int c = nucleus_cutoff(sh_p, V, a.t32);
+    const int c = nucleus_cutoff(sh_p, V, a.t32, ttot, tex, tdl);
     if (t == 0) b.i0 = c;
   }
   __syncthreads();
@@ -522,7 +675,7 @@ __global__ __launch_bounds__(kT) void sample_nucleus_kernel(SArgs a) {
 
 // ---------------------------------------------------------------- host side
 struct SLayout {
-  size_t keys0, keys1, ids0, ids1, hist, bytes;
+  size_t keys0, keys1, ids0, ids1, hist, table, bsum, bytes;
 };
 
 static size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
@@ -535,19 +688,21 @@ static SLayout slayout(int V) {
   s.ids0 = 2 * arr;
   s.ids1 = 3 * arr;
   s.hist = 4 * arr;
-  s.bytes = s.hist + align256(size_t(kPasses) * kHistWords * sizeof(uint32_t));
+  s.table = s.hist + align256(size_t(kPasses) * kHistWords * sizeof(uint32_t));
+  s.bsum = s.table + align256(size_t(3) * (kVMax / 64) * sizeof(int));
+  s.bytes = s.bsum + 256;
   return s;
 }
 
 static hipError_t set_lds_once() {
   static bool done = false;
   if (done) return hipSuccess;
-  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&sample_prep_kernel),
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, int(kLdsBig));
-  if (e != hipSuccess) return e;
-  e = hipFuncSetAttribute(reinterpret_cast<const void*>(&sample_nucleus_kernel),
-                          hipFuncAttributeMaxDynamicSharedMemorySize, int(kLdsBig));
-  if (e != hipSuccess) return e;
+  const void* big[] = {reinterpret_cast<const void*>(&sample_full_kernel),
+                       reinterpret_cast<const void*>(&sample_nucleus_kernel)};
+  for (const void* k : big) {
+    const hipError_t e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, int(kLdsBig));
+    if (e != hipSuccess) return e;
+  }
   done = true;
   return hipSuccess;
 }
@@ -587,6 +742,8 @@ extern "C" int32_t msd_sample_token(const float* logits, int32_t vocab, double t
   a.ids[0] = reinterpret_cast<uint32_t*>(ws + L.ids0);
   a.ids[1] = reinterpret_cast<uint32_t*>(ws + L.ids1);
   a.hist = reinterpret_cast<uint32_t*>(ws + L.hist);
+  a.table = reinterpret_cast<int*>(ws + L.table);
+  a.bsum = reinterpret_cast<float*>(ws + L.bsum);
   a.V = vocab;
   a.use_pen = rep_penalty != 1.0;
   a.pen = float(rep_penalty);
@@ -597,14 +754,26 @@ extern "C" int32_t msd_sample_token(const float* logits, int32_t vocab, double t
   a.t32 = t32;
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (set_lds_once() != hipSuccess) return MSD_E_HIP;
-  hipLaunchKernelGGL(sample_prep_kernel, dim3(1), dim3(kT), kLdsBig, s, a);
+  if (a.mode == kGreedy) {
+    hipLaunchKernelGGL(sample_greedy_kernel, dim3(1), dim3(kT), 0, s, a);
+    return hipGetLastError() == hipSuccess ? MSD_OK : MSD_E_HIP;
+  }
+  const int ntiles = (vocab + kTile - 1) / kTile;
+  hipLaunchKernelGGL(sample_softmax_kernel, dim3((vocab + kRedChunk - 1) / kRedChunk), dim3(kT), kLdsBuf, s, a);
+  hipLaunchKernelGGL(sample_norm_kernel, dim3(ntiles), dim3(kTile), 0, s, a);
   if (hipGetLastError() != hipSuccess) return MSD_E_HIP;
-  if (a.mode == kNucleus) {
-    const int ntiles = (vocab + kTile - 1) / kTile;
+  if (a.mode == kFull) {
+    hipLaunchKernelGGL(sample_full_kernel, dim3(1), dim3(kT), kLdsBig, s, a);
+    return hipGetLastError() == hipSuccess ? MSD_OK : MSD_E_HIP;
+  }
+  {
     for (int p = 0; p < kPasses; ++p) {
       hipLaunchKernelGGL(sample_radix_kernel, dim3(ntiles), dim3(kTileThreads), 0, s, a, p);
       if (hipGetLastError() != hipSuccess) return MSD_E_HIP;
     }
+    hipLaunchKernelGGL(sample_table_kernel, dim3(std::max(1, (vocab / 64 + kTabChunks - 1) / kTabChunks)), dim3(kT), 0, s,
+                       a);
+    if (hipGetLastError() != hipSuccess) return MSD_E_HIP;
     hipLaunchKernelGGL(sample_nucleus_kernel, dim3(1), dim3(kT), kLdsBig, s, a);
     if (hipGetLastError() != hipSuccess) return MSD_E_HIP;
   }
