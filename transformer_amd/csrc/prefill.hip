@@ -423,39 +423,44 @@ __global__ __launch_bounds__(256) void mx_attention_prefill(const float* qkv, in
 
 // Batched decode: row m (one sequence at position p = pos(m)) and head blockIdx.y attend over
 // the cached rows 0..p-1 of the sequence (bf16, through its page table) and the row's
-// current, un-rounded K/V (multi_sm_decode.py:182-221).  Wave w takes the positions
-// 64*(w + 4*i) + lane (scores: lane = position) with its own running max and sum; each lane
-// looks its position's cache row up once and leaves it in LDS for the value loads, which are
-// issued 16 positions at a time; the four waves' states are merged in LDS at the end
-// (output: lane = dimension).
-__global__ __launch_bounds__(256) void mx_attention_decode(const float* qkv, Rows rows, int H, int KV,
-                                                           const uint16_t* kc, const uint16_t* vc, uint16_t* att) {
+// current, un-rounded K/V (multi_sm_decode.py:182-221).  Wave w takes positions
+// [64w, 64w + 64) (contexts up to 512): each lane looks its position's cache row up, then the
+// wave requests its K rows (lane = position) and all its V values (lane = dimension) at once,
+// so the block costs two memory round trips; each wave keeps its own maximum and sum and the
+// waves' states are merged in LDS at the end.
+constexpr int kAttnWaves = 8;
+
+__global__ __launch_bounds__(64 * kAttnWaves) void mx_attention_decode(const float* qkv, Rows rows, int H, int KV,
+                                                                       const uint16_t* kc, const uint16_t* vc,
+                                                                       uint16_t* att) {
   __shared__ float sq[kDh];
-  __shared__ float sp[4][64];
-  __shared__ int srow[4][64];
-  __shared__ float so[4][kDh];
-  __shared__ float sml[4][2];
+  __shared__ float sp[kAttnWaves][64];
+  __shared__ int srow[kAttnWaves][64];
+  __shared__ float so[kAttnWaves][kDh];
+  __shared__ float sml[kAttnWaves][2];
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int m = blockIdx.x, h = blockIdx.y, g = h / (H / KV);
   const int nqkv = (H + 2 * KV) * kDh, d = H * kDh;
   const int p = row_pos(rows, m);
   const float* qr = qkv + int64_t(m) * nqkv;
   if (threadIdx.x < kDh) sq[threadIdx.x] = qr[h * kDh + threadIdx.x];
-  __syncthreads();
   const uint16_t* kg = kc + int64_t(g) * rows.pool * kDh;
   const uint16_t* vg = vc + int64_t(g) * rows.pool * kDh;
-  const float vcur = qr[(H + KV + g) * kDh + lane];
+  const int j0 = 64 * wv, j = j0 + lane;
+  const int nj = max(0, min(64, p + 1 - j0));   // positions of this wave (the last one may be p)
+  srow[wv][lane] = j < p ? int(cache_row(rows, m, j)) : 0;
+  __syncthreads();
   float mx = -INFINITY, ls = 0.f, o = 0.f;
-  for (int j0 = 64 * wv; j0 <= p; j0 += 256) {
-    const int j = j0 + lane;
-    const int64_t crow = j < p ? cache_row(rows, m, j) : 0;
-    srow[wv][lane] = int(crow);
-    float s = -INFINITY;
-    if (j < p) {   // cached row: bf16
-      const uint4* kr = reinterpret_cast<const uint4*>(kg + crow * kDh);
-      uint4 ku[kDh / 8];
+  if (nj > 0) {
+    uint4 ku[kDh / 8];
+    const uint4* kr = reinterpret_cast<const uint4*>(kg + int64_t(srow[wv][lane]) * kDh);
 #pragma unroll
-      for (int e8 = 0; e8 < kDh / 8; ++e8) ku[e8] = kr[e8];
+    for (int e8 = 0; e8 < kDh / 8; ++e8) ku[e8] = kr[e8];
+    uint16_t vv[64];
+#pragma unroll
+    for (int jj = 0; jj < 64; ++jj) vv[jj] = vg[int64_t(srow[wv][jj]) * kDh + lane];
+    float s = -INFINITY;
+    if (j < p) {
       float a0 = 0.f, a1 = 0.f;
 #pragma unroll
       for (int e8 = 0; e8 < kDh / 8; ++e8) {
@@ -468,36 +473,27 @@ __global__ __launch_bounds__(256) void mx_attention_decode(const float* qkv, Row
       }
       s = (a0 + a1) * 0.125f;
     } else if (j == p) {   // current position: f32 K from this row's projection
-      const float* kr = qr + (H + g) * kDh;
+      const float* kq = qr + (H + g) * kDh;
       float a0 = 0.f, a1 = 0.f;
       for (int e = 0; e < kDh; e += 2) {
-        a0 += sq[e] * kr[e];
-        a1 += sq[e + 1] * kr[e + 1];
+        a0 += sq[e] * kq[e];
+        a1 += sq[e + 1] * kq[e + 1];
       }
       s = (a0 + a1) * 0.125f;
     }
-    const float mn = fmaxf(mx, wave_max(s));
-    const float e = (s == -INFINITY) ? 0.f : expf(s - mn);
-    const float es = wave_sum(e);
-    const float alpha = (mx == -INFINITY) ? 0.f : expf(mx - mn);
-    ls = ls * alpha + es;
-    o *= alpha;
-    mx = mn;
+    mx = wave_max(s);
+    const float e = (s == -INFINITY) ? 0.f : expf(s - mx);
+    ls = wave_sum(e);
     sp[wv][lane] = e;
     __builtin_amdgcn_wave_barrier();
-    const int nj = min(64, p + 1 - j0);
-    for (int jb = 0; jb < nj; jb += 16) {
-      float vv[16];
+    const float vcur = qr[(H + KV + g) * kDh + lane];
+    float o4[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int k = 0; k < 16; ++k) {
-        const int jj = jb + k;
-        vv[k] = jj < nj ? (j0 + jj < p ? bf2f(vg[int64_t(srow[wv][jj]) * kDh + lane]) : vcur) : 0.f;
-      }
-#pragma unroll
-      for (int k = 0; k < 16; ++k)
-        if (jb + k < nj) o += sp[wv][jb + k] * vv[k];
+    for (int jj = 0; jj < 64; ++jj) {
+      const float v = j0 + jj < p ? bf2f(vv[jj]) : (j0 + jj == p ? vcur : 0.f);
+      o4[jj & 3] += sp[wv][jj] * v;
     }
-    __builtin_amdgcn_wave_barrier();
+    o = (o4[0] + o4[1]) + (o4[2] + o4[3]);
   }
   so[wv][lane] = o;
   if (lane == 0) {
@@ -507,9 +503,9 @@ __global__ __launch_bounds__(256) void mx_attention_decode(const float* qkv, Row
   __syncthreads();
   if (wv == 0) {
     float M = -INFINITY;
-    for (int w = 0; w < 4; ++w) M = fmaxf(M, sml[w][0]);
+    for (int w = 0; w < kAttnWaves; ++w) M = fmaxf(M, sml[w][0]);
     float num = 0.f, den = 0.f;
-    for (int w = 0; w < 4; ++w) {
+    for (int w = 0; w < kAttnWaves; ++w) {
       if (sml[w][0] == -INFINITY) continue;
       const float a = expf(sml[w][0] - M);
       num += a * so[w][lane];
@@ -674,7 +670,7 @@ static int run_layers(const msd_config* cfg, const Weights& wt, const Rows& rows
       hipLaunchKernelGGL(mx_attention_prefill, dim3(H, (M + kAttnQ - 1) / kAttnQ), dim3(256), 0, s, qkv, M, H, KV,
                          att);
     else
-      hipLaunchKernelGGL(mx_attention_decode, dim3(M, H), dim3(256), 0, s, qkv, rows, H, KV, kc, vc, att);
+      hipLaunchKernelGGL(mx_attention_decode, dim3(M, H), dim3(64 * kAttnWaves), 0, s, qkv, rows, H, KV, kc, vc, att);
     if ((err = gemm(att, d, Wl + off_o, M, d, d, part, d, so, s)) != hipSuccess) break;
     hipLaunchKernelGGL(mx_norm, dim3(M), dim3(kNormThreads), 0, s, h, part, so, M, d, Wl + off_ln2, xn, 0);
     if ((err = gemm(xn, d, Wl + off_gu, M, 2 * ff, d, part, 2 * ff, sg, s)) != hipSuccess) break;
@@ -784,6 +780,7 @@ extern "C" int32_t msd_batch_decode_step(const msd_config* cfg, const void* toke
       !aligned16(workspace))
     return MSD_E_ARG;
   if (max_pages <= 0 || max_pages > (cfg->context_len + kPage - 1) / kPage || pool_pages <= 0) return MSD_E_ARG;
+  if (cfg->context_len > 64 * kAttnWaves) return MSD_E_CONFIG;   // one 64-position block per attention wave
   hipStream_t s = static_cast<hipStream_t>(stream);
   const Weights wt{static_cast<const uint16_t*>(token_emb), static_cast<const uint16_t*>(output_proj),
                    static_cast<const uint16_t*>(packed_w), static_cast<const uint16_t*>(lnf_s), rope};
