@@ -7,27 +7,37 @@
 // argmax resolving ties to the lowest index) follow kernels/multi_sm_decode.py.
 //
 // Execution model
-//   * grid = one workgroup per compute unit (256 on MI355X), 256 threads (4 wave64s);
-//     every workgroup is resident for the whole step (1 workgroup per CU, launched on an
-//     otherwise idle device), so workgroups may wait on each other.
-//   * weights are bf16 in an (out, in) row layout: every output element is one
-//     contiguous dot product, read with 128-bit loads (each lane 8 bf16 per load) and
-//     reduced across the wave; bf16 is widened to f32 in registers and all activation
-//     arithmetic is f32.
-//   * every workgroup keeps its own copy of the residual stream h (d floats in LDS) and
-//     recomputes the RMSNorms redundantly; only projection outputs cross workgroups.
+//   * grid = one workgroup per compute unit (256 on MI355X), 9 wave64s per workgroup;
+//     every workgroup is resident for the whole step (one per CU, launched on an otherwise
+//     idle device), so workgroups may wait on each other.
+//   * two kinds of workgroups:
+//       - row workgroups (all but the last H * nsplit) own fixed output rows of every
+//         projection and of the tied logits.  4 compute waves take the dot products,
+//         4 exchange waves keep the residual stream h, apply residual adds and RMSNorms,
+//         publish this workgroup's outputs and gather the next phase's input, and a
+//         loader wave streams the weight rows by DMA into an LDS ring one layer ahead;
+//       - attention workgroups (one per query head and context split of 512 positions)
+//         hold their KV head's cached rows in LDS (bf16, streamed in by their loader wave
+//         during the previous layer), gather the head's q and the new k, v, and publish
+//         the head's (max, sum, unnormalised output); row workgroups merge the splits.
+//   * weights are bf16 in an (out, in) row layout: every output element is one contiguous
+//     dot product; a lane reads 16 bytes (8 bf16) per 512-element block from LDS, widens
+//     them to f32 and the wave reduces with DPP.  All activation arithmetic is f32.
 //   * cross-workgroup exchange uses tagged 64-bit words: (f32 value | 32-bit epoch tag),
 //     written with device-scope atomic stores and polled with device-scope atomic loads.
 //     A word carries its own validity, so no separate flag, fence or barrier is needed;
 //     each (layer, exchange) has its own buffer so tags only need to differ per step.
-//   * per layer: QKV rows (+RoPE, KV write) -> attention over position chunks per KV head
-//     -> chunk merge -> O rows (+residual) -> gate/up rows (+SwiGLU) -> down rows
+//     Weight and KV streaming goes through the LDS-DMA path (global_load_lds), whose
+//     returns do not queue ahead of the exchange waves' polls the way loads into
+//     registers do.
+//   * per layer and row workgroup: QKV rows (+RoPE, KV write) -> attention (attention
+//     workgroups) -> O rows (+residual) -> gate/up rows (+SwiGLU) -> down rows
 //     (+residual); then final RMSNorm, vocabulary rows of the tied embedding, argmax via
 //     a 64-bit atomic max of (ordered value, inverted index) and a last-arriver counter.
-//   * every wait is bounded: a workgroup that exceeds the spin bound sets the status word
-//     and stops waiting; the others see the status and stop as well, so a broken step
-//     still drains the grid.
-
+//   * every cross-workgroup wait is bounded: a workgroup that exceeds the spin bound sets
+//     the status word and stops waiting; the others see the status and stop as well, so a
+//     broken step still drains the grid.  Waits between the waves of one workgroup use
+//     LDS counters (the loader wave never meets a workgroup barrier).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -37,61 +47,68 @@
 
 namespace msd {
 
-// Optional phase timestamps for profiling builds (-DMSD_TRACE): lane 0 of the first exchange
-// wave and of compute wave 0 record s_memrealtime (100 MHz) at phase boundaries of one layer
-// into msd_trace_buffer[workgroup][slot].  Compiled out otherwise.
+// Optional phase timestamps for profiling builds (-DMSD_TRACE): lane 0 of a wave records
+// s_memrealtime (100 MHz) at phase boundaries of layer MSD_TRACE_LAYER into
+// msd_trace_buffer[workgroup][slot].  Compiled out otherwise.
 #ifdef MSD_TRACE
 __device__ uint64_t msd_trace_buffer[4096 * 32];
-#define MSD_TRACE_POINT(cond, slot)                                                        \
+#define MSD_TRACE_POINT(cond, layer, slot)                                                \
   do {                                                                                    \
-    if ((cond) && l == MSD_TRACE_LAYER && c.lane == 0)                                    \
-      msd_trace_buffer[c.wg * 32 + (slot)] = __builtin_amdgcn_s_memrealtime();           \
+    if ((cond) && (layer) == MSD_TRACE_LAYER && (threadIdx.x & 63) == 0)                  \
+      msd_trace_buffer[blockIdx.x * 32 + (slot)] = __builtin_amdgcn_s_memrealtime();      \
+  } while (0)
+#define MSD_TRACE_CLOCK(cond, layer, slot)                                                \
+  do {                                                                                    \
+    if ((cond) && (layer) == MSD_TRACE_LAYER && (threadIdx.x & 63) == 0)                  \
+      msd_trace_buffer[blockIdx.x * 32 + (slot)] = __builtin_amdgcn_s_memtime();          \
   } while (0)
 #else
-#define MSD_TRACE_POINT(cond, slot) \
-  do {                              \
+#define MSD_TRACE_POINT(cond, layer, slot) \
+  do {                                     \
+  } while (0)
+#define MSD_TRACE_CLOCK(cond, layer, slot) \
+  do {                                     \
   } while (0)
 #endif
 
 constexpr int kDh = 64;          // head dimension (fixed)
-constexpr int kChunkMax = 64;    // attention positions per chunk (one per lane of a wave)
-constexpr int kPartStride = 66;  // per (chunk, head): m, l, o[64]
-// LDS row stride of cached K rows (floats): 16-byte aligned rows whose 128-bit reads by 16
-// consecutive lanes (one LDS pass) start 4 banks apart, so they never conflict.
-constexpr int kKPad = kDh + 4;
+constexpr int kPart = 66;        // per (head, split): m, l, o[64]
+constexpr int kAttCap = 512;     // cached positions an attention workgroup holds in LDS
+constexpr int kKRowB = 144;      // LDS bytes per cached K row: 128 + 16 padding, so 16-byte
+                                 // reads of consecutive rows by consecutive lanes never conflict
+constexpr int kVRowB = 128;      // LDS bytes per cached V row
 constexpr uint32_t kSpinLimit = 1u << 20;
 
-constexpr int kWavesC = 4;      // compute waves per workgroup
-constexpr int kWavesX = 4;      // exchange waves per workgroup
+constexpr int kWavesC = 4;       // compute waves of a row workgroup
+constexpr int kWavesX = 4;       // exchange waves of a row workgroup
+constexpr int kWavesA = 8;       // attention waves of an attention workgroup
+constexpr int kLoader = 8;       // wave index of the loader (both kinds)
+constexpr int kThreadsWG = 9 * 64;
+constexpr int kMbox = 8;         // outputs per compute wave and phase
+constexpr int kRep = 8;          // replicas of every vector all row workgroups gather
+static_assert(kWavesA == kRep, "each attention wave stores one replica");
+constexpr int kDmaWindow = 48;   // 1 KB DMA instructions a loader keeps in flight
 
 constexpr uint32_t kStatusTimeout = 1u;
 constexpr uint32_t kStatusBadToken = 2u;
+
+__host__ __device__ inline int cdiv(int a, int b) { return (a + b - 1) / b; }
+__host__ __device__ inline int64_t align64(int64_t v) { return (v + 63) & ~int64_t(63); }
 
 // ---------------------------------------------------------------- layout
 struct Layout {
   // packed weights, per layer (bf16 elements)
   int64_t off_ln1, off_ln2, off_qkv, off_o, off_gu, off_dn, layer_elems;
-  // exchange words per layer (uint64)
-  int64_t x_qkv, x_part, x_attn, x_hd1, x_act, x_hd2, x_layer;
-  int64_t x_rep;   // word stride between the replicas of the all-gathered vectors
+  // exchange words per layer (uint64): x_qkv once, then kRep replicas (stride x_rep) of
+  // [attention partials | hd1 | act | hd2]
+  int64_t x_qkv, x_att, x_hd1, x_act, x_hd2, x_rep, x_layer;
   int64_t ctrl_bytes;
-  // producer flags: flags[(layer * kNumEx + exchange) * G + producer_workgroup] (uint32)
-  int64_t flag_words;   // uint32 flags per layer
 };
 
-// Replicas of every exchange vector that all workgroups gather (workgroup w reads replica
-// w % kRep, its XCD under the round-robin dispatch of workgroups to XCDs).
-constexpr int kRep = 8;
+__host__ __device__ inline int att_cap(int ctx) { return ctx < kAttCap ? ctx : kAttCap; }
+__host__ __device__ inline int att_splits(int ctx) { return cdiv(ctx, att_cap(ctx)); }
 
-// exchanges of a layer (index into the flag arrays)
-enum { kExQkv = 0, kExPart = 1, kExAttn = 2, kExHd1 = 3, kExAct = 4, kExHd2 = 5, kNumEx = 6 };
-
-__host__ __device__ inline int64_t align64(int64_t v) { return (v + 63) & ~int64_t(63); }
-
-// attention chunks per KV head: enough that a chunk of the full context fits a wave
-__host__ __device__ inline int n_chunks(int ctx) { return (ctx + kChunkMax - 1) / kChunkMax; }
-
-__host__ __device__ inline Layout make_layout(int d, int H, int KV, int ff, int ctx, int G = 0) {
+__host__ __device__ inline Layout make_layout(int d, int H, int KV, int ff, int ctx) {
   Layout t;
   const int64_t nqkv = int64_t(H + 2 * KV) * kDh;
   t.off_ln1 = 0;
@@ -101,20 +118,16 @@ __host__ __device__ inline Layout make_layout(int d, int H, int KV, int ff, int 
   t.off_gu = t.off_o + int64_t(d) * d;
   t.off_dn = t.off_gu + 2 * int64_t(ff) * d;
   t.layer_elems = t.off_dn + int64_t(d) * ff;
-  const int GQ = H / KV;
   t.x_qkv = 0;
-  t.x_part = t.x_qkv + align64(nqkv);
-  t.x_attn = t.x_part + align64(int64_t(KV) * n_chunks(ctx) * GQ * kPartStride);
-  t.x_hd1 = t.x_attn + align64(d);
+  t.x_att = align64(nqkv);
+  t.x_hd1 = t.x_att + align64(int64_t(H) * att_splits(ctx) * kPart);
   t.x_act = t.x_hd1 + align64(d);
   t.x_hd2 = t.x_act + align64(ff);
-  // attn, hd1, act and hd2 are read by every workgroup: kRep replicas (at a stride that is
-  // not a multiple of 4 KB) spread those reads over the memory channels
-  const int64_t rep_words = t.x_hd2 + align64(d) - t.x_attn;
+  // replicas at a stride that is not a multiple of 4 KB spread the reads over channels
+  const int64_t rep_words = t.x_hd2 + align64(d) - t.x_att;
   t.x_rep = ((rep_words + 511) & ~int64_t(511)) + 32;
-  t.x_layer = t.x_attn + kRep * t.x_rep;
+  t.x_layer = t.x_att + kRep * t.x_rep;
   t.ctrl_bytes = 256;
-  t.flag_words = int64_t(kNumEx) * G;
   return t;
 }
 
@@ -130,10 +143,13 @@ struct Args {
   const int32_t* token_dev;
   uint32_t* ctrl;   // [0] status, [1] arrival counter, [2..3] argmax key (u64)
   uint64_t* xw;     // exchange words, n_layers * x_layer
-  uint32_t* flags;  // producer flags, n_layers * flag_words
   int token, pos;
   uint32_t epoch;
-  int H, KV, L, ff, V, ctx, nch;
+  int H, KV, L, ff, V, ctx;
+  int nsplit, cap, NA, GR;   // attention splits, positions per split, attention / row workgroups
+  // row workgroups: LDS ring regions (bytes) of the QKV, O, gate/up and down rows, the
+  // ring size, and logit rows per ring half
+  int ring_q, ring_o, ring_g, ring_d, ring_bytes, log_rows;
   Layout lay;
 };
 
@@ -150,7 +166,7 @@ __device__ __forceinline__ uint16_t f2bf(float f) {  // round to nearest even
 // row_shr 1/2/4/8, then row_bcast 15/31 carry the row totals into lane 63, which is read
 // back as a wave-uniform value.  The addition order is fixed, so every call is
 // deterministic.
-__device__ __forceinline__ float dpp_f(float v, int ctrl, int row_mask) {
+__device__ __forceinline__ float dpp_f(float v, int ctrl) {
   switch (ctrl) {   // the control word must be a compile-time constant
     case 0x111: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x111, 0xf, 0xf, true));
     case 0x112: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x112, 0xf, 0xf, true));
@@ -159,15 +175,14 @@ __device__ __forceinline__ float dpp_f(float v, int ctrl, int row_mask) {
     case 0x142: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x142, 0xa, 0xf, true));
     default: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x143, 0xc, 0xf, true));
   }
-  (void)row_mask;
 }
 __device__ __forceinline__ float wave_sum(float v) {
-  v += dpp_f(v, 0x111, 0xf);
-  v += dpp_f(v, 0x112, 0xf);
-  v += dpp_f(v, 0x114, 0xf);
-  v += dpp_f(v, 0x118, 0xf);
-  v += dpp_f(v, 0x142, 0xa);
-  v += dpp_f(v, 0x143, 0xc);
+  v += dpp_f(v, 0x111);
+  v += dpp_f(v, 0x112);
+  v += dpp_f(v, 0x114);
+  v += dpp_f(v, 0x118);
+  v += dpp_f(v, 0x142);
+  v += dpp_f(v, 0x143);
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 // max over the wave; -inf fills lanes without a DPP source
@@ -192,6 +207,26 @@ __device__ __forceinline__ float wave_max(float v) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
+// N independent wave sums taken one DPP step at a time across all N values (the chains
+// interleave); same addition order as wave_sum.
+template <int N>
+__device__ __forceinline__ void wave_sum_n(float (&v)[N]) {
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] += dpp_f(v[i], 0x111);
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] += dpp_f(v[i], 0x112);
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] += dpp_f(v[i], 0x114);
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] += dpp_f(v[i], 0x118);
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] += dpp_f(v[i], 0x142);
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] += dpp_f(v[i], 0x143);
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v[i]), 63));
+}
+
 __device__ __forceinline__ void st_tag(uint64_t* p, float v, uint32_t tag) {
   __hip_atomic_store(p, (uint64_t(tag) << 32) | __float_as_uint(v), __ATOMIC_RELAXED,
                      __HIP_MEMORY_SCOPE_AGENT);
@@ -199,131 +234,161 @@ __device__ __forceinline__ void st_tag(uint64_t* p, float v, uint32_t tag) {
 __device__ __forceinline__ uint64_t ld_tag(const uint64_t* p) {
   return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ void st_flag(uint32_t* p, uint32_t tag) {
-  __hip_atomic_store(p, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ uint32_t ld_flag(const uint32_t* p) {
-  return __hip_atomic_load(const_cast<uint32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 __device__ __forceinline__ uint32_t ld_status(uint32_t* ctrl) {
   return __hip_atomic_load(ctrl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Poll NW tagged words per lane (word k of lane at src[idx(k)]) until every tag equals
-// `tag`.  A bounded spin: after kSpinLimit rounds, or when another workgroup has reported a
-// timeout in the status word, the wave stops waiting and `bad` is set.
-constexpr int kXW = 12;   // words per lane per exchange wave and batch (3072 words per batch)
-
-// The exchange waves share a gather: 64-word blocks are dealt round-robin to the
-// kWavesX waves (block b -> wave b % kWavesX), so wave ew, lane j handles words
-// 64 * (kWavesX * k + ew) + j.
-__device__ __forceinline__ int xidx(int k, int ew, int lane) { return 64 * (kWavesX * k + ew) + lane; }
-
-__device__ void gather_x(const uint64_t* src, int n, float* dst, uint32_t tag, uint32_t* ctrl,
-                         int ew, int lane, bool& bad) {
-  for (int base = 0; base < n; base += 64 * kWavesX * kXW) {
-    uint64_t w[kXW];
-#pragma unroll
-    for (int k = 0; k < kXW; ++k) {
-      const int i = base + xidx(k, ew, lane);
-      w[k] = (i < n) ? ld_tag(src + i) : (uint64_t(tag) << 32);
-    }
-    uint32_t spins = 0;
-    while (!bad) {
-      bool ok = true;
-#pragma unroll
-      for (int k = 0; k < kXW; ++k) {
-        if (uint32_t(w[k] >> 32) != tag) {
-          ok = false;
-          w[k] = ld_tag(src + base + xidx(k, ew, lane));
-        }
-      }
-      if (__all(ok)) break;
-      ++spins;
-      if ((spins & 255u) == 0 && (ld_status(ctrl) & kStatusTimeout)) bad = true;
-      if (spins > kSpinLimit) {
-        if (lane == 0) atomicOr(ctrl, kStatusTimeout);
-        bad = true;
-      }
-    }
-#pragma unroll
-    for (int k = 0; k < kXW; ++k) {
-      const int i = base + xidx(k, ew, lane);
-      if (i < n) dst[i] = __uint_as_float(uint32_t(w[k]));
-    }
+// One step of a bounded spin: after kSpinLimit rounds, or when another workgroup has
+// reported a timeout in the status word, the wave stops waiting and `bad` is set.
+__device__ __forceinline__ void spin_step(uint32_t& spins, uint32_t* ctrl, int lane, bool& bad) {
+  __builtin_amdgcn_s_sleep(2);   // a short pause between poll rounds (measured: less contention)
+  ++spins;
+  if ((spins & 255u) == 0 && (ld_status(ctrl) & kStatusTimeout)) bad = true;
+  if (spins > kSpinLimit) {
+    if (lane == 0) atomicOr(ctrl, kStatusTimeout);
+    bad = true;
   }
 }
 
-// Producer-flag gating of gathers.  With MSD_FLAG_POLL defined, consumers first wait for the
-// producers' flags and then read the data; otherwise they poll the tagged data words
-// directly (one round trip less; the flags are still raised).
-#ifdef MSD_FLAG_POLL
-constexpr bool kFlagPoll = true;
-#else
-constexpr bool kFlagPoll = false;
-#endif
+// Polling of tagged words.  Lane j of wave w (of nw waves sharing a vector) handles slots
+// k < NK, word xidx(k, w, j): 64-word blocks are dealt round-robin to the waves.  Each
+// round re-loads only the words whose tag is not yet current and waits for them; a
+// single round is in flight, so the polls of one CU never queue many loads ahead of its
+// latency-critical stores.
+template <int NW>
+__device__ __forceinline__ int xidx(int k, int w, int lane) { return 64 * (NW * k + w) + lane; }
 
-// Wait until the producer flags f[0..n) all equal `tag` (one wave; bounded spin).  A
-// producer raises its flag after issuing its tagged data words, so a consumer polls n
-// 4-byte flags instead of all data words; the data words are still validated by their tags.
-__device__ void poll_flags(const uint32_t* f, int n, uint32_t tag, uint32_t* ctrl, int lane, bool& bad) {
-  if (!kFlagPoll) return;
-  for (int base = 0; base < n; base += 64 * 4) {
-    uint32_t v[4];
+template <int NW, int NK>
+__device__ __forceinline__ bool repoll(uint64_t (&wd)[NK], const uint64_t* src, int n, uint32_t tag, int w, int lane) {
+  bool ok = true;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int i = base + lane + 64 * k;
-      v[k] = (i < n) ? ld_flag(f + i) : tag;
+  for (int k = 0; k < NK; ++k) {
+    if (uint32_t(wd[k] >> 32) != tag) {
+      ok = false;
+      wd[k] = ld_tag(src + xidx<NW>(k, w, lane));
     }
-    uint32_t spins = 0;
-    while (!bad) {
-      bool ok = true;
+  }
+  return ok;
+}
+
+template <int NW, int NK, int SLEEP = 0>
+__device__ __forceinline__ void poll_words(const uint64_t* src, int n, uint32_t tag, float (&v)[NK],
+                                           uint32_t* ctrl, int w, int lane, bool& bad) {
+  uint64_t wd[NK];
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        if (v[k] != tag) {
-          ok = false;
-          v[k] = ld_flag(f + base + lane + 64 * k);
-        }
-      }
-      if (__all(ok)) break;
-      ++spins;
-      if ((spins & 255u) == 0 && (ld_status(ctrl) & kStatusTimeout)) bad = true;
-      if (spins > kSpinLimit) {
-        if (lane == 0) atomicOr(ctrl, kStatusTimeout);
-        bad = true;
+  for (int k = 0; k < NK; ++k) {
+    const int i = xidx<NW>(k, w, lane);
+    wd[k] = (i < n) ? ld_tag(src + i) : (uint64_t(tag) << 32);
+  }
+  uint32_t spins = 0;
+  while (!bad && !__all(repoll<NW, NK>(wd, src, n, tag, w, lane))) {
+    if constexpr (SLEEP > 0) __builtin_amdgcn_s_sleep(SLEEP);   // fewer polls during long waits
+    spin_step(spins, ctrl, lane, bad);
+  }
+#pragma unroll
+  for (int k = 0; k < NK; ++k) v[k] = __uint_as_float(uint32_t(wd[k]));
+}
+
+// Gather n tagged words src[0..n) into dst (LDS floats), NW waves sharing the words.
+template <int NW, int NK, int SLEEP = 0>
+__device__ __forceinline__ void gather_x(const uint64_t* src, int n, float* dst, uint32_t tag, uint32_t* ctrl,
+                                         int w, int lane, bool& bad) {
+  float v[NK];
+  poll_words<NW, NK, SLEEP>(src, n, tag, v, ctrl, w, lane, bad);
+#pragma unroll
+  for (int k = 0; k < NK; ++k) {
+    const int i = xidx<NW>(k, w, lane);
+    if (i < n) dst[i] = v[k];
+  }
+}
+
+// Store R outputs of a wave (values y, word indices ix; the first nv are valid) to the
+// exchange block X: one store instruction per output, lane r writing replica r (lane 0
+// only when not replicated).
+template <int R>
+__device__ __forceinline__ void store_out(uint64_t* X, const float (&y)[R], const int (&ix)[R], int nv,
+                                          bool replicated, int64_t x_rep, uint32_t tag, int lane) {
+  const int nl = replicated ? kRep : 1;
+#pragma unroll
+  for (int j = 0; j < R; ++j)
+    if (j < nv && lane < nl) st_tag(X + ix[j] + lane * x_rep, y[j], tag);
+}
+
+// LDS counters between the waves of one workgroup.
+__device__ __forceinline__ int lds_ld(int* ctr) {
+  return __hip_atomic_load(ctr, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+// Bounded like the cross-workgroup waits: every 1024 spins the wave checks the status word
+// and gives up once a timeout has been reported; after kLdsSpinLimit spins it reports one.
+constexpr uint32_t kLdsSpinLimit = 1u << 22;
+__device__ __forceinline__ void lds_wait(int* ctr, int target, uint32_t* gctrl) {
+  uint32_t spins = 0;
+  while (lds_ld(ctr) < target) {
+    __builtin_amdgcn_s_sleep(1);
+    if ((++spins & 1023u) == 0) {
+      if (ld_status(gctrl) & kStatusTimeout) return;
+      if (spins > kLdsSpinLimit) {
+        atomicOr(gctrl, kStatusTimeout);
+        return;
       }
     }
   }
 }
-
-// LDS spin-wait until *ctr >= target (intra-workgroup hand-off between wave roles).
-__device__ __forceinline__ void lds_wait(int* ctr, int target) {
-  while (__hip_atomic_load(ctr, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < target) __builtin_amdgcn_s_sleep(1);
-}
+// Bump after this wave's LDS writes are done (lgkmcnt(0)).
 __device__ __forceinline__ void lds_bump(int* ctr, int lane) {
-  __builtin_amdgcn_s_waitcnt(0xc07f);   // this wave's LDS writes are done (lgkmcnt(0))
+  __builtin_amdgcn_s_waitcnt(0xc07f);
   if (lane == 0) __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
-
-// Synchronise the exchange waves only (the compute waves are not involved): every wave
-// bumps an LDS counter and waits for the other waves' bumps.  `phase` counts calls.
-__device__ __forceinline__ void xsync(int* ctr, int& phase, int lane) {
-  phase += kWavesX;
-  __builtin_amdgcn_s_waitcnt(0xc07f);   // this wave's LDS writes are done (lgkmcnt(0))
-  if (lane == 0) __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
-  while (__hip_atomic_load(ctr, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < phase) __builtin_amdgcn_s_sleep(1);
+__device__ __forceinline__ void lds_set(int* ctr, int v, int lane) {
+  __builtin_amdgcn_s_waitcnt(0xc07f);
+  if (lane == 0) __hip_atomic_store(ctr, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+// Barrier of n waves on an LDS counter; `phase` counts calls.
+__device__ __forceinline__ void wsync(int* ctr, int& phase, int n, int lane, uint32_t* gctrl) {
+  phase += n;
+  lds_bump(ctr, lane);
+  lds_wait(ctr, phase, gctrl);
 }
 
-// Row layout for the matrix-vector products.  A row of K bf16 values is cut into blocks of
-// 512 (the last block may be shorter: S = 8*m values, m lanes); in block b, lane l holds the
-// 16 bytes at packed offset 512*b + 8*l, and its k-th value (k < 8) multiplies input element
-// 512*b + k*m + l.  The packer applies that in-dimension permutation to every row, so the
-// lane's 8 inputs are x[512*b + k*m + l]: consecutive lanes read consecutive LDS words
-// (no bank conflicts) and each lane keeps its inputs in registers for all rows of a phase.
-template <int NL>
-struct Row {
-  uint4 v[NL];
+// ---------------------------------------------------------------- LDS-DMA streaming
+// global_load_lds_dwordx4: lane i copies 16 bytes from its global address to
+// lds_base + 16 * i.  A loader keeps at most kDmaWindow instructions in flight.
+__device__ __forceinline__ constexpr int vmcnt_imm(int k) {
+  return (k & 0xF) | ((k >> 4) << 14) | (7 << 4) | (0xF << 8);
+}
+struct Dma {
+  int inflight = 0;
+  __device__ __forceinline__ void issue(const void* src, uint8_t* lds_base) {
+    __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds_base, 16, 0, 0);
+    if (++inflight == kDmaWindow) {
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(kDmaWindow - 1));
+      inflight = kDmaWindow - 1;
+    }
+  }
+  __device__ __forceinline__ void drain() {
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    inflight = 0;
+  }
 };
+
+// Copy `bytes` (a multiple of 16) from src to lds: instruction t covers bytes
+// [1024 t, 1024 t + 1024); lanes past the end re-read the last 16 bytes into the
+// padding that rounds every region up to 1 KB.
+__device__ __forceinline__ void dma_copy(Dma& d, const uint8_t* src, uint8_t* lds, int64_t bytes, int lane) {
+  for (int64_t t = 0; t * 1024 < bytes; ++t) {
+    int64_t o = t * 1024 + 16 * lane;
+    if (o > bytes - 16) o = bytes - 16;
+    d.issue(src + o, lds + t * 1024);
+  }
+}
+
+// ---------------------------------------------------------------- row dot products
+// Row layout: a row of K bf16 values is cut into blocks of 512 (the last block may be
+// shorter: S = 8*m values, m lanes); in block b, lane l holds the 16 bytes at packed
+// offset 512*b + 8*l, and its k-th value (k < 8) multiplies input element 512*b + k*m + l.
+// The packer applies that in-dimension permutation to every row, so the lane's 8 inputs
+// are x[512*b + k*m + l]: consecutive lanes read consecutive LDS words (no bank conflicts)
+// and each lane keeps its inputs in registers for all rows of a phase.
 template <int NL>
 struct XV {
   float v[NL][8];
@@ -332,13 +397,6 @@ struct XV {
 __device__ __forceinline__ int block_lanes(int k, int b) {
   const int rem = k - 512 * b;
   return rem >= 512 ? 64 : (rem > 0 ? rem / 8 : 0);
-}
-
-template <int NL>
-__device__ __forceinline__ void load_row(Row<NL>& r, const uint16_t* row, int k, int lane) {
-  const uint4* p = reinterpret_cast<const uint4*>(row);
-#pragma unroll
-  for (int j = 0; j < NL; ++j) r.v[j] = (lane < block_lanes(k, j)) ? p[j * 64 + lane] : make_uint4(0, 0, 0, 0);
 }
 
 template <int NL>
@@ -351,45 +409,36 @@ __device__ __forceinline__ void load_x(XV<NL>& xv, const float* x, int k, int la
   }
 }
 
-template <int NL>
-__device__ __forceinline__ float dot_row(const Row<NL>& r, const XV<NL>& xv) {
-  float acc = 0.f;
+// Dot products of R rows (in LDS) with the lane's inputs: every 16-byte piece of every row
+// is read before the first multiply, then the R wave sums run interleaved.  Lanes past a
+// short last block read in-bounds LDS bytes beyond the row and zero them.
+template <int NL, int R>
+__device__ __forceinline__ void dot_rows(const uint8_t* const (&rows)[R], const XV<NL>& xv, int k, int lane,
+                                         float (&out)[R]) {
+  uint4 w[R][NL];
 #pragma unroll
-  for (int j = 0; j < NL; ++j) {
-    const uint4 w = r.v[j];
-    acc += bf_lo(w.x) * xv.v[j][0];
-    acc += bf_hi(w.x) * xv.v[j][1];
-    acc += bf_lo(w.y) * xv.v[j][2];
-    acc += bf_hi(w.y) * xv.v[j][3];
-    acc += bf_lo(w.z) * xv.v[j][4];
-    acc += bf_hi(w.z) * xv.v[j][5];
-    acc += bf_lo(w.w) * xv.v[j][6];
-    acc += bf_hi(w.w) * xv.v[j][7];
+  for (int i = 0; i < R; ++i)
+#pragma unroll
+    for (int j = 0; j < NL; ++j) w[i][j] = *reinterpret_cast<const uint4*>(rows[i] + 1024 * j + 16 * lane);
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    float acc = 0.f;
+#pragma unroll
+    for (int j = 0; j < NL; ++j) {
+      uint4 u = w[i][j];
+      if (lane >= block_lanes(k, j)) u = make_uint4(0, 0, 0, 0);
+      acc += bf_lo(u.x) * xv.v[j][0];
+      acc += bf_hi(u.x) * xv.v[j][1];
+      acc += bf_lo(u.y) * xv.v[j][2];
+      acc += bf_hi(u.y) * xv.v[j][3];
+      acc += bf_lo(u.z) * xv.v[j][4];
+      acc += bf_hi(u.z) * xv.v[j][5];
+      acc += bf_lo(u.w) * xv.v[j][6];
+      acc += bf_hi(u.w) * xv.v[j][7];
+    }
+    out[i] = acc;
   }
-  return wave_sum(acc);
-}
-
-// Same as dot_row, with the lane's inputs read from LDS block by block (single-row phases).
-template <int NL>
-__device__ __forceinline__ float dot_row_lds(const Row<NL>& r, const float* x, int k, int lane) {
-  float acc = 0.f;
-#pragma unroll
-  for (int j = 0; j < NL; ++j) {
-    const int m = block_lanes(k, j);
-    float xv[8];
-#pragma unroll
-    for (int q = 0; q < 8; ++q) xv[q] = (lane < m) ? x[512 * j + q * m + lane] : 0.f;
-    const uint4 w = r.v[j];
-    acc += bf_lo(w.x) * xv[0];
-    acc += bf_hi(w.x) * xv[1];
-    acc += bf_lo(w.y) * xv[2];
-    acc += bf_hi(w.y) * xv[3];
-    acc += bf_lo(w.z) * xv[4];
-    acc += bf_hi(w.z) * xv[5];
-    acc += bf_lo(w.w) * xv[6];
-    acc += bf_hi(w.w) * xv[7];
-  }
-  return wave_sum(acc);
+  wave_sum_n<R>(out);
 }
 
 __device__ __forceinline__ void split(int total, int parts, int idx, int& lo, int& hi) {
@@ -403,510 +452,407 @@ __device__ __forceinline__ uint64_t argmax_key(float v, int idx) {
   return (uint64_t(u) << 32) | uint64_t(0xffffffffu - uint32_t(idx));
 }
 
-// ---------------------------------------------------------------- kernel
-// Workgroup = 4 compute waves + 1 exchange wave.
-//   compute waves: own fixed output rows of every projection; the weights of a phase for
-//     layer l+1 are loaded into registers right after the phase of layer l used them, so
-//     weight streaming runs a whole layer ahead of the dependency chain.
-//   exchange wave: waits for the inputs of the next phase (tagged words), keeps the
-//     residual stream h in its registers, applies the residual adds and RMSNorms, and
-//     writes the next phase's input vector into one of two LDS buffers (alternating).
-// Phases per layer (all waves meet at a workgroup barrier between phases):
-//   B0: x0 = rmsnorm1(h)         | compute: QKV rows (+RoPE, KV write)   | exch: q/k/v of the head group (attention WGs)
-//   B1:                          | compute: attention chunk (attention WGs) | exch: merge (merger WGs), attn -> x1
-//   B2: x1 = attention output    | compute: O rows -> hd1                | exch: h += hd1, x0 = rmsnorm2(h)
-//   B3: x0                       | compute: gate/up rows -> act          | exch: act -> x1
-//   B4: x1 = act                 | compute: down rows -> hd2             | exch: h += hd2, x0 = rmsnorm1'(h)
-constexpr int kThreadsWG = (kWavesC + kWavesX) * 64;
-
-// Shared per-step quantities of one workgroup.
-struct Ctx {
-  int G, wg, lane, wv;
-  int H, KV, GQ, ff, L, nch, npart, nqkv;
-  int pos;
-  uint32_t tag;
-  bool att, merger;
-  int ag, ac, q0, q1, P, ncached;
-  float* sh_x0;
-  float* sh_x1;
-  float* sh_k;
-  float* sh_v;
-  float* sh_q;
-  float* sh_e;
-  float* sh_red;
-  int* sh_sync;
-  // mailbox from compute waves to the publishing exchange wave
-  float* mb_val;   // kWavesC * kMbox values
-  int* mb_idx;     // word index in the layer's exchange words, -1 = unused
-  int* mb_out;     // compute waves: outputs written (bumped once per wave and phase)
-  int* mb_pub;     // exchange wave 0: outputs published (bumped once per phase)
-};
-
-constexpr int kMbox = 4;   // outputs per compute wave and phase
-
 __device__ __forceinline__ uint64_t* layer_x(const Args& a, int l) { return a.xw + int64_t(l) * a.lay.x_layer; }
 __device__ __forceinline__ const uint16_t* layer_w(const Args& a, int l) { return a.w + int64_t(l) * a.lay.layer_elems; }
 __device__ __forceinline__ uint16_t* layer_k(const Args& a, int l) { return a.kv + int64_t(l) * 2 * a.KV * a.ctx * kDh; }
 
-// ---------------------------------------------------------------- exchange waves
-// kWavesX waves.  Per phase they first publish this workgroup's outputs (exchange wave 0
-// takes them from the compute waves' LDS mailbox, stores the tagged words, then raises the
-// workgroup's flag), then wait for the producer flags of the next input and gather it in
-// parallel (gather_x).  They keep the residual stream h (element xidx(k, ew, lane)) and
-// apply the residual adds and the RMSNorms.
-template <int D>
-__device__ void exchange_role(const Args& a, const Ctx& c, int token) {
-  constexpr int HPW = D / (64 * kWavesX);   // residual elements per lane of each exchange wave
-  const int lane = c.lane, ew = c.wv - kWavesC;
-  const int G = c.G;
-  bool bad = false;
-  int sphase = 0, pphase = 0, aphase = 0;
-  float* ss_slot = c.sh_red + 32;           // per-wave partial sums of squares
-  float h[HPW];
-  float sc[HPW];                            // prefetched RMSNorm scale
-#pragma unroll
-  for (int k = 0; k < HPW; ++k) h[k] = bf2f(a.emb[int64_t(token) * D + xidx(k, ew, lane)]);
-  auto flagp = [&](int l, int ex) { return a.flags + (int64_t(l) * kNumEx + ex) * G; };
-  auto load_scale = [&](const uint16_t* scale) {
-#pragma unroll
-    for (int k = 0; k < HPW; ++k) sc[k] = bf2f(scale[xidx(k, ew, lane)]);
-  };
-  // x = scale * (h / sqrt(mean(h^2) + eps)) into LDS (model.py:94-98)
-  auto norm_to = [&](float* x) {
-    float ss = 0.f;
-#pragma unroll
-    for (int k = 0; k < HPW; ++k) ss += h[k] * h[k];
-    ss = wave_sum(ss);
-    const int slot = (sphase / kWavesX) % 2;
-    if (lane == 0) ss_slot[slot * kWavesX + ew] = ss;
-    xsync(c.sh_sync, sphase, lane);
-    float tot = 0.f;
-#pragma unroll
-    for (int w = 0; w < kWavesX; ++w) tot += ss_slot[slot * kWavesX + w];
-    const float r = sqrtf(tot / float(D) + 1e-5f);
-#pragma unroll
-    for (int k = 0; k < HPW; ++k) x[xidx(k, ew, lane)] = sc[k] * (h[k] / r);
-  };
-  auto add_h = [&](const uint64_t* src) {
-    uint64_t wd[HPW];
-#pragma unroll
-    for (int k = 0; k < HPW; ++k) wd[k] = ld_tag(src + xidx(k, ew, lane));
-    uint32_t spins = 0;
-    while (!bad) {
-      bool ok = true;
-#pragma unroll
-      for (int k = 0; k < HPW; ++k) {
-        if (uint32_t(wd[k] >> 32) != c.tag) {
-          ok = false;
-          wd[k] = ld_tag(src + xidx(k, ew, lane));
-        }
-      }
-      if (__all(ok)) break;
-      ++spins;
-      if ((spins & 255u) == 0 && (ld_status(a.ctrl) & kStatusTimeout)) bad = true;
-      if (spins > kSpinLimit) {
-        if (lane == 0) atomicOr(a.ctrl, kStatusTimeout);
-        bad = true;
-      }
+// ---------------------------------------------------------------- row workgroups
+// Shared state of a row workgroup (LDS pointers, row ranges).
+struct RowCtx {
+  int wr, lane, wv;
+  uint32_t tag;
+  int qp0, qp1, or0, or1, f0, f1, v0, v1;   // QKV pairs, O/down rows, gate/up pairs, vocabulary rows
+  int nlog;                                 // logit chunks
+  uint8_t* ring;
+  float* hres;    // residual stream h, two buffers (written alternately by compute wave 0)
+  float* xatt;    // attention vector (input of the O rows)
+  float* xhd1;    // O output (gathered)
+  float* xact;    // SwiGLU activation (input of the down rows)
+  float* xhd2;    // down output (gathered)
+  float* xa;      // gathered attention partials
+  int* ctr;       // [0] exchange-wave sync, [1] inputs ready, [2] outputs stored (compute
+                  // wave bumps), [4] ring jobs consumed, [5] ring jobs loaded, [6] compute-wave sync
+  float* red_v;   // argmax per compute wave
+  int* red_i;
+};
+enum { kCtrXs = 0, kCtrReady = 1, kCtrStored = 2, kCtrUsed = 4, kCtrLoaded = 5, kCtrCs = 6 };
+
+// Loader wave of a row workgroup.  Jobs in order: per layer the QKV, O, gate/up and down
+// rows of this workgroup (into their fixed ring regions), then the logit rows in chunks
+// alternating between the two ring halves.  Job j may overwrite its region once the job
+// that last used it has been consumed by all compute waves.
+template <int D, int FF>
+__device__ void row_loader(const Args& a, const RowCtx& c) {
+  const Layout& lay = a.lay;
+  const int lane = c.lane;
+  Dma d;
+  const int half = a.ring_bytes / 2;
+  const int njobs = 4 * a.L + c.nlog;
+  for (int j = 0; j < njobs; ++j) {
+    const uint16_t* src;
+    int64_t bytes;
+    int off, need;
+    if (j < 4 * a.L) {
+      const int l = j / 4, p = j % 4;
+      const uint16_t* w = layer_w(a, l);
+      if (p == 0) { src = w + lay.off_qkv + int64_t(2 * c.qp0) * D; bytes = int64_t(2 * (c.qp1 - c.qp0)) * D * 2; off = a.ring_q; }
+      else if (p == 1) { src = w + lay.off_o + int64_t(c.or0) * D; bytes = int64_t(c.or1 - c.or0) * D * 2; off = a.ring_o; }
+      else if (p == 2) { src = w + lay.off_gu + int64_t(2 * c.f0) * D; bytes = int64_t(2 * (c.f1 - c.f0)) * D * 2; off = a.ring_g; }
+      else { src = w + lay.off_dn + int64_t(c.or0) * FF; bytes = int64_t(c.or1 - c.or0) * FF * 2; off = a.ring_d; }
+      need = l == 0 ? 0 : j - 3;   // job j - 4 (same region, previous layer) consumed
+    } else {
+      const int k = j - 4 * a.L;
+      const int r0 = c.v0 + k * a.log_rows;
+      const int r1 = min(c.v1, r0 + a.log_rows);
+      src = a.outp + int64_t(r0) * D;
+      bytes = int64_t(r1 - r0) * D * 2;
+      off = (k & 1) * half;
+      need = k < 2 ? 4 * a.L : 4 * a.L + k - 1;   // every layer job, or logit chunk k - 2
     }
-#pragma unroll
-    for (int k = 0; k < HPW; ++k) h[k] = h[k] + __uint_as_float(uint32_t(wd[k]));
-  };
-  // exchange wave 0: publish the compute waves' outputs of this phase, then the flag
-  auto publish = [&](uint64_t* X, uint32_t* flag, bool replicated) {
-    ++pphase;
-    if (ew != 0) return;
-    lds_wait(c.mb_out, kWavesC * pphase);
-    constexpr int E = kWavesC * kMbox;   // mailbox entries; 64 / E replicas per pass
-    const int e = lane % E;
-    const int idx = c.mb_idx[e];
-    const float v = c.mb_val[e];
-    if (replicated) {
-      for (int r = lane / E; r < kRep; r += 64 / E)
-        if (idx >= 0) st_tag(X + idx + r * a.lay.x_rep, v, c.tag);
-    } else if (lane < E && idx >= 0) {
-      st_tag(X + idx, v, c.tag);
+    if (need > 0 && lds_ld(c.ctr + kCtrUsed) < kWavesC * need) {
+      d.drain();
+      lds_wait(c.ctr + kCtrUsed, kWavesC * need, a.ctrl);
     }
-    if (lane == 0) st_flag(flag, c.tag);
-    lds_bump(c.mb_pub, lane);
-  };
-  const int64_t myrep = int64_t(c.wg % kRep) * a.lay.x_rep;
-  load_scale(a.w + a.lay.off_ln1);
-  norm_to(c.sh_x0);
-  __syncthreads();
-  for (int l = 0; l < c.L; ++l) {
-    const Layout& lay = a.lay;
-    uint64_t* X = layer_x(a, l);
-    load_scale(layer_w(a, l) + lay.off_ln2);
-    // B0 .. B1: publish q/k/v rows; attention workgroups gather q of their head group and the new k, v
-    publish(X, flagp(l, kExQkv) + c.wg, false);
-    if (c.att) {
-      poll_flags(flagp(l, kExQkv), G, c.tag, a.ctrl, lane, bad);
-      gather_x(X + lay.x_qkv + int64_t(c.ag) * c.GQ * kDh, c.GQ * kDh, c.sh_q, c.tag, a.ctrl, ew, lane, bad);
-      if (c.pos >= c.q0 && c.pos < c.q1 && ew < 2) {   // current position: un-rounded K/V (multi_sm_decode.py:197,205)
-        const int prow = c.pos - c.q0;
-        const int hh = ew == 0 ? c.H + c.ag : c.H + c.KV + c.ag;
-        float* dst = ew == 0 ? c.sh_k + prow * kKPad : c.sh_v + prow * kDh;
-        uint64_t w = ld_tag(X + lay.x_qkv + int64_t(hh) * kDh + lane);
-        uint32_t spins = 0;
-        while (!bad && uint32_t(w >> 32) != c.tag) {
-          w = ld_tag(X + lay.x_qkv + int64_t(hh) * kDh + lane);
-          if (++spins > kSpinLimit) {
-            if (lane == 0) atomicOr(a.ctrl, kStatusTimeout);
-            bad = true;
-          }
-        }
-        dst[lane] = __uint_as_float(uint32_t(w));
-      }
-    }
-    MSD_TRACE_POINT(ew == 0, 0);
-    __syncthreads();  // B1
-    MSD_TRACE_POINT(ew == 0, 1);
-    // B1 .. B2: flag of this chunk's partials; merge the chunks of a KV head
-    // (multi_sm_decode.py:243-259); everyone gathers the attention vector -> x1
-    if (c.att) {
-      ++aphase;
-      if (ew == 0) {
-        lds_wait(c.mb_out + 2, kWavesC * aphase);   // the compute waves issued their partials
-        if (lane == 0) st_flag(flagp(l, kExPart) + c.wg, c.tag);
-      }
-    }
-    if (c.merger) {
-      poll_flags(flagp(l, kExPart) + c.ag * c.nch, c.nch, c.tag, a.ctrl, lane, bad);
-      gather_x(X + lay.x_part + int64_t(c.ag) * c.npart, c.npart, c.sh_x1, c.tag, a.ctrl, ew, lane, bad);
-      xsync(c.sh_sync, sphase, lane);
-      for (int n = ew; n < c.GQ; n += kWavesX) {
-        float M = -INFINITY;
-        for (int ch = 0; ch < c.nch; ++ch) {
-          const float* pc = c.sh_x1 + (ch * c.GQ + n) * kPartStride;
-          if (pc[1] > 0.f) M = fmaxf(M, pc[0]);
-        }
-        float num = 0.f, den = 0.f;
-        for (int ch = 0; ch < c.nch; ++ch) {
-          const float* pc = c.sh_x1 + (ch * c.GQ + n) * kPartStride;
-          if (pc[1] > 0.f) {
-            const float wgt = expf(pc[0] - M);
-            num += wgt * pc[2 + lane];
-            den += wgt * pc[1];
-          }
-        }
-        for (int r = 0; r < kRep; ++r)
-          st_tag(X + lay.x_attn + r * lay.x_rep + (c.ag * c.GQ + n) * kDh + lane, num / den, c.tag);
-      }
-      xsync(c.sh_sync, sphase, lane);   // every head's words are issued, the partials in x1 are no longer read
-      if (ew == 0 && lane == 0) st_flag(flagp(l, kExAttn) + c.ag, c.tag);
-      MSD_TRACE_POINT(ew == 0, 2);
-    }
-    poll_flags(flagp(l, kExAttn), c.KV, c.tag, a.ctrl, lane, bad);
-    gather_x(X + lay.x_attn + myrep, D, c.sh_x1, c.tag, a.ctrl, ew, lane, bad);
-    MSD_TRACE_POINT(ew == 0, 3);
-    __syncthreads();  // B2
-    MSD_TRACE_POINT(ew == 0, 4);
-    // B2 .. B3: publish O rows; h += O output, x0 = rmsnorm2(h)
-    publish(X, flagp(l, kExHd1) + c.wg, true);
-    poll_flags(flagp(l, kExHd1), G, c.tag, a.ctrl, lane, bad);
-    add_h(X + lay.x_hd1 + myrep);
-    MSD_TRACE_POINT(ew == 0, 5);
-    norm_to(c.sh_x0);
-    MSD_TRACE_POINT(ew == 0, 6);
-    load_scale(l + 1 < c.L ? layer_w(a, l + 1) + lay.off_ln1 : a.lnf);
-    __syncthreads();  // B3
-    MSD_TRACE_POINT(ew == 0, 7);
-    // B3 .. B4: publish gate/up outputs; act -> x1
-    publish(X, flagp(l, kExAct) + c.wg, true);
-    poll_flags(flagp(l, kExAct), G, c.tag, a.ctrl, lane, bad);
-    gather_x(X + lay.x_act + myrep, c.ff, c.sh_x1, c.tag, a.ctrl, ew, lane, bad);
-    MSD_TRACE_POINT(ew == 0, 8);
-    __syncthreads();  // B4
-    MSD_TRACE_POINT(ew == 0, 9);
-    // B4 .. B0': publish down rows; h += down output, x0 = rmsnorm1 of the next layer (or the final norm)
-    publish(X, flagp(l, kExHd2) + c.wg, true);
-    poll_flags(flagp(l, kExHd2), G, c.tag, a.ctrl, lane, bad);
-    add_h(X + lay.x_hd2 + myrep);
-    MSD_TRACE_POINT(ew == 0, 10);
-    norm_to(c.sh_x0);
-    __syncthreads();  // B0'
-    MSD_TRACE_POINT(ew == 0, 11);
+    if (bytes > 0) dma_copy(d, reinterpret_cast<const uint8_t*>(src), c.ring + off, bytes, lane);
+    d.drain();
+    lds_set(c.ctr + kCtrLoaded, j + 1, lane);
+    MSD_TRACE_POINT(j < 4 * a.L, j / 4, 28 + (j % 4));
   }
-  __syncthreads();  // logits done
 }
 
-// ---------------------------------------------------------------- compute waves
-template <int D, int FF, int FRW>
-__device__ void compute_role(const Args& a, const Ctx& c) {
+// Exchange waves of a row workgroup: per phase, once this workgroup's compute waves have
+// issued their stores (so those never queue behind the polls), they gather the phase's
+// vector (the outputs of every row workgroup) into its LDS buffer and signal the compute
+// waves.  Each buffer is rewritten only after every compute wave has stored the outputs of a
+// later phase, so no compute wave still reads it.
+template <int D, int FF>
+__device__ void row_exchange(const Args& a, const RowCtx& c) {
+  constexpr int HPW = D / (64 * kWavesX);                           // words per lane of a d-vector
+  constexpr int NKF = (FF + 64 * kWavesX - 1) / (64 * kWavesX);    // act words per lane
+  constexpr int H = D / kDh;
+  constexpr int NKA1 = (H * kPart + 64 * kWavesX - 1) / (64 * kWavesX);       // attention words, 1 split
+  constexpr int NKA2 = (2 * H * kPart + 64 * kWavesX - 1) / (64 * kWavesX);   // 2 splits
+  const int lane = c.lane, ew = c.wv - kWavesC;
+  const Layout& lay = a.lay;
+  bool bad = false;
+  int xs = 0, nst = 0;
+  const int64_t myrep = int64_t(c.wr % kRep) * lay.x_rep;
+  const int natt = a.H * a.nsplit;
+  auto wait_stored = [&]() {
+    ++nst;
+    lds_wait(c.ctr + kCtrStored, kWavesC * nst, a.ctrl);
+  };
+  for (int l = 0; l < a.L; ++l) {
+    uint64_t* X = layer_x(a, l);
+    // attention partials of every (head, split) -> attention vector (multi_sm_decode.py:243-259)
+    wait_stored();
+    MSD_TRACE_POINT(ew == 0, l, 0);
+    if (a.nsplit == 1)
+      gather_x<kWavesX, NKA1>(X + lay.x_att + myrep, natt * kPart, c.xa, c.tag, a.ctrl, ew, lane, bad);
+    else
+      gather_x<kWavesX, NKA2>(X + lay.x_att + myrep, natt * kPart, c.xa, c.tag, a.ctrl, ew, lane, bad);
+    wsync(c.ctr + kCtrXs, xs, kWavesX, lane, a.ctrl);
+    if (a.nsplit == 1) {
+      for (int i = ew * 64 + lane; i < D; i += kWavesX * 64) {
+        const float* ps = c.xa + (i / kDh) * kPart;
+        const float den = ps[1];
+        c.xatt[i] = den > 0.f ? ps[2 + i % kDh] / den : 0.f;
+      }
+    } else {
+      for (int i = ew * 64 + lane; i < D; i += kWavesX * 64) {
+        const int hd = i / kDh, dim = i % kDh;
+        float M = -INFINITY;
+        for (int s = 0; s < a.nsplit; ++s) {
+          const float* ps = c.xa + (hd * a.nsplit + s) * kPart;
+          if (ps[1] > 0.f) M = fmaxf(M, ps[0]);
+        }
+        float num = 0.f, den = 0.f;
+        for (int s = 0; s < a.nsplit; ++s) {
+          const float* ps = c.xa + (hd * a.nsplit + s) * kPart;
+          if (ps[1] > 0.f) {
+            const float wgt = expf(ps[0] - M);
+            num += wgt * ps[2 + dim];
+            den += wgt * ps[1];
+          }
+        }
+        c.xatt[i] = den > 0.f ? num / den : 0.f;
+      }
+    }
+    lds_bump(c.ctr + kCtrReady, lane);
+    MSD_TRACE_POINT(ew == 0, l, 1);
+    // O output
+    wait_stored();
+    gather_x<kWavesX, HPW>(X + lay.x_hd1 + myrep, D, c.xhd1, c.tag, a.ctrl, ew, lane, bad);
+    lds_bump(c.ctr + kCtrReady, lane);
+    MSD_TRACE_POINT(ew == 0, l, 2);
+    // SwiGLU activation
+    wait_stored();
+    gather_x<kWavesX, NKF>(X + lay.x_act + myrep, a.ff, c.xact, c.tag, a.ctrl, ew, lane, bad);
+    lds_bump(c.ctr + kCtrReady, lane);
+    MSD_TRACE_POINT(ew == 0, l, 5);
+    // down output
+    wait_stored();
+    gather_x<kWavesX, HPW>(X + lay.x_hd2 + myrep, D, c.xhd2, c.tag, a.ctrl, ew, lane, bad);
+    lds_bump(c.ctr + kCtrReady, lane);
+    MSD_TRACE_POINT(ew == 0, l, 6);
+  }
+}
+
+// Compute waves of a row workgroup.  Every compute wave keeps the residual stream h in
+// registers, in the lane layout of the row dot products (lane l holds elements
+// 512 j + k m + l), adds the gathered O and down outputs itself and takes the RMSNorms with a
+// wave reduction, so a norm needs no exchange between waves.  Per phase: wait for the input
+// vector and the ring job, take the dot products of this wave's rows (workgroup-local items
+// w, w + 4, ...; at most QPW QKV pairs, ORW O/down rows and GPW gate/up pairs per wave),
+// store the outputs to the exchange words and release the ring region.
+template <int D, int FF, int QPW, int ORW, int GPW>
+__device__ void row_compute(const Args& a, const RowCtx& c, int token) {
   constexpr int NLD = (D + 511) / 512;
-  constexpr int FFL = (FF + 511) / 512;
-  constexpr int ff = FF;
+  constexpr int NLF = (FF + 511) / 512;
   const int lane = c.lane, wv = c.wv;
   const Layout& lay = a.lay;
-  const int tidc = wv * 64 + lane;   // index among the compute threads
-  int qp0, qp1, or0, or1, f0, f1;
-  split(c.nqkv / 2, c.G, c.wg, qp0, qp1);
-  split(D, c.G, c.wg, or0, or1);
-  split(ff, c.G, c.wg, f0, f1);
-  const int myqp = qp0 + wv, myor = or0 + wv;
-  const bool has_qp = myqp < qp1, has_or = myor < or1;
-  const float* rope = a.rope + int64_t(c.pos) * kDh;
-  const int nkv16 = c.att ? c.ncached * 16 : 0;   // 16-byte pieces of cached K/V: 8 of K, 8 of V per row
-
-  // Weights are loaded one phase ahead: right after a phase's dot products, the rows of
-  // the next phase are requested, so the loads overlap the exchange that precedes it.
-  Row<NLD> qb0, qb1, ob, gbg[FRW], gbu[FRW];
-  Row<FFL> db;
-  uint4 kvr[4];
-  auto load_qkv = [&](int l) {
-    if (has_qp) {
-      load_row(qb0, layer_w(a, l) + lay.off_qkv + int64_t(2 * myqp) * D, D, lane);
-      load_row(qb1, layer_w(a, l) + lay.off_qkv + int64_t(2 * myqp + 1) * D, D, lane);
-    }
-    // cached K/V rows of this workgroup's attention chunk (rows < pos of layer l)
-    uint16_t* kc = layer_k(a, l);
-    uint16_t* vc = kc + int64_t(c.KV) * a.ctx * kDh;
+  const int nq = c.qp1 - c.qp0, no = c.or1 - c.or0, ng = c.f1 - c.f0;
+  // rotary factors of this wave's QKV pairs (q/k rows), loaded once
+  float cs[QPW], sn[QPW];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int t = tidc + j * (kWavesC * 64);
-      if (t < nkv16) {
-        const int prow = t >> 4, piece = t & 15;
-        const uint16_t* src = ((piece >= 8) ? vc : kc) + (int64_t(c.ag) * a.ctx + c.q0 + prow) * kDh + (piece & 7) * 8;
-        kvr[j] = *reinterpret_cast<const uint4*>(src);
+  for (int i = 0; i < QPW; ++i) {
+    cs[i] = 1.f;
+    sn[i] = 0.f;
+    const int rel = wv + kWavesC * i;
+    if (rel < nq) {
+      const int row = 2 * (c.qp0 + rel);
+      if (row / kDh < a.H + a.KV) {
+        const float* rope = a.rope + int64_t(a.pos) * kDh + (row % kDh) / 2;
+        cs[i] = rope[0];
+        sn[i] = rope[kDh / 2];
       }
     }
-  };
-  auto load_o = [&](int l) { if (has_or) load_row(ob, layer_w(a, l) + lay.off_o + int64_t(myor) * D, D, lane); };
-  auto load_gu = [&](int l) {
+  }
+  // residual stream and RMSNorm scales in the lane layout
+  auto load_vec = [&](XV<NLD>& v, const uint16_t* src) {
 #pragma unroll
-    for (int j = 0; j < FRW; ++j) {
-      const int f = f0 + wv * FRW + j;   // contiguous gate/up pairs per wave
-      if (f < f1) {
-        load_row(gbg[j], layer_w(a, l) + lay.off_gu + int64_t(2 * f) * D, D, lane);
-        load_row(gbu[j], layer_w(a, l) + lay.off_gu + int64_t(2 * f + 1) * D, D, lane);
-      }
+    for (int j = 0; j < NLD; ++j) {
+      const int m = block_lanes(D, j);
+#pragma unroll
+      for (int q = 0; q < 8; ++q) v.v[j][q] = (lane < m) ? bf2f(src[512 * j + q * m + lane]) : 0.f;
     }
   };
-  auto load_dn = [&](int l) { if (has_or) load_row(db, layer_w(a, l) + lay.off_dn + int64_t(myor) * ff, ff, lane); };
-
-  // Outputs go through the LDS mailbox to exchange wave 0, which stores them; the compute
-  // waves request the next phase's weights only after the outputs are published, so the
-  // latency-critical stores leave this CU ahead of the bulk loads.
-  int cphase = 0;
-  auto post = [&](int j, int idx, float v) {
-    if (lane == 0) {
-      c.mb_idx[wv * kMbox + j] = idx;
-      c.mb_val[wv * kMbox + j] = v;
+  XV<NLD> h, sc;
+  load_vec(h, a.emb + int64_t(token) * D);
+  load_vec(sc, layer_w(a, 0) + lay.off_ln1);
+  auto add_res = [&](const float* buf) {   // h += gathered output
+    XV<NLD> t;
+    load_x(t, buf, D, lane);
+#pragma unroll
+    for (int j = 0; j < NLD; ++j)
+#pragma unroll
+      for (int q = 0; q < 8; ++q) h.v[j][q] = h.v[j][q] + t.v[j][q];
+  };
+  auto norm = [&](XV<NLD>& x) {   // x = sc * (h / sqrt(mean(h^2) + eps)) (model.py:94-98)
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < NLD; ++j)
+#pragma unroll
+      for (int q = 0; q < 8; ++q) ss += h.v[j][q] * h.v[j][q];
+    ss = wave_sum(ss);
+    const float r = sqrtf(ss / float(D) + 1e-5f);
+#pragma unroll
+    for (int j = 0; j < NLD; ++j)
+#pragma unroll
+      for (int q = 0; q < 8; ++q) x.v[j][q] = sc.v[j][q] * (h.v[j][q] / r);
+  };
+  int nin = 0;
+  auto wait_in = [&](bool input, int job) {
+    if (input) {
+      ++nin;
+      lds_wait(c.ctr + kCtrReady, kWavesX * nin, a.ctrl);
     }
+    lds_wait(c.ctr + kCtrLoaded, job + 1, a.ctrl);
   };
-  auto handoff = [&]() {
-    ++cphase;
-    lds_bump(c.mb_out, lane);
-    lds_wait(c.mb_pub, cphase);
+  auto release = [&]() { lds_bump(c.ctr + kCtrUsed, lane); };
+  auto stored = [&]() { lds_bump(c.ctr + kCtrStored, lane); };
+  // LDS row of workgroup-local item rel (the region's first row when rel is past the end)
+  auto at = [&](int region, int rel, int n, int item_bytes) {
+    return c.ring + region + int64_t(rel < n ? rel : 0) * item_bytes;
+  };
+  auto count = [&](int n, int cap) {   // this wave's items among n (items w, w + 4, ...)
+    return n > wv ? min(cap, (n - wv + kWavesC - 1) / kWavesC) : 0;
   };
 
-  load_qkv(0);
-  __syncthreads();
-  for (int l = 0; l < c.L; ++l) {
+  for (int l = 0; l < a.L; ++l) {
     uint64_t* X = layer_x(a, l);
     uint16_t* kcache = layer_k(a, l);
-    uint16_t* vcache = kcache + int64_t(c.KV) * a.ctx * kDh;
-
-    // ---- B0 .. B1: QKV rows, RoPE, KV write (multi_sm_decode.py:121-180)
-    MSD_TRACE_POINT(wv == 0, 16);
-    // Stores share the in-order vmcnt counter with loads, so every phase computes its dot
-    // products first, then requests the next phase's weights, and publishes last: later
-    // waits for those weights never wait behind a store.
-    int i0 = 0, i1 = 0, head = 0;
-    float o0 = 0.f, o1 = 0.f;
-    if (has_qp) {
+    uint16_t* vcache = kcache + int64_t(a.KV) * a.ctx * kDh;
+    // ---- h += down output of the previous layer; x = rmsnorm1(h); QKV rows, RoPE, KV write
+    //      (multi_sm_decode.py:121-180)
+    wait_in(l > 0, 4 * l);
+    if (l > 0) add_res(c.xhd2);
+    MSD_TRACE_POINT(wv == 0, l, 16);
+    MSD_TRACE_CLOCK(wv == 0, l, 12);
+    {
       XV<NLD> xv;
-      load_x(xv, c.sh_x0, D, lane);
-      const float s0 = dot_row(qb0, xv);
-      const float s1 = dot_row(qb1, xv);
-      const int row = 2 * myqp;
-      head = row / kDh;
-      const int rr = row % kDh;
-      if (head < c.H + c.KV) {  // q or k rows (i, i+32): rotate-half RoPE (model.py:110-117)
-        const int i = rr / 2;
-        const float cs = rope[i], sn = rope[kDh / 2 + i];
-        o0 = s0 * cs - s1 * sn;
-        o1 = s0 * sn + s1 * cs;
-        i0 = head * kDh + i;
-        i1 = i0 + kDh / 2;
-      } else {
-        o0 = s0;
-        o1 = s1;
-        i0 = head * kDh + rr;
-        i1 = i0 + 1;
+      norm(xv);
+      const uint8_t* rows[2 * QPW];
+#pragma unroll
+      for (int i = 0; i < QPW; ++i) {
+        rows[2 * i] = at(a.ring_q, wv + kWavesC * i, nq, 2 * D * 2);
+        rows[2 * i + 1] = rows[2 * i] + D * 2;
       }
-    }
-    MSD_TRACE_POINT(wv == 0, 17);
-    post(0, has_qp ? int(lay.x_qkv) + i0 : -1, o0);
-    post(1, has_qp ? int(lay.x_qkv) + i1 : -1, o1);
+      float sd[2 * QPW];
+      dot_rows<NLD, 2 * QPW>(rows, xv, D, lane, sd);
+      release();
+      float y[2 * QPW];
+      int ix[2 * QPW];
 #pragma unroll
-    for (int j = 2; j < kMbox; ++j) post(j, -1, 0.f);
-    handoff();
-    load_o(l);
-    if (has_qp && lane == 0) {
-      if (head >= c.H) {  // K (post-RoPE) or V row of the cache at pos, bf16 (multi_sm_decode.py:179-180)
-        const bool isv = head >= c.H + c.KV;
-        const int kvh = isv ? head - c.H - c.KV : head - c.H;
-        uint16_t* cp = (isv ? vcache : kcache) + (int64_t(kvh) * a.ctx + c.pos) * kDh;
-        cp[i0 - head * kDh] = f2bf(o0);
-        cp[i1 - head * kDh] = f2bf(o1);
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int t = tidc + j * (kWavesC * 64);
-      if (t < nkv16) {   // K rows padded to kKPad floats (conflict-free 128-bit reads in the score loop)
-        const int prow = t >> 4, piece = t & 15;
-        float* dst = (piece >= 8) ? c.sh_v + prow * kDh + (piece & 7) * 8 : c.sh_k + prow * kKPad + (piece & 7) * 8;
-        const uint4 u = kvr[j];
-        dst[0] = bf_lo(u.x); dst[1] = bf_hi(u.x); dst[2] = bf_lo(u.y); dst[3] = bf_hi(u.y);
-        dst[4] = bf_lo(u.z); dst[5] = bf_hi(u.z); dst[6] = bf_lo(u.w); dst[7] = bf_hi(u.w);
-      }
-    }
-    __syncthreads();  // B1
-    MSD_TRACE_POINT(wv == 0, 18);
-
-    // ---- B1 .. B2: attention over this chunk, one head per compute wave (multi_sm_decode.py:182-221)
-    if (c.att) {
-      for (int n = wv; n < c.GQ; n += kWavesC) {
-        // scores: lane = position; q (same for every lane) in registers, the lane's K row
-        // read as 16 independent 128-bit LDS loads
-        const float4* q4 = reinterpret_cast<const float4*>(c.sh_q + n * kDh);
-        float s = -INFINITY;
-        if (lane < c.P) {
-          const float4* kr = reinterpret_cast<const float4*>(c.sh_k + lane * kKPad);
-          float4 kk[kDh / 4];
-#pragma unroll
-          for (int j = 0; j < kDh / 4; ++j) kk[j] = kr[j];
-          float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
-#pragma unroll
-          for (int j = 0; j < kDh / 4; ++j) {
-            const float4 qq = q4[j];
-            a0 += qq.x * kk[j].x;
-            a1 += qq.y * kk[j].y;
-            a2 += qq.z * kk[j].z;
-            a3 += qq.w * kk[j].w;
-          }
-          s = ((a0 + a1) + (a2 + a3)) * 0.125f;
+      for (int i = 0; i < QPW; ++i) {
+        const int rel = wv + kWavesC * i;
+        const int row = 2 * (c.qp0 + (rel < nq ? rel : 0));
+        const int head = row / kDh;
+        const int rr = row % kDh;
+        const float s0 = sd[2 * i], s1 = sd[2 * i + 1];
+        if (head < a.H + a.KV) {  // q or k rows (i, i+32): rotate-half RoPE (model.py:110-117)
+          y[2 * i] = s0 * cs[i] - s1 * sn[i];
+          y[2 * i + 1] = s0 * sn[i] + s1 * cs[i];
+          ix[2 * i] = head * kDh + rr / 2;
+          ix[2 * i + 1] = ix[2 * i] + kDh / 2;
+        } else {
+          y[2 * i] = s0;
+          y[2 * i + 1] = s1;
+          ix[2 * i] = head * kDh + rr;
+          ix[2 * i + 1] = ix[2 * i] + 1;
         }
-        const float m = wave_max(s);
-        const float e = (lane < c.P) ? expf(s - m) : 0.f;
-        const float lsum = wave_sum(e);
-        // o[lane = dim] = sum_p e[p] * V[p][lane]: V entries read 16 positions ahead, the
-        // weights e[p] taken from lane p as wave-uniform values
-        float o4[4] = {0.f, 0.f, 0.f, 0.f};
-        for (int p0 = 0; p0 < c.P; p0 += 16) {
-          float vv[16];
-#pragma unroll
-          for (int k = 0; k < 16; ++k) vv[k] = (p0 + k < c.P) ? c.sh_v[(p0 + k) * kDh + lane] : 0.f;
-#pragma unroll
-          for (int k = 0; k < 16; ++k) {
-            const float ek = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), p0 + k));
-            o4[k & 3] += ek * vv[k];
-          }
+        if (rel < nq && head >= a.H && lane == 0) {  // K (post-RoPE) or V row of the cache at pos, bf16 (multi_sm_decode.py:179-180)
+          const bool isv = head >= a.H + a.KV;
+          const int kvh = isv ? head - a.H - a.KV : head - a.H;
+          uint16_t* cp = (isv ? vcache : kcache) + (int64_t(kvh) * a.ctx + a.pos) * kDh;
+          cp[ix[2 * i] - head * kDh] = f2bf(y[2 * i]);
+          cp[ix[2 * i + 1] - head * kDh] = f2bf(y[2 * i + 1]);
         }
-        const float o = (o4[0] + o4[1]) + (o4[2] + o4[3]);
-        uint64_t* part = X + lay.x_part + (int64_t(c.ag * c.nch + c.ac) * c.GQ + n) * kPartStride;
-        if (lane == 0) {
-          st_tag(part + 0, c.P > 0 ? m : -INFINITY, c.tag);
-          st_tag(part + 1, lsum, c.tag);
-        }
-        st_tag(part + 2 + lane, o, c.tag);
-        __builtin_amdgcn_wave_barrier();
       }
-      lds_bump(c.mb_out + 2, lane);   // exchange wave 0 raises the chunk's flag after all heads
-      MSD_TRACE_POINT(wv == 0, 19);
+      store_out<2 * QPW>(X + lay.x_qkv, y, ix, 2 * count(nq, QPW), false, lay.x_rep, c.tag, lane);
+      stored();
+      load_vec(sc, layer_w(a, l) + lay.off_ln2);   // scale of the next norm
     }
-    __syncthreads();  // B2
-    MSD_TRACE_POINT(wv == 0, 20);
-
-    // ---- B2 .. B3: O rows (multi_sm_decode.py:223-232)
-    float yo = 0.f;
-    if (has_or) {
+    MSD_TRACE_POINT(wv == 0, l, 17);
+    // ---- O rows (multi_sm_decode.py:223-232)
+    wait_in(true, 4 * l + 1);
+    MSD_TRACE_POINT(wv == 0, l, 18);
+    {
       XV<NLD> xv;
-      load_x(xv, c.sh_x1, D, lane);
-      yo = dot_row(ob, xv);
-    }
-    MSD_TRACE_POINT(wv == 0, 21);
-    post(0, has_or ? int(lay.x_hd1) + myor : -1, yo);
+      load_x(xv, c.xatt, D, lane);
+      const uint8_t* rows[ORW];
+      int ix[ORW];
 #pragma unroll
-    for (int j = 1; j < kMbox; ++j) post(j, -1, 0.f);
-    handoff();
-    load_gu(l);
-    __syncthreads();  // B3
-    MSD_TRACE_POINT(wv == 0, 22);
-
-    // ---- B3 .. B4: gate/up rows + SwiGLU (multi_sm_decode.py:262-289, model.py:159)
-    XV<NLD> xg;
-    if (f0 + wv * FRW < f1) load_x(xg, c.sh_x0, D, lane);
-    float act[FRW];
-#pragma unroll
-    for (int j = 0; j < FRW; ++j) {
-      const int f = f0 + wv * FRW + j;   // contiguous gate/up pairs per wave
-      act[j] = 0.f;
-      if (f < f1) {
-        const float gt = dot_row(gbg[j], xg);
-        const float up = dot_row(gbu[j], xg);
-        act[j] = (gt * (1.f / (1.f + expf(-gt)))) * up;
+      for (int i = 0; i < ORW; ++i) {
+        rows[i] = at(a.ring_o, wv + kWavesC * i, no, D * 2);
+        ix[i] = int(lay.x_hd1) + c.or0 + wv + kWavesC * i;
       }
+      float y[ORW];
+      dot_rows<NLD, ORW>(rows, xv, D, lane, y);
+      release();
+      store_out<ORW>(X, y, ix, count(no, ORW), true, lay.x_rep, c.tag, lane);
+      stored();
     }
-    MSD_TRACE_POINT(wv == 0, 23);
+    MSD_TRACE_POINT(wv == 0, l, 19);
+    // ---- h += O output; x = rmsnorm2(h); gate/up rows + SwiGLU (multi_sm_decode.py:262-289, model.py:159)
+    wait_in(true, 4 * l + 2);
+    add_res(c.xhd1);
+    MSD_TRACE_POINT(wv == 0, l, 20);
+    {
+      XV<NLD> xv;
+      norm(xv);
+      const uint8_t* rows[2 * GPW];
+      int ix[GPW];
 #pragma unroll
-    for (int j = 0; j < kMbox; ++j) {
-      const int f = f0 + wv * FRW + j;   // contiguous gate/up pairs per wave
-      post(j, (j < FRW && f < f1) ? int(lay.x_act) + f : -1, j < FRW ? act[j < FRW ? j : 0] : 0.f);
+      for (int i = 0; i < GPW; ++i) {
+        rows[2 * i] = at(a.ring_g, wv + kWavesC * i, ng, 2 * D * 2);
+        rows[2 * i + 1] = rows[2 * i] + D * 2;
+        ix[i] = int(lay.x_act) + c.f0 + wv + kWavesC * i;
+      }
+      float gu[2 * GPW];
+      dot_rows<NLD, 2 * GPW>(rows, xv, D, lane, gu);
+      release();
+      float y[GPW];
+#pragma unroll
+      for (int i = 0; i < GPW; ++i) {
+        const float gt = gu[2 * i], up = gu[2 * i + 1];
+        y[i] = (gt * (1.f / (1.f + expf(-gt)))) * up;
+      }
+      store_out<GPW>(X, y, ix, count(ng, GPW), true, lay.x_rep, c.tag, lane);
+      stored();
     }
-    handoff();
-    load_dn(l);
-    __syncthreads();  // B4
-    MSD_TRACE_POINT(wv == 0, 24);
-
-    // ---- B4 .. B0': down rows (multi_sm_decode.py:273-291)
-    float yd = 0.f;
-    if (has_or) yd = dot_row_lds(db, c.sh_x1, ff, lane);
-    MSD_TRACE_POINT(wv == 0, 25);
-    post(0, has_or ? int(lay.x_hd2) + myor : -1, yd);
+    MSD_TRACE_POINT(wv == 0, l, 21);
+    // ---- down rows (multi_sm_decode.py:273-291)
+    wait_in(true, 4 * l + 3);
+    MSD_TRACE_POINT(wv == 0, l, 22);
+    {
+      XV<NLF> xv;
+      load_x(xv, c.xact, FF, lane);
+      const uint8_t* rows[ORW];
+      int ix[ORW];
 #pragma unroll
-    for (int j = 1; j < kMbox; ++j) post(j, -1, 0.f);
-    handoff();
-    if (l + 1 < c.L) load_qkv(l + 1);
-    __syncthreads();  // B0'
-    MSD_TRACE_POINT(wv == 0, 26);
+      for (int i = 0; i < ORW; ++i) {
+        rows[i] = at(a.ring_d, wv + kWavesC * i, no, FF * 2);
+        ix[i] = int(lay.x_hd2) + c.or0 + wv + kWavesC * i;
+      }
+      float y[ORW];
+      dot_rows<NLF, ORW>(rows, xv, FF, lane, y);
+      release();
+      store_out<ORW>(X, y, ix, count(no, ORW), true, lay.x_rep, c.tag, lane);
+      stored();
+    }
+    load_vec(sc, l + 1 < a.L ? layer_w(a, l + 1) + lay.off_ln1 : a.lnf);   // scale of the next norm
+    MSD_TRACE_POINT(wv == 0, l, 23);
+    MSD_TRACE_CLOCK(wv == 0, l, 13);
   }
-  // ---- tied logits over this workgroup's vocabulary rows (multi_sm_decode.py:314-337)
-  int v0, v1;
-  split(a.V, c.G, c.wg, v0, v1);
+  // ---- h += last down output; x = final rmsnorm(h); tied logits over this workgroup's
+  //      vocabulary rows (multi_sm_decode.py:314-337)
+  ++nin;
+  lds_wait(c.ctr + kCtrReady, kWavesX * nin, a.ctrl);
+  add_res(c.xhd2);
+  XV<NLD> xv;
+  norm(xv);
   float best = -INFINITY;
   int besti = 0x7fffffff;
-  constexpr int B = 4;
-  XV<NLD> xv;
-  load_x(xv, c.sh_x0, D, lane);
-  for (int base = v0 + wv * B; base < v1; base += kWavesC * B) {
-    Row<NLD> rr[B];
+  const int half = a.ring_bytes / 2;
+  constexpr int RB = 4;   // rows per batch of LDS reads
+  for (int k = 0; k < c.nlog; ++k) {
+    lds_wait(c.ctr + kCtrLoaded, 4 * a.L + k + 1, a.ctrl);
+    const int r0 = c.v0 + k * a.log_rows;
+    const int n = min(c.v1, r0 + a.log_rows) - r0;
+    const uint8_t* base = c.ring + (k & 1) * half;
+    for (int b = wv; b < n; b += kWavesC * RB) {
+      const uint8_t* rows[RB];
 #pragma unroll
-    for (int j = 0; j < B; ++j)
-      if (base + j < v1) load_row(rr[j], a.outp + int64_t(base + j) * D, D, lane);
+      for (int i = 0; i < RB; ++i) {
+        const int rel = b + kWavesC * i;
+        rows[i] = base + int64_t(rel < n ? rel : 0) * D * 2;
+      }
+      float y[RB];
+      dot_rows<NLD, RB>(rows, xv, D, lane, y);
 #pragma unroll
-    for (int j = 0; j < B; ++j) {
-      if (base + j < v1) {
-        const float y = dot_row(rr[j], xv);
-        if (lane == 0) a.logits[base + j] = y;
-        if (y > best) { best = y; besti = base + j; }
+      for (int i = 0; i < RB; ++i) {
+        const int rel = b + kWavesC * i;
+        if (rel < n) {
+          if (lane == 0) a.logits[r0 + rel] = y[i];
+          if (y[i] > best) { best = y[i]; besti = r0 + rel; }
+        }
       }
     }
+    release();
   }
   if (lane == 0) {
-    c.sh_red[wv] = best;
-    reinterpret_cast<int*>(c.sh_red)[8 + wv] = besti;
+    c.red_v[wv] = best;
+    c.red_i[wv] = besti;
   }
-  __syncthreads();  // logits done
+  int cs_ = 0;
+  wsync(c.ctr + kCtrCs, cs_, kWavesC, lane, a.ctrl);
   if (wv == 0 && lane == 0) {   // argmax: larger value wins, ties -> lower index (np.argmax)
-    float bv = c.sh_red[0];
-    int bi = reinterpret_cast<int*>(c.sh_red)[8];
+    float bv = c.red_v[0];
+    int bi = c.red_i[0];
     for (int w = 1; w < kWavesC; ++w) {
-      const float v = c.sh_red[w];
-      const int i = reinterpret_cast<int*>(c.sh_red)[8 + w];
+      const float v = c.red_v[w];
+      const int i = c.red_i[w];
       if (v > bv || (v == bv && i < bi)) { bv = v; bi = i; }
     }
     uint64_t* keyp = reinterpret_cast<uint64_t*>(a.ctrl + 2);
@@ -915,7 +861,7 @@ __device__ void compute_role(const Args& a, const Ctx& c) {
     // the max above completes before the arrival below is issued
     __builtin_amdgcn_s_waitcnt(0);
     const uint32_t old = __hip_atomic_fetch_add(a.ctrl + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if ((old % uint32_t(c.G)) == uint32_t(c.G - 1)) {   // last arriver publishes the token
+    if ((old % uint32_t(a.GR)) == uint32_t(a.GR - 1)) {   // last arriver publishes the token
       const uint64_t key = __hip_atomic_load(keyp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       a.next_token[0] = int32_t(0xffffffffu - uint32_t(key & 0xffffffffu));
       a.next_token[1] = int32_t(ld_status(a.ctrl));
@@ -924,70 +870,241 @@ __device__ void compute_role(const Args& a, const Ctx& c) {
   }
 }
 
-template <int D, int FF, int FRW>
-__global__ __launch_bounds__(kThreadsWG, 1) void decode_step_kernel(Args a) {
-  extern __shared__ float smem[];
-  Ctx c;
-  c.G = gridDim.x;
-  c.wg = blockIdx.x;
-  c.lane = threadIdx.x & 63;
-  c.wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform (scalar register)
-  c.H = a.H;
-  c.KV = a.KV;
-  c.GQ = a.H / a.KV;
-  c.ff = a.ff;
-  c.L = a.L;
-  c.nch = a.nch;
-  c.npart = c.nch * c.GQ * kPartStride;
-  c.nqkv = (a.H + 2 * a.KV) * kDh;
-  c.pos = a.pos;
-  c.tag = a.epoch;
-  const int ch_max = (a.ctx + c.nch - 1) / c.nch;
-  // attention: workgroup i < KV*nch handles KV head i / nch, position chunk i % nch
-  c.att = c.wg < c.KV * c.nch;
-  c.ag = c.wg / c.nch;
-  c.ac = c.wg % c.nch;
-  c.merger = c.att && c.ac == 0;
-  const int npos = c.pos + 1;
-  const int cs = (npos + c.nch - 1) / c.nch;
-  c.q0 = min(c.ac * cs, npos);
-  c.q1 = min(c.q0 + cs, npos);
-  c.P = c.q1 - c.q0;
-  c.ncached = max(0, min(c.q1, c.pos) - c.q0);
-  const int xmax = (max(max(D, c.ff), c.npart) + 3) & ~3;   // keeps sh_k 16-byte aligned
-  c.sh_x0 = smem;
-  c.sh_x1 = c.sh_x0 + D;
-  c.sh_k = c.sh_x1 + xmax;
-  c.sh_v = c.sh_k + ch_max * kKPad;
-  c.sh_q = c.sh_v + ch_max * kDh;
-  c.sh_e = c.sh_q + c.GQ * kDh;
-  c.sh_red = c.sh_e + kWavesC * 64;
-  c.sh_sync = reinterpret_cast<int*>(c.sh_red + 64);
-  c.mb_val = c.sh_red + 64 + 4;
-  c.mb_idx = reinterpret_cast<int*>(c.mb_val + kWavesC * kMbox);
-  c.mb_out = c.mb_idx + kWavesC * kMbox;   // [0] outputs written, [2] attention partials issued
-  c.mb_pub = c.mb_out + 1;
-  if (threadIdx.x == 0) {
-    *c.sh_sync = 0;
-    c.mb_out[0] = 0;
-    c.mb_out[1] = 0;
-    c.mb_out[2] = 0;
+// ---------------------------------------------------------------- attention workgroups
+// One query head h and one split s of the context: cached positions [lo, lo + cap) below
+// pos, plus the current position when it falls in the split (multi_sm_decode.py:182-221).
+struct AttCtx {
+  int h, g, lo, ncached, lane, wv;
+  bool has_cur;
+  uint32_t tag;
+  int64_t part;     // word offset of this (head, split) in the attention partials
+  uint8_t* K;       // cap rows of kKRowB bytes (bf16 K, post-RoPE)
+  uint8_t* V;       // cap rows of kVRowB bytes
+  float* sq;        // [2][3][64]: q, new k, new v (double-buffered by layer parity)
+  float* ow;        // [kWavesA][64] partial outputs
+  float* mw;        // [kWavesA] partial maxima
+  float* lw;        // [kWavesA] partial sums
+  int* ctr;         // [0] wave sync, [1] KV layers loaded, [2] KV layers consumed (wave bumps)
+};
+
+// Loader wave of an attention workgroup: per layer, once every attention wave has
+// finished with the previous layer's rows, DMA this split's cached K rows (9 slots of
+// 16 bytes per row; the 9th is padding) and V rows (8 slots) into LDS.
+__device__ void att_loader(const Args& a, const AttCtx& c) {
+  const int lane = c.lane;
+  Dma d;
+  for (int l = 0; l < a.L; ++l) {
+    if (l > 0) lds_wait(c.ctr + 2, kWavesA * l, a.ctrl);
+    if (c.ncached > 0) {
+      const uint16_t* kc = layer_k(a, l) + (int64_t(c.g) * a.ctx + c.lo) * kDh;
+      const uint16_t* vc = kc + int64_t(a.KV) * a.ctx * kDh;
+      const int nk = cdiv(c.ncached * 9, 64);
+      for (int t = 0; t < nk; ++t) {
+        const int i = 64 * t + lane;
+        const int r = min(i / 9, c.ncached - 1), p = min(i % 9, 7);
+        d.issue(kc + r * kDh + p * 8, c.K + t * 1024);
+      }
+      const int nv = cdiv(c.ncached, 8);
+      for (int t = 0; t < nv; ++t) {
+        const int i = 64 * t + lane;
+        const int r = min(i / 8, c.ncached - 1), p = i % 8;
+        d.issue(vc + r * kDh + p * 8, c.V + t * 1024);
+      }
+    }
+    d.drain();
+    lds_set(c.ctr + 1, l + 1, lane);
+    MSD_TRACE_POINT(true, l, 28);
   }
-  __syncthreads();
+}
+
+__device__ void att_waves(const Args& a, const AttCtx& c) {
+  const int lane = c.lane, wv = c.wv;
+  const Layout& lay = a.lay;
+  bool bad = false;
+  int ws = 0;
+  for (int l = 0; l < a.L; ++l) {
+    uint64_t* X = layer_x(a, l);
+    float* sq = c.sq + (l & 1) * 3 * kDh;
+    // q of the head, new k and v of its KV head (waves 0..2), un-rounded (multi_sm_decode.py:197,205)
+    if (wv < 3) {
+      const int idx = wv == 0 ? c.h * kDh : (wv == 1 ? (a.H + c.g) * kDh : (a.H + a.KV + c.g) * kDh);
+      float v[1];
+      poll_words<1, 1>(X + lay.x_qkv + idx, kDh, c.tag, v, a.ctrl, 0, lane, bad);
+      sq[wv * kDh + lane] = v[0];
+    }
+    wsync(c.ctr, ws, kWavesA, lane, a.ctrl);
+    MSD_TRACE_POINT(wv == 0, l, 24);
+    lds_wait(c.ctr + 1, l + 1, a.ctrl);   // cached rows of layer l are in LDS
+    MSD_TRACE_POINT(wv == 0, l, 25);
+    // block wv: cached rows [bs wv, bs wv + bs), bs a multiple of 16 (at most 64) that
+    // spreads the cached rows over all attention waves
+    const int bs = min(64, max(16, (cdiv(c.ncached, kWavesA) + 15) & ~15));
+    float m = -INFINITY, lsum = 0.f, o = 0.f;
+    const int r0 = wv * bs;
+    if (r0 < c.ncached) {
+      const int np = min(bs, c.ncached - r0);
+      // scores: lane = position (rows past np re-read row np - 1 and are masked), q
+      // wave-uniform from LDS
+      const uint8_t* kr = c.K + (r0 + min(lane, np - 1)) * kKRowB;
+      const float4* q4 = reinterpret_cast<const float4*>(sq);
+      uint4 kk[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) kk[j] = *reinterpret_cast<const uint4*>(kr + 16 * j);
+      float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float4 qa = q4[2 * j], qb = q4[2 * j + 1];
+        a0 += qa.x * bf_lo(kk[j].x);
+        a1 += qa.y * bf_hi(kk[j].x);
+        a2 += qa.z * bf_lo(kk[j].y);
+        a3 += qa.w * bf_hi(kk[j].y);
+        a0 += qb.x * bf_lo(kk[j].z);
+        a1 += qb.y * bf_hi(kk[j].z);
+        a2 += qb.z * bf_lo(kk[j].w);
+        a3 += qb.w * bf_hi(kk[j].w);
+      }
+      const float s = lane < np ? ((a0 + a1) + (a2 + a3)) * 0.125f : -INFINITY;
+      m = wave_max(s);
+      const float e = (lane < np) ? expf(s - m) : 0.f;
+      lsum = wave_sum(e);
+      // o[lane = dim] = sum_p e[p] * V[p][dim]: 16 positions per batch of LDS reads (rows
+      // past np re-read row np - 1; their weights e are 0), e[p] taken from lane p
+      const uint16_t* vr = reinterpret_cast<const uint16_t*>(c.V + r0 * kVRowB) + lane;
+      float o4[4] = {0.f, 0.f, 0.f, 0.f};
+      for (int p0 = 0; p0 < np; p0 += 16) {
+        float vv[16];
+#pragma unroll
+        for (int k = 0; k < 16; ++k) vv[k] = bf2f(vr[min(p0 + k, np - 1) * kDh]);
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+          const float ek = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), p0 + k));
+          o4[k & 3] += ek * vv[k];
+        }
+      }
+      o = (o4[0] + o4[1]) + (o4[2] + o4[3]);
+    }
+    lds_bump(c.ctr + 2, lane);   // this wave is done with the cached rows of layer l
+    c.ow[wv * kDh + lane] = o;
+    if (lane == 0) {
+      c.mw[wv] = m;
+      c.lw[wv] = lsum;
+    }
+    wsync(c.ctr, ws, kWavesA, lane, a.ctrl);
+    MSD_TRACE_POINT(wv == 0, l, 26);
+    {   // merge the blocks and the current position (log-sum-exp); every wave computes the
+        // result and stores one replica
+      float mv[kWavesA], lv[kWavesA], ov[kWavesA];
+#pragma unroll
+      for (int w = 0; w < kWavesA; ++w) {
+        mv[w] = c.mw[w];
+        lv[w] = c.lw[w];
+        ov[w] = c.ow[w * kDh + lane];
+      }
+      const float scur = c.has_cur ? wave_sum(sq[lane] * sq[kDh + lane]) * 0.125f : -INFINITY;
+      float M = scur;
+#pragma unroll
+      for (int w = 0; w < kWavesA; ++w) M = lv[w] > 0.f ? fmaxf(M, mv[w]) : M;
+      float Ls = 0.f, O = 0.f;
+      if (M != -INFINITY) {
+#pragma unroll
+        for (int w = 0; w < kWavesA; ++w) {
+          const float f = lv[w] > 0.f ? expf(mv[w] - M) : 0.f;
+          Ls += f * lv[w];
+          O += f * ov[w];
+        }
+        if (c.has_cur) {
+          const float f = expf(scur - M);
+          Ls += f;
+          O += f * sq[2 * kDh + lane];
+        }
+      }
+      uint64_t* dst = X + lay.x_att + c.part + wv * lay.x_rep;   // replica wv (kWavesA == kRep)
+      st_tag(dst + 2 + lane, O, c.tag);
+      if (lane < 2) st_tag(dst + lane, lane == 0 ? M : Ls, c.tag);
+      MSD_TRACE_POINT(wv == 0, l, 27);
+    }
+  }
+}
+
+// ---------------------------------------------------------------- kernel
+template <int D, int FF, int QPW, int ORW, int GPW>
+__global__ __launch_bounds__(kThreadsWG, 1) void decode_step_kernel(Args a) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform
+  const int wg = blockIdx.x;
+  const uint32_t tag = a.epoch;
+
+  if (wg >= a.GR) {   // ------------------------------------------ attention workgroup
+    const int i = wg - a.GR;
+    // heads of one KV group on as few XCDs as possible (workgroup w runs on XCD w % 8)
+    int item = i;
+    if (a.NA % 8 == 0 && a.GR % 8 == 0) item = (i % 8) * (a.NA / 8) + i / 8;
+    AttCtx c;
+    c.h = item / a.nsplit;
+    const int s = item % a.nsplit;
+    c.g = c.h / (a.H / a.KV);
+    c.lo = s * a.cap;
+    c.ncached = max(0, min(a.pos, c.lo + a.cap) - c.lo);
+    c.has_cur = a.pos >= c.lo && a.pos < c.lo + a.cap;
+    c.lane = lane;
+    c.wv = wv;
+    c.tag = tag;
+    c.part = int64_t(item) * kPart;
+    c.K = smem;
+    c.V = c.K + cdiv(a.cap * 9, 64) * 1024;
+    c.sq = reinterpret_cast<float*>(c.V + cdiv(a.cap, 8) * 1024);
+    c.ow = c.sq + 2 * 3 * kDh;
+    c.mw = c.ow + kWavesA * kDh;
+    c.lw = c.mw + kWavesA;
+    c.ctr = reinterpret_cast<int*>(c.lw + kWavesA);
+    if (threadIdx.x < 4) c.ctr[threadIdx.x] = 0;
+    __syncthreads();   // the only workgroup barrier; the roles below meet on LDS counters
+    if (wv == kLoader) att_loader(a, c);
+    else att_waves(a, c);
+    return;
+  }
+
+  // --------------------------------------------------------------- row workgroup
+  RowCtx c;
+  c.wr = wg;
+  c.lane = lane;
+  c.wv = wv;
+  c.tag = tag;
+  const int nqkv = (a.H + 2 * a.KV) * kDh;
+  split(nqkv / 2, a.GR, wg, c.qp0, c.qp1);
+  split(D, a.GR, wg, c.or0, c.or1);
+  split(a.ff, a.GR, wg, c.f0, c.f1);
+  split(a.V, a.GR, wg, c.v0, c.v1);
+  c.nlog = cdiv(c.v1 - c.v0, a.log_rows);
+  c.ring = smem;
+  c.hres = reinterpret_cast<float*>(smem + a.ring_bytes);
+  c.xatt = c.hres + 2 * D;
+  c.xhd1 = c.xatt + D;
+  c.xhd2 = c.xhd1 + D;
+  c.xact = c.xhd2 + D;
+  c.xa = c.xact + ((FF + 3) & ~3);
+  c.ctr = reinterpret_cast<int*>(c.xa + ((a.H * a.nsplit * kPart + 3) & ~3));
+  c.red_v = reinterpret_cast<float*>(c.ctr + 8);
+  c.red_i = reinterpret_cast<int*>(c.red_v + kWavesC);
+  if (threadIdx.x < 8) c.ctr[threadIdx.x] = 0;
+  __syncthreads();   // the only workgroup barrier; the roles below meet on LDS counters
 
   int token = a.token_dev ? *a.token_dev : a.token;
   if (token < 0 || token >= a.V) {
-    if (c.wg == 0 && threadIdx.x == 0) atomicOr(a.ctrl, kStatusBadToken);
+    if (wg == 0 && threadIdx.x == 0) atomicOr(a.ctrl, kStatusBadToken);
     token = token < 0 ? 0 : a.V - 1;
   }
-  if (c.wv >= kWavesC) exchange_role<D>(a, c, token);
-  else compute_role<D, FF, FRW>(a, c);
+  if (wv == kLoader) row_loader<D, FF>(a, c);
+  else if (wv >= kWavesC) row_exchange<D, FF>(a, c);
+  else row_compute<D, FF, QPW, ORW, GPW>(a, c, token);
 }
 
 // ---------------------------------------------------------------- host side
 struct Plan {   // per-config launch parameters
-  int frw;      // gate/up rows per compute wave
-  int ffl;      // 16-byte pieces per lane of a d_ff row
+  int nsplit, cap, NA, GR;
+  int qpw, orw, gpw;   // QKV pairs, O/down rows and gate/up pairs per compute wave (at most)
+  int ring_q, ring_o, ring_g, ring_d, ring_bytes, log_rows;
   size_t lds;
 };
 
@@ -997,58 +1114,77 @@ static bool config_ok(const msd_config* c) {
   if (c->n_heads * kDh != c->d_model || c->n_heads % c->n_kv_heads != 0) return false;
   if (c->d_ff <= 0 || c->d_ff % 16 != 0 || c->vocab_size <= 0 || c->context_len <= 0) return false;
   if (c->context_len > 1024) return false;
-  if (c->d_model != 256 && c->d_model != 1024) return false;
+  if (!((c->d_model == 256 && c->d_ff == 704) || (c->d_model == 1024 && c->d_ff == 2816))) return false;
   return true;
 }
 
-static int cdiv(int a, int b) { return (a + b - 1) / b; }
+constexpr int kMaxLds = 160 * 1024;
+// At least this much LDS per workgroup, so that no two workgroups of a step share a
+// compute unit: the grid then spreads over every CU.
+constexpr int kMinLds = 84 * 1024;
 
-// Shapes the kernel instantiations cover for n_workgroups workgroups; false if unsupported.
+// Shapes for n_workgroups workgroups; false if unsupported.
 static bool make_plan(const msd_config* c, int G, Plan* p) {
   if (!config_ok(c) || G <= 0) return false;
-  const int nqkv = (c->n_heads + 2 * c->n_kv_heads) * kDh;
-  if (cdiv(nqkv / 2, G) > kWavesC || cdiv(c->d_model, G) > kWavesC) return false;
-  if (c->n_kv_heads * n_chunks(c->context_len) > G) return false;
-  p->frw = cdiv(cdiv(c->d_ff, G), kWavesC);
-  p->ffl = cdiv(c->d_ff, 512);
-  const int GQ = c->n_heads / c->n_kv_heads;
-  const int nch = n_chunks(c->context_len);
-  const int ch_max = cdiv(c->context_len, nch);
-  const int xmax = (std::max(std::max(c->d_model, c->d_ff), nch * GQ * kPartStride) + 3) & ~3;
-  const size_t floats = size_t(c->d_model) + xmax + ch_max * (kKPad + kDh) + GQ * kDh + kWavesC * 64 + 64 + 4 +
-                        2 * kWavesC * kMbox + 8;
-  p->lds = floats * 4;
-  return true;
+  const int D = c->d_model, ff = c->d_ff, H = c->n_heads, KV = c->n_kv_heads;
+  const int nqkv = (H + 2 * KV) * kDh;
+  p->cap = att_cap(c->context_len);
+  p->nsplit = att_splits(c->context_len);
+  p->NA = H * p->nsplit;
+  p->GR = G - p->NA;
+  // every row workgroup owns at least one O/down row and one gate/up pair: its own outputs
+  // are then part of every vector it gathers, which orders its LDS buffer reuse
+  if (p->GR < 8 || p->GR > D || p->GR > ff) return false;
+  const int qpairs = cdiv(nqkv / 2, p->GR), orows = cdiv(D, p->GR), gpairs = cdiv(ff, p->GR);
+  p->qpw = cdiv(qpairs, kWavesC);
+  p->orw = cdiv(orows, kWavesC);
+  p->gpw = cdiv(gpairs, kWavesC);
+  if (2 * p->qpw > kMbox || p->orw > kMbox || p->gpw > kMbox) return false;
+  auto kb = [](int64_t b) { return int((b + 1023) / 1024 * 1024); };
+  p->ring_q = 0;
+  p->ring_o = p->ring_q + kb(int64_t(2) * qpairs * D * 2);
+  p->ring_g = p->ring_o + kb(int64_t(orows) * D * 2);
+  p->ring_d = p->ring_g + kb(int64_t(2) * gpairs * D * 2);
+  int ring = p->ring_d + kb(int64_t(orows) * ff * 2);
+  ring = std::max(ring, 4 * D * 2);          // at least two logit rows per ring half
+  ring = (ring + 2047) / 2048 * 2048;        // halves of whole KB
+  const int natt = H * p->nsplit * kPart;
+  const int row_other = 4 * (5 * D + ((ff + 3) & ~3) + ((natt + 3) & ~3) + 8 + 2 * kWavesC);
+  const int att_lds = cdiv(p->cap * 9, 64) * 1024 + cdiv(p->cap, 8) * 1024 +
+                      4 * (2 * 3 * kDh + kWavesA * kDh + 2 * kWavesA + 4);
+  const int budget = std::max(std::max(att_lds, kMinLds), ring + row_other);
+  ring = std::max(ring, (budget - row_other) / 2048 * 2048);   // spare LDS widens the logit halves
+  p->ring_bytes = ring;
+  p->log_rows = (ring / 2) / (D * 2);
+  p->lds = size_t(std::max(std::max(att_lds, ring + row_other), kMinLds));
+  return p->lds <= size_t(kMaxLds);
 }
 
-// At least this much LDS per workgroup, so that no two workgroups of a step share a
-// compute unit (160 KB per CU): the grid then spreads over every CU.
-constexpr size_t kMinLds = 84 * 1024;
-
-template <int D, int FF, int FRW>
+template <int D, int FF, int QPW, int ORW, int GPW>
 static hipError_t launch_t(const Args& a, int grid, size_t lds, hipStream_t s) {
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&decode_step_kernel<D, FF, FRW>),
+  static size_t attr_lds = 0;
+  if (attr_lds < lds) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&decode_step_kernel<D, FF, QPW, ORW, GPW>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
     if (e != hipSuccess) return e;
-    attr_set = true;
+    attr_lds = lds;
   }
-  hipLaunchKernelGGL((decode_step_kernel<D, FF, FRW>), dim3(grid), dim3(kThreadsWG), lds, s, a);
+  hipLaunchKernelGGL((decode_step_kernel<D, FF, QPW, ORW, GPW>), dim3(grid), dim3(kThreadsWG), lds, s, a);
   return hipGetLastError();
 }
 
-// Instantiated shapes (d_model, d_ff, gate/up rows per compute wave): the tiny and the
-// 306M configurations on 256 workgroups, and the same shapes on fewer workgroups.
-static hipError_t launch(const Args& a, const Plan& p, int d, int ff, int grid, size_t lds, hipStream_t s) {
-  if (d == 256 && ff == 704 && p.frw == 1) return launch_t<256, 704, 1>(a, grid, lds, s);
-  if (d == 1024 && ff == 2816 && p.frw == 3) return launch_t<1024, 2816, 3>(a, grid, lds, s);
-  return hipErrorInvalidValue;
+// Instantiated shapes (d_model, d_ff, per-wave row caps): the tiny and the 306M
+// configurations on 256 workgroups (and on any grid whose per-wave rows fit the caps).
+static bool plan_instantiated(const msd_config* c, const Plan& p) {
+  if (c->d_model == 256 && c->d_ff == 704) return p.qpw <= 1 && p.orw <= 1 && p.gpw <= 1;
+  if (c->d_model == 1024 && c->d_ff == 2816) return p.qpw <= 1 && p.orw <= 2 && p.gpw <= 3;
+  return false;
 }
 
-static bool plan_instantiated(const msd_config* c, const Plan& p) {
-  return (c->d_model == 256 && c->d_ff == 704 && p.frw == 1) ||
-         (c->d_model == 1024 && c->d_ff == 2816 && p.frw == 3);
+static hipError_t launch(const Args& a, int d, int ff, int grid, size_t lds, hipStream_t s) {
+  if (d == 256 && ff == 704) return launch_t<256, 704, 1, 1, 1>(a, grid, lds, s);
+  if (d == 1024 && ff == 2816) return launch_t<1024, 2816, 1, 2, 3>(a, grid, lds, s);
+  return hipErrorInvalidValue;
 }
 
 }  // namespace msd
@@ -1065,9 +1201,8 @@ extern "C" int64_t msd_workspace_bytes(const msd_config* cfg, int32_t n_workgrou
   Plan p;
   if (!config_ok(cfg)) return MSD_E_CONFIG;
   if (!make_plan(cfg, n_workgroups, &p) || !plan_instantiated(cfg, p)) return MSD_E_CONFIG;
-  const Layout t = make_layout(cfg->d_model, cfg->n_heads, cfg->n_kv_heads, cfg->d_ff, cfg->context_len, n_workgroups);
-  return t.ctrl_bytes + t.x_layer * cfg->n_layers * int64_t(sizeof(uint64_t)) +
-         t.flag_words * cfg->n_layers * int64_t(sizeof(uint32_t));
+  const Layout t = make_layout(cfg->d_model, cfg->n_heads, cfg->n_kv_heads, cfg->d_ff, cfg->context_len);
+  return t.ctrl_bytes + t.x_layer * cfg->n_layers * int64_t(sizeof(uint64_t));
 }
 
 extern "C" int32_t msd_default_workgroups(int32_t device) {
@@ -1105,9 +1240,8 @@ extern "C" int32_t msd_decode_step(const msd_config* cfg, const void* token_emb,
   a.next_token = next_token;
   a.token_dev = token_dev;
   a.ctrl = static_cast<uint32_t*>(workspace);
-  a.lay = make_layout(cfg->d_model, cfg->n_heads, cfg->n_kv_heads, cfg->d_ff, cfg->context_len, n_workgroups);
+  a.lay = make_layout(cfg->d_model, cfg->n_heads, cfg->n_kv_heads, cfg->d_ff, cfg->context_len);
   a.xw = reinterpret_cast<uint64_t*>(static_cast<char*>(workspace) + a.lay.ctrl_bytes);
-  a.flags = reinterpret_cast<uint32_t*>(a.xw + a.lay.x_layer * cfg->n_layers);
   a.token = token_id;
   a.pos = pos;
   a.epoch = epoch;
@@ -1117,9 +1251,17 @@ extern "C" int32_t msd_decode_step(const msd_config* cfg, const void* token_emb,
   a.ff = cfg->d_ff;
   a.V = cfg->vocab_size;
   a.ctx = cfg->context_len;
-  a.nch = n_chunks(cfg->context_len);
-  const size_t lds = std::max(p.lds, kMinLds);
-  const hipError_t e = launch(a, p, cfg->d_model, cfg->d_ff, n_workgroups, lds, static_cast<hipStream_t>(stream));
+  a.nsplit = p.nsplit;
+  a.cap = p.cap;
+  a.NA = p.NA;
+  a.GR = p.GR;
+  a.ring_q = p.ring_q;
+  a.ring_o = p.ring_o;
+  a.ring_g = p.ring_g;
+  a.ring_d = p.ring_d;
+  a.ring_bytes = p.ring_bytes;
+  a.log_rows = p.log_rows;
+  const hipError_t e = launch(a, cfg->d_model, cfg->d_ff, n_workgroups, p.lds, static_cast<hipStream_t>(stream));
   return e == hipSuccess ? MSD_OK : MSD_E_HIP;
 }
 
