@@ -79,8 +79,7 @@ constexpr int kKRowB = 144;      // LDS bytes per cached K row: 128 + 16 padding
 constexpr int kVRowB = 128;      // LDS bytes per cached V row
 constexpr uint32_t kSpinLimit = 1u << 20;
 
-constexpr int kWavesC = 4;       // compute waves of a row workgroup
-constexpr int kWavesX = 4;       // exchange waves of a row workgroup
+constexpr int kWavesR = 8;       // worker waves of a row workgroup
 constexpr int kWavesA = 8;       // attention waves of an attention workgroup
 constexpr int kLoader = 8;       // wave index of the loader (both kinds)
 constexpr int kThreadsWG = 9 * 64;
@@ -464,18 +463,16 @@ struct RowCtx {
   int qp0, qp1, or0, or1, f0, f1, v0, v1;   // QKV pairs, O/down rows, gate/up pairs, vocabulary rows
   int nlog;                                 // logit chunks
   uint8_t* ring;
-  float* hres;    // residual stream h, two buffers (written alternately by compute wave 0)
   float* xatt;    // attention vector (input of the O rows)
   float* xhd1;    // O output (gathered)
   float* xact;    // SwiGLU activation (input of the down rows)
   float* xhd2;    // down output (gathered)
   float* xa;      // gathered attention partials
-  int* ctr;       // [0] exchange-wave sync, [1] inputs ready, [2] outputs stored (compute
-                  // wave bumps), [4] ring jobs consumed, [5] ring jobs loaded, [6] compute-wave sync
-  float* red_v;   // argmax per compute wave
+  int* ctr;       // [0] worker barrier, [4] ring jobs consumed (worker bumps), [5] ring jobs loaded
+  float* red_v;   // argmax per worker wave
   int* red_i;
 };
-enum { kCtrXs = 0, kCtrReady = 1, kCtrStored = 2, kCtrUsed = 4, kCtrLoaded = 5, kCtrCs = 6 };
+enum { kCtrBar = 0, kCtrUsed = 4, kCtrLoaded = 5 };
 
 // Loader wave of a row workgroup.  Jobs in order: per layer the QKV, O, gate/up and down
 // rows of this workgroup (into their fixed ring regions), then the logit rows in chunks
@@ -509,9 +506,9 @@ __device__ void row_loader(const Args& a, const RowCtx& c) {
       off = (k & 1) * half;
       need = k < 2 ? 4 * a.L : 4 * a.L + k - 1;   // every layer job, or logit chunk k - 2
     }
-    if (need > 0 && lds_ld(c.ctr + kCtrUsed) < kWavesC * need) {
+    if (need > 0 && lds_ld(c.ctr + kCtrUsed) < kWavesR * need) {
       d.drain();
-      lds_wait(c.ctr + kCtrUsed, kWavesC * need, a.ctrl);
+      lds_wait(c.ctr + kCtrUsed, kWavesR * need, a.ctrl);
     }
     if (bytes > 0) dma_copy(d, reinterpret_cast<const uint8_t*>(src), c.ring + off, bytes, lane);
     d.drain();
@@ -520,97 +517,31 @@ __device__ void row_loader(const Args& a, const RowCtx& c) {
   }
 }
 
-// Exchange waves of a row workgroup: per phase, once this workgroup's compute waves have
-// issued their stores (so those never queue behind the polls), they gather the phase's
-// vector (the outputs of every row workgroup) into its LDS buffer and signal the compute
-// waves.  Each buffer is rewritten only after every compute wave has stored the outputs of a
-// later phase, so no compute wave still reads it.
-template <int D, int FF>
-__device__ void row_exchange(const Args& a, const RowCtx& c) {
-  constexpr int HPW = D / (64 * kWavesX);                           // words per lane of a d-vector
-  constexpr int NKF = (FF + 64 * kWavesX - 1) / (64 * kWavesX);    // act words per lane
-  constexpr int H = D / kDh;
-  constexpr int NKA1 = (H * kPart + 64 * kWavesX - 1) / (64 * kWavesX);       // attention words, 1 split
-  constexpr int NKA2 = (2 * H * kPart + 64 * kWavesX - 1) / (64 * kWavesX);   // 2 splits
-  const int lane = c.lane, ew = c.wv - kWavesC;
-  const Layout& lay = a.lay;
-  bool bad = false;
-  int xs = 0, nst = 0;
-  const int64_t myrep = int64_t(c.wr % kRep) * lay.x_rep;
-  const int natt = a.H * a.nsplit;
-  auto wait_stored = [&]() {
-    ++nst;
-    lds_wait(c.ctr + kCtrStored, kWavesC * nst, a.ctrl);
-  };
-  for (int l = 0; l < a.L; ++l) {
-    uint64_t* X = layer_x(a, l);
-    // attention partials of every (head, split) -> attention vector (multi_sm_decode.py:243-259)
-    wait_stored();
-    MSD_TRACE_POINT(ew == 0, l, 0);
-    if (a.nsplit == 1)
-      gather_x<kWavesX, NKA1>(X + lay.x_att + myrep, natt * kPart, c.xa, c.tag, a.ctrl, ew, lane, bad);
-    else
-      gather_x<kWavesX, NKA2>(X + lay.x_att + myrep, natt * kPart, c.xa, c.tag, a.ctrl, ew, lane, bad);
-    wsync(c.ctr + kCtrXs, xs, kWavesX, lane, a.ctrl);
-    if (a.nsplit == 1) {
-      for (int i = ew * 64 + lane; i < D; i += kWavesX * 64) {
-        const float* ps = c.xa + (i / kDh) * kPart;
-        const float den = ps[1];
-        c.xatt[i] = den > 0.f ? ps[2 + i % kDh] / den : 0.f;
-      }
-    } else {
-      for (int i = ew * 64 + lane; i < D; i += kWavesX * 64) {
-        const int hd = i / kDh, dim = i % kDh;
-        float M = -INFINITY;
-        for (int s = 0; s < a.nsplit; ++s) {
-          const float* ps = c.xa + (hd * a.nsplit + s) * kPart;
-          if (ps[1] > 0.f) M = fmaxf(M, ps[0]);
-        }
-        float num = 0.f, den = 0.f;
-        for (int s = 0; s < a.nsplit; ++s) {
-          const float* ps = c.xa + (hd * a.nsplit + s) * kPart;
-          if (ps[1] > 0.f) {
-            const float wgt = expf(ps[0] - M);
-            num += wgt * ps[2 + dim];
-            den += wgt * ps[1];
-          }
-        }
-        c.xatt[i] = den > 0.f ? num / den : 0.f;
-      }
-    }
-    lds_bump(c.ctr + kCtrReady, lane);
-    MSD_TRACE_POINT(ew == 0, l, 1);
-    // O output
-    wait_stored();
-    gather_x<kWavesX, HPW>(X + lay.x_hd1 + myrep, D, c.xhd1, c.tag, a.ctrl, ew, lane, bad);
-    lds_bump(c.ctr + kCtrReady, lane);
-    MSD_TRACE_POINT(ew == 0, l, 2);
-    // SwiGLU activation
-    wait_stored();
-    gather_x<kWavesX, NKF>(X + lay.x_act + myrep, a.ff, c.xact, c.tag, a.ctrl, ew, lane, bad);
-    lds_bump(c.ctr + kCtrReady, lane);
-    MSD_TRACE_POINT(ew == 0, l, 5);
-    // down output
-    wait_stored();
-    gather_x<kWavesX, HPW>(X + lay.x_hd2 + myrep, D, c.xhd2, c.tag, a.ctrl, ew, lane, bad);
-    lds_bump(c.ctr + kCtrReady, lane);
-    MSD_TRACE_POINT(ew == 0, l, 6);
-  }
-}
-
-// Compute waves of a row workgroup.  Every compute wave keeps the residual stream h in
-// registers, in the lane layout of the row dot products (lane l holds elements
-// 512 j + k m + l), adds the gathered O and down outputs itself and takes the RMSNorms with a
-// wave reduction, so a norm needs no exchange between waves.  Per phase: wait for the input
-// vector and the ring job, take the dot products of this wave's rows (workgroup-local items
-// w, w + 4, ...; at most QPW QKV pairs, ORW O/down rows and GPW gate/up pairs per wave),
-// store the outputs to the exchange words and release the ring region.
+// Worker waves of a row workgroup (8 waves; the loader wave streams the weights).  Every
+// worker keeps the residual stream h in registers in the lane layout of the row dot
+// products (lane l holds elements 512 j + k m + l), so each takes the RMSNorms itself with
+// one wave reduction.  Per phase every worker takes the dot products of its rows
+// (workgroup-local items w, w + 8, ...; at most QPW QKV pairs, ORW O/down rows and GPW
+// gate/up pairs), stores the outputs to the exchange words, and once all workers have
+// stored (so this workgroup's stores never queue behind its own polls) the workers gather
+// the next vector, each an eighth of its words, into LDS.  Workgroup-local barriers are LDS
+// counters among the 8 workers.
 template <int D, int FF, int QPW, int ORW, int GPW>
-__device__ void row_compute(const Args& a, const RowCtx& c, int token) {
+__device__ void row_worker(const Args& a, const RowCtx& c, int token) {
   constexpr int NLD = (D + 511) / 512;
   constexpr int NLF = (FF + 511) / 512;
+  constexpr int HPW = (D + 64 * kWavesR - 1) / (64 * kWavesR);    // d-vector words per lane
+  constexpr int NKF = (FF + 64 * kWavesR - 1) / (64 * kWavesR);   // act words per lane
+  constexpr int H = D / kDh;
+  constexpr int NKA1 = (H * kPart + 64 * kWavesR - 1) / (64 * kWavesR);       // attention words, 1 split
+  constexpr int NKA2 = (2 * H * kPart + 64 * kWavesR - 1) / (64 * kWavesR);   // 2 splits
   const int lane = c.lane, wv = c.wv;
   const Layout& lay = a.lay;
+  bool bad = false;
+  int bars = 0;
+  auto bar = [&]() { wsync(c.ctr + kCtrBar, bars, kWavesR, lane, a.ctrl); };
+  const int64_t myrep = int64_t(c.wr % kRep) * lay.x_rep;
+  const int natt = a.H * a.nsplit;
   const int nq = c.qp1 - c.qp0, no = c.or1 - c.or0, ng = c.f1 - c.f0;
   // rotary factors of this wave's QKV pairs (q/k rows), loaded once
   float cs[QPW], sn[QPW];
@@ -618,7 +549,7 @@ __device__ void row_compute(const Args& a, const RowCtx& c, int token) {
   for (int i = 0; i < QPW; ++i) {
     cs[i] = 1.f;
     sn[i] = 0.f;
-    const int rel = wv + kWavesC * i;
+    const int rel = wv + kWavesR * i;
     if (rel < nq) {
       const int row = 2 * (c.qp0 + rel);
       if (row / kDh < a.H + a.KV) {
@@ -648,35 +579,29 @@ __device__ void row_compute(const Args& a, const RowCtx& c, int token) {
 #pragma unroll
       for (int q = 0; q < 8; ++q) h.v[j][q] = h.v[j][q] + t.v[j][q];
   };
-  auto norm = [&](XV<NLD>& x) {   // x = sc * (h / sqrt(mean(h^2) + eps)) (model.py:94-98)
+  // x = sc * h * (1 / sqrt(mean(h^2) + eps)): model.py:94-98, with the reciprocal taken once
+  // as the reference kernel does (multi_sm_decode.py:122-126 multiplies by rsqrt)
+  auto norm = [&](XV<NLD>& x) {
     float ss = 0.f;
 #pragma unroll
     for (int j = 0; j < NLD; ++j)
 #pragma unroll
       for (int q = 0; q < 8; ++q) ss += h.v[j][q] * h.v[j][q];
     ss = wave_sum(ss);
-    const float r = sqrtf(ss / float(D) + 1e-5f);
+    const float inv = 1.f / sqrtf(ss / float(D) + 1e-5f);
 #pragma unroll
     for (int j = 0; j < NLD; ++j)
 #pragma unroll
-      for (int q = 0; q < 8; ++q) x.v[j][q] = sc.v[j][q] * (h.v[j][q] / r);
+      for (int q = 0; q < 8; ++q) x.v[j][q] = sc.v[j][q] * (h.v[j][q] * inv);
   };
-  int nin = 0;
-  auto wait_in = [&](bool input, int job) {
-    if (input) {
-      ++nin;
-      lds_wait(c.ctr + kCtrReady, kWavesX * nin, a.ctrl);
-    }
-    lds_wait(c.ctr + kCtrLoaded, job + 1, a.ctrl);
-  };
+  auto weights = [&](int job) { lds_wait(c.ctr + kCtrLoaded, job + 1, a.ctrl); };
   auto release = [&]() { lds_bump(c.ctr + kCtrUsed, lane); };
-  auto stored = [&]() { lds_bump(c.ctr + kCtrStored, lane); };
   // LDS row of workgroup-local item rel (the region's first row when rel is past the end)
   auto at = [&](int region, int rel, int n, int item_bytes) {
     return c.ring + region + int64_t(rel < n ? rel : 0) * item_bytes;
   };
-  auto count = [&](int n, int cap) {   // this wave's items among n (items w, w + 4, ...)
-    return n > wv ? min(cap, (n - wv + kWavesC - 1) / kWavesC) : 0;
+  auto count = [&](int n, int cap) {   // this wave's items among n (items w, w + 8, ...)
+    return n > wv ? min(cap, (n - wv + kWavesR - 1) / kWavesR) : 0;
   };
 
   for (int l = 0; l < a.L; ++l) {
@@ -685,8 +610,13 @@ __device__ void row_compute(const Args& a, const RowCtx& c, int token) {
     uint16_t* vcache = kcache + int64_t(a.KV) * a.ctx * kDh;
     // ---- h += down output of the previous layer; x = rmsnorm1(h); QKV rows, RoPE, KV write
     //      (multi_sm_decode.py:121-180)
-    wait_in(l > 0, 4 * l);
-    if (l > 0) add_res(c.xhd2);
+    if (l > 0) {
+      gather_x<kWavesR, HPW>(layer_x(a, l - 1) + lay.x_hd2 + myrep, D, c.xhd2, c.tag, a.ctrl, wv, lane, bad);
+      bar();
+      add_res(c.xhd2);
+      MSD_TRACE_POINT(wv == 0, l - 1, 6);
+    }
+    weights(4 * l);
     MSD_TRACE_POINT(wv == 0, l, 16);
     MSD_TRACE_CLOCK(wv == 0, l, 12);
     {
@@ -695,7 +625,7 @@ __device__ void row_compute(const Args& a, const RowCtx& c, int token) {
       const uint8_t* rows[2 * QPW];
 #pragma unroll
       for (int i = 0; i < QPW; ++i) {
-        rows[2 * i] = at(a.ring_q, wv + kWavesC * i, nq, 2 * D * 2);
+        rows[2 * i] = at(a.ring_q, wv + kWavesR * i, nq, 2 * D * 2);
         rows[2 * i + 1] = rows[2 * i] + D * 2;
       }
       float sd[2 * QPW];
@@ -705,7 +635,7 @@ __device__ void row_compute(const Args& a, const RowCtx& c, int token) {
       int ix[2 * QPW];
 #pragma unroll
       for (int i = 0; i < QPW; ++i) {
-        const int rel = wv + kWavesC * i;
+        const int rel = wv + kWavesR * i;
         const int row = 2 * (c.qp0 + (rel < nq ? rel : 0));
         const int head = row / kDh;
         const int rr = row % kDh;
@@ -730,12 +660,46 @@ __device__ void row_compute(const Args& a, const RowCtx& c, int token) {
         }
       }
       store_out<2 * QPW>(X + lay.x_qkv, y, ix, 2 * count(nq, QPW), false, lay.x_rep, c.tag, lane);
-      stored();
-      load_vec(sc, layer_w(a, l) + lay.off_ln2);   // scale of the next norm
     }
+    load_vec(sc, layer_w(a, l) + lay.off_ln2);   // scale of the next norm
+    bar();   // every QKV output of this workgroup is issued
     MSD_TRACE_POINT(wv == 0, l, 17);
+    // ---- attention partials of every (head, split) -> attention vector (multi_sm_decode.py:243-259)
+    if (a.nsplit == 1)
+      gather_x<kWavesR, NKA1>(X + lay.x_att + myrep, natt * kPart, c.xa, c.tag, a.ctrl, wv, lane, bad);
+    else
+      gather_x<kWavesR, NKA2>(X + lay.x_att + myrep, natt * kPart, c.xa, c.tag, a.ctrl, wv, lane, bad);
+    bar();
+    if (a.nsplit == 1) {
+      for (int i = wv * 64 + lane; i < D; i += kWavesR * 64) {
+        const float* ps = c.xa + (i / kDh) * kPart;
+        const float den = ps[1];
+        c.xatt[i] = den > 0.f ? ps[2 + i % kDh] / den : 0.f;
+      }
+    } else {
+      for (int i = wv * 64 + lane; i < D; i += kWavesR * 64) {
+        const int hd = i / kDh, dim = i % kDh;
+        float M = -INFINITY;
+        for (int s = 0; s < a.nsplit; ++s) {
+          const float* ps = c.xa + (hd * a.nsplit + s) * kPart;
+          if (ps[1] > 0.f) M = fmaxf(M, ps[0]);
+        }
+        float num = 0.f, den = 0.f;
+        for (int s = 0; s < a.nsplit; ++s) {
+          const float* ps = c.xa + (hd * a.nsplit + s) * kPart;
+          if (ps[1] > 0.f) {
+            const float wgt = expf(ps[0] - M);
+            num += wgt * ps[2 + dim];
+            den += wgt * ps[1];
+          }
+        }
+        c.xatt[i] = den > 0.f ? num / den : 0.f;
+      }
+    }
+    bar();
+    MSD_TRACE_POINT(wv == 0, l, 1);
     // ---- O rows (multi_sm_decode.py:223-232)
-    wait_in(true, 4 * l + 1);
+    weights(4 * l + 1);
     MSD_TRACE_POINT(wv == 0, l, 18);
     {
       XV<NLD> xv;
@@ -744,19 +708,22 @@ __device__ void row_compute(const Args& a, const RowCtx& c, int token) {
       int ix[ORW];
 #pragma unroll
       for (int i = 0; i < ORW; ++i) {
-        rows[i] = at(a.ring_o, wv + kWavesC * i, no, D * 2);
-        ix[i] = int(lay.x_hd1) + c.or0 + wv + kWavesC * i;
+        rows[i] = at(a.ring_o, wv + kWavesR * i, no, D * 2);
+        ix[i] = int(lay.x_hd1) + c.or0 + wv + kWavesR * i;
       }
       float y[ORW];
       dot_rows<NLD, ORW>(rows, xv, D, lane, y);
       release();
       store_out<ORW>(X, y, ix, count(no, ORW), true, lay.x_rep, c.tag, lane);
-      stored();
     }
+    bar();
     MSD_TRACE_POINT(wv == 0, l, 19);
     // ---- h += O output; x = rmsnorm2(h); gate/up rows + SwiGLU (multi_sm_decode.py:262-289, model.py:159)
-    wait_in(true, 4 * l + 2);
+    gather_x<kWavesR, HPW>(X + lay.x_hd1 + myrep, D, c.xhd1, c.tag, a.ctrl, wv, lane, bad);
+    bar();
+    MSD_TRACE_POINT(wv == 0, l, 2);
     add_res(c.xhd1);
+    weights(4 * l + 2);
     MSD_TRACE_POINT(wv == 0, l, 20);
     {
       XV<NLD> xv;
@@ -765,9 +732,9 @@ __device__ void row_compute(const Args& a, const RowCtx& c, int token) {
       int ix[GPW];
 #pragma unroll
       for (int i = 0; i < GPW; ++i) {
-        rows[2 * i] = at(a.ring_g, wv + kWavesC * i, ng, 2 * D * 2);
+        rows[2 * i] = at(a.ring_g, wv + kWavesR * i, ng, 2 * D * 2);
         rows[2 * i + 1] = rows[2 * i] + D * 2;
-        ix[i] = int(lay.x_act) + c.f0 + wv + kWavesC * i;
+        ix[i] = int(lay.x_act) + c.f0 + wv + kWavesR * i;
       }
       float gu[2 * GPW];
       dot_rows<NLD, 2 * GPW>(rows, xv, D, lane, gu);
@@ -779,11 +746,14 @@ __device__ void row_compute(const Args& a, const RowCtx& c, int token) {
         y[i] = (gt * (1.f / (1.f + expf(-gt)))) * up;
       }
       store_out<GPW>(X, y, ix, count(ng, GPW), true, lay.x_rep, c.tag, lane);
-      stored();
     }
+    bar();
     MSD_TRACE_POINT(wv == 0, l, 21);
-    // ---- down rows (multi_sm_decode.py:273-291)
-    wait_in(true, 4 * l + 3);
+    // ---- act -> LDS; down rows (multi_sm_decode.py:273-291)
+    gather_x<kWavesR, NKF>(X + lay.x_act + myrep, a.ff, c.xact, c.tag, a.ctrl, wv, lane, bad);
+    bar();
+    MSD_TRACE_POINT(wv == 0, l, 5);
+    weights(4 * l + 3);
     MSD_TRACE_POINT(wv == 0, l, 22);
     {
       XV<NLF> xv;
@@ -792,23 +762,23 @@ __device__ void row_compute(const Args& a, const RowCtx& c, int token) {
       int ix[ORW];
 #pragma unroll
       for (int i = 0; i < ORW; ++i) {
-        rows[i] = at(a.ring_d, wv + kWavesC * i, no, FF * 2);
-        ix[i] = int(lay.x_hd2) + c.or0 + wv + kWavesC * i;
+        rows[i] = at(a.ring_d, wv + kWavesR * i, no, FF * 2);
+        ix[i] = int(lay.x_hd2) + c.or0 + wv + kWavesR * i;
       }
       float y[ORW];
       dot_rows<NLF, ORW>(rows, xv, FF, lane, y);
       release();
       store_out<ORW>(X, y, ix, count(no, ORW), true, lay.x_rep, c.tag, lane);
-      stored();
     }
     load_vec(sc, l + 1 < a.L ? layer_w(a, l + 1) + lay.off_ln1 : a.lnf);   // scale of the next norm
+    bar();
     MSD_TRACE_POINT(wv == 0, l, 23);
     MSD_TRACE_CLOCK(wv == 0, l, 13);
   }
   // ---- h += last down output; x = final rmsnorm(h); tied logits over this workgroup's
   //      vocabulary rows (multi_sm_decode.py:314-337)
-  ++nin;
-  lds_wait(c.ctr + kCtrReady, kWavesX * nin, a.ctrl);
+  gather_x<kWavesR, HPW>(layer_x(a, a.L - 1) + lay.x_hd2 + myrep, D, c.xhd2, c.tag, a.ctrl, wv, lane, bad);
+  bar();
   add_res(c.xhd2);
   XV<NLD> xv;
   norm(xv);
@@ -817,22 +787,22 @@ __device__ void row_compute(const Args& a, const RowCtx& c, int token) {
   const int half = a.ring_bytes / 2;
   constexpr int RB = 4;   // rows per batch of LDS reads
   for (int k = 0; k < c.nlog; ++k) {
-    lds_wait(c.ctr + kCtrLoaded, 4 * a.L + k + 1, a.ctrl);
+    weights(4 * a.L + k);
     const int r0 = c.v0 + k * a.log_rows;
     const int n = min(c.v1, r0 + a.log_rows) - r0;
     const uint8_t* base = c.ring + (k & 1) * half;
-    for (int b = wv; b < n; b += kWavesC * RB) {
+    for (int b = wv; b < n; b += kWavesR * RB) {
       const uint8_t* rows[RB];
 #pragma unroll
       for (int i = 0; i < RB; ++i) {
-        const int rel = b + kWavesC * i;
+        const int rel = b + kWavesR * i;
         rows[i] = base + int64_t(rel < n ? rel : 0) * D * 2;
       }
       float y[RB];
       dot_rows<NLD, RB>(rows, xv, D, lane, y);
 #pragma unroll
       for (int i = 0; i < RB; ++i) {
-        const int rel = b + kWavesC * i;
+        const int rel = b + kWavesR * i;
         if (rel < n) {
           if (lane == 0) a.logits[r0 + rel] = y[i];
           if (y[i] > best) { best = y[i]; besti = r0 + rel; }
@@ -845,12 +815,11 @@ __device__ void row_compute(const Args& a, const RowCtx& c, int token) {
     c.red_v[wv] = best;
     c.red_i[wv] = besti;
   }
-  int cs_ = 0;
-  wsync(c.ctr + kCtrCs, cs_, kWavesC, lane, a.ctrl);
+  bar();
   if (wv == 0 && lane == 0) {   // argmax: larger value wins, ties -> lower index (np.argmax)
     float bv = c.red_v[0];
     int bi = c.red_i[0];
-    for (int w = 1; w < kWavesC; ++w) {
+    for (int w = 1; w < kWavesR; ++w) {
       const float v = c.red_v[w];
       const int i = c.red_i[w];
       if (v > bv || (v == bv && i < bi)) { bv = v; bi = i; }
@@ -1078,15 +1047,14 @@ __global__ __launch_bounds__(kThreadsWG, 1) void decode_step_kernel(Args a) {
   split(a.V, a.GR, wg, c.v0, c.v1);
   c.nlog = cdiv(c.v1 - c.v0, a.log_rows);
   c.ring = smem;
-  c.hres = reinterpret_cast<float*>(smem + a.ring_bytes);
-  c.xatt = c.hres + 2 * D;
+  c.xatt = reinterpret_cast<float*>(smem + a.ring_bytes);
   c.xhd1 = c.xatt + D;
   c.xhd2 = c.xhd1 + D;
   c.xact = c.xhd2 + D;
   c.xa = c.xact + ((FF + 3) & ~3);
   c.ctr = reinterpret_cast<int*>(c.xa + ((a.H * a.nsplit * kPart + 3) & ~3));
   c.red_v = reinterpret_cast<float*>(c.ctr + 8);
-  c.red_i = reinterpret_cast<int*>(c.red_v + kWavesC);
+  c.red_i = reinterpret_cast<int*>(c.red_v + kWavesR);
   if (threadIdx.x < 8) c.ctr[threadIdx.x] = 0;
   __syncthreads();   // the only workgroup barrier; the roles below meet on LDS counters
 
@@ -1096,8 +1064,7 @@ __global__ __launch_bounds__(kThreadsWG, 1) void decode_step_kernel(Args a) {
     token = token < 0 ? 0 : a.V - 1;
   }
   if (wv == kLoader) row_loader<D, FF>(a, c);
-  else if (wv >= kWavesC) row_exchange<D, FF>(a, c);
-  else row_compute<D, FF, QPW, ORW, GPW>(a, c, token);
+  else row_worker<D, FF, QPW, ORW, GPW>(a, c, token);
 }
 
 // ---------------------------------------------------------------- host side
@@ -1136,9 +1103,9 @@ static bool make_plan(const msd_config* c, int G, Plan* p) {
   // are then part of every vector it gathers, which orders its LDS buffer reuse
   if (p->GR < 8 || p->GR > D || p->GR > ff) return false;
   const int qpairs = cdiv(nqkv / 2, p->GR), orows = cdiv(D, p->GR), gpairs = cdiv(ff, p->GR);
-  p->qpw = cdiv(qpairs, kWavesC);
-  p->orw = cdiv(orows, kWavesC);
-  p->gpw = cdiv(gpairs, kWavesC);
+  p->qpw = cdiv(qpairs, kWavesR);
+  p->orw = cdiv(orows, kWavesR);
+  p->gpw = cdiv(gpairs, kWavesR);
   if (2 * p->qpw > kMbox || p->orw > kMbox || p->gpw > kMbox) return false;
   auto kb = [](int64_t b) { return int((b + 1023) / 1024 * 1024); };
   p->ring_q = 0;
@@ -1149,7 +1116,7 @@ static bool make_plan(const msd_config* c, int G, Plan* p) {
   ring = std::max(ring, 4 * D * 2);          // at least two logit rows per ring half
   ring = (ring + 2047) / 2048 * 2048;        // halves of whole KB
   const int natt = H * p->nsplit * kPart;
-  const int row_other = 4 * (5 * D + ((ff + 3) & ~3) + ((natt + 3) & ~3) + 8 + 2 * kWavesC);
+  const int row_other = 4 * (3 * D + ((ff + 3) & ~3) + ((natt + 3) & ~3) + 8 + 2 * kWavesR);
   const int att_lds = cdiv(p->cap * 9, 64) * 1024 + cdiv(p->cap, 8) * 1024 +
                       4 * (2 * 3 * kDh + kWavesA * kDh + 2 * kWavesA + 4);
   const int budget = std::max(std::max(att_lds, kMinLds), ring + row_other);
@@ -1177,13 +1144,13 @@ static hipError_t launch_t(const Args& a, int grid, size_t lds, hipStream_t s) {
 // configurations on 256 workgroups (and on any grid whose per-wave rows fit the caps).
 static bool plan_instantiated(const msd_config* c, const Plan& p) {
   if (c->d_model == 256 && c->d_ff == 704) return p.qpw <= 1 && p.orw <= 1 && p.gpw <= 1;
-  if (c->d_model == 1024 && c->d_ff == 2816) return p.qpw <= 1 && p.orw <= 2 && p.gpw <= 3;
+  if (c->d_model == 1024 && c->d_ff == 2816) return p.qpw <= 1 && p.orw <= 1 && p.gpw <= 2;
   return false;
 }
 
 static hipError_t launch(const Args& a, int d, int ff, int grid, size_t lds, hipStream_t s) {
   if (d == 256 && ff == 704) return launch_t<256, 704, 1, 1, 1>(a, grid, lds, s);
-  if (d == 1024 && ff == 2816) return launch_t<1024, 2816, 1, 2, 3>(a, grid, lds, s);
+  if (d == 1024 && ff == 2816) return launch_t<1024, 2816, 1, 1, 2>(a, grid, lds, s);
   return hipErrorInvalidValue;
 }
 
