@@ -84,8 +84,11 @@ constexpr int kWavesA = 8;       // attention waves of an attention workgroup
 constexpr int kLoader = 8;       // wave index of the loader (both kinds)
 constexpr int kThreadsWG = 9 * 64;
 constexpr int kMbox = 8;         // outputs per compute wave and phase
-constexpr int kRep = 8;          // replicas of every vector all row workgroups gather
-static_assert(kWavesA == kRep, "each attention wave stores one replica");
+#ifndef MSD_REPLICAS
+#define MSD_REPLICAS 8
+#endif
+constexpr int kRep = MSD_REPLICAS;   // replicas of every vector all row workgroups gather
+static_assert(kRep % kWavesA == 0 && kRep <= 64, "attention waves store whole sets of replicas");
 constexpr int kDmaWindow = 48;   // 1 KB DMA instructions a loader keeps in flight
 
 constexpr uint32_t kStatusTimeout = 1u;
@@ -270,10 +273,16 @@ __device__ __forceinline__ bool repoll(uint64_t (&wd)[NK], const uint64_t* src, 
   return ok;
 }
 
+// The first round waits kFirstPoll s_sleep units (~0.4 us): the remote outputs cannot land
+// sooner, and an early round over words still being written costs a full round trip
+// (measured: 9% per token).
+constexpr int kFirstPoll = 16;
+
 template <int NW, int NK, int SLEEP = 0>
 __device__ __forceinline__ void poll_words(const uint64_t* src, int n, uint32_t tag, float (&v)[NK],
                                            uint32_t* ctrl, int w, int lane, bool& bad) {
   uint64_t wd[NK];
+  __builtin_amdgcn_s_sleep(kFirstPoll);
 #pragma unroll
   for (int k = 0; k < NK; ++k) {
     const int i = xidx<NW>(k, w, lane);
@@ -728,6 +737,7 @@ __device__ void row_worker(const Args& a, const RowCtx& c, int token) {
     {
       XV<NLD> xv;
       norm(xv);
+      MSD_TRACE_POINT(wv == 0, l, 8);
       const uint8_t* rows[2 * GPW];
       int ix[GPW];
 #pragma unroll
@@ -738,6 +748,7 @@ __device__ void row_worker(const Args& a, const RowCtx& c, int token) {
       }
       float gu[2 * GPW];
       dot_rows<NLD, 2 * GPW>(rows, xv, D, lane, gu);
+      MSD_TRACE_POINT(wv == 0, l, 9);
       release();
       float y[GPW];
 #pragma unroll
@@ -746,6 +757,7 @@ __device__ void row_worker(const Args& a, const RowCtx& c, int token) {
         y[i] = (gt * (1.f / (1.f + expf(-gt)))) * up;
       }
       store_out<GPW>(X, y, ix, count(ng, GPW), true, lay.x_rep, c.tag, lane);
+      MSD_TRACE_POINT(wv == 0, l, 10);
     }
     bar();
     MSD_TRACE_POINT(wv == 0, l, 21);
@@ -936,6 +948,7 @@ __device__ void att_waves(const Args& a, const AttCtx& c) {
       m = wave_max(s);
       const float e = (lane < np) ? expf(s - m) : 0.f;
       lsum = wave_sum(e);
+      MSD_TRACE_POINT(wv == 0, l, 29);
       // o[lane = dim] = sum_p e[p] * V[p][dim]: 16 positions per batch of LDS reads (rows
       // past np re-read row np - 1; their weights e are 0), e[p] taken from lane p
       const uint16_t* vr = reinterpret_cast<const uint16_t*>(c.V + r0 * kVRowB) + lane;
@@ -951,6 +964,7 @@ __device__ void att_waves(const Args& a, const AttCtx& c) {
         }
       }
       o = (o4[0] + o4[1]) + (o4[2] + o4[3]);
+      MSD_TRACE_POINT(wv == 0, l, 30);
     }
     lds_bump(c.ctr + 2, lane);   // this wave is done with the cached rows of layer l
     c.ow[wv * kDh + lane] = o;
@@ -961,35 +975,29 @@ __device__ void att_waves(const Args& a, const AttCtx& c) {
     wsync(c.ctr, ws, kWavesA, lane, a.ctrl);
     MSD_TRACE_POINT(wv == 0, l, 26);
     {   // merge the blocks and the current position (log-sum-exp); every wave computes the
-        // result and stores one replica
-      float mv[kWavesA], lv[kWavesA], ov[kWavesA];
-#pragma unroll
-      for (int w = 0; w < kWavesA; ++w) {
-        mv[w] = c.mw[w];
-        lv[w] = c.lw[w];
-        ov[w] = c.ow[w * kDh + lane];
-      }
+        // result and stores one replica.  Lane w < 8 holds block w's max and sum.
+      const float mv = lane < kWavesA ? c.mw[lane] : -INFINITY;
+      const float lv = lane < kWavesA ? c.lw[lane] : 0.f;
       const float scur = c.has_cur ? wave_sum(sq[lane] * sq[kDh + lane]) * 0.125f : -INFINITY;
-      float M = scur;
-#pragma unroll
-      for (int w = 0; w < kWavesA; ++w) M = lv[w] > 0.f ? fmaxf(M, mv[w]) : M;
+      const float M = fmaxf(wave_max(lv > 0.f ? mv : -INFINITY), scur);
       float Ls = 0.f, O = 0.f;
       if (M != -INFINITY) {
+        const float f = lv > 0.f ? expf(mv - M) : 0.f;   // block weights, one exp per lane
+        Ls = wave_sum(f * lv);
 #pragma unroll
-        for (int w = 0; w < kWavesA; ++w) {
-          const float f = lv[w] > 0.f ? expf(mv[w] - M) : 0.f;
-          Ls += f * lv[w];
-          O += f * ov[w];
-        }
+        for (int w = 0; w < kWavesA; ++w)
+          O += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(f), w)) * c.ow[w * kDh + lane];
         if (c.has_cur) {
-          const float f = expf(scur - M);
-          Ls += f;
-          O += f * sq[2 * kDh + lane];
+          const float fc = expf(scur - M);
+          Ls += fc;
+          O += fc * sq[2 * kDh + lane];
         }
       }
-      uint64_t* dst = X + lay.x_att + c.part + wv * lay.x_rep;   // replica wv (kWavesA == kRep)
-      st_tag(dst + 2 + lane, O, c.tag);
-      if (lane < 2) st_tag(dst + lane, lane == 0 ? M : Ls, c.tag);
+      for (int r = wv; r < kRep; r += kWavesA) {   // replicas wv, wv + 8, ...
+        uint64_t* dst = X + lay.x_att + c.part + r * lay.x_rep;
+        st_tag(dst + 2 + lane, O, c.tag);
+        if (lane < 2) st_tag(dst + lane, lane == 0 ? M : Ls, c.tag);
+      }
       MSD_TRACE_POINT(wv == 0, l, 27);
     }
   }
@@ -1013,9 +1021,12 @@ __global__ __launch_bounds__(kThreadsWG, 1) void decode_step_kernel(Args a) {
     c.h = item / a.nsplit;
     const int s = item % a.nsplit;
     c.g = c.h / (a.H / a.KV);
-    c.lo = s * a.cap;
-    c.ncached = max(0, min(a.pos, c.lo + a.cap) - c.lo);
-    c.has_cur = a.pos >= c.lo && a.pos < c.lo + a.cap;
+    // the cached positions [0, pos) are cut into nsplit equal ranges (at most cap each); the
+    // last split also takes the current position
+    const int chunk = cdiv(a.pos, a.nsplit);
+    c.lo = s * chunk;
+    c.ncached = max(0, min(a.pos - c.lo, chunk));
+    c.has_cur = s == a.nsplit - 1;
     c.lane = lane;
     c.wv = wv;
     c.tag = tag;
