@@ -57,6 +57,13 @@ __device__ uint64_t msd_trace_buffer[4096 * 32];
     if ((cond) && (layer) == MSD_TRACE_LAYER && (threadIdx.x & 63) == 0)                  \
       msd_trace_buffer[blockIdx.x * 32 + (slot)] = __builtin_amdgcn_s_memrealtime();      \
   } while (0)
+__device__ uint64_t msd_trace_waves[4096 * 16 * 8];
+#define MSD_TRACE_WAVE(layer, slot)                                                         \
+  do {                                                                                    \
+    if ((layer) == MSD_TRACE_LAYER && (threadIdx.x & 63) == 0)                            \
+      msd_trace_waves[(blockIdx.x * 16 + (threadIdx.x >> 6)) * 8 + (slot)] =              \
+          __builtin_amdgcn_s_memrealtime();                                               \
+  } while (0)
 #define MSD_TRACE_CLOCK(cond, layer, slot)                                                \
   do {                                                                                    \
     if ((cond) && (layer) == MSD_TRACE_LAYER && (threadIdx.x & 63) == 0)                  \
@@ -68,6 +75,9 @@ __device__ uint64_t msd_trace_buffer[4096 * 32];
   } while (0)
 #define MSD_TRACE_CLOCK(cond, layer, slot) \
   do {                                     \
+  } while (0)
+#define MSD_TRACE_WAVE(layer, slot) \
+  do {                              \
   } while (0)
 #endif
 
@@ -277,12 +287,19 @@ __device__ __forceinline__ bool repoll(uint64_t (&wd)[NK], const uint64_t* src, 
 // sooner, and an early round over words still being written costs a full round trip
 // (measured: 9% per token).
 constexpr int kFirstPoll = 16;
+// The attention partials take the attention workgroups' gather and compute (a few us)
+// before they can land, so that gather starts polling later.
+#ifndef MSD_ATT_FIRST_POLL
+#define MSD_ATT_FIRST_POLL 16
+#endif
+constexpr int kAttFirstPoll = MSD_ATT_FIRST_POLL;
 
-template <int NW, int NK, int SLEEP = 0>
+template <int NW, int NK, int SLEEP = 0, int FIRST = kFirstPoll>
 __device__ __forceinline__ void poll_words(const uint64_t* src, int n, uint32_t tag, float (&v)[NK],
                                            uint32_t* ctrl, int w, int lane, bool& bad) {
   uint64_t wd[NK];
-  __builtin_amdgcn_s_sleep(kFirstPoll);
+  if constexpr (FIRST > 0) __builtin_amdgcn_s_sleep(FIRST > 127 ? 127 : FIRST);
+  if constexpr (FIRST > 127) __builtin_amdgcn_s_sleep(FIRST - 127 > 127 ? 127 : FIRST - 127);
 #pragma unroll
   for (int k = 0; k < NK; ++k) {
     const int i = xidx<NW>(k, w, lane);
@@ -298,11 +315,11 @@ __device__ __forceinline__ void poll_words(const uint64_t* src, int n, uint32_t 
 }
 
 // Gather n tagged words src[0..n) into dst (LDS floats), NW waves sharing the words.
-template <int NW, int NK, int SLEEP = 0>
+template <int NW, int NK, int SLEEP = 0, int FIRST = kFirstPoll>
 __device__ __forceinline__ void gather_x(const uint64_t* src, int n, float* dst, uint32_t tag, uint32_t* ctrl,
                                          int w, int lane, bool& bad) {
   float v[NK];
-  poll_words<NW, NK, SLEEP>(src, n, tag, v, ctrl, w, lane, bad);
+  poll_words<NW, NK, SLEEP, FIRST>(src, n, tag, v, ctrl, w, lane, bad);
 #pragma unroll
   for (int k = 0; k < NK; ++k) {
     const int i = xidx<NW>(k, w, lane);
@@ -631,14 +648,16 @@ __device__ void row_worker(const Args& a, const RowCtx& c, int token) {
     {
       XV<NLD> xv;
       norm(xv);
+      MSD_TRACE_POINT(wv == 0, l, 11);
       const uint8_t* rows[2 * QPW];
 #pragma unroll
       for (int i = 0; i < QPW; ++i) {
         rows[2 * i] = at(a.ring_q, wv + kWavesR * i, nq, 2 * D * 2);
         rows[2 * i + 1] = rows[2 * i] + D * 2;
       }
-      float sd[2 * QPW];
-      dot_rows<NLD, 2 * QPW>(rows, xv, D, lane, sd);
+      float sd[2 * QPW] = {};
+      if (count(nq, QPW) > 0) dot_rows<NLD, 2 * QPW>(rows, xv, D, lane, sd);   // idle waves leave the SIMD to others
+      MSD_TRACE_POINT(wv == 0, l, 14);
       release();
       float y[2 * QPW];
       int ix[2 * QPW];
@@ -675,15 +694,17 @@ __device__ void row_worker(const Args& a, const RowCtx& c, int token) {
     MSD_TRACE_POINT(wv == 0, l, 17);
     // ---- attention partials of every (head, split) -> attention vector (multi_sm_decode.py:243-259)
     if (a.nsplit == 1)
-      gather_x<kWavesR, NKA1>(X + lay.x_att + myrep, natt * kPart, c.xa, c.tag, a.ctrl, wv, lane, bad);
+      gather_x<kWavesR, NKA1, 0, kAttFirstPoll>(X + lay.x_att + myrep, natt * kPart, c.xa, c.tag, a.ctrl, wv, lane, bad);
     else
-      gather_x<kWavesR, NKA2>(X + lay.x_att + myrep, natt * kPart, c.xa, c.tag, a.ctrl, wv, lane, bad);
+      gather_x<kWavesR, NKA2, 0, kAttFirstPoll>(X + lay.x_att + myrep, natt * kPart, c.xa, c.tag, a.ctrl, wv, lane, bad);
+    MSD_TRACE_POINT(wv == 0, l, 3);
     bar();
+    MSD_TRACE_POINT(wv == 0, l, 4);
     if (a.nsplit == 1) {
       for (int i = wv * 64 + lane; i < D; i += kWavesR * 64) {
         const float* ps = c.xa + (i / kDh) * kPart;
         const float den = ps[1];
-        c.xatt[i] = den > 0.f ? ps[2 + i % kDh] / den : 0.f;
+        c.xatt[i] = den > 0.f ? ps[2 + i % kDh] * (1.f / den) : 0.f;
       }
     } else {
       for (int i = wv * 64 + lane; i < D; i += kWavesR * 64) {
@@ -720,8 +741,8 @@ __device__ void row_worker(const Args& a, const RowCtx& c, int token) {
         rows[i] = at(a.ring_o, wv + kWavesR * i, no, D * 2);
         ix[i] = int(lay.x_hd1) + c.or0 + wv + kWavesR * i;
       }
-      float y[ORW];
-      dot_rows<NLD, ORW>(rows, xv, D, lane, y);
+      float y[ORW] = {};
+      if (count(no, ORW) > 0) dot_rows<NLD, ORW>(rows, xv, D, lane, y);
       release();
       store_out<ORW>(X, y, ix, count(no, ORW), true, lay.x_rep, c.tag, lane);
     }
@@ -734,10 +755,12 @@ __device__ void row_worker(const Args& a, const RowCtx& c, int token) {
     add_res(c.xhd1);
     weights(4 * l + 2);
     MSD_TRACE_POINT(wv == 0, l, 20);
+    MSD_TRACE_WAVE(l, 0);
     {
       XV<NLD> xv;
       norm(xv);
       MSD_TRACE_POINT(wv == 0, l, 8);
+      MSD_TRACE_WAVE(l, 1);
       const uint8_t* rows[2 * GPW];
       int ix[GPW];
 #pragma unroll
@@ -746,9 +769,10 @@ __device__ void row_worker(const Args& a, const RowCtx& c, int token) {
         rows[2 * i + 1] = rows[2 * i] + D * 2;
         ix[i] = int(lay.x_act) + c.f0 + wv + kWavesR * i;
       }
-      float gu[2 * GPW];
-      dot_rows<NLD, 2 * GPW>(rows, xv, D, lane, gu);
+      float gu[2 * GPW] = {};
+      if (count(ng, GPW) > 0) dot_rows<NLD, 2 * GPW>(rows, xv, D, lane, gu);
       MSD_TRACE_POINT(wv == 0, l, 9);
+      MSD_TRACE_WAVE(l, 2);
       release();
       float y[GPW];
 #pragma unroll
@@ -758,8 +782,10 @@ __device__ void row_worker(const Args& a, const RowCtx& c, int token) {
       }
       store_out<GPW>(X, y, ix, count(ng, GPW), true, lay.x_rep, c.tag, lane);
       MSD_TRACE_POINT(wv == 0, l, 10);
+      MSD_TRACE_WAVE(l, 3);
     }
     bar();
+    MSD_TRACE_WAVE(l, 4);
     MSD_TRACE_POINT(wv == 0, l, 21);
     // ---- act -> LDS; down rows (multi_sm_decode.py:273-291)
     gather_x<kWavesR, NKF>(X + lay.x_act + myrep, a.ff, c.xact, c.tag, a.ctrl, wv, lane, bad);
@@ -777,8 +803,9 @@ __device__ void row_worker(const Args& a, const RowCtx& c, int token) {
         rows[i] = at(a.ring_d, wv + kWavesR * i, no, FF * 2);
         ix[i] = int(lay.x_hd2) + c.or0 + wv + kWavesR * i;
       }
-      float y[ORW];
-      dot_rows<NLF, ORW>(rows, xv, FF, lane, y);
+      float y[ORW] = {};
+      if (count(no, ORW) > 0) dot_rows<NLF, ORW>(rows, xv, FF, lane, y);
+      MSD_TRACE_POINT(wv == 0, l, 15);
       release();
       store_out<ORW>(X, y, ix, count(no, ORW), true, lay.x_rep, c.tag, lane);
     }
@@ -1258,6 +1285,9 @@ extern "C" int32_t msd_check_status(void* workspace, void* stream) {
 }
 
 #ifdef MSD_TRACE
+extern "C" int msd_trace_waves_copy(void* host) {
+  return hipMemcpyFromSymbol(host, HIP_SYMBOL(msd::msd_trace_waves), sizeof(uint64_t) * 4096 * 16 * 8) == hipSuccess ? 0 : -1;
+}
 extern "C" int msd_trace_copy(void* host) {
   return hipMemcpyFromSymbol(host, HIP_SYMBOL(msd::msd_trace_buffer), sizeof(uint64_t) * 4096 * 32) == hipSuccess ? 0 : -1;
 }
