@@ -4,6 +4,7 @@
   stream_tokens(params, config, prompt_ids, max_tokens, temperature,
                 top_p, rep_penalty, seed)                                 generate.py:92-123
   generate_tokens(...)                                                    generate.py:126-130
+  main()  (python -m transformer_amd.generate)                           generate.py:133-236
 
 Sampling runs on the device (``msd_sample_token``): the logits never leave the GPU and the
 drawn token feeds the next decode step on the device.  The uniform draw of each sampled
@@ -212,3 +213,99 @@ def generate_tokens(params, config, prompt_ids, n_tokens=128, temperature=0.0, t
     us = _uniforms(n_tokens, temperature, seed)
     return list(run_generation(dec, [int(t) for t in prompt_ids], n_tokens, temperature, top_p,
                                rep_penalty, uniforms=us, sync_each=False))
+
+
+def main(argv=None):
+    """Command line text generation from a trained checkpoint (generate.py:133-236).
+
+    ``python -m transformer_amd.generate --prompt TEXT --weights weights.pkl`` with the
+    reference's options (--max-tokens, --no-stream, --temp, --top-p, --rep-penalty,
+    --seed).  Relative ``--weights`` paths are taken from the working directory; the
+    tokenizer comes from ``--tokenizer`` (a data directory holding ``bpe_vocab.pkl``, that
+    file itself, or a ``tokenizer.json``), by default the ``data`` directory beside the
+    weights file, the reference's layout.  Generated text goes to stdout, the model summary
+    and timing to stderr, as in the reference.
+    """
+    import argparse
+    import os
+    import sys
+    import time
+
+    from .checkpoint import load_bpe_vocab, load_weights
+
+    parser = argparse.ArgumentParser(description="Generate text with the MI355X decode kernels")
+    parser.add_argument("--prompt", type=str, default="Once upon a time", help="Text prompt to continue")
+    parser.add_argument("--max-tokens", type=int, default=256, help="Maximum tokens to generate")
+    parser.add_argument("--weights", type=str, default="weights.pkl", help="Path to weights file")
+    parser.add_argument("--tokenizer", type=str, default=None,
+                        help="data directory with bpe_vocab.pkl, that file, or a tokenizer.json")
+    parser.add_argument("--no-stream", action="store_true", help="Generate all tokens at once (no streaming)")
+    parser.add_argument("--temp", type=float, default=0.0, help="Sampling temperature (0 = greedy)")
+    parser.add_argument("--top-p", type=float, default=1.0, help="Nucleus sampling threshold")
+    parser.add_argument("--rep-penalty", type=float, default=1.0, help="Repetition penalty (1.0 = off)")
+    parser.add_argument("--seed", type=int, default=None, help="Random seed for reproducible sampling")
+    parser.add_argument("--device", type=str, default="cuda", help="torch device of the GPU")
+    args = parser.parse_args(argv)
+
+    params, config = load_weights(args.weights)
+    tok_src = args.tokenizer or os.path.join(os.path.dirname(os.path.abspath(args.weights)), "data")
+    bpe = load_bpe_vocab(tok_src)
+    decode_fn, encode_fn = bpe["decode_fn"], bpe["encode_fn"]
+    ctx_len = config["context_len"]
+
+    print(f"Model: d={config['d_model']} h={config['n_heads']} l={config['n_layers']} ctx={ctx_len}",
+          file=sys.stderr)
+    print(f"Params: {sum(p.size for p in params.values()):,}", file=sys.stderr)
+    if args.temp > 0:
+        print(f"Sampling: temp={args.temp} top_p={args.top_p} rep_penalty={args.rep_penalty}", file=sys.stderr)
+    else:
+        print("Decoding: greedy (argmax)", file=sys.stderr)
+    print(file=sys.stderr)
+
+    prompt_ids = list(encode_fn(args.prompt))
+    if len(prompt_ids) >= ctx_len:
+        prompt_ids = prompt_ids[:ctx_len - 1]
+    if not prompt_ids:
+        raise SystemExit("the prompt encodes to no tokens")
+    max_gen = min(args.max_tokens, ctx_len - len(prompt_ids))
+
+    print(f"Prompt ({len(prompt_ids)} tokens): {args.prompt}", file=sys.stderr)
+    print(f"Generating {max_gen} tokens...", file=sys.stderr)
+    print(file=sys.stderr)
+    sys.stdout.write(args.prompt)
+    sys.stdout.flush()
+
+    t0 = time.perf_counter()
+    if args.no_stream:
+        tokens = generate_tokens(params, config, prompt_ids, max_gen, args.temp, args.top_p,
+                                 args.rep_penalty, args.seed, device=args.device)
+        elapsed = time.perf_counter() - t0
+        sys.stdout.write(decode_fn(tokens))
+        sys.stdout.write("\n")
+        sys.stdout.flush()
+        print(f"\n[{max_gen} tokens in {elapsed * 1000:.0f}ms = {max_gen / elapsed:.0f} tok/s"
+              f" (includes weight packing)]", file=sys.stderr)
+        return tokens
+    tokens, t_first = [], None
+    for token_id in stream_tokens(params, config, prompt_ids, max_gen, args.temp, args.top_p,
+                                  args.rep_penalty, args.seed, device=args.device):
+        if t_first is None:
+            t_first = time.perf_counter()
+        tokens.append(token_id)
+        new_text = decode_fn([token_id])
+        if new_text:
+            sys.stdout.write(new_text)
+            sys.stdout.flush()
+    elapsed = time.perf_counter() - t0
+    sys.stdout.write("\n")
+    sys.stdout.flush()
+    ttft = (t_first - t0) * 1000 if t_first else 0
+    decode_time = elapsed - (t_first - t0) if t_first else elapsed
+    decode_tok_s = (max_gen - 1) / decode_time if decode_time > 0 else 0
+    print(f"\n[{max_gen} tokens, TTFT={ttft:.0f}ms (includes weight packing), decode={decode_tok_s:.0f} tok/s]",
+          file=sys.stderr)
+    return tokens
+
+
+if __name__ == "__main__":
+    main()
