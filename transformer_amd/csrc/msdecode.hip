@@ -12,14 +12,16 @@
 //     idle device), so workgroups may wait on each other.
 //   * two kinds of workgroups:
 //       - row workgroups (all but the last H * nsplit) own fixed output rows of every
-//         projection and of the tied logits.  4 compute waves take the dot products,
-//         4 exchange waves keep the residual stream h, apply residual adds and RMSNorms,
-//         publish this workgroup's outputs and gather the next phase's input, and a
-//         loader wave streams the weight rows by DMA into an LDS ring one layer ahead;
+//         projection and of the tied logits.  A loader wave streams this workgroup's rows
+//         by DMA (global_load_lds) into an LDS ring one layer ahead; 8 worker waves, all
+//         alike, keep the residual stream h in registers, take the RMSNorms, the dot
+//         products of their rows from LDS, store the outputs and gather an eighth of the
+//         next input vector each;
 //       - attention workgroups (one per query head and context split of 512 positions)
 //         hold their KV head's cached rows in LDS (bf16, streamed in by their loader wave
-//         during the previous layer), gather the head's q and the new k, v, and publish
-//         the head's (max, sum, unnormalised output); row workgroups merge the splits.
+//         during the previous layer); 8 attention waves poll the head's q, take the scores
+//         of a block of positions on the matrix cores and P.V on the vector units, poll the
+//         new k, v and merge the blocks by log-sum-exp.
 //   * weights are bf16 in an (out, in) row layout: every output element is one contiguous
 //     dot product; a lane reads 16 bytes (8 bf16) per 512-element block from LDS, widens
 //     them to f32 and the wave reduces with DPP.  All activation arithmetic is f32.
@@ -27,9 +29,8 @@
 //     written with device-scope atomic stores and polled with device-scope atomic loads.
 //     A word carries its own validity, so no separate flag, fence or barrier is needed;
 //     each (layer, exchange) has its own buffer so tags only need to differ per step.
-//     Weight and KV streaming goes through the LDS-DMA path (global_load_lds), whose
-//     returns do not queue ahead of the exchange waves' polls the way loads into
-//     registers do.
+//     Weight and KV streaming goes through the LDS-DMA path, whose returns do not queue
+//     ahead of the polls the way loads into registers do.
 //   * per layer and row workgroup: QKV rows (+RoPE, KV write) -> attention (attention
 //     workgroups) -> O rows (+residual) -> gate/up rows (+SwiGLU) -> down rows
 //     (+residual); then final RMSNorm, vocabulary rows of the tied embedding, argmax via
@@ -119,6 +120,12 @@ struct Layout {
 
 __host__ __device__ inline int att_cap(int ctx) { return ctx < kAttCap ? ctx : kAttCap; }
 __host__ __device__ inline int att_splits(int ctx) { return cdiv(ctx, att_cap(ctx)); }
+// Attention words per replica: with one split, the normalised head outputs (H * 64); with
+// several, every (head, split)'s (max, sum, unnormalised output) for the row workgroups to merge.
+__host__ __device__ inline int64_t att_words(int H, int ctx) {
+  const int ns = att_splits(ctx);
+  return ns == 1 ? int64_t(H) * kDh : int64_t(H) * ns * kPart;
+}
 
 __host__ __device__ inline Layout make_layout(int d, int H, int KV, int ff, int ctx) {
   Layout t;
@@ -132,7 +139,7 @@ __host__ __device__ inline Layout make_layout(int d, int H, int KV, int ff, int 
   t.layer_elems = t.off_dn + int64_t(d) * ff;
   t.x_qkv = 0;
   t.x_att = align64(nqkv);
-  t.x_hd1 = t.x_att + align64(int64_t(H) * att_splits(ctx) * kPart);
+  t.x_hd1 = t.x_att + align64(att_words(H, ctx));
   t.x_act = t.x_hd1 + align64(d);
   t.x_hd2 = t.x_act + align64(ff);
   // replicas at a stride that is not a multiple of 4 KB spread the reads over channels
@@ -559,7 +566,6 @@ __device__ void row_worker(const Args& a, const RowCtx& c, int token) {
   constexpr int HPW = (D + 64 * kWavesR - 1) / (64 * kWavesR);    // d-vector words per lane
   constexpr int NKF = (FF + 64 * kWavesR - 1) / (64 * kWavesR);   // act words per lane
   constexpr int H = D / kDh;
-  constexpr int NKA1 = (H * kPart + 64 * kWavesR - 1) / (64 * kWavesR);       // attention words, 1 split
   constexpr int NKA2 = (2 * H * kPart + 64 * kWavesR - 1) / (64 * kWavesR);   // 2 splits
   const int lane = c.lane, wv = c.wv;
   const Layout& lay = a.lay;
@@ -692,21 +698,17 @@ __device__ void row_worker(const Args& a, const RowCtx& c, int token) {
     load_vec(sc, layer_w(a, l) + lay.off_ln2);   // scale of the next norm
     bar();   // every QKV output of this workgroup is issued
     MSD_TRACE_POINT(wv == 0, l, 17);
-    // ---- attention partials of every (head, split) -> attention vector (multi_sm_decode.py:243-259)
-    if (a.nsplit == 1)
-      gather_x<kWavesR, NKA1, 0, kAttFirstPoll>(X + lay.x_att + myrep, natt * kPart, c.xa, c.tag, a.ctrl, wv, lane, bad);
-    else
-      gather_x<kWavesR, NKA2, 0, kAttFirstPoll>(X + lay.x_att + myrep, natt * kPart, c.xa, c.tag, a.ctrl, wv, lane, bad);
-    MSD_TRACE_POINT(wv == 0, l, 3);
-    bar();
-    MSD_TRACE_POINT(wv == 0, l, 4);
+    // ---- attention vector (multi_sm_decode.py:243-259): with one split the attention
+    //      workgroups publish each head's normalised output, gathered straight into xatt;
+    //      with several, the (head, split) partials are merged here by log-sum-exp
     if (a.nsplit == 1) {
-      for (int i = wv * 64 + lane; i < D; i += kWavesR * 64) {
-        const float* ps = c.xa + (i / kDh) * kPart;
-        const float den = ps[1];
-        c.xatt[i] = den > 0.f ? ps[2 + i % kDh] * (1.f / den) : 0.f;
-      }
+      gather_x<kWavesR, HPW, 0, kAttFirstPoll>(X + lay.x_att + myrep, D, c.xatt, c.tag, a.ctrl, wv, lane, bad);
+      MSD_TRACE_POINT(wv == 0, l, 3);
     } else {
+      gather_x<kWavesR, NKA2, 0, kAttFirstPoll>(X + lay.x_att + myrep, natt * kPart, c.xa, c.tag, a.ctrl, wv, lane, bad);
+      MSD_TRACE_POINT(wv == 0, l, 3);
+      bar();
+      MSD_TRACE_POINT(wv == 0, l, 4);
       for (int i = wv * 64 + lane; i < D; i += kWavesR * 64) {
         const int hd = i / kDh, dim = i % kDh;
         float M = -INFINITY;
@@ -885,13 +887,14 @@ struct AttCtx {
   int h, g, lo, ncached, lane, wv;
   bool has_cur;
   uint32_t tag;
-  int64_t part;     // word offset of this (head, split) in the attention partials
+  int64_t part;     // word offset of this head's output (one split) or (head, split)'s partials
   uint8_t* K;       // cap rows of kKRowB bytes (bf16 K, post-RoPE)
   uint8_t* V;       // cap rows of kVRowB bytes
-  float* sq;        // [2][3][64]: q, new k, new v (double-buffered by layer parity)
-  float* ow;        // [kWavesA][64] partial outputs
-  float* mw;        // [kWavesA] partial maxima
-  float* lw;        // [kWavesA] partial sums
+  float* sqw;       // [kWavesA][64]: each wave's q (A-operand staging)
+  float* pw;        // [kWavesA][64]: each wave's softmax weights in P.V order
+  float* ow;        // [2][kWavesA][64] block outputs (double-buffered by layer parity)
+  float* mw;        // [2][kWavesA] block maxima
+  float* lw;        // [2][kWavesA] block sums
   int* ctr;         // [0] wave sync, [1] KV layers loaded, [2] KV layers consumed (wave bumps)
 };
 
@@ -925,87 +928,176 @@ __device__ void att_loader(const Args& a, const AttCtx& c) {
   }
 }
 
+// Three bf16 parts of x, taken by truncation: x = hi + mid + lo exactly (each part holds the
+// next 8 significant bits), so products with bf16 K values summed in f32 reproduce f32
+// products.  sel[i] is all ones for the part this lane holds (at most one), so the result
+// (in the high 16 bits) is that part, or 0.  Branch-free: the lanes of a wave hold
+// different parts.
+__device__ __forceinline__ uint32_t bf16_part(float x, const uint32_t (&sel)[3]) {
+  const uint32_t hb = __float_as_uint(x) & 0xffff0000u;
+  const float r1 = x - __uint_as_float(hb);
+  const uint32_t mb = __float_as_uint(r1) & 0xffff0000u;
+  const uint32_t lb = __float_as_uint(r1 - __uint_as_float(mb));
+  return (hb & sel[0]) | (mb & sel[1]) | (lb & sel[2]);
+}
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ bf16x8 as_bf16x8(uint4 u) { return __builtin_bit_cast(bf16x8, u); }
+
+// Attention waves.  Per layer every wave polls the head's q itself (lane = dim), takes a
+// block of the cached positions (block size a multiple of 16, at most 64, so that all waves
+// share the rows) and computes
+//   scores on the matrix cores: v_mfma_f32_16x16x32_bf16 with A = the three bf16 parts of q
+//     in rows 0..2 (zero elsewhere) and B = 16 K rows from LDS, so lanes 0..15 receive the
+//     three partial scores of 16 positions in one tile (two products per 64 dims);
+//   softmax over the block (wave max / sum);
+//   P.V on the vector units: lane (g, dq) = (lane / 16, lane % 16) accumulates dims
+//     4 dq .. 4 dq + 3 over positions 4 i + g (two lane groups read two consecutive 128-byte V
+//     rows per half-wave: no bank conflicts), then the four groups are summed.
+// The wave then polls the new k and v (un-rounded, multi_sm_decode.py:197,205), meets the
+// others, and every wave merges the blocks and the current position by log-sum-exp and
+// stores one replica: with one split the normalised head output (the row workgroups'
+// merge, multi_sm_decode.py:243-259, done here), else (max, sum, unnormalised output).
 __device__ void att_waves(const Args& a, const AttCtx& c) {
   const int lane = c.lane, wv = c.wv;
   const Layout& lay = a.lay;
   bool bad = false;
   int ws = 0;
+  const int m16 = lane & 15, kb = lane >> 4;
+  float* sqw = c.sqw + wv * kDh;
+  float* pw = c.pw + wv * kDh;
   for (int l = 0; l < a.L; ++l) {
     uint64_t* X = layer_x(a, l);
-    float* sq = c.sq + (l & 1) * 3 * kDh;
-    // q of the head, new k and v of its KV head (waves 0..2), un-rounded (multi_sm_decode.py:197,205)
-    if (wv < 3) {
-      const int idx = wv == 0 ? c.h * kDh : (wv == 1 ? (a.H + c.g) * kDh : (a.H + a.KV + c.g) * kDh);
-      float v[1];
-      poll_words<1, 1>(X + lay.x_qkv + idx, kDh, c.tag, v, a.ctrl, 0, lane, bad);
-      sq[wv * kDh + lane] = v[0];
-    }
-    wsync(c.ctr, ws, kWavesA, lane, a.ctrl);
+    float* ow = c.ow + (l & 1) * kWavesA * kDh;   // double-buffered: a wave may start the next
+    float* mw = c.mw + (l & 1) * kWavesA;         // layer while another still merges this one
+    float* lw = c.lw + (l & 1) * kWavesA;
+    float qv[1];
+    poll_words<1, 1>(X + lay.x_qkv + c.h * kDh, kDh, c.tag, qv, a.ctrl, 0, lane, bad);
     MSD_TRACE_POINT(wv == 0, l, 24);
+    // new k and v of the KV head: first loads now (they land during the block work), the
+    // rest of the poll after it
+    const uint64_t* kvsrc[2] = {X + lay.x_qkv + (a.H + c.g) * kDh + lane, X + lay.x_qkv + (a.H + a.KV + c.g) * kDh + lane};
+    uint64_t kvw[2] = {uint64_t(c.tag) << 32, uint64_t(c.tag) << 32};
+    if (c.has_cur) {
+      kvw[0] = ld_tag(kvsrc[0]);
+      kvw[1] = ld_tag(kvsrc[1]);
+    }
     lds_wait(c.ctr + 1, l + 1, a.ctrl);   // cached rows of layer l are in LDS
     MSD_TRACE_POINT(wv == 0, l, 25);
-    // block wv: cached rows [bs wv, bs wv + bs), bs a multiple of 16 (at most 64) that
-    // spreads the cached rows over all attention waves
     const int bs = min(64, max(16, (cdiv(c.ncached, kWavesA) + 15) & ~15));
-    float m = -INFINITY, lsum = 0.f, o = 0.f;
+    float m = -INFINITY, lsum = 0.f;
+    float o[4] = {0.f, 0.f, 0.f, 0.f};
     const int r0 = wv * bs;
     if (r0 < c.ncached) {
       const int np = min(bs, c.ncached - r0);
-      // scores: lane = position (rows past np re-read row np - 1 and are masked), q
-      // wave-uniform from LDS
-      const uint8_t* kr = c.K + (r0 + min(lane, np - 1)) * kKRowB;
-      const float4* q4 = reinterpret_cast<const float4*>(sq);
-      uint4 kk[8];
+      const int nt = cdiv(np, 16);
+      // q parts in the A layout: lane row m16 < 3 holds part m16 of dims 32 ch + 8 kb .. + 8
+      sqw[lane] = qv[0];
+      __builtin_amdgcn_s_waitcnt(0xc07f);
+      __builtin_amdgcn_wave_barrier();
+      const uint32_t sel[3] = {m16 == 0 ? ~0u : 0u, m16 == 1 ? ~0u : 0u, m16 == 2 ? ~0u : 0u};
+      uint4 aq[2];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) kk[j] = *reinterpret_cast<const uint4*>(kr + 16 * j);
-      float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+      for (int ch = 0; ch < 2; ++ch) {
+        const float4 x0 = *reinterpret_cast<const float4*>(sqw + 32 * ch + 8 * kb);
+        const float4 x1 = *reinterpret_cast<const float4*>(sqw + 32 * ch + 8 * kb + 4);
+        const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+        uint32_t wd[4];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const float4 qa = q4[2 * j], qb = q4[2 * j + 1];
-        a0 += qa.x * bf_lo(kk[j].x);
-        a1 += qa.y * bf_hi(kk[j].x);
-        a2 += qa.z * bf_lo(kk[j].y);
-        a3 += qa.w * bf_hi(kk[j].y);
-        a0 += qb.x * bf_lo(kk[j].z);
-        a1 += qb.y * bf_hi(kk[j].z);
-        a2 += qb.z * bf_lo(kk[j].w);
-        a3 += qb.w * bf_hi(kk[j].w);
+        for (int j = 0; j < 4; ++j)
+          wd[j] = (bf16_part(xs[2 * j], sel) >> 16) | (bf16_part(xs[2 * j + 1], sel) & 0xffff0000u);
+        aq[ch] = make_uint4(wd[0], wd[1], wd[2], wd[3]);
       }
-      const float s = lane < np ? ((a0 + a1) + (a2 + a3)) * 0.125f : -INFINITY;
-      m = wave_max(s);
-      const float e = (lane < np) ? expf(s - m) : 0.f;
-      lsum = wave_sum(e);
-      MSD_TRACE_POINT(wv == 0, l, 29);
-      // o[lane = dim] = sum_p e[p] * V[p][dim]: 16 positions per batch of LDS reads (rows
-      // past np re-read row np - 1; their weights e are 0), e[p] taken from lane p
-      const uint16_t* vr = reinterpret_cast<const uint16_t*>(c.V + r0 * kVRowB) + lane;
-      float o4[4] = {0.f, 0.f, 0.f, 0.f};
-      for (int p0 = 0; p0 < np; p0 += 16) {
-        float vv[16];
+      // scores: tile t covers positions r0 + 16 t .. + 16 (rows past the cached ones re-read
+      // the last cached row and are masked)
+      uint4 kk[4][2];
 #pragma unroll
-        for (int k = 0; k < 16; ++k) vv[k] = bf2f(vr[min(p0 + k, np - 1) * kDh]);
+      for (int t = 0; t < 4; ++t) {
+        const int row = min(r0 + 16 * t + m16, c.ncached - 1);
+        const uint8_t* kr = c.K + row * kKRowB + 16 * kb;
+        kk[t][0] = *reinterpret_cast<const uint4*>(kr);
+        kk[t][1] = *reinterpret_cast<const uint4*>(kr + 64);
+      }
+      float sv[4];
 #pragma unroll
-        for (int k = 0; k < 16; ++k) {
-          const float ek = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), p0 + k));
-          o4[k & 3] += ek * vv[k];
+      for (int t = 0; t < 4; ++t) {
+        sv[t] = -INFINITY;
+        if (t < nt) {
+          f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(aq[0]), as_bf16x8(kk[t][0]), acc, 0, 0, 0);
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(aq[1]), as_bf16x8(kk[t][1]), acc, 0, 0, 0);
+          if (lane < 16 && 16 * t + lane < np) sv[t] = ((acc[0] + acc[1]) + acc[2]) * 0.125f;
         }
       }
-      o = (o4[0] + o4[1]) + (o4[2] + o4[3]);
+      m = wave_max(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])));
+      float e[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) e[t] = expf(sv[t] - m);   // 0 for masked positions
+      lsum = wave_sum((e[0] + e[1]) + (e[2] + e[3]));
+      // weights to LDS in the P.V order: position q at slot (q % 4) * 16 + q / 4
+      if (lane < 16) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const int q = 16 * t + lane;
+          pw[(q & 3) * 16 + (q >> 2)] = e[t];
+        }
+      }
+      MSD_TRACE_POINT(wv == 0, l, 29);
+      __builtin_amdgcn_s_waitcnt(0xc07f);
+      __builtin_amdgcn_wave_barrier();
+      const int g = kb, dq = m16;
+      const int steps = cdiv(np, 4);
+      const uint8_t* vb = c.V + r0 * kVRowB + 8 * dq;
+      for (int i4 = 0; i4 < steps; i4 += 4) {
+        const float4 p4 = *reinterpret_cast<const float4*>(pw + g * 16 + i4);
+        const float pk[4] = {p4.x, p4.y, p4.z, p4.w};
+        uint2 vv[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+          vv[k] = *reinterpret_cast<const uint2*>(vb + min(4 * (i4 + k) + g, np - 1) * kVRowB);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          o[0] += pk[k] * bf_lo(vv[k].x);
+          o[1] += pk[k] * bf_hi(vv[k].x);
+          o[2] += pk[k] * bf_lo(vv[k].y);
+          o[3] += pk[k] * bf_hi(vv[k].y);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) o[j] += __shfl_xor(o[j], 16);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) o[j] += __shfl_xor(o[j], 32);
       MSD_TRACE_POINT(wv == 0, l, 30);
     }
     lds_bump(c.ctr + 2, lane);   // this wave is done with the cached rows of layer l
-    c.ow[wv * kDh + lane] = o;
+    if (lane < 16) *reinterpret_cast<float4*>(ow + wv * kDh + 4 * lane) = make_float4(o[0], o[1], o[2], o[3]);
     if (lane == 0) {
-      c.mw[wv] = m;
-      c.lw[wv] = lsum;
+      mw[wv] = m;
+      lw[wv] = lsum;
     }
+    {
+      uint32_t spins = 0;
+      bool ok = false;
+      while (!bad && !__all(ok)) {
+        ok = true;
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+          if (uint32_t(kvw[i] >> 32) != c.tag) {
+            ok = false;
+            kvw[i] = ld_tag(kvsrc[i]);
+          }
+        if (!__all(ok)) spin_step(spins, a.ctrl, lane, bad);
+      }
+    }
+    const float kv2[2] = {__uint_as_float(uint32_t(kvw[0])), __uint_as_float(uint32_t(kvw[1]))};
     wsync(c.ctr, ws, kWavesA, lane, a.ctrl);
     MSD_TRACE_POINT(wv == 0, l, 26);
-    {   // merge the blocks and the current position (log-sum-exp); every wave computes the
-        // result and stores one replica.  Lane w < 8 holds block w's max and sum.
-      const float mv = lane < kWavesA ? c.mw[lane] : -INFINITY;
-      const float lv = lane < kWavesA ? c.lw[lane] : 0.f;
-      const float scur = c.has_cur ? wave_sum(sq[lane] * sq[kDh + lane]) * 0.125f : -INFINITY;
+    {   // merge the blocks and the current position (log-sum-exp).  Lane w < 8 holds block
+        // w's max and sum.
+      const float mv = lane < kWavesA ? mw[lane] : -INFINITY;
+      const float lv = lane < kWavesA ? lw[lane] : 0.f;
+      const float scur = c.has_cur ? wave_sum(qv[0] * kv2[0]) * 0.125f : -INFINITY;
       const float M = fmaxf(wave_max(lv > 0.f ? mv : -INFINITY), scur);
       float Ls = 0.f, O = 0.f;
       if (M != -INFINITY) {
@@ -1013,17 +1105,22 @@ __device__ void att_waves(const Args& a, const AttCtx& c) {
         Ls = wave_sum(f * lv);
 #pragma unroll
         for (int w = 0; w < kWavesA; ++w)
-          O += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(f), w)) * c.ow[w * kDh + lane];
+          O += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(f), w)) * ow[w * kDh + lane];
         if (c.has_cur) {
           const float fc = expf(scur - M);
           Ls += fc;
-          O += fc * sq[2 * kDh + lane];
+          O += fc * kv2[1];
         }
       }
-      for (int r = wv; r < kRep; r += kWavesA) {   // replicas wv, wv + 8, ...
-        uint64_t* dst = X + lay.x_att + c.part + r * lay.x_rep;
-        st_tag(dst + 2 + lane, O, c.tag);
-        if (lane < 2) st_tag(dst + lane, lane == 0 ? M : Ls, c.tag);
+      if (a.nsplit == 1) {
+        const float y = Ls > 0.f ? O * (1.f / Ls) : 0.f;
+        for (int r = wv; r < kRep; r += kWavesA) st_tag(X + lay.x_att + c.part + r * lay.x_rep + lane, y, c.tag);
+      } else {
+        for (int r = wv; r < kRep; r += kWavesA) {   // replicas wv, wv + 8, ...
+          uint64_t* dst = X + lay.x_att + c.part + r * lay.x_rep;
+          st_tag(dst + 2 + lane, O, c.tag);
+          if (lane < 2) st_tag(dst + lane, lane == 0 ? M : Ls, c.tag);
+        }
       }
       MSD_TRACE_POINT(wv == 0, l, 27);
     }
@@ -1057,14 +1154,15 @@ __global__ __launch_bounds__(kThreadsWG, 1) void decode_step_kernel(Args a) {
     c.lane = lane;
     c.wv = wv;
     c.tag = tag;
-    c.part = int64_t(item) * kPart;
+    c.part = a.nsplit == 1 ? int64_t(c.h) * kDh : int64_t(item) * kPart;
     c.K = smem;
     c.V = c.K + cdiv(a.cap * 9, 64) * 1024;
-    c.sq = reinterpret_cast<float*>(c.V + cdiv(a.cap, 8) * 1024);
-    c.ow = c.sq + 2 * 3 * kDh;
-    c.mw = c.ow + kWavesA * kDh;
-    c.lw = c.mw + kWavesA;
-    c.ctr = reinterpret_cast<int*>(c.lw + kWavesA);
+    c.sqw = reinterpret_cast<float*>(c.V + cdiv(a.cap, 8) * 1024);
+    c.pw = c.sqw + kWavesA * kDh;
+    c.ow = c.pw + kWavesA * kDh;
+    c.mw = c.ow + 2 * kWavesA * kDh;
+    c.lw = c.mw + 2 * kWavesA;
+    c.ctr = reinterpret_cast<int*>(c.lw + 2 * kWavesA);
     if (threadIdx.x < 4) c.ctr[threadIdx.x] = 0;
     __syncthreads();   // the only workgroup barrier; the roles below meet on LDS counters
     if (wv == kLoader) att_loader(a, c);
@@ -1156,7 +1254,7 @@ static bool make_plan(const msd_config* c, int G, Plan* p) {
   const int natt = H * p->nsplit * kPart;
   const int row_other = 4 * (3 * D + ((ff + 3) & ~3) + ((natt + 3) & ~3) + 8 + 2 * kWavesR);
   const int att_lds = cdiv(p->cap * 9, 64) * 1024 + cdiv(p->cap, 8) * 1024 +
-                      4 * (2 * 3 * kDh + kWavesA * kDh + 2 * kWavesA + 4);
+                      4 * (4 * kWavesA * kDh + 4 * kWavesA + 4);
   const int budget = std::max(std::max(att_lds, kMinLds), ring + row_other);
   ring = std::max(ring, (budget - row_other) / 2048 * 2048);   // spare LDS widens the logit halves
   p->ring_bytes = ring;
