@@ -100,7 +100,19 @@ constexpr int kMbox = 8;         // outputs per compute wave and phase
 #endif
 constexpr int kRep = MSD_REPLICAS;   // replicas of every vector all row workgroups gather
 static_assert(kRep % kWavesA == 0 && kRep <= 64, "attention waves store whole sets of replicas");
-constexpr int kDmaWindow = 48;   // 1 KB DMA instructions a loader keeps in flight
+// 1 KB DMA instructions a loader keeps in flight.  Fewer bytes in flight across the device
+// shorten the round trip of the exchange polls; the layer weights and KV rows need only a
+// few per CU to stay a layer ahead, the logit rows at the end stream with a wide window.
+#ifndef MSD_DMA_LAYER
+#define MSD_DMA_LAYER 8
+#endif
+#ifndef MSD_DMA_KV
+#define MSD_DMA_KV 16
+#endif
+#ifndef MSD_DMA_LOGITS
+#define MSD_DMA_LOGITS 48
+#endif
+constexpr int kDmaLayer = MSD_DMA_LAYER, kDmaKV = MSD_DMA_KV, kDmaLogits = MSD_DMA_LOGITS;
 
 constexpr uint32_t kStatusTimeout = 1u;
 constexpr uint32_t kStatusBadToken = 2u;
@@ -384,17 +396,18 @@ __device__ __forceinline__ void wsync(int* ctr, int& phase, int n, int lane, uin
 
 // ---------------------------------------------------------------- LDS-DMA streaming
 // global_load_lds_dwordx4: lane i copies 16 bytes from its global address to
-// lds_base + 16 * i.  A loader keeps at most kDmaWindow instructions in flight.
+// lds_base + 16 * i.  A loader keeps at most W instructions in flight.
 __device__ __forceinline__ constexpr int vmcnt_imm(int k) {
   return (k & 0xF) | ((k >> 4) << 14) | (7 << 4) | (0xF << 8);
 }
+template <int W>
 struct Dma {
   int inflight = 0;
   __device__ __forceinline__ void issue(const void* src, uint8_t* lds_base) {
     __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds_base, 16, 0, 0);
-    if (++inflight == kDmaWindow) {
-      __builtin_amdgcn_s_waitcnt(vmcnt_imm(kDmaWindow - 1));
-      inflight = kDmaWindow - 1;
+    if (++inflight == W) {
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(W - 1));
+      inflight = W - 1;
     }
   }
   __device__ __forceinline__ void drain() {
@@ -406,7 +419,8 @@ struct Dma {
 // Copy `bytes` (a multiple of 16) from src to lds: instruction t covers bytes
 // [1024 t, 1024 t + 1024); lanes past the end re-read the last 16 bytes into the
 // padding that rounds every region up to 1 KB.
-__device__ __forceinline__ void dma_copy(Dma& d, const uint8_t* src, uint8_t* lds, int64_t bytes, int lane) {
+template <int W>
+__device__ __forceinline__ void dma_copy(Dma<W>& d, const uint8_t* src, uint8_t* lds, int64_t bytes, int lane) {
   for (int64_t t = 0; t * 1024 < bytes; ++t) {
     int64_t o = t * 1024 + 16 * lane;
     if (o > bytes - 16) o = bytes - 16;
@@ -515,7 +529,8 @@ template <int D, int FF>
 __device__ void row_loader(const Args& a, const RowCtx& c) {
   const Layout& lay = a.lay;
   const int lane = c.lane;
-  Dma d;
+  Dma<kDmaLayer> d;
+  Dma<kDmaLogits> dl;
   const int half = a.ring_bytes / 2;
   const int njobs = 4 * a.L + c.nlog;
   for (int j = 0; j < njobs; ++j) {
@@ -539,12 +554,16 @@ __device__ void row_loader(const Args& a, const RowCtx& c) {
       off = (k & 1) * half;
       need = k < 2 ? 4 * a.L : 4 * a.L + k - 1;   // every layer job, or logit chunk k - 2
     }
-    if (need > 0 && lds_ld(c.ctr + kCtrUsed) < kWavesR * need) {
-      d.drain();
-      lds_wait(c.ctr + kCtrUsed, kWavesR * need, a.ctrl);
+    if (need > 0 && lds_ld(c.ctr + kCtrUsed) < kWavesR * need) lds_wait(c.ctr + kCtrUsed, kWavesR * need, a.ctrl);
+    if (bytes > 0) {
+      if (j < 4 * a.L) {
+        dma_copy(d, reinterpret_cast<const uint8_t*>(src), c.ring + off, bytes, lane);
+        d.drain();
+      } else {
+        dma_copy(dl, reinterpret_cast<const uint8_t*>(src), c.ring + off, bytes, lane);
+        dl.drain();
+      }
     }
-    if (bytes > 0) dma_copy(d, reinterpret_cast<const uint8_t*>(src), c.ring + off, bytes, lane);
-    d.drain();
     lds_set(c.ctr + kCtrLoaded, j + 1, lane);
     MSD_TRACE_POINT(j < 4 * a.L, j / 4, 28 + (j % 4));
   }
@@ -890,7 +909,7 @@ struct AttCtx {
   int64_t part;     // word offset of this head's output (one split) or (head, split)'s partials
   uint8_t* K;       // cap rows of kKRowB bytes (bf16 K, post-RoPE)
   uint8_t* V;       // cap rows of kVRowB bytes
-  float* sqw;       // [kWavesA][64]: each wave's q (A-operand staging)
+  uint16_t* apw;    // [kWavesA][3][64]: each wave's q as three bf16 parts (A-operand staging)
   float* pw;        // [kWavesA][64]: each wave's softmax weights in P.V order
   float* ow;        // [2][kWavesA][64] block outputs (double-buffered by layer parity)
   float* mw;        // [2][kWavesA] block maxima
@@ -903,7 +922,7 @@ struct AttCtx {
 // 16 bytes per row; the 9th is padding) and V rows (8 slots) into LDS.
 __device__ void att_loader(const Args& a, const AttCtx& c) {
   const int lane = c.lane;
-  Dma d;
+  Dma<kDmaKV> d;
   for (int l = 0; l < a.L; ++l) {
     if (l > 0) lds_wait(c.ctr + 2, kWavesA * l, a.ctrl);
     if (c.ncached > 0) {
@@ -928,17 +947,19 @@ __device__ void att_loader(const Args& a, const AttCtx& c) {
   }
 }
 
-// Three bf16 parts of x, taken by truncation: x = hi + mid + lo exactly (each part holds the
-// next 8 significant bits), so products with bf16 K values summed in f32 reproduce f32
-// products.  sel[i] is all ones for the part this lane holds (at most one), so the result
-// (in the high 16 bits) is that part, or 0.  Branch-free: the lanes of a wave hold
-// different parts.
-__device__ __forceinline__ uint32_t bf16_part(float x, const uint32_t (&sel)[3]) {
-  const uint32_t hb = __float_as_uint(x) & 0xffff0000u;
-  const float r1 = x - __uint_as_float(hb);
-  const uint32_t mb = __float_as_uint(r1) & 0xffff0000u;
-  const uint32_t lb = __float_as_uint(r1 - __uint_as_float(mb));
-  return (hb & sel[0]) | (mb & sel[1]) | (lb & sel[2]);
+// Sum / max over lanes 0..7 (three DPP steps; lanes 8.. must not matter), read from lane 7.
+// For a value that is zero (or -inf) outside lanes 0..7 the sum equals wave_sum's bit for bit.
+__device__ __forceinline__ float sum8(float v) {
+  v += dpp_f(v, 0x111);
+  v += dpp_f(v, 0x112);
+  v += dpp_f(v, 0x114);
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 7));
+}
+__device__ __forceinline__ float max8(float v) {
+  v = fmaxf(v, dppm_f(v, 0x111));
+  v = fmaxf(v, dppm_f(v, 0x112));
+  v = fmaxf(v, dppm_f(v, 0x114));
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 7));
 }
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -965,7 +986,7 @@ __device__ void att_waves(const Args& a, const AttCtx& c) {
   bool bad = false;
   int ws = 0;
   const int m16 = lane & 15, kb = lane >> 4;
-  float* sqw = c.sqw + wv * kDh;
+  uint16_t* apw = c.apw + wv * 3 * kDh;
   float* pw = c.pw + wv * kDh;
   for (int l = 0; l < a.L; ++l) {
     uint64_t* X = layer_x(a, l);
@@ -975,6 +996,18 @@ __device__ void att_waves(const Args& a, const AttCtx& c) {
     float qv[1];
     poll_words<1, 1>(X + lay.x_qkv + c.h * kDh, kDh, c.tag, qv, a.ctrl, 0, lane, bad);
     MSD_TRACE_POINT(wv == 0, l, 24);
+    {   // q = hi + mid + lo exactly, three bf16 parts taken by truncation (each holds the next
+        // 8 significant bits), so bf16 products summed in f32 reproduce the f32 products.
+        // Staged before the loads below: a wait for q must not wait for them.
+      const float x = qv[0];
+      const uint32_t hb = __float_as_uint(x) & 0xffff0000u;
+      const float r1 = x - __uint_as_float(hb);
+      const uint32_t mb = __float_as_uint(r1) & 0xffff0000u;
+      const uint32_t lb = __float_as_uint(r1 - __uint_as_float(mb));
+      apw[lane] = uint16_t(hb >> 16);
+      apw[kDh + lane] = uint16_t(mb >> 16);
+      apw[2 * kDh + lane] = uint16_t(lb >> 16);
+    }
     // new k and v of the KV head: first loads now (they land during the block work), the
     // rest of the poll after it
     const uint64_t* kvsrc[2] = {X + lay.x_qkv + (a.H + c.g) * kDh + lane, X + lay.x_qkv + (a.H + a.KV + c.g) * kDh + lane};
@@ -993,21 +1026,13 @@ __device__ void att_waves(const Args& a, const AttCtx& c) {
       const int np = min(bs, c.ncached - r0);
       const int nt = cdiv(np, 16);
       // q parts in the A layout: lane row m16 < 3 holds part m16 of dims 32 ch + 8 kb .. + 8
-      sqw[lane] = qv[0];
       __builtin_amdgcn_s_waitcnt(0xc07f);
       __builtin_amdgcn_wave_barrier();
-      const uint32_t sel[3] = {m16 == 0 ? ~0u : 0u, m16 == 1 ? ~0u : 0u, m16 == 2 ? ~0u : 0u};
       uint4 aq[2];
 #pragma unroll
       for (int ch = 0; ch < 2; ++ch) {
-        const float4 x0 = *reinterpret_cast<const float4*>(sqw + 32 * ch + 8 * kb);
-        const float4 x1 = *reinterpret_cast<const float4*>(sqw + 32 * ch + 8 * kb + 4);
-        const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-        uint32_t wd[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          wd[j] = (bf16_part(xs[2 * j], sel) >> 16) | (bf16_part(xs[2 * j + 1], sel) & 0xffff0000u);
-        aq[ch] = make_uint4(wd[0], wd[1], wd[2], wd[3]);
+        const uint4 u = *reinterpret_cast<const uint4*>(apw + (m16 < 3 ? m16 : 0) * kDh + 32 * ch + 8 * kb);
+        aq[ch] = m16 < 3 ? u : make_uint4(0u, 0u, 0u, 0u);
       }
       // scores: tile t covers positions r0 + 16 t .. + 16 (rows past the cached ones re-read
       // the last cached row and are masked)
@@ -1044,6 +1069,11 @@ __device__ void att_waves(const Args& a, const AttCtx& c) {
         }
       }
       MSD_TRACE_POINT(wv == 0, l, 29);
+      // k or v not there at the first load: load again now, so the final check after P.V
+      // rarely needs another round trip
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        if (uint32_t(kvw[i] >> 32) != c.tag) kvw[i] = ld_tag(kvsrc[i]);
       __builtin_amdgcn_s_waitcnt(0xc07f);
       __builtin_amdgcn_wave_barrier();
       const int g = kb, dq = m16;
@@ -1098,11 +1128,11 @@ __device__ void att_waves(const Args& a, const AttCtx& c) {
       const float mv = lane < kWavesA ? mw[lane] : -INFINITY;
       const float lv = lane < kWavesA ? lw[lane] : 0.f;
       const float scur = c.has_cur ? wave_sum(qv[0] * kv2[0]) * 0.125f : -INFINITY;
-      const float M = fmaxf(wave_max(lv > 0.f ? mv : -INFINITY), scur);
+      const float M = fmaxf(max8(lv > 0.f ? mv : -INFINITY), scur);
       float Ls = 0.f, O = 0.f;
       if (M != -INFINITY) {
         const float f = lv > 0.f ? expf(mv - M) : 0.f;   // block weights, one exp per lane
-        Ls = wave_sum(f * lv);
+        Ls = sum8(f * lv);
 #pragma unroll
         for (int w = 0; w < kWavesA; ++w)
           O += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(f), w)) * ow[w * kDh + lane];
@@ -1157,8 +1187,8 @@ __global__ __launch_bounds__(kThreadsWG, 1) void decode_step_kernel(Args a) {
     c.part = a.nsplit == 1 ? int64_t(c.h) * kDh : int64_t(item) * kPart;
     c.K = smem;
     c.V = c.K + cdiv(a.cap * 9, 64) * 1024;
-    c.sqw = reinterpret_cast<float*>(c.V + cdiv(a.cap, 8) * 1024);
-    c.pw = c.sqw + kWavesA * kDh;
+    c.apw = reinterpret_cast<uint16_t*>(c.V + cdiv(a.cap, 8) * 1024);
+    c.pw = reinterpret_cast<float*>(c.apw + kWavesA * 3 * kDh);
     c.ow = c.pw + kWavesA * kDh;
     c.mw = c.ow + 2 * kWavesA * kDh;
     c.lw = c.mw + 2 * kWavesA;
@@ -1254,7 +1284,7 @@ static bool make_plan(const msd_config* c, int G, Plan* p) {
   const int natt = H * p->nsplit * kPart;
   const int row_other = 4 * (3 * D + ((ff + 3) & ~3) + ((natt + 3) & ~3) + 8 + 2 * kWavesR);
   const int att_lds = cdiv(p->cap * 9, 64) * 1024 + cdiv(p->cap, 8) * 1024 +
-                      4 * (4 * kWavesA * kDh + 4 * kWavesA + 4);
+                      2 * 3 * kWavesA * kDh + 4 * (3 * kWavesA * kDh + 4 * kWavesA + 4);
   const int budget = std::max(std::max(att_lds, kMinLds), ring + row_other);
   ring = std::max(ring, (budget - row_other) / 2048 * 2048);   // spare LDS widens the logit halves
   p->ring_bytes = ring;
