@@ -96,10 +96,10 @@ constexpr int kLoader = 8;       // wave index of the loader (both kinds)
 constexpr int kThreadsWG = 9 * 64;
 constexpr int kMbox = 8;         // outputs per compute wave and phase
 #ifndef MSD_REPLICAS
-#define MSD_REPLICAS 8
+#define MSD_REPLICAS 4
 #endif
 constexpr int kRep = MSD_REPLICAS;   // replicas of every vector all row workgroups gather
-static_assert(kRep % kWavesA == 0 && kRep <= 64, "attention waves store whole sets of replicas");
+static_assert((kRep % kWavesA == 0 || kRep < kWavesA) && kRep <= 64, "attention waves store whole sets of replicas");
 // 1 KB DMA instructions a loader keeps in flight.  Fewer bytes in flight across the device
 // shorten the round trip of the exchange polls; the layer weights and KV rows need only a
 // few per CU to stay a layer ahead, the logit rows at the end stream with a wide window.
