@@ -400,11 +400,14 @@ __device__ __forceinline__ void wsync(int* ctr, int& phase, int n, int lane, uin
 __device__ __forceinline__ constexpr int vmcnt_imm(int k) {
   return (k & 0xF) | ((k >> 4) << 14) | (7 << 4) | (0xF << 8);
 }
-template <int W>
+#ifndef MSD_DMA_AUX
+#define MSD_DMA_AUX 2
+#endif
+template <int W, int AUX = 0>
 struct Dma {
   int inflight = 0;
   __device__ __forceinline__ void issue(const void* src, uint8_t* lds_base) {
-    __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds_base, 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds_base, 16, 0, AUX);
     if (++inflight == W) {
       __builtin_amdgcn_s_waitcnt(vmcnt_imm(W - 1));
       inflight = W - 1;
@@ -419,8 +422,8 @@ struct Dma {
 // Copy `bytes` (a multiple of 16) from src to lds: instruction t covers bytes
 // [1024 t, 1024 t + 1024); lanes past the end re-read the last 16 bytes into the
 // padding that rounds every region up to 1 KB.
-template <int W>
-__device__ __forceinline__ void dma_copy(Dma<W>& d, const uint8_t* src, uint8_t* lds, int64_t bytes, int lane) {
+template <int W, int AUX>
+__device__ __forceinline__ void dma_copy(Dma<W, AUX>& d, const uint8_t* src, uint8_t* lds, int64_t bytes, int lane) {
   for (int64_t t = 0; t * 1024 < bytes; ++t) {
     int64_t o = t * 1024 + 16 * lane;
     if (o > bytes - 16) o = bytes - 16;
@@ -529,8 +532,8 @@ template <int D, int FF>
 __device__ void row_loader(const Args& a, const RowCtx& c) {
   const Layout& lay = a.lay;
   const int lane = c.lane;
-  Dma<kDmaLayer> d;
-  Dma<kDmaLogits> dl;
+  Dma<kDmaLayer, MSD_DMA_AUX> d;
+  Dma<kDmaLogits, MSD_DMA_AUX> dl;
   const int half = a.ring_bytes / 2;
   const int njobs = 4 * a.L + c.nlog;
   for (int j = 0; j < njobs; ++j) {
@@ -996,6 +999,7 @@ __device__ void att_waves(const Args& a, const AttCtx& c) {
     float qv[1];
     poll_words<1, 1>(X + lay.x_qkv + c.h * kDh, kDh, c.tag, qv, a.ctrl, 0, lane, bad);
     MSD_TRACE_POINT(wv == 0, l, 24);
+    MSD_TRACE_WAVE(l, 0);
     {   // q = hi + mid + lo exactly, three bf16 parts taken by truncation (each holds the next
         // 8 significant bits), so bf16 products summed in f32 reproduce the f32 products.
         // Staged before the loads below: a wait for q must not wait for them.
@@ -1018,6 +1022,7 @@ __device__ void att_waves(const Args& a, const AttCtx& c) {
     }
     lds_wait(c.ctr + 1, l + 1, a.ctrl);   // cached rows of layer l are in LDS
     MSD_TRACE_POINT(wv == 0, l, 25);
+    MSD_TRACE_WAVE(l, 1);
     const int bs = min(64, max(16, (cdiv(c.ncached, kWavesA) + 15) & ~15));
     float m = -INFINITY, lsum = 0.f;
     float o[4] = {0.f, 0.f, 0.f, 0.f};
@@ -1069,6 +1074,7 @@ __device__ void att_waves(const Args& a, const AttCtx& c) {
         }
       }
       MSD_TRACE_POINT(wv == 0, l, 29);
+      MSD_TRACE_WAVE(l, 2);
       // k or v not there at the first load: load again now, so the final check after P.V
       // rarely needs another round trip
 #pragma unroll
@@ -1099,6 +1105,7 @@ __device__ void att_waves(const Args& a, const AttCtx& c) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) o[j] += __shfl_xor(o[j], 32);
       MSD_TRACE_POINT(wv == 0, l, 30);
+      MSD_TRACE_WAVE(l, 3);
     }
     lds_bump(c.ctr + 2, lane);   // this wave is done with the cached rows of layer l
     if (lane < 16) *reinterpret_cast<float4*>(ow + wv * kDh + 4 * lane) = make_float4(o[0], o[1], o[2], o[3]);
@@ -1121,8 +1128,10 @@ __device__ void att_waves(const Args& a, const AttCtx& c) {
       }
     }
     const float kv2[2] = {__uint_as_float(uint32_t(kvw[0])), __uint_as_float(uint32_t(kvw[1]))};
+    MSD_TRACE_WAVE(l, 4);
     wsync(c.ctr, ws, kWavesA, lane, a.ctrl);
     MSD_TRACE_POINT(wv == 0, l, 26);
+    MSD_TRACE_WAVE(l, 5);
     {   // merge the blocks and the current position (log-sum-exp).  Lane w < 8 holds block
         // w's max and sum.
       const float mv = lane < kWavesA ? mw[lane] : -INFINITY;
@@ -1153,6 +1162,7 @@ __device__ void att_waves(const Args& a, const AttCtx& c) {
         }
       }
       MSD_TRACE_POINT(wv == 0, l, 27);
+      MSD_TRACE_WAVE(l, 6);
     }
   }
 }
