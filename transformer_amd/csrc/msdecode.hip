@@ -958,6 +958,21 @@ __device__ __forceinline__ float sum8(float v) {
   v += dpp_f(v, 0x114);
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 7));
 }
+// Sum / max over lanes 0..15 (one DPP row), read from lane 15.
+__device__ __forceinline__ float sum16(float v) {
+  v += dpp_f(v, 0x111);
+  v += dpp_f(v, 0x112);
+  v += dpp_f(v, 0x114);
+  v += dpp_f(v, 0x118);
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 15));
+}
+__device__ __forceinline__ float max16(float v) {
+  v = fmaxf(v, dppm_f(v, 0x111));
+  v = fmaxf(v, dppm_f(v, 0x112));
+  v = fmaxf(v, dppm_f(v, 0x114));
+  v = fmaxf(v, dppm_f(v, 0x118));
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 15));
+}
 __device__ __forceinline__ float max8(float v) {
   v = fmaxf(v, dppm_f(v, 0x111));
   v = fmaxf(v, dppm_f(v, 0x112));
@@ -1023,13 +1038,16 @@ __device__ void att_waves(const Args& a, const AttCtx& c) {
     lds_wait(c.ctr + 1, l + 1, a.ctrl);   // cached rows of layer l are in LDS
     MSD_TRACE_POINT(wv == 0, l, 25);
     MSD_TRACE_WAVE(l, 1);
-    const int bs = min(64, max(16, (cdiv(c.ncached, kWavesA) + 15) & ~15));
+    // block of this wave: tiles [t0, t1) of 16 cached positions, the tiles split evenly over
+    // the waves (at most 4 each: ncached <= 512); waves w and w + 4 share a SIMD, and the
+    // even split keeps every SIMD's tile count within one of the others'
+    int t0, t1;
+    split(cdiv(c.ncached, 16), kWavesA, wv, t0, t1);
     float m = -INFINITY, lsum = 0.f;
     float o[4] = {0.f, 0.f, 0.f, 0.f};
-    const int r0 = wv * bs;
-    if (r0 < c.ncached) {
-      const int np = min(bs, c.ncached - r0);
-      const int nt = cdiv(np, 16);
+    const int r0 = 16 * t0;
+    if (t1 > t0) {
+      const int np = min(16 * (t1 - t0), c.ncached - r0);
       // q parts in the A layout: lane row m16 < 3 holds part m16 of dims 32 ch + 8 kb .. + 8
       __builtin_amdgcn_s_waitcnt(0xc07f);
       __builtin_amdgcn_wave_barrier();
@@ -1049,22 +1067,21 @@ __device__ void att_waves(const Args& a, const AttCtx& c) {
         kk[t][0] = *reinterpret_cast<const uint4*>(kr);
         kk[t][1] = *reinterpret_cast<const uint4*>(kr + 64);
       }
+      // all four tiles are computed (independent chains the matrix core overlaps) and the
+      // positions past the block masked; the scores sit in lanes 0..15
       float sv[4];
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
-        sv[t] = -INFINITY;
-        if (t < nt) {
-          f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(aq[0]), as_bf16x8(kk[t][0]), acc, 0, 0, 0);
-          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(aq[1]), as_bf16x8(kk[t][1]), acc, 0, 0, 0);
-          if (lane < 16 && 16 * t + lane < np) sv[t] = ((acc[0] + acc[1]) + acc[2]) * 0.125f;
-        }
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(aq[0]), as_bf16x8(kk[t][0]), acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(aq[1]), as_bf16x8(kk[t][1]), acc, 0, 0, 0);
+        sv[t] = (lane < 16 && 16 * t + lane < np) ? ((acc[0] + acc[1]) + acc[2]) * 0.125f : -INFINITY;
       }
-      m = wave_max(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])));
+      m = max16(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])));
       float e[4];
 #pragma unroll
       for (int t = 0; t < 4; ++t) e[t] = expf(sv[t] - m);   // 0 for masked positions
-      lsum = wave_sum((e[0] + e[1]) + (e[2] + e[3]));
+      lsum = sum16((e[0] + e[1]) + (e[2] + e[3]));
       // weights to LDS in the P.V order: position q at slot (q % 4) * 16 + q / 4
       if (lane < 16) {
 #pragma unroll
@@ -1128,6 +1145,8 @@ __device__ void att_waves(const Args& a, const AttCtx& c) {
       }
     }
     const float kv2[2] = {__uint_as_float(uint32_t(kvw[0])), __uint_as_float(uint32_t(kvw[1]))};
+    // score of the current position (un-rounded k), taken while the other waves finish
+    const float scur = c.has_cur ? wave_sum(qv[0] * kv2[0]) * 0.125f : -INFINITY;
     MSD_TRACE_WAVE(l, 4);
     wsync(c.ctr, ws, kWavesA, lane, a.ctrl);
     MSD_TRACE_POINT(wv == 0, l, 26);
@@ -1136,7 +1155,6 @@ __device__ void att_waves(const Args& a, const AttCtx& c) {
         // w's max and sum.
       const float mv = lane < kWavesA ? mw[lane] : -INFINITY;
       const float lv = lane < kWavesA ? lw[lane] : 0.f;
-      const float scur = c.has_cur ? wave_sum(qv[0] * kv2[0]) * 0.125f : -INFINITY;
       const float M = fmaxf(max8(lv > 0.f ? mv : -INFINITY), scur);
       float Ls = 0.f, O = 0.f;
       if (M != -INFINITY) {
