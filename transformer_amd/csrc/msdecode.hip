@@ -333,8 +333,22 @@ __device__ __forceinline__ void poll_words(const uint64_t* src, int n, uint32_t 
   for (int k = 0; k < NK; ++k) v[k] = __uint_as_float(uint32_t(wd[k]));
 }
 
-// Gather n tagged words src[0..n) into dst (LDS floats), NW waves sharing the words.
-template <int NW, int NK, int SLEEP = 0, int FIRST = kFirstPoll>
+// LDS position of element e of a K-long vector in the lane-major order of the row dot
+// products: in block b of 512 (the last block holds S = 8m elements, m lanes), element
+// 512b + q m + l sits at 512b + 8l + q, so lane l reads its 8 inputs of a block as two
+// 16-byte pieces (the order of the kernel row layout's packed weights).
+template <int K>
+__device__ __forceinline__ int lane_major(int e) {
+  const int b = e >> 9, r = e & 511;
+  constexpr int mt = (K % 512) / 8;   // lanes of a short last block
+  const int m = (mt > 0 && b == K / 512) ? mt : 64;
+  const int q = m == 64 ? (r >> 6) : r / m;
+  return (b << 9) + 8 * (r - q * m) + q;
+}
+
+// Gather n tagged words src[0..n) into dst (LDS floats), NW waves sharing the words; with
+// K > 0 the words land in the lane-major order of a K-long vector.
+template <int NW, int NK, int SLEEP = 0, int FIRST = kFirstPoll, int K = 0>
 __device__ __forceinline__ void gather_x(const uint64_t* src, int n, float* dst, uint32_t tag, uint32_t* ctrl,
                                          int w, int lane, bool& bad) {
   float v[NK];
@@ -342,7 +356,7 @@ __device__ __forceinline__ void gather_x(const uint64_t* src, int n, float* dst,
 #pragma unroll
   for (int k = 0; k < NK; ++k) {
     const int i = xidx<NW>(k, w, lane);
-    if (i < n) dst[i] = v[k];
+    if (i < n) dst[K > 0 ? lane_major<K>(i) : i] = v[k];
   }
 }
 
@@ -448,13 +462,23 @@ __device__ __forceinline__ int block_lanes(int k, int b) {
   return rem >= 512 ? 64 : (rem > 0 ? rem / 8 : 0);
 }
 
+// The lane's inputs of a K-long vector held in LDS in lane-major order (lane_major<K>).
 template <int NL>
 __device__ __forceinline__ void load_x(XV<NL>& xv, const float* x, int k, int lane) {
 #pragma unroll
   for (int j = 0; j < NL; ++j) {
     const int m = block_lanes(k, j);
-#pragma unroll
-    for (int q = 0; q < 8; ++q) xv.v[j][q] = (lane < m) ? x[512 * j + q * m + lane] : 0.f;
+    const float4* p = reinterpret_cast<const float4*>(x + 512 * j + 8 * (lane < m ? lane : 0));
+    const float4 a = p[0], b = p[1];
+    const bool on = lane < m;
+    xv.v[j][0] = on ? a.x : 0.f;
+    xv.v[j][1] = on ? a.y : 0.f;
+    xv.v[j][2] = on ? a.z : 0.f;
+    xv.v[j][3] = on ? a.w : 0.f;
+    xv.v[j][4] = on ? b.x : 0.f;
+    xv.v[j][5] = on ? b.y : 0.f;
+    xv.v[j][6] = on ? b.z : 0.f;
+    xv.v[j][7] = on ? b.w : 0.f;
   }
 }
 
@@ -665,7 +689,7 @@ __device__ void row_worker(const Args& a, const RowCtx& c, int token) {
     // ---- h += down output of the previous layer; x = rmsnorm1(h); QKV rows, RoPE, KV write
     //      (multi_sm_decode.py:121-180)
     if (l > 0) {
-      gather_x<kWavesR, HPW>(layer_x(a, l - 1) + lay.x_hd2 + myrep, D, c.xhd2, c.tag, a.ctrl, wv, lane, bad);
+      gather_x<kWavesR, HPW, 0, kFirstPoll, D>(layer_x(a, l - 1) + lay.x_hd2 + myrep, D, c.xhd2, c.tag, a.ctrl, wv, lane, bad);
       bar();
       add_res(c.xhd2);
       MSD_TRACE_POINT(wv == 0, l - 1, 6);
@@ -724,7 +748,7 @@ __device__ void row_worker(const Args& a, const RowCtx& c, int token) {
     //      workgroups publish each head's normalised output, gathered straight into xatt;
     //      with several, the (head, split) partials are merged here by log-sum-exp
     if (a.nsplit == 1) {
-      gather_x<kWavesR, HPW, 0, kAttFirstPoll>(X + lay.x_att + myrep, D, c.xatt, c.tag, a.ctrl, wv, lane, bad);
+      gather_x<kWavesR, HPW, 0, kAttFirstPoll, D>(X + lay.x_att + myrep, D, c.xatt, c.tag, a.ctrl, wv, lane, bad);
       MSD_TRACE_POINT(wv == 0, l, 3);
     } else {
       gather_x<kWavesR, NKA2, 0, kAttFirstPoll>(X + lay.x_att + myrep, natt * kPart, c.xa, c.tag, a.ctrl, wv, lane, bad);
@@ -747,7 +771,7 @@ __device__ void row_worker(const Args& a, const RowCtx& c, int token) {
             den += wgt * ps[1];
           }
         }
-        c.xatt[i] = den > 0.f ? num / den : 0.f;
+        c.xatt[lane_major<D>(i)] = den > 0.f ? num / den : 0.f;
       }
     }
     bar();
@@ -773,7 +797,7 @@ __device__ void row_worker(const Args& a, const RowCtx& c, int token) {
     bar();
     MSD_TRACE_POINT(wv == 0, l, 19);
     // ---- h += O output; x = rmsnorm2(h); gate/up rows + SwiGLU (multi_sm_decode.py:262-289, model.py:159)
-    gather_x<kWavesR, HPW>(X + lay.x_hd1 + myrep, D, c.xhd1, c.tag, a.ctrl, wv, lane, bad);
+    gather_x<kWavesR, HPW, 0, kFirstPoll, D>(X + lay.x_hd1 + myrep, D, c.xhd1, c.tag, a.ctrl, wv, lane, bad);
     bar();
     MSD_TRACE_POINT(wv == 0, l, 2);
     add_res(c.xhd1);
@@ -812,7 +836,7 @@ __device__ void row_worker(const Args& a, const RowCtx& c, int token) {
     MSD_TRACE_WAVE(l, 4);
     MSD_TRACE_POINT(wv == 0, l, 21);
     // ---- act -> LDS; down rows (multi_sm_decode.py:273-291)
-    gather_x<kWavesR, NKF>(X + lay.x_act + myrep, a.ff, c.xact, c.tag, a.ctrl, wv, lane, bad);
+    gather_x<kWavesR, NKF, 0, kFirstPoll, FF>(X + lay.x_act + myrep, a.ff, c.xact, c.tag, a.ctrl, wv, lane, bad);
     bar();
     MSD_TRACE_POINT(wv == 0, l, 5);
     weights(4 * l + 3);
@@ -840,7 +864,7 @@ __device__ void row_worker(const Args& a, const RowCtx& c, int token) {
   }
   // ---- h += last down output; x = final rmsnorm(h); tied logits over this workgroup's
   //      vocabulary rows (multi_sm_decode.py:314-337)
-  gather_x<kWavesR, HPW>(layer_x(a, a.L - 1) + lay.x_hd2 + myrep, D, c.xhd2, c.tag, a.ctrl, wv, lane, bad);
+  gather_x<kWavesR, HPW, 0, kFirstPoll, D>(layer_x(a, a.L - 1) + lay.x_hd2 + myrep, D, c.xhd2, c.tag, a.ctrl, wv, lane, bad);
   bar();
   add_res(c.xhd2);
   XV<NLD> xv;
