@@ -157,6 +157,18 @@ def test_tiny_teacher_forced_all_positions(tiny):
     assert not flips, flips
 
 
+def test_tiny_long_context_two_splits(tiny):
+    """Context 1024: each head's cached positions are split over two attention workgroups, whose
+    (max, sum, output) partials the row workgroups merge; every position checked."""
+    params, _, _ = tiny
+    cfg = dict(TINY, context_len=1024)
+    w = prepare_decode_weights_nlayer(params, cfg)
+    seq = make_prompt(cfg["context_len"], cfg["vocab_size"], seed=7)
+    worst, flips = _teacher_forced(params, w, cfg, seq)
+    print("tiny ctx-1024 teacher-forced max |logit diff|:", worst)
+    assert not flips, flips
+
+
 @pytest.fixture(scope="module")
 def m306():
     params = make_params(M306, seed=0, resid_scaled=True)
