@@ -157,6 +157,48 @@ def test_tiny_teacher_forced_all_positions(tiny):
     assert not flips, flips
 
 
+def test_bad_arguments_are_rejected_or_reported(tiny):
+    """Host-side checks (pos, host token) raise before launch; an out-of-range device token is
+    reported in the status word (the kernel clamps it for addressing) and the decoder recovers."""
+    from transformer_amd import _lib
+    params, prompt, w = tiny
+    dec = Decoder(w, TINY)
+    with pytest.raises(ValueError):
+        dec.step(int(prompt[0]), TINY["context_len"])
+    with pytest.raises(ValueError):
+        dec.step(TINY["vocab_size"], 0)
+    bad = torch.tensor([TINY["vocab_size"] + 5], dtype=torch.int32, device="cuda")
+    with pytest.raises(_lib.MsdError) as e:
+        dec.step(bad, 0)
+    assert e.value.code == _lib.MSD_E_ARG
+    # the status word was cleared: a valid step works and matches the oracle
+    tok, lg = dec.step(int(prompt[0]), 0)
+    kc, vc = om.new_kv_cache(TINY)
+    ref, rtok = om.decode_step(params, TINY, int(prompt[0]), 0, kc, vc)
+    np.testing.assert_allclose(lg.cpu().numpy(), ref, atol=1e-4, rtol=1e-4)
+    assert tok == rtok
+
+
+def test_reported_timeout_is_cleared_and_the_decoder_recovers(tiny):
+    """A timeout bit left in the status word (as a failed step leaves it) is reported by the
+    next step as MSD_E_TIMEOUT (waits that run long see it and stop; the others finish), the
+    check clears it, and the decoder then produces the oracle's results again."""
+    from transformer_amd import _lib
+    params, prompt, w = tiny
+    dec = Decoder(w, TINY)
+    dec.workspace[0:4].copy_(torch.tensor([1, 0, 0, 0], dtype=torch.uint8))   # status = timeout
+    with pytest.raises(_lib.MsdError) as e:
+        dec.step(int(prompt[0]), 0)
+    assert e.value.code == _lib.MSD_E_TIMEOUT
+    assert int(dec.workspace[0:4].view(torch.int32).item()) == 0   # cleared by the check
+    kc, vc = om.new_kv_cache(TINY)
+    for p, t in enumerate(prompt[:4]):   # restart from position 0 (the failed step wrote row 0)
+        tok, lg = dec.step(int(t), p)
+        ref, rtok = om.decode_step(params, TINY, int(t), p, kc, vc)
+        np.testing.assert_allclose(lg.cpu().numpy(), ref, atol=1e-4, rtol=1e-4)
+        assert tok == rtok
+
+
 def test_tiny_long_context_two_splits(tiny):
     """Context 1024: each head's cached positions are split over two attention workgroups, whose
     (max, sum, output) partials the row workgroups merge; every position checked."""
