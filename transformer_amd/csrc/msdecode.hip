@@ -112,7 +112,12 @@ static_assert((kRep % kWavesA == 0 || kRep < kWavesA) && kRep <= 64, "attention 
 #ifndef MSD_DMA_LOGITS
 #define MSD_DMA_LOGITS 48
 #endif
+#ifndef MSD_DMA_FIRST
+#define MSD_DMA_FIRST 32
+#endif
 constexpr int kDmaLayer = MSD_DMA_LAYER, kDmaKV = MSD_DMA_KV, kDmaLogits = MSD_DMA_LOGITS;
+// the first layer's rows load before any exchange traffic: a wider window
+constexpr int kDmaFirst = MSD_DMA_FIRST;
 
 constexpr uint32_t kStatusTimeout = 1u;
 constexpr uint32_t kStatusBadToken = 2u;
@@ -181,6 +186,7 @@ struct Args {
   // row workgroups: LDS ring regions (bytes) of the QKV, O, gate/up and down rows, the
   // ring size, and logit rows per ring half
   int ring_q, ring_o, ring_g, ring_d, ring_bytes, log_rows;
+  int keep;   // layers whose rows are read with the caching policy (the rest stream)
   Layout lay;
 };
 
@@ -414,9 +420,19 @@ __device__ __forceinline__ void wsync(int* ctr, int& phase, int n, int lane, uin
 __device__ __forceinline__ constexpr int vmcnt_imm(int k) {
   return (k & 0xF) | ((k >> 4) << 14) | (7 << 4) | (0xF << 8);
 }
+// Cache policy of the weight DMA.  The device's last-level cache (256 MB on MI355X) keeps
+// whatever is read with the default policy; the whole model does not fit, so the rows of the
+// first `keep` layers (as many as fit in kKeepBytes, leaving room for the KV cache) are read
+// with the default policy and stay cached from one step to the next, and every other weight
+// row is read non-temporal (nt) so that it streams past without evicting them.
 #ifndef MSD_DMA_AUX
 #define MSD_DMA_AUX 2
 #endif
+constexpr int kAuxKeep = 0;
+#ifndef MSD_KEEP_MB
+#define MSD_KEEP_MB 230
+#endif
+constexpr int64_t kKeepBytes = int64_t(MSD_KEEP_MB) << 20;
 template <int W, int AUX = 0>
 struct Dma {
   int inflight = 0;
@@ -557,6 +573,8 @@ __device__ void row_loader(const Args& a, const RowCtx& c) {
   const Layout& lay = a.lay;
   const int lane = c.lane;
   Dma<kDmaLayer, MSD_DMA_AUX> d;
+  Dma<kDmaLayer, kAuxKeep> dk;
+  Dma<kDmaFirst, kAuxKeep> d0;
   Dma<kDmaLogits, MSD_DMA_AUX> dl;
   const int half = a.ring_bytes / 2;
   const int njobs = 4 * a.L + c.nlog;
@@ -583,7 +601,13 @@ __device__ void row_loader(const Args& a, const RowCtx& c) {
     }
     if (need > 0 && lds_ld(c.ctr + kCtrUsed) < kWavesR * need) lds_wait(c.ctr + kCtrUsed, kWavesR * need, a.ctrl);
     if (bytes > 0) {
-      if (j < 4 * a.L) {
+      if (j < 4 && a.keep > 0) {
+        dma_copy(d0, reinterpret_cast<const uint8_t*>(src), c.ring + off, bytes, lane);
+        d0.drain();
+      } else if (j < 4 * a.keep) {
+        dma_copy(dk, reinterpret_cast<const uint8_t*>(src), c.ring + off, bytes, lane);
+        dk.drain();
+      } else if (j < 4 * a.L) {
         dma_copy(d, reinterpret_cast<const uint8_t*>(src), c.ring + off, bytes, lane);
         d.drain();
       } else {
@@ -947,28 +971,32 @@ struct AttCtx {
 // Loader wave of an attention workgroup: per layer, once every attention wave has
 // finished with the previous layer's rows, DMA this split's cached K rows (9 slots of
 // 16 bytes per row; the 9th is padding) and V rows (8 slots) into LDS.
+template <class DMA>
+__device__ __forceinline__ void att_copy(DMA& d, const Args& a, const AttCtx& c, int l) {
+  const int lane = c.lane;
+  const uint16_t* kc = layer_k(a, l) + (int64_t(c.g) * a.ctx + c.lo) * kDh;
+  const uint16_t* vc = kc + int64_t(a.KV) * a.ctx * kDh;
+  const int nk = cdiv(c.ncached * 9, 64);
+  for (int t = 0; t < nk; ++t) {
+    const int i = 64 * t + lane;
+    const int r = min(i / 9, c.ncached - 1), p = min(i % 9, 7);
+    d.issue(kc + r * kDh + p * 8, c.K + t * 1024);
+  }
+  const int nv = cdiv(c.ncached, 8);
+  for (int t = 0; t < nv; ++t) {
+    const int i = 64 * t + lane;
+    const int r = min(i / 8, c.ncached - 1), p = i % 8;
+    d.issue(vc + r * kDh + p * 8, c.V + t * 1024);
+  }
+  d.drain();
+}
+
 __device__ void att_loader(const Args& a, const AttCtx& c) {
   const int lane = c.lane;
   Dma<kDmaKV> d;
   for (int l = 0; l < a.L; ++l) {
     if (l > 0) lds_wait(c.ctr + 2, kWavesA * l, a.ctrl);
-    if (c.ncached > 0) {
-      const uint16_t* kc = layer_k(a, l) + (int64_t(c.g) * a.ctx + c.lo) * kDh;
-      const uint16_t* vc = kc + int64_t(a.KV) * a.ctx * kDh;
-      const int nk = cdiv(c.ncached * 9, 64);
-      for (int t = 0; t < nk; ++t) {
-        const int i = 64 * t + lane;
-        const int r = min(i / 9, c.ncached - 1), p = min(i % 9, 7);
-        d.issue(kc + r * kDh + p * 8, c.K + t * 1024);
-      }
-      const int nv = cdiv(c.ncached, 8);
-      for (int t = 0; t < nv; ++t) {
-        const int i = 64 * t + lane;
-        const int r = min(i / 8, c.ncached - 1), p = i % 8;
-        d.issue(vc + r * kDh + p * 8, c.V + t * 1024);
-      }
-    }
-    d.drain();
+    if (c.ncached > 0) att_copy(d, a, c, l);
     lds_set(c.ctr + 1, l + 1, lane);
     MSD_TRACE_POINT(true, l, 28);
   }
@@ -1446,6 +1474,7 @@ extern "C" int32_t msd_decode_step(const msd_config* cfg, const void* token_emb,
   a.ring_d = p.ring_d;
   a.ring_bytes = p.ring_bytes;
   a.log_rows = p.log_rows;
+  a.keep = int(std::min<int64_t>(cfg->n_layers, kKeepBytes / (a.lay.layer_elems * 2)));
   const hipError_t e = launch(a, cfg->d_model, cfg->d_ff, n_workgroups, p.lds, static_cast<hipStream_t>(stream));
   return e == hipSuccess ? MSD_OK : MSD_E_HIP;
 }
