@@ -1,9 +1,9 @@
 /* C ABI of the MI355X fused whole-model decode step (libmsdecode.so, gfx950).
  *
  * Every entry point takes plain device pointers and sizes, runs on the caller's
- * HIP stream and returns 0 on success or a negative MSD_E* code.  Nothing here
- * allocates device memory: buffers are sized with the msd_*_bytes/elems
- * queries and owned by the caller.
+ * HIP stream and returns 0 on success or a negative MSD_E* code.  Apart from
+ * msd_workspace_acquire, nothing here allocates device memory: buffers are sized
+ * with the msd_*_bytes/elems queries and owned by the caller.
  *
  * Reference interfaces replaced (zahlmann/transformer):
  *   msd_decode_step       <- kernels/multi_sm_decode.py:369-432
@@ -106,6 +106,20 @@ int32_t msd_decode_step(const msd_config* cfg, const void* token_emb, const void
 /* Reads and clears the device status word of a workspace (synchronous on `stream`).
  * Returns MSD_OK, MSD_E_TIMEOUT when a wait of an earlier step ran out, or MSD_E_HIP. */
 int32_t msd_check_status(void* workspace, void* stream);
+
+/* A zero-filled decode workspace of `bytes` bytes on device `device`, in uncached device
+ * memory: the exchange words the workgroups poll then bypass the L2 caches, which shortens
+ * every cross-workgroup hop (any zero-filled device memory works; this is the fast kind).
+ * Blocks come from a process-wide pool and are never freed (uncached memory must outlive
+ * every kernel that read it): msd_workspace_release returns one to the pool, and a later
+ * acquire of the same size on the same device re-zeroes and reuses it (after a device
+ * synchronisation).  No counterpart in the reference (its exchange buffers are jax arrays,
+ * kernels/multi_sm_decode.py:390-400).  Thread-safe.  MSD_E_ARG for bytes <= 0 or a NULL
+ * `out`, MSD_E_HIP when the allocation fails. */
+int32_t msd_workspace_acquire(int32_t device, int64_t bytes, void** out);
+/* Returns a block from msd_workspace_acquire to the pool (MSD_E_ARG for an unknown pointer).
+ * The caller must not use it afterwards; work still queued on it is waited for before reuse. */
+int32_t msd_workspace_release(void* workspace);
 
 /* Bytes of device workspace msd_sample_token needs for a vocabulary of `vocab` ids
  * (vocab <= 32768; MSD_E_CONFIG otherwise).  No initialisation is needed. */

@@ -1,4 +1,6 @@
 """Parity of the HIP decode step against the oracle (GPU)."""
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -179,6 +181,60 @@ def test_bad_arguments_are_rejected_or_reported(tiny):
     assert tok == rtok
 
 
+def _status_word(dec, value=None):
+    """Read (or write) the status word at the start of a decoder's workspace."""
+    hip = ctypes.CDLL("libamdhip64.so")
+    hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+    torch.cuda.synchronize()
+    word = ctypes.c_uint32(0 if value is None else value)
+    if value is None:
+        assert hip.hipMemcpy(ctypes.addressof(word), dec.workspace_ptr, 4, 2) == 0   # device to host
+    else:
+        assert hip.hipMemcpy(dec.workspace_ptr, ctypes.addressof(word), 4, 1) == 0   # host to device
+    return word.value
+
+
+def test_workspace_pool_reuses_zeroed_blocks(tiny):
+    """A released workspace goes back to the pool; the next acquire of the same size gets
+    the same block zero-filled again; a block in use is never handed out twice; a decoder
+    whose workspace came from the pool decodes exactly."""
+    from transformer_amd import _lib
+    L = _lib.lib()
+    hip = ctypes.CDLL("libamdhip64.so")
+    hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+    dev = torch.cuda.current_device()
+    n = 4096 * 3 + 40   # a size no decoder uses, so the pool holds no other free block of it
+    p1 = ctypes.c_void_p()
+    assert L.msd_workspace_acquire(dev, n, ctypes.byref(p1)) == 0
+    junk = (ctypes.c_uint8 * n)(*([0xA5] * n))
+    assert hip.hipMemcpy(p1, ctypes.addressof(junk), n, 1) == 0
+    p2 = ctypes.c_void_p()
+    assert L.msd_workspace_acquire(dev, n, ctypes.byref(p2)) == 0   # p1 in use: a new block
+    assert p2.value != p1.value
+    assert L.msd_workspace_release(p1) == 0
+    assert L.msd_workspace_release(p1) == _lib.MSD_E_ARG   # not in use any more
+    p3 = ctypes.c_void_p()
+    assert L.msd_workspace_acquire(dev, n, ctypes.byref(p3)) == 0
+    assert p3.value == p1.value
+    host = (ctypes.c_uint8 * n)()
+    assert hip.hipMemcpy(ctypes.addressof(host), p3, n, 2) == 0
+    assert not any(host)
+    for p in (p2, p3):
+        assert L.msd_workspace_release(p) == 0
+    assert L.msd_workspace_acquire(dev, 0, ctypes.byref(p3)) == _lib.MSD_E_ARG
+    assert L.msd_workspace_release(ctypes.c_void_p(12345)) == _lib.MSD_E_ARG
+    params, prompt, w = tiny
+    dec = Decoder(w, TINY)
+    kc, vc = om.new_kv_cache(TINY)
+    for p, t in enumerate(prompt[:3]):
+        tok, lg = dec.step(int(t), p)
+        ref, rtok = om.decode_step(params, TINY, int(t), p, kc, vc)
+        np.testing.assert_allclose(lg.cpu().numpy(), ref, atol=1e-4, rtol=1e-4)
+        assert tok == rtok
+    dec.close()
+    assert dec.workspace_ptr is None
+
+
 def test_reported_timeout_is_cleared_and_the_decoder_recovers(tiny):
     """A timeout bit left in the status word (as a failed step leaves it) is reported by the
     next step as MSD_E_TIMEOUT (waits that run long see it and stop; the others finish), the
@@ -186,11 +242,11 @@ def test_reported_timeout_is_cleared_and_the_decoder_recovers(tiny):
     from transformer_amd import _lib
     params, prompt, w = tiny
     dec = Decoder(w, TINY)
-    dec.workspace[0:4].copy_(torch.tensor([1, 0, 0, 0], dtype=torch.uint8))   # status = timeout
+    _status_word(dec, 1)   # status = timeout
     with pytest.raises(_lib.MsdError) as e:
         dec.step(int(prompt[0]), 0)
     assert e.value.code == _lib.MSD_E_TIMEOUT
-    assert int(dec.workspace[0:4].view(torch.int32).item()) == 0   # cleared by the check
+    assert _status_word(dec) == 0   # cleared by the check
     kc, vc = om.new_kv_cache(TINY)
     for p, t in enumerate(prompt[:4]):   # restart from position 0 (the failed step wrote row 0)
         tok, lg = dec.step(int(t), p)

@@ -23,7 +23,7 @@ _ERRNAMES = {MSD_E_CONFIG: "unsupported config", MSD_E_ARG: "invalid argument",
 EXPORTS = ("msd_packed_weight_elems", "msd_workspace_bytes", "msd_default_workgroups",
            "msd_decode_step", "msd_check_status", "msd_sample_workspace_bytes", "msd_sample_token",
            "msd_prefill_workspace_bytes", "msd_prefill", "msd_prefill_paged", "msd_batch_workspace_bytes",
-           "msd_batch_decode_step")
+           "msd_batch_decode_step", "msd_workspace_acquire", "msd_workspace_release")
 
 
 class MsdConfig(ctypes.Structure):
@@ -66,6 +66,10 @@ def lib():
     L.msd_decode_step.restype = I32
     L.msd_check_status.argtypes = [P, P]
     L.msd_check_status.restype = I32
+    L.msd_workspace_acquire.argtypes = [I32, I64, ctypes.POINTER(ctypes.c_void_p)]
+    L.msd_workspace_acquire.restype = I32
+    L.msd_workspace_release.argtypes = [P]
+    L.msd_workspace_release.restype = I32
     D = ctypes.c_double
     L.msd_sample_workspace_bytes.argtypes = [I32]
     L.msd_sample_workspace_bytes.restype = I64

@@ -43,6 +43,8 @@
 #include <stdint.h>
 
 #include <algorithm>
+#include <mutex>
+#include <vector>
 
 #include "../../include/msdecode.h"
 
@@ -1477,6 +1479,61 @@ extern "C" int32_t msd_decode_step(const msd_config* cfg, const void* token_emb,
   a.keep = int(std::min<int64_t>(cfg->n_layers, kKeepBytes / (a.lay.layer_elems * 2)));
   const hipError_t e = launch(a, cfg->d_model, cfg->d_ff, n_workgroups, p.lds, static_cast<hipStream_t>(stream));
   return e == hipSuccess ? MSD_OK : MSD_E_HIP;
+}
+
+// Decode workspaces in uncached device memory, pooled per (device, size) and never freed.
+namespace {
+struct WsBlock {
+  int dev;
+  int64_t bytes;
+  void* ptr;
+  bool used;
+};
+std::mutex g_ws_mu;
+std::vector<WsBlock> g_ws;
+}  // namespace
+
+extern "C" int32_t msd_workspace_acquire(int32_t device, int64_t bytes, void** out) {
+  if (!out || bytes <= 0) return MSD_E_ARG;
+  *out = nullptr;
+  std::lock_guard<std::mutex> lk(g_ws_mu);
+  int prev = 0;
+  if (hipGetDevice(&prev) != hipSuccess) return MSD_E_HIP;
+  if (prev != device && hipSetDevice(device) != hipSuccess) return MSD_E_HIP;
+  WsBlock* blk = nullptr;
+  for (auto& b : g_ws)
+    if (!b.used && b.dev == device && b.bytes == bytes) {
+      blk = &b;
+      break;
+    }
+  hipError_t e = hipSuccess;
+  if (blk) {
+    e = hipDeviceSynchronize();   // the previous owner's steps may still be queued
+  } else {
+    void* p = nullptr;
+    e = hipExtMallocWithFlags(&p, size_t(bytes), hipDeviceMallocUncached);
+    if (e == hipSuccess) {
+      g_ws.push_back({device, bytes, p, false});
+      blk = &g_ws.back();
+    }
+  }
+  if (e == hipSuccess) e = hipMemset(blk->ptr, 0, size_t(bytes));
+  if (e == hipSuccess) e = hipDeviceSynchronize();
+  if (prev != device) hipSetDevice(prev);
+  if (e != hipSuccess) return MSD_E_HIP;
+  blk->used = true;
+  *out = blk->ptr;
+  return MSD_OK;
+}
+
+extern "C" int32_t msd_workspace_release(void* workspace) {
+  std::lock_guard<std::mutex> lk(g_ws_mu);
+  for (auto& b : g_ws)
+    if (b.ptr == workspace && b.used) {
+      b.used = false;
+      return MSD_OK;
+    }
+  return MSD_E_ARG;
 }
 
 extern "C" int32_t msd_check_status(void* workspace, void* stream) {

@@ -8,8 +8,10 @@ Differences from the reference call, by design:
   * the KV cache is updated in place at ``pos`` (the returned kv is the same tensor); a
     step writes ``pos`` before reading it and never reads rows > pos, so replaying from
     the same start position (profile_kernels.py:54-63) gives the same results;
-  * the workspace is allocated once per decoder and never re-zeroed: exchange words are
-    tagged with a per-call epoch instead (multi_sm_decode.py:400 zero-fills per call).
+  * the workspace is taken once per decoder from the library's pool of zero-filled
+    uncached device memory (msd_workspace_acquire: the polled exchange words bypass the L2
+    caches) and never re-zeroed while the decoder lives: exchange words are tagged with a
+    per-call epoch instead (multi_sm_decode.py:400 zero-fills per call).
 """
 import ctypes
 
@@ -36,13 +38,34 @@ class Decoder:
         self.n_workgroups = int(n_workgroups)
         nbytes = _lib.check(L.msd_workspace_bytes(ctypes.byref(self._cfg), self.n_workgroups),
                             "msd_workspace_bytes")
-        self.workspace = torch.zeros(nbytes, dtype=torch.uint8, device=self.device)
+        # zero-filled uncached device memory from the library's pool (never freed; returned to
+        # the pool when this decoder goes away)
+        ws = ctypes.c_void_p()
+        _lib.check(L.msd_workspace_acquire(self._device_index(), nbytes, ctypes.byref(ws)),
+                   "msd_workspace_acquire")
+        self.workspace_ptr = ws.value
+        self.workspace_bytes = nbytes
         self.kv = kv_packed if kv_packed is not None else new_kv_packed(self.config, self.device)
         self.logits = torch.empty(self.config["vocab_size"], dtype=torch.float32, device=self.device)
         self.out = torch.zeros(2, dtype=torch.int32, device=self.device)   # [token, status]
         self._host = torch.zeros(2, dtype=torch.int32).pin_memory()
         self.epoch = 0
         self._check_kv(self.kv)
+
+    def _device_index(self):
+        return self.device.index if self.device.index is not None else torch.cuda.current_device()
+
+    def close(self):
+        """Return the workspace to the library's pool (the decoder is unusable afterwards)."""
+        ptr, self.workspace_ptr = getattr(self, "workspace_ptr", None), None
+        if ptr:
+            _lib.lib().msd_workspace_release(ptr)
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
     def _check_kv(self, kv):
         c = self.config
@@ -78,7 +101,7 @@ class Decoder:
             ctypes.byref(self._cfg), w["token_emb"].data_ptr(), w["output_proj"].data_ptr(),
             w["packed_w"].data_ptr(),
             w["lnf_s"].data_ptr(), w["rope"].data_ptr(), tok, tok_dev, pos, self.kv.data_ptr(),
-            self.workspace.data_ptr(), self.epoch, self.logits.data_ptr(), out.data_ptr(),
+            self.workspace_ptr, self.epoch, self.logits.data_ptr(), out.data_ptr(),
             self.n_workgroups, ctypes.c_void_p(s.cuda_stream))
         _lib.check(rc, "msd_decode_step")
         return out
@@ -93,7 +116,7 @@ class Decoder:
         torch.cuda.current_stream(self.device).synchronize()
         tok, status = int(self._host[0]), int(self._host[1])
         if status != 0:
-            _lib.lib().msd_check_status(self.workspace.data_ptr(),
+            _lib.lib().msd_check_status(self.workspace_ptr,
                                         ctypes.c_void_p(torch.cuda.current_stream(self.device).cuda_stream))
             raise _lib.MsdError(_lib.MSD_E_TIMEOUT if status & 1 else _lib.MSD_E_ARG,
                                 f"decode step at pos {pos} (status {status:#x})")
