@@ -277,10 +277,13 @@ __device__ __forceinline__ uint32_t ld_status(uint32_t* ctrl) {
   return __hip_atomic_load(ctrl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+#ifndef MSD_ROUND_SLEEP
+#define MSD_ROUND_SLEEP 2
+#endif
 // One step of a bounded spin: after kSpinLimit rounds, or when another workgroup has
 // reported a timeout in the status word, the wave stops waiting and `bad` is set.
 __device__ __forceinline__ void spin_step(uint32_t& spins, uint32_t* ctrl, int lane, bool& bad) {
-  __builtin_amdgcn_s_sleep(2);   // a short pause between poll rounds (measured: less contention)
+  __builtin_amdgcn_s_sleep(MSD_ROUND_SLEEP);   // a short pause between poll rounds (measured: less contention)
   ++spins;
   if ((spins & 255u) == 0 && (ld_status(ctrl) & kStatusTimeout)) bad = true;
   if (spins > kSpinLimit) {
@@ -313,7 +316,10 @@ __device__ __forceinline__ bool repoll(uint64_t (&wd)[NK], const uint64_t* src, 
 // The first round waits kFirstPoll s_sleep units (~0.4 us): the remote outputs cannot land
 // sooner, and an early round over words still being written costs a full round trip
 // (measured: 9% per token).
-constexpr int kFirstPoll = 16;
+#ifndef MSD_FIRST_POLL
+#define MSD_FIRST_POLL 16
+#endif
+constexpr int kFirstPoll = MSD_FIRST_POLL;
 // The attention partials take the attention workgroups' gather and compute (a few us)
 // before they can land, so that gather starts polling later.
 #ifndef MSD_ATT_FIRST_POLL
@@ -1519,7 +1525,7 @@ extern "C" int32_t msd_workspace_acquire(int32_t device, int64_t bytes, void** o
   }
   if (e == hipSuccess) e = hipMemset(blk->ptr, 0, size_t(bytes));
   if (e == hipSuccess) e = hipDeviceSynchronize();
-  if (prev != device) hipSetDevice(prev);
+  if (prev != device) (void)hipSetDevice(prev);
   if (e != hipSuccess) return MSD_E_HIP;
   blk->used = true;
   *out = blk->ptr;
