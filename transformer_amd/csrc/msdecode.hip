@@ -1160,27 +1160,42 @@ __device__ void att_waves(const Args& a, const AttCtx& c) {
       __builtin_amdgcn_s_waitcnt(0xc07f);
       __builtin_amdgcn_wave_barrier();
       const int g = kb, dq = m16;
-      const int steps = cdiv(np, 4);
+      // all reads first (one LDS round trip); steps past the block (at most 4 of 4 positions
+      // per group: np <= 64) use weight 0 on the last row, which adds exact zeros (fewer
+      // steps for small blocks measured slower)
       const uint8_t* vb = c.V + r0 * kVRowB + 8 * dq;
-      for (int i4 = 0; i4 < steps; i4 += 4) {
-        const float4 p4 = *reinterpret_cast<const float4*>(pw + g * 16 + i4);
-        const float pk[4] = {p4.x, p4.y, p4.z, p4.w};
-        uint2 vv[4];
+      float4 p4[4];
+      uint2 vv[4][4];
+#pragma unroll
+      for (int it = 0; it < 4; ++it) {
+        p4[it] = *reinterpret_cast<const float4*>(pw + g * 16 + 4 * it);
 #pragma unroll
         for (int k = 0; k < 4; ++k)
-          vv[k] = *reinterpret_cast<const uint2*>(vb + min(4 * (i4 + k) + g, np - 1) * kVRowB);
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          o[0] += pk[k] * bf_lo(vv[k].x);
-          o[1] += pk[k] * bf_hi(vv[k].x);
-          o[2] += pk[k] * bf_lo(vv[k].y);
-          o[3] += pk[k] * bf_hi(vv[k].y);
-        }
+          vv[it][k] = *reinterpret_cast<const uint2*>(vb + min(4 * (4 * it + k) + g, np - 1) * kVRowB);
       }
 #pragma unroll
-      for (int j = 0; j < 4; ++j) o[j] += __shfl_xor(o[j], 16);
+      for (int it = 0; it < 4; ++it) {
+        const float pk[4] = {p4[it].x, p4[it].y, p4[it].z, p4[it].w};
 #pragma unroll
-      for (int j = 0; j < 4; ++j) o[j] += __shfl_xor(o[j], 32);
+        for (int k = 0; k < 4; ++k) {
+          o[0] += pk[k] * bf_lo(vv[it][k].x);
+          o[1] += pk[k] * bf_hi(vv[it][k].x);
+          o[2] += pk[k] * bf_lo(vv[it][k].y);
+          o[3] += pk[k] * bf_hi(vv[it][k].y);
+        }
+      }
+      // sum the four position groups (rows of 16 lanes): lane l adds lane l ^ 16, then l ^ 32,
+      // with the row-swapping permutes (no LDS traffic); a + b in either order, as before
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(o[j]), __float_as_uint(o[j]), false, false);
+        o[j] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(o[j]), __float_as_uint(o[j]), false, false);
+        o[j] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+      }
       MSD_TRACE_POINT(wv == 0, l, 30);
       MSD_TRACE_WAVE(l, 3);
     }
