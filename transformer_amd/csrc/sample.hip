@@ -18,9 +18,11 @@
 //
 // Kernels, all on the caller's stream:
 //   sample_greedy_kernel   temperature 0: argmax of the penalised logits (1 workgroup)
-//   sample_softmax_kernel  one workgroup per 8192-id numpy reduction buffer: maximum, correctly
-//                          rounded exponentials and the buffer's pairwise sum
-//   sample_norm_kernel     512 ids per workgroup: normalisation, radix keys, first digit counts
+//   sample_max_kernel      512 ids per workgroup: penalised, scaled logits and their maxima
+//   sample_leaf_kernel     one wave per leaf of numpy's pairwise sum (<= 128 ids): correctly
+//                          rounded exponentials and the leaf's sum
+//   sample_norm_kernel     512 ids per workgroup: the pairwise trees over the leaf sums,
+//                          normalisation, radix keys, first digit counts
 //   sample_full_kernel     top_p >= 1: inverse CDF over all ids (1 workgroup)
 //   sample_radix_kernel    4 stable LSD passes of 8 bits over (probability bits, id), tiles of
 //                          512 entries per workgroup; each pass counts the next pass's digits
@@ -56,7 +58,6 @@ constexpr int kSlots = 255;                 // heap slots of one buffer's pairwi
 // Large LDS arrays keep entry j at j + j/32: a thread's 32 consecutive entries then start on
 // a different bank from its neighbours'.
 constexpr size_t kLdsBig = size_t(kVMax + kVMax / 32) * sizeof(float);
-constexpr size_t kLdsBuf = size_t(kRedChunk + kRedChunk / 32) * sizeof(float);
 
 enum Mode { kGreedy = 0, kFull = 1, kNucleus = 2 };
 
@@ -71,7 +72,8 @@ struct SArgs {
   uint32_t* ids[2];
   uint32_t* hist;         // [kPasses][kMaxTiles][256]
   int* table;             // [3][kVMax / 64]: chunk totals, binades, odd-start changes
-  float* bsum;            // [kVMax / 8192]: numpy's per-buffer sums of the exponentials
+  float* tmax;            // [kVMax / 512]: maxima of the penalised, scaled logits per tile
+  float* lsum;            // [kVMax / 8192][256]: numpy's pairwise leaf sums by buffer and heap slot
   int V;
   int mode;
   int use_pen;
@@ -131,22 +133,11 @@ __device__ inline int binade(float s) { return int((__float_as_uint(s) >> 23) & 
 struct BlockScratch {   // small shared scratch of the 1024-thread kernels
   float vals[kT];       // pairwise-tree node sums
   double dw[kWaves];
-  float fw[kWaves];
   int iw[kWaves];
   uint64_t kw[kWaves];
-  double dtot;
+  double dthr;          // inverse CDF threshold
   int i0;
 };
-
-__device__ float block_max(float v, BlockScratch& b) {
-  v = wave_max(v);
-  if (lane_id() == 0) b.fw[threadIdx.x >> 6] = v;
-  __syncthreads();
-  float m = b.fw[0];
-  for (int i = 1; i < kWaves; ++i) m = fmaxf(m, b.fw[i]);
-  __syncthreads();
-  return m;
-}
 
 __device__ int block_sum_i(int v, BlockScratch& b) {
   v = wave_sum_i(v);
@@ -262,13 +253,29 @@ __device__ float np_sum(const float* a, int n, BlockScratch& b) {
 }
 
 // ---------------------------------------------------------------- inverse CDF draw
+// The largest double x with x / total <= u (float64 division): the division by total > 0 is
+// correctly rounded and so nondecreasing in x, and fl(u * total) lies within an ulp or two of
+// that boundary, so a few steps of one ulp from it find x.  cdf[i] / total <= u then holds
+// exactly when cdf[i] <= x.
+__device__ double cdf_threshold(double total, double u) {
+  double x = u * total;
+  for (int i = 0; i < 16 && x / total > u; ++i) x = nextafter(x, -INFINITY);
+  for (int i = 0; i < 16; ++i) {
+    const double y = nextafter(x, INFINITY);
+    if (!(y / total <= u)) break;
+    x = y;
+  }
+  return x;
+}
+
 // RandomState.choice on one uniform: the number of i < n with cdf[i] / cdf[n-1] <= u, where
 // cdf is the float64 running sum of w[i] = (divide ? v[i] / div : v[i]) (float32 values,
 // padded LDS layout; with divide the entries are replaced by w).  Thread t adds entries
 // [32t, 32t+32) in order on top of the sum of all earlier entries, so every partial sum equals
 // the sequential one whenever the float64 sums are exact (float32 terms spanning fewer than 29
-// binades below the total).  cdf / total is nondecreasing, so each thread tests its last entry
-// and only the thread whose range crosses u tests its entries one by one.
+// binades below the total).  cdf is nondecreasing, so each thread tests its last entry against
+// the threshold of cdf_threshold and only the thread whose range crosses it tests its entries
+// one by one.
 __device__ int inverse_cdf(float* v, int n, bool divide, float div, double u, BlockScratch& b) {
   __shared__ uint8_t flag[kT];
   const int t = threadIdx.x, base = t * kPer;
@@ -287,10 +294,10 @@ __device__ int inverse_cdf(float* v, int n, bool divide, float div, double u, Bl
 #pragma unroll 8
   for (int i = 0; i < kPer; ++i)
     if (i < cnt) r += double(v[pad(base + i)]);
-  if (cnt > 0 && base + cnt == n) b.dtot = r;   // cdf[n-1] as accumulated by its owner
+  if (cnt > 0 && base + cnt == n) b.dthr = cdf_threshold(r, u);   // r = cdf[n-1] here
   __syncthreads();
-  const double total = b.dtot;
-  const bool below = cnt > 0 && r / total <= u;
+  const double thr = b.dthr;
+  const bool below = cnt > 0 && r <= thr;
   flag[t] = below;
   __syncthreads();
   int c = below ? cnt : 0;
@@ -298,7 +305,7 @@ __device__ int inverse_cdf(float* v, int n, bool divide, float div, double u, Bl
     double rr = excl;
     for (int i = 0; i < cnt; ++i) {
       rr += double(v[pad(base + i)]);
-      if (rr / total <= u) ++c;
+      if (rr <= thr) ++c;
     }
   }
   const int cs = block_sum_i(c, b);
@@ -420,11 +427,12 @@ __device__ void finish(const SArgs& a, int token) {
   }
 }
 
-// Penalised logit of id j (generate.py:33-39), divided by the temperature when scaled
-// (generate.py:45-46); float32 operations as numpy performs them.
-__device__ __forceinline__ float penalised(const SArgs& a, int j, bool scaled) {
-  float v = a.logits[j];
-  if (a.use_pen && a.seen[j]) v = v > 0.f ? v / a.pen : v * a.pen;
+// Penalised logit v of an id with history flag `seen` (generate.py:33-39), divided by the
+// temperature when scaled (generate.py:45-46); float32 operations as numpy performs them.
+// Callers load v and seen from a clamped index, unconditionally, and issue all their loads
+// before the first use: a load under a branch makes the compiler wait for it at the join.
+__device__ __forceinline__ float penalised(const SArgs& a, float v, uint8_t seen, bool scaled) {
+  if (a.use_pen && seen) v = v > 0.f ? v / a.pen : v * a.pen;
   if (scaled && a.scale) v = v / a.temp;
   return v;
 }
@@ -433,66 +441,143 @@ __device__ __forceinline__ float penalised(const SArgs& a, int j, bool scaled) {
 __global__ __launch_bounds__(kT) void sample_greedy_kernel(SArgs a) {
   __shared__ BlockScratch b;
   const int t = threadIdx.x;
-  float l[kPer];
-#pragma unroll
-  for (int i = 0; i < kPer; ++i) l[i] = t + kT * i < a.V ? penalised(a, t + kT * i, false) : 0.f;
+  constexpr int kHalf = kPer / 2;   // 16 ids per thread in flight at a time
   uint64_t best = 0;
+  for (int h = 0; h < 2; ++h) {
+    float l[kHalf];
+    uint8_t sn[kHalf];
 #pragma unroll
-  for (int i = 0; i < kPer; ++i) {
-    const int j = t + kT * i;
-    if (j < a.V) {
+    for (int i = 0; i < kHalf; ++i) {
+      const int jc = min(t + kT * (h * kHalf + i), a.V - 1);
+      l[i] = a.logits[jc];
+      sn[i] = a.seen[jc];
+    }
+#pragma unroll
+    for (int i = 0; i < kHalf; ++i) {
+      const int j = t + kT * (h * kHalf + i);
+      l[i] = penalised(a, l[i], sn[i], false);
       const uint64_t key = (uint64_t(ordered(l[i])) << 32) | uint32_t(0xffffffffu - uint32_t(j));
-      best = key > best ? key : best;
+      best = j < a.V && key > best ? key : best;
     }
   }
   best = block_max_u64(best, b);
   finish(a, int(0xffffffffu - uint32_t(best & 0xffffffffu)));
 }
 
-// Softmax numerator (generate.py:48-50), one workgroup per numpy reduction buffer of 8192 ids:
-// every workgroup forms the maximum of all penalised, scaled logits (identically), then the
-// correctly rounded exp(l - max) of its buffer (to keys[1]) and numpy's pairwise sum of the
-// buffer (to bsum[buffer]).
-__global__ __launch_bounds__(kT) void sample_softmax_kernel(SArgs a) {
-  extern __shared__ float sh_e[];   // one buffer, padded layout
-  __shared__ BlockScratch b;
-  const int t = threadIdx.x, V = a.V;
-  float l[kPer];
-#pragma unroll
-  for (int i = 0; i < kPer; ++i) l[i] = t + kT * i < V ? penalised(a, t + kT * i, true) : -INFINITY;
-  float m = -INFINITY;
-#pragma unroll
-  for (int i = 0; i < kPer; ++i) m = fmaxf(m, l[i]);
-  m = block_max(m, b);
-  const int b0 = blockIdx.x * kRedChunk, bn = min(kRedChunk, V - b0);
-  float* eo = reinterpret_cast<float*>(a.keys[1]);
-#pragma unroll
-  for (int i = 0; i < kRedChunk / kT; ++i) {
-    const int jl = t + kT * i;
-    if (jl < bn) {
-      const float e = float(exp(double(penalised(a, b0 + jl, true) - m)));
-      sh_e[pad(jl)] = e;
-      eo[b0 + jl] = e;
-    }
-  }
+// Softmax, first step (generate.py:33-48): workgroup w takes ids [512w, 512w+512), stores the
+// penalised, scaled logits (to keys[1]) and their maximum (to tmax[w]).
+__global__ __launch_bounds__(kTile) void sample_max_kernel(SArgs a) {
+  __shared__ float wm[kTile / 64];
+  const int t = threadIdx.x, j = blockIdx.x * kTile + t;
+  const int jc = min(j, a.V - 1);
+  const float lv = a.logits[jc];
+  const uint8_t sn = a.seen[jc];
+  const float pv = penalised(a, lv, sn, true);
+  const float l = j < a.V ? pv : -INFINITY;
+  if (j < a.V) reinterpret_cast<float*>(a.keys[1])[j] = l;
+  const float m = wave_max(l);
+  if (lane_id() == 0) wm[t >> 6] = m;
   __syncthreads();
-  const float sb = np_sum(sh_e, bn, b);
-  if (t == 0) a.bsum[blockIdx.x] = sb;
+  if (t == 0) {
+    float mm = wm[0];
+    for (int i = 1; i < kTile / 64; ++i) mm = fmaxf(mm, wm[i]);
+    a.tmax[blockIdx.x] = mm;
+  }
+}
+
+// Softmax numerator (generate.py:49-50) and the leaves of numpy's float32 sum: wave g takes heap
+// slot g % 255 of reduction buffer g / 255 and, when that node is a leaf (<= 128 ids), writes
+// the correctly rounded exp(l - max) of its ids (to keys[0]) and the leaf's pairwise sum (to
+// lsum[256 * buffer + slot]).  The leaves of a buffer partition it, so every id is covered once.
+constexpr int kLeafWaves = 4;
+
+__global__ __launch_bounds__(64 * kLeafWaves) void sample_leaf_kernel(SArgs a) {
+  const int lane = lane_id();
+  const int g = blockIdx.x * kLeafWaves + (threadIdx.x >> 6);
+  const int k = g / kSlots, slot = g - k * kSlots;
+  const int V = a.V;
+  if (k * kRedChunk >= V) return;
+  const int bn = min(kRedChunk, V - k * kRedChunk);
+  int start = 0, len = 0;
+  if (!pw_node(bn, slot, start, len) || len > kPwBlock) return;
+  const int ntiles = (V + kTile - 1) / kTile;
+  const int j0 = k * kRedChunk + start;
+  const float* lg = reinterpret_cast<const float*>(a.keys[1]);
+  float* eo = reinterpret_cast<float*>(a.keys[0]);
+  const float l0 = lg[j0 + min(lane, len - 1)], l1 = lg[j0 + min(lane + 64, len - 1)];
+  const float tm = a.tmax[min(lane, ntiles - 1)];
+  const float m = wave_max(lane < ntiles ? tm : -INFINITY);
+  float x0 = 0.f, x1 = 0.f;   // e of leaf entries lane and lane + 64
+  if (lane < len) {
+    x0 = float(exp(double(l0 - m)));
+    eo[j0 + lane] = x0;
+  }
+  if (lane + 64 < len) {
+    x1 = float(exp(double(l1 - m)));
+    eo[j0 + lane + 64] = x1;
+  }
+  float res = 0.f;
+  int i = 0;
+  if (len >= 8) {
+    // lanes 0..7: accumulator r_lane = e[lane] + e[lane + 8] + ... in order
+    const int lim = len - len % 8;
+    float r = x0;
+#pragma unroll
+    for (int q = 1; q < 16; ++q) {
+      const int idx = lane + 8 * q;
+      const float v = q < 8 ? __shfl(x0, idx & 63) : __shfl(x1, idx & 63);
+      if (idx < lim) r += v;
+    }
+    res = ((readlane_f(r, 0) + readlane_f(r, 1)) + (readlane_f(r, 2) + readlane_f(r, 3))) +
+          ((readlane_f(r, 4) + readlane_f(r, 5)) + (readlane_f(r, 6) + readlane_f(r, 7)));
+    i = lim;
+  }
+  for (; i < len; ++i) res += readlane_f(i < 64 ? x0 : x1, i & 63);
+  if (lane == 0) a.lsum[k * 256 + slot] = res;
 }
 
 // Normalisation (generate.py:51): p = e / sum with numpy's sum = the buffer sums added in order
-// to 0.  Workgroup w takes ids [512w, 512w+512): probabilities (optionally to probs_out), and for
-// top_p < 1 the radix keys in id order with this tile's counts of the first digit.
+// to 0, each buffer's sum its pairwise tree over the leaf sums (inner nodes by decreasing
+// depth; every workgroup evaluates the tree identically).  Workgroup w takes ids
+// [512w, 512w+512): probabilities (optionally to probs_out), and for top_p < 1 the radix keys
+// in id order with this tile's counts of the first digit.
+constexpr int kMaxBufs = kVMax / kRedChunk;
+
 __global__ __launch_bounds__(kTile) void sample_norm_kernel(SArgs a) {
   __shared__ uint32_t hl[256];
+  __shared__ float node[kMaxBufs * 256];
   const int t = threadIdx.x, w = blockIdx.x, V = a.V, j = w * kTile + t;
   const int nbuf = (V + kRedChunk - 1) / kRedChunk;
-  float total = 0.f;
-  for (int q = 0; q < nbuf; ++q) total += a.bsum[q];
+  constexpr int kNodeRounds = kMaxBufs * 256 / kTile;
+  int depth[kNodeRounds];
+  bool inner[kNodeRounds];
+  const float e = reinterpret_cast<const float*>(a.keys[0])[min(j, V - 1)];
+  float ls[kNodeRounds];
+#pragma unroll
+  for (int r = 0; r < kNodeRounds; ++r) ls[r] = a.lsum[t + kTile * r];
+#pragma unroll
+  for (int r = 0; r < kNodeRounds; ++r) {
+    const int q = t + kTile * r, k = q >> 8, slot = q & 255;
+    int start = 0, len = 0;
+    const bool valid = k < nbuf && slot < kSlots && pw_node(min(kRedChunk, V - k * kRedChunk), slot, start, len);
+    inner[r] = valid && len > kPwBlock;
+    depth[r] = 31 - __clz(slot + 1);
+    if (valid && len <= kPwBlock) node[q] = ls[r];
+  }
   if (t < 256) hl[t] = 0;
   __syncthreads();
+  for (int d = 6; d >= 0; --d) {
+#pragma unroll
+    for (int r = 0; r < kNodeRounds; ++r) {
+      const int q = t + kTile * r, kb = q & ~255, slot = q & 255;
+      if (inner[r] && depth[r] == d) node[q] = node[kb + 2 * slot + 1] + node[kb + 2 * slot + 2];
+    }
+    __syncthreads();
+  }
+  float total = 0.f;
+  for (int q = 0; q < nbuf; ++q) total += node[q << 8];
   if (j < V) {
-    const float pj = reinterpret_cast<const float*>(a.keys[1])[j] / total;
+    const float pj = e / total;
     if (a.probs_out) a.probs_out[j] = pj;
     const uint32_t key = __float_as_uint(pj);
     a.keys[0][j] = key;
@@ -513,7 +598,7 @@ __global__ __launch_bounds__(kT) void sample_full_kernel(SArgs a) {
   const int t = threadIdx.x, V = a.V;
   uint32_t kv[kPer];
 #pragma unroll
-  for (int i = 0; i < kPer; ++i) kv[i] = t + kT * i < V ? a.keys[0][t + kT * i] : 0u;
+  for (int i = 0; i < kPer; ++i) kv[i] = a.keys[0][min(t + kT * i, V - 1)];
 #pragma unroll
   for (int i = 0; i < kPer; ++i)
     if (t + kT * i < V) sh_p[pad(t + kT * i)] = __uint_as_float(kv[i]);
@@ -542,14 +627,18 @@ __global__ __launch_bounds__(kT) void sample_table_kernel(SArgs a) {
   // requested at once; the order is irrelevant: only the binade with its margin is used)
   float pv[kPer];
 #pragma unroll
-  for (int i = 0; i < kPer; ++i) pv[i] = t + kT * i < 64 * c0 ? p[t + kT * i] : 0.f;
+  for (int i = 0; i < kPer; ++i) {
+    const float v = p[min(t + kT * i, n - 1)];
+    pv[i] = t + kT * i < 64 * c0 ? v : 0.f;
+  }
   double pre = 0.0;
 #pragma unroll
   for (int i = 0; i < kPer; ++i) pre += double(pv[i]);
   for (int o = 32; o; o >>= 1) pre += __shfl_xor(pre, o);
   if (lane == 0) red[wv] = pre;
   const int c = c0 + wv;
-  const float x = c < nch ? p[64 * c + lane] : 0.f;
+  const float xl = p[min(64 * c + lane, n - 1)];
+  const float x = c < nch ? xl : 0.f;
   double v = x;
   for (int o = 32; o; o >>= 1) v += __shfl_xor(v, o);
   if (lane == 0) csum[wv] = v;
@@ -584,13 +673,23 @@ __global__ __launch_bounds__(kTileThreads) void sample_radix_kernel(SArgs a, int
   __shared__ uint32_t base[256], run[256], wcnt[kTileThreads / 64][256], wtot[kTileThreads / 64];
   const int t = threadIdx.x, w = blockIdx.x, wv = t >> 6, lane = lane_id();
   const int V = a.V, ntiles = (V + kTile - 1) / kTile;
+  const uint32_t* kin = a.keys[pass & 1];
+  const uint32_t* iin = a.ids[pass & 1];
+  uint32_t key[kRounds], id[kRounds];   // this thread's entries, requested with the counts
+#pragma unroll
+  for (int r = 0; r < kRounds; ++r) {
+    const int e = w * kTile + r * kTileThreads + t;
+    key[r] = kin[min(e, V - 1)];
+    id[r] = iin[min(e, V - 1)];
+  }
   const uint32_t* H = a.hist + pass * kHistWords;
   uint32_t tot = 0, part = 0;
 #pragma unroll
   for (int i = 0; i < kMaxTiles; ++i) {
-    const uint32_t h = i < ntiles ? H[i * 256 + t] : 0u;
+    const uint32_t hl = H[min(i, ntiles - 1) * 256 + t];
+    const uint32_t h = i < ntiles ? hl : 0u;
     tot += h;
-    if (i < w) part += h;
+    part += i < w ? h : 0u;
   }
   const int inc = wave_incl_scan(int(tot));
   if (lane == 63) wtot[wv] = uint32_t(inc);
@@ -599,20 +698,16 @@ __global__ __launch_bounds__(kTileThreads) void sample_radix_kernel(SArgs a, int
   for (int i = 0; i < wv; ++i) off += wtot[i];
   base[t] = off + uint32_t(inc) - tot + part;
   run[t] = 0;
-  const uint32_t* kin = a.keys[pass & 1];
-  const uint32_t* iin = a.ids[pass & 1];
   uint32_t* kout = a.keys[(pass + 1) & 1];
   uint32_t* iout = a.ids[(pass + 1) & 1];
   const int shift = 8 * pass;
   const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+#pragma unroll
   for (int r = 0; r < kRounds; ++r) {
     for (int i = 0; i < kTileThreads / 64; ++i) wcnt[i][t] = 0;
     __syncthreads();
-    const int e = w * kTile + r * kTileThreads + t;
-    const bool valid = e < V;
-    const uint32_t key = valid ? kin[e] : 0u;
-    const uint32_t id = valid ? iin[e] : 0u;
-    const uint32_t dig = 255u - ((key >> shift) & 255u);
+    const bool valid = w * kTile + r * kTileThreads + t < V;
+    const uint32_t dig = 255u - ((key[r] >> shift) & 255u);
     uint64_t peers = __ballot(valid);
     for (int bit = 0; bit < 8; ++bit) {
       const bool on = (dig >> bit) & 1u;
@@ -631,10 +726,10 @@ __global__ __launch_bounds__(kTileThreads) void sample_radix_kernel(SArgs a, int
     __syncthreads();
     const uint32_t pos = base[dig] + run[dig] + wcnt[wv][dig] + uint32_t(rk);
     if (valid && pos < uint32_t(V)) {   // always true when the counts are consistent
-      kout[pos] = key;
-      iout[pos] = id;
+      kout[pos] = key[r];
+      iout[pos] = id[r];
       if (pass + 1 < kPasses) {
-        const uint32_t nd = 255u - ((key >> (shift + 8)) & 255u);
+        const uint32_t nd = 255u - ((key[r] >> (shift + 8)) & 255u);
         atomicAdd(&a.hist[(pass + 1) * kHistWords + (pos / kTile) * 256 + nd], 1u);
       }
     }
@@ -651,7 +746,7 @@ __global__ __launch_bounds__(kT) void sample_nucleus_kernel(SArgs a) {
   const uint32_t* ks = a.keys[kPasses & 1];
   uint32_t kv[kPer];   // every load issued before the first LDS store
 #pragma unroll
-  for (int i = 0; i < kPer; ++i) kv[i] = t + kT * i < V ? ks[t + kT * i] : 0u;
+  for (int i = 0; i < kPer; ++i) kv[i] = ks[min(t + kT * i, V - 1)];
   for (int c = t; c < V / 64; c += kT) {
     ttot[c] = a.table[c];
     tex[c] = a.table[kChunks + c];
@@ -675,7 +770,7 @@ __global__ __launch_bounds__(kT) void sample_nucleus_kernel(SArgs a) {
 
 // ---------------------------------------------------------------- host side
 struct SLayout {
-  size_t keys0, keys1, ids0, ids1, hist, table, bsum, bytes;
+  size_t keys0, keys1, ids0, ids1, hist, table, tmax, lsum, bytes;
 };
 
 static size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
@@ -689,8 +784,9 @@ static SLayout slayout(int V) {
   s.ids1 = 3 * arr;
   s.hist = 4 * arr;
   s.table = s.hist + align256(size_t(kPasses) * kHistWords * sizeof(uint32_t));
-  s.bsum = s.table + align256(size_t(3) * (kVMax / 64) * sizeof(int));
-  s.bytes = s.bsum + 256;
+  s.tmax = s.table + align256(size_t(3) * (kVMax / 64) * sizeof(int));
+  s.lsum = s.tmax + align256(size_t(kMaxTiles) * sizeof(float));
+  s.bytes = s.lsum + size_t(kVMax / kRedChunk) * 256 * sizeof(float);
   return s;
 }
 
@@ -743,7 +839,8 @@ extern "C" int32_t msd_sample_token(const float* logits, int32_t vocab, double t
   a.ids[1] = reinterpret_cast<uint32_t*>(ws + L.ids1);
   a.hist = reinterpret_cast<uint32_t*>(ws + L.hist);
   a.table = reinterpret_cast<int*>(ws + L.table);
-  a.bsum = reinterpret_cast<float*>(ws + L.bsum);
+  a.tmax = reinterpret_cast<float*>(ws + L.tmax);
+  a.lsum = reinterpret_cast<float*>(ws + L.lsum);
   a.V = vocab;
   a.use_pen = rep_penalty != 1.0;
   a.pen = float(rep_penalty);
@@ -759,7 +856,10 @@ extern "C" int32_t msd_sample_token(const float* logits, int32_t vocab, double t
     return hipGetLastError() == hipSuccess ? MSD_OK : MSD_E_HIP;
   }
   const int ntiles = (vocab + kTile - 1) / kTile;
-  hipLaunchKernelGGL(sample_softmax_kernel, dim3((vocab + kRedChunk - 1) / kRedChunk), dim3(kT), kLdsBuf, s, a);
+  const int nbuf = (vocab + kRedChunk - 1) / kRedChunk;
+  hipLaunchKernelGGL(sample_max_kernel, dim3(ntiles), dim3(kTile), 0, s, a);
+  hipLaunchKernelGGL(sample_leaf_kernel, dim3((nbuf * kSlots + kLeafWaves - 1) / kLeafWaves), dim3(64 * kLeafWaves), 0, s,
+                     a);
   hipLaunchKernelGGL(sample_norm_kernel, dim3(ntiles), dim3(kTile), 0, s, a);
   if (hipGetLastError() != hipSuccess) return MSD_E_HIP;
   if (a.mode == kFull) {
