@@ -170,30 +170,25 @@ __global__ __launch_bounds__(256) void mx_gemm(GemmArgs g) {
       for (int cb = 0; cb < CB; ++cb)
         acc[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a[rb]), as_bf16x8(w[cb]), acc[rb][cb], 0, 0, 0);
   };
-  int c = c0;
-  for (; c + U <= c1; c += U) {
+  // U chunks per round, all loads issued before the first MMA; the last round's chunks past c1
+  // reload chunk c1 - 1 and are skipped (loads stay unconditional: a load under a branch is
+  // waited for at the join)
+  for (int c = c0; c < c1; c += U) {
     uint4 a[U][RB], w[U][CB];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int k = (c + u) * kBK;
+      const int k = min(c + u, c1 - 1) * kBK;
 #pragma unroll
-      for (int rb = 0; rb < RB; ++rb)
-        a[u][rb] = aval[rb] ? *reinterpret_cast<const uint4*>(arow[rb] + k) : make_uint4(0, 0, 0, 0);
+      for (int rb = 0; rb < RB; ++rb) {
+        const uint4 v = *reinterpret_cast<const uint4*>(arow[rb] + k);
+        a[u][rb] = aval[rb] ? v : make_uint4(0, 0, 0, 0);
+      }
 #pragma unroll
       for (int cb = 0; cb < CB; ++cb) w[u][cb] = *reinterpret_cast<const uint4*>(wrow[cb] + k);
     }
 #pragma unroll
-    for (int u = 0; u < U; ++u) step(a[u], w[u]);
-  }
-  for (; c < c1; ++c) {
-    const int k = c * kBK;
-    uint4 a[RB], w[CB];
-#pragma unroll
-    for (int rb = 0; rb < RB; ++rb)
-      a[rb] = aval[rb] ? *reinterpret_cast<const uint4*>(arow[rb] + k) : make_uint4(0, 0, 0, 0);
-#pragma unroll
-    for (int cb = 0; cb < CB; ++cb) w[cb] = *reinterpret_cast<const uint4*>(wrow[cb] + k);
-    step(a, w);
+    for (int u = 0; u < U; ++u)
+      if (c + u < c1) step(a[u], w[u]);
   }
   // D layout of a 16 x 16 tile: lane holds rows 4*(lane/16) + r (r < 4) of column lane % 16
   float* out = g.splits > 1 ? g.out + int64_t(blockIdx.z) * g.M * g.N : g.out;
