@@ -224,17 +224,22 @@ __global__ __launch_bounds__(kNormThreads) void mx_norm(float* h, const float* p
   __shared__ float hs[kMaxRows];
   const int m = blockIdx.x + row0;
   float* hr = h + int64_t(m) * d;
+  // every load (residual, partials, the scales of this thread's outputs) is issued up front from
+  // clamped indices: a load under a branch is waited for at the join
   float v[NE];
+  uint16_t sc[NE];
 #pragma unroll
   for (int i = 0; i < NE; ++i) {
     const int n = threadIdx.x + kNormThreads * i;
-    v[i] = n < d ? hr[n] : 0.f;
+    const float hv = hr[min(n, d - 1)];
+    v[i] = n < d ? hv : 0.f;
+    sc[i] = scale[perm_elem(min(n, d - 1), d)];
   }
-  if (splits > 0) {
+  {   // partials (none when splits == 0: then split 0 is read and ignored)
     float pv[kMaxSplitK][NE];
 #pragma unroll
     for (int z = 0; z < kMaxSplitK; ++z) {
-      const int zc = min(z, splits - 1);
+      const int zc = min(z, max(splits, 1) - 1);
 #pragma unroll
       for (int i = 0; i < NE; ++i) {
         const int n = min(threadIdx.x + kNormThreads * i, d - 1);
@@ -259,9 +264,10 @@ __global__ __launch_bounds__(kNormThreads) void mx_norm(float* h, const float* p
   }
   ss = block_sum256(ss, red);
   const float r = sqrtf(ss / float(d) + 1e-5f);
-  for (int j = threadIdx.x; j < d; j += kNormThreads) {
-    const int i = perm_elem(j, d);
-    xn[int64_t(blockIdx.x) * d + j] = f2bf(bf2f(scale[i]) * (hs[i] / r));
+#pragma unroll
+  for (int q = 0; q < NE; ++q) {
+    const int j = threadIdx.x + kNormThreads * q;
+    if (j < d) xn[int64_t(blockIdx.x) * d + j] = f2bf(bf2f(sc[q]) * (hs[perm_elem(j, d)] / r));
   }
 }
 
@@ -285,12 +291,17 @@ __global__ __launch_bounds__(256) void mx_qkv_fin(const float* part, int splits,
   const int m = blockIdx.x, nq = (H + 2 * KV) * kDh;
   const int t = blockIdx.y * 256 + threadIdx.x;
   if (t >= nq / 2) return;
-  const int p = row_pos(rows, m);
   const int col = 2 * t;
   float2 pv[kMaxSplitK];
 #pragma unroll
   for (int z = 0; z < kMaxSplitK; ++z)
     pv[z] = *reinterpret_cast<const float2*>(part + (int64_t(min(z, splits - 1)) * M + m) * nq + col);
+  // the loads that depend on the position (RoPE row, cache row) are issued together, for every
+  // column (a load under a branch is waited for at the join)
+  const int p = row_pos(rows, m);
+  const int64_t crow = cache_row(rows, m, p);
+  const int ri = (col % kDh) >> 1;
+  const float cs = rope[int64_t(p) * kDh + ri], sn = rope[int64_t(p) * kDh + kDh / 2 + ri];
   float s0 = 0.f, s1 = 0.f;
 #pragma unroll
   for (int z = 0; z < kMaxSplitK; ++z)
@@ -299,23 +310,17 @@ __global__ __launch_bounds__(256) void mx_qkv_fin(const float* part, int splits,
       s1 += pv[z].y;
     }
   const int head = col / kDh, rr = col % kDh;
-  float o0 = s0, o1 = s1;
-  int d0 = rr, d1 = rr + 1;
-  if (head < H + KV) {
-    const int i = rr >> 1;
-    const float cs = rope[int64_t(p) * kDh + i], sn = rope[int64_t(p) * kDh + kDh / 2 + i];
-    o0 = s0 * cs - s1 * sn;
-    o1 = s0 * sn + s1 * cs;
-    d0 = i;
-    d1 = i + kDh / 2;
-  }
+  const bool rot = head < H + KV;   // q and k get RoPE, v is stored as projected
+  const float r0 = s0 * cs - s1 * sn, r1 = s0 * sn + s1 * cs;
+  const float o0 = rot ? r0 : s0, o1 = rot ? r1 : s1;
+  const int d0 = rot ? ri : rr, d1 = rot ? ri + kDh / 2 : rr + 1;
   float* q = qkv + int64_t(m) * nq + head * kDh;
   q[d0] = o0;
   q[d1] = o1;
   if (head >= H) {
     const bool isv = head >= H + KV;
     const int g = isv ? head - H - KV : head - H;
-    uint16_t* cp = (isv ? vc : kc) + (int64_t(g) * rows.pool + cache_row(rows, m, p)) * kDh;
+    uint16_t* cp = (isv ? vc : kc) + (int64_t(g) * rows.pool + crow) * kDh;
     cp[d0] = f2bf(o0);
     cp[d1] = f2bf(o1);
   }
