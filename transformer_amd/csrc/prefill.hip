@@ -441,14 +441,19 @@ __global__ __launch_bounds__(64 * kAttnWaves) void mx_attention_decode(const flo
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int m = blockIdx.x, h = blockIdx.y, g = h / (H / KV);
   const int nqkv = (H + 2 * KV) * kDh, d = H * kDh;
-  const int p = row_pos(rows, m);
+  const int j0 = 64 * wv, j = j0 + lane;
+  // q, the page-table entries and p are loaded together: the page-table load does not wait for
+  // p (every entry of a row is a sanitized page; p only selects which rows are cached
+  // positions), and no load sits under a branch (it would be waited for at the join)
   const float* qr = qkv + int64_t(m) * nqkv;
-  if (threadIdx.x < kDh) sq[threadIdx.x] = qr[h * kDh + threadIdx.x];
+  const float qv = qr[h * kDh + (threadIdx.x & (kDh - 1))];
+  const int64_t cr = cache_row(rows, m, rows.pages ? min(j, rows.max_pages * kPage - 1) : j);
+  const int p = row_pos(rows, m);
+  if (threadIdx.x < kDh) sq[threadIdx.x] = qv;
   const uint16_t* kg = kc + int64_t(g) * rows.pool * kDh;
   const uint16_t* vg = vc + int64_t(g) * rows.pool * kDh;
-  const int j0 = 64 * wv, j = j0 + lane;
   const int nj = max(0, min(64, p + 1 - j0));   // positions of this wave (the last one may be p)
-  srow[wv][lane] = j < p ? int(cache_row(rows, m, j)) : 0;
+  srow[wv][lane] = j < p ? int(cr) : 0;
   __syncthreads();
   float mx = -INFINITY, ls = 0.f, o = 0.f;
   if (nj > 0) {
