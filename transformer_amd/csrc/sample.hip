@@ -280,15 +280,20 @@ __device__ int inverse_cdf(float* v, int n, bool divide, float div, double u, Bl
   __shared__ uint8_t flag[kT];
   const int t = threadIdx.x, base = t * kPer;
   const int cnt = max(0, min(kPer, n - base));
+  double tot = 0.0;
   if (divide) {
 #pragma unroll 8
     for (int i = 0; i < kPer; ++i)
-      if (i < cnt) v[pad(base + i)] = v[pad(base + i)] / div;
-  }
-  double tot = 0.0;
+      if (i < cnt) {
+        const float w = v[pad(base + i)] / div;
+        v[pad(base + i)] = w;
+        tot += double(w);
+      }
+  } else {
 #pragma unroll 8
-  for (int i = 0; i < kPer; ++i)
-    if (i < cnt) tot += double(v[pad(base + i)]);
+    for (int i = 0; i < kPer; ++i)
+      if (i < cnt) tot += double(v[pad(base + i)]);
+  }
   const double excl = block_excl_scan_f64(tot, b);
   double r = excl;
 #pragma unroll 8
@@ -361,6 +366,13 @@ __device__ int nucleus_cutoff(const float* p, int n, float t32, const int* ttot,
     const int E = binade(s);
     const int S = int(ldexpf(s, 23 - E));
     const int lim = te == E ? int(ldexpf(t32, 23 - E)) : (1 << 24);
+    // the LDS reads of both paths are issued together, from clamped indices
+    const int end = min(n, (k & ~63) + 64);   // the rest of the current chunk
+    const bool valid = k + lane < end;
+    const float xl = p[pad(min(k + lane, n - 1))];
+    const int cc = (k >> 6) + lane;
+    const int ccl = min(cc, kChunks - 1);
+    const int tvl = ttot[ccl], tel = tex[ccl], tdv = tdl[ccl];
     if ((k & 63) == 0) {
       // up to 64 whole chunks at once, lane = chunk k/64 + lane.  A chunk with ties leaves the
       // sum's parity at the parity of its even-start total whatever it started with; one
@@ -368,11 +380,10 @@ __device__ int nucleus_cutoff(const float* p, int n, float t32, const int* ttot,
       // chunks since the last chunk with ties, and an inclusive scan of the totals gives the
       // sum after every chunk; the run stops before the first chunk outside the table's
       // binade or whose sum would reach the binade's end or top_p.
-      const int cc = (k >> 6) + lane;
       const bool in = (cc + 1) * 64 <= n;
-      const int tv = in ? ttot[cc] : -1;
-      const bool good = tv >= 0 && tex[cc] == E;
-      const int dv = good ? tdl[cc] : 0;
+      const int tv = in ? tvl : -1;
+      const bool good = tv >= 0 && tel == E;
+      const int dv = good ? tdv : 0;
       const uint64_t gm = __ballot(good);
       const int ngood = ~gm == 0 ? 64 : __ffsll(static_cast<unsigned long long>(~gm)) - 1;
       if (ngood > 0) {
@@ -397,9 +408,7 @@ __device__ int nucleus_cutoff(const float* p, int n, float t32, const int* ttot,
         }
       }
     }
-    const int end = min(n, (k & ~63) + 64);   // the rest of the current chunk
-    const bool valid = k + lane < end;
-    const float x = valid ? p[pad(k + lane)] : 0.f;
+    const float x = valid ? xl : 0.f;
     uint64_t tm, bm;
     const int pi = chunk_prefix(x, valid, S, E, tm, bm);
     const uint64_t m = __ballot(valid && S + pi >= lim);
