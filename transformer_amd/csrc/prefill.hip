@@ -221,46 +221,38 @@ __global__ __launch_bounds__(kNormThreads) void mx_norm(float* h, const float* p
                                                         const uint16_t* scale, uint16_t* xn, int row0) {
   constexpr int NE = kMaxRows / kNormThreads;
   __shared__ float red[4];
-  __shared__ float hs[kMaxRows];
+  __shared__ __align__(16) float hs[kMaxRows];
   const int m = blockIdx.x + row0;
   float* hr = h + int64_t(m) * d;
   // every load (residual, partials, the scales of this thread's outputs) is issued up front from
-  // clamped indices: a load under a branch is waited for at the join
-  float v[NE];
+  // clamped indices: a load under a branch is waited for at the join.  Thread t sums elements
+  // 4t..4t+3 (16-byte loads; d is a multiple of 32) and writes outputs t, t + 256, ...
+  static_assert(kMaxRows == 4 * kNormThreads, "one float4 of the row per thread");
+  const int n4 = 4 * threadIdx.x, n4c = min(n4, d - 4);
+  const bool own = n4 < d;
   uint16_t sc[NE];
 #pragma unroll
-  for (int i = 0; i < NE; ++i) {
-    const int n = threadIdx.x + kNormThreads * i;
-    const float hv = hr[min(n, d - 1)];
-    v[i] = n < d ? hv : 0.f;
-    sc[i] = scale[perm_elem(min(n, d - 1), d)];
-  }
+  for (int i = 0; i < NE; ++i) sc[i] = scale[perm_elem(min(int(threadIdx.x) + kNormThreads * i, d - 1), d)];
+  float4 v = *reinterpret_cast<const float4*>(hr + n4c);
   {   // partials (none when splits == 0: then split 0 is read and ignored)
-    float pv[kMaxSplitK][NE];
-#pragma unroll
-    for (int z = 0; z < kMaxSplitK; ++z) {
-      const int zc = min(z, max(splits, 1) - 1);
-#pragma unroll
-      for (int i = 0; i < NE; ++i) {
-        const int n = min(threadIdx.x + kNormThreads * i, d - 1);
-        pv[z][i] = part[(int64_t(zc) * M + m) * d + n];
-      }
-    }
+    float4 pv[kMaxSplitK];
 #pragma unroll
     for (int z = 0; z < kMaxSplitK; ++z)
+      pv[z] = *reinterpret_cast<const float4*>(part + (int64_t(min(z, max(splits, 1) - 1)) * M + m) * d + n4c);
 #pragma unroll
-      for (int i = 0; i < NE; ++i)
-        if (z < splits) v[i] += pv[z][i];
+    for (int z = 0; z < kMaxSplitK; ++z)
+      if (z < splits) {
+        v.x += pv[z].x;
+        v.y += pv[z].y;
+        v.z += pv[z].z;
+        v.w += pv[z].w;
+      }
   }
   float ss = 0.f;
-#pragma unroll
-  for (int i = 0; i < NE; ++i) {
-    const int n = threadIdx.x + kNormThreads * i;
-    if (n < d) {
-      if (splits) hr[n] = v[i];
-      hs[n] = v[i];
-      ss += v[i] * v[i];
-    }
+  if (own) {
+    if (splits) *reinterpret_cast<float4*>(hr + n4) = v;
+    *reinterpret_cast<float4*>(hs + n4) = v;
+    ss = ((v.x * v.x + v.y * v.y) + v.z * v.z) + v.w * v.w;
   }
   ss = block_sum256(ss, red);
   const float r = sqrtf(ss / float(d) + 1e-5f);
