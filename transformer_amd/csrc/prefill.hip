@@ -282,59 +282,70 @@ __global__ __launch_bounds__(256) void mx_qkv_fin(const float* part, int splits,
                                                   float* qkv) {
   const int m = blockIdx.x, nq = (H + 2 * KV) * kDh;
   const int t = blockIdx.y * 256 + threadIdx.x;
-  if (t >= nq / 2) return;
-  const int col = 2 * t;
-  float2 pv[kMaxSplitK];
+  if (t >= nq / 4) return;
+  const int col = 4 * t;   // column pairs (col, col + 1) and (col + 2, col + 3), one head
+  float4 pv[kMaxSplitK];
 #pragma unroll
   for (int z = 0; z < kMaxSplitK; ++z)
-    pv[z] = *reinterpret_cast<const float2*>(part + (int64_t(min(z, splits - 1)) * M + m) * nq + col);
+    pv[z] = *reinterpret_cast<const float4*>(part + (int64_t(min(z, splits - 1)) * M + m) * nq + col);
   // the loads that depend on the position (RoPE row, cache row) are issued together, for every
   // column (a load under a branch is waited for at the join)
   const int p = row_pos(rows, m);
   const int64_t crow = cache_row(rows, m, p);
   const int ri = (col % kDh) >> 1;
-  const float cs = rope[int64_t(p) * kDh + ri], sn = rope[int64_t(p) * kDh + kDh / 2 + ri];
-  float s0 = 0.f, s1 = 0.f;
+  const float2 cs = *reinterpret_cast<const float2*>(rope + int64_t(p) * kDh + ri);
+  const float2 sn = *reinterpret_cast<const float2*>(rope + int64_t(p) * kDh + kDh / 2 + ri);
+  float4 sv = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
   for (int z = 0; z < kMaxSplitK; ++z)
     if (z < splits) {
-      s0 += pv[z].x;
-      s1 += pv[z].y;
+      sv.x += pv[z].x;
+      sv.y += pv[z].y;
+      sv.z += pv[z].z;
+      sv.w += pv[z].w;
     }
   const int head = col / kDh, rr = col % kDh;
   const bool rot = head < H + KV;   // q and k get RoPE, v is stored as projected
-  const float r0 = s0 * cs - s1 * sn, r1 = s0 * sn + s1 * cs;
-  const float o0 = rot ? r0 : s0, o1 = rot ? r1 : s1;
-  const int d0 = rot ? ri : rr, d1 = rot ? ri + kDh / 2 : rr + 1;
   float* q = qkv + int64_t(m) * nq + head * kDh;
-  q[d0] = o0;
-  q[d1] = o1;
-  if (head >= H) {
-    const bool isv = head >= H + KV;
-    const int g = isv ? head - H - KV : head - H;
-    uint16_t* cp = (isv ? vc : kc) + (int64_t(g) * rows.pool + crow) * kDh;
-    cp[d0] = f2bf(o0);
-    cp[d1] = f2bf(o1);
+  const bool isv = head >= H + KV;
+  const int g = isv ? head - H - KV : head - H;
+  uint16_t* cp = (isv ? vc : kc) + (int64_t(g) * rows.pool + crow) * kDh;
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    const float s0 = e ? sv.z : sv.x, s1 = e ? sv.w : sv.y;
+    const float c = e ? cs.y : cs.x, sg = e ? sn.y : sn.x;
+    const float r0 = s0 * c - s1 * sg, r1 = s0 * sg + s1 * c;
+    const float o0 = rot ? r0 : s0, o1 = rot ? r1 : s1;
+    const int d0 = rot ? ri + e : rr + 2 * e, d1 = rot ? ri + e + kDh / 2 : rr + 2 * e + 1;
+    q[d0] = o0;
+    q[d1] = o1;
+    if (head >= H) {
+      cp[d0] = f2bf(o0);
+      cp[d1] = f2bf(o1);
+    }
   }
 }
 
 // Row blockIdx.x: act_f = silu(gate_f) * up_f over the summed partials (gate/up are the packed
 // rows 2f, 2f+1; model.py:159), bf16 at the down projection's input position of f.
 __global__ __launch_bounds__(256) void mx_swiglu_fin(const float* part, int splits, int M, int F, uint16_t* act) {
-  const int m = blockIdx.x, f = blockIdx.y * 256 + threadIdx.x;
+  const int m = blockIdx.x, f = 2 * (blockIdx.y * 256 + threadIdx.x);   // outputs f and f + 1 (F is even)
   if (f >= F) return;
-  float2 pv[kMaxSplitK];
+  float4 pv[kMaxSplitK];
 #pragma unroll
   for (int z = 0; z < kMaxSplitK; ++z)
-    pv[z] = *reinterpret_cast<const float2*>(part + (int64_t(min(z, splits - 1)) * M + m) * (2 * F) + 2 * f);
-  float gt = 0.f, up = 0.f;
+    pv[z] = *reinterpret_cast<const float4*>(part + (int64_t(min(z, splits - 1)) * M + m) * (2 * F) + 2 * f);
+  float g0 = 0.f, u0 = 0.f, g1 = 0.f, u1 = 0.f;
 #pragma unroll
   for (int z = 0; z < kMaxSplitK; ++z)
     if (z < splits) {
-      gt += pv[z].x;
-      up += pv[z].y;
+      g0 += pv[z].x;
+      u0 += pv[z].y;
+      g1 += pv[z].z;
+      u1 += pv[z].w;
     }
-  act[int64_t(m) * F + perm_pos(f, F)] = f2bf((gt * (1.f / (1.f + expf(-gt)))) * up);
+  act[int64_t(m) * F + perm_pos(f, F)] = f2bf((g0 * (1.f / (1.f + expf(-g0)))) * u0);
+  act[int64_t(m) * F + perm_pos(f + 1, F)] = f2bf((g1 * (1.f / (1.f + expf(-g1)))) * u1);
 }
 
 // Prefill: causal GQA attention of query block blockIdx.y (16 rows) for head blockIdx.x.
@@ -661,7 +672,7 @@ static int run_layers(const msd_config* cfg, const Weights& wt, const Rows& rows
     uint16_t* vc = kc + int64_t(KV) * rows.pool * kDh;
     hipLaunchKernelGGL(mx_norm, dim3(M), dim3(kNormThreads), 0, s, h, part, pending, M, d, Wl, xn, 0);
     if ((err = gemm(xn, d, Wl + off_qkv, M, nqkv, d, part, nqkv, sq, s)) != hipSuccess) break;
-    hipLaunchKernelGGL(mx_qkv_fin, dim3(M, (nqkv / 2 + 255) / 256), dim3(256), 0, s, part, sq, M, H, KV, wt.rope, rows,
+    hipLaunchKernelGGL(mx_qkv_fin, dim3(M, (nqkv / 4 + 255) / 256), dim3(256), 0, s, part, sq, M, H, KV, wt.rope, rows,
                        kc, vc, qkv);
     if (prefill)
       hipLaunchKernelGGL(mx_attention_prefill, dim3(H, (M + kAttnQ - 1) / kAttnQ), dim3(256), 0, s, qkv, M, H, KV,
@@ -671,7 +682,7 @@ static int run_layers(const msd_config* cfg, const Weights& wt, const Rows& rows
     if ((err = gemm(att, d, Wl + off_o, M, d, d, part, d, so, s)) != hipSuccess) break;
     hipLaunchKernelGGL(mx_norm, dim3(M), dim3(kNormThreads), 0, s, h, part, so, M, d, Wl + off_ln2, xn, 0);
     if ((err = gemm(xn, d, Wl + off_gu, M, 2 * ff, d, part, 2 * ff, sg, s)) != hipSuccess) break;
-    hipLaunchKernelGGL(mx_swiglu_fin, dim3(M, (ff + 255) / 256), dim3(256), 0, s, part, sg, M, ff, act);
+    hipLaunchKernelGGL(mx_swiglu_fin, dim3(M, (ff / 2 + 255) / 256), dim3(256), 0, s, part, sg, M, ff, act);
     if ((err = gemm(act, ff, Wl + off_dn, M, d, ff, part, d, sd, s)) != hipSuccess) break;
     pending = sd;
   }
