@@ -107,11 +107,6 @@ __device__ inline float wave_max(float v) {
   return v;
 }
 
-__device__ inline int wave_sum_i(int v) {
-  for (int o = 32; o; o >>= 1) v += __shfl_xor(v, o);
-  return v;
-}
-
 __device__ inline uint64_t wave_max_u64(uint64_t v) {
   for (int o = 32; o; o >>= 1) {
     const uint64_t w = __shfl_xor(v, o);
@@ -133,21 +128,10 @@ __device__ inline int binade(float s) { return int((__float_as_uint(s) >> 23) & 
 struct BlockScratch {   // small shared scratch of the 1024-thread kernels
   float vals[kT];       // pairwise-tree node sums
   double dw[kWaves];
-  int iw[kWaves];
   uint64_t kw[kWaves];
   double dthr;          // inverse CDF threshold
   int i0;
 };
-
-__device__ int block_sum_i(int v, BlockScratch& b) {
-  v = wave_sum_i(v);
-  if (lane_id() == 0) b.iw[threadIdx.x >> 6] = v;
-  __syncthreads();
-  int s = 0;
-  for (int i = 0; i < kWaves; ++i) s += b.iw[i];
-  __syncthreads();
-  return s;
-}
 
 __device__ uint64_t block_max_u64(uint64_t v, BlockScratch& b) {
   v = wave_max_u64(v);
@@ -232,14 +216,18 @@ __device__ float pw_leaf(const float* a, int start, int n) {
 // Buffers of 8192 entries are reduced by the pairwise recursion (thread 256*k + slot evaluates
 // heap slot `slot` of buffer k; leaves first, then inner nodes by decreasing depth) and their
 // results added in buffer order to 0.
-__device__ float np_sum(const float* a, int n, BlockScratch& b) {
+// `pre` (optional): the leaf sums of full buffers, pre[64 k + j] = pw_leaf of entries
+// [8192 k + 128 j, +128) -- the leaves of a full buffer are exactly these 64 blocks.
+__device__ float np_sum(const float* a, int n, BlockScratch& b, const float* pre = nullptr) {
   const int t = threadIdx.x, k = t >> 8, slot = t & 255;
   const int nbuf = (n + kRedChunk - 1) / kRedChunk;
   const int bn = k < nbuf ? min(kRedChunk, n - k * kRedChunk) : 0;
   int start = 0, len = 0;
   const bool valid = k < nbuf && slot < kSlots && pw_node(bn, slot, start, len);
   const bool leaf = valid && len <= kPwBlock;
-  if (leaf) b.vals[t] = pw_leaf(a, k * kRedChunk + start, len);
+  if (leaf)
+    b.vals[t] = pre && bn == kRedChunk ? pre[k * (kRedChunk / kPwBlock) + start / kPwBlock]
+                                       : pw_leaf(a, k * kRedChunk + start, len);
   __syncthreads();
   const int depth = 31 - __clz(slot + 1);
   for (int d = 6; d >= 0; --d) {
@@ -300,20 +288,26 @@ __device__ int inverse_cdf(float* v, int n, bool divide, float div, double u, Bl
   for (int i = 0; i < kPer; ++i)
     if (i < cnt) r += double(v[pad(base + i)]);
   if (cnt > 0 && base + cnt == n) b.dthr = cdf_threshold(r, u);   // r = cdf[n-1] here
+  if (t == 0) b.i0 = n;   // no range crosses: every entry is <= the threshold
   __syncthreads();
   const double thr = b.dthr;
   const bool below = cnt > 0 && r <= thr;
   flag[t] = below;
   __syncthreads();
-  int c = below ? cnt : 0;
+  // cdf is nondecreasing: every range before the crossing one is entirely below, so the count
+  // is the crossing range's base plus its entries below
   if (cnt > 0 && !below && (t == 0 || flag[t - 1])) {   // the range that crosses u
     double rr = excl;
+    int c = 0;
     for (int i = 0; i < cnt; ++i) {
       rr += double(v[pad(base + i)]);
       if (rr <= thr) ++c;
     }
+    b.i0 = base + c;
   }
-  const int cs = block_sum_i(c, b);
+  __syncthreads();
+  const int cs = b.i0;
+  __syncthreads();
   return min(cs, n - 1);
 }
 
@@ -751,6 +745,7 @@ __global__ __launch_bounds__(kT) void sample_nucleus_kernel(SArgs a) {
   extern __shared__ float sh_p[];   // sorted probabilities, padded layout
   __shared__ BlockScratch b;
   __shared__ int ttot[kChunks], tex[kChunks], tdl[kChunks];
+  __shared__ float pre[kVMax / kPwBlock];   // leaf sums of the full 8192-id buffers
   const int t = threadIdx.x, V = a.V;
   const uint32_t* ks = a.keys[kPasses & 1];
   uint32_t kv[kPer];   // every load issued before the first LDS store
@@ -768,10 +763,15 @@ __global__ __launch_bounds__(kT) void sample_nucleus_kernel(SArgs a) {
   if (t < 64) {
     const int c = nucleus_cutoff(sh_p, V, a.t32, ttot, tex, tdl);
     if (t == 0) b.i0 = c;
+  } else if (t - 64 < kVMax / kPwBlock) {
+    // meanwhile the other waves sum the leaves of every full buffer: the renormalising sum
+    // of the kept prefix reuses those of its full buffers
+    const int li = t - 64, k = li / (kRedChunk / kPwBlock);
+    if ((k + 1) * kRedChunk <= V) pre[li] = pw_leaf(sh_p, li * kPwBlock, kPwBlock);
   }
   __syncthreads();
   const int kept = min(b.i0, V);
-  const float fsum = np_sum(sh_p, kept, b);
+  const float fsum = np_sum(sh_p, kept, b, pre);
   const int pos = inverse_cdf(sh_p, kept, true, fsum, a.u[0], b);
   if (t == 0 && a.kept_out) a.kept_out[0] = kept;
   finish(a, int(a.ids[kPasses & 1][pos]));
