@@ -360,9 +360,21 @@ __global__ __launch_bounds__(256) void mx_attention_prefill(const float* qkv, in
   const int h = blockIdx.x, g = h / (H / KV);
   const int nqkv = (H + 2 * KV) * kDh, d = H * kDh;
   const int q0 = blockIdx.y * kAttnQ;
-  for (int t = threadIdx.x; t < kAttnQ * kDh; t += 256) {
-    const int i = q0 + t / kDh;
-    sq[t] = i < M ? qkv[int64_t(i) * nqkv + h * kDh + (t % kDh)] : 0.f;
+  // all loads of a staging step are issued from clamped rows before the LDS stores (a load
+  // under a branch is waited for at the join)
+  constexpr int kQLoads = kAttnQ * kDh / 256, kKVLoads = 64 * kDh / 256;
+  {
+    float qv[kQLoads];
+#pragma unroll
+    for (int u = 0; u < kQLoads; ++u) {
+      const int t = threadIdx.x + 256 * u;
+      qv[u] = qkv[int64_t(min(q0 + t / kDh, M - 1)) * nqkv + h * kDh + (t % kDh)];
+    }
+#pragma unroll
+    for (int u = 0; u < kQLoads; ++u) {
+      const int t = threadIdx.x + 256 * u;
+      sq[t] = q0 + t / kDh < M ? qv[u] : 0.f;
+    }
   }
   float mx[kQW], ls[kQW], o[kQW];
 #pragma unroll
@@ -373,12 +385,21 @@ __global__ __launch_bounds__(256) void mx_attention_prefill(const float* qkv, in
   }
   const int nchunk = min((q0 + kAttnQ + 63) / 64, (M + 63) / 64);
   for (int c = 0; c < nchunk; ++c) {
+    float kb[kKVLoads], vb[kKVLoads];
+#pragma unroll
+    for (int u = 0; u < kKVLoads; ++u) {
+      const int t = threadIdx.x + 256 * u;
+      const int64_t row = int64_t(min(64 * c + t / kDh, M - 1)) * nqkv;
+      kb[u] = qkv[row + (H + g) * kDh + t % kDh];
+      vb[u] = qkv[row + (H + KV + g) * kDh + t % kDh];
+    }
     __syncthreads();
-    for (int t = threadIdx.x; t < 64 * kDh; t += 256) {
-      const int j = 64 * c + t / kDh, e = t % kDh;
-      const bool ok = j < M;
-      sk[(t / kDh) * kKStride + e] = ok ? qkv[int64_t(j) * nqkv + (H + g) * kDh + e] : 0.f;
-      sv[t] = ok ? qkv[int64_t(j) * nqkv + (H + KV + g) * kDh + e] : 0.f;
+#pragma unroll
+    for (int u = 0; u < kKVLoads; ++u) {
+      const int t = threadIdx.x + 256 * u;
+      const bool ok = 64 * c + t / kDh < M;
+      sk[(t / kDh) * kKStride + t % kDh] = ok ? kb[u] : 0.f;
+      sv[t] = ok ? vb[u] : 0.f;
     }
     __syncthreads();
     const int j = 64 * c + lane;
