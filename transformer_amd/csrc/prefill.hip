@@ -550,11 +550,19 @@ __global__ __launch_bounds__(1024) void mx_argmax(const float* logits, int V, in
   __shared__ uint64_t red[16];
   const float* lr = logits + int64_t(blockIdx.x) * ld;
   uint64_t best = 0;
-  for (int j = threadIdx.x; j < V; j += 1024) {
-    uint32_t u = __float_as_uint(lr[j]);
-    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-    const uint64_t key = (uint64_t(u) << 32) | uint64_t(0xffffffffu - uint32_t(j));
-    best = key > best ? key : best;
+  constexpr int kBatch = 16;   // loads in flight per thread (clamped, so none sits under a branch)
+  for (int j0 = threadIdx.x; j0 < V; j0 += kBatch * 1024) {
+    float x[kBatch];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) x[u] = lr[min(j0 + 1024 * u, V - 1)];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int j = j0 + 1024 * u;
+      uint32_t b = __float_as_uint(x[u]);
+      b = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+      const uint64_t key = (uint64_t(b) << 32) | uint64_t(0xffffffffu - uint32_t(j));
+      best = j < V && key > best ? key : best;
+    }
   }
   for (int o = 32; o; o >>= 1) {
     const uint64_t w = __shfl_xor(best, o);
