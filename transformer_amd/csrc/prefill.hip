@@ -271,7 +271,15 @@ __global__ __launch_bounds__(256) void mx_embed(const uint16_t* emb, const int32
     if (threadIdx.x == 0) atomicOr(status, 2);
     t = 0;
   }
-  for (int n = threadIdx.x; n < d; n += 256) h[int64_t(m) * d + n] = bf2f(emb[int64_t(t) * d + n]);
+  constexpr int NE = kMaxRows / 256;   // every load issued before the first store
+  uint16_t e[NE];
+#pragma unroll
+  for (int i = 0; i < NE; ++i) e[i] = emb[int64_t(t) * d + min(int(threadIdx.x) + 256 * i, d - 1)];
+#pragma unroll
+  for (int i = 0; i < NE; ++i) {
+    const int n = threadIdx.x + 256 * i;
+    if (n < d) h[int64_t(m) * d + n] = bf2f(e[i]);
+  }
 }
 
 // Row blockIdx.x: q/k/v = sum_z part[z] (z in order) over the packed q/k/v rows; RoPE on the
@@ -589,13 +597,21 @@ __global__ void mx_sanitize_rows(const int32_t* pos, int fixed_pos, const int32_
   int p = pos ? pos[m] : fixed_pos;
   bool bad = p < 0 || p >= ctx || p / kPage >= max_pages;
   if (bad) p = 0;
-  for (int i = 0; i < max_pages; ++i) {
-    int pg = pages[int64_t(m) * max_pages + i];
-    if (pg < 0 || pg >= pool_pages) {
-      if (i <= p / kPage) bad = true;
-      pg = 0;
+  constexpr int kBatch = 8;   // page-table loads in flight (clamped indices, stores after)
+  for (int i0 = 0; i0 < max_pages; i0 += kBatch) {
+    int pv[kBatch];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) pv[u] = pages[int64_t(m) * max_pages + min(i0 + u, max_pages - 1)];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int i = i0 + u;
+      int pg = pv[u];
+      if (pg < 0 || pg >= pool_pages) {
+        if (i < max_pages && i <= p / kPage) bad = true;
+        pg = 0;
+      }
+      if (i < max_pages) pages_out[int64_t(m) * max_pages + i] = pg;
     }
-    pages_out[int64_t(m) * max_pages + i] = pg;
   }
   if (pos_out) pos_out[m] = p;
   if (bad) atomicOr(status, 4);
