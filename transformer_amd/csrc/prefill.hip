@@ -465,7 +465,7 @@ constexpr int kAttnWaves = 8;
 __global__ __launch_bounds__(64 * kAttnWaves) void mx_attention_decode(const float* qkv, Rows rows, int H, int KV,
                                                                        const uint16_t* kc, const uint16_t* vc,
                                                                        uint16_t* att) {
-  __shared__ float sq[kDh];
+  __shared__ float sq[kDh], skc[kDh], svc[kDh];   // q, and the current position's f32 k and v
   __shared__ float sp[kAttnWaves][64];
   __shared__ int srow[kAttnWaves][64];
   __shared__ float so[kAttnWaves][kDh];
@@ -478,10 +478,11 @@ __global__ __launch_bounds__(64 * kAttnWaves) void mx_attention_decode(const flo
   // p (every entry of a row is a sanitized page; p only selects which rows are cached
   // positions), and no load sits under a branch (it would be waited for at the join)
   const float* qr = qkv + int64_t(m) * nqkv;
-  const float qv = qr[h * kDh + (threadIdx.x & (kDh - 1))];
+  const int qsel = min(int(threadIdx.x) / kDh, 2);   // threads 0..63: q, 64..127: k, others: v
+  const float qv = qr[(qsel == 0 ? h : (qsel == 1 ? H + g : H + KV + g)) * kDh + (threadIdx.x & (kDh - 1))];
   const int64_t cr = cache_row(rows, m, rows.pages ? min(j, rows.max_pages * kPage - 1) : j);
   const int p = row_pos(rows, m);
-  if (threadIdx.x < kDh) sq[threadIdx.x] = qv;
+  if (threadIdx.x < 3 * kDh) (qsel == 0 ? sq : (qsel == 1 ? skc : svc))[threadIdx.x & (kDh - 1)] = qv;
   const uint16_t* kg = kc + int64_t(g) * rows.pool * kDh;
   const uint16_t* vg = vc + int64_t(g) * rows.pool * kDh;
   const int nj = max(0, min(64, p + 1 - j0));   // positions of this wave (the last one may be p)
@@ -510,11 +511,10 @@ __global__ __launch_bounds__(64 * kAttnWaves) void mx_attention_decode(const flo
       }
       s = (a0 + a1) * 0.125f;
     } else if (j == p) {   // current position: f32 K from this row's projection
-      const float* kq = qr + (H + g) * kDh;
       float a0 = 0.f, a1 = 0.f;
       for (int e = 0; e < kDh; e += 2) {
-        a0 += sq[e] * kq[e];
-        a1 += sq[e + 1] * kq[e + 1];
+        a0 += sq[e] * skc[e];
+        a1 += sq[e + 1] * skc[e + 1];
       }
       s = (a0 + a1) * 0.125f;
     }
@@ -523,7 +523,7 @@ __global__ __launch_bounds__(64 * kAttnWaves) void mx_attention_decode(const flo
     ls = wave_sum(e);
     sp[wv][lane] = e;
     __builtin_amdgcn_wave_barrier();
-    const float vcur = qr[(H + KV + g) * kDh + lane];
+    const float vcur = svc[lane];
     float o4[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int jj = 0; jj < 64; ++jj) {
