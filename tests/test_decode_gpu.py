@@ -294,3 +294,108 @@ def test_306m_greedy_full_generation_token_exact(m306):
     assert toks == rtoks
     for a, b in zip(logs[::40], rlogs[::40]):
         np.testing.assert_allclose(a, b, atol=ATOL, rtol=RTOL)
+
+
+def _poke(ptr, offset, data):
+    """Write raw bytes into device memory at ptr + offset (synchronous)."""
+    hip = ctypes.CDLL("libamdhip64.so")
+    hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+    torch.cuda.synchronize()
+    buf = ctypes.create_string_buffer(bytes(data), len(data))
+    assert hip.hipMemcpy(ptr + offset, ctypes.addressof(buf), len(data), 1) == 0
+
+
+def test_arrival_counter_near_wrap_and_stale_key(tiny):
+    """The arrival counter 16 below 2**32 and a garbage argmax key left in the workspace: every
+    step still publishes exactly the oracle's token (the counter and key are reset at the start
+    of each step), and the logits match."""
+    params, prompt, w = tiny
+    dec = Decoder(w, TINY)
+    _poke(dec.workspace_ptr, 4, (2**32 - 16).to_bytes(4, "little"))
+    _poke(dec.workspace_ptr, 8, (0xDEADBEEFCAFEF00D).to_bytes(8, "little"))
+    kc, vc = om.new_kv_cache(TINY)
+    for p, t in enumerate(prompt[:3]):
+        tok, lg = dec.step(int(t), p)
+        ref, rtok = om.decode_step(params, TINY, int(t), p, kc, vc)
+        np.testing.assert_allclose(lg.cpu().numpy(), ref, atol=1e-4, rtol=1e-4)
+        assert tok == rtok
+
+
+def test_argmax_ties_resolve_to_the_lowest_index(tiny):
+    """Planted ties at the maximum (a copy of the argmax's embedding row elsewhere: tied logits
+    are bitwise equal): the token is the lower id, whether the two rows belong to different
+    workgroups, to neighbouring rows of one workgroup or to one wave (multi_sm_decode.py:348-357,
+    np.argmax)."""
+    params, prompt, _ = tiny
+    kc, vc = om.new_kv_cache(TINY)
+    _, a = om.decode_step(params, TINY, int(prompt[0]), 0, kc, vc)
+    V = TINY["vocab_size"]
+    for off in (7919, 1, 8):
+        other = a - off if a - off >= 0 else a + off
+        lo, hi = min(a, other), max(a, other)
+        p2 = dict(params)
+        emb = params["token_emb"].copy()
+        emb[other] = emb[a]
+        p2["token_emb"] = emb
+        assert int(prompt[0]) not in (lo, hi) and hi < V
+        w2 = prepare_decode_weights_nlayer(p2, TINY)
+        dec = Decoder(w2, TINY)
+        tok, lg = dec.step(int(prompt[0]), 0)
+        got = lg.cpu().numpy()
+        assert got[lo] == got[hi] == got.max(), (off, got[lo], got[hi], got.max())
+        assert tok == lo, (off, tok, lo, hi)
+        dec.close()
+
+
+def test_dropin_reports_a_bad_device_token():
+    """The reference-signature entry point returns before its step runs; a step whose device
+    token is out of range is reported (MsdError) by the next call, the status is cleared, and
+    later calls give the oracle's results again."""
+    from transformer_amd import _lib
+    from transformer_amd import multi_sm_decode as msd
+    from transformer_amd.fused_decode_nlayer import new_kv_packed
+    params = make_params(TINY, seed=0)
+    prompt = make_prompt(4, TINY["vocab_size"], seed=1)
+    w = prepare_decode_weights_nlayer(params, TINY)
+    kv = new_kv_packed(TINY)
+    bad = torch.tensor([TINY["vocab_size"] + 5], dtype=torch.int32, device="cuda")
+    msd.multi_sm_decode_nlayer(w, TINY, bad, 0, kv)
+    with pytest.raises(_lib.MsdError) as e:
+        msd.multi_sm_decode_nlayer(w, TINY, int(prompt[0]), 0, kv)
+    assert e.value.code == _lib.MSD_E_ARG
+    msd.check_pending()   # nothing left to report
+    kc, vc = om.new_kv_cache(TINY)
+    for p, t in enumerate(prompt):
+        nt, logits, _ = msd.multi_sm_decode_nlayer(w, TINY, int(t), p, kv)
+        ref, rt = om.decode_step(params, TINY, int(t), p, kc, vc)
+    msd.check_pending()
+    assert int(nt) == rt
+    np.testing.assert_allclose(logits.cpu().numpy(), ref, atol=1e-4, rtol=1e-4)
+    # a bad token at the last call is reported by check_pending()
+    msd.multi_sm_decode_nlayer(w, TINY, bad, 4, kv)
+    with pytest.raises(_lib.MsdError):
+        msd.check_pending()
+
+
+def test_dropin_cache_is_bounded():
+    from transformer_amd import multi_sm_decode as msd
+    from transformer_amd.fused_decode_nlayer import new_kv_packed
+    params = make_params(TINY, seed=0)
+    w = prepare_decode_weights_nlayer(params, TINY)
+    for _ in range(msd.MAX_CACHED_DECODERS + 3):
+        msd.multi_sm_decode_nlayer(w, TINY, 1, 0, new_kv_packed(TINY))
+    msd.check_pending()
+    assert len(msd._decoders) <= msd.MAX_CACHED_DECODERS
+
+
+def test_grid_larger_than_the_device_is_rejected(m306):
+    """Every workgroup of a step waits on others, so the grid must be resident at once: a grid of
+    twice the compute units is refused with MSD_E_CONFIG before anything is launched."""
+    from transformer_amd import _lib
+    params, w = m306
+    cus = _lib.lib().msd_default_workgroups(torch.cuda.current_device())
+    dec = Decoder(w, M306, n_workgroups=2 * cus)
+    with pytest.raises(_lib.MsdError) as e:
+        dec.launch(1, 0)
+    assert e.value.code == _lib.MSD_E_CONFIG
+    dec.close()

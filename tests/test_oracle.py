@@ -289,3 +289,80 @@ def test_synthetic_generator_is_seeded():
     assert np.array_equal(a, b) and not np.array_equal(a, c)
     assert np.array_equal(bf16_round_np(a), a)
     assert abs(a.std() - 0.02) < 1e-3
+
+
+_ROUNDED = ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj")
+
+
+def _hf_bf16_inputs(m, skip=None):
+    """Forward pre-hooks rounding the input of every projection (and of the tied output
+    projection, i.e. the final norm's output) to bf16: float64 -> float32 -> bf16 (RNE), the
+    oracle's rounding.  ``skip`` names one projection left unrounded (negative control)."""
+    def rnd(mod, args):
+        x = args[0]
+        return (x.to(torch.float32).to(torch.bfloat16).to(x.dtype),) + tuple(args[1:])
+    hooks = []
+    for layer in m.model.layers:
+        for name in _ROUNDED:
+            if name == skip:
+                continue
+            mod = getattr(layer.self_attn, name, None) or getattr(layer.mlp, name)
+            hooks.append(mod.register_forward_pre_hook(rnd))
+    if skip != "lm_head":
+        hooks.append(m.lm_head.register_forward_pre_hook(rnd))
+    return hooks
+
+
+def _hf_exact_f64(m, cfg):
+    """Make the HF model's RMSNorm and RoPE tables float64 end to end (it computes the norm in
+    float32 and the RoPE angles' cos/sin in float32 whatever the model dtype); the RoPE tables
+    become the oracle's.  Otherwise float32-level differences flip an occasional bf16 rounding
+    of a projection input when rounding points are inserted."""
+    from transformers.models.llama.modeling_llama import LlamaRMSNorm
+    cos, sin = om.precompute_rope_table(cfg["context_len"], cfg["d_head"], dtype=np.float64)
+    C = torch.from_numpy(np.concatenate([cos, cos], -1))
+    S = torch.from_numpy(np.concatenate([sin, sin], -1))
+    m.model.rotary_emb.forward = lambda x, position_ids: (C[position_ids].to(x.dtype), S[position_ids].to(x.dtype))
+    for mod in m.modules():
+        if isinstance(mod, LlamaRMSNorm):
+            mod.forward = (lambda n: lambda h: n.weight * (h / torch.sqrt(h.pow(2).mean(-1, keepdim=True)
+                                                                          + n.variance_epsilon)))(mod)
+
+
+def test_act_round_bf16_matches_hf_llama_with_rounded_projection_inputs(tiny_params):
+    """act_round="bf16" (the numerics of the matrix-core prefill and batched decode) equals an
+    independent Llama in float64 whose projection inputs are rounded to bf16 by pre-hooks:
+    x before q/k/v, the attention output before o, x2 before gate/up, the SwiGLU activation
+    before down and the final norm's output before the tied logits
+    (kernels/multi_sm_decode.py:143, 229, 268, 289, 320).  Leaving any one of those points
+    unrounded moves the logits by far more than the tolerance, so a missing or misplaced
+    rounding point in the oracle fails here."""
+    cfg = dict(TINY)
+    p64 = {k: v.astype(np.float64) for k, v in tiny_params.items()}
+    rng = np.random.default_rng(6)
+    for k in p64:
+        if k.endswith("scale"):
+            p64[k] = 1.0 + 0.1 * rng.standard_normal(p64[k].shape)
+    toks = make_prompt(24, cfg["vocab_size"], seed=2)
+    ours = om.forward(p64, cfg, toks, act_round="bf16")
+    m = _hf_llama(p64, cfg, torch.float64)
+    _hf_exact_f64(m, cfg)
+    ids = torch.from_numpy(toks.astype(np.int64))[None]
+
+    def hf(skip=None):
+        hooks = _hf_bf16_inputs(m, skip)
+        try:
+            with torch.no_grad():
+                return m(ids).logits[0].numpy()
+        finally:
+            for h in hooks:
+                h.remove()
+    ref = hf()
+    err = float(np.max(np.abs(ours - ref)))
+    assert err < 1e-6, err
+    # the f32 oracle differs from the rounded reference by the bf16 effect itself
+    assert float(np.max(np.abs(om.forward(p64, cfg, toks) - ref))) > 1e-4
+    # negative controls: each rounding point is needed
+    for skip in _ROUNDED + ("lm_head",):
+        off = float(np.max(np.abs(ours - hf(skip))))
+        assert off > 100 * max(err, 1e-9), (skip, off, err)

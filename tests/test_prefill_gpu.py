@@ -78,6 +78,10 @@ def test_306m_prefill_128_matches_oracle(m306):
     print("306M prefill max |logit diff|:", float(np.max(np.abs(la - ref))))
     np.testing.assert_allclose(la, ref, atol=ATOL, rtol=RTOL)
     _check_kv(kv, M306, 128, kc, vc)
+    # against the f32 model.py forward itself (no rounding points), the bound of the task
+    f32 = om.forward(params, M306, toks)
+    print("306M prefill max |logit diff| vs f32 model.py:", float(np.max(np.abs(la - f32))))
+    np.testing.assert_allclose(la, f32, atol=ATOL, rtol=RTOL)
 
 
 def _gpu_greedy_after_prefill(w, cfg, prompt, n):
@@ -97,7 +101,7 @@ def test_prefill_then_decode_token_exact(cfgname, request):
     params, w = request.getfixturevalue(cfgname)
     cfg = TINY if cfgname == "tiny" else M306
     prompt = make_prompt(48 if cfgname == "tiny" else 128, cfg["vocab_size"], seed=9)
-    n = 48 if cfgname == "tiny" else 96
+    n = 48 if cfgname == "tiny" else 128
     got = _gpu_greedy_after_prefill(w, cfg, prompt, n)
     ref = om.greedy_generate(params, cfg, prompt, n, prefill="full", act_round=None, prefill_act_round="bf16")
     assert got == ref

@@ -42,6 +42,20 @@ class MsdError(RuntimeError):
         self.code = code
 
 
+# Bits of a step's status output (next_token[1]): a cross-workgroup wait ran out, a device
+# token was out of range, or the step never completed its arrivals (the value it starts with).
+STATUS_TIMEOUT = 0x1
+STATUS_BAD_TOKEN = 0x2
+STATUS_UNFINISHED = 0x80000000
+
+
+def status_error(status, what):
+    """The MsdError for a non-zero step status word (timeouts and unfinished steps first)."""
+    status = int(status) & 0xFFFFFFFF
+    code = MSD_E_TIMEOUT if status & (STATUS_TIMEOUT | STATUS_UNFINISHED) else MSD_E_ARG
+    return MsdError(code, f"{what} (status {status:#x})")
+
+
 _lib = None
 
 

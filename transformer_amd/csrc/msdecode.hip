@@ -123,6 +123,8 @@ constexpr int kDmaFirst = MSD_DMA_FIRST;
 
 constexpr uint32_t kStatusTimeout = 1u;
 constexpr uint32_t kStatusBadToken = 2u;
+// next_token[1] between the start of a step and its last arrival
+constexpr uint32_t kStatusUnfinished = 0x80000000u;
 
 __host__ __device__ inline int cdiv(int a, int b) { return (a + b - 1) / b; }
 __host__ __device__ inline int64_t align64(int64_t v) { return (v + 63) & ~int64_t(63); }
@@ -948,12 +950,14 @@ __device__ void row_worker(const Args& a, const RowCtx& c, int token) {
       __hip_atomic_fetch_max(keyp, argmax_key(bv, bi), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     // the max above completes before the arrival below is issued
     __builtin_amdgcn_s_waitcnt(0);
+    // The counter and the key were reset by workgroup 0 at the start of this step (before
+    // any of its outputs, which every arrival here depends on), so exactly one arrival sees
+    // GR - 1, whatever the counter held before the step.
     const uint32_t old = __hip_atomic_fetch_add(a.ctrl + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if ((old % uint32_t(a.GR)) == uint32_t(a.GR - 1)) {   // last arriver publishes the token
+    if (old == uint32_t(a.GR - 1)) {   // last arriver publishes the token and the status
       const uint64_t key = __hip_atomic_load(keyp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       a.next_token[0] = int32_t(0xffffffffu - uint32_t(key & 0xffffffffu));
       a.next_token[1] = int32_t(ld_status(a.ctrl));
-      __hip_atomic_store(keyp, uint64_t(0), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
 }
@@ -1325,13 +1329,25 @@ __global__ __launch_bounds__(kThreadsWG, 1) void decode_step_kernel(Args a) {
   c.red_v = reinterpret_cast<float*>(c.ctr + 8);
   c.red_i = reinterpret_cast<int*>(c.red_v + kWavesR);
   if (threadIdx.x < 8) c.ctr[threadIdx.x] = 0;
+  int token = a.token_dev ? *a.token_dev : a.token;
+  const bool bad_token = token < 0 || token >= a.V;
+  if (bad_token) token = token < 0 ? 0 : a.V - 1;   // clamped for addressing, reported below
+  if (wg == 0 && threadIdx.x == 0) {
+    // Start of the step: the arrival counter and the argmax key start from zero, the
+    // bad-token bit of the status word describes this step's token, and the status output
+    // holds a sentinel until the last arriver overwrites it, so a step whose arrivals never
+    // complete still reports a non-zero status.  The stores complete before this workgroup
+    // publishes anything, and every arrival waits for its outputs.
+    __hip_atomic_store(a.ctrl + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(reinterpret_cast<uint64_t*>(a.ctrl + 2), uint64_t(0), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+    if (bad_token) atomicOr(a.ctrl, kStatusBadToken);
+    else atomicAnd(a.ctrl, ~kStatusBadToken);
+    a.next_token[1] = int32_t(kStatusUnfinished);
+    __builtin_amdgcn_s_waitcnt(0);
+  }
   __syncthreads();   // the only workgroup barrier; the roles below meet on LDS counters
 
-  int token = a.token_dev ? *a.token_dev : a.token;
-  if (token < 0 || token >= a.V) {
-    if (wg == 0 && threadIdx.x == 0) atomicOr(a.ctrl, kStatusBadToken);
-    token = token < 0 ? 0 : a.V - 1;
-  }
   if (wv == kLoader) row_loader<D, FF>(a, c);
   else row_worker<D, FF, QPW, ORW, GPW>(a, c, token);
 }
@@ -1396,14 +1412,43 @@ static bool make_plan(const msd_config* c, int G, Plan* p) {
   return p->lds <= size_t(kMaxLds);
 }
 
+// Workgroups of the step that the device can hold at once (compute units x workgroups per
+// unit at this LDS size): every workgroup waits on others, so a grid larger than this could
+// never finish (its waits would run out instead).  Cached per device and LDS size.
+static int resident_capacity(const void* fn, size_t lds) {
+  struct Entry {
+    const void* fn;
+    size_t lds;
+    int dev, cap;
+  };
+  static std::mutex mu;
+  static std::vector<Entry> cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return -1;
+  std::lock_guard<std::mutex> lk(mu);
+  for (const Entry& e : cache)
+    if (e.fn == fn && e.lds == lds && e.dev == dev) return e.cap;
+  int cus = 0, per_cu = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return -1;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kThreadsWG, lds) != hipSuccess) return -1;
+  cache.push_back({fn, lds, dev, cus * per_cu});
+  return cus * per_cu;
+}
+
 template <int D, int FF, int QPW, int ORW, int GPW>
-static hipError_t launch_t(const Args& a, int grid, size_t lds, hipStream_t s) {
+static hipError_t launch_t(const Args& a, int grid, size_t lds, hipStream_t s, bool* not_resident) {
   static size_t attr_lds = 0;
+  const void* fn = reinterpret_cast<const void*>(&decode_step_kernel<D, FF, QPW, ORW, GPW>);
   if (attr_lds < lds) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&decode_step_kernel<D, FF, QPW, ORW, GPW>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
+    hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
     if (e != hipSuccess) return e;
     attr_lds = lds;
+  }
+  const int cap = resident_capacity(fn, lds);
+  if (cap < 0) return hipErrorInvalidValue;
+  if (grid > cap) {
+    *not_resident = true;
+    return hipSuccess;
   }
   hipLaunchKernelGGL((decode_step_kernel<D, FF, QPW, ORW, GPW>), dim3(grid), dim3(kThreadsWG), lds, s, a);
   return hipGetLastError();
@@ -1417,9 +1462,9 @@ static bool plan_instantiated(const msd_config* c, const Plan& p) {
   return false;
 }
 
-static hipError_t launch(const Args& a, int d, int ff, int grid, size_t lds, hipStream_t s) {
-  if (d == 256 && ff == 704) return launch_t<256, 704, 1, 1, 1>(a, grid, lds, s);
-  if (d == 1024 && ff == 2816) return launch_t<1024, 2816, 1, 1, 2>(a, grid, lds, s);
+static hipError_t launch(const Args& a, int d, int ff, int grid, size_t lds, hipStream_t s, bool* not_resident) {
+  if (d == 256 && ff == 704) return launch_t<256, 704, 1, 1, 1>(a, grid, lds, s, not_resident);
+  if (d == 1024 && ff == 2816) return launch_t<1024, 2816, 1, 1, 2>(a, grid, lds, s, not_resident);
   return hipErrorInvalidValue;
 }
 
@@ -1498,7 +1543,10 @@ extern "C" int32_t msd_decode_step(const msd_config* cfg, const void* token_emb,
   a.ring_bytes = p.ring_bytes;
   a.log_rows = p.log_rows;
   a.keep = int(std::min<int64_t>(cfg->n_layers, kKeepBytes / (a.lay.layer_elems * 2)));
-  const hipError_t e = launch(a, cfg->d_model, cfg->d_ff, n_workgroups, p.lds, static_cast<hipStream_t>(stream));
+  bool not_resident = false;
+  const hipError_t e =
+      launch(a, cfg->d_model, cfg->d_ff, n_workgroups, p.lds, static_cast<hipStream_t>(stream), &not_resident);
+  if (not_resident) return MSD_E_CONFIG;
   return e == hipSuccess ? MSD_OK : MSD_E_HIP;
 }
 

@@ -112,11 +112,11 @@ def _prepare(params, config, device):
     return Decoder(w, config, device=device)
 
 
-def _check_status(st, what):
+def _check_status(dec, st, what):
+    """Raise for the first non-zero status in ``st`` (clearing the decoder's status word)."""
     bad = np.nonzero(st)[0]
     if len(bad):
-        code = int(st[bad[0]])
-        raise _lib.MsdError(_lib.MSD_E_TIMEOUT if code & 1 else _lib.MSD_E_ARG, f"{what} (status {code:#x})")
+        dec.raise_for_status(int(st[bad[0]]), what)
 
 
 def run_generation(dec, prompt_ids, max_tokens, temperature=0.0, top_p=1.0, rep_penalty=1.0,
@@ -179,12 +179,12 @@ def run_generation(dec, prompt_ids, max_tokens, temperature=0.0, top_p=1.0, rep_
             host[0:1].copy_(toks[i:i + 1], non_blocking=True)
             host[1:2].copy_(dec_out[i, 1:2], non_blocking=True)
             torch.cuda.current_stream(dev).synchronize()
-            _check_status(np.array([int(host[1])]), f"decode step at pos {P - 1 + i}")
+            _check_status(dec, np.array([int(host[1])]), f"decode step at pos {P - 1 + i}")
             yield int(host[0])
     if not sync_each:
         out = torch.stack([toks, dec_out[:, 1]], 1).cpu().numpy()
         st = np.concatenate([out[:, 1], pre.cpu().numpy()[1:]])
-        _check_status(st, "decode step")
+        _check_status(dec, st, "decode step")
         for t in out[:, 0]:
             yield int(t)
 

@@ -12,7 +12,11 @@ Differences from the reference call, by design:
     uncached device memory (msd_workspace_acquire: the polled exchange words bypass the L2
     caches) and never re-zeroed while the decoder lives: exchange words are tagged with a
     per-call epoch instead (multi_sm_decode.py:400 zero-fills per call).
+  * a step reports failures in its status output; ``Decoder.step`` raises on them at once,
+    ``multi_sm_decode_nlayer`` (which returns before the step has run, as the reference's
+    asynchronous dispatch does) raises them on its next call or from ``check_pending()``.
 """
+import collections
 import ctypes
 
 import torch
@@ -106,6 +110,15 @@ class Decoder:
         _lib.check(rc, "msd_decode_step")
         return out
 
+    def raise_for_status(self, status, what):
+        """Raise the MsdError for a non-zero step status, after clearing the workspace's
+        status word (a timeout bit left set would cut every later step's waits short)."""
+        if int(status) == 0:
+            return
+        _lib.lib().msd_check_status(self.workspace_ptr,
+                                    ctypes.c_void_p(torch.cuda.current_stream(self.device).cuda_stream))
+        raise _lib.status_error(status, what)
+
     def step(self, token, pos):
         """Run one step and return (next_token: int, logits: (V,) f32 device tensor).
 
@@ -115,15 +128,41 @@ class Decoder:
         self._host.copy_(out, non_blocking=True)
         torch.cuda.current_stream(self.device).synchronize()
         tok, status = int(self._host[0]), int(self._host[1])
-        if status != 0:
-            _lib.lib().msd_check_status(self.workspace_ptr,
-                                        ctypes.c_void_p(torch.cuda.current_stream(self.device).cuda_stream))
-            raise _lib.MsdError(_lib.MSD_E_TIMEOUT if status & 1 else _lib.MSD_E_ARG,
-                                f"decode step at pos {pos} (status {status:#x})")
+        self.raise_for_status(status, f"decode step at pos {pos}")
         return tok, self.logits
 
 
-_decoders = {}
+# Decoders of the reference-signature entry point, keyed by (weights dict, KV buffer); the
+# least recently used one is dropped (its workspace returns to the pool) beyond this many.
+MAX_CACHED_DECODERS = 4
+_decoders = collections.OrderedDict()
+
+
+class _Pending:
+    """Status of a launched step, copied to pinned host memory behind an event."""
+
+    def __init__(self, dec, out, pos):
+        self.dec, self.pos = dec, pos
+        self.host = torch.empty(1, dtype=torch.int32).pin_memory()
+        self.host.copy_(out[1:2], non_blocking=True)
+        self.event = torch.cuda.Event()
+        self.event.record(torch.cuda.current_stream(dec.device))
+
+    def check(self):
+        self.event.synchronize()
+        self.dec.raise_for_status(int(self.host[0]), f"decode step at pos {self.pos}")
+
+
+_pending = []
+
+
+def check_pending():
+    """Wait for the steps ``multi_sm_decode_nlayer`` launched and not yet checked, and raise
+    the MsdError of the first one whose status is set (the later ones are dropped)."""
+    global _pending
+    todo, _pending = _pending, []
+    for p in todo:
+        p.check()
 
 
 def multi_sm_decode_nlayer(w, config, token_id, pos, kv_packed, kv_splits=1):
@@ -132,11 +171,31 @@ def multi_sm_decode_nlayer(w, config, token_id, pos, kv_packed, kv_splits=1):
     next_token is a device int32 scalar tensor, logits a fresh (V,) f32 tensor, kv the
     same ``kv_packed`` tensor updated in place.  ``kv_splits`` is accepted for signature
     compatibility; the kernel chooses its own split of the attention work.
+
+    The step runs asynchronously.  Its status is checked when the next call has been
+    enqueued (or by ``check_pending()``): a failed step (a cross-workgroup wait that ran out,
+    an out-of-range device token) raises ``MsdError`` there.
     """
     key = (id(w), kv_packed.data_ptr())
-    dec = _decoders.get(key)
-    if dec is None:
+    dec = _decoders.pop(key, None)
+    if dec is None or dec.w is not w or dec.kv is not kv_packed:
+        if dec is not None:
+            dec.close()
         dec = Decoder(w, config, kv_packed)
-        _decoders[key] = dec
-    out = dec.launch(token_id, pos)
+    _decoders[key] = dec
+    while len(_decoders) > MAX_CACHED_DECODERS:
+        _, old = _decoders.popitem(last=False)
+        check_pending()
+        old.close()
+    out = torch.empty(2, dtype=torch.int32, device=dec.device)
+    dec.launch(token_id, pos, out=out)
+    earlier = _pending[:]
+    _pending.append(_Pending(dec, out, int(pos)))
+    for p in earlier:   # the previous steps ran before this one: check them now
+        _pending.remove(p)
+        try:
+            p.check()
+        except _lib.MsdError:
+            _pending.clear()   # later steps ran with the failed state
+            raise
     return out[0].clone(), dec.logits.clone(), kv_packed
