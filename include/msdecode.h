@@ -153,6 +153,19 @@ int32_t msd_sample_token(const float* logits, int32_t vocab, double temperature,
                          int32_t* token_out, float* probs_out, int32_t* kept_out,
                          void* workspace, void* stream);
 
+/* msd_sample_token without a workspace argument: the scratch lives in a static device array
+ * of the library (one per device, 796,928 bytes, held until the process ends; sized for the
+ * largest vocabulary, so vocab <= 32768 and MSD_E_CONFIG beyond).  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  It calls no allocating
+ * routine.  All calls on one device share the scratch, so calls that overlap on one device
+ * (two streams, two threads) race; calls ordered on one stream are safe.  The scratch needs
+ * no initialisation and each call overwrites what it reads.  Same arguments, numerics and
+ * errors as msd_sample_token otherwise. */
+int32_t msd_sample_token_noalloc(const float* logits, int32_t vocab, double temperature, double top_p,
+                                 double rep_penalty, uint8_t* seen, const double* uniform,
+                                 int32_t* token_out, float* probs_out, int32_t* kept_out, void* stream);
+
 /* Bytes of device workspace msd_prefill needs for a prompt of n_tokens tokens. */
 int64_t msd_prefill_workspace_bytes(const msd_config* cfg, int32_t n_tokens);
 

@@ -23,7 +23,8 @@ _ERRNAMES = {MSD_E_CONFIG: "unsupported config", MSD_E_ARG: "invalid argument",
 EXPORTS = ("msd_packed_weight_elems", "msd_workspace_bytes", "msd_default_workgroups",
            "msd_decode_step", "msd_check_status", "msd_sample_workspace_bytes", "msd_sample_token",
            "msd_prefill_workspace_bytes", "msd_prefill", "msd_prefill_paged", "msd_batch_workspace_bytes",
-           "msd_batch_decode_step", "msd_workspace_acquire", "msd_workspace_release")
+           "msd_batch_decode_step", "msd_workspace_acquire", "msd_workspace_release",
+           "msd_sample_token_noalloc")
 
 
 class MsdConfig(ctypes.Structure):
@@ -89,6 +90,8 @@ def lib():
     L.msd_sample_workspace_bytes.restype = I64
     L.msd_sample_token.argtypes = [P, I32, D, D, D, P, P, P, P, P, P, P]
     L.msd_sample_token.restype = I32
+    L.msd_sample_token_noalloc.argtypes = [P, I32, D, D, D, P, P, P, P, P, P]
+    L.msd_sample_token_noalloc.restype = I32
     L.msd_prefill_workspace_bytes.argtypes = [CP, I32]
     L.msd_prefill_workspace_bytes.restype = I64
     L.msd_prefill.argtypes = [CP, P, P, P, P, P, P, I32, P, P, P, P, P, P]

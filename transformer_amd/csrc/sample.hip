@@ -34,6 +34,7 @@
 #include <math.h>
 
 #include <algorithm>
+#include <mutex>
 
 #include "../../include/msdecode.h"
 
@@ -782,10 +783,10 @@ struct SLayout {
   size_t keys0, keys1, ids0, ids1, hist, table, tmax, lsum, bytes;
 };
 
-static size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+constexpr size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
-static SLayout slayout(int V) {
-  SLayout s;
+constexpr SLayout slayout(int V) {
+  SLayout s{};
   const size_t arr = align256(size_t(V) * sizeof(uint32_t));
   s.keys0 = 0;
   s.keys1 = arr;
@@ -821,10 +822,17 @@ extern "C" int64_t msd_sample_workspace_bytes(int32_t vocab) {
   return int64_t(slayout(vocab).bytes);
 }
 
-extern "C" int32_t msd_sample_token(const float* logits, int32_t vocab, double temperature, double top_p,
-                                    double rep_penalty, uint8_t* seen, const double* uniform,
-                                    int32_t* token_out, float* probs_out, int32_t* kept_out,
-                                    void* workspace, void* stream) {
+namespace mss {
+
+// Scratch of msd_sample_token_noalloc: the workspace of the largest vocabulary, one copy per
+// device (its address is taken once per device with hipGetSymbolAddress; host code never
+// passes the symbol itself to a kernel).  Every call on a device shares it.
+constexpr size_t kScratchBytes = slayout(kVMax).bytes;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+static int32_t sample_impl(const float* logits, int32_t vocab, double temperature, double top_p,
+                           double rep_penalty, uint8_t* seen, const double* uniform, int32_t* token_out,
+                           float* probs_out, int32_t* kept_out, void* workspace, void* stream) {
   if (vocab <= 0 || vocab > kVMax) return MSD_E_CONFIG;
   if (!logits || !seen || !token_out || !workspace) return MSD_E_ARG;
   if (!(temperature >= 0.0) || !isfinite(temperature) || !isfinite(rep_penalty) || rep_penalty == 0.0 ||
@@ -887,4 +895,40 @@ extern "C" int32_t msd_sample_token(const float* logits, int32_t vocab, double t
     if (hipGetLastError() != hipSuccess) return MSD_E_HIP;
   }
   return MSD_OK;
+}
+
+}  // namespace mss
+
+extern "C" int32_t msd_sample_token(const float* logits, int32_t vocab, double temperature, double top_p,
+                                    double rep_penalty, uint8_t* seen, const double* uniform,
+                                    int32_t* token_out, float* probs_out, int32_t* kept_out,
+                                    void* workspace, void* stream) {
+  return sample_impl(logits, vocab, temperature, top_p, rep_penalty, seen, uniform, token_out, probs_out,
+                     kept_out, workspace, stream);
+}
+
+namespace {
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[64] = {};   // device address of `scratch` per device, taken once
+}  // namespace
+
+extern "C" int32_t msd_sample_token_noalloc(const float* logits, int32_t vocab, double temperature, double top_p,
+                                            double rep_penalty, uint8_t* seen, const double* uniform,
+                                            int32_t* token_out, float* probs_out, int32_t* kept_out,
+                                            void* stream) {
+  if (vocab <= 0 || vocab > kVMax || slayout(vocab).bytes > kScratchBytes) return MSD_E_CONFIG;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return MSD_E_HIP;
+  void* ws = nullptr;
+  {
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+      void* p = nullptr;
+      if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return MSD_E_HIP;
+      g_scratch_ptr[dev] = p;
+    }
+    ws = g_scratch_ptr[dev];
+  }
+  return sample_impl(logits, vocab, temperature, top_p, rep_penalty, seen, uniform, token_out, probs_out, kept_out,
+                     ws, stream);
 }
