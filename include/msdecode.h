@@ -92,9 +92,14 @@ int32_t msd_default_workgroups(int32_t device);
  *               [1] the workspace status word at the end of the step (0 = ok; bit 0 = a
  *               cross-workgroup wait ran out, bit 1 = token_dev held an out-of-range id)
  *
- * Supported shapes: d_head 64, d_model 256 or 1024, d_ff a multiple of 16 up to 4096,
- * context_len up to 1024, n_workgroups >= 16 * n_kv_heads.  Returns MSD_E_CONFIG otherwise.
- * Calls that share a workspace must be ordered on one stream.
+ * Supported shapes: d_head 64 and (d_model, d_ff) one of (256, 704), (256, 768), (512, 1408),
+ * (768, 2048), (1024, 2816) -- the reference's d_ff = 8 d / 3 rounded up to 128 (model.py:13-20)
+ * for d_model 256..1024, and the tiny benchmark shape -- with any n_heads = d_model / 64,
+ * n_kv_heads dividing n_heads, context_len up to 1024 and n_workgroups no more than the device
+ * holds at once (every workgroup waits on others; msd_default_workgroups is one per compute
+ * unit).  Returns MSD_E_CONFIG otherwise.  Calls that share a workspace must be ordered on one
+ * stream, and only one step may run on a device at a time (a concurrent kernel could keep some
+ * of its workgroups from starting).
  */
 int32_t msd_decode_step(const msd_config* cfg, const void* token_emb, const void* output_proj,
                         const void* packed_w,

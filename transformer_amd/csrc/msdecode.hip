@@ -51,14 +51,21 @@
 namespace msd {
 
 // Optional phase timestamps for profiling builds (-DMSD_TRACE): lane 0 of a wave records
-// s_memrealtime (100 MHz) at phase boundaries of layer MSD_TRACE_LAYER into
-// msd_trace_buffer[workgroup][slot].  Compiled out otherwise.
+// s_memrealtime (100 MHz) at phase boundaries of every layer into
+// msd_trace_buffer[layer][workgroup][slot] (the tail after the last layer is recorded as layer
+// n_layers), and per-wave stamps of layer MSD_TRACE_LAYER into msd_trace_waves.  Compiled out
+// otherwise.
 #ifdef MSD_TRACE
-__device__ uint64_t msd_trace_buffer[4096 * 32];
-#define MSD_TRACE_POINT(cond, layer, slot)                                                \
-  do {                                                                                    \
-    if ((cond) && (layer) == MSD_TRACE_LAYER && (threadIdx.x & 63) == 0)                  \
-      msd_trace_buffer[blockIdx.x * 32 + (slot)] = __builtin_amdgcn_s_memrealtime();      \
+#ifndef MSD_TRACE_LAYER
+#define MSD_TRACE_LAYER 10
+#endif
+constexpr int kTraceLayers = 64, kTraceWgs = 512, kTraceSlots = 32;
+__device__ uint64_t msd_trace_buffer[kTraceLayers * kTraceWgs * kTraceSlots];
+#define MSD_TRACE_POINT(cond, layer, slot)                                                              \
+  do {                                                                                                  \
+    if ((cond) && (layer) < kTraceLayers && blockIdx.x < kTraceWgs && (threadIdx.x & 63) == 0)          \
+      msd_trace_buffer[((layer) * kTraceWgs + blockIdx.x) * kTraceSlots + (slot)] =                     \
+          __builtin_amdgcn_s_memrealtime();                                                             \
   } while (0)
 __device__ uint64_t msd_trace_waves[4096 * 16 * 8];
 #define MSD_TRACE_WAVE(layer, slot)                                                         \
@@ -67,16 +74,8 @@ __device__ uint64_t msd_trace_waves[4096 * 16 * 8];
       msd_trace_waves[(blockIdx.x * 16 + (threadIdx.x >> 6)) * 8 + (slot)] =              \
           __builtin_amdgcn_s_memrealtime();                                               \
   } while (0)
-#define MSD_TRACE_CLOCK(cond, layer, slot)                                                \
-  do {                                                                                    \
-    if ((cond) && (layer) == MSD_TRACE_LAYER && (threadIdx.x & 63) == 0)                  \
-      msd_trace_buffer[blockIdx.x * 32 + (slot)] = __builtin_amdgcn_s_memtime();          \
-  } while (0)
 #else
 #define MSD_TRACE_POINT(cond, layer, slot) \
-  do {                                     \
-  } while (0)
-#define MSD_TRACE_CLOCK(cond, layer, slot) \
   do {                                     \
   } while (0)
 #define MSD_TRACE_WAVE(layer, slot) \
@@ -730,7 +729,6 @@ __device__ void row_worker(const Args& a, const RowCtx& c, int token) {
     }
     weights(4 * l);
     MSD_TRACE_POINT(wv == 0, l, 16);
-    MSD_TRACE_CLOCK(wv == 0, l, 12);
     {
       XV<NLD> xv;
       norm(xv);
@@ -894,12 +892,12 @@ __device__ void row_worker(const Args& a, const RowCtx& c, int token) {
     load_vec(sc, l + 1 < a.L ? layer_w(a, l + 1) + lay.off_ln1 : a.lnf);   // scale of the next norm
     bar();
     MSD_TRACE_POINT(wv == 0, l, 23);
-    MSD_TRACE_CLOCK(wv == 0, l, 13);
   }
   // ---- h += last down output; x = final rmsnorm(h); tied logits over this workgroup's
   //      vocabulary rows (multi_sm_decode.py:314-337)
   gather_x<kWavesR, HPW, 0, kFirstPoll, D>(layer_x(a, a.L - 1) + lay.x_hd2 + myrep, D, c.xhd2, c.tag, a.ctrl, wv, lane, bad);
   bar();
+  MSD_TRACE_POINT(wv == 0, a.L - 1, 6);
   add_res(c.xhd2);
   XV<NLD> xv;
   norm(xv);
@@ -937,6 +935,7 @@ __device__ void row_worker(const Args& a, const RowCtx& c, int token) {
     c.red_i[wv] = besti;
   }
   bar();
+  MSD_TRACE_POINT(wv == 0, a.L, 12);
   if (wv == 0 && lane == 0) {   // argmax: larger value wins, ties -> lower index (np.argmax)
     float bv = c.red_v[0];
     int bi = c.red_i[0];
@@ -1360,14 +1359,40 @@ struct Plan {   // per-config launch parameters
   size_t lds;
 };
 
+// Instantiated shapes: (d_model, d_ff, per-wave caps of QKV pairs, O/down rows and gate/up
+// pairs).  The reference's configurations (d_ff = 8d/3 rounded up to 128, model.py:13-20, for
+// d = 256, 512, 768, 1024) and the tiny benchmark configuration (d 256, d_ff 704); on 256
+// workgroups every one of them needs at most the listed rows per wave, with up to one KV head
+// per query head.
+#define MSD_SHAPES(X)        \
+  X(256, 704, 1, 1, 1)       \
+  X(256, 768, 1, 1, 1)       \
+  X(512, 1408, 1, 1, 1)      \
+  X(768, 2048, 1, 1, 2)      \
+  X(1024, 2816, 1, 1, 2)
+
+struct Shape {
+  int d, ff, qpw, orw, gpw;
+};
+static const Shape kShapes[] = {
+#define MSD_SHAPE_ENTRY(D, FF, Q, O, G) {D, FF, Q, O, G},
+    MSD_SHAPES(MSD_SHAPE_ENTRY)
+#undef MSD_SHAPE_ENTRY
+};
+
+static const Shape* find_shape(int d, int ff) {
+  for (const Shape& sh : kShapes)
+    if (sh.d == d && sh.ff == ff) return &sh;
+  return nullptr;
+}
+
 static bool config_ok(const msd_config* c) {
   if (!c) return false;
   if (c->d_head != kDh || c->n_heads <= 0 || c->n_kv_heads <= 0 || c->n_layers <= 0) return false;
   if (c->n_heads * kDh != c->d_model || c->n_heads % c->n_kv_heads != 0) return false;
   if (c->d_ff <= 0 || c->d_ff % 16 != 0 || c->vocab_size <= 0 || c->context_len <= 0) return false;
   if (c->context_len > 1024) return false;
-  if (!((c->d_model == 256 && c->d_ff == 704) || (c->d_model == 1024 && c->d_ff == 2816))) return false;
-  return true;
+  return find_shape(c->d_model, c->d_ff) != nullptr;
 }
 
 constexpr int kMaxLds = 160 * 1024;
@@ -1454,17 +1479,17 @@ static hipError_t launch_t(const Args& a, int grid, size_t lds, hipStream_t s, b
   return hipGetLastError();
 }
 
-// Instantiated shapes (d_model, d_ff, per-wave row caps): the tiny and the 306M
-// configurations on 256 workgroups (and on any grid whose per-wave rows fit the caps).
+// The plan's per-wave row counts must fit the instance compiled for the shape.
 static bool plan_instantiated(const msd_config* c, const Plan& p) {
-  if (c->d_model == 256 && c->d_ff == 704) return p.qpw <= 1 && p.orw <= 1 && p.gpw <= 1;
-  if (c->d_model == 1024 && c->d_ff == 2816) return p.qpw <= 1 && p.orw <= 1 && p.gpw <= 2;
-  return false;
+  const Shape* sh = find_shape(c->d_model, c->d_ff);
+  return sh && p.qpw <= sh->qpw && p.orw <= sh->orw && p.gpw <= sh->gpw;
 }
 
 static hipError_t launch(const Args& a, int d, int ff, int grid, size_t lds, hipStream_t s, bool* not_resident) {
-  if (d == 256 && ff == 704) return launch_t<256, 704, 1, 1, 1>(a, grid, lds, s, not_resident);
-  if (d == 1024 && ff == 2816) return launch_t<1024, 2816, 1, 1, 2>(a, grid, lds, s, not_resident);
+#define MSD_SHAPE_LAUNCH(D, FF, Q, O, G) \
+  if (d == D && ff == FF) return launch_t<D, FF, Q, O, G>(a, grid, lds, s, not_resident);
+  MSD_SHAPES(MSD_SHAPE_LAUNCH)
+#undef MSD_SHAPE_LAUNCH
   return hipErrorInvalidValue;
 }
 
@@ -1624,6 +1649,7 @@ extern "C" int msd_trace_waves_copy(void* host) {
   return hipMemcpyFromSymbol(host, HIP_SYMBOL(msd::msd_trace_waves), sizeof(uint64_t) * 4096 * 16 * 8) == hipSuccess ? 0 : -1;
 }
 extern "C" int msd_trace_copy(void* host) {
-  return hipMemcpyFromSymbol(host, HIP_SYMBOL(msd::msd_trace_buffer), sizeof(uint64_t) * 4096 * 32) == hipSuccess ? 0 : -1;
+  return hipMemcpyFromSymbol(host, HIP_SYMBOL(msd::msd_trace_buffer),
+                             sizeof(uint64_t) * kTraceLayers * kTraceWgs * kTraceSlots) == hipSuccess ? 0 : -1;
 }
 #endif
