@@ -188,6 +188,27 @@ int32_t msd_prefill(const msd_config* cfg, const void* token_emb, const void* ou
                     const int32_t* tokens, int32_t n_tokens, void* kv, void* workspace,
                     float* logits_last, float* logits_all, int32_t* next_token, void* stream);
 
+/* Bytes of device workspace msd_verify needs for n_tokens rows. */
+int64_t msd_verify_workspace_bytes(const msd_config* cfg, int32_t n_tokens);
+
+/* Speculative-decode verification: the target model's forward pass over tokens[0..n_tokens)
+ * (device int32) at positions start_pos..start_pos+n_tokens-1, over a contiguous KV cache that
+ * holds rows 0..start_pos-1.  Row i attends as a decode step at its position: cached rows
+ * 0..start_pos+i-1 as stored (bf16; the rows of tokens 0..i-1 are written by this call first)
+ * and its own un-rounded K/V (multi_sm_decode.py:182-221), so its logits are those the
+ * sequential decode steps would give once tokens 0..i-1 are accepted.  Writes the K/V rows of
+ * every position, the f32 logits of every row (n_tokens x vocab_size) and argmax[2i] = the
+ * argmax of row i (lowest index on ties), argmax[2i+1] = status (bit 1 = a token id out of
+ * range).  Numerics of msd_prefill (bf16 projection inputs on the matrix cores).  Requires
+ * start_pos >= 1, start_pos + n_tokens <= context_len <= 512.
+ * Replaces the parallel verification kernel the reference describes (K draft tokens through the
+ * full target in one call, a mini-prefill with an existing KV cache: knowledge/program.md:
+ * 147-155; no code of it is in the reference snapshot, so the interface is this library's own). */
+int32_t msd_verify(const msd_config* cfg, const void* token_emb, const void* output_proj,
+                   const void* packed_w, const void* lnf_s, const float* rope, const int32_t* tokens,
+                   int32_t n_tokens, int32_t start_pos, void* kv, void* workspace, float* logits,
+                   int32_t* argmax, void* stream);
+
 /* Paged KV cache (used by msd_prefill_paged and msd_batch_decode_step): a pool of pages of 16
  * positions, bf16, laid out [layer][K, V][kv_head][pool_pages * 16][d_head].  A sequence's
  * position p is stored at page page_table[p / 16], slot p % 16.  (The contiguous cache of

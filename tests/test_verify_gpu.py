@@ -1,0 +1,96 @@
+"""Speculative-decode verification (msd_verify) and the greedy speculative loop (GPU).
+
+The reference describes a parallel verification kernel: K draft tokens through the full target
+in one call, a mini-prefill over the existing KV cache (knowledge/program.md:147-155).  Row i
+of a verification must give the logits of the sequential decode step at its position once rows
+0..i-1 are accepted, so the oracle is ``decode_step`` teacher-forced through the draft tokens
+after ``prefill_with_kv`` of the prompt, with the matrix-core rounding points
+(act_round="bf16"); logits within 2e-2 abs / 1e-2 rel, argmax equal, cache rows equal.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import model as om
+from transformer_amd import _lib
+from transformer_amd.configs import M306, TINY
+from transformer_amd.fused_decode_nlayer import new_kv_packed, prepare_decode_weights_nlayer, unpack_kv_caches
+from transformer_amd.prefill import Prefiller
+from transformer_amd.speculative import Verifier, speculative_generate
+from transformer_amd.synthetic import make_params, make_prompt
+
+pytestmark = pytest.mark.gpu
+
+ATOL, RTOL = 2e-2, 1e-2
+
+
+def _check_rows(params, cfg, w, P, draft, start_check_kv=True):
+    prompt = make_prompt(P, cfg["vocab_size"], seed=21)
+    kv = new_kv_packed(cfg)
+    Prefiller(w, cfg, max_tokens=P).launch(prompt, kv)
+    ver = Verifier(w, cfg, max_tokens=len(draft))
+    logits, am = ver.launch(draft, P, kv)
+    got, gam = logits.cpu().numpy(), am.cpu().numpy()
+    _, kc, vc = om.prefill_with_kv(params, cfg, prompt, act_round="bf16")
+    rope = om.precompute_rope_table(cfg["context_len"], cfg["d_head"])
+    worst = 0.0
+    for i, t in enumerate(draft):
+        ref, ra = om.decode_step(params, cfg, int(t), P + i, kc, vc, act_round="bf16", rope=rope)
+        np.testing.assert_allclose(got[i], ref, atol=ATOL, rtol=RTOL)
+        worst = max(worst, float(np.abs(got[i] - ref).max()))
+        assert gam[i, 0] == ra and gam[i, 1] == 0, i
+    if start_check_kv:
+        ks, vs = unpack_kv_caches(kv, cfg["n_layers"], cfg["n_kv_heads"], cfg["context_len"], cfg["d_head"])
+        n = P + len(draft)
+        for l in (0, cfg["n_layers"] - 1):
+            np.testing.assert_allclose(ks[l][:, :n].float().cpu().numpy(), kc[l][:, :n], atol=ATOL, rtol=RTOL)
+            np.testing.assert_allclose(vs[l][:, :n].float().cpu().numpy(), vc[l][:, :n], atol=ATOL, rtol=RTOL)
+    return worst
+
+
+def test_tiny_verification_rows_equal_sequential_decode_steps():
+    params = make_params(TINY, seed=0)
+    w = prepare_decode_weights_nlayer(params, TINY)
+    for P, k in ((20, 6), (1, 1), (100, 9)):
+        draft = make_prompt(k, TINY["vocab_size"], seed=30 + P)
+        worst = _check_rows(params, TINY, w, P, draft)
+        print(f"tiny verify P={P} k={k} max |logit diff| {worst}")
+
+
+def test_306m_verification_rows_equal_sequential_decode_steps():
+    params = make_params(M306, seed=0, resid_scaled=True)
+    w = prepare_decode_weights_nlayer(params, M306)
+    draft = make_prompt(5, M306["vocab_size"], seed=41)
+    worst = _check_rows(params, M306, w, 64, draft)
+    print("306M verify max |logit diff|", worst)
+
+
+@pytest.mark.parametrize("draft_kind", ["same_model", "other_model"])
+def test_speculative_generation_is_the_target_greedy_generation(draft_kind):
+    params = make_params(TINY, seed=0)
+    w = prepare_decode_weights_nlayer(params, TINY)
+    if draft_kind == "same_model":
+        dparams, dw = params, w
+    else:
+        dcfg_params = make_params(TINY, seed=9)
+        dparams, dw = dcfg_params, prepare_decode_weights_nlayer(dcfg_params, TINY)
+    prompt = make_prompt(16, TINY["vocab_size"], seed=1)
+    toks, stats = speculative_generate(w, TINY, dw, TINY, prompt, 40, k=4)
+    ref = om.greedy_generate(params, TINY, prompt, 40, prefill="full", act_round="bf16")
+    print(draft_kind, stats)
+    assert toks == ref
+    if draft_kind == "same_model":
+        assert stats["accepted_draft_tokens"] > 0
+
+
+def test_verification_argument_checks():
+    params = make_params(TINY, seed=0)
+    w = prepare_decode_weights_nlayer(params, TINY)
+    kv = new_kv_packed(TINY)
+    ver = Verifier(w, TINY, max_tokens=4)
+    with pytest.raises(ValueError):
+        ver.launch([1, 2], 0, kv)                       # start 0 is a prefill
+    with pytest.raises(ValueError):
+        ver.launch([1, 2], TINY["context_len"] - 1, kv)   # past the context
+    with pytest.raises(ValueError):
+        ver.launch([1, 2, 3, 4, 5], 3, kv)               # more rows than the workspace holds

@@ -24,7 +24,7 @@ EXPORTS = ("msd_packed_weight_elems", "msd_workspace_bytes", "msd_default_workgr
            "msd_decode_step", "msd_check_status", "msd_sample_workspace_bytes", "msd_sample_token",
            "msd_prefill_workspace_bytes", "msd_prefill", "msd_prefill_paged", "msd_batch_workspace_bytes",
            "msd_batch_decode_step", "msd_workspace_acquire", "msd_workspace_release",
-           "msd_sample_token_noalloc")
+           "msd_sample_token_noalloc", "msd_verify_workspace_bytes", "msd_verify")
 
 
 class MsdConfig(ctypes.Structure):
@@ -102,6 +102,10 @@ def lib():
     L.msd_batch_workspace_bytes.restype = I64
     L.msd_batch_decode_step.argtypes = [CP, P, P, P, P, P, P, P, I32, P, I32, P, I32, P, P, P, P]
     L.msd_batch_decode_step.restype = I32
+    L.msd_verify_workspace_bytes.argtypes = [CP, I32]
+    L.msd_verify_workspace_bytes.restype = I64
+    L.msd_verify.argtypes = [CP, P, P, P, P, P, P, I32, I32, P, P, P, P, P]
+    L.msd_verify.restype = I32
     _lib = L
     return L
 

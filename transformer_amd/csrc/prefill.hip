@@ -113,13 +113,14 @@ __device__ __forceinline__ int perm_elem(int j, int K) {
 // Rows of a pass: row m is sequence seq(m) at position pos(m).
 struct Rows {
   int M;
-  const int32_t* pos;     // NULL: pos(m) = m (prefill)
+  const int32_t* pos;     // NULL: pos(m) = pos0 + m (prefill from pos0)
   int batched;            // seq(m) = m; else every row is sequence 0
   const int32_t* pages;   // [seq][max_pages] page table, NULL = identity
   int max_pages;
   int pool;               // pool positions (16 * pages)
+  int pos0;               // position of row 0 when pos is NULL
 };
-__device__ __forceinline__ int row_pos(const Rows& r, int m) { return r.pos ? r.pos[m] : m; }
+__device__ __forceinline__ int row_pos(const Rows& r, int m) { return r.pos ? r.pos[m] : r.pos0 + m; }
 __device__ __forceinline__ int64_t cache_row(const Rows& r, int m, int p) {
   const int seq = r.batched ? m : 0;
   const int page = r.pages ? r.pages[int64_t(seq) * r.max_pages + p / kPage] : p / kPage;
@@ -747,19 +748,30 @@ extern "C" int64_t msd_prefill_workspace_bytes(const msd_config* cfg, int32_t n_
   return int64_t(layout(cfg, n_tokens).bytes);
 }
 
+// The forward pass over tokens[0..n_tokens) at positions start..start+n_tokens-1.  With
+// start == 0 this is the prompt prefill (causal attention within the pass, f32 keys and values
+// of the pass, model.py:194-231).  With start > 0 it is the verification of draft tokens over an
+// existing cache: every row attends like a decode step at its position (cached rows 0..p-1 as
+// stored bf16, including the draft rows this pass has just written, and its own un-rounded K/V,
+// multi_sm_decode.py:182-221), so row i's logits are those the sequential decode steps would
+// give after accepting rows 0..i-1.  argmax_all (optional) receives every row's
+// (argmax, status) pair.
 static int32_t prefill_impl(const msd_config* cfg, const Weights& wt, const int32_t* tokens, int32_t n_tokens,
-                            const int32_t* page_table, int32_t max_pages, int32_t pool_pages, void* kv,
-                            void* workspace, float* logits_last, float* logits_all, int32_t* next_token,
-                            hipStream_t s) {
+                            int32_t start, const int32_t* page_table, int32_t max_pages, int32_t pool_pages,
+                            void* kv, void* workspace, float* logits_last, float* logits_all, int32_t* next_token,
+                            int32_t* argmax_all, hipStream_t s) {
   if (!mx_config_ok(cfg)) return MSD_E_CONFIG;
   const int M = n_tokens;
-  if (M <= 0 || M > cfg->context_len) return MSD_E_ARG;
+  if (M <= 0 || start < 0 || start + M > cfg->context_len) return MSD_E_ARG;
+  if (start > 0 && cfg->context_len > 64 * kAttnWaves) return MSD_E_CONFIG;   // decode attention: 512 positions
+  if (argmax_all && !logits_all) return MSD_E_ARG;
   if (!wt.emb || !wt.outp || !wt.w || !wt.lnf || !wt.rope || !tokens || !kv || !workspace || !logits_last ||
       !next_token)
     return MSD_E_ARG;
   if (!aligned16(wt.emb) || !aligned16(wt.outp) || !aligned16(wt.w) || !aligned16(kv) || !aligned16(workspace))
     return MSD_E_ARG;
-  if (page_table && (max_pages * kPage < M || max_pages > (cfg->context_len + kPage - 1) / kPage || pool_pages <= 0))
+  if (page_table && (max_pages * kPage < start + M || max_pages > (cfg->context_len + kPage - 1) / kPage ||
+                     pool_pages <= 0))
     return MSD_E_ARG;
   const int d = cfg->d_model, V = cfg->vocab_size;
   const Layout L = layout(cfg, M);
@@ -771,21 +783,26 @@ static int32_t prefill_impl(const msd_config* cfg, const Weights& wt, const int3
   int32_t* pages = reinterpret_cast<int32_t*>(ws + L.pages);
   if (hipMemsetAsync(status, 0, 4, s) != hipSuccess) return MSD_E_HIP;
   if (page_table)
-    hipLaunchKernelGGL(mx_sanitize_rows, dim3(1), dim3(64), 0, s, nullptr, M - 1, page_table, 1, max_pages,
+    hipLaunchKernelGGL(mx_sanitize_rows, dim3(1), dim3(64), 0, s, nullptr, start + M - 1, page_table, 1, max_pages,
                        cfg->context_len, pool_pages, nullptr, pages, status);
-  Rows rows{M, nullptr, 0, page_table ? pages : nullptr, max_pages, page_table ? pool_pages * kPage : cfg->context_len};
+  Rows rows{M, nullptr, 0, page_table ? pages : nullptr, max_pages, page_table ? pool_pages * kPage : cfg->context_len,
+            start};
   hipLaunchKernelGGL(mx_embed, dim3(M), dim3(256), 0, s, wt.emb, tokens, d, h, status, V);
   hipError_t err;
-  const int pending = run_layers(cfg, wt, rows, static_cast<uint16_t*>(kv), L, ws, true, s, err);
+  const int pending = run_layers(cfg, wt, rows, static_cast<uint16_t*>(kv), L, ws, start == 0, s, err);
   if (err != hipSuccess) return MSD_E_HIP;
   // final norm of the rows whose logits are wanted, then the tied output projection
   const int r0 = logits_all ? 0 : M - 1, nr = M - r0;
   hipLaunchKernelGGL(mx_norm, dim3(nr), dim3(kNormThreads), 0, s, h, part, pending, M, d, wt.lnf, xn, r0);
   if (gemm(xn, d, wt.outp, nr, V, d, logits_all ? logits_all : logits_last, V, 1, s) != hipSuccess) return MSD_E_HIP;
   const float* last = logits_all ? logits_all + int64_t(M - 1) * V : logits_last;
-  if (logits_all && hipMemcpyAsync(logits_last, last, size_t(V) * 4, hipMemcpyDeviceToDevice, s) != hipSuccess)
+  if (logits_all && last != logits_last &&
+      hipMemcpyAsync(logits_last, last, size_t(V) * 4, hipMemcpyDeviceToDevice, s) != hipSuccess)
     return MSD_E_HIP;
-  hipLaunchKernelGGL(mx_argmax, dim3(1), dim3(1024), 0, s, logits_last, V, V, next_token, status);
+  if (argmax_all)   // every row (next_token points at the last row's pair)
+    hipLaunchKernelGGL(mx_argmax, dim3(M), dim3(1024), 0, s, logits_all, V, V, argmax_all, status);
+  else
+    hipLaunchKernelGGL(mx_argmax, dim3(1), dim3(1024), 0, s, logits_last, V, V, next_token, status);
   return hipGetLastError() == hipSuccess ? MSD_OK : MSD_E_HIP;
 }
 
@@ -795,8 +812,8 @@ extern "C" int32_t msd_prefill(const msd_config* cfg, const void* token_emb, con
                                float* logits_all, int32_t* next_token, void* stream) {
   const Weights wt{static_cast<const uint16_t*>(token_emb), static_cast<const uint16_t*>(output_proj),
                    static_cast<const uint16_t*>(packed_w), static_cast<const uint16_t*>(lnf_s), rope};
-  return prefill_impl(cfg, wt, tokens, n_tokens, nullptr, 0, 0, kv, workspace, logits_last, logits_all, next_token,
-                      static_cast<hipStream_t>(stream));
+  return prefill_impl(cfg, wt, tokens, n_tokens, 0, nullptr, 0, 0, kv, workspace, logits_last, logits_all, next_token,
+                      nullptr, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int32_t msd_prefill_paged(const msd_config* cfg, const void* token_emb, const void* output_proj,
@@ -807,8 +824,25 @@ extern "C" int32_t msd_prefill_paged(const msd_config* cfg, const void* token_em
   if (!page_table) return MSD_E_ARG;
   const Weights wt{static_cast<const uint16_t*>(token_emb), static_cast<const uint16_t*>(output_proj),
                    static_cast<const uint16_t*>(packed_w), static_cast<const uint16_t*>(lnf_s), rope};
-  return prefill_impl(cfg, wt, tokens, n_tokens, page_table, max_pages, pool_pages, kv_pool, workspace, logits_last,
-                      nullptr, next_token, static_cast<hipStream_t>(stream));
+  return prefill_impl(cfg, wt, tokens, n_tokens, 0, page_table, max_pages, pool_pages, kv_pool, workspace, logits_last,
+                      nullptr, next_token, nullptr, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int64_t msd_verify_workspace_bytes(const msd_config* cfg, int32_t n_tokens) {
+  return msd_prefill_workspace_bytes(cfg, n_tokens);
+}
+
+extern "C" int32_t msd_verify(const msd_config* cfg, const void* token_emb, const void* output_proj,
+                              const void* packed_w, const void* lnf_s, const float* rope, const int32_t* tokens,
+                              int32_t n_tokens, int32_t start_pos, void* kv, void* workspace, float* logits,
+                              int32_t* argmax, void* stream) {
+  if (!cfg || !logits || !argmax || n_tokens <= 0 || start_pos < 1) return MSD_E_ARG;
+  const Weights wt{static_cast<const uint16_t*>(token_emb), static_cast<const uint16_t*>(output_proj),
+                   static_cast<const uint16_t*>(packed_w), static_cast<const uint16_t*>(lnf_s), rope};
+  // the last row's logits land in logits (as part of logits_all); its argmax again in argmax[2(n-1)]
+  return prefill_impl(cfg, wt, tokens, n_tokens, start_pos, nullptr, 0, 0, kv, workspace,
+                      logits + int64_t(n_tokens - 1) * cfg->vocab_size, logits, argmax + 2 * (n_tokens - 1), argmax,
+                      static_cast<hipStream_t>(stream));
 }
 
 extern "C" int64_t msd_batch_workspace_bytes(const msd_config* cfg, int32_t batch) {
@@ -849,7 +883,7 @@ extern "C" int32_t msd_batch_decode_step(const msd_config* cfg, const void* toke
   if (hipMemsetAsync(status, 0, 4, s) != hipSuccess) return MSD_E_HIP;
   hipLaunchKernelGGL(mx_sanitize_rows, dim3((M + 255) / 256), dim3(256), 0, s, positions, 0, page_tables, M, max_pages,
                      cfg->context_len, pool_pages, rowpos, pages, status);
-  Rows rows{M, rowpos, 1, pages, max_pages, pool_pages * kPage};
+  Rows rows{M, rowpos, 1, pages, max_pages, pool_pages * kPage, 0};
   hipLaunchKernelGGL(mx_embed, dim3(M), dim3(256), 0, s, wt.emb, tokens, d, h, status, V);
   hipError_t err;
   const int pending = run_layers(cfg, wt, rows, static_cast<uint16_t*>(kv_pool), L, ws, false, s, err);
