@@ -69,7 +69,7 @@ def _events_ms(fn, reps):
     return times[len(times) // 2]
 
 
-def secondary(w, cfg, dec):
+def secondary(w, cfg, dec, first_token):
     """Prefill (128 tokens) and sampled-decode figures, on the decoder's weights and KV."""
     import numpy as np
     import torch
@@ -146,6 +146,16 @@ def secondary(w, cfg, dec):
     bms = _events_ms(batched, 3)
     if bool((ring[1:, 1::2] != 0).any()):
         raise RuntimeError("status set in the batched run")
+    # the whole generation of the headline workload in one launch (tokens fed back on the device)
+    pos_end = cfg["context_len"] - 1
+    tok0 = torch.tensor([int(first_token)], dtype=torch.int32, device="cuda")
+    nsteps = pos_end - 32
+    one = lambda: dec.launch_steps(tok0, 32, nsteps)
+    one()
+    lms = _events_ms(one, 3)
+    out["decode_one_launch"] = {"tok_s": round(nsteps / (lms / 1e3), 1), "us_per_token": round(lms / nsteps * 1e3, 2),
+                                "workload": f"306M, {nsteps} greedy steps at positions 32..{pos_end - 1} in one "
+                                            "launch (each step's argmax fed to the next inside the kernel)"}
     out["batched_paged_decode"] = {"tok_s": round(B * steps / (bms / 1e3), 1), "ms_per_step": round(bms / steps, 4),
                                    "workload": "306M, 8 sequences (prompts U[16,256]) x 128 steps, 16-token "
                                                "pages from a shuffled pool, all 8 stepped per call"}
@@ -277,7 +287,7 @@ def main():
 
     extra = {}
     if args.secondary:
-        extra = secondary(w, cfg, dec)
+        extra = secondary(w, cfg, dec, first)
 
     line = {
         "metric": METRIC,

@@ -108,6 +108,21 @@ int32_t msd_decode_step(const msd_config* cfg, const void* token_emb, const void
                         uint32_t epoch, float* logits, int32_t* next_token,
                         int32_t n_workgroups, void* stream);
 
+/* n_steps greedy decode steps in one launch: step s runs at position pos + s on the argmax of
+ * step s - 1 (step 0 on token_id / token_dev), fed back on the device without leaving the
+ * kernel.  Tags epoch .. epoch + n_steps - 1 (the next call on this workspace starts above
+ * them).  tokens_out: device int32[2 * n_steps], (argmax, status) per step; logits:
+ * n_steps x vocab_size f32 when all_logits != 0, else vocab_size (the last step's).  Other
+ * arguments and requirements as msd_decode_step, with pos + n_steps <= context_len.
+ * Replaces the persistent decode the reference describes (one launch for N steps with the
+ * next token written in-kernel: knowledge/program.md:246-249, 441-444); no code of it is in
+ * the reference snapshot. */
+int32_t msd_decode_steps(const msd_config* cfg, const void* token_emb, const void* output_proj,
+                         const void* packed_w, const void* lnf_s, const float* rope, int32_t token_id,
+                         const int32_t* token_dev, int32_t pos, int32_t n_steps, void* kv,
+                         void* workspace, uint32_t epoch, float* logits, int32_t all_logits,
+                         int32_t* tokens_out, int32_t n_workgroups, void* stream);
+
 /* Reads and clears the device status word of a workspace (synchronous on `stream`).
  * Returns MSD_OK, MSD_E_TIMEOUT when a wait of an earlier step ran out, or MSD_E_HIP. */
 int32_t msd_check_status(void* workspace, void* stream);

@@ -399,3 +399,47 @@ def test_grid_larger_than_the_device_is_rejected(m306):
         dec.launch(1, 0)
     assert e.value.code == _lib.MSD_E_CONFIG
     dec.close()
+
+
+def test_tiny_steps_in_one_launch_equal_single_steps(tiny):
+    """n greedy steps in one launch (the next token fed back inside the kernel) give the oracle's
+    tokens, and bit for bit the logits of one launch per step."""
+    params, prompt, w = tiny
+    P = len(prompt)
+    single = Decoder(w, TINY)
+    for p, t in enumerate(prompt):
+        tok, _ = single.step(int(t), p)
+    first = tok
+    sl = []
+    for i in range(32):
+        tok, lg = single.step(tok, P + i)
+        sl.append(lg.cpu().numpy().copy())
+    multi = Decoder(w, TINY)
+    for p, t in enumerate(prompt):
+        multi.step(int(t), p)
+    toks, logits = multi.generate(first, P, 32, all_logits=True)
+    ml = logits.cpu().numpy()
+    rtoks = om.greedy_generate(params, TINY, prompt, 33, prefill="step")
+    assert toks == rtoks[1:]
+    for i in range(32):
+        assert np.array_equal(ml[i], sl[i]), i
+    # launches of several steps chained with single steps: the tags carry on
+    more = multi.generate(toks[-1], P + 32, 8)
+    t2, _ = multi.step(more[-1], P + 40)
+    ref = om.greedy_generate(params, TINY, prompt, 43, prefill="step")
+    assert more == ref[33:41] and t2 == ref[41]
+
+
+def test_306m_whole_generation_in_one_launch(m306):
+    """Config 2's 479 greedy steps (positions 32..510) in a single launch, token-exact."""
+    params, w = m306
+    prompt = make_prompt(32, M306["vocab_size"], seed=1)
+    dec = Decoder(w, M306)
+    for p, t in enumerate(prompt):
+        first, _ = dec.step(int(t), p)
+    toks, logits = dec.generate(first, 32, 479, all_logits=True)
+    rtoks, rlogs = om.greedy_generate(params, M306, prompt, 480, prefill="step", return_logits=True)
+    assert [first] + toks == rtoks
+    lg = logits.cpu().numpy()
+    for i in range(0, 479, 60):
+        np.testing.assert_allclose(lg[i], rlogs[i + 1], atol=ATOL, rtol=RTOL)

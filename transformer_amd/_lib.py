@@ -24,7 +24,8 @@ EXPORTS = ("msd_packed_weight_elems", "msd_workspace_bytes", "msd_default_workgr
            "msd_decode_step", "msd_check_status", "msd_sample_workspace_bytes", "msd_sample_token",
            "msd_prefill_workspace_bytes", "msd_prefill", "msd_prefill_paged", "msd_batch_workspace_bytes",
            "msd_batch_decode_step", "msd_workspace_acquire", "msd_workspace_release",
-           "msd_sample_token_noalloc", "msd_verify_workspace_bytes", "msd_verify")
+           "msd_sample_token_noalloc", "msd_verify_workspace_bytes", "msd_verify",
+           "msd_decode_steps")
 
 
 class MsdConfig(ctypes.Structure):
@@ -79,6 +80,8 @@ def lib():
     L.msd_default_workgroups.restype = I32
     L.msd_decode_step.argtypes = [CP, P, P, P, P, P, I32, P, I32, P, P, U32, P, P, I32, P]
     L.msd_decode_step.restype = I32
+    L.msd_decode_steps.argtypes = [CP, P, P, P, P, P, I32, P, I32, I32, P, P, U32, P, I32, P, I32, P]
+    L.msd_decode_steps.restype = I32
     L.msd_check_status.argtypes = [P, P]
     L.msd_check_status.restype = I32
     L.msd_workspace_acquire.argtypes = [I32, I64, ctypes.POINTER(ctypes.c_void_p)]

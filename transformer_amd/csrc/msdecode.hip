@@ -178,12 +178,14 @@ struct Args {
   const float* rope;
   uint16_t* kv;
   float* logits;
-  int32_t* next_token;
+  int32_t* next_token;   // [2 * nsteps]: per step (argmax, status)
   const int32_t* token_dev;
-  uint32_t* ctrl;   // [0] status, [1] arrival counter, [2..3] argmax key (u64)
+  uint32_t* ctrl;   // [0] status, [1] arrival counter, [2..3] argmax key (u64), [16..47] token words
   uint64_t* xw;     // exchange words, n_layers * x_layer
-  int token, pos;
-  uint32_t epoch;
+  int token, pos;   // input token and position of step 0 (step s runs at pos + s)
+  uint32_t epoch;   // tag of step 0 (step s tags its words epoch + s)
+  int nsteps;       // greedy steps of this launch; step s + 1 feeds step s's argmax
+  int64_t logits_stride;   // floats between the logits of consecutive steps (0: one buffer)
   int H, KV, L, ff, V, ctx;
   int nsplit, cap, NA, GR;   // attention splits, positions per split, attention / row workgroups
   // row workgroups: LDS ring regions (bytes) of the QKV, O, gate/up and down rows, the
@@ -273,6 +275,12 @@ __device__ __forceinline__ void st_tag(uint64_t* p, float v, uint32_t tag) {
 }
 __device__ __forceinline__ uint64_t ld_tag(const uint64_t* p) {
   return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Stores to the step outputs (token, status): written by workgroup 0 at the start of a step
+// and by the last arriver at its end, on different XCDs, so they go through to memory in the
+// order the step imposes instead of waiting in two L2 caches whose write-back order is free.
+__device__ __forceinline__ void put_out(int32_t* p, int32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ uint32_t ld_status(uint32_t* ctrl) {
   return __hip_atomic_load(ctrl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -554,11 +562,27 @@ __device__ __forceinline__ uint64_t* layer_x(const Args& a, int l) { return a.xw
 __device__ __forceinline__ const uint16_t* layer_w(const Args& a, int l) { return a.w + int64_t(l) * a.lay.layer_elems; }
 __device__ __forceinline__ uint16_t* layer_k(const Args& a, int l) { return a.kv + int64_t(l) * 2 * a.KV * a.ctx * kDh; }
 
+// Token words: the last arriver of step s stores (epoch + s | argmax) to kTokReps replicas, which
+// the next step's workgroups poll (a replica per 16 workgroups: fewer pollers per address).
+constexpr int kTokReps = 16;
+__device__ __forceinline__ uint64_t* tok_words(const Args& a) { return reinterpret_cast<uint64_t*>(a.ctrl + 16); }
+// Wait for step s's token (tag epoch + s) on replica `rep`; returns it (0 if the wait ran out).
+__device__ __forceinline__ int poll_token(const Args& a, int s, int rep, int lane, bool& bad) {
+  const uint32_t want = a.epoch + uint32_t(s);
+  const uint64_t* src = tok_words(a) + rep % kTokReps;
+  uint64_t w = ld_tag(src);
+  uint32_t spins = 0;
+  while (!bad && uint32_t(w >> 32) != want) {
+    spin_step(spins, a.ctrl, lane, bad);
+    w = ld_tag(src);
+  }
+  return uint32_t(w >> 32) == want ? int(uint32_t(w)) : 0;
+}
+
 // ---------------------------------------------------------------- row workgroups
 // Shared state of a row workgroup (LDS pointers, row ranges).
 struct RowCtx {
   int wr, lane, wv;
-  uint32_t tag;
   int qp0, qp1, or0, or1, f0, f1, v0, v1;   // QKV pairs, O/down rows, gate/up pairs, vocabulary rows
   int nlog;                                 // logit chunks
   uint8_t* ring;
@@ -567,17 +591,20 @@ struct RowCtx {
   float* xact;    // SwiGLU activation (input of the down rows)
   float* xhd2;    // down output (gathered)
   float* xa;      // gathered attention partials
-  int* ctr;       // [0] worker barrier, [4] ring jobs consumed (worker bumps), [5] ring jobs loaded
+  int* ctr;       // [0] worker barrier, [4] ring jobs consumed (worker bumps), [5] ring jobs loaded,
+                  // [6] the step's input token
   float* red_v;   // argmax per worker wave
   int* red_i;
 };
-enum { kCtrBar = 0, kCtrUsed = 4, kCtrLoaded = 5 };
+enum { kCtrBar = 0, kCtrUsed = 4, kCtrLoaded = 5, kCtrTok = 6 };
 
-// Loader wave of a row workgroup.  Jobs in order: per layer the QKV, O, gate/up and down
-// rows of this workgroup (into their fixed ring regions), then the logit rows in chunks
-// alternating between the two ring halves.  Job j may overwrite its region once the job
-// that last used it has been consumed by all compute waves.
-template <int D, int FF>
+// Loader wave of a row workgroup.  Jobs in order, per step: per layer the QKV, O, gate/up and
+// down rows of this workgroup (into their fixed ring regions), then the logit rows in chunks
+// alternating between the two ring halves.  Job j may overwrite its region once the job that
+// last used it has been consumed by all compute waves (a step's first job: every job of the
+// previous step, whose logit chunks spread over the whole ring).  Job indices run on across the
+// steps of a launch, as do the LDS counters.
+template <int D, int FF, bool MULTI>
 __device__ void row_loader(const Args& a, const RowCtx& c) {
   const Layout& lay = a.lay;
   const int lane = c.lane;
@@ -587,45 +614,51 @@ __device__ void row_loader(const Args& a, const RowCtx& c) {
   Dma<kDmaLogits, MSD_DMA_AUX> dl;
   const int half = a.ring_bytes / 2;
   const int njobs = 4 * a.L + c.nlog;
-  for (int j = 0; j < njobs; ++j) {
-    const uint16_t* src;
-    int64_t bytes;
-    int off, need;
-    if (j < 4 * a.L) {
-      const int l = j / 4, p = j % 4;
-      const uint16_t* w = layer_w(a, l);
-      if (p == 0) { src = w + lay.off_qkv + int64_t(2 * c.qp0) * D; bytes = int64_t(2 * (c.qp1 - c.qp0)) * D * 2; off = a.ring_q; }
-      else if (p == 1) { src = w + lay.off_o + int64_t(c.or0) * D; bytes = int64_t(c.or1 - c.or0) * D * 2; off = a.ring_o; }
-      else if (p == 2) { src = w + lay.off_gu + int64_t(2 * c.f0) * D; bytes = int64_t(2 * (c.f1 - c.f0)) * D * 2; off = a.ring_g; }
-      else { src = w + lay.off_dn + int64_t(c.or0) * FF; bytes = int64_t(c.or1 - c.or0) * FF * 2; off = a.ring_d; }
-      need = l == 0 ? 0 : j - 3;   // job j - 4 (same region, previous layer) consumed
-    } else {
-      const int k = j - 4 * a.L;
-      const int r0 = c.v0 + k * a.log_rows;
-      const int r1 = min(c.v1, r0 + a.log_rows);
-      src = a.outp + int64_t(r0) * D;
-      bytes = int64_t(r1 - r0) * D * 2;
-      off = (k & 1) * half;
-      need = k < 2 ? 4 * a.L : 4 * a.L + k - 1;   // every layer job, or logit chunk k - 2
-    }
-    if (need > 0 && lds_ld(c.ctr + kCtrUsed) < kWavesR * need) lds_wait(c.ctr + kCtrUsed, kWavesR * need, a.ctrl);
-    if (bytes > 0) {
-      if (j < 4 && a.keep > 0) {
-        dma_copy(d0, reinterpret_cast<const uint8_t*>(src), c.ring + off, bytes, lane);
-        d0.drain();
-      } else if (j < 4 * a.keep) {
-        dma_copy(dk, reinterpret_cast<const uint8_t*>(src), c.ring + off, bytes, lane);
-        dk.drain();
-      } else if (j < 4 * a.L) {
-        dma_copy(d, reinterpret_cast<const uint8_t*>(src), c.ring + off, bytes, lane);
-        d.drain();
+  const int nsteps = MULTI ? a.nsteps : 1;
+  for (int st = 0; st < nsteps; ++st) {
+    const int base = st * njobs;
+    for (int j = 0; j < njobs; ++j) {
+      const uint16_t* src;
+      int64_t bytes;
+      int off, need;
+      if (j < 4 * a.L) {
+        const int l = j / 4, p = j % 4;
+        const uint16_t* w = layer_w(a, l);
+        if (p == 0) { src = w + lay.off_qkv + int64_t(2 * c.qp0) * D; bytes = int64_t(2 * (c.qp1 - c.qp0)) * D * 2; off = a.ring_q; }
+        else if (p == 1) { src = w + lay.off_o + int64_t(c.or0) * D; bytes = int64_t(c.or1 - c.or0) * D * 2; off = a.ring_o; }
+        else if (p == 2) { src = w + lay.off_gu + int64_t(2 * c.f0) * D; bytes = int64_t(2 * (c.f1 - c.f0)) * D * 2; off = a.ring_g; }
+        else { src = w + lay.off_dn + int64_t(c.or0) * FF; bytes = int64_t(c.or1 - c.or0) * FF * 2; off = a.ring_d; }
+        // job j - 4 (same region, previous layer) consumed; a step's first layer: the whole
+        // previous step
+        need = l == 0 ? base : base + j - 3;
       } else {
-        dma_copy(dl, reinterpret_cast<const uint8_t*>(src), c.ring + off, bytes, lane);
-        dl.drain();
+        const int k = j - 4 * a.L;
+        const int r0 = c.v0 + k * a.log_rows;
+        const int r1 = min(c.v1, r0 + a.log_rows);
+        src = a.outp + int64_t(r0) * D;
+        bytes = int64_t(r1 - r0) * D * 2;
+        off = (k & 1) * half;
+        need = base + (k < 2 ? 4 * a.L : 4 * a.L + k - 1);   // every layer job, or logit chunk k - 2
       }
+      if (need > 0 && lds_ld(c.ctr + kCtrUsed) < kWavesR * need) lds_wait(c.ctr + kCtrUsed, kWavesR * need, a.ctrl);
+      if (bytes > 0) {
+        if (j < 4 && a.keep > 0) {
+          dma_copy(d0, reinterpret_cast<const uint8_t*>(src), c.ring + off, bytes, lane);
+          d0.drain();
+        } else if (j < 4 * a.keep) {
+          dma_copy(dk, reinterpret_cast<const uint8_t*>(src), c.ring + off, bytes, lane);
+          dk.drain();
+        } else if (j < 4 * a.L) {
+          dma_copy(d, reinterpret_cast<const uint8_t*>(src), c.ring + off, bytes, lane);
+          d.drain();
+        } else {
+          dma_copy(dl, reinterpret_cast<const uint8_t*>(src), c.ring + off, bytes, lane);
+          dl.drain();
+        }
+      }
+      lds_set(c.ctr + kCtrLoaded, base + j + 1, lane);
+      MSD_TRACE_POINT(st == 0 && j < 4 * a.L, j / 4, 28 + (j % 4));
     }
-    lds_set(c.ctr + kCtrLoaded, j + 1, lane);
-    MSD_TRACE_POINT(j < 4 * a.L, j / 4, 28 + (j % 4));
   }
 }
 
@@ -638,7 +671,7 @@ __device__ void row_loader(const Args& a, const RowCtx& c) {
 // stored (so this workgroup's stores never queue behind its own polls) the workers gather
 // the next vector, each an eighth of its words, into LDS.  Workgroup-local barriers are LDS
 // counters among the 8 workers.
-template <int D, int FF, int QPW, int ORW, int GPW>
+template <int D, int FF, int QPW, int ORW, int GPW, bool MULTI>
 __device__ void row_worker(const Args& a, const RowCtx& c, int token) {
   constexpr int NLD = (D + 511) / 512;
   constexpr int NLF = (FF + 511) / 512;
@@ -654,22 +687,7 @@ __device__ void row_worker(const Args& a, const RowCtx& c, int token) {
   const int64_t myrep = int64_t(c.wr % kRep) * lay.x_rep;
   const int natt = a.H * a.nsplit;
   const int nq = c.qp1 - c.qp0, no = c.or1 - c.or0, ng = c.f1 - c.f0;
-  // rotary factors of this wave's QKV pairs (q/k rows), loaded once
-  float cs[QPW], sn[QPW];
-#pragma unroll
-  for (int i = 0; i < QPW; ++i) {
-    cs[i] = 1.f;
-    sn[i] = 0.f;
-    const int rel = wv + kWavesR * i;
-    if (rel < nq) {
-      const int row = 2 * (c.qp0 + rel);
-      if (row / kDh < a.H + a.KV) {
-        const float* rope = a.rope + int64_t(a.pos) * kDh + (row % kDh) / 2;
-        cs[i] = rope[0];
-        sn[i] = rope[kDh / 2];
-      }
-    }
-  }
+  float cs[QPW], sn[QPW];   // rotary factors of this wave's QKV pairs (q/k rows) at the step's position
   // residual stream and RMSNorm scales in the lane layout
   auto load_vec = [&](XV<NLD>& v, const uint16_t* src) {
 #pragma unroll
@@ -680,8 +698,6 @@ __device__ void row_worker(const Args& a, const RowCtx& c, int token) {
     }
   };
   XV<NLD> h, sc;
-  load_vec(h, a.emb + int64_t(token) * D);
-  load_vec(sc, layer_w(a, 0) + lay.off_ln1);
   auto add_res = [&](const float* buf) {   // h += gathered output
     XV<NLD> t;
     load_x(t, buf, D, lane);
@@ -714,260 +730,317 @@ __device__ void row_worker(const Args& a, const RowCtx& c, int token) {
   auto count = [&](int n, int cap) {   // this wave's items among n (items w, w + 8, ...)
     return n > wv ? min(cap, (n - wv + kWavesR - 1) / kWavesR) : 0;
   };
+  const int njobs = 4 * a.L + c.nlog;
+  const int nsteps = MULTI ? a.nsteps : 1;
 
-  for (int l = 0; l < a.L; ++l) {
-    uint64_t* X = layer_x(a, l);
-    uint16_t* kcache = layer_k(a, l);
-    uint16_t* vcache = kcache + int64_t(a.KV) * a.ctx * kDh;
-    // ---- h += down output of the previous layer; x = rmsnorm1(h); QKV rows, RoPE, KV write
-    //      (multi_sm_decode.py:121-180)
-    if (l > 0) {
-      gather_x<kWavesR, HPW, 0, kFirstPoll, D>(layer_x(a, l - 1) + lay.x_hd2 + myrep, D, c.xhd2, c.tag, a.ctrl, wv, lane, bad);
-      bar();
-      add_res(c.xhd2);
-      MSD_TRACE_POINT(wv == 0, l - 1, 6);
-    }
-    weights(4 * l);
-    MSD_TRACE_POINT(wv == 0, l, 16);
-    {
-      XV<NLD> xv;
-      norm(xv);
-      MSD_TRACE_POINT(wv == 0, l, 11);
-      const uint8_t* rows[2 * QPW];
-#pragma unroll
-      for (int i = 0; i < QPW; ++i) {
-        rows[2 * i] = at(a.ring_q, wv + kWavesR * i, nq, 2 * D * 2);
-        rows[2 * i + 1] = rows[2 * i] + D * 2;
-      }
-      float sd[2 * QPW] = {};
-      if (count(nq, QPW) > 0) dot_rows<NLD, 2 * QPW>(rows, xv, D, lane, sd);   // idle waves leave the SIMD to others
-      MSD_TRACE_POINT(wv == 0, l, 14);
-      release();
-      float y[2 * QPW];
-      int ix[2 * QPW];
-#pragma unroll
-      for (int i = 0; i < QPW; ++i) {
-        const int rel = wv + kWavesR * i;
-        const int row = 2 * (c.qp0 + (rel < nq ? rel : 0));
-        const int head = row / kDh;
-        const int rr = row % kDh;
-        const float s0 = sd[2 * i], s1 = sd[2 * i + 1];
-        if (head < a.H + a.KV) {  // q or k rows (i, i+32): rotate-half RoPE (model.py:110-117)
-          y[2 * i] = s0 * cs[i] - s1 * sn[i];
-          y[2 * i + 1] = s0 * sn[i] + s1 * cs[i];
-          ix[2 * i] = head * kDh + rr / 2;
-          ix[2 * i + 1] = ix[2 * i] + kDh / 2;
-        } else {
-          y[2 * i] = s0;
-          y[2 * i + 1] = s1;
-          ix[2 * i] = head * kDh + rr;
-          ix[2 * i + 1] = ix[2 * i] + 1;
-        }
-        if (rel < nq && head >= a.H && lane == 0) {  // K (post-RoPE) or V row of the cache at pos, bf16 (multi_sm_decode.py:179-180)
-          const bool isv = head >= a.H + a.KV;
-          const int kvh = isv ? head - a.H - a.KV : head - a.H;
-          uint16_t* cp = (isv ? vcache : kcache) + (int64_t(kvh) * a.ctx + a.pos) * kDh;
-          cp[ix[2 * i] - head * kDh] = f2bf(y[2 * i]);
-          cp[ix[2 * i + 1] - head * kDh] = f2bf(y[2 * i + 1]);
-        }
-      }
-      store_out<2 * QPW>(X + lay.x_qkv, y, ix, 2 * count(nq, QPW), false, lay.x_rep, c.tag, lane);
-    }
-    load_vec(sc, layer_w(a, l) + lay.off_ln2);   // scale of the next norm
-    bar();   // every QKV output of this workgroup is issued
-    MSD_TRACE_POINT(wv == 0, l, 17);
-    // ---- attention vector (multi_sm_decode.py:243-259): with one split the attention
-    //      workgroups publish each head's normalised output, gathered straight into xatt;
-    //      with several, the (head, split) partials are merged here by log-sum-exp
-    if (a.nsplit == 1) {
-      gather_x<kWavesR, HPW, 0, kAttFirstPoll, D>(X + lay.x_att + myrep, D, c.xatt, c.tag, a.ctrl, wv, lane, bad);
-      MSD_TRACE_POINT(wv == 0, l, 3);
-    } else {
-      gather_x<kWavesR, NKA2, 0, kAttFirstPoll>(X + lay.x_att + myrep, natt * kPart, c.xa, c.tag, a.ctrl, wv, lane, bad);
-      MSD_TRACE_POINT(wv == 0, l, 3);
-      bar();
-      MSD_TRACE_POINT(wv == 0, l, 4);
-      for (int i = wv * 64 + lane; i < D; i += kWavesR * 64) {
-        const int hd = i / kDh, dim = i % kDh;
-        float M = -INFINITY;
-        for (int s = 0; s < a.nsplit; ++s) {
-          const float* ps = c.xa + (hd * a.nsplit + s) * kPart;
-          if (ps[1] > 0.f) M = fmaxf(M, ps[0]);
-        }
-        float num = 0.f, den = 0.f;
-        for (int s = 0; s < a.nsplit; ++s) {
-          const float* ps = c.xa + (hd * a.nsplit + s) * kPart;
-          if (ps[1] > 0.f) {
-            const float wgt = expf(ps[0] - M);
-            num += wgt * ps[2 + dim];
-            den += wgt * ps[1];
+  for (int st = 0; st < nsteps; ++st) {
+    const int pos = a.pos + st;
+    const uint32_t tag = a.epoch + uint32_t(st);
+    const int jb = st * njobs;   // this step's first ring job
+    if (st > 0) {
+      // the input token is the previous step's argmax, published by its last arriver
+      if (wv == 0) {
+        const int t = poll_token(a, st - 1, c.wr, lane, bad);
+        if (lane == 0) {
+          c.ctr[kCtrTok] = t;
+          if (c.wr == 0) {   // step start (as the kernel entry does for step 0)
+            __hip_atomic_store(a.ctrl + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(reinterpret_cast<uint64_t*>(a.ctrl + 2), uint64_t(0), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+            atomicAnd(a.ctrl, ~kStatusBadToken);
+            put_out(a.next_token + 2 * st + 1, int32_t(kStatusUnfinished));
+            __builtin_amdgcn_s_waitcnt(0);
           }
         }
-        c.xatt[lane_major<D>(i)] = den > 0.f ? num / den : 0.f;
       }
+      bar();
+      token = __hip_atomic_load(c.ctr + kCtrTok, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     }
-    bar();
-    MSD_TRACE_POINT(wv == 0, l, 1);
-    // ---- O rows (multi_sm_decode.py:223-232)
-    weights(4 * l + 1);
-    MSD_TRACE_POINT(wv == 0, l, 18);
-    {
-      XV<NLD> xv;
-      load_x(xv, c.xatt, D, lane);
-      const uint8_t* rows[ORW];
-      int ix[ORW];
 #pragma unroll
-      for (int i = 0; i < ORW; ++i) {
-        rows[i] = at(a.ring_o, wv + kWavesR * i, no, D * 2);
-        ix[i] = int(lay.x_hd1) + c.or0 + wv + kWavesR * i;
-      }
-      float y[ORW] = {};
-      if (count(no, ORW) > 0) dot_rows<NLD, ORW>(rows, xv, D, lane, y);
-      release();
-      store_out<ORW>(X, y, ix, count(no, ORW), true, lay.x_rep, c.tag, lane);
-    }
-    bar();
-    MSD_TRACE_POINT(wv == 0, l, 19);
-    // ---- h += O output; x = rmsnorm2(h); gate/up rows + SwiGLU (multi_sm_decode.py:262-289, model.py:159)
-    gather_x<kWavesR, HPW, 0, kFirstPoll, D>(X + lay.x_hd1 + myrep, D, c.xhd1, c.tag, a.ctrl, wv, lane, bad);
-    bar();
-    MSD_TRACE_POINT(wv == 0, l, 2);
-    add_res(c.xhd1);
-    weights(4 * l + 2);
-    MSD_TRACE_POINT(wv == 0, l, 20);
-    MSD_TRACE_WAVE(l, 0);
-    {
-      XV<NLD> xv;
-      norm(xv);
-      MSD_TRACE_POINT(wv == 0, l, 8);
-      MSD_TRACE_WAVE(l, 1);
-      const uint8_t* rows[2 * GPW];
-      int ix[GPW];
-#pragma unroll
-      for (int i = 0; i < GPW; ++i) {
-        rows[2 * i] = at(a.ring_g, wv + kWavesR * i, ng, 2 * D * 2);
-        rows[2 * i + 1] = rows[2 * i] + D * 2;
-        ix[i] = int(lay.x_act) + c.f0 + wv + kWavesR * i;
-      }
-      float gu[2 * GPW] = {};
-      if (count(ng, GPW) > 0) dot_rows<NLD, 2 * GPW>(rows, xv, D, lane, gu);
-      MSD_TRACE_POINT(wv == 0, l, 9);
-      MSD_TRACE_WAVE(l, 2);
-      release();
-      float y[GPW];
-#pragma unroll
-      for (int i = 0; i < GPW; ++i) {
-        const float gt = gu[2 * i], up = gu[2 * i + 1];
-        y[i] = (gt * (1.f / (1.f + expf(-gt)))) * up;
-      }
-      store_out<GPW>(X, y, ix, count(ng, GPW), true, lay.x_rep, c.tag, lane);
-      MSD_TRACE_POINT(wv == 0, l, 10);
-      MSD_TRACE_WAVE(l, 3);
-    }
-    bar();
-    MSD_TRACE_WAVE(l, 4);
-    MSD_TRACE_POINT(wv == 0, l, 21);
-    // ---- act -> LDS; down rows (multi_sm_decode.py:273-291)
-    gather_x<kWavesR, NKF, 0, kFirstPoll, FF>(X + lay.x_act + myrep, a.ff, c.xact, c.tag, a.ctrl, wv, lane, bad);
-    bar();
-    MSD_TRACE_POINT(wv == 0, l, 5);
-    weights(4 * l + 3);
-    MSD_TRACE_POINT(wv == 0, l, 22);
-    {
-      XV<NLF> xv;
-      load_x(xv, c.xact, FF, lane);
-      const uint8_t* rows[ORW];
-      int ix[ORW];
-#pragma unroll
-      for (int i = 0; i < ORW; ++i) {
-        rows[i] = at(a.ring_d, wv + kWavesR * i, no, FF * 2);
-        ix[i] = int(lay.x_hd2) + c.or0 + wv + kWavesR * i;
-      }
-      float y[ORW] = {};
-      if (count(no, ORW) > 0) dot_rows<NLF, ORW>(rows, xv, FF, lane, y);
-      MSD_TRACE_POINT(wv == 0, l, 15);
-      release();
-      store_out<ORW>(X, y, ix, count(no, ORW), true, lay.x_rep, c.tag, lane);
-    }
-    load_vec(sc, l + 1 < a.L ? layer_w(a, l + 1) + lay.off_ln1 : a.lnf);   // scale of the next norm
-    bar();
-    MSD_TRACE_POINT(wv == 0, l, 23);
-  }
-  // ---- h += last down output; x = final rmsnorm(h); tied logits over this workgroup's
-  //      vocabulary rows (multi_sm_decode.py:314-337)
-  gather_x<kWavesR, HPW, 0, kFirstPoll, D>(layer_x(a, a.L - 1) + lay.x_hd2 + myrep, D, c.xhd2, c.tag, a.ctrl, wv, lane, bad);
-  bar();
-  MSD_TRACE_POINT(wv == 0, a.L - 1, 6);
-  add_res(c.xhd2);
-  XV<NLD> xv;
-  norm(xv);
-  float best = -INFINITY;
-  int besti = 0x7fffffff;
-  const int half = a.ring_bytes / 2;
-  constexpr int RB = 4;   // rows per batch of LDS reads
-  for (int k = 0; k < c.nlog; ++k) {
-    weights(4 * a.L + k);
-    const int r0 = c.v0 + k * a.log_rows;
-    const int n = min(c.v1, r0 + a.log_rows) - r0;
-    const uint8_t* base = c.ring + (k & 1) * half;
-    for (int b = wv; b < n; b += kWavesR * RB) {
-      const uint8_t* rows[RB];
-#pragma unroll
-      for (int i = 0; i < RB; ++i) {
-        const int rel = b + kWavesR * i;
-        rows[i] = base + int64_t(rel < n ? rel : 0) * D * 2;
-      }
-      float y[RB];
-      dot_rows<NLD, RB>(rows, xv, D, lane, y);
-#pragma unroll
-      for (int i = 0; i < RB; ++i) {
-        const int rel = b + kWavesR * i;
-        if (rel < n) {
-          if (lane == 0) a.logits[r0 + rel] = y[i];
-          if (y[i] > best) { best = y[i]; besti = r0 + rel; }
+    for (int i = 0; i < QPW; ++i) {
+      cs[i] = 1.f;
+      sn[i] = 0.f;
+      const int rel = wv + kWavesR * i;
+      if (rel < nq) {
+        const int row = 2 * (c.qp0 + rel);
+        if (row / kDh < a.H + a.KV) {
+          const float* rope = a.rope + int64_t(pos) * kDh + (row % kDh) / 2;
+          cs[i] = rope[0];
+          sn[i] = rope[kDh / 2];
         }
       }
     }
-    release();
-  }
-  if (lane == 0) {
-    c.red_v[wv] = best;
-    c.red_i[wv] = besti;
-  }
-  bar();
-  MSD_TRACE_POINT(wv == 0, a.L, 12);
-  if (wv == 0 && lane == 0) {   // argmax: larger value wins, ties -> lower index (np.argmax)
-    float bv = c.red_v[0];
-    int bi = c.red_i[0];
-    for (int w = 1; w < kWavesR; ++w) {
-      const float v = c.red_v[w];
-      const int i = c.red_i[w];
-      if (v > bv || (v == bv && i < bi)) { bv = v; bi = i; }
+    load_vec(h, a.emb + int64_t(token) * D);
+    load_vec(sc, layer_w(a, 0) + lay.off_ln1);
+
+    for (int l = 0; l < a.L; ++l) {
+      uint64_t* X = layer_x(a, l);
+      uint16_t* kcache = layer_k(a, l);
+      uint16_t* vcache = kcache + int64_t(a.KV) * a.ctx * kDh;
+      // ---- h += down output of the previous layer; x = rmsnorm1(h); QKV rows, RoPE, KV write
+      //      (multi_sm_decode.py:121-180)
+      if (l > 0) {
+        gather_x<kWavesR, HPW, 0, kFirstPoll, D>(layer_x(a, l - 1) + lay.x_hd2 + myrep, D, c.xhd2, tag, a.ctrl, wv, lane, bad);
+        bar();
+        add_res(c.xhd2);
+        MSD_TRACE_POINT(wv == 0, l - 1, 6);
+      }
+      weights(jb + 4 * l);
+      MSD_TRACE_POINT(wv == 0, l, 16);
+      {
+        XV<NLD> xv;
+        norm(xv);
+        MSD_TRACE_POINT(wv == 0, l, 11);
+        const uint8_t* rows[2 * QPW];
+#pragma unroll
+        for (int i = 0; i < QPW; ++i) {
+          rows[2 * i] = at(a.ring_q, wv + kWavesR * i, nq, 2 * D * 2);
+          rows[2 * i + 1] = rows[2 * i] + D * 2;
+        }
+        float sd[2 * QPW] = {};
+        if (count(nq, QPW) > 0) dot_rows<NLD, 2 * QPW>(rows, xv, D, lane, sd);   // idle waves leave the SIMD to others
+        MSD_TRACE_POINT(wv == 0, l, 14);
+        release();
+        float y[2 * QPW];
+        int ix[2 * QPW];
+#pragma unroll
+        for (int i = 0; i < QPW; ++i) {
+          const int rel = wv + kWavesR * i;
+          const int row = 2 * (c.qp0 + (rel < nq ? rel : 0));
+          const int head = row / kDh;
+          const int rr = row % kDh;
+          const float s0 = sd[2 * i], s1 = sd[2 * i + 1];
+          if (head < a.H + a.KV) {  // q or k rows (i, i+32): rotate-half RoPE (model.py:110-117)
+            y[2 * i] = s0 * cs[i] - s1 * sn[i];
+            y[2 * i + 1] = s0 * sn[i] + s1 * cs[i];
+            ix[2 * i] = head * kDh + rr / 2;
+            ix[2 * i + 1] = ix[2 * i] + kDh / 2;
+          } else {
+            y[2 * i] = s0;
+            y[2 * i + 1] = s1;
+            ix[2 * i] = head * kDh + rr;
+            ix[2 * i + 1] = ix[2 * i] + 1;
+          }
+          if (rel < nq && head >= a.H && lane == 0) {  // K (post-RoPE) or V row of the cache at pos, bf16 (multi_sm_decode.py:179-180)
+            const bool isv = head >= a.H + a.KV;
+            const int kvh = isv ? head - a.H - a.KV : head - a.H;
+            uint16_t* cp = (isv ? vcache : kcache) + (int64_t(kvh) * a.ctx + pos) * kDh;
+            if constexpr (MULTI) {
+              // agent-scope stores write through to memory: a later step of the same launch
+              // reads the row from another workgroup (on another XCD) without a cache flush
+              __hip_atomic_store(cp + (ix[2 * i] - head * kDh), f2bf(y[2 * i]), __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT);
+              __hip_atomic_store(cp + (ix[2 * i + 1] - head * kDh), f2bf(y[2 * i + 1]), __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT);
+            } else {   // read by later launches only (the launch boundary orders them)
+              cp[ix[2 * i] - head * kDh] = f2bf(y[2 * i]);
+              cp[ix[2 * i + 1] - head * kDh] = f2bf(y[2 * i + 1]);
+            }
+          }
+        }
+        store_out<2 * QPW>(X + lay.x_qkv, y, ix, 2 * count(nq, QPW), false, lay.x_rep, tag, lane);
+      }
+      load_vec(sc, layer_w(a, l) + lay.off_ln2);   // scale of the next norm
+      bar();   // every QKV output of this workgroup is issued
+      MSD_TRACE_POINT(wv == 0, l, 17);
+      // ---- attention vector (multi_sm_decode.py:243-259): with one split the attention
+      //      workgroups publish each head's normalised output, gathered straight into xatt;
+      //      with several, the (head, split) partials are merged here by log-sum-exp
+      if (a.nsplit == 1) {
+        gather_x<kWavesR, HPW, 0, kAttFirstPoll, D>(X + lay.x_att + myrep, D, c.xatt, tag, a.ctrl, wv, lane, bad);
+        MSD_TRACE_POINT(wv == 0, l, 3);
+      } else {
+        gather_x<kWavesR, NKA2, 0, kAttFirstPoll>(X + lay.x_att + myrep, natt * kPart, c.xa, tag, a.ctrl, wv, lane, bad);
+        MSD_TRACE_POINT(wv == 0, l, 3);
+        bar();
+        MSD_TRACE_POINT(wv == 0, l, 4);
+        for (int i = wv * 64 + lane; i < D; i += kWavesR * 64) {
+          const int hd = i / kDh, dim = i % kDh;
+          float M = -INFINITY;
+          for (int s = 0; s < a.nsplit; ++s) {
+            const float* ps = c.xa + (hd * a.nsplit + s) * kPart;
+            if (ps[1] > 0.f) M = fmaxf(M, ps[0]);
+          }
+          float num = 0.f, den = 0.f;
+          for (int s = 0; s < a.nsplit; ++s) {
+            const float* ps = c.xa + (hd * a.nsplit + s) * kPart;
+            if (ps[1] > 0.f) {
+              const float wgt = expf(ps[0] - M);
+              num += wgt * ps[2 + dim];
+              den += wgt * ps[1];
+            }
+          }
+          c.xatt[lane_major<D>(i)] = den > 0.f ? num / den : 0.f;
+        }
+      }
+      bar();
+      MSD_TRACE_POINT(wv == 0, l, 1);
+      // ---- O rows (multi_sm_decode.py:223-232)
+      weights(jb + 4 * l + 1);
+      MSD_TRACE_POINT(wv == 0, l, 18);
+      {
+        XV<NLD> xv;
+        load_x(xv, c.xatt, D, lane);
+        const uint8_t* rows[ORW];
+        int ix[ORW];
+#pragma unroll
+        for (int i = 0; i < ORW; ++i) {
+          rows[i] = at(a.ring_o, wv + kWavesR * i, no, D * 2);
+          ix[i] = int(lay.x_hd1) + c.or0 + wv + kWavesR * i;
+        }
+        float y[ORW] = {};
+        if (count(no, ORW) > 0) dot_rows<NLD, ORW>(rows, xv, D, lane, y);
+        release();
+        store_out<ORW>(X, y, ix, count(no, ORW), true, lay.x_rep, tag, lane);
+      }
+      bar();
+      MSD_TRACE_POINT(wv == 0, l, 19);
+      // ---- h += O output; x = rmsnorm2(h); gate/up rows + SwiGLU (multi_sm_decode.py:262-289, model.py:159)
+      gather_x<kWavesR, HPW, 0, kFirstPoll, D>(X + lay.x_hd1 + myrep, D, c.xhd1, tag, a.ctrl, wv, lane, bad);
+      bar();
+      MSD_TRACE_POINT(wv == 0, l, 2);
+      add_res(c.xhd1);
+      weights(jb + 4 * l + 2);
+      MSD_TRACE_POINT(wv == 0, l, 20);
+      MSD_TRACE_WAVE(l, 0);
+      {
+        XV<NLD> xv;
+        norm(xv);
+        MSD_TRACE_POINT(wv == 0, l, 8);
+        MSD_TRACE_WAVE(l, 1);
+        const uint8_t* rows[2 * GPW];
+        int ix[GPW];
+#pragma unroll
+        for (int i = 0; i < GPW; ++i) {
+          rows[2 * i] = at(a.ring_g, wv + kWavesR * i, ng, 2 * D * 2);
+          rows[2 * i + 1] = rows[2 * i] + D * 2;
+          ix[i] = int(lay.x_act) + c.f0 + wv + kWavesR * i;
+        }
+        float gu[2 * GPW] = {};
+        if (count(ng, GPW) > 0) dot_rows<NLD, 2 * GPW>(rows, xv, D, lane, gu);
+        MSD_TRACE_POINT(wv == 0, l, 9);
+        MSD_TRACE_WAVE(l, 2);
+        release();
+        float y[GPW];
+#pragma unroll
+        for (int i = 0; i < GPW; ++i) {
+          const float gt = gu[2 * i], up = gu[2 * i + 1];
+          y[i] = (gt * (1.f / (1.f + expf(-gt)))) * up;
+        }
+        store_out<GPW>(X, y, ix, count(ng, GPW), true, lay.x_rep, tag, lane);
+        MSD_TRACE_POINT(wv == 0, l, 10);
+        MSD_TRACE_WAVE(l, 3);
+      }
+      bar();
+      MSD_TRACE_WAVE(l, 4);
+      MSD_TRACE_POINT(wv == 0, l, 21);
+      // ---- act -> LDS; down rows (multi_sm_decode.py:273-291)
+      gather_x<kWavesR, NKF, 0, kFirstPoll, FF>(X + lay.x_act + myrep, a.ff, c.xact, tag, a.ctrl, wv, lane, bad);
+      bar();
+      MSD_TRACE_POINT(wv == 0, l, 5);
+      weights(jb + 4 * l + 3);
+      MSD_TRACE_POINT(wv == 0, l, 22);
+      {
+        XV<NLF> xv;
+        load_x(xv, c.xact, FF, lane);
+        const uint8_t* rows[ORW];
+        int ix[ORW];
+#pragma unroll
+        for (int i = 0; i < ORW; ++i) {
+          rows[i] = at(a.ring_d, wv + kWavesR * i, no, FF * 2);
+          ix[i] = int(lay.x_hd2) + c.or0 + wv + kWavesR * i;
+        }
+        float y[ORW] = {};
+        if (count(no, ORW) > 0) dot_rows<NLF, ORW>(rows, xv, FF, lane, y);
+        MSD_TRACE_POINT(wv == 0, l, 15);
+        release();
+        store_out<ORW>(X, y, ix, count(no, ORW), true, lay.x_rep, tag, lane);
+      }
+      load_vec(sc, l + 1 < a.L ? layer_w(a, l + 1) + lay.off_ln1 : a.lnf);   // scale of the next norm
+      bar();
+      MSD_TRACE_POINT(wv == 0, l, 23);
     }
-    uint64_t* keyp = reinterpret_cast<uint64_t*>(a.ctrl + 2);
-    if (bi != 0x7fffffff)
-      __hip_atomic_fetch_max(keyp, argmax_key(bv, bi), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    // the max above completes before the arrival below is issued
-    __builtin_amdgcn_s_waitcnt(0);
-    // The counter and the key were reset by workgroup 0 at the start of this step (before
-    // any of its outputs, which every arrival here depends on), so exactly one arrival sees
-    // GR - 1, whatever the counter held before the step.
-    const uint32_t old = __hip_atomic_fetch_add(a.ctrl + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (old == uint32_t(a.GR - 1)) {   // last arriver publishes the token and the status
-      const uint64_t key = __hip_atomic_load(keyp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      a.next_token[0] = int32_t(0xffffffffu - uint32_t(key & 0xffffffffu));
-      a.next_token[1] = int32_t(ld_status(a.ctrl));
+    // ---- h += last down output; x = final rmsnorm(h); tied logits over this workgroup's
+    //      vocabulary rows (multi_sm_decode.py:314-337)
+    gather_x<kWavesR, HPW, 0, kFirstPoll, D>(layer_x(a, a.L - 1) + lay.x_hd2 + myrep, D, c.xhd2, tag, a.ctrl, wv, lane, bad);
+    bar();
+    MSD_TRACE_POINT(wv == 0, a.L - 1, 6);
+    add_res(c.xhd2);
+    XV<NLD> xv;
+    norm(xv);
+    float best = -INFINITY;
+    int besti = 0x7fffffff;
+    const int half = a.ring_bytes / 2;
+    constexpr int RB = 4;   // rows per batch of LDS reads
+    for (int k = 0; k < c.nlog; ++k) {
+      weights(jb + 4 * a.L + k);
+      const int r0 = c.v0 + k * a.log_rows;
+      const int n = min(c.v1, r0 + a.log_rows) - r0;
+      const uint8_t* base = c.ring + (k & 1) * half;
+      for (int b = wv; b < n; b += kWavesR * RB) {
+        const uint8_t* rows[RB];
+#pragma unroll
+        for (int i = 0; i < RB; ++i) {
+          const int rel = b + kWavesR * i;
+          rows[i] = base + int64_t(rel < n ? rel : 0) * D * 2;
+        }
+        float y[RB];
+        dot_rows<NLD, RB>(rows, xv, D, lane, y);
+#pragma unroll
+        for (int i = 0; i < RB; ++i) {
+          const int rel = b + kWavesR * i;
+          if (rel < n) {
+            if (lane == 0) a.logits[st * a.logits_stride + r0 + rel] = y[i];
+            if (y[i] > best) { best = y[i]; besti = r0 + rel; }
+          }
+        }
+      }
+      release();
     }
-  }
+    if (lane == 0) {
+      c.red_v[wv] = best;
+      c.red_i[wv] = besti;
+    }
+    // every store of this wave (cache rows, logits) completes before the arrival below, so the
+    // next step of the launch, which starts after the last arrival, sees them
+    if constexpr (MULTI) __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    bar();
+    MSD_TRACE_POINT(wv == 0, a.L, 12);
+    if (wv == 0 && lane == 0) {   // argmax: larger value wins, ties -> lower index (np.argmax)
+      float bv = c.red_v[0];
+      int bi = c.red_i[0];
+      for (int w = 1; w < kWavesR; ++w) {
+        const float v = c.red_v[w];
+        const int i = c.red_i[w];
+        if (v > bv || (v == bv && i < bi)) { bv = v; bi = i; }
+      }
+      uint64_t* keyp = reinterpret_cast<uint64_t*>(a.ctrl + 2);
+      if (bi != 0x7fffffff)
+        __hip_atomic_fetch_max(keyp, argmax_key(bv, bi), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      // the max above completes before the arrival below is issued
+      __builtin_amdgcn_s_waitcnt(0);
+      // The counter and the key were reset by workgroup 0 at the start of this step (before
+      // any of its outputs, which every arrival here depends on), so exactly one arrival sees
+      // GR - 1, whatever the counter held before the step.
+      const uint32_t old = __hip_atomic_fetch_add(a.ctrl + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (old == uint32_t(a.GR - 1)) {   // last arriver publishes the token and the status
+        const uint64_t key = __hip_atomic_load(keyp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const uint32_t tok = 0xffffffffu - uint32_t(key & 0xffffffffu);
+        put_out(a.next_token + 2 * st, int32_t(tok));
+        put_out(a.next_token + 2 * st + 1, int32_t(ld_status(a.ctrl)));
+        if (MULTI && st + 1 < nsteps)
+          for (int r = 0; r < kTokReps; ++r) st_tag(tok_words(a) + r, __uint_as_float(tok), tag);
+      }
+    }
+  }   // steps
 }
 
 // ---------------------------------------------------------------- attention workgroups
 // One query head h and one split s of the context: cached positions [lo, lo + cap) below
 // pos, plus the current position when it falls in the split (multi_sm_decode.py:182-221).
 struct AttCtx {
-  int h, g, lo, ncached, lane, wv;
+  int h, g, split, item, lane, wv;
   bool has_cur;
-  uint32_t tag;
   int64_t part;     // word offset of this head's output (one split) or (head, split)'s partials
   uint8_t* K;       // cap rows of kKRowB bytes (bf16 K, post-RoPE)
   uint8_t* V;       // cap rows of kVRowB bytes
@@ -983,33 +1056,60 @@ struct AttCtx {
 // finished with the previous layer's rows, DMA this split's cached K rows (9 slots of
 // 16 bytes per row; the 9th is padding) and V rows (8 slots) into LDS.
 template <class DMA>
-__device__ __forceinline__ void att_copy(DMA& d, const Args& a, const AttCtx& c, int l) {
+__device__ __forceinline__ void att_copy(DMA& d, const Args& a, const AttCtx& c, int l, int lo, int ncached) {
   const int lane = c.lane;
-  const uint16_t* kc = layer_k(a, l) + (int64_t(c.g) * a.ctx + c.lo) * kDh;
+  const uint16_t* kc = layer_k(a, l) + (int64_t(c.g) * a.ctx + lo) * kDh;
   const uint16_t* vc = kc + int64_t(a.KV) * a.ctx * kDh;
-  const int nk = cdiv(c.ncached * 9, 64);
+  const int nk = cdiv(ncached * 9, 64);
   for (int t = 0; t < nk; ++t) {
     const int i = 64 * t + lane;
-    const int r = min(i / 9, c.ncached - 1), p = min(i % 9, 7);
+    const int r = min(i / 9, ncached - 1), p = min(i % 9, 7);
     d.issue(kc + r * kDh + p * 8, c.K + t * 1024);
   }
-  const int nv = cdiv(c.ncached, 8);
+  const int nv = cdiv(ncached, 8);
   for (int t = 0; t < nv; ++t) {
     const int i = 64 * t + lane;
-    const int r = min(i / 8, c.ncached - 1), p = i % 8;
+    const int r = min(i / 8, ncached - 1), p = i % 8;
     d.issue(vc + r * kDh + p * 8, c.V + t * 1024);
   }
   d.drain();
 }
 
+// This workgroup's cached positions at position pos: [0, pos) is cut into nsplit equal ranges
+// (at most cap each); the last split also takes the current position.
+__device__ __forceinline__ void att_range(const Args& a, const AttCtx& c, int pos, int& lo, int& ncached) {
+  const int chunk = cdiv(pos, a.nsplit);
+  lo = c.split * chunk;
+  ncached = max(0, min(pos - lo, chunk));
+}
+
+// Device-scope DMA policy for the cached rows when a launch runs several steps: rows written by
+// an earlier step of the same launch are then read from memory, not from a cache.
+constexpr int kAuxDevice = 16;
+
+template <bool MULTI>
 __device__ void att_loader(const Args& a, const AttCtx& c) {
   const int lane = c.lane;
   Dma<kDmaKV> d;
-  for (int l = 0; l < a.L; ++l) {
-    if (l > 0) lds_wait(c.ctr + 2, kWavesA * l, a.ctrl);
-    if (c.ncached > 0) att_copy(d, a, c, l);
-    lds_set(c.ctr + 1, l + 1, lane);
-    MSD_TRACE_POINT(true, l, 28);
+  Dma<kDmaKV, kAuxDevice> dd;
+  bool bad = false;
+  const int nsteps = MULTI ? a.nsteps : 1;
+  for (int st = 0; st < nsteps; ++st) {
+    int lo, ncached;
+    att_range(a, c, a.pos + st, lo, ncached);
+    // the previous step's cache rows are complete once its token is published (every row
+    // workgroup waits for its stores before arriving)
+    if (st > 0) poll_token(a, st - 1, c.item, lane, bad);
+    for (int l = 0; l < a.L; ++l) {
+      const int gl = st * a.L + l;   // layers run on across the steps of a launch
+      if (gl > 0) lds_wait(c.ctr + 2, kWavesA * gl, a.ctrl);
+      if (ncached > 0) {
+        if (MULTI) att_copy(dd, a, c, l, lo, ncached);
+        else att_copy(d, a, c, l, lo, ncached);
+      }
+      lds_set(c.ctr + 1, gl + 1, lane);
+      MSD_TRACE_POINT(true, l, 28);
+    }
   }
 }
 
@@ -1061,6 +1161,7 @@ __device__ __forceinline__ bf16x8 as_bf16x8(uint4 u) { return __builtin_bit_cast
 // others, and every wave merges the blocks and the current position by log-sum-exp and
 // stores one replica: with one split the normalised head output (the row workgroups'
 // merge, multi_sm_decode.py:243-259, done here), else (max, sum, unnormalised output).
+template <bool MULTI>
 __device__ void att_waves(const Args& a, const AttCtx& c) {
   const int lane = c.lane, wv = c.wv;
   const Layout& lay = a.lay;
@@ -1069,13 +1170,19 @@ __device__ void att_waves(const Args& a, const AttCtx& c) {
   const int m16 = lane & 15, kb = lane >> 4;
   uint16_t* apw = c.apw + wv * 3 * kDh;
   float* pw = c.pw + wv * kDh;
+  const int nsteps = MULTI ? a.nsteps : 1;
+  for (int st = 0; st < nsteps; ++st) {
+  int lo, ncached;
+  att_range(a, c, a.pos + st, lo, ncached);
+  const uint32_t tag = a.epoch + uint32_t(st);
   for (int l = 0; l < a.L; ++l) {
+    const int gl = st * a.L + l;   // layers run on across the steps of a launch
     uint64_t* X = layer_x(a, l);
-    float* ow = c.ow + (l & 1) * kWavesA * kDh;   // double-buffered: a wave may start the next
-    float* mw = c.mw + (l & 1) * kWavesA;         // layer while another still merges this one
-    float* lw = c.lw + (l & 1) * kWavesA;
+    float* ow = c.ow + (gl & 1) * kWavesA * kDh;   // double-buffered: a wave may start the next
+    float* mw = c.mw + (gl & 1) * kWavesA;         // layer while another still merges this one
+    float* lw = c.lw + (gl & 1) * kWavesA;
     float qv[1];
-    poll_words<1, 1>(X + lay.x_qkv + c.h * kDh, kDh, c.tag, qv, a.ctrl, 0, lane, bad);
+    poll_words<1, 1>(X + lay.x_qkv + c.h * kDh, kDh, tag, qv, a.ctrl, 0, lane, bad);
     MSD_TRACE_POINT(wv == 0, l, 24);
     MSD_TRACE_WAVE(l, 0);
     {   // q = hi + mid + lo exactly, three bf16 parts taken by truncation (each holds the next
@@ -1093,24 +1200,24 @@ __device__ void att_waves(const Args& a, const AttCtx& c) {
     // new k and v of the KV head: first loads now (they land during the block work), the
     // rest of the poll after it
     const uint64_t* kvsrc[2] = {X + lay.x_qkv + (a.H + c.g) * kDh + lane, X + lay.x_qkv + (a.H + a.KV + c.g) * kDh + lane};
-    uint64_t kvw[2] = {uint64_t(c.tag) << 32, uint64_t(c.tag) << 32};
+    uint64_t kvw[2] = {uint64_t(tag) << 32, uint64_t(tag) << 32};
     if (c.has_cur) {
       kvw[0] = ld_tag(kvsrc[0]);
       kvw[1] = ld_tag(kvsrc[1]);
     }
-    lds_wait(c.ctr + 1, l + 1, a.ctrl);   // cached rows of layer l are in LDS
+    lds_wait(c.ctr + 1, gl + 1, a.ctrl);   // cached rows of layer l are in LDS
     MSD_TRACE_POINT(wv == 0, l, 25);
     MSD_TRACE_WAVE(l, 1);
     // block of this wave: tiles [t0, t1) of 16 cached positions, the tiles split evenly over
     // the waves (at most 4 each: ncached <= 512); waves w and w + 4 share a SIMD, and the
     // even split keeps every SIMD's tile count within one of the others'
     int t0, t1;
-    split(cdiv(c.ncached, 16), kWavesA, wv, t0, t1);
+    split(cdiv(ncached, 16), kWavesA, wv, t0, t1);
     float m = -INFINITY, lsum = 0.f;
     float o[4] = {0.f, 0.f, 0.f, 0.f};
     const int r0 = 16 * t0;
     if (t1 > t0) {
-      const int np = min(16 * (t1 - t0), c.ncached - r0);
+      const int np = min(16 * (t1 - t0), ncached - r0);
       // q parts in the A layout: lane row m16 < 3 holds part m16 of dims 32 ch + 8 kb .. + 8
       __builtin_amdgcn_s_waitcnt(0xc07f);
       __builtin_amdgcn_wave_barrier();
@@ -1125,7 +1232,7 @@ __device__ void att_waves(const Args& a, const AttCtx& c) {
       uint4 kk[4][2];
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
-        const int row = min(r0 + 16 * t + m16, c.ncached - 1);
+        const int row = min(r0 + 16 * t + m16, ncached - 1);
         const uint8_t* kr = c.K + row * kKRowB + 16 * kb;
         kk[t][0] = *reinterpret_cast<const uint4*>(kr);
         kk[t][1] = *reinterpret_cast<const uint4*>(kr + 64);
@@ -1159,7 +1266,7 @@ __device__ void att_waves(const Args& a, const AttCtx& c) {
       // rarely needs another round trip
 #pragma unroll
       for (int i = 0; i < 2; ++i)
-        if (uint32_t(kvw[i] >> 32) != c.tag) kvw[i] = ld_tag(kvsrc[i]);
+        if (uint32_t(kvw[i] >> 32) != tag) kvw[i] = ld_tag(kvsrc[i]);
       __builtin_amdgcn_s_waitcnt(0xc07f);
       __builtin_amdgcn_wave_barrier();
       const int g = kb, dq = m16;
@@ -1215,7 +1322,7 @@ __device__ void att_waves(const Args& a, const AttCtx& c) {
         ok = true;
 #pragma unroll
         for (int i = 0; i < 2; ++i)
-          if (uint32_t(kvw[i] >> 32) != c.tag) {
+          if (uint32_t(kvw[i] >> 32) != tag) {
             ok = false;
             kvw[i] = ld_tag(kvsrc[i]);
           }
@@ -1249,28 +1356,30 @@ __device__ void att_waves(const Args& a, const AttCtx& c) {
       }
       if (a.nsplit == 1) {
         const float y = Ls > 0.f ? O * (1.f / Ls) : 0.f;
-        for (int r = wv; r < kRep; r += kWavesA) st_tag(X + lay.x_att + c.part + r * lay.x_rep + lane, y, c.tag);
+        for (int r = wv; r < kRep; r += kWavesA) st_tag(X + lay.x_att + c.part + r * lay.x_rep + lane, y, tag);
       } else {
         for (int r = wv; r < kRep; r += kWavesA) {   // replicas wv, wv + 8, ...
           uint64_t* dst = X + lay.x_att + c.part + r * lay.x_rep;
-          st_tag(dst + 2 + lane, O, c.tag);
-          if (lane < 2) st_tag(dst + lane, lane == 0 ? M : Ls, c.tag);
+          st_tag(dst + 2 + lane, O, tag);
+          if (lane < 2) st_tag(dst + lane, lane == 0 ? M : Ls, tag);
         }
       }
       MSD_TRACE_POINT(wv == 0, l, 27);
       MSD_TRACE_WAVE(l, 6);
     }
   }
+  }   // steps
 }
 
 // ---------------------------------------------------------------- kernel
-template <int D, int FF, int QPW, int ORW, int GPW>
+// MULTI: several greedy steps per launch (a.nsteps); otherwise one step, without the stores and
+// waits only the steps of one launch need of each other.
+template <int D, int FF, int QPW, int ORW, int GPW, bool MULTI>
 __global__ __launch_bounds__(kThreadsWG, 1) void decode_step_kernel(Args a) {
   extern __shared__ __align__(16) uint8_t smem[];
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform
   const int wg = blockIdx.x;
-  const uint32_t tag = a.epoch;
 
   if (wg >= a.GR) {   // ------------------------------------------ attention workgroup
     const int i = wg - a.GR;
@@ -1278,18 +1387,13 @@ __global__ __launch_bounds__(kThreadsWG, 1) void decode_step_kernel(Args a) {
     int item = i;
     if (a.NA % 8 == 0 && a.GR % 8 == 0) item = (i % 8) * (a.NA / 8) + i / 8;
     AttCtx c;
+    c.item = item;
     c.h = item / a.nsplit;
-    const int s = item % a.nsplit;
+    c.split = item % a.nsplit;
     c.g = c.h / (a.H / a.KV);
-    // the cached positions [0, pos) are cut into nsplit equal ranges (at most cap each); the
-    // last split also takes the current position
-    const int chunk = cdiv(a.pos, a.nsplit);
-    c.lo = s * chunk;
-    c.ncached = max(0, min(a.pos - c.lo, chunk));
-    c.has_cur = s == a.nsplit - 1;
+    c.has_cur = c.split == a.nsplit - 1;
     c.lane = lane;
     c.wv = wv;
-    c.tag = tag;
     c.part = a.nsplit == 1 ? int64_t(c.h) * kDh : int64_t(item) * kPart;
     c.K = smem;
     c.V = c.K + cdiv(a.cap * 9, 64) * 1024;
@@ -1301,8 +1405,8 @@ __global__ __launch_bounds__(kThreadsWG, 1) void decode_step_kernel(Args a) {
     c.ctr = reinterpret_cast<int*>(c.lw + 2 * kWavesA);
     if (threadIdx.x < 4) c.ctr[threadIdx.x] = 0;
     __syncthreads();   // the only workgroup barrier; the roles below meet on LDS counters
-    if (wv == kLoader) att_loader(a, c);
-    else att_waves(a, c);
+    if (wv == kLoader) att_loader<MULTI>(a, c);
+    else att_waves<MULTI>(a, c);
     return;
   }
 
@@ -1311,7 +1415,6 @@ __global__ __launch_bounds__(kThreadsWG, 1) void decode_step_kernel(Args a) {
   c.wr = wg;
   c.lane = lane;
   c.wv = wv;
-  c.tag = tag;
   const int nqkv = (a.H + 2 * a.KV) * kDh;
   split(nqkv / 2, a.GR, wg, c.qp0, c.qp1);
   split(D, a.GR, wg, c.or0, c.or1);
@@ -1342,13 +1445,13 @@ __global__ __launch_bounds__(kThreadsWG, 1) void decode_step_kernel(Args a) {
                        __HIP_MEMORY_SCOPE_AGENT);
     if (bad_token) atomicOr(a.ctrl, kStatusBadToken);
     else atomicAnd(a.ctrl, ~kStatusBadToken);
-    a.next_token[1] = int32_t(kStatusUnfinished);
+    put_out(a.next_token + 1, int32_t(kStatusUnfinished));
     __builtin_amdgcn_s_waitcnt(0);
   }
   __syncthreads();   // the only workgroup barrier; the roles below meet on LDS counters
 
-  if (wv == kLoader) row_loader<D, FF>(a, c);
-  else row_worker<D, FF, QPW, ORW, GPW>(a, c, token);
+  if (wv == kLoader) row_loader<D, FF, MULTI>(a, c);
+  else row_worker<D, FF, QPW, ORW, GPW, MULTI>(a, c, token);
 }
 
 // ---------------------------------------------------------------- host side
@@ -1460,10 +1563,10 @@ static int resident_capacity(const void* fn, size_t lds) {
   return cus * per_cu;
 }
 
-template <int D, int FF, int QPW, int ORW, int GPW>
+template <int D, int FF, int QPW, int ORW, int GPW, bool MULTI>
 static hipError_t launch_t(const Args& a, int grid, size_t lds, hipStream_t s, bool* not_resident) {
   static size_t attr_lds = 0;
-  const void* fn = reinterpret_cast<const void*>(&decode_step_kernel<D, FF, QPW, ORW, GPW>);
+  const void* fn = reinterpret_cast<const void*>(&decode_step_kernel<D, FF, QPW, ORW, GPW, MULTI>);
   if (attr_lds < lds) {
     hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
     if (e != hipSuccess) return e;
@@ -1475,7 +1578,7 @@ static hipError_t launch_t(const Args& a, int grid, size_t lds, hipStream_t s, b
     *not_resident = true;
     return hipSuccess;
   }
-  hipLaunchKernelGGL((decode_step_kernel<D, FF, QPW, ORW, GPW>), dim3(grid), dim3(kThreadsWG), lds, s, a);
+  hipLaunchKernelGGL((decode_step_kernel<D, FF, QPW, ORW, GPW, MULTI>), dim3(grid), dim3(kThreadsWG), lds, s, a);
   return hipGetLastError();
 }
 
@@ -1486,8 +1589,10 @@ static bool plan_instantiated(const msd_config* c, const Plan& p) {
 }
 
 static hipError_t launch(const Args& a, int d, int ff, int grid, size_t lds, hipStream_t s, bool* not_resident) {
-#define MSD_SHAPE_LAUNCH(D, FF, Q, O, G) \
-  if (d == D && ff == FF) return launch_t<D, FF, Q, O, G>(a, grid, lds, s, not_resident);
+#define MSD_SHAPE_LAUNCH(D, FF, Q, O, G)                                                     \
+  if (d == D && ff == FF)                                                                    \
+    return a.nsteps > 1 ? launch_t<D, FF, Q, O, G, true>(a, grid, lds, s, not_resident)      \
+                        : launch_t<D, FF, Q, O, G, false>(a, grid, lds, s, not_resident);
   MSD_SHAPES(MSD_SHAPE_LAUNCH)
 #undef MSD_SHAPE_LAUNCH
   return hipErrorInvalidValue;
@@ -1517,20 +1622,20 @@ extern "C" int32_t msd_default_workgroups(int32_t device) {
   return n;
 }
 
-extern "C" int32_t msd_decode_step(const msd_config* cfg, const void* token_emb, const void* output_proj,
-                                   const void* packed_w, const void* lnf_s, const float* rope, int32_t token_id,
-                                   const int32_t* token_dev, int32_t pos, void* kv, void* workspace,
-                                   uint32_t epoch, float* logits, int32_t* next_token,
-                                   int32_t n_workgroups, void* stream) {
+static int32_t decode_impl(const msd_config* cfg, const void* token_emb, const void* output_proj,
+                           const void* packed_w, const void* lnf_s, const float* rope, int32_t token_id,
+                           const int32_t* token_dev, int32_t pos, int32_t n_steps, void* kv, void* workspace,
+                           uint32_t epoch, float* logits, int64_t logits_stride, int32_t* next_token,
+                           int32_t n_workgroups, hipStream_t stream) {
   Plan p;
   if (!config_ok(cfg)) return MSD_E_CONFIG;
   if (n_workgroups <= 0 || n_workgroups > 4096) return MSD_E_ARG;
   if (!make_plan(cfg, n_workgroups, &p) || !plan_instantiated(cfg, p)) return MSD_E_CONFIG;
   if (!token_emb || !output_proj || !packed_w || !lnf_s || !rope || !kv || !workspace || !logits || !next_token)
     return MSD_E_ARG;
-  if (pos < 0 || pos >= cfg->context_len) return MSD_E_ARG;
+  if (n_steps <= 0 || pos < 0 || int64_t(pos) + n_steps > cfg->context_len) return MSD_E_ARG;
   if (!token_dev && (token_id < 0 || token_id >= cfg->vocab_size)) return MSD_E_ARG;
-  if (epoch == 0) return MSD_E_ARG;
+  if (epoch == 0 || uint64_t(epoch) + uint64_t(n_steps - 1) > 0xffffffffull) return MSD_E_ARG;
   const uintptr_t al = reinterpret_cast<uintptr_t>(token_emb) | reinterpret_cast<uintptr_t>(packed_w) |
                        reinterpret_cast<uintptr_t>(output_proj) |
                        reinterpret_cast<uintptr_t>(kv) | reinterpret_cast<uintptr_t>(workspace);
@@ -1551,6 +1656,8 @@ extern "C" int32_t msd_decode_step(const msd_config* cfg, const void* token_emb,
   a.token = token_id;
   a.pos = pos;
   a.epoch = epoch;
+  a.nsteps = n_steps;
+  a.logits_stride = logits_stride;
   a.H = cfg->n_heads;
   a.KV = cfg->n_kv_heads;
   a.L = cfg->n_layers;
@@ -1569,10 +1676,29 @@ extern "C" int32_t msd_decode_step(const msd_config* cfg, const void* token_emb,
   a.log_rows = p.log_rows;
   a.keep = int(std::min<int64_t>(cfg->n_layers, kKeepBytes / (a.lay.layer_elems * 2)));
   bool not_resident = false;
-  const hipError_t e =
-      launch(a, cfg->d_model, cfg->d_ff, n_workgroups, p.lds, static_cast<hipStream_t>(stream), &not_resident);
+  const hipError_t e = launch(a, cfg->d_model, cfg->d_ff, n_workgroups, p.lds, stream, &not_resident);
   if (not_resident) return MSD_E_CONFIG;
   return e == hipSuccess ? MSD_OK : MSD_E_HIP;
+}
+
+extern "C" int32_t msd_decode_step(const msd_config* cfg, const void* token_emb, const void* output_proj,
+                                   const void* packed_w, const void* lnf_s, const float* rope, int32_t token_id,
+                                   const int32_t* token_dev, int32_t pos, void* kv, void* workspace,
+                                   uint32_t epoch, float* logits, int32_t* next_token,
+                                   int32_t n_workgroups, void* stream) {
+  return decode_impl(cfg, token_emb, output_proj, packed_w, lnf_s, rope, token_id, token_dev, pos, 1, kv, workspace,
+                     epoch, logits, 0, next_token, n_workgroups, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int32_t msd_decode_steps(const msd_config* cfg, const void* token_emb, const void* output_proj,
+                                    const void* packed_w, const void* lnf_s, const float* rope, int32_t token_id,
+                                    const int32_t* token_dev, int32_t pos, int32_t n_steps, void* kv,
+                                    void* workspace, uint32_t epoch, float* logits, int32_t all_logits,
+                                    int32_t* tokens_out, int32_t n_workgroups, void* stream) {
+  if (!cfg) return MSD_E_CONFIG;
+  return decode_impl(cfg, token_emb, output_proj, packed_w, lnf_s, rope, token_id, token_dev, pos, n_steps, kv,
+                     workspace, epoch, logits, all_logits ? int64_t(cfg->vocab_size) : 0, tokens_out, n_workgroups,
+                     static_cast<hipStream_t>(stream));
 }
 
 // Decode workspaces in uncached device memory, pooled per (device, size) and never freed.

@@ -19,6 +19,7 @@ Differences from the reference call, by design:
 import collections
 import ctypes
 
+import numpy as np
 import torch
 
 from . import _lib
@@ -98,17 +99,76 @@ class Decoder:
             if not 0 <= tok < c["vocab_size"]:
                 raise ValueError(f"token {tok} outside [0, {c['vocab_size']})")
         out = self.out if out is None else out
-        self.epoch = (self.epoch % 0xFFFFFFFE) + 1
+        epoch = self._next_epochs(1)
         s = stream if stream is not None else torch.cuda.current_stream(self.device)
         w = self.w
         rc = _lib.lib().msd_decode_step(
             ctypes.byref(self._cfg), w["token_emb"].data_ptr(), w["output_proj"].data_ptr(),
             w["packed_w"].data_ptr(),
             w["lnf_s"].data_ptr(), w["rope"].data_ptr(), tok, tok_dev, pos, self.kv.data_ptr(),
-            self.workspace_ptr, self.epoch, self.logits.data_ptr(), out.data_ptr(),
+            self.workspace_ptr, epoch, self.logits.data_ptr(), out.data_ptr(),
             self.n_workgroups, ctypes.c_void_p(s.cuda_stream))
         _lib.check(rc, "msd_decode_step")
         return out
+
+    def _next_epochs(self, n):
+        """Tags for n steps: the next n values after the last one used, restarting at 1 when they
+        would pass 0xFFFFFFFE (every step rewrites every exchange word, so old tags never linger)."""
+        if self.epoch + n > 0xFFFFFFFE:
+            self.epoch = 0
+        e = self.epoch + 1
+        self.epoch += n
+        return e
+
+    def launch_steps(self, token, pos, n_steps, all_logits=False, out=None, logits=None, stream=None):
+        """Enqueue ``n_steps`` greedy steps in one launch (step s at pos + s on step s - 1's argmax).
+
+        Returns the device int32 (n_steps, 2) array of (argmax, status) per step; the logits of
+        every step land in ``logits`` (n_steps, V) with ``all_logits``, else the last step's in
+        ``self.logits``.
+        """
+        c = self.config
+        pos, n_steps = int(pos), int(n_steps)
+        if n_steps < 1 or not 0 <= pos or pos + n_steps > c["context_len"]:
+            raise ValueError(f"positions {pos}..{pos + n_steps - 1} outside [0, {c['context_len']})")
+        tok_dev, tok = None, 0
+        if isinstance(token, torch.Tensor) and token.is_cuda:
+            if token.dtype != torch.int32:
+                raise ValueError("device token must be int32")
+            tok_dev = token.data_ptr()
+        else:
+            tok = int(token)
+            if not 0 <= tok < c["vocab_size"]:
+                raise ValueError(f"token {tok} outside [0, {c['vocab_size']})")
+        if out is None:
+            out = torch.empty((n_steps, 2), dtype=torch.int32, device=self.device)
+        if all_logits:
+            if logits is None:
+                logits = torch.empty((n_steps, c["vocab_size"]), dtype=torch.float32, device=self.device)
+        else:
+            logits = self.logits
+        s = stream if stream is not None else torch.cuda.current_stream(self.device)
+        w = self.w
+        rc = _lib.lib().msd_decode_steps(
+            ctypes.byref(self._cfg), w["token_emb"].data_ptr(), w["output_proj"].data_ptr(),
+            w["packed_w"].data_ptr(), w["lnf_s"].data_ptr(), w["rope"].data_ptr(), tok, tok_dev, pos, n_steps,
+            self.kv.data_ptr(), self.workspace_ptr, self._next_epochs(n_steps), logits.data_ptr(),
+            1 if all_logits else 0, out.data_ptr(), self.n_workgroups, ctypes.c_void_p(s.cuda_stream))
+        _lib.check(rc, "msd_decode_steps")
+        self._keep = (out, logits)
+        return out
+
+    def generate(self, token, pos, n_steps, all_logits=False):
+        """``n_steps`` greedy tokens after ``token`` at ``pos`` in one launch; returns the host list
+        of tokens (and the (n_steps, V) logits when ``all_logits``)."""
+        out = self.launch_steps(token, pos, n_steps, all_logits=all_logits)
+        logits = self._keep[1]
+        host = out.cpu().numpy()
+        bad = np.nonzero(host[:, 1])[0]
+        if len(bad):
+            self.raise_for_status(int(host[bad[0], 1]), f"decode step at pos {int(pos) + int(bad[0])}")
+        toks = [int(t) for t in host[:, 0]]
+        return (toks, logits) if all_logits else toks
 
     def raise_for_status(self, status, what):
         """Raise the MsdError for a non-zero step status, after clearing the workspace's
