@@ -1,8 +1,8 @@
 """Parity of the matrix-core prefill (msd_prefill) with the oracle (GPU).
 
-The prefill rounds every projection input to bf16 and accumulates in f32, so the oracle
-is ``prefill_with_kv(..., act_round="bf16")`` (model.py:194-231 with those rounding points);
-logits are compared to 2e-2 abs / 1e-2 rel, the bf16 KV cache rows to the same bound.
+Every projection input enters the matrix cores as two bf16 parts (hi + lo, f32 to about
+2^-17), so the oracle is the f32 ``prefill_with_kv`` (model.py:194-231); logits are compared to
+2e-2 abs / 1e-2 rel, the bf16 KV cache rows to the same bound.
 """
 import numpy as np
 import pytest
@@ -59,7 +59,7 @@ def test_tiny_prefill_matches_oracle(tiny, T):
     params, w = tiny
     toks = make_prompt(T, TINY["vocab_size"], seed=100 + T)
     la, last, out, kv = _run(w, TINY, toks)
-    ref, kc, vc = om.prefill_with_kv(params, TINY, toks, act_round="bf16")
+    ref, kc, vc = om.prefill_with_kv(params, TINY, toks)
     np.testing.assert_allclose(la, ref, atol=ATOL, rtol=RTOL)
     assert np.array_equal(last, la[-1])
     assert out[0] == int(np.argmax(la[-1])) and out[1] == 0
@@ -74,14 +74,13 @@ def test_306m_prefill_128_matches_oracle(m306):
     params, w = m306
     toks = make_prompt(128, M306["vocab_size"], seed=3)
     la, last, out, kv = _run(w, M306, toks)
-    ref, kc, vc = om.prefill_with_kv(params, M306, toks, act_round="bf16")
-    print("306M prefill max |logit diff|:", float(np.max(np.abs(la - ref))))
+    ref, kc, vc = om.prefill_with_kv(params, M306, toks)
+    print("306M prefill max |logit diff| vs f32 model.py:", float(np.max(np.abs(la - ref))))
     np.testing.assert_allclose(la, ref, atol=ATOL, rtol=RTOL)
     _check_kv(kv, M306, 128, kc, vc)
-    # against the f32 model.py forward itself (no rounding points), the bound of the task
-    f32 = om.forward(params, M306, toks)
-    print("306M prefill max |logit diff| vs f32 model.py:", float(np.max(np.abs(la - f32))))
-    np.testing.assert_allclose(la, f32, atol=ATOL, rtol=RTOL)
+    # the reference kernel's bf16 rounding points move the logits by more than this path does
+    b16 = om.prefill_with_kv(params, M306, toks, act_round="bf16")[0]
+    assert np.max(np.abs(la - ref)) < 0.25 * np.max(np.abs(b16 - ref))
 
 
 def _gpu_greedy_after_prefill(w, cfg, prompt, n):
@@ -103,7 +102,7 @@ def test_prefill_then_decode_token_exact(cfgname, request):
     prompt = make_prompt(48 if cfgname == "tiny" else 128, cfg["vocab_size"], seed=9)
     n = 48 if cfgname == "tiny" else 128
     got = _gpu_greedy_after_prefill(w, cfg, prompt, n)
-    ref = om.greedy_generate(params, cfg, prompt, n, prefill="full", act_round=None, prefill_act_round="bf16")
+    ref = om.greedy_generate(params, cfg, prompt, n, prefill="full")
     assert got == ref
 
 
@@ -111,7 +110,7 @@ def test_reference_signature_prefill_with_kv(tiny):
     params, w = tiny
     toks = make_prompt(20, TINY["vocab_size"], seed=4)
     logits, ks, vs = prefill_with_kv(params, TINY, toks)
-    ref, kc, vc = om.prefill_with_kv(params, TINY, toks, act_round="bf16")
+    ref, kc, vc = om.prefill_with_kv(params, TINY, toks)
     assert tuple(logits.shape) == (20, TINY["vocab_size"])
     np.testing.assert_allclose(logits.cpu().numpy(), ref, atol=ATOL, rtol=RTOL)
     assert len(ks) == TINY["n_layers"] and tuple(ks[0].shape) == (1, 128, 64)
@@ -137,7 +136,7 @@ def test_306m_prefill_full_context(m306):
     params, w = m306
     toks = make_prompt(512, M306["vocab_size"], seed=8)
     _, last, out, kv = _run(w, M306, toks, all_logits=False)
-    ref, kc, vc = om.prefill_with_kv(params, M306, toks, act_round="bf16")
+    ref, kc, vc = om.prefill_with_kv(params, M306, toks)
     np.testing.assert_allclose(last, ref[-1], atol=ATOL, rtol=RTOL)
     ks, vs = unpack_kv_caches(kv, M306["n_layers"], M306["n_kv_heads"], M306["context_len"], M306["d_head"])
     for l in (0, 11, 23):

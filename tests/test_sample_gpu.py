@@ -138,7 +138,7 @@ def _teacher_forced_sampled(params, cfg, prompt, n, temperature, top_p, pen, see
     for i in range(n):
         assert osm.sample_token(rec[i], temperature, top_p, pen, toks[:i], us[i], exp="rounded") == toks[i], i
     # oracle: prefill with bf16 projection inputs (as the matrix-core prefill), then f32 steps
-    first, kc, vc = om.prefill_with_kv(params, cfg, prompt, act_round="bf16")
+    first, kc, vc = om.prefill_with_kv(params, cfg, prompt)
     rope = om.precompute_rope_table(cfg["context_len"], cfg["d_head"])
     np.testing.assert_allclose(rec[0], first[-1], atol=ATOL, rtol=RTOL)
     worst = float(np.max(np.abs(rec[0] - first[-1])))
@@ -173,7 +173,7 @@ def test_stream_and_generate_agree():
     b = generate_tokens(params, TINY, prompt, 40, temperature=0.8, top_p=0.9, rep_penalty=1.1, seed=3)
     assert a == b
     g = generate_tokens(params, TINY, prompt, 40)
-    assert g == om.greedy_generate(params, TINY, prompt, 40, prefill="full", prefill_act_round="bf16")
+    assert g == om.greedy_generate(params, TINY, prompt, 40, prefill="full")
     dec = Decoder(prepare_decode_weights_nlayer(params, TINY), TINY)
     st = list(run_generation(dec, list(prompt), 40, prefill="step"))
     assert st == om.greedy_generate(params, TINY, prompt, 40, prefill="step")

@@ -77,5 +77,5 @@ def test_cli_runs_a_d512_checkpoint(tmp_path):
     prompt = "A wider model through the same command line."
     ids = ck.load_bpe_vocab(str(tmp_path / "data"))["encode_fn"](prompt)
     toks = gen.main(["--prompt", prompt, "--weights", str(tmp_path / "weights.pkl"), "--max-tokens", "16"])
-    ref = om.greedy_generate(params, cfg, np.array(ids, np.int32), 16, prefill="full", prefill_act_round="bf16")
+    ref = om.greedy_generate(params, cfg, np.array(ids, np.int32), 16, prefill="full")
     assert toks == ref

@@ -3,9 +3,9 @@
 The reference describes a parallel verification kernel: K draft tokens through the full target
 in one call, a mini-prefill over the existing KV cache (knowledge/program.md:147-155).  Row i
 of a verification must give the logits of the sequential decode step at its position once rows
-0..i-1 are accepted, so the oracle is ``decode_step`` teacher-forced through the draft tokens
-after ``prefill_with_kv`` of the prompt, with the matrix-core rounding points
-(act_round="bf16"); logits within 2e-2 abs / 1e-2 rel, argmax equal, cache rows equal.
+0..i-1 are accepted, so the oracle is ``decode_step`` (the f32 model.py maths with the bf16
+cache) teacher-forced through the draft tokens after ``prefill_with_kv`` of the prompt; logits
+within 2e-2 abs / 1e-2 rel, argmax equal, cache rows equal.
 """
 import numpy as np
 import pytest
@@ -31,11 +31,11 @@ def _check_rows(params, cfg, w, P, draft, start_check_kv=True):
     ver = Verifier(w, cfg, max_tokens=len(draft))
     logits, am = ver.launch(draft, P, kv)
     got, gam = logits.cpu().numpy(), am.cpu().numpy()
-    _, kc, vc = om.prefill_with_kv(params, cfg, prompt, act_round="bf16")
+    _, kc, vc = om.prefill_with_kv(params, cfg, prompt)
     rope = om.precompute_rope_table(cfg["context_len"], cfg["d_head"])
     worst = 0.0
     for i, t in enumerate(draft):
-        ref, ra = om.decode_step(params, cfg, int(t), P + i, kc, vc, act_round="bf16", rope=rope)
+        ref, ra = om.decode_step(params, cfg, int(t), P + i, kc, vc, rope=rope)
         np.testing.assert_allclose(got[i], ref, atol=ATOL, rtol=RTOL)
         worst = max(worst, float(np.abs(got[i] - ref).max()))
         assert gam[i, 0] == ra and gam[i, 1] == 0, i
@@ -76,7 +76,7 @@ def test_speculative_generation_is_the_target_greedy_generation(draft_kind):
         dparams, dw = dcfg_params, prepare_decode_weights_nlayer(dcfg_params, TINY)
     prompt = make_prompt(16, TINY["vocab_size"], seed=1)
     toks, stats = speculative_generate(w, TINY, dw, TINY, prompt, 40, k=4)
-    ref = om.greedy_generate(params, TINY, prompt, 40, prefill="full", act_round="bf16")
+    ref = om.greedy_generate(params, TINY, prompt, 40, prefill="full")
     print(draft_kind, stats)
     assert toks == ref
     if draft_kind == "same_model":

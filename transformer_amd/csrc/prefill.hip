@@ -68,6 +68,16 @@ __device__ __forceinline__ uint16_t f2bf(float f) {   // round to nearest even
   return uint16_t((u + (((u >> 16) & 1u) + 0x7fffu)) >> 16);
 }
 
+// An activation entering a projection as two bf16 parts, hi = bf16(x) and lo = bf16(x - hi): the
+// matrix cores multiply both with the bf16 weight and add in f32, so the product carries x to
+// about 2^-17 relative instead of bf16's 2^-9 (the f32 activations of model.py, not the
+// reference kernel's bf16 rounding points).  The lo part lives in a second plane of the buffer.
+__device__ __forceinline__ void put_split(uint16_t* hi, int64_t plane, float x) {
+  const uint16_t h = f2bf(x);
+  hi[0] = h;
+  hi[plane] = f2bf(x - bf2f(h));
+}
+
 // Wave64 reductions with DPP row shifts and row broadcasts (fixed order, no LDS traffic);
 // the result is read from lane 63 as a wave-uniform value.
 template <int CTRL, int ROWMASK>
@@ -128,7 +138,8 @@ __device__ __forceinline__ int64_t cache_row(const Rows& r, int m, int p) {
 }
 
 struct GemmArgs {
-  const uint16_t* A;   // [M][lda] bf16
+  const uint16_t* A;   // [M][lda] bf16: the hi parts; the lo parts follow at A + a_plane
+  int64_t a_plane;
   const uint16_t* W;   // [N][K] bf16
   float* out;          // partials [splits][M][N] f32, or [M][ldo] (single split)
   int M, N, K, lda, ldo, splits;
@@ -148,7 +159,7 @@ __global__ __launch_bounds__(256) void mx_gemm(GemmArgs g) {
   const int c0 = (nchunks * int(blockIdx.z)) / g.splits, c1 = (nchunks * (int(blockIdx.z) + 1)) / g.splits;
   const int kq = 8 * (lane >> 4);   // this lane's 8-element K run within a 32 chunk
   const int r16 = lane & 15;
-  const uint16_t* arow[RB];
+  const uint16_t* arow[RB];   // hi parts (the lo parts a_plane elements further)
   bool aval[RB];
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb) {
@@ -164,32 +175,36 @@ __global__ __launch_bounds__(256) void mx_gemm(GemmArgs g) {
   for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
     for (int cb = 0; cb < CB; ++cb) acc[rb][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
-  auto step = [&](const uint4* a, const uint4* w) {
+  auto step = [&](const uint4* a, const uint4* al, const uint4* w) {
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-      for (int cb = 0; cb < CB; ++cb)
+      for (int cb = 0; cb < CB; ++cb) {
         acc[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a[rb]), as_bf16x8(w[cb]), acc[rb][cb], 0, 0, 0);
+        acc[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(al[rb]), as_bf16x8(w[cb]), acc[rb][cb], 0, 0, 0);
+      }
   };
   // U chunks per round, all loads issued before the first MMA; the last round's chunks past c1
   // reload chunk c1 - 1 and are skipped (loads stay unconditional: a load under a branch is
   // waited for at the join)
   for (int c = c0; c < c1; c += U) {
-    uint4 a[U][RB], w[U][CB];
+    uint4 a[U][RB], al[U][RB], w[U][CB];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int k = min(c + u, c1 - 1) * kBK;
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb) {
         const uint4 v = *reinterpret_cast<const uint4*>(arow[rb] + k);
+        const uint4 vl = *reinterpret_cast<const uint4*>(arow[rb] + g.a_plane + k);
         a[u][rb] = aval[rb] ? v : make_uint4(0, 0, 0, 0);
+        al[u][rb] = aval[rb] ? vl : make_uint4(0, 0, 0, 0);
       }
 #pragma unroll
       for (int cb = 0; cb < CB; ++cb) w[u][cb] = *reinterpret_cast<const uint4*>(wrow[cb] + k);
     }
 #pragma unroll
     for (int u = 0; u < U; ++u)
-      if (c + u < c1) step(a[u], w[u]);
+      if (c + u < c1) step(a[u], al[u], w[u]);
   }
   // D layout of a 16 x 16 tile: lane holds rows 4*(lane/16) + r (r < 4) of column lane % 16
   float* out = g.splits > 1 ? g.out + int64_t(blockIdx.z) * g.M * g.N : g.out;
@@ -215,11 +230,12 @@ __device__ __forceinline__ float block_sum256(float v, float* red) {
 }
 
 // Row blockIdx.x + row0: h += sum_z part[z] (z in order), then
-// xn[j] = bf16(scale[i] * (h[i] / sqrt(mean(h^2) + 1e-5))) with i the input element at
-// position j of the packed row layout (model.py:94-98).  Every partial is requested before
+// xn[j] = scale[i] * (h[i] / sqrt(mean(h^2) + 1e-5)) as hi/lo bf16 parts (planes `plane` apart),
+// with i the input element at position j of the packed row layout (model.py:94-98).  Every partial is requested before
 // the first is added, so the sum costs one memory round trip.
 __global__ __launch_bounds__(kNormThreads) void mx_norm(float* h, const float* part, int splits, int M, int d,
-                                                        const uint16_t* scale, uint16_t* xn, int row0) {
+                                                        const uint16_t* scale, uint16_t* xn, int64_t plane,
+                                                        int row0) {
   constexpr int NE = kMaxRows / kNormThreads;
   __shared__ float red[4];
   __shared__ __align__(16) float hs[kMaxRows];
@@ -260,7 +276,7 @@ __global__ __launch_bounds__(kNormThreads) void mx_norm(float* h, const float* p
 #pragma unroll
   for (int q = 0; q < NE; ++q) {
     const int j = threadIdx.x + kNormThreads * q;
-    if (j < d) xn[int64_t(blockIdx.x) * d + j] = f2bf(bf2f(sc[q]) * (hs[perm_elem(j, d)] / r));
+    if (j < d) put_split(xn + int64_t(blockIdx.x) * d + j, plane, bf2f(sc[q]) * (hs[perm_elem(j, d)] / r));
   }
 }
 
@@ -336,8 +352,9 @@ __global__ __launch_bounds__(256) void mx_qkv_fin(const float* part, int splits,
 }
 
 // Row blockIdx.x: act_f = silu(gate_f) * up_f over the summed partials (gate/up are the packed
-// rows 2f, 2f+1; model.py:159), bf16 at the down projection's input position of f.
-__global__ __launch_bounds__(256) void mx_swiglu_fin(const float* part, int splits, int M, int F, uint16_t* act) {
+// rows 2f, 2f+1; model.py:159), as hi/lo bf16 parts at the down projection's input position of f.
+__global__ __launch_bounds__(256) void mx_swiglu_fin(const float* part, int splits, int M, int F, uint16_t* act,
+                                                     int64_t plane) {
   const int m = blockIdx.x, f = 2 * (blockIdx.y * 256 + threadIdx.x);   // outputs f and f + 1 (F is even)
   if (f >= F) return;
   float4 pv[kMaxSplitK];
@@ -353,14 +370,15 @@ __global__ __launch_bounds__(256) void mx_swiglu_fin(const float* part, int spli
       g1 += pv[z].z;
       u1 += pv[z].w;
     }
-  act[int64_t(m) * F + perm_pos(f, F)] = f2bf((g0 * (1.f / (1.f + expf(-g0)))) * u0);
-  act[int64_t(m) * F + perm_pos(f + 1, F)] = f2bf((g1 * (1.f / (1.f + expf(-g1)))) * u1);
+  put_split(act + int64_t(m) * F + perm_pos(f, F), plane, (g0 * (1.f / (1.f + expf(-g0)))) * u0);
+  put_split(act + int64_t(m) * F + perm_pos(f + 1, F), plane, (g1 * (1.f / (1.f + expf(-g1)))) * u1);
 }
 
 // Prefill: causal GQA attention of query block blockIdx.y (16 rows) for head blockIdx.x.
 // Each wave owns 4 queries; key chunks of 64 rows go through LDS, with an online softmax per
 // query (scores: lane = key; output: lane = dimension).  Scale 1/sqrt(64) (model.py:98).
-__global__ __launch_bounds__(256) void mx_attention_prefill(const float* qkv, int M, int H, int KV, uint16_t* att) {
+__global__ __launch_bounds__(256) void mx_attention_prefill(const float* qkv, int M, int H, int KV, uint16_t* att,
+                                                            int64_t plane) {
   __shared__ float sk[64 * kKStride];
   __shared__ float sv[64 * kDh];
   __shared__ float sq[kAttnQ * kDh];
@@ -450,7 +468,7 @@ __global__ __launch_bounds__(256) void mx_attention_prefill(const float* qkv, in
 #pragma unroll
   for (int t = 0; t < kQW; ++t) {
     const int i = q0 + kQW * wv + t;
-    if (i < M) att[int64_t(i) * d + perm_pos(h * kDh + lane, d)] = f2bf(o[t] / ls[t]);
+    if (i < M) put_split(att + int64_t(i) * d + perm_pos(h * kDh + lane, d), plane, o[t] / ls[t]);
   }
 }
 
@@ -465,7 +483,7 @@ constexpr int kAttnWaves = 8;
 
 __global__ __launch_bounds__(64 * kAttnWaves) void mx_attention_decode(const float* qkv, Rows rows, int H, int KV,
                                                                        const uint16_t* kc, const uint16_t* vc,
-                                                                       uint16_t* att) {
+                                                                       uint16_t* att, int64_t plane) {
   __shared__ float sq[kDh], skc[kDh], svc[kDh];   // q, and the current position's f32 k and v
   __shared__ float sp[kAttnWaves][64];
   __shared__ int srow[kAttnWaves][64];
@@ -549,7 +567,7 @@ __global__ __launch_bounds__(64 * kAttnWaves) void mx_attention_decode(const flo
       num += a * so[w][lane];
       den += a * sml[w][1];
     }
-    att[int64_t(m) * d + perm_pos(h * kDh + lane, d)] = f2bf(num / den);
+    put_split(att + int64_t(m) * d + perm_pos(h * kDh + lane, d), plane, num / den);
   }
 }
 
@@ -651,10 +669,10 @@ static Layout layout(const msd_config* c, int M) {
   Layout L;
   size_t o = 0;
   L.h = o;      o += al256(size_t(M) * d * 4);
-  L.xn = o;     o += al256(size_t(M) * d * 2);
+  L.xn = o;     o += al256(size_t(M) * d * 2 * 2);    // hi and lo planes
   L.qkv = o;    o += al256(size_t(M) * nqkv * 4);
-  L.att = o;    o += al256(size_t(M) * d * 2);
-  L.act = o;    o += al256(size_t(M) * ff * 2);
+  L.att = o;    o += al256(size_t(M) * d * 2 * 2);
+  L.act = o;    o += al256(size_t(M) * ff * 2 * 2);
   L.part = o;   o += al256(part_floats(c, M) * 4);
   L.status = o; o += 256;
   L.rowpos = o; o += al256(size_t(M) * 4);
@@ -673,9 +691,9 @@ static bool mx_config_ok(const msd_config* c) {
 
 // C = A W^T split over K: partials [splits][M][N] (pass ldo = N), or with splits == 1 rows
 // of stride ldo
-static hipError_t gemm(const uint16_t* A, int lda, const uint16_t* W, int M, int N, int K, float* out, int ldo,
-                       int splits, hipStream_t s) {
-  GemmArgs g{A, W, out, M, N, K, lda, ldo, splits};
+static hipError_t gemm(const uint16_t* A, int64_t a_plane, int lda, const uint16_t* W, int M, int N, int K, float* out,
+                       int ldo, int splits, hipStream_t s) {
+  GemmArgs g{A, a_plane, W, out, M, N, K, lda, ldo, splits};
   const int bm = bm_for(M);
   const dim3 grid(N / kBN, (M + bm - 1) / bm, splits);
   if (bm == 16) hipLaunchKernelGGL((mx_gemm<1, 1>), grid, dim3(256), 0, s, g);
@@ -716,20 +734,22 @@ static int run_layers(const msd_config* cfg, const Weights& wt, const Rows& rows
     const uint16_t* Wl = wt.w + int64_t(l) * layer;
     uint16_t* kc = kv + int64_t(l) * 2 * KV * rows.pool * kDh;
     uint16_t* vc = kc + int64_t(KV) * rows.pool * kDh;
-    hipLaunchKernelGGL(mx_norm, dim3(M), dim3(kNormThreads), 0, s, h, part, pending, M, d, Wl, xn, 0);
-    if ((err = gemm(xn, d, Wl + off_qkv, M, nqkv, d, part, nqkv, sq, s)) != hipSuccess) break;
+    const int64_t pd = int64_t(M) * d, pf = int64_t(M) * ff;   // lo planes after the hi planes
+    hipLaunchKernelGGL(mx_norm, dim3(M), dim3(kNormThreads), 0, s, h, part, pending, M, d, Wl, xn, pd, 0);
+    if ((err = gemm(xn, pd, d, Wl + off_qkv, M, nqkv, d, part, nqkv, sq, s)) != hipSuccess) break;
     hipLaunchKernelGGL(mx_qkv_fin, dim3(M, (nqkv / 4 + 255) / 256), dim3(256), 0, s, part, sq, M, H, KV, wt.rope, rows,
                        kc, vc, qkv);
     if (prefill)
       hipLaunchKernelGGL(mx_attention_prefill, dim3(H, (M + kAttnQ - 1) / kAttnQ), dim3(256), 0, s, qkv, M, H, KV,
-                         att);
+                         att, pd);
     else
-      hipLaunchKernelGGL(mx_attention_decode, dim3(M, H), dim3(64 * kAttnWaves), 0, s, qkv, rows, H, KV, kc, vc, att);
-    if ((err = gemm(att, d, Wl + off_o, M, d, d, part, d, so, s)) != hipSuccess) break;
-    hipLaunchKernelGGL(mx_norm, dim3(M), dim3(kNormThreads), 0, s, h, part, so, M, d, Wl + off_ln2, xn, 0);
-    if ((err = gemm(xn, d, Wl + off_gu, M, 2 * ff, d, part, 2 * ff, sg, s)) != hipSuccess) break;
-    hipLaunchKernelGGL(mx_swiglu_fin, dim3(M, (ff / 2 + 255) / 256), dim3(256), 0, s, part, sg, M, ff, act);
-    if ((err = gemm(act, ff, Wl + off_dn, M, d, ff, part, d, sd, s)) != hipSuccess) break;
+      hipLaunchKernelGGL(mx_attention_decode, dim3(M, H), dim3(64 * kAttnWaves), 0, s, qkv, rows, H, KV, kc, vc, att,
+                         pd);
+    if ((err = gemm(att, pd, d, Wl + off_o, M, d, d, part, d, so, s)) != hipSuccess) break;
+    hipLaunchKernelGGL(mx_norm, dim3(M), dim3(kNormThreads), 0, s, h, part, so, M, d, Wl + off_ln2, xn, pd, 0);
+    if ((err = gemm(xn, pd, d, Wl + off_gu, M, 2 * ff, d, part, 2 * ff, sg, s)) != hipSuccess) break;
+    hipLaunchKernelGGL(mx_swiglu_fin, dim3(M, (ff / 2 + 255) / 256), dim3(256), 0, s, part, sg, M, ff, act, pf);
+    if ((err = gemm(act, pf, ff, Wl + off_dn, M, d, ff, part, d, sd, s)) != hipSuccess) break;
     pending = sd;
   }
   if (err == hipSuccess) err = hipGetLastError();
@@ -793,8 +813,10 @@ static int32_t prefill_impl(const msd_config* cfg, const Weights& wt, const int3
   if (err != hipSuccess) return MSD_E_HIP;
   // final norm of the rows whose logits are wanted, then the tied output projection
   const int r0 = logits_all ? 0 : M - 1, nr = M - r0;
-  hipLaunchKernelGGL(mx_norm, dim3(nr), dim3(kNormThreads), 0, s, h, part, pending, M, d, wt.lnf, xn, r0);
-  if (gemm(xn, d, wt.outp, nr, V, d, logits_all ? logits_all : logits_last, V, 1, s) != hipSuccess) return MSD_E_HIP;
+  hipLaunchKernelGGL(mx_norm, dim3(nr), dim3(kNormThreads), 0, s, h, part, pending, M, d, wt.lnf, xn,
+                     int64_t(nr) * d, r0);
+  if (gemm(xn, int64_t(nr) * d, d, wt.outp, nr, V, d, logits_all ? logits_all : logits_last, V, 1, s) != hipSuccess)
+    return MSD_E_HIP;
   const float* last = logits_all ? logits_all + int64_t(M - 1) * V : logits_last;
   if (logits_all && last != logits_last &&
       hipMemcpyAsync(logits_last, last, size_t(V) * 4, hipMemcpyDeviceToDevice, s) != hipSuccess)
@@ -888,8 +910,8 @@ extern "C" int32_t msd_batch_decode_step(const msd_config* cfg, const void* toke
   hipError_t err;
   const int pending = run_layers(cfg, wt, rows, static_cast<uint16_t*>(kv_pool), L, ws, false, s, err);
   if (err != hipSuccess) return MSD_E_HIP;
-  hipLaunchKernelGGL(mx_norm, dim3(M), dim3(kNormThreads), 0, s, h, part, pending, M, d, wt.lnf, xn, 0);
-  if (gemm(xn, d, wt.outp, M, V, d, logits, V, 1, s) != hipSuccess) return MSD_E_HIP;
+  hipLaunchKernelGGL(mx_norm, dim3(M), dim3(kNormThreads), 0, s, h, part, pending, M, d, wt.lnf, xn, int64_t(M) * d, 0);
+  if (gemm(xn, int64_t(M) * d, d, wt.outp, M, V, d, logits, V, 1, s) != hipSuccess) return MSD_E_HIP;
   hipLaunchKernelGGL(mx_argmax, dim3(M), dim3(1024), 0, s, logits, V, V, next_tokens, status);
   return hipGetLastError() == hipSuccess ? MSD_OK : MSD_E_HIP;
 }

@@ -5,9 +5,9 @@
 generation loop uses: it fills a packed KV buffer in place and returns the last position's
 logits and argmax without leaving the device.
 
-The projections run on the matrix cores with bf16 activations (``msd_prefill``), so the
-numerics are those of the reference maths with every projection input rounded to bf16
-(the oracle's ``act_round="bf16"``).
+The projections run on the matrix cores (``msd_prefill``) with every input activation split
+into two bf16 parts (hi + lo, f32 to about 2^-17) against the bf16 weights, accumulated in f32,
+so the numerics are those of the f32 reference maths (model.py:194-231).
 """
 import ctypes
 
