@@ -194,8 +194,9 @@ int64_t msd_prefill_workspace_bytes(const msd_config* cfg, int32_t n_tokens);
  * logits of the last position; with logits_all != NULL also the logits of every position
  * (n_tokens x vocab_size, row-major).  next_token (device int32[2]) receives the argmax of the
  * last position's logits (lowest index on ties) and a status word (bit 1 = a token id was out
- * of range).  Every projection is a bf16 x bf16 matrix-core product accumulated in f32 with the
- * activations rounded to bf16 on entry; residual stream, RoPE, softmax and SwiGLU are f32.
+ * of range).  Every projection runs on the matrix cores with its f32 input split into two bf16
+ * parts (hi = bf16(x), lo = bf16(x - hi): x to about 2^-17 relative) against the bf16 weights,
+ * accumulated in f32; residual stream, RoPE, softmax and SwiGLU are f32 (model.py's maths).
  * Weight arguments as for msd_decode_step.  Requires d_model, 2*d_ff and vocab_size to be
  * multiples of 64, d_ff a multiple of 32 and n_tokens <= context_len. */
 int32_t msd_prefill(const msd_config* cfg, const void* token_emb, const void* output_proj,
@@ -214,7 +215,7 @@ int64_t msd_verify_workspace_bytes(const msd_config* cfg, int32_t n_tokens);
  * sequential decode steps would give once tokens 0..i-1 are accepted.  Writes the K/V rows of
  * every position, the f32 logits of every row (n_tokens x vocab_size) and argmax[2i] = the
  * argmax of row i (lowest index on ties), argmax[2i+1] = status (bit 1 = a token id out of
- * range).  Numerics of msd_prefill (bf16 projection inputs on the matrix cores).  Requires
+ * range).  Numerics of msd_prefill (projection inputs as hi/lo bf16 parts).  Requires
  * start_pos >= 1, start_pos + n_tokens <= context_len <= 512.
  * Replaces the parallel verification kernel the reference describes (K draft tokens through the
  * full target in one call, a mini-prefill with an existing KV cache: knowledge/program.md:
@@ -247,7 +248,7 @@ int64_t msd_batch_workspace_bytes(const msd_config* cfg, int32_t batch);
  * page_tables[b * max_pages ...] and writes its K/V row at positions[b].  Outputs logits
  * (batch x vocab_size f32) and next_tokens (device int32[2 * batch]: argmax of row b at 2b,
  * the step's status word at 2b+1; bit 1 = token out of range, bit 2 = position or page out of
- * range).  Same numerics as msd_prefill (bf16 projection inputs on the matrix cores); the
+ * range).  Same numerics as msd_prefill (projection inputs as hi/lo bf16 parts); the
  * current position attends with its un-rounded K/V. */
 int32_t msd_batch_decode_step(const msd_config* cfg, const void* token_emb, const void* output_proj,
                               const void* packed_w, const void* lnf_s, const float* rope,

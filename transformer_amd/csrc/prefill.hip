@@ -7,13 +7,14 @@
 // writing the KV cache rows of every layer and the logits, with every projection on the
 // matrix cores.
 //
-// Numerics: model.py:94-191 with the activations entering each projection rounded to bf16
-// (RMSNorm outputs, attention output, SwiGLU output, final norm) — the rounding points of the
-// reference decode kernel (multi_sm_decode.py:143,229,268,289,320) — the projections as
-// bf16 x bf16 products accumulated in f32 (v_mfma_f32_16x16x32_bf16), the residual stream,
-// RoPE, softmax attention and SwiGLU in f32, K/V stored to the cache as bf16 after RoPE
-// (model.py:212-215).  In batched decode the current position attends with its un-rounded
-// K/V (multi_sm_decode.py:197,205).
+// Numerics: model.py:94-191 in f32.  Each activation entering a projection (RMSNorm outputs,
+// attention output, SwiGLU output, final norm) is stored as two bf16 parts, hi = bf16(x) and
+// lo = bf16(x - hi), and both are multiplied with the bf16 weights on the matrix cores
+// (v_mfma_f32_16x16x32_bf16) into one f32 accumulator: the projection sees x to about 2^-17
+// relative, where the reference kernel rounds it to bf16 (multi_sm_decode.py:143,229,268,289,
+// 320).  The residual stream, RoPE, softmax attention and SwiGLU are f32, K/V are stored to the
+// cache as bf16 after RoPE (model.py:212-215).  In batched decode the current position attends
+// with its un-rounded K/V (multi_sm_decode.py:197,205).
 //
 // KV cache: [layer][K, V][kv_head][pool positions][64] bf16 with pool positions = 16 * pages.
 // A row's position p lives at page table[p / 16] * 16 + p % 16; without a table the page is
