@@ -240,7 +240,10 @@ int32_t msd_prefill_paged(const msd_config* cfg, const void* token_emb, const vo
                           int32_t max_pages, void* kv_pool, int32_t pool_pages, void* workspace,
                           float* logits_last, int32_t* next_token, void* stream);
 
-/* Bytes of device workspace msd_batch_decode_step needs for `batch` sequences. */
+/* Bytes of device workspace msd_batch_decode_step needs for `batch` sequences.  The workspace
+ * must be zero-filled before its first step and then kept for the steps of this batch decoder
+ * (it holds the persistent step's epoch and barrier flags); one step may be in flight per
+ * workspace. */
 int64_t msd_batch_workspace_bytes(const msd_config* cfg, int32_t batch);
 
 /* One decode step of `batch` independent sequences: sequence b feeds tokens[b] at position
@@ -249,7 +252,10 @@ int64_t msd_batch_workspace_bytes(const msd_config* cfg, int32_t batch);
  * (batch x vocab_size f32) and next_tokens (device int32[2 * batch]: argmax of row b at 2b,
  * the step's status word at 2b+1; bit 1 = token out of range, bit 2 = position or page out of
  * range).  Same numerics as msd_prefill (projection inputs as hi/lo bf16 parts); the
- * current position attends with its un-rounded K/V. */
+ * current position attends with its un-rounded K/V.  Up to 8 sequences run as ONE persistent
+ * launch (one workgroup per compute unit, all resident, grid barriers between the phases of a
+ * layer); larger batches, or a device that cannot hold the grid resident, take the multi-kernel
+ * matrix-core pass. */
 int32_t msd_batch_decode_step(const msd_config* cfg, const void* token_emb, const void* output_proj,
                               const void* packed_w, const void* lnf_s, const float* rope,
                               const int32_t* tokens, const int32_t* positions, int32_t batch,

@@ -125,3 +125,46 @@ def test_bad_positions_and_pages_are_reported():
     p = torch.tensor([16, 16], dtype=torch.int32, device="cuda")
     out = bd.launch(t, p).cpu().numpy()
     assert out[1] & 4
+
+
+def test_persistent_step_matches_multi_kernel_step():
+    """Up to 8 sequences step in one persistent launch; 9 take the multi-kernel pass.  The same
+    8 sequences through both agree (different summation orders: 1e-4), with the same tokens."""
+    params = make_params(TINY, seed=0)
+    rng = np.random.default_rng(11)
+    lens = [int(x) for x in rng.integers(16, 65, 9)]
+    bd9, pool9, tables, prompts, first = _setup(TINY, params, 9, lens, 6, 128, seed=12)
+    pool8 = PagePool(TINY, 128)
+    pool8.data.copy_(pool9.data)
+    bd8 = PagedBatchDecoder(bd9.w, TINY, pool8, 8)
+    for b in range(8):
+        bd8.set_pages(b, tables[b])
+    toks9, toks8 = list(first), list(first[:8])
+    for i in range(6):
+        n9, l9 = bd9.step(toks9, [lens[b] + i for b in range(9)])
+        n8, l8 = bd8.step(toks8, [lens[b] + i for b in range(8)])
+        np.testing.assert_allclose(l8.cpu().numpy(), l9.cpu().numpy()[:8], atol=1e-4, rtol=1e-4)
+        assert n8 == n9[:8]
+        toks9, toks8 = n9, n8
+
+
+def test_persistent_step_epoch_wrap():
+    """The step's epoch (first word of its workspace) wraps from 0xFFFFFFFE to 1: steps across
+    the wrap give the same results as on a fresh workspace."""
+    params = make_params(TINY, seed=0)
+    lens = [18, 40, 25]
+    bd, pool, tables, prompts, first = _setup(TINY, params, 3, lens, 4, 64, seed=13)
+    pool2 = PagePool(TINY, 64)
+    pool2.data.copy_(pool.data)
+    bd2 = PagedBatchDecoder(bd.w, TINY, pool2, 3)
+    for b in range(3):
+        bd2.set_pages(b, tables[b])
+    bd2.workspace[:4].copy_(torch.tensor([0xFFFFFFFD], dtype=torch.int64).to(torch.int32).view(torch.uint8))
+    ta, tb = list(first), list(first)
+    for i in range(4):
+        na, la = bd.step(ta, [lens[b] + i for b in range(3)])
+        nb, lb = bd2.step(tb, [lens[b] + i for b in range(3)])
+        assert np.array_equal(la.cpu().numpy(), lb.cpu().numpy())
+        assert na == nb
+        ta, tb = na, nb
+    assert int(bd2.workspace[:4].view(torch.int32).item()) == 3   # 0xFFFFFFFE, 1, 2, 3 after 0xFFFFFFFD

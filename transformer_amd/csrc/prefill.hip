@@ -46,6 +46,7 @@
 #include <algorithm>
 
 #include "../../include/msdecode.h"
+#include "batched.h"
 
 namespace mpf {
 
@@ -868,10 +869,14 @@ extern "C" int32_t msd_verify(const msd_config* cfg, const void* token_emb, cons
                       static_cast<hipStream_t>(stream));
 }
 
+// The batched workspace: the persistent step's region (fixed size per shape, first, so that
+// its epoch and flags stay put whatever the batch), then the multi-kernel step's buffers.
+static int64_t batch_region(const msd_config* cfg) { return (mbd::region_bytes(cfg) + 255) & ~int64_t(255); }
+
 extern "C" int64_t msd_batch_workspace_bytes(const msd_config* cfg, int32_t batch) {
   if (!mx_config_ok(cfg)) return MSD_E_CONFIG;
   if (batch <= 0 || batch > kMaxRows) return MSD_E_ARG;
-  return int64_t(layout(cfg, batch).bytes);
+  return batch_region(cfg) + int64_t(layout(cfg, batch).bytes);
 }
 
 extern "C" int32_t msd_batch_decode_step(const msd_config* cfg, const void* token_emb, const void* output_proj,
@@ -892,11 +897,19 @@ extern "C" int32_t msd_batch_decode_step(const msd_config* cfg, const void* toke
   if (max_pages <= 0 || max_pages > (cfg->context_len + kPage - 1) / kPage || pool_pages <= 0) return MSD_E_ARG;
   if (cfg->context_len > 64 * kAttnWaves) return MSD_E_CONFIG;   // one 64-position block per attention wave
   hipStream_t s = static_cast<hipStream_t>(stream);
+  {   // up to 8 sequences: one persistent launch when the shape and the device allow it
+    const mbd::StepArgs sa{cfg, static_cast<const uint16_t*>(token_emb), static_cast<const uint16_t*>(output_proj),
+                           static_cast<const uint16_t*>(packed_w), static_cast<const uint16_t*>(lnf_s), rope, tokens,
+                           positions, batch, page_tables, max_pages, static_cast<uint16_t*>(kv_pool), pool_pages,
+                           workspace, logits, next_tokens, s};
+    const int32_t rc = mbd::try_step(sa);
+    if (rc != 1) return rc;
+  }
   const Weights wt{static_cast<const uint16_t*>(token_emb), static_cast<const uint16_t*>(output_proj),
                    static_cast<const uint16_t*>(packed_w), static_cast<const uint16_t*>(lnf_s), rope};
   const int d = cfg->d_model, V = cfg->vocab_size;
   const Layout L = layout(cfg, M);
-  char* ws = static_cast<char*>(workspace);
+  char* ws = static_cast<char*>(workspace) + batch_region(cfg);
   float* h = reinterpret_cast<float*>(ws + L.h);
   uint16_t* xn = reinterpret_cast<uint16_t*>(ws + L.xn);
   float* part = reinterpret_cast<float*>(ws + L.part);

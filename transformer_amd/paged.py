@@ -10,8 +10,11 @@ on the matrix-core passes of ``msd_prefill_paged`` / ``msd_batch_decode_step``:
   toks, logits = bd.step(tokens, positions)        # one token of every sequence per call
 
 Page tables are int32 (batch, max_pages); sequence b's position p lives in page
-``tables[b, p // 16]``, slot ``p % 16``.  Numerics are those of the prefill (bf16 projection
-inputs, f32 accumulation); the current position attends with its un-rounded K/V.
+``tables[b, p // 16]``, slot ``p % 16``.  Up to 8 sequences step in ONE persistent kernel
+launch (grid-wide barriers between the phases of a layer); larger batches use the
+multi-kernel matrix-core pass.  Projection inputs enter the matrix cores as hi/lo bf16 parts
+(f32 to about 2^-17), accumulated in f32; the current position attends with its un-rounded
+K/V.
 """
 import ctypes
 
@@ -60,7 +63,10 @@ class PagedBatchDecoder:
         nb = _lib.check(L.msd_batch_workspace_bytes(ctypes.byref(self._cfg), self.batch), "msd_batch_workspace_bytes")
         npf = _lib.check(L.msd_prefill_workspace_bytes(ctypes.byref(self._cfg), config["context_len"]),
                          "msd_prefill_workspace_bytes")
-        self.workspace = torch.empty(max(nb, npf), dtype=torch.uint8, device=self.device)
+        # the step's workspace holds its barrier flags and epoch: zero-filled once, used by no
+        # other call (the prompt prefill has its own)
+        self.workspace = torch.zeros(nb, dtype=torch.uint8, device=self.device)
+        self.pf_workspace = torch.empty(npf, dtype=torch.uint8, device=self.device)
         self.tables = torch.zeros((self.batch, self.max_pages), dtype=torch.int32, device=self.device)
         self.logits = torch.empty((self.batch, config["vocab_size"]), dtype=torch.float32, device=self.device)
         self.out = torch.zeros(2 * self.batch, dtype=torch.int32, device=self.device)
@@ -88,7 +94,7 @@ class PagedBatchDecoder:
         s = stream if stream is not None else torch.cuda.current_stream(self.device)
         rc = _lib.lib().msd_prefill_paged(
             ctypes.byref(self._cfg), *self._w(), toks.data_ptr(), toks.numel(), self.tables[b].data_ptr(),
-            self.max_pages, self.pool.data.data_ptr(), self.pool.n_pages, self.workspace.data_ptr(),
+            self.max_pages, self.pool.data.data_ptr(), self.pool.n_pages, self.pf_workspace.data_ptr(),
             self.last.data_ptr(), self.pf_out.data_ptr(), ctypes.c_void_p(s.cuda_stream))
         _lib.check(rc, "msd_prefill_paged")
         self._keep = toks
