@@ -251,7 +251,8 @@ int64_t msd_batch_workspace_bytes(const msd_config* cfg, int32_t batch);
  * page_tables[b * max_pages ...] and writes its K/V row at positions[b].  Outputs logits
  * (batch x vocab_size f32) and next_tokens (device int32[2 * batch]: argmax of row b at 2b,
  * the step's status word at 2b+1; bit 1 = token out of range, bit 2 = position or page out of
- * range).  Same numerics as msd_prefill (projection inputs as hi/lo bf16 parts); the
+ * range, bit 0 = a wait of the persistent step timed out).  Same numerics as msd_prefill
+ * (projection inputs as hi/lo bf16 parts); the
  * current position attends with its un-rounded K/V.  Up to 8 sequences run as ONE persistent
  * launch (one workgroup per compute unit, all resident, grid barriers between the phases of a
  * layer); larger batches, or a device that cannot hold the grid resident, take the multi-kernel
