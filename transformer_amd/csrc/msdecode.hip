@@ -91,10 +91,13 @@ constexpr int kKRowB = 144;      // LDS bytes per cached K row: 128 + 16 padding
 constexpr int kVRowB = 128;      // LDS bytes per cached V row
 constexpr uint32_t kSpinLimit = 1u << 20;
 
-constexpr int kWavesR = 8;       // worker waves of a row workgroup
+#ifndef MSD_ROW_WAVES
+#define MSD_ROW_WAVES 8
+#endif
+constexpr int kWavesR = MSD_ROW_WAVES;   // worker waves of a row workgroup (the rest of 0..7 exit)
 constexpr int kWavesA = 8;       // attention waves of an attention workgroup
-constexpr int kLoader = 8;       // wave index of the loader (both kinds)
-constexpr int kThreadsWG = 9 * 64;
+constexpr int kLoader = kWavesR > 8 ? kWavesR : 8;   // wave index of the loader (both kinds)
+constexpr int kThreadsWG = (kLoader + 1) * 64;
 constexpr int kMbox = 8;         // outputs per compute wave and phase
 #ifndef MSD_REPLICAS
 #define MSD_REPLICAS 4
@@ -329,6 +332,16 @@ __device__ __forceinline__ bool repoll(uint64_t (&wd)[NK], const uint64_t* src, 
 #define MSD_FIRST_POLL 16
 #endif
 constexpr int kFirstPoll = MSD_FIRST_POLL;
+// Barrier after each phase's output stores, so that no wave's polls of the next vector enter
+// the memory pipeline ahead of another wave's stores.
+#ifndef MSD_STORE_BAR
+#define MSD_STORE_BAR 1
+#endif
+constexpr bool kStoreBar = MSD_STORE_BAR != 0;
+// s_sleep units between the polls of an LDS counter (0: spin; measured fastest)
+#ifndef MSD_LDS_SLEEP
+#define MSD_LDS_SLEEP 0
+#endif
 // The attention partials take the attention workgroups' gather and compute (a few us)
 // before they can land, so that gather starts polling later.
 #ifndef MSD_ATT_FIRST_POLL
@@ -405,7 +418,7 @@ constexpr uint32_t kLdsSpinLimit = 1u << 22;
 __device__ __forceinline__ void lds_wait(int* ctr, int target, uint32_t* gctrl) {
   uint32_t spins = 0;
   while (lds_ld(ctr) < target) {
-    __builtin_amdgcn_s_sleep(1);
+    if constexpr (MSD_LDS_SLEEP > 0) __builtin_amdgcn_s_sleep(MSD_LDS_SLEEP);
     if ((++spins & 1023u) == 0) {
       if (ld_status(gctrl) & kStatusTimeout) return;
       if (spins > kLdsSpinLimit) {
@@ -545,6 +558,60 @@ __device__ __forceinline__ void dot_rows(const uint8_t* const (&rows)[R], const 
     out[i] = acc;
   }
   wave_sum_n<R>(out);
+}
+
+// dot_rows with one more wave sum taken in the same reduction chain: out[R] = sum over the
+// wave of `extra` (the lane's partial sum of squares of a folded RMSNorm).
+template <int NL, int R>
+__device__ __forceinline__ void dot_rows_x(const uint8_t* const (&rows)[R], const XV<NL>& xv, int k, int lane,
+                                           float extra, float (&out)[R + 1]) {
+  uint4 w[R][NL];
+#pragma unroll
+  for (int i = 0; i < R; ++i)
+#pragma unroll
+    for (int j = 0; j < NL; ++j) w[i][j] = *reinterpret_cast<const uint4*>(rows[i] + 1024 * j + 16 * lane);
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    float acc = 0.f;
+#pragma unroll
+    for (int j = 0; j < NL; ++j) {
+      uint4 u = w[i][j];
+      if (lane >= block_lanes(k, j)) u = make_uint4(0, 0, 0, 0);
+      acc += bf_lo(u.x) * xv.v[j][0];
+      acc += bf_hi(u.x) * xv.v[j][1];
+      acc += bf_lo(u.y) * xv.v[j][2];
+      acc += bf_hi(u.y) * xv.v[j][3];
+      acc += bf_lo(u.z) * xv.v[j][4];
+      acc += bf_hi(u.z) * xv.v[j][5];
+      acc += bf_lo(u.w) * xv.v[j][6];
+      acc += bf_hi(u.w) * xv.v[j][7];
+    }
+    out[i] = acc;
+  }
+  out[R] = extra;
+  wave_sum_n<R + 1>(out);
+}
+
+// RMSNorm folded into R row dot products (model.py:94-98): the rows multiply sc * h, the sum
+// of squares of h is reduced in the same chain, and the outputs are scaled by
+// 1 / sqrt(mean(h^2) + eps) afterwards, so the dot products do not wait for the norm.
+template <int NL, int R>
+__device__ __forceinline__ void normed_dots(const uint8_t* const (&rows)[R], const XV<NL>& h, const XV<NL>& sc, int k,
+                                            int lane, float (&out)[R]) {
+  XV<NL> x;
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < NL; ++j)
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      ss += h.v[j][q] * h.v[j][q];
+      x.v[j][q] = sc.v[j][q] * h.v[j][q];
+    }
+  float t[R + 1];
+  dot_rows_x<NL, R>(rows, x, k, lane, ss, t);
+  const float inv = 1.f / sqrtf(t[R] / float(k) + 1e-5f);
+#pragma unroll
+  for (int i = 0; i < R; ++i) out[i] = t[i] * inv;
 }
 
 __device__ __forceinline__ void split(int total, int parts, int idx, int& lo, int& hi) {
@@ -788,8 +855,6 @@ __device__ void row_worker(const Args& a, const RowCtx& c, int token) {
       weights(jb + 4 * l);
       MSD_TRACE_POINT(wv == 0, l, 16);
       {
-        XV<NLD> xv;
-        norm(xv);
         MSD_TRACE_POINT(wv == 0, l, 11);
         const uint8_t* rows[2 * QPW];
 #pragma unroll
@@ -798,7 +863,8 @@ __device__ void row_worker(const Args& a, const RowCtx& c, int token) {
           rows[2 * i + 1] = rows[2 * i] + D * 2;
         }
         float sd[2 * QPW] = {};
-        if (count(nq, QPW) > 0) dot_rows<NLD, 2 * QPW>(rows, xv, D, lane, sd);   // idle waves leave the SIMD to others
+        // idle waves leave the SIMD to others
+        if (count(nq, QPW) > 0) normed_dots<NLD, 2 * QPW>(rows, h, sc, D, lane, sd);
         MSD_TRACE_POINT(wv == 0, l, 14);
         release();
         float y[2 * QPW];
@@ -821,27 +887,35 @@ __device__ void row_worker(const Args& a, const RowCtx& c, int token) {
             ix[2 * i] = head * kDh + rr;
             ix[2 * i + 1] = ix[2 * i] + 1;
           }
-          if (rel < nq && head >= a.H && lane == 0) {  // K (post-RoPE) or V row of the cache at pos, bf16 (multi_sm_decode.py:179-180)
-            const bool isv = head >= a.H + a.KV;
-            const int kvh = isv ? head - a.H - a.KV : head - a.H;
-            uint16_t* cp = (isv ? vcache : kcache) + (int64_t(kvh) * a.ctx + pos) * kDh;
-            if constexpr (MULTI) {
-              // agent-scope stores write through to memory: a later step of the same launch
-              // reads the row from another workgroup (on another XCD) without a cache flush
-              __hip_atomic_store(cp + (ix[2 * i] - head * kDh), f2bf(y[2 * i]), __ATOMIC_RELAXED,
-                                 __HIP_MEMORY_SCOPE_AGENT);
-              __hip_atomic_store(cp + (ix[2 * i + 1] - head * kDh), f2bf(y[2 * i + 1]), __ATOMIC_RELAXED,
-                                 __HIP_MEMORY_SCOPE_AGENT);
-            } else {   // read by later launches only (the launch boundary orders them)
-              cp[ix[2 * i] - head * kDh] = f2bf(y[2 * i]);
-              cp[ix[2 * i + 1] - head * kDh] = f2bf(y[2 * i + 1]);
+        }
+        store_out<2 * QPW>(X + lay.x_qkv, y, ix, 2 * count(nq, QPW), false, lay.x_rep, tag, lane);
+        {
+          // K (post-RoPE) and V rows of the cache at pos, bf16 (multi_sm_decode.py:179-180), after
+          // the exchange stores: the attention workgroups wait for k and v, not for the cache
+#pragma unroll
+          for (int i = 0; i < QPW; ++i) {
+            const int rel = wv + kWavesR * i;
+            const int row = 2 * (c.qp0 + (rel < nq ? rel : 0));
+            const int head = row / kDh;
+            if (rel < nq && head >= a.H && lane == 0) {
+              const bool isv = head >= a.H + a.KV;
+              const int kvh = isv ? head - a.H - a.KV : head - a.H;
+              uint16_t* cp = (isv ? vcache : kcache) + (int64_t(kvh) * a.ctx + pos) * kDh;
+              if constexpr (MULTI) {
+                __hip_atomic_store(cp + (ix[2 * i] - head * kDh), f2bf(y[2 * i]), __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(cp + (ix[2 * i + 1] - head * kDh), f2bf(y[2 * i + 1]), __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+              } else {
+                cp[ix[2 * i] - head * kDh] = f2bf(y[2 * i]);
+                cp[ix[2 * i + 1] - head * kDh] = f2bf(y[2 * i + 1]);
+              }
             }
           }
         }
-        store_out<2 * QPW>(X + lay.x_qkv, y, ix, 2 * count(nq, QPW), false, lay.x_rep, tag, lane);
       }
       load_vec(sc, layer_w(a, l) + lay.off_ln2);   // scale of the next norm
-      bar();   // every QKV output of this workgroup is issued
+      if constexpr (kStoreBar) bar();   // every QKV output of this workgroup is issued
       MSD_TRACE_POINT(wv == 0, l, 17);
       // ---- attention vector (multi_sm_decode.py:243-259): with one split the attention
       //      workgroups publish each head's normalised output, gathered straight into xatt;
@@ -893,7 +967,7 @@ __device__ void row_worker(const Args& a, const RowCtx& c, int token) {
         release();
         store_out<ORW>(X, y, ix, count(no, ORW), true, lay.x_rep, tag, lane);
       }
-      bar();
+      if constexpr (kStoreBar) bar();
       MSD_TRACE_POINT(wv == 0, l, 19);
       // ---- h += O output; x = rmsnorm2(h); gate/up rows + SwiGLU (multi_sm_decode.py:262-289, model.py:159)
       gather_x<kWavesR, HPW, 0, kFirstPoll, D>(X + lay.x_hd1 + myrep, D, c.xhd1, tag, a.ctrl, wv, lane, bad);
@@ -904,8 +978,6 @@ __device__ void row_worker(const Args& a, const RowCtx& c, int token) {
       MSD_TRACE_POINT(wv == 0, l, 20);
       MSD_TRACE_WAVE(l, 0);
       {
-        XV<NLD> xv;
-        norm(xv);
         MSD_TRACE_POINT(wv == 0, l, 8);
         MSD_TRACE_WAVE(l, 1);
         const uint8_t* rows[2 * GPW];
@@ -917,7 +989,7 @@ __device__ void row_worker(const Args& a, const RowCtx& c, int token) {
           ix[i] = int(lay.x_act) + c.f0 + wv + kWavesR * i;
         }
         float gu[2 * GPW] = {};
-        if (count(ng, GPW) > 0) dot_rows<NLD, 2 * GPW>(rows, xv, D, lane, gu);
+        if (count(ng, GPW) > 0) normed_dots<NLD, 2 * GPW>(rows, h, sc, D, lane, gu);
         MSD_TRACE_POINT(wv == 0, l, 9);
         MSD_TRACE_WAVE(l, 2);
         release();
@@ -931,7 +1003,7 @@ __device__ void row_worker(const Args& a, const RowCtx& c, int token) {
         MSD_TRACE_POINT(wv == 0, l, 10);
         MSD_TRACE_WAVE(l, 3);
       }
-      bar();
+      if constexpr (kStoreBar) bar();
       MSD_TRACE_WAVE(l, 4);
       MSD_TRACE_POINT(wv == 0, l, 21);
       // ---- act -> LDS; down rows (multi_sm_decode.py:273-291)
@@ -957,7 +1029,7 @@ __device__ void row_worker(const Args& a, const RowCtx& c, int token) {
         store_out<ORW>(X, y, ix, count(no, ORW), true, lay.x_rep, tag, lane);
       }
       load_vec(sc, l + 1 < a.L ? layer_w(a, l + 1) + lay.off_ln1 : a.lnf);   // scale of the next norm
-      bar();
+      if constexpr (kStoreBar) bar();
       MSD_TRACE_POINT(wv == 0, l, 23);
     }
     // ---- h += last down output; x = final rmsnorm(h); tied logits over this workgroup's
@@ -1208,6 +1280,12 @@ __device__ void att_waves(const Args& a, const AttCtx& c) {
     lds_wait(c.ctr + 1, gl + 1, a.ctrl);   // cached rows of layer l are in LDS
     MSD_TRACE_POINT(wv == 0, l, 25);
     MSD_TRACE_WAVE(l, 1);
+    // a second load of k and v issued before the block work, consumed after the scores
+    uint64_t kvx[2] = {0, 0};
+    if (c.has_cur) {
+      kvx[0] = ld_tag(kvsrc[0]);
+      kvx[1] = ld_tag(kvsrc[1]);
+    }
     // block of this wave: tiles [t0, t1) of 16 cached positions, the tiles split evenly over
     // the waves (at most 4 each: ncached <= 512); waves w and w + 4 share a SIMD, and the
     // even split keeps every SIMD's tile count within one of the others'
@@ -1266,7 +1344,10 @@ __device__ void att_waves(const Args& a, const AttCtx& c) {
       // rarely needs another round trip
 #pragma unroll
       for (int i = 0; i < 2; ++i)
-        if (uint32_t(kvw[i] >> 32) != tag) kvw[i] = ld_tag(kvsrc[i]);
+        if (uint32_t(kvw[i] >> 32) != tag) {
+          if (uint32_t(kvx[i] >> 32) == tag) kvw[i] = kvx[i];
+          else kvw[i] = ld_tag(kvsrc[i]);
+        }
       __builtin_amdgcn_s_waitcnt(0xc07f);
       __builtin_amdgcn_wave_barrier();
       const int g = kb, dq = m16;
@@ -1406,7 +1487,7 @@ __global__ __launch_bounds__(kThreadsWG, 1) void decode_step_kernel(Args a) {
     if (threadIdx.x < 4) c.ctr[threadIdx.x] = 0;
     __syncthreads();   // the only workgroup barrier; the roles below meet on LDS counters
     if (wv == kLoader) att_loader<MULTI>(a, c);
-    else att_waves<MULTI>(a, c);
+    else if (wv < kWavesA) att_waves<MULTI>(a, c);
     return;
   }
 
@@ -1451,7 +1532,7 @@ __global__ __launch_bounds__(kThreadsWG, 1) void decode_step_kernel(Args a) {
   __syncthreads();   // the only workgroup barrier; the roles below meet on LDS counters
 
   if (wv == kLoader) row_loader<D, FF, MULTI>(a, c);
-  else row_worker<D, FF, QPW, ORW, GPW, MULTI>(a, c, token);
+  else if (wv < kWavesR) row_worker<D, FF, QPW, ORW, GPW, MULTI>(a, c, token);
 }
 
 // ---------------------------------------------------------------- host side
@@ -1467,12 +1548,28 @@ struct Plan {   // per-config launch parameters
 // d = 256, 512, 768, 1024) and the tiny benchmark configuration (d 256, d_ff 704); on 256
 // workgroups every one of them needs at most the listed rows per wave, with up to one KV head
 // per query head.
+#if MSD_ROW_WAVES >= 12
+#define MSD_SHAPES(X)        \
+  X(256, 704, 1, 1, 1)       \
+  X(256, 768, 1, 1, 1)       \
+  X(512, 1408, 1, 1, 1)      \
+  X(768, 2048, 1, 1, 1)      \
+  X(1024, 2816, 1, 1, 1)
+#elif MSD_ROW_WAVES >= 8
 #define MSD_SHAPES(X)        \
   X(256, 704, 1, 1, 1)       \
   X(256, 768, 1, 1, 1)       \
   X(512, 1408, 1, 1, 1)      \
   X(768, 2048, 1, 1, 2)      \
   X(1024, 2816, 1, 1, 2)
+#else
+#define MSD_SHAPES(X)        \
+  X(256, 704, 1, 1, 1)       \
+  X(256, 768, 1, 1, 1)       \
+  X(512, 1408, 1, 1, 2)      \
+  X(768, 2048, 1, 1, 3)      \
+  X(1024, 2816, 1, 2, 3)
+#endif
 
 struct Shape {
   int d, ff, qpw, orw, gpw;
