@@ -84,6 +84,24 @@ constexpr int kMaxCtx = 64 * kBlocks;
 constexpr int kLdsTotal = 160 * 1024;
 constexpr uint32_t kStTimeout = 1u, kStBadToken = 2u, kStBadPos = 4u;
 constexpr uint32_t kSpinLimit = 1u << 21;      // grid-barrier poll rounds (~1 s)
+// Replicas of every barrier flag: workgroup w polls replica w % kFlagReps, so the pollers of a
+// barrier spread over kFlagReps regions instead of meeting on one.
+#ifndef MBD_FLAG_REPS
+#define MBD_FLAG_REPS 8
+#endif
+constexpr int kFlagReps = MBD_FLAG_REPS;
+#ifndef MBD_BAR_SLEEP
+#define MBD_BAR_SLEEP 1
+#endif
+// s_sleep units between the polls of an LDS counter (0: spin)
+#ifndef MBD_LDS_SLEEP
+#define MBD_LDS_SLEEP 1
+#endif
+// the wave that polls the QKV barrier (the others request their first attention block meanwhile)
+#ifndef MBD_QKV_POLLER
+#define MBD_QKV_POLLER 6
+#endif
+constexpr int kQkvPoller = MBD_QKV_POLLER;
 constexpr uint32_t kLdsSpinLimit = 1u << 23;   // LDS-counter spins
 // control words (uint32 offsets in the control block)
 constexpr int kCtlEpoch = 0, kCtlStatus = 16;   // status slot k at kCtlStatus + 16 k
@@ -284,7 +302,7 @@ __device__ __forceinline__ int lds_ld(int* c) { return __hip_atomic_load(c, __AT
 __device__ __forceinline__ void lds_wait(int* c, int target, uint32_t* status) {
   uint32_t spins = 0;
   while (lds_ld(c) < target) {
-    __builtin_amdgcn_s_sleep(1);
+    if constexpr (MBD_LDS_SLEEP > 0) __builtin_amdgcn_s_sleep(MBD_LDS_SLEEP);
     if ((++spins & 1023u) == 0) {
       if (ld_u32(status) & kStTimeout) return;
       if (spins > kLdsSpinLimit) {
@@ -315,22 +333,24 @@ __device__ __forceinline__ void wsync(Sync& sy, int lane) {
 __device__ __forceinline__ void grid_arrive(const Args& a, Sync& sy, int b, uint32_t epoch, int wv, int lane) {
   __builtin_amdgcn_s_waitcnt(0);
   wsync(sy, lane);
-  if (wv == 0 && lane == 0) st_u32(a.flags + int64_t(b) * kMaxGrid + blockIdx.x, epoch);
+  if (wv == 0 && lane < kFlagReps) st_u32(a.flags + (int64_t(b) * kFlagReps + lane) * kMaxGrid + blockIdx.x, epoch);
 }
-__device__ __forceinline__ void grid_wait(const Args& a, Sync& sy, int b, uint32_t epoch, int wv, int lane) {
-  if (wv == 0) {
-    const uint32_t* f = a.flags + int64_t(b) * kMaxGrid;
+__device__ __forceinline__ void grid_wait(const Args& a, Sync& sy, int b, uint32_t epoch, int wv, int lane,
+                                          int poller = 0) {
+  if (wv == poller) {
+    const uint32_t* f = a.flags + (int64_t(b) * kFlagReps + blockIdx.x % kFlagReps) * kMaxGrid;
     const int G = gridDim.x, nk = (G + 63) / 64;
     uint32_t pend = 0;   // bit k: flag 64 k + lane not seen yet
     for (int k = 0; k < nk; ++k)
       if (64 * k + lane < G) pend |= 1u << k;
     uint32_t spins = 0;
     while (true) {
+      // only the flags not seen yet are read again (measured: fewer polls beat fewer round trips)
       for (int k = 0; k < nk; ++k)
         if ((pend >> k) & 1u)
           if (ld_u32(f + 64 * k + lane) == epoch) pend &= ~(1u << k);
       if (__all(pend == 0)) break;
-      __builtin_amdgcn_s_sleep(1);
+      if constexpr (MBD_BAR_SLEEP > 0) __builtin_amdgcn_s_sleep(MBD_BAR_SLEEP);
       if ((++spins & 255u) == 0 && (ld_u32(sy.status) & kStTimeout)) break;
       if (spins > kSpinLimit) {
         if (lane == 0) atomicOr(sy.status, kStTimeout);
@@ -851,9 +871,9 @@ __global__ __launch_bounds__(kThreads) void batch_step_kernel(Args a) {
         ++j;
       }
       grid_arrive(a, sy, bl, epoch, wv, lane);
-      // wave 0 polls; the others request their K/V block meanwhile (wave 0 after the barrier)
-      if (s_att.nitems > 0 && wv != 0 && 64 * wv <= s_att.it[0].p) att_load(a, l, s_att.it[0], wv, lane, pre);
-      grid_wait(a, sy, bl, epoch, wv, lane);
+      // one wave polls; the others request their K/V block meanwhile (the poller after the barrier)
+      if (s_att.nitems > 0 && wv != kQkvPoller && 64 * wv <= s_att.it[0].p) att_load(a, l, s_att.it[0], wv, lane, pre);
+      grid_wait(a, sy, bl, epoch, wv, lane, kQkvPoller);
       MBD_T(wv_ == 0, 40 + 5 * l + 0);
       MBD_T(wv_ == 0 && l == kTraceLayer, 5);
     }
@@ -862,7 +882,7 @@ __global__ __launch_bounds__(kThreads) void batch_step_kernel(Args a) {
       MBD_T(wv_ == 0 && l == kTraceLayer, 8);
       for (int n = 0; n < s_att.nitems; ++n) {
         const int lane = opaque(lane_), wv = opaque(wv_);
-        att_compute(a, l, s_att.it[n], pre, n == 0 && wv != 0, s_att, sy, wv, lane);
+        att_compute(a, l, s_att.it[n], pre, n == 0 && wv != kQkvPoller, s_att, sy, wv, lane);
       }
       MBD_T(wv_ == 0 && l == kTraceLayer, 12);
       grid_sync(a, sy, bl + 1, epoch, wv, lane);
@@ -1044,7 +1064,7 @@ static Region region(const msd_config* c) {
   int64_t o = 0;
   R.ctrl = o;  o += 256;
   R.keys = o;  o += 256;
-  R.flags = o; o += al256(int64_t(5 * c->n_layers + 2) * kMaxGrid * 4);
+  R.flags = o; o += al256(int64_t(5 * c->n_layers + 2) * kFlagReps * kMaxGrid * 4);
   R.x_layer = al256(x_block_floats(c->d_model, nqkv, c->d_ff) * 4) / 4;   // floats
   R.x = o;     o += R.x_layer * 4 * (c->n_layers + 1);
   R.bytes = o;
