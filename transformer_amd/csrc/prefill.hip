@@ -222,6 +222,72 @@ __global__ __launch_bounds__(256) void mx_gemm(GemmArgs g) {
       }
 }
 
+// C = A W^T for many rows (M >= 48): a workgroup owns 16 rows x 16 CT columns over the whole of K,
+// so it streams CT * 16 complete weight rows (contiguous in memory) and writes final outputs (no
+// split-K partials).  The four waves take interleaved 32-wide K steps (wave w: steps w, w + 4,
+// ...) with P steps of loads in flight, and add their tiles through LDS in wave order, so the
+// result is deterministic.  Tiles are dealt XCD-aware: every row tile of a column tile runs on
+// one XCD (workgroup b on XCD b mod 8), which then fetches that column tile's weights into its L2
+// once.
+template <int CT, int P>
+__global__ __launch_bounds__(256) void mx_gemm_rows(GemmArgs g) {
+  __shared__ f32x4 red[4][CT][64];
+  // wave-uniform wave index: the step count and its loop stay scalar (a per-lane loop would copy
+  // the accumulators out of and back into the AGPRs around every step)
+  const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int T = (g.M + 15) / 16, C = g.N / (16 * CT);
+  const int b = blockIdx.x, slot = b >> 3;
+  const int t = slot % T, c = (slot / T) * 8 + (b & 7);
+  if (c >= C) return;
+  const int m0 = 16 * t, n0 = 16 * CT * c;
+  const int r16 = lane & 15, kq = 8 * (lane >> 4);
+  // rows past M read row M - 1: an MFMA row only feeds its own output row, which is not stored
+  const uint16_t* ar = g.A + int64_t(min(m0 + r16, g.M - 1)) * g.lda + kq;
+  const uint16_t* wr = g.W + int64_t(n0 + r16) * g.K + kq;
+  const int S = g.K / kBK;
+  const int ns = (S - wv + 3) / 4;   // K steps of this wave (S >= 4: every wave has one)
+  f32x4 acc[CT];
+#pragma unroll
+  for (int ct = 0; ct < CT; ++ct) acc[ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+  uint4 a[P], al[P], w[P][CT];
+  // step i of this wave, clamped to its last: loads stay unconditional, so no wait lands at a
+  // branch join
+  auto load = [&](int p, int i) {
+    const int k = (wv + 4 * min(i, ns - 1)) * kBK;
+    a[p] = *reinterpret_cast<const uint4*>(ar + k);
+    al[p] = *reinterpret_cast<const uint4*>(ar + g.a_plane + k);
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) w[p][ct] = *reinterpret_cast<const uint4*>(wr + int64_t(16 * ct) * g.K + k);
+  };
+#pragma unroll
+  for (int p = 0; p < P; ++p) load(p, p);
+  // every round runs all P steps (a step past the end multiplies a zero A fragment), so the
+  // accumulators stay in the AGPRs across the loop
+  for (int i0 = 0; i0 < ns; i0 += P) {
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      const bool live = i0 + p < ns;
+      const uint4 x = live ? a[p] : make_uint4(0, 0, 0, 0), xl = live ? al[p] : make_uint4(0, 0, 0, 0);
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) {
+        acc[ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(x), as_bf16x8(w[p][ct]), acc[ct], 0, 0, 0);
+        acc[ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(xl), as_bf16x8(w[p][ct]), acc[ct], 0, 0, 0);
+      }
+      load(p, i0 + p + P);
+    }
+  }
+#pragma unroll
+  for (int ct = 0; ct < CT; ++ct) red[wv][ct][lane] = acc[ct];
+  __syncthreads();
+  // D layout of a 16 x 16 tile: lane holds rows 4 (lane / 16) + r of column lane % 16
+  for (int idx = threadIdx.x; idx < CT * 256; idx += 256) {
+    const int ct = idx >> 8, e = idx & 255, r = e >> 6, l = e & 63;
+    const float v = ((red[0][ct][l][r] + red[1][ct][l][r]) + red[2][ct][l][r]) + red[3][ct][l][r];
+    const int row = m0 + 4 * (l >> 4) + r;
+    if (row < g.M) g.out[int64_t(row) * g.ldo + n0 + 16 * ct + (l & 15)] = v;
+  }
+}
+
 __device__ __forceinline__ float block_sum256(float v, float* red) {
   v = wave_sum(v);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
@@ -237,7 +303,7 @@ __device__ __forceinline__ float block_sum256(float v, float* red) {
 // the first is added, so the sum costs one memory round trip.
 __global__ __launch_bounds__(kNormThreads) void mx_norm(float* h, const float* part, int splits, int M, int d,
                                                         const uint16_t* scale, uint16_t* xn, int64_t plane,
-                                                        int row0) {
+                                                        int row0, int ldx) {
   constexpr int NE = kMaxRows / kNormThreads;
   __shared__ float red[4];
   __shared__ __align__(16) float hs[kMaxRows];
@@ -278,7 +344,7 @@ __global__ __launch_bounds__(kNormThreads) void mx_norm(float* h, const float* p
 #pragma unroll
   for (int q = 0; q < NE; ++q) {
     const int j = threadIdx.x + kNormThreads * q;
-    if (j < d) put_split(xn + int64_t(blockIdx.x) * d + j, plane, bf2f(sc[q]) * (hs[perm_elem(j, d)] / r));
+    if (j < d) put_split(xn + int64_t(blockIdx.x) * ldx + j, plane, bf2f(sc[q]) * (hs[perm_elem(j, d)] / r));
   }
 }
 
@@ -356,7 +422,7 @@ __global__ __launch_bounds__(256) void mx_qkv_fin(const float* part, int splits,
 // Row blockIdx.x: act_f = silu(gate_f) * up_f over the summed partials (gate/up are the packed
 // rows 2f, 2f+1; model.py:159), as hi/lo bf16 parts at the down projection's input position of f.
 __global__ __launch_bounds__(256) void mx_swiglu_fin(const float* part, int splits, int M, int F, uint16_t* act,
-                                                     int64_t plane) {
+                                                     int64_t plane, int ldx) {
   const int m = blockIdx.x, f = 2 * (blockIdx.y * 256 + threadIdx.x);   // outputs f and f + 1 (F is even)
   if (f >= F) return;
   float4 pv[kMaxSplitK];
@@ -372,15 +438,15 @@ __global__ __launch_bounds__(256) void mx_swiglu_fin(const float* part, int spli
       g1 += pv[z].z;
       u1 += pv[z].w;
     }
-  put_split(act + int64_t(m) * F + perm_pos(f, F), plane, (g0 * (1.f / (1.f + expf(-g0)))) * u0);
-  put_split(act + int64_t(m) * F + perm_pos(f + 1, F), plane, (g1 * (1.f / (1.f + expf(-g1)))) * u1);
+  put_split(act + int64_t(m) * ldx + perm_pos(f, F), plane, (g0 * (1.f / (1.f + expf(-g0)))) * u0);
+  put_split(act + int64_t(m) * ldx + perm_pos(f + 1, F), plane, (g1 * (1.f / (1.f + expf(-g1)))) * u1);
 }
 
 // Prefill: causal GQA attention of query block blockIdx.y (16 rows) for head blockIdx.x.
 // Each wave owns 4 queries; key chunks of 64 rows go through LDS, with an online softmax per
 // query (scores: lane = key; output: lane = dimension).  Scale 1/sqrt(64) (model.py:98).
 __global__ __launch_bounds__(256) void mx_attention_prefill(const float* qkv, int M, int H, int KV, uint16_t* att,
-                                                            int64_t plane) {
+                                                            int64_t plane, int ldx) {
   __shared__ float sk[64 * kKStride];
   __shared__ float sv[64 * kDh];
   __shared__ float sq[kAttnQ * kDh];
@@ -470,7 +536,7 @@ __global__ __launch_bounds__(256) void mx_attention_prefill(const float* qkv, in
 #pragma unroll
   for (int t = 0; t < kQW; ++t) {
     const int i = q0 + kQW * wv + t;
-    if (i < M) put_split(att + int64_t(i) * d + perm_pos(h * kDh + lane, d), plane, o[t] / ls[t]);
+    if (i < M) put_split(att + int64_t(i) * ldx + perm_pos(h * kDh + lane, d), plane, o[t] / ls[t]);
   }
 }
 
@@ -485,7 +551,7 @@ constexpr int kAttnWaves = 8;
 
 __global__ __launch_bounds__(64 * kAttnWaves) void mx_attention_decode(const float* qkv, Rows rows, int H, int KV,
                                                                        const uint16_t* kc, const uint16_t* vc,
-                                                                       uint16_t* att, int64_t plane) {
+                                                                       uint16_t* att, int64_t plane, int ldx) {
   __shared__ float sq[kDh], skc[kDh], svc[kDh];   // q, and the current position's f32 k and v
   __shared__ float sp[kAttnWaves][64];
   __shared__ int srow[kAttnWaves][64];
@@ -569,7 +635,7 @@ __global__ __launch_bounds__(64 * kAttnWaves) void mx_attention_decode(const flo
       num += a * so[w][lane];
       den += a * sml[w][1];
     }
-    put_split(att + int64_t(m) * d + perm_pos(h * kDh + lane, d), plane, num / den);
+    put_split(att + int64_t(m) * ldx + perm_pos(h * kDh + lane, d), plane, num / den);
   }
 }
 
@@ -645,8 +711,31 @@ struct Layout {
 
 static size_t al256(size_t x) { return (x + 255) & ~size_t(255); }
 
-// K splits of a projection: enough workgroups to occupy every compute unit, at least 4 K steps each
+// Row stride of the bf16 activation planes the projections read: K plus 16 bytes.  Rows exactly
+// 2 KB (or any multiple of 128 bytes) apart put the 16 rows an MFMA fragment load touches at the
+// same offset on the same memory channel; the 16-byte skew spreads them (measured: the 128-row
+// prefill's four projections 55 -> 45 us per layer).
+static int act_ld(int K) { return K + 8; }
+
+// Widest projection mx_gemm_rows takes: wider ones (the 306M gate/up, 5632 outputs) run faster
+// on the split-K kernel (measured: 128-token prefill 1.95 -> 1.79 ms).
+constexpr int kRowsMaxN = 4096;
+
+// Column tiles (of 16) per workgroup of mx_gemm_rows: the widest that still gives about one
+// workgroup per compute unit; 0 when the projection has too few output tiles for it (few rows),
+// or too short a K for every wave to take a step, and the split-K kernel runs instead.
+static int rows_ct(int M, int N, int K) {
+  const int T = (M + 15) / 16, n16 = N / 16;
+  if (K / kBK < 4 || M < 48 || N > kRowsMaxN) return 0;
+  for (int ct : {8, 6, 4, 3, 2, 1})
+    if (n16 % ct == 0 && T * (n16 / ct) >= 224) return ct;
+  return 0;
+}
+
+// K splits of a projection: 1 for mx_gemm_rows, else enough split-K workgroups to occupy every
+// compute unit, at least 4 K steps each
 static int splits_for(int M, int N, int K, int bm) {
+  if (rows_ct(M, N, K) > 0) return 1;
   const int tiles = (N / kBN) * ((M + bm - 1) / bm);
   int s = 1;
   while (tiles * s < 256 && (K / kBK) / (2 * s) >= 4 && 2 * s <= kMaxSplitK) s *= 2;
@@ -671,10 +760,10 @@ static Layout layout(const msd_config* c, int M) {
   Layout L;
   size_t o = 0;
   L.h = o;      o += al256(size_t(M) * d * 4);
-  L.xn = o;     o += al256(size_t(M) * d * 2 * 2);    // hi and lo planes
+  L.xn = o;     o += al256(size_t(M) * act_ld(d) * 2 * 2);    // hi and lo planes
   L.qkv = o;    o += al256(size_t(M) * nqkv * 4);
-  L.att = o;    o += al256(size_t(M) * d * 2 * 2);
-  L.act = o;    o += al256(size_t(M) * ff * 2 * 2);
+  L.att = o;    o += al256(size_t(M) * act_ld(d) * 2 * 2);
+  L.act = o;    o += al256(size_t(M) * act_ld(ff) * 2 * 2);
   L.part = o;   o += al256(part_floats(c, M) * 4);
   L.status = o; o += 256;
   L.rowpos = o; o += al256(size_t(M) * 4);
@@ -693,9 +782,26 @@ static bool mx_config_ok(const msd_config* c) {
 
 // C = A W^T split over K: partials [splits][M][N] (pass ldo = N), or with splits == 1 rows
 // of stride ldo
+// rows_ok: mx_gemm_rows may run (single split only).  The tied logits pass false: one row and
+// every row then come from the same kernel and summation order, so the last row's logits are
+// bitwise the same either way.
 static hipError_t gemm(const uint16_t* A, int64_t a_plane, int lda, const uint16_t* W, int M, int N, int K, float* out,
-                       int ldo, int splits, hipStream_t s) {
+                       int ldo, int splits, hipStream_t s, bool rows_ok = true) {
   GemmArgs g{A, a_plane, W, out, M, N, K, lda, ldo, splits};
+  const int ct = splits == 1 && rows_ok ? rows_ct(M, N, K) : 0;
+  if (ct > 0) {
+    const int T = (M + 15) / 16, C = N / (16 * ct);
+    const dim3 grid(8 * ((C + 7) / 8) * T);
+    switch (ct) {
+      case 8: hipLaunchKernelGGL((mx_gemm_rows<8, 3>), grid, dim3(256), 0, s, g); break;
+      case 6: hipLaunchKernelGGL((mx_gemm_rows<6, 3>), grid, dim3(256), 0, s, g); break;
+      case 4: hipLaunchKernelGGL((mx_gemm_rows<4, 4>), grid, dim3(256), 0, s, g); break;
+      case 3: hipLaunchKernelGGL((mx_gemm_rows<3, 4>), grid, dim3(256), 0, s, g); break;
+      case 2: hipLaunchKernelGGL((mx_gemm_rows<2, 4>), grid, dim3(256), 0, s, g); break;
+      default: hipLaunchKernelGGL((mx_gemm_rows<1, 4>), grid, dim3(256), 0, s, g); break;
+    }
+    return hipGetLastError();
+  }
   const int bm = bm_for(M);
   const dim3 grid(N / kBN, (M + bm - 1) / bm, splits);
   if (bm == 16) hipLaunchKernelGGL((mx_gemm<1, 1>), grid, dim3(256), 0, s, g);
@@ -736,22 +842,23 @@ static int run_layers(const msd_config* cfg, const Weights& wt, const Rows& rows
     const uint16_t* Wl = wt.w + int64_t(l) * layer;
     uint16_t* kc = kv + int64_t(l) * 2 * KV * rows.pool * kDh;
     uint16_t* vc = kc + int64_t(KV) * rows.pool * kDh;
-    const int64_t pd = int64_t(M) * d, pf = int64_t(M) * ff;   // lo planes after the hi planes
-    hipLaunchKernelGGL(mx_norm, dim3(M), dim3(kNormThreads), 0, s, h, part, pending, M, d, Wl, xn, pd, 0);
-    if ((err = gemm(xn, pd, d, Wl + off_qkv, M, nqkv, d, part, nqkv, sq, s)) != hipSuccess) break;
+    const int ldd = act_ld(d), ldf = act_ld(ff);
+    const int64_t pd = int64_t(M) * ldd, pf = int64_t(M) * ldf;   // lo planes after the hi planes
+    hipLaunchKernelGGL(mx_norm, dim3(M), dim3(kNormThreads), 0, s, h, part, pending, M, d, Wl, xn, pd, 0, ldd);
+    if ((err = gemm(xn, pd, ldd, Wl + off_qkv, M, nqkv, d, part, nqkv, sq, s)) != hipSuccess) break;
     hipLaunchKernelGGL(mx_qkv_fin, dim3(M, (nqkv / 4 + 255) / 256), dim3(256), 0, s, part, sq, M, H, KV, wt.rope, rows,
                        kc, vc, qkv);
     if (prefill)
       hipLaunchKernelGGL(mx_attention_prefill, dim3(H, (M + kAttnQ - 1) / kAttnQ), dim3(256), 0, s, qkv, M, H, KV,
-                         att, pd);
+                         att, pd, ldd);
     else
       hipLaunchKernelGGL(mx_attention_decode, dim3(M, H), dim3(64 * kAttnWaves), 0, s, qkv, rows, H, KV, kc, vc, att,
-                         pd);
-    if ((err = gemm(att, pd, d, Wl + off_o, M, d, d, part, d, so, s)) != hipSuccess) break;
-    hipLaunchKernelGGL(mx_norm, dim3(M), dim3(kNormThreads), 0, s, h, part, so, M, d, Wl + off_ln2, xn, pd, 0);
-    if ((err = gemm(xn, pd, d, Wl + off_gu, M, 2 * ff, d, part, 2 * ff, sg, s)) != hipSuccess) break;
-    hipLaunchKernelGGL(mx_swiglu_fin, dim3(M, (ff / 2 + 255) / 256), dim3(256), 0, s, part, sg, M, ff, act, pf);
-    if ((err = gemm(act, pf, ff, Wl + off_dn, M, d, ff, part, d, sd, s)) != hipSuccess) break;
+                         pd, ldd);
+    if ((err = gemm(att, pd, ldd, Wl + off_o, M, d, d, part, d, so, s)) != hipSuccess) break;
+    hipLaunchKernelGGL(mx_norm, dim3(M), dim3(kNormThreads), 0, s, h, part, so, M, d, Wl + off_ln2, xn, pd, 0, ldd);
+    if ((err = gemm(xn, pd, ldd, Wl + off_gu, M, 2 * ff, d, part, 2 * ff, sg, s)) != hipSuccess) break;
+    hipLaunchKernelGGL(mx_swiglu_fin, dim3(M, (ff / 2 + 255) / 256), dim3(256), 0, s, part, sg, M, ff, act, pf, ldf);
+    if ((err = gemm(act, pf, ldf, Wl + off_dn, M, d, ff, part, d, sd, s)) != hipSuccess) break;
     pending = sd;
   }
   if (err == hipSuccess) err = hipGetLastError();
@@ -816,8 +923,9 @@ static int32_t prefill_impl(const msd_config* cfg, const Weights& wt, const int3
   // final norm of the rows whose logits are wanted, then the tied output projection
   const int r0 = logits_all ? 0 : M - 1, nr = M - r0;
   hipLaunchKernelGGL(mx_norm, dim3(nr), dim3(kNormThreads), 0, s, h, part, pending, M, d, wt.lnf, xn,
-                     int64_t(nr) * d, r0);
-  if (gemm(xn, int64_t(nr) * d, d, wt.outp, nr, V, d, logits_all ? logits_all : logits_last, V, 1, s) != hipSuccess)
+                     int64_t(nr) * d, r0, d);
+  if (gemm(xn, int64_t(nr) * d, d, wt.outp, nr, V, d, logits_all ? logits_all : logits_last, V, 1, s, false) !=
+      hipSuccess)
     return MSD_E_HIP;
   const float* last = logits_all ? logits_all + int64_t(M - 1) * V : logits_last;
   if (logits_all && last != logits_last &&
@@ -924,8 +1032,9 @@ extern "C" int32_t msd_batch_decode_step(const msd_config* cfg, const void* toke
   hipError_t err;
   const int pending = run_layers(cfg, wt, rows, static_cast<uint16_t*>(kv_pool), L, ws, false, s, err);
   if (err != hipSuccess) return MSD_E_HIP;
-  hipLaunchKernelGGL(mx_norm, dim3(M), dim3(kNormThreads), 0, s, h, part, pending, M, d, wt.lnf, xn, int64_t(M) * d, 0);
-  if (gemm(xn, int64_t(M) * d, d, wt.outp, M, V, d, logits, V, 1, s) != hipSuccess) return MSD_E_HIP;
+  hipLaunchKernelGGL(mx_norm, dim3(M), dim3(kNormThreads), 0, s, h, part, pending, M, d, wt.lnf, xn, int64_t(M) * d, 0,
+                     d);
+  if (gemm(xn, int64_t(M) * d, d, wt.outp, M, V, d, logits, V, 1, s, false) != hipSuccess) return MSD_E_HIP;
   hipLaunchKernelGGL(mx_argmax, dim3(M), dim3(1024), 0, s, logits, V, V, next_tokens, status);
   return hipGetLastError() == hipSuccess ? MSD_OK : MSD_E_HIP;
 }
