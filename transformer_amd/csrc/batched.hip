@@ -185,32 +185,35 @@ __device__ __forceinline__ void split(int total, int parts, int idx, int& lo, in
 }
 
 // Exchange block of layer l (block l + 1; block 0 holds the embedding rows as "layer -1"):
-//   qkv      f32 [kRows][nqkv]     raw q/k/v projections, packed row order
-//   att      bf16 [2][kRows][d]    attention output as hi/lo planes, packed input order of O
-//   act      bf16 [2][kRows][ff]   SwiGLU output as hi/lo planes, packed input order of down
-//   hop, hdp bf16 [2][kRows][d]    the residual stream after O times ln2 and after down times the
-//                                  next ln1 (or the final norm), hi/lo planes, packed input order
-//   sso, ssd f32 [kRows][d / 8]    sums of squares of those residuals over each group of 8 elements
-// (the f32 residual stream itself stays in the LDS of the workgroup that owns its elements)
+//   qkv      f32 [kRows][nqkv]        raw q/k/v projections, packed row order
+//   att      bf16 [2][kRows][ld(d)]   attention output as hi/lo planes, packed input order of O
+//   act      bf16 [2][kRows][ld(ff)]  SwiGLU output as hi/lo planes, packed input order of down
+//   hop, hdp bf16 [2][kRows][ld(d)]   the residual stream after O times ln2 and after down times
+//                                     the next ln1 (or the final norm), hi/lo planes, packed order
+//   sso, ssd f32 [kRows][d / 8]       sums of squares of those residuals over each group of 8
+// (the f32 residual stream itself stays in the LDS of the workgroup that owns its elements).
+// Plane rows are K + 8 elements apart: with rows a multiple of 128 bytes apart, the 8 sequences'
+// fragments an MFMA operand load touches sit at the same offset on one memory channel.
+__host__ __device__ __forceinline__ int plane_ld(int K) { return K + 8; }
 __device__ __forceinline__ float* x_blk(const Args& a, int l) { return a.x + int64_t(l + 1) * a.x_layer; }
 __device__ __forceinline__ float* x_qkv(const Args& a, int l) { return x_blk(a, l); }
 __device__ __forceinline__ uint16_t* x_att(const Args& a, int l) {
   return reinterpret_cast<uint16_t*>(x_qkv(a, l) + int64_t(kRows) * a.nqkv);
 }
 __device__ __forceinline__ uint16_t* x_act(const Args& a, int l) {
-  return reinterpret_cast<uint16_t*>(x_qkv(a, l) + int64_t(kRows) * a.nqkv + kRows * a.d);
+  return reinterpret_cast<uint16_t*>(x_qkv(a, l) + int64_t(kRows) * (a.nqkv + plane_ld(a.d)));
 }
 __device__ __forceinline__ uint16_t* x_hop(const Args& a, int l) {
-  return reinterpret_cast<uint16_t*>(x_qkv(a, l) + int64_t(kRows) * (a.nqkv + a.ff) + kRows * a.d);
+  return reinterpret_cast<uint16_t*>(x_qkv(a, l) + int64_t(kRows) * (a.nqkv + plane_ld(a.d) + plane_ld(a.ff)));
 }
-__device__ __forceinline__ uint16_t* x_hdp(const Args& a, int l) { return x_hop(a, l) + 2 * kRows * a.d; }
+__device__ __forceinline__ uint16_t* x_hdp(const Args& a, int l) { return x_hop(a, l) + 2 * kRows * plane_ld(a.d); }
 __device__ __forceinline__ float* x_sso(const Args& a, int l) {
-  return x_qkv(a, l) + int64_t(kRows) * (a.nqkv + a.ff) + 3 * kRows * a.d;
+  return x_qkv(a, l) + int64_t(kRows) * (a.nqkv + 3 * plane_ld(a.d) + plane_ld(a.ff));
 }
 __device__ __forceinline__ float* x_ssd(const Args& a, int l) { return x_sso(a, l) + a.d; }
 // floats of one exchange block
 __host__ __device__ __forceinline__ int64_t x_block_floats(int d, int nqkv, int ff) {
-  return int64_t(kRows) * (3 * d + nqkv + ff) + 2 * d;
+  return int64_t(kRows) * (3 * plane_ld(d) + nqkv + plane_ld(ff)) + 2 * d;
 }
 
 __device__ __forceinline__ uint32_t ld_u32(const uint32_t* p) {
@@ -769,7 +772,8 @@ __device__ __forceinline__ void att_compute(const Args& a, int l, const Item& it
       num += f * S.o[b][lane];
       den += f * S.ml[b][1];
     }
-    st_split(x_att(a, l) + int64_t(m) * a.d + perm_pos(h * kDh + lane, a.d), int64_t(kRows) * a.d, num / den);
+    st_split(x_att(a, l) + int64_t(m) * plane_ld(a.d) + perm_pos(h * kDh + lane, a.d), int64_t(kRows) * plane_ld(a.d),
+             num / den);
   }
   wsync(sy, lane);   // the LDS state is reused by the next item
 }
@@ -782,8 +786,8 @@ __device__ __forceinline__ void att_compute(const Args& a, int l, const Item& it
 // lane has an element.
 __device__ __forceinline__ void put_residual(const Args& a, bool act, int m, int grp, int e, float h1,
                                              uint16_t* planes, float* ss, float scale, int n) {
-  const int64_t o = int64_t(m) * a.d + perm_pos(e, a.d);
-  if (act) st_split(planes + o, int64_t(kRows) * a.d, h1 * scale);
+  const int64_t o = int64_t(m) * plane_ld(a.d) + perm_pos(e, a.d);
+  if (act) st_split(planes + o, int64_t(kRows) * plane_ld(a.d), h1 * scale);
   float v = act ? h1 * h1 : 0.f;
   v += __shfl_xor(v, 1);
   v += __shfl_xor(v, 2);
@@ -851,7 +855,7 @@ __global__ __launch_bounds__(kThreads) void batch_step_kernel(Args a) {
       if (jb.ng > 0) {
         const int lane = opaque(lane_), wv = opaque(wv_);
         split(a.d / 32, kWorkers, wv, s0, s1);
-        load_parts(x_hdp(a, l - 1), a.d, s0, s1 - s0, lane, A);
+        load_parts(x_hdp(a, l - 1), plane_ld(a.d), s0, s1 - s0, lane, A);
         if (wv == 0) row_inv(x_ssd(a, l - 1), a.d, s_inv, lane);
         MBD_T(wv == 0 && l == kTraceLayer, 1);
         int tiles;
@@ -896,7 +900,7 @@ __global__ __launch_bounds__(kThreads) void batch_step_kernel(Args a) {
       if (jb.ng > 0) {
         const int lane = opaque(lane_), wv = opaque(wv_);
         split(a.d / 32, kWorkers, wv, s0, s1);
-        load_parts(x_att(a, l), a.d, s0, s1 - s0, lane, A);
+        load_parts(x_att(a, l), plane_ld(a.d), s0, s1 - s0, lane, A);
         // the next norm's scale of this thread's epilogue element (one per thread: 2 tiles at most)
         const int i0 = wv * 64 + lane, gi0 = 2 * (i0 >> 7) + ((i0 & 15) >> 3);
         const float sc = bf2f(wl[a.off_ln2 + 8 * (jb.g0 + min(gi0, jb.ng - 1)) + (i0 & 7)]);
@@ -931,7 +935,7 @@ __global__ __launch_bounds__(kThreads) void batch_step_kernel(Args a) {
       if (jb.ng > 0) {
         const int lane = opaque(lane_), wv = opaque(wv_);
         split(a.d / 32, kWorkers, wv, s0, s1);
-        load_parts(x_hop(a, l), a.d, s0, s1 - s0, lane, A);
+        load_parts(x_hop(a, l), plane_ld(a.d), s0, s1 - s0, lane, A);
         if (wv == 0) row_inv(x_sso(a, l), a.d, s_inv, lane);
         MBD_T(wv == 0 && l == kTraceLayer, 25);
         int tiles;
@@ -943,7 +947,7 @@ __global__ __launch_bounds__(kThreads) void batch_step_kernel(Args a) {
           if (2 * t + (n >> 3) < jb.ng && m < M) {
             const float gt = tile_out(red, tiles, t, m, n) * s_inv[m], up = tile_out(red, tiles, t, m, n + 1) * s_inv[m];
             const int f = (8 * (jb.g0 + 2 * t + (n >> 3)) + (n & 7)) >> 1;
-            st_split(x_act(a, l) + int64_t(m) * a.ff + perm_pos(f, a.ff), int64_t(kRows) * a.ff,
+            st_split(x_act(a, l) + int64_t(m) * plane_ld(a.ff) + perm_pos(f, a.ff), int64_t(kRows) * plane_ld(a.ff),
                      (gt * (1.f / (1.f + expf(-gt)))) * up);
           }
         }
@@ -963,7 +967,7 @@ __global__ __launch_bounds__(kThreads) void batch_step_kernel(Args a) {
         const int lane = opaque(lane_), wv = opaque(wv_);
         split(a.ff / 32, kWorkers, wv, s0, s1);
         AOp<kStepsF> Af;
-        load_parts(x_act(a, l), a.ff, s0, s1 - s0, lane, Af);
+        load_parts(x_act(a, l), plane_ld(a.ff), s0, s1 - s0, lane, Af);
         // the next RMSNorm's scale (the next layer's ln1, or the final norm) of this thread's
         // epilogue element (one per thread: 1 tile)
         const uint16_t* nsc = l + 1 < a.L ? wl + a.layer_elems : a.lnf;
@@ -1000,7 +1004,7 @@ __global__ __launch_bounds__(kThreads) void batch_step_kernel(Args a) {
   if (t1 > t0) {
     const int lane = opaque(lane_), wv = opaque(wv_);
     split(a.d / 32, kWorkers, wv, s0, s1);
-    load_parts(x_hdp(a, a.L - 1), a.d, s0, s1 - s0, lane, A);
+    load_parts(x_hdp(a, a.L - 1), plane_ld(a.d), s0, s1 - s0, lane, A);
     if (wv == 0) row_inv(x_ssd(a, a.L - 1), a.d, s_inv, lane);
     const int m = ((wv * 64 + lane) >> 4) & 7;   // the same sequence for every output of this thread
     uint64_t best = 0;
