@@ -21,6 +21,10 @@
  *                            generate.py:70-90 (_prefill)
  *   msd_prefill_workspace_bytes
  *                         <- the activations XLA allocates for prefill_with_kv
+ *   msd_tiles_bytes, msd_pack_tiles
+ *                         <- no counterpart in the reference (its XLA prefill reads the f32
+ *                            parameter arrays of model.py:194-231 as they are): a second copy
+ *                            of the projection weights in matrix-core operand order
  *   msd_prefill_paged, msd_batch_decode_step, msd_batch_workspace_bytes
  *                         <- the batched decode over a paged KV cache that the reference
  *                            describes (PagePool with in-kernel page tables, batched decode
@@ -189,6 +193,21 @@ int32_t msd_sample_token_noalloc(const float* logits, int32_t vocab, double temp
 /* Bytes of device workspace msd_prefill needs for a prompt of n_tokens tokens. */
 int64_t msd_prefill_workspace_bytes(const msd_config* cfg, int32_t n_tokens);
 
+/* Bytes of the tile copy of the layer weights (the QKV, O, gate/up and down matrices of every
+ * layer: the same bf16 values as packed_w's projection rows, 2 bytes each). */
+int64_t msd_tiles_bytes(const msd_config* cfg);
+
+/* Writes the tile copy of packed_w's projection matrices to `tiles` (msd_tiles_bytes bytes,
+ * 16-byte aligned, device memory): every N x K matrix as 16-row x 32-column tiles of 1 KB in
+ * matrix-core operand order (lane l of tile (n / 16, k / 32) holds row 16 (n / 16) + l % 16,
+ * columns 32 (k / 32) + 8 (l / 16) .. + 8), tile (n / 16, k / 32) at ((n / 16) (K / 32) +
+ * k / 32) * 512 elements, layer after layer.  The multi-row passes (msd_prefill, msd_prefill_paged,
+ * msd_verify and the multi-kernel pass of msd_batch_decode_step) read their projection weights
+ * from it when it is given: a fragment load is then one 1 KB piece instead of 16 row segments
+ * (128-token prefill of the 306M model measured 1.79 -> 1.50 ms).  Rebuild it whenever packed_w
+ * changes. */
+int32_t msd_pack_tiles(const msd_config* cfg, const void* packed_w, void* tiles, void* stream);
+
 /* Forward pass over a prompt: tokens[0..n_tokens) at positions 0..n_tokens-1 (device int32).
  * Writes the KV cache rows 0..n_tokens-1 of every layer (bf16, post-RoPE K) and the f32
  * logits of the last position; with logits_all != NULL also the logits of every position
@@ -197,10 +216,11 @@ int64_t msd_prefill_workspace_bytes(const msd_config* cfg, int32_t n_tokens);
  * of range).  Every projection runs on the matrix cores with its f32 input split into two bf16
  * parts (hi = bf16(x), lo = bf16(x - hi): x to about 2^-17 relative) against the bf16 weights,
  * accumulated in f32; residual stream, RoPE, softmax and SwiGLU are f32 (model.py's maths).
- * Weight arguments as for msd_decode_step.  Requires d_model, 2*d_ff and vocab_size to be
- * multiples of 64, d_ff a multiple of 32 and n_tokens <= context_len. */
+ * Weight arguments as for msd_decode_step; `tiles` is the tile copy of packed_w (msd_pack_tiles)
+ * or NULL (the projections then read packed_w's rows: same results, slower).  Requires d_model,
+ * 2*d_ff and vocab_size to be multiples of 64, d_ff a multiple of 32 and n_tokens <= context_len. */
 int32_t msd_prefill(const msd_config* cfg, const void* token_emb, const void* output_proj,
-                    const void* packed_w, const void* lnf_s, const float* rope,
+                    const void* packed_w, const void* tiles, const void* lnf_s, const float* rope,
                     const int32_t* tokens, int32_t n_tokens, void* kv, void* workspace,
                     float* logits_last, float* logits_all, int32_t* next_token, void* stream);
 
@@ -215,15 +235,15 @@ int64_t msd_verify_workspace_bytes(const msd_config* cfg, int32_t n_tokens);
  * sequential decode steps would give once tokens 0..i-1 are accepted.  Writes the K/V rows of
  * every position, the f32 logits of every row (n_tokens x vocab_size) and argmax[2i] = the
  * argmax of row i (lowest index on ties), argmax[2i+1] = status (bit 1 = a token id out of
- * range).  Numerics of msd_prefill (projection inputs as hi/lo bf16 parts).  Requires
- * start_pos >= 1, start_pos + n_tokens <= context_len <= 512.
+ * range).  Numerics of msd_prefill (projection inputs as hi/lo bf16 parts); `tiles` as there.
+ * Requires start_pos >= 1, start_pos + n_tokens <= context_len <= 512.
  * Replaces the parallel verification kernel the reference describes (K draft tokens through the
  * full target in one call, a mini-prefill with an existing KV cache: knowledge/program.md:
  * 147-155; no code of it is in the reference snapshot, so the interface is this library's own). */
 int32_t msd_verify(const msd_config* cfg, const void* token_emb, const void* output_proj,
-                   const void* packed_w, const void* lnf_s, const float* rope, const int32_t* tokens,
-                   int32_t n_tokens, int32_t start_pos, void* kv, void* workspace, float* logits,
-                   int32_t* argmax, void* stream);
+                   const void* packed_w, const void* tiles, const void* lnf_s, const float* rope,
+                   const int32_t* tokens, int32_t n_tokens, int32_t start_pos, void* kv, void* workspace,
+                   float* logits, int32_t* argmax, void* stream);
 
 /* Paged KV cache (used by msd_prefill_paged and msd_batch_decode_step): a pool of pages of 16
  * positions, bf16, laid out [layer][K, V][kv_head][pool_pages * 16][d_head].  A sequence's
@@ -235,7 +255,7 @@ int32_t msd_verify(const msd_config* cfg, const void* token_emb, const void* out
 /* msd_prefill into a paged cache: page_table is a device int32 array of max_pages entries
  * (max_pages * 16 >= n_tokens, max_pages <= ceil(context_len / 16)) for this sequence. */
 int32_t msd_prefill_paged(const msd_config* cfg, const void* token_emb, const void* output_proj,
-                          const void* packed_w, const void* lnf_s, const float* rope,
+                          const void* packed_w, const void* tiles, const void* lnf_s, const float* rope,
                           const int32_t* tokens, int32_t n_tokens, const int32_t* page_table,
                           int32_t max_pages, void* kv_pool, int32_t pool_pages, void* workspace,
                           float* logits_last, int32_t* next_token, void* stream);
@@ -256,9 +276,9 @@ int64_t msd_batch_workspace_bytes(const msd_config* cfg, int32_t batch);
  * current position attends with its un-rounded K/V.  Up to 8 sequences run as ONE persistent
  * launch (one workgroup per compute unit, all resident, grid barriers between the phases of a
  * layer); larger batches, or a device that cannot hold the grid resident, take the multi-kernel
- * matrix-core pass. */
+ * matrix-core pass, which reads `tiles` (as for msd_prefill; NULL allowed). */
 int32_t msd_batch_decode_step(const msd_config* cfg, const void* token_emb, const void* output_proj,
-                              const void* packed_w, const void* lnf_s, const float* rope,
+                              const void* packed_w, const void* tiles, const void* lnf_s, const float* rope,
                               const int32_t* tokens, const int32_t* positions, int32_t batch,
                               const int32_t* page_tables, int32_t max_pages, void* kv_pool,
                               int32_t pool_pages, void* workspace, float* logits,

@@ -11,7 +11,7 @@ import torch
 from oracle import model as om
 from transformer_amd.configs import M306, TINY
 from transformer_amd.fused_decode_nlayer import (new_kv_packed, prepare_decode_weights_nlayer,
-                                                 unpack_kv_caches)
+                                                 unpack_kv_caches, weight_tiles)
 from transformer_amd.multi_sm_decode import Decoder
 from transformer_amd.prefill import Prefiller, prefill_with_kv
 from transformer_amd.synthetic import make_params, make_prompt
@@ -34,9 +34,9 @@ def m306():
     return params, prepare_decode_weights_nlayer(params, M306)
 
 
-def _run(w, cfg, toks, all_logits=True):
+def _run(w, cfg, toks, all_logits=True, tiles=True):
     T = len(toks)
-    pf = Prefiller(w, cfg, max_tokens=T)
+    pf = Prefiller(w, cfg, max_tokens=T, tiles=tiles)
     kv = new_kv_packed(cfg).fill_(SENTINEL)
     la = torch.empty((T, cfg["vocab_size"]), dtype=torch.float32, device="cuda") if all_logits else None
     out = pf.launch(toks, kv, logits_all=la)
@@ -54,19 +54,43 @@ def _check_kv(kv, cfg, T, kc, vc):
         assert np.all(k[:, T:] == SENTINEL) and np.all(v[:, T:] == SENTINEL), "rows >= T were written"
 
 
+@pytest.mark.parametrize("tiles", [True, False], ids=["tiles", "rows"])
 @pytest.mark.parametrize("T", [1, 16, 77, 128])
-def test_tiny_prefill_matches_oracle(tiny, T):
+def test_tiny_prefill_matches_oracle(tiny, T, tiles):
+    """Both weight layouts: the tile copy (msd_pack_tiles) and the packed rows."""
     params, w = tiny
     toks = make_prompt(T, TINY["vocab_size"], seed=100 + T)
-    la, last, out, kv = _run(w, TINY, toks)
+    la, last, out, kv = _run(w, TINY, toks, tiles=tiles)
     ref, kc, vc = om.prefill_with_kv(params, TINY, toks)
     np.testing.assert_allclose(la, ref, atol=ATOL, rtol=RTOL)
     assert np.array_equal(last, la[-1])
     assert out[0] == int(np.argmax(la[-1])) and out[1] == 0
     _check_kv(kv, TINY, T, kc, vc)
     # the last-position-only path computes the same row bitwise
-    _, last2, out2, _ = _run(w, TINY, toks, all_logits=False)
+    _, last2, out2, _ = _run(w, TINY, toks, all_logits=False, tiles=tiles)
     assert np.array_equal(last2, last) and out2[0] == out[0]
+
+
+def test_pack_tiles_layout(tiny):
+    """msd_pack_tiles against a numpy re-tiling of every projection matrix of every layer: tile
+    (n / 16, k / 32) holds rows 16 (n / 16) .. + 16 x columns 32 (k / 32) .. + 32, lane
+    r + 16 q = row r, columns 8 q .. 8 q + 8."""
+    params, w = tiny
+    cfg = TINY
+    d, ff, L = cfg["d_model"], cfg["d_ff"], cfg["n_layers"]
+    nqkv = (cfg["n_heads"] + 2 * cfg["n_kv_heads"]) * cfg["d_head"]
+    got = weight_tiles(w, cfg).view(torch.int16).cpu().numpy()
+    packed = w["packed_w"].view(torch.int16).cpu().numpy()
+    layer = 2 * d + nqkv * d + d * d + 2 * ff * d + d * ff
+    want = []
+    for l in range(L):
+        off = l * layer + 2 * d
+        for N, K in ((nqkv, d), (d, d), (2 * ff, d), (d, ff)):
+            W = packed[off:off + N * K].reshape(N // 16, 16, K // 32, 4, 8)
+            want.append(W.transpose(0, 2, 3, 1, 4).reshape(-1))
+            off += N * K
+    want = np.concatenate(want)
+    assert got.shape == want.shape and np.array_equal(got, want)
 
 
 def test_306m_prefill_128_matches_oracle(m306):

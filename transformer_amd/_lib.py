@@ -25,7 +25,7 @@ EXPORTS = ("msd_packed_weight_elems", "msd_workspace_bytes", "msd_default_workgr
            "msd_prefill_workspace_bytes", "msd_prefill", "msd_prefill_paged", "msd_batch_workspace_bytes",
            "msd_batch_decode_step", "msd_workspace_acquire", "msd_workspace_release",
            "msd_sample_token_noalloc", "msd_verify_workspace_bytes", "msd_verify",
-           "msd_decode_steps")
+           "msd_decode_steps", "msd_tiles_bytes", "msd_pack_tiles")
 
 
 class MsdConfig(ctypes.Structure):
@@ -97,17 +97,21 @@ def lib():
     L.msd_sample_token_noalloc.restype = I32
     L.msd_prefill_workspace_bytes.argtypes = [CP, I32]
     L.msd_prefill_workspace_bytes.restype = I64
-    L.msd_prefill.argtypes = [CP, P, P, P, P, P, P, I32, P, P, P, P, P, P]
+    L.msd_tiles_bytes.argtypes = [CP]
+    L.msd_tiles_bytes.restype = I64
+    L.msd_pack_tiles.argtypes = [CP, P, P, P]
+    L.msd_pack_tiles.restype = I32
+    L.msd_prefill.argtypes = [CP, P, P, P, P, P, P, P, I32, P, P, P, P, P, P]
     L.msd_prefill.restype = I32
-    L.msd_prefill_paged.argtypes = [CP, P, P, P, P, P, P, I32, P, I32, P, I32, P, P, P, P]
+    L.msd_prefill_paged.argtypes = [CP, P, P, P, P, P, P, P, I32, P, I32, P, I32, P, P, P, P]
     L.msd_prefill_paged.restype = I32
     L.msd_batch_workspace_bytes.argtypes = [CP, I32]
     L.msd_batch_workspace_bytes.restype = I64
-    L.msd_batch_decode_step.argtypes = [CP, P, P, P, P, P, P, P, I32, P, I32, P, I32, P, P, P, P]
+    L.msd_batch_decode_step.argtypes = [CP, P, P, P, P, P, P, P, P, I32, P, I32, P, I32, P, P, P, P]
     L.msd_batch_decode_step.restype = I32
     L.msd_verify_workspace_bytes.argtypes = [CP, I32]
     L.msd_verify_workspace_bytes.restype = I64
-    L.msd_verify.argtypes = [CP, P, P, P, P, P, P, I32, I32, P, P, P, P, P]
+    L.msd_verify.argtypes = [CP, P, P, P, P, P, P, P, I32, I32, P, P, P, P, P]
     L.msd_verify.restype = I32
     _lib = L
     return L

@@ -122,6 +122,16 @@ __device__ __forceinline__ int perm_elem(int j, int K) {
   return (b << 9) + (o & 7) * m + (o >> 3);
 }
 
+// Element (m, j) of an activation plane with rows of K (j a packed position).  ldx > 0: rows
+// ldx apart.  ldx == 0: matrix-core tile order, the layout the projections read: 16 rows x 32
+// positions form a tile of 64 lanes x 16 bytes in MFMA operand order (row m % 16 and positions
+// 8 ((j % 32) / 8) .. + 8 in lane (m % 16) + 16 ((j % 32) / 8)), tile (m / 16, j / 32) at
+// ((m / 16) (K / 32) + j / 32) 512 elements, so a wave's operand load reads 1 KB in one piece.
+__device__ __forceinline__ int64_t act_index(int m, int j, int K, int ldx) {
+  if (ldx > 0) return int64_t(m) * ldx + j;
+  return ((int64_t(m >> 4) * (K >> 5) + (j >> 5)) * 64 + (m & 15) + 16 * ((j & 31) >> 3)) * 8 + (j & 7);
+}
+
 // Rows of a pass: row m is sequence seq(m) at position pos(m).
 struct Rows {
   int M;
@@ -140,17 +150,18 @@ __device__ __forceinline__ int64_t cache_row(const Rows& r, int m, int p) {
 }
 
 struct GemmArgs {
-  const uint16_t* A;   // [M][lda] bf16: the hi parts; the lo parts follow at A + a_plane
-  int64_t a_plane;
-  const uint16_t* W;   // [N][K] bf16
+  const uint16_t* A;   // [M][lda] bf16 (or tile order, see act_index): the hi parts; the lo
+  int64_t a_plane;     // parts follow at A + a_plane
+  const uint16_t* W;   // [N][K] bf16 (or tile order: tile (n / 16, k / 32) at ((n / 16) (K / 32) + k / 32) 512)
   float* out;          // partials [splits][M][N] f32, or [M][ldo] (single split)
   int M, N, K, lda, ldo, splits;
 };
 
 __device__ __forceinline__ bf16x8 as_bf16x8(uint4 u) { return __builtin_bit_cast(bf16x8, u); }
 
-// Four waves as WM x (4 / WM); a wave covers RB 16-row blocks and (WM) 16-column blocks.
-template <int RB, int WM>
+// Four waves as WM x (4 / WM); a wave covers RB 16-row blocks and (WM) 16-column blocks.  TA / TW:
+// the activations / weights in tile order (one 1 KB piece per operand load).
+template <int RB, int WM, bool TA, bool TW>
 __global__ __launch_bounds__(256) void mx_gemm(GemmArgs g) {
   constexpr int WN = 4 / WM, CB = 4 / WN, BM = 16 * RB * WM;
   constexpr int U = RB * CB <= 2 ? 8 : 4;   // K steps with loads in flight
@@ -161,17 +172,24 @@ __global__ __launch_bounds__(256) void mx_gemm(GemmArgs g) {
   const int c0 = (nchunks * int(blockIdx.z)) / g.splits, c1 = (nchunks * (int(blockIdx.z) + 1)) / g.splits;
   const int kq = 8 * (lane >> 4);   // this lane's 8-element K run within a 32 chunk
   const int r16 = lane & 15;
+  // operand pointers of chunk 0; chunk c is kstep(c) elements further
   const uint16_t* arow[RB];   // hi parts (the lo parts a_plane elements further)
   bool aval[RB];
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb) {
     const int m = m0 + 16 * rb + r16;
     aval[rb] = m < g.M;
-    arow[rb] = g.A + int64_t(aval[rb] ? m : 0) * g.lda + kq;
+    if constexpr (TA)   // tiles past the last one read the last (those rows are zeroed)
+      arow[rb] = g.A + (int64_t(min(m0 + 16 * rb, g.M - 1) >> 4) * nchunks * 64 + lane) * 8;
+    else
+      arow[rb] = g.A + int64_t(aval[rb] ? m : 0) * g.lda + kq;
   }
   const uint16_t* wrow[CB];
 #pragma unroll
-  for (int cb = 0; cb < CB; ++cb) wrow[cb] = g.W + int64_t(n0 + 16 * cb + r16) * g.K + kq;
+  for (int cb = 0; cb < CB; ++cb)
+    wrow[cb] = TW ? g.W + (int64_t((n0 + 16 * cb) >> 4) * nchunks * 64 + lane) * 8
+                  : g.W + int64_t(n0 + 16 * cb + r16) * g.K + kq;
+  auto kstep = [](int c, bool tiled) { return tiled ? int64_t(c) * 512 : int64_t(c) * kBK; };
   f32x4 acc[RB][CB];
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb)
@@ -193,16 +211,17 @@ __global__ __launch_bounds__(256) void mx_gemm(GemmArgs g) {
     uint4 a[U][RB], al[U][RB], w[U][CB];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int k = min(c + u, c1 - 1) * kBK;
+      const int ch = min(c + u, c1 - 1);
+      const int64_t ka = kstep(ch, TA), kw = kstep(ch, TW);
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb) {
-        const uint4 v = *reinterpret_cast<const uint4*>(arow[rb] + k);
-        const uint4 vl = *reinterpret_cast<const uint4*>(arow[rb] + g.a_plane + k);
+        const uint4 v = *reinterpret_cast<const uint4*>(arow[rb] + ka);
+        const uint4 vl = *reinterpret_cast<const uint4*>(arow[rb] + g.a_plane + ka);
         a[u][rb] = aval[rb] ? v : make_uint4(0, 0, 0, 0);
         al[u][rb] = aval[rb] ? vl : make_uint4(0, 0, 0, 0);
       }
 #pragma unroll
-      for (int cb = 0; cb < CB; ++cb) w[u][cb] = *reinterpret_cast<const uint4*>(wrow[cb] + k);
+      for (int cb = 0; cb < CB; ++cb) w[u][cb] = *reinterpret_cast<const uint4*>(wrow[cb] + kw);
     }
 #pragma unroll
     for (int u = 0; u < U; ++u)
@@ -228,8 +247,8 @@ __global__ __launch_bounds__(256) void mx_gemm(GemmArgs g) {
 // ...) with P steps of loads in flight, and add their tiles through LDS in wave order, so the
 // result is deterministic.  Tiles are dealt XCD-aware: every row tile of a column tile runs on
 // one XCD (workgroup b on XCD b mod 8), which then fetches that column tile's weights into its L2
-// once.
-template <int CT, int P>
+// once.  TA / TW as for mx_gemm.
+template <int CT, int P, bool TA, bool TW>
 __global__ __launch_bounds__(256) void mx_gemm_rows(GemmArgs g) {
   __shared__ f32x4 red[4][CT][64];
   // wave-uniform wave index: the step count and its loop stay scalar (a per-lane loop would copy
@@ -241,10 +260,14 @@ __global__ __launch_bounds__(256) void mx_gemm_rows(GemmArgs g) {
   if (c >= C) return;
   const int m0 = 16 * t, n0 = 16 * CT * c;
   const int r16 = lane & 15, kq = 8 * (lane >> 4);
-  // rows past M read row M - 1: an MFMA row only feeds its own output row, which is not stored
-  const uint16_t* ar = g.A + int64_t(min(m0 + r16, g.M - 1)) * g.lda + kq;
-  const uint16_t* wr = g.W + int64_t(n0 + r16) * g.K + kq;
   const int S = g.K / kBK;
+  // rows past M read row M - 1 (row layout) or whatever their tile holds: an MFMA row only
+  // feeds its own output row, which is not stored
+  const uint16_t* ar = TA ? g.A + (int64_t(t) * S * 64 + lane) * 8 : g.A + int64_t(min(m0 + r16, g.M - 1)) * g.lda + kq;
+  const uint16_t* wr = TW ? g.W + (int64_t(n0 >> 4) * S * 64 + lane) * 8 : g.W + int64_t(n0 + r16) * g.K + kq;
+  // element offsets of step ks and of column tile ct
+  const int64_t astep = TA ? 512 : kBK, wstep = TW ? 512 : kBK;
+  const int64_t wtile = TW ? int64_t(S) * 512 : int64_t(16) * g.K;
   const int ns = (S - wv + 3) / 4;   // K steps of this wave (S >= 4: every wave has one)
   f32x4 acc[CT];
 #pragma unroll
@@ -253,11 +276,11 @@ __global__ __launch_bounds__(256) void mx_gemm_rows(GemmArgs g) {
   // step i of this wave, clamped to its last: loads stay unconditional, so no wait lands at a
   // branch join
   auto load = [&](int p, int i) {
-    const int k = (wv + 4 * min(i, ns - 1)) * kBK;
-    a[p] = *reinterpret_cast<const uint4*>(ar + k);
-    al[p] = *reinterpret_cast<const uint4*>(ar + g.a_plane + k);
+    const int ks = wv + 4 * min(i, ns - 1);
+    a[p] = *reinterpret_cast<const uint4*>(ar + ks * astep);
+    al[p] = *reinterpret_cast<const uint4*>(ar + g.a_plane + ks * astep);
 #pragma unroll
-    for (int ct = 0; ct < CT; ++ct) w[p][ct] = *reinterpret_cast<const uint4*>(wr + int64_t(16 * ct) * g.K + k);
+    for (int ct = 0; ct < CT; ++ct) w[p][ct] = *reinterpret_cast<const uint4*>(wr + ct * wtile + ks * wstep);
   };
 #pragma unroll
   for (int p = 0; p < P; ++p) load(p, p);
@@ -344,7 +367,7 @@ __global__ __launch_bounds__(kNormThreads) void mx_norm(float* h, const float* p
 #pragma unroll
   for (int q = 0; q < NE; ++q) {
     const int j = threadIdx.x + kNormThreads * q;
-    if (j < d) put_split(xn + int64_t(blockIdx.x) * ldx + j, plane, bf2f(sc[q]) * (hs[perm_elem(j, d)] / r));
+    if (j < d) put_split(xn + act_index(blockIdx.x, j, d, ldx), plane, bf2f(sc[q]) * (hs[perm_elem(j, d)] / r));
   }
 }
 
@@ -438,8 +461,8 @@ __global__ __launch_bounds__(256) void mx_swiglu_fin(const float* part, int spli
       g1 += pv[z].z;
       u1 += pv[z].w;
     }
-  put_split(act + int64_t(m) * ldx + perm_pos(f, F), plane, (g0 * (1.f / (1.f + expf(-g0)))) * u0);
-  put_split(act + int64_t(m) * ldx + perm_pos(f + 1, F), plane, (g1 * (1.f / (1.f + expf(-g1)))) * u1);
+  put_split(act + act_index(m, perm_pos(f, F), F, ldx), plane, (g0 * (1.f / (1.f + expf(-g0)))) * u0);
+  put_split(act + act_index(m, perm_pos(f + 1, F), F, ldx), plane, (g1 * (1.f / (1.f + expf(-g1)))) * u1);
 }
 
 // Prefill: causal GQA attention of query block blockIdx.y (16 rows) for head blockIdx.x.
@@ -536,7 +559,7 @@ __global__ __launch_bounds__(256) void mx_attention_prefill(const float* qkv, in
 #pragma unroll
   for (int t = 0; t < kQW; ++t) {
     const int i = q0 + kQW * wv + t;
-    if (i < M) put_split(att + int64_t(i) * ldx + perm_pos(h * kDh + lane, d), plane, o[t] / ls[t]);
+    if (i < M) put_split(att + act_index(i, perm_pos(h * kDh + lane, d), d, ldx), plane, o[t] / ls[t]);
   }
 }
 
@@ -635,7 +658,7 @@ __global__ __launch_bounds__(64 * kAttnWaves) void mx_attention_decode(const flo
       num += a * so[w][lane];
       den += a * sml[w][1];
     }
-    put_split(att + int64_t(m) * ldx + perm_pos(h * kDh + lane, d), plane, num / den);
+    put_split(att + act_index(m, perm_pos(h * kDh + lane, d), d, ldx), plane, num / den);
   }
 }
 
@@ -704,6 +727,20 @@ __global__ void mx_sanitize_rows(const int32_t* pos, int fixed_pos, const int32_
   if (bad) atomicOr(status, 4);
 }
 
+// One 16-byte piece per thread of the tile copy of an N x K matrix W (rows in packed order): piece
+// p is lane p % 64 of tile p / 64 = (n / 16) (K / 32) + k / 32, i.e. row 16 (tile / (K / 32)) + lane % 16
+// at positions 32 (tile % (K / 32)) + 8 (lane / 16) .. + 8.
+__global__ __launch_bounds__(256) void mx_pack_tiles(const uint16_t* W, int N, int K, uint16_t* T) {
+  const int64_t p = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  const int S = K / kBK;
+  if (p >= int64_t(N) * S * 64) return;
+  const int lane = int(p & 63);
+  const int64_t tile = p >> 6;
+  const int64_t n = 16 * (tile / S) + (lane & 15);
+  const int k = kBK * int(tile % S) + 8 * (lane >> 4);
+  *reinterpret_cast<uint4*>(T + p * 8) = *reinterpret_cast<const uint4*>(W + n * K + k);
+}
+
 // ---------------------------------------------------------------- host side
 struct Layout {
   size_t h, xn, qkv, att, act, part, status, rowpos, pages, bytes;
@@ -711,22 +748,18 @@ struct Layout {
 
 static size_t al256(size_t x) { return (x + 255) & ~size_t(255); }
 
-// Row stride of the bf16 activation planes the projections read: K plus 16 bytes.  Rows exactly
-// 2 KB (or any multiple of 128 bytes) apart put the 16 rows an MFMA fragment load touches at the
-// same offset on the same memory channel; the 16-byte skew spreads them (measured: the 128-row
-// prefill's four projections 55 -> 45 us per layer).
-static int act_ld(int K) { return K + 8; }
 
-// Widest projection mx_gemm_rows takes: wider ones (the 306M gate/up, 5632 outputs) run faster
-// on the split-K kernel (measured: 128-token prefill 1.95 -> 1.79 ms).
+// Widest projection mx_gemm_rows takes with weights in row order: wider ones (the 306M gate/up,
+// 5632 outputs) run faster on the split-K kernel (measured: 128-token prefill 1.95 -> 1.79 ms).
+// With the weights in tile order it takes every width (gate/up at 128 rows: 18.7 -> 10.1 us).
 constexpr int kRowsMaxN = 4096;
 
 // Column tiles (of 16) per workgroup of mx_gemm_rows: the widest that still gives about one
 // workgroup per compute unit; 0 when the projection has too few output tiles for it (few rows),
 // or too short a K for every wave to take a step, and the split-K kernel runs instead.
-static int rows_ct(int M, int N, int K) {
+static int rows_ct(int M, int N, int K, bool tw) {
   const int T = (M + 15) / 16, n16 = N / 16;
-  if (K / kBK < 4 || M < 48 || N > kRowsMaxN) return 0;
+  if (K / kBK < 4 || M < 48 || (N > kRowsMaxN && !tw)) return 0;
   for (int ct : {8, 6, 4, 3, 2, 1})
     if (n16 % ct == 0 && T * (n16 / ct) >= 224) return ct;
   return 0;
@@ -734,8 +767,8 @@ static int rows_ct(int M, int N, int K) {
 
 // K splits of a projection: 1 for mx_gemm_rows, else enough split-K workgroups to occupy every
 // compute unit, at least 4 K steps each
-static int splits_for(int M, int N, int K, int bm) {
-  if (rows_ct(M, N, K) > 0) return 1;
+static int splits_for(int M, int N, int K, int bm, bool tw) {
+  if (rows_ct(M, N, K, tw) > 0) return 1;
   const int tiles = (N / kBN) * ((M + bm - 1) / bm);
   int s = 1;
   while (tiles * s < 256 && (K / kBK) / (2 * s) >= 4 && 2 * s <= kMaxSplitK) s *= 2;
@@ -748,22 +781,27 @@ static size_t part_floats(const msd_config* c, int M) {
   const int d = c->d_model, ff = c->d_ff, nqkv = (c->n_heads + 2 * c->n_kv_heads) * kDh;
   const int bm = bm_for(M);
   size_t mx = 0;
-  mx = std::max(mx, size_t(splits_for(M, nqkv, d, bm)) * nqkv);
-  mx = std::max(mx, size_t(splits_for(M, d, d, bm)) * d);
-  mx = std::max(mx, size_t(splits_for(M, 2 * ff, d, bm)) * 2 * ff);
-  mx = std::max(mx, size_t(splits_for(M, d, ff, bm)) * d);
+  for (bool tw : {false, true}) {
+    mx = std::max(mx, size_t(splits_for(M, nqkv, d, bm, tw)) * nqkv);
+    mx = std::max(mx, size_t(splits_for(M, d, d, bm, tw)) * d);
+    mx = std::max(mx, size_t(splits_for(M, 2 * ff, d, bm, tw)) * 2 * ff);
+    mx = std::max(mx, size_t(splits_for(M, d, ff, bm, tw)) * d);
+  }
   return mx * M;
 }
+
+static int pad16(int M) { return (M + 15) & ~15; }
 
 static Layout layout(const msd_config* c, int M) {
   const int d = c->d_model, ff = c->d_ff, nqkv = (c->n_heads + 2 * c->n_kv_heads) * kDh;
   Layout L;
   size_t o = 0;
   L.h = o;      o += al256(size_t(M) * d * 4);
-  L.xn = o;     o += al256(size_t(M) * act_ld(d) * 2 * 2);    // hi and lo planes
+  // activation planes (hi and lo) in tile order, rows padded to whole tiles
+  L.xn = o;     o += al256(size_t(pad16(M)) * d * 2 * 2);
   L.qkv = o;    o += al256(size_t(M) * nqkv * 4);
-  L.att = o;    o += al256(size_t(M) * act_ld(d) * 2 * 2);
-  L.act = o;    o += al256(size_t(M) * act_ld(ff) * 2 * 2);
+  L.att = o;    o += al256(size_t(pad16(M)) * d * 2 * 2);
+  L.act = o;    o += al256(size_t(pad16(M)) * ff * 2 * 2);
   L.part = o;   o += al256(part_floats(c, M) * 4);
   L.status = o; o += 256;
   L.rowpos = o; o += al256(size_t(M) * 4);
@@ -780,33 +818,48 @@ static bool mx_config_ok(const msd_config* c) {
   return true;
 }
 
+template <bool TA, bool TW>
+static void launch_rows(int ct, dim3 grid, hipStream_t s, const GemmArgs& g) {
+  switch (ct) {
+    case 8: hipLaunchKernelGGL((mx_gemm_rows<8, 3, TA, TW>), grid, dim3(256), 0, s, g); break;
+    case 6: hipLaunchKernelGGL((mx_gemm_rows<6, 3, TA, TW>), grid, dim3(256), 0, s, g); break;
+    case 4: hipLaunchKernelGGL((mx_gemm_rows<4, 4, TA, TW>), grid, dim3(256), 0, s, g); break;
+    case 3: hipLaunchKernelGGL((mx_gemm_rows<3, 4, TA, TW>), grid, dim3(256), 0, s, g); break;
+    case 2: hipLaunchKernelGGL((mx_gemm_rows<2, 4, TA, TW>), grid, dim3(256), 0, s, g); break;
+    default: hipLaunchKernelGGL((mx_gemm_rows<1, 4, TA, TW>), grid, dim3(256), 0, s, g); break;
+  }
+}
+
+template <bool TA, bool TW>
+static void launch_splitk(int bm, dim3 grid, hipStream_t s, const GemmArgs& g) {
+  if (bm == 16) hipLaunchKernelGGL((mx_gemm<1, 1, TA, TW>), grid, dim3(256), 0, s, g);
+  else if (bm == 64) hipLaunchKernelGGL((mx_gemm<2, 2, TA, TW>), grid, dim3(256), 0, s, g);
+  else hipLaunchKernelGGL((mx_gemm<4, 2, TA, TW>), grid, dim3(256), 0, s, g);
+}
+
 // C = A W^T split over K: partials [splits][M][N] (pass ldo = N), or with splits == 1 rows
-// of stride ldo
+// of stride ldo.  lda == 0: A in tile order (act_index); tw: W in tile order (msd_pack_tiles).
 // rows_ok: mx_gemm_rows may run (single split only).  The tied logits pass false: one row and
 // every row then come from the same kernel and summation order, so the last row's logits are
 // bitwise the same either way.
-static hipError_t gemm(const uint16_t* A, int64_t a_plane, int lda, const uint16_t* W, int M, int N, int K, float* out,
-                       int ldo, int splits, hipStream_t s, bool rows_ok = true) {
+static hipError_t gemm(const uint16_t* A, int64_t a_plane, int lda, const uint16_t* W, bool tw, int M, int N, int K,
+                       float* out, int ldo, int splits, hipStream_t s, bool rows_ok = true) {
   GemmArgs g{A, a_plane, W, out, M, N, K, lda, ldo, splits};
-  const int ct = splits == 1 && rows_ok ? rows_ct(M, N, K) : 0;
+  const bool ta = lda == 0;
+  const int ct = splits == 1 && rows_ok ? rows_ct(M, N, K, tw) : 0;
   if (ct > 0) {
     const int T = (M + 15) / 16, C = N / (16 * ct);
     const dim3 grid(8 * ((C + 7) / 8) * T);
-    switch (ct) {
-      case 8: hipLaunchKernelGGL((mx_gemm_rows<8, 3>), grid, dim3(256), 0, s, g); break;
-      case 6: hipLaunchKernelGGL((mx_gemm_rows<6, 3>), grid, dim3(256), 0, s, g); break;
-      case 4: hipLaunchKernelGGL((mx_gemm_rows<4, 4>), grid, dim3(256), 0, s, g); break;
-      case 3: hipLaunchKernelGGL((mx_gemm_rows<3, 4>), grid, dim3(256), 0, s, g); break;
-      case 2: hipLaunchKernelGGL((mx_gemm_rows<2, 4>), grid, dim3(256), 0, s, g); break;
-      default: hipLaunchKernelGGL((mx_gemm_rows<1, 4>), grid, dim3(256), 0, s, g); break;
-    }
+    if (ta && tw) launch_rows<true, true>(ct, grid, s, g);
+    else if (ta) launch_rows<true, false>(ct, grid, s, g);
+    else launch_rows<false, false>(ct, grid, s, g);
     return hipGetLastError();
   }
   const int bm = bm_for(M);
   const dim3 grid(N / kBN, (M + bm - 1) / bm, splits);
-  if (bm == 16) hipLaunchKernelGGL((mx_gemm<1, 1>), grid, dim3(256), 0, s, g);
-  else if (bm == 64) hipLaunchKernelGGL((mx_gemm<2, 2>), grid, dim3(256), 0, s, g);
-  else hipLaunchKernelGGL((mx_gemm<4, 2>), grid, dim3(256), 0, s, g);
+  if (ta && tw) launch_splitk<true, true>(bm, grid, s, g);
+  else if (ta) launch_splitk<true, false>(bm, grid, s, g);
+  else launch_splitk<false, false>(bm, grid, s, g);
   return hipGetLastError();
 }
 
@@ -816,7 +869,15 @@ struct Weights {
   const uint16_t* w;
   const uint16_t* lnf;
   const float* rope;
+  const uint16_t* tiles;   // the projections in tile order (msd_pack_tiles), or NULL
 };
+
+// Elements of one layer's projections in the tile copy: QKV, O, gate/up, down, each N x K in
+// tile order, layer after layer.
+static int64_t tile_layer_elems(const msd_config* c) {
+  const int64_t d = c->d_model, ff = c->d_ff, nqkv = int64_t(c->n_heads + 2 * c->n_kv_heads) * kDh;
+  return nqkv * d + d * d + 2 * ff * d + d * ff;
+}
 
 // The layer stack over M rows whose residual stream is already in h; leaves the last
 // projection's partials pending (returned split count).
@@ -834,31 +895,39 @@ static int run_layers(const msd_config* cfg, const Weights& wt, const Rows& rows
                 off_gu = off_o + int64_t(d) * d, off_dn = off_gu + 2 * int64_t(ff) * d,
                 layer = off_dn + int64_t(d) * ff;
   const int bm = bm_for(M);
-  const int sq = splits_for(M, nqkv, d, bm), so = splits_for(M, d, d, bm), sg = splits_for(M, 2 * ff, d, bm),
-            sd = splits_for(M, d, ff, bm);
+  const bool tw = wt.tiles != nullptr;
+  const int sq = splits_for(M, nqkv, d, bm, tw), so = splits_for(M, d, d, bm, tw),
+            sg = splits_for(M, 2 * ff, d, bm, tw), sd = splits_for(M, d, ff, bm, tw);
+  // the projections' weights: tile order when the tile copy is given, else the packed rows
+  const int64_t toff_o = int64_t(nqkv) * d, toff_gu = toff_o + int64_t(d) * d, toff_dn = toff_gu + 2 * int64_t(ff) * d;
   int pending = 0;
   err = hipSuccess;
   for (int l = 0; l < cfg->n_layers && err == hipSuccess; ++l) {
     const uint16_t* Wl = wt.w + int64_t(l) * layer;
+    const uint16_t* Tl = tw ? wt.tiles + int64_t(l) * tile_layer_elems(cfg) : nullptr;
+    const uint16_t* Wqkv = tw ? Tl : Wl + off_qkv;
+    const uint16_t* Wo = tw ? Tl + toff_o : Wl + off_o;
+    const uint16_t* Wgu = tw ? Tl + toff_gu : Wl + off_gu;
+    const uint16_t* Wdn = tw ? Tl + toff_dn : Wl + off_dn;
     uint16_t* kc = kv + int64_t(l) * 2 * KV * rows.pool * kDh;
     uint16_t* vc = kc + int64_t(KV) * rows.pool * kDh;
-    const int ldd = act_ld(d), ldf = act_ld(ff);
-    const int64_t pd = int64_t(M) * ldd, pf = int64_t(M) * ldf;   // lo planes after the hi planes
-    hipLaunchKernelGGL(mx_norm, dim3(M), dim3(kNormThreads), 0, s, h, part, pending, M, d, Wl, xn, pd, 0, ldd);
-    if ((err = gemm(xn, pd, ldd, Wl + off_qkv, M, nqkv, d, part, nqkv, sq, s)) != hipSuccess) break;
+    // activation planes in tile order (ldx 0), the lo planes after the hi planes
+    const int64_t pd = int64_t(pad16(M)) * d, pf = int64_t(pad16(M)) * ff;
+    hipLaunchKernelGGL(mx_norm, dim3(M), dim3(kNormThreads), 0, s, h, part, pending, M, d, Wl, xn, pd, 0, 0);
+    if ((err = gemm(xn, pd, 0, Wqkv, tw, M, nqkv, d, part, nqkv, sq, s)) != hipSuccess) break;
     hipLaunchKernelGGL(mx_qkv_fin, dim3(M, (nqkv / 4 + 255) / 256), dim3(256), 0, s, part, sq, M, H, KV, wt.rope, rows,
                        kc, vc, qkv);
     if (prefill)
       hipLaunchKernelGGL(mx_attention_prefill, dim3(H, (M + kAttnQ - 1) / kAttnQ), dim3(256), 0, s, qkv, M, H, KV,
-                         att, pd, ldd);
+                         att, pd, 0);
     else
       hipLaunchKernelGGL(mx_attention_decode, dim3(M, H), dim3(64 * kAttnWaves), 0, s, qkv, rows, H, KV, kc, vc, att,
-                         pd, ldd);
-    if ((err = gemm(att, pd, ldd, Wl + off_o, M, d, d, part, d, so, s)) != hipSuccess) break;
-    hipLaunchKernelGGL(mx_norm, dim3(M), dim3(kNormThreads), 0, s, h, part, so, M, d, Wl + off_ln2, xn, pd, 0, ldd);
-    if ((err = gemm(xn, pd, ldd, Wl + off_gu, M, 2 * ff, d, part, 2 * ff, sg, s)) != hipSuccess) break;
-    hipLaunchKernelGGL(mx_swiglu_fin, dim3(M, (ff / 2 + 255) / 256), dim3(256), 0, s, part, sg, M, ff, act, pf, ldf);
-    if ((err = gemm(act, pf, ldf, Wl + off_dn, M, d, ff, part, d, sd, s)) != hipSuccess) break;
+                         pd, 0);
+    if ((err = gemm(att, pd, 0, Wo, tw, M, d, d, part, d, so, s)) != hipSuccess) break;
+    hipLaunchKernelGGL(mx_norm, dim3(M), dim3(kNormThreads), 0, s, h, part, so, M, d, Wl + off_ln2, xn, pd, 0, 0);
+    if ((err = gemm(xn, pd, 0, Wgu, tw, M, 2 * ff, d, part, 2 * ff, sg, s)) != hipSuccess) break;
+    hipLaunchKernelGGL(mx_swiglu_fin, dim3(M, (ff / 2 + 255) / 256), dim3(256), 0, s, part, sg, M, ff, act, pf, 0);
+    if ((err = gemm(act, pf, 0, Wdn, tw, M, d, ff, part, d, sd, s)) != hipSuccess) break;
     pending = sd;
   }
   if (err == hipSuccess) err = hipGetLastError();
@@ -897,7 +966,8 @@ static int32_t prefill_impl(const msd_config* cfg, const Weights& wt, const int3
   if (!wt.emb || !wt.outp || !wt.w || !wt.lnf || !wt.rope || !tokens || !kv || !workspace || !logits_last ||
       !next_token)
     return MSD_E_ARG;
-  if (!aligned16(wt.emb) || !aligned16(wt.outp) || !aligned16(wt.w) || !aligned16(kv) || !aligned16(workspace))
+  if (!aligned16(wt.emb) || !aligned16(wt.outp) || !aligned16(wt.w) || !aligned16(kv) || !aligned16(workspace) ||
+      !aligned16(wt.tiles))
     return MSD_E_ARG;
   if (page_table && (max_pages * kPage < start + M || max_pages > (cfg->context_len + kPage - 1) / kPage ||
                      pool_pages <= 0))
@@ -924,7 +994,7 @@ static int32_t prefill_impl(const msd_config* cfg, const Weights& wt, const int3
   const int r0 = logits_all ? 0 : M - 1, nr = M - r0;
   hipLaunchKernelGGL(mx_norm, dim3(nr), dim3(kNormThreads), 0, s, h, part, pending, M, d, wt.lnf, xn,
                      int64_t(nr) * d, r0, d);
-  if (gemm(xn, int64_t(nr) * d, d, wt.outp, nr, V, d, logits_all ? logits_all : logits_last, V, 1, s, false) !=
+  if (gemm(xn, int64_t(nr) * d, d, wt.outp, false, nr, V, d, logits_all ? logits_all : logits_last, V, 1, s, false) !=
       hipSuccess)
     return MSD_E_HIP;
   const float* last = logits_all ? logits_all + int64_t(M - 1) * V : logits_last;
@@ -938,24 +1008,54 @@ static int32_t prefill_impl(const msd_config* cfg, const Weights& wt, const int3
   return hipGetLastError() == hipSuccess ? MSD_OK : MSD_E_HIP;
 }
 
+extern "C" int64_t msd_tiles_bytes(const msd_config* cfg) {
+  if (!mx_config_ok(cfg)) return MSD_E_CONFIG;
+  return tile_layer_elems(cfg) * cfg->n_layers * 2;
+}
+
+extern "C" int32_t msd_pack_tiles(const msd_config* cfg, const void* packed_w, void* tiles, void* stream) {
+  if (!mx_config_ok(cfg)) return MSD_E_CONFIG;
+  if (!packed_w || !tiles || !aligned16(packed_w) || !aligned16(tiles)) return MSD_E_ARG;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int d = cfg->d_model, ff = cfg->d_ff, nqkv = (cfg->n_heads + 2 * cfg->n_kv_heads) * kDh;
+  const int64_t off_qkv = 2 * int64_t(d), off_o = off_qkv + int64_t(nqkv) * d, off_gu = off_o + int64_t(d) * d,
+                off_dn = off_gu + 2 * int64_t(ff) * d, layer = off_dn + int64_t(d) * ff;
+  const struct { int64_t src, dst; int N, K; } mats[4] = {
+      {off_qkv, 0, nqkv, d},
+      {off_o, int64_t(nqkv) * d, d, d},
+      {off_gu, int64_t(nqkv) * d + int64_t(d) * d, 2 * ff, d},
+      {off_dn, int64_t(nqkv) * d + int64_t(d) * d + 2 * int64_t(ff) * d, d, ff}};
+  const uint16_t* w = static_cast<const uint16_t*>(packed_w);
+  uint16_t* t = static_cast<uint16_t*>(tiles);
+  for (int l = 0; l < cfg->n_layers; ++l)
+    for (const auto& m : mats) {
+      const int64_t pieces = int64_t(m.N) * m.K / 8;
+      hipLaunchKernelGGL(mx_pack_tiles, dim3(unsigned((pieces + 255) / 256)), dim3(256), 0, s,
+                         w + l * layer + m.src, m.N, m.K, t + l * tile_layer_elems(cfg) + m.dst);
+    }
+  return hipGetLastError() == hipSuccess ? MSD_OK : MSD_E_HIP;
+}
+
 extern "C" int32_t msd_prefill(const msd_config* cfg, const void* token_emb, const void* output_proj,
-                               const void* packed_w, const void* lnf_s, const float* rope, const int32_t* tokens,
-                               int32_t n_tokens, void* kv, void* workspace, float* logits_last,
+                               const void* packed_w, const void* tiles, const void* lnf_s, const float* rope,
+                               const int32_t* tokens, int32_t n_tokens, void* kv, void* workspace, float* logits_last,
                                float* logits_all, int32_t* next_token, void* stream) {
   const Weights wt{static_cast<const uint16_t*>(token_emb), static_cast<const uint16_t*>(output_proj),
-                   static_cast<const uint16_t*>(packed_w), static_cast<const uint16_t*>(lnf_s), rope};
+                   static_cast<const uint16_t*>(packed_w), static_cast<const uint16_t*>(lnf_s), rope,
+                   static_cast<const uint16_t*>(tiles)};
   return prefill_impl(cfg, wt, tokens, n_tokens, 0, nullptr, 0, 0, kv, workspace, logits_last, logits_all, next_token,
                       nullptr, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int32_t msd_prefill_paged(const msd_config* cfg, const void* token_emb, const void* output_proj,
-                                     const void* packed_w, const void* lnf_s, const float* rope,
+                                     const void* packed_w, const void* tiles, const void* lnf_s, const float* rope,
                                      const int32_t* tokens, int32_t n_tokens, const int32_t* page_table,
                                      int32_t max_pages, void* kv_pool, int32_t pool_pages, void* workspace,
                                      float* logits_last, int32_t* next_token, void* stream) {
   if (!page_table) return MSD_E_ARG;
   const Weights wt{static_cast<const uint16_t*>(token_emb), static_cast<const uint16_t*>(output_proj),
-                   static_cast<const uint16_t*>(packed_w), static_cast<const uint16_t*>(lnf_s), rope};
+                   static_cast<const uint16_t*>(packed_w), static_cast<const uint16_t*>(lnf_s), rope,
+                   static_cast<const uint16_t*>(tiles)};
   return prefill_impl(cfg, wt, tokens, n_tokens, 0, page_table, max_pages, pool_pages, kv_pool, workspace, logits_last,
                       nullptr, next_token, nullptr, static_cast<hipStream_t>(stream));
 }
@@ -965,12 +1065,13 @@ extern "C" int64_t msd_verify_workspace_bytes(const msd_config* cfg, int32_t n_t
 }
 
 extern "C" int32_t msd_verify(const msd_config* cfg, const void* token_emb, const void* output_proj,
-                              const void* packed_w, const void* lnf_s, const float* rope, const int32_t* tokens,
-                              int32_t n_tokens, int32_t start_pos, void* kv, void* workspace, float* logits,
-                              int32_t* argmax, void* stream) {
+                              const void* packed_w, const void* tiles, const void* lnf_s, const float* rope,
+                              const int32_t* tokens, int32_t n_tokens, int32_t start_pos, void* kv, void* workspace,
+                              float* logits, int32_t* argmax, void* stream) {
   if (!cfg || !logits || !argmax || n_tokens <= 0 || start_pos < 1) return MSD_E_ARG;
   const Weights wt{static_cast<const uint16_t*>(token_emb), static_cast<const uint16_t*>(output_proj),
-                   static_cast<const uint16_t*>(packed_w), static_cast<const uint16_t*>(lnf_s), rope};
+                   static_cast<const uint16_t*>(packed_w), static_cast<const uint16_t*>(lnf_s), rope,
+                   static_cast<const uint16_t*>(tiles)};
   // the last row's logits land in logits (as part of logits_all); its argmax again in argmax[2(n-1)]
   return prefill_impl(cfg, wt, tokens, n_tokens, start_pos, nullptr, 0, 0, kv, workspace,
                       logits + int64_t(n_tokens - 1) * cfg->vocab_size, logits, argmax + 2 * (n_tokens - 1), argmax,
@@ -988,7 +1089,7 @@ extern "C" int64_t msd_batch_workspace_bytes(const msd_config* cfg, int32_t batc
 }
 
 extern "C" int32_t msd_batch_decode_step(const msd_config* cfg, const void* token_emb, const void* output_proj,
-                                         const void* packed_w, const void* lnf_s, const float* rope,
+                                         const void* packed_w, const void* tiles, const void* lnf_s, const float* rope,
                                          const int32_t* tokens, const int32_t* positions, int32_t batch,
                                          const int32_t* page_tables, int32_t max_pages, void* kv_pool,
                                          int32_t pool_pages, void* workspace, float* logits,
@@ -1000,7 +1101,7 @@ extern "C" int32_t msd_batch_decode_step(const msd_config* cfg, const void* toke
       !kv_pool || !workspace || !logits || !next_tokens)
     return MSD_E_ARG;
   if (!aligned16(token_emb) || !aligned16(output_proj) || !aligned16(packed_w) || !aligned16(kv_pool) ||
-      !aligned16(workspace))
+      !aligned16(workspace) || !aligned16(tiles))
     return MSD_E_ARG;
   if (max_pages <= 0 || max_pages > (cfg->context_len + kPage - 1) / kPage || pool_pages <= 0) return MSD_E_ARG;
   if (cfg->context_len > 64 * kAttnWaves) return MSD_E_CONFIG;   // one 64-position block per attention wave
@@ -1014,7 +1115,8 @@ extern "C" int32_t msd_batch_decode_step(const msd_config* cfg, const void* toke
     if (rc != 1) return rc;
   }
   const Weights wt{static_cast<const uint16_t*>(token_emb), static_cast<const uint16_t*>(output_proj),
-                   static_cast<const uint16_t*>(packed_w), static_cast<const uint16_t*>(lnf_s), rope};
+                   static_cast<const uint16_t*>(packed_w), static_cast<const uint16_t*>(lnf_s), rope,
+                   static_cast<const uint16_t*>(tiles)};
   const int d = cfg->d_model, V = cfg->vocab_size;
   const Layout L = layout(cfg, M);
   char* ws = static_cast<char*>(workspace) + batch_region(cfg);
@@ -1034,7 +1136,7 @@ extern "C" int32_t msd_batch_decode_step(const msd_config* cfg, const void* toke
   if (err != hipSuccess) return MSD_E_HIP;
   hipLaunchKernelGGL(mx_norm, dim3(M), dim3(kNormThreads), 0, s, h, part, pending, M, d, wt.lnf, xn, int64_t(M) * d, 0,
                      d);
-  if (gemm(xn, int64_t(M) * d, d, wt.outp, M, V, d, logits, V, 1, s, false) != hipSuccess) return MSD_E_HIP;
+  if (gemm(xn, int64_t(M) * d, d, wt.outp, false, M, V, d, logits, V, 1, s, false) != hipSuccess) return MSD_E_HIP;
   hipLaunchKernelGGL(mx_argmax, dim3(M), dim3(1024), 0, s, logits, V, V, next_tokens, status);
   return hipGetLastError() == hipSuccess ? MSD_OK : MSD_E_HIP;
 }

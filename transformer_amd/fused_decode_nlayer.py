@@ -24,6 +24,8 @@ row in the kernel row layout (no transpose, no padding).  ``vocab_pad`` is still
 reported as the reference computes it.  RoPE tables stay float32 (model.py:101-107) instead of the reference's bf16
 copies (fused_decode_nlayer.py:317-318); ``rope`` holds them as one (ctx, d_head) table.
 """
+import ctypes
+
 import numpy as np
 import torch
 
@@ -137,7 +139,8 @@ def prepare_decode_weights_nlayer(params, config, kv_splits=1, device=None):
 
     Keys: token_emb (V, d) bf16, output_proj (V, d) bf16 in the kernel row layout,
     packed_w (kernel layout), lnf_s (d) bf16, cos/sin (ctx, d_head/2) f32,
-    rope (ctx, d_head) f32 = [cos | sin], vocab_pad (reference value).
+    rope (ctx, d_head) f32 = [cos | sin], vocab_pad (reference value).  The multi-row passes add
+    ``tiles`` (``weight_tiles``) on first use.
     """
     from .configs import check_config
     dh = check_config(config)
@@ -158,3 +161,22 @@ def prepare_decode_weights_nlayer(params, config, kv_splits=1, device=None):
         "rope": torch.from_numpy(np.ascontiguousarray(rope)).to(dev),
         "vocab_pad": vocab_pad,
     }
+
+
+def weight_tiles(w, config):
+    """The tile copy of ``w``'s projection weights (``msd_pack_tiles``: every matrix as 16 x 32
+    tiles in matrix-core operand order), built on the device on first use and kept in
+    ``w["tiles"]``.  The multi-row passes (prefill, verification, the multi-kernel batched step)
+    read their projections from it; it takes as much device memory as ``packed_w``."""
+    t = w.get("tiles")
+    if t is None:
+        cfg = _lib.MsdConfig.from_dict(config)
+        L = _lib.lib()
+        nbytes = _lib.check(L.msd_tiles_bytes(ctypes.byref(cfg)), "msd_tiles_bytes")
+        dev = w["packed_w"].device
+        t = torch.empty(nbytes // 2, dtype=torch.bfloat16, device=dev)
+        s = torch.cuda.current_stream(dev)
+        _lib.check(L.msd_pack_tiles(ctypes.byref(cfg), w["packed_w"].data_ptr(), t.data_ptr(),
+                                    ctypes.c_void_p(s.cuda_stream)), "msd_pack_tiles")
+        w["tiles"] = t
+    return t

@@ -51,8 +51,13 @@ class PagePool:
 
 
 class PagedBatchDecoder:
-    def __init__(self, w, config, pool, batch, max_pages=None, device=None):
+    """Batched decode of ``batch`` sequences over ``pool``.  With ``tiles`` (default) the prompt
+    prefill and the multi-kernel step read the tile copy of the weights (``weight_tiles``)."""
+
+    def __init__(self, w, config, pool, batch, max_pages=None, device=None, tiles=True):
+        from .fused_decode_nlayer import weight_tiles
         self.w = w
+        self.tiles = weight_tiles(w, config) if tiles else None
         self.config = dict(config)
         self.pool = pool
         self.batch = int(batch)
@@ -76,7 +81,7 @@ class PagedBatchDecoder:
     def _w(self):
         w = self.w
         return (w["token_emb"].data_ptr(), w["output_proj"].data_ptr(), w["packed_w"].data_ptr(),
-                w["lnf_s"].data_ptr(), w["rope"].data_ptr())
+                None if self.tiles is None else self.tiles.data_ptr(), w["lnf_s"].data_ptr(), w["rope"].data_ptr())
 
     def set_pages(self, b, pages):
         pages = np.asarray(pages, dtype=np.int32)

@@ -18,10 +18,14 @@ from . import _lib
 
 
 class Prefiller:
-    """Prefill of prompts up to ``max_tokens`` long with the prepared decode weights ``w``."""
+    """Prefill of prompts up to ``max_tokens`` long with the prepared decode weights ``w``.
+    With ``tiles`` (default) the projections read the tile copy of the weights
+    (``weight_tiles``, one more copy of ``packed_w`` on the device); without, the packed rows."""
 
-    def __init__(self, w, config, max_tokens=None, device=None):
+    def __init__(self, w, config, max_tokens=None, device=None, tiles=True):
+        from .fused_decode_nlayer import weight_tiles
         self.w = w
+        self.tiles = weight_tiles(w, config) if tiles else None
         self.config = dict(config)
         self.device = torch.device(device) if device is not None else w["packed_w"].device
         if self.device.type == "cuda" and self.device.index is None:
@@ -58,7 +62,8 @@ class Prefiller:
         w = self.w
         rc = _lib.lib().msd_prefill(
             ctypes.byref(self._cfg), w["token_emb"].data_ptr(), w["output_proj"].data_ptr(),
-            w["packed_w"].data_ptr(), w["lnf_s"].data_ptr(), w["rope"].data_ptr(), tok.data_ptr(), T,
+            w["packed_w"].data_ptr(), None if self.tiles is None else self.tiles.data_ptr(), w["lnf_s"].data_ptr(),
+            w["rope"].data_ptr(), tok.data_ptr(), T,
             kv.data_ptr(), self.workspace.data_ptr(), self.logits.data_ptr(),
             None if logits_all is None else logits_all.data_ptr(), out.data_ptr(), ctypes.c_void_p(s.cuda_stream))
         _lib.check(rc, "msd_prefill")

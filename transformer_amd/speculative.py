@@ -27,8 +27,10 @@ from . import _lib
 class Verifier:
     """``msd_verify`` for up to ``max_tokens`` rows with the prepared target weights ``w``."""
 
-    def __init__(self, w, config, max_tokens=8, device=None):
+    def __init__(self, w, config, max_tokens=8, device=None, tiles=True):
+        from .fused_decode_nlayer import weight_tiles
         self.w = w
+        self.tiles = weight_tiles(w, config) if tiles else None
         self.config = dict(config)
         self.device = torch.device(device) if device is not None else w["packed_w"].device
         if self.device.type == "cuda" and self.device.index is None:
@@ -60,7 +62,8 @@ class Verifier:
         w = self.w
         rc = _lib.lib().msd_verify(
             ctypes.byref(self._cfg), w["token_emb"].data_ptr(), w["output_proj"].data_ptr(), w["packed_w"].data_ptr(),
-            w["lnf_s"].data_ptr(), w["rope"].data_ptr(), self._tok.data_ptr(), n, int(start), kv.data_ptr(),
+            None if self.tiles is None else self.tiles.data_ptr(), w["lnf_s"].data_ptr(), w["rope"].data_ptr(),
+            self._tok.data_ptr(), n, int(start), kv.data_ptr(),
             self.workspace.data_ptr(), self.logits.data_ptr(), self.argmax.data_ptr(), ctypes.c_void_p(s.cuda_stream))
         _lib.check(rc, "msd_verify")
         return self.logits[:n], self.argmax[:n]
