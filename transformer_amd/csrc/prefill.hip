@@ -149,12 +149,27 @@ __device__ __forceinline__ int64_t cache_row(const Rows& r, int m, int p) {
   return int64_t(page) * kPage + p % kPage;
 }
 
+// What mx_gemm_rows does with its final outputs.
+enum Epi { kEpiStore = 0, kEpiSwiglu = 1, kEpiQkv = 2 };
+// Operands of the fused epilogues.
+struct EpiArgs {
+  uint16_t* act;       // SwiGLU: the down projection's input planes (tile order), lo plane act_plane further
+  int64_t act_plane;
+  const float* rope;   // QKV: RoPE table, rows, cache and the f32 q/k/v rows (as mx_qkv_fin)
+  Rows rows;
+  uint16_t* kc;
+  uint16_t* vc;
+  float* qkv;
+  int H, KV;
+};
+
 struct GemmArgs {
   const uint16_t* A;   // [M][lda] bf16 (or tile order, see act_index): the hi parts; the lo
   int64_t a_plane;     // parts follow at A + a_plane
   const uint16_t* W;   // [N][K] bf16 (or tile order: tile (n / 16, k / 32) at ((n / 16) (K / 32) + k / 32) 512)
   float* out;          // partials [splits][M][N] f32, or [M][ldo] (single split)
   int M, N, K, lda, ldo, splits;
+  EpiArgs e;
 };
 
 __device__ __forceinline__ bf16x8 as_bf16x8(uint4 u) { return __builtin_bit_cast(bf16x8, u); }
@@ -241,14 +256,36 @@ __global__ __launch_bounds__(256) void mx_gemm(GemmArgs g) {
       }
 }
 
+// SwiGLU of a gate/up pair (packed rows 2f, 2f + 1; model.py:159).
+__device__ __forceinline__ float swiglu(float g, float u) { return (g * (1.f / (1.f + expf(-g)))) * u; }
+
+// Outputs s0, s1 of the packed q/k/v rows col, col + 1 (col even) of row m, whose position has
+// RoPE factors c, sg for this pair: q and k pairs are rotated (dims i, i + 32; model.py:110-117),
+// v is stored as projected; f32 q/k/v in natural head-dim order to `q`, bf16 K/V to the cache
+// row cp (multi_sm_decode.py:179-180).
+__device__ __forceinline__ void qkv_pair(float s0, float s1, float c, float sg, int col, int H, int KV, float* q,
+                                         uint16_t* cp) {
+  const int head = col / kDh, rr = col % kDh, ri = rr >> 1;
+  const bool rot = head < H + KV;
+  const float o0 = rot ? s0 * c - s1 * sg : s0, o1 = rot ? s0 * sg + s1 * c : s1;
+  const int d0 = rot ? ri : rr, d1 = rot ? ri + kDh / 2 : rr + 1;
+  q[d0] = o0;
+  q[d1] = o1;
+  if (head >= H) {
+    cp[d0] = f2bf(o0);
+    cp[d1] = f2bf(o1);
+  }
+}
+
 // C = A W^T for many rows (M >= 48): a workgroup owns 16 rows x 16 CT columns over the whole of K,
 // so it streams CT * 16 complete weight rows (contiguous in memory) and writes final outputs (no
 // split-K partials).  The four waves take interleaved 32-wide K steps (wave w: steps w, w + 4,
 // ...) with P steps of loads in flight, and add their tiles through LDS in wave order, so the
 // result is deterministic.  Tiles are dealt XCD-aware: every row tile of a column tile runs on
 // one XCD (workgroup b on XCD b mod 8), which then fetches that column tile's weights into its L2
-// once.  TA / TW as for mx_gemm.
-template <int CT, int P, bool TA, bool TW>
+// once.  TA / TW as for mx_gemm.  EPI: store the outputs, or finish them in place of
+// mx_swiglu_fin / mx_qkv_fin (column pairs per thread, the same arithmetic, so the same values).
+template <int CT, int P, bool TA, bool TW, int EPI>
 __global__ __launch_bounds__(256) void mx_gemm_rows(GemmArgs g) {
   __shared__ f32x4 red[4][CT][64];
   // wave-uniform wave index: the step count and its loop stay scalar (a per-lane loop would copy
@@ -303,11 +340,36 @@ __global__ __launch_bounds__(256) void mx_gemm_rows(GemmArgs g) {
   for (int ct = 0; ct < CT; ++ct) red[wv][ct][lane] = acc[ct];
   __syncthreads();
   // D layout of a 16 x 16 tile: lane holds rows 4 (lane / 16) + r of column lane % 16
-  for (int idx = threadIdx.x; idx < CT * 256; idx += 256) {
-    const int ct = idx >> 8, e = idx & 255, r = e >> 6, l = e & 63;
-    const float v = ((red[0][ct][l][r] + red[1][ct][l][r]) + red[2][ct][l][r]) + red[3][ct][l][r];
-    const int row = m0 + 4 * (l >> 4) + r;
-    if (row < g.M) g.out[int64_t(row) * g.ldo + n0 + 16 * ct + (l & 15)] = v;
+  if constexpr (EPI == kEpiStore) {
+    for (int idx = threadIdx.x; idx < CT * 256; idx += 256) {
+      const int ct = idx >> 8, e = idx & 255, r = e >> 6, l = e & 63;
+      const float v = ((red[0][ct][l][r] + red[1][ct][l][r]) + red[2][ct][l][r]) + red[3][ct][l][r];
+      const int row = m0 + 4 * (l >> 4) + r;
+      if (row < g.M) g.out[int64_t(row) * g.ldo + n0 + 16 * ct + (l & 15)] = v;
+    }
+  } else {
+    // one column pair (lanes l, l + 1 of a row) per thread
+    for (int idx = threadIdx.x; idx < CT * 128; idx += 256) {
+      const int ct = idx >> 7, e = idx & 127, r = e >> 5, l = 16 * ((e >> 3) & 3) + 2 * (e & 7);
+      const float v0 = ((red[0][ct][l][r] + red[1][ct][l][r]) + red[2][ct][l][r]) + red[3][ct][l][r];
+      const float v1 = ((red[0][ct][l + 1][r] + red[1][ct][l + 1][r]) + red[2][ct][l + 1][r]) + red[3][ct][l + 1][r];
+      const int row = m0 + 4 * (l >> 4) + r, col = n0 + 16 * ct + (l & 15);
+      if (row >= g.M) continue;
+      const EpiArgs& ea = g.e;
+      if constexpr (EPI == kEpiSwiglu) {
+        const int F = g.N / 2, f = col >> 1;
+        put_split(ea.act + act_index(row, perm_pos(f, F), F, 0), ea.act_plane, swiglu(v0, v1));
+      } else {
+        const int p = row_pos(ea.rows, row);
+        const int64_t crow = cache_row(ea.rows, row, p);
+        const int head = col / kDh, ri = (col % kDh) >> 1;
+        const float c = ea.rope[int64_t(p) * kDh + ri], sg = ea.rope[int64_t(p) * kDh + kDh / 2 + ri];
+        const bool isv = head >= ea.H + ea.KV;
+        const int gi = isv ? head - ea.H - ea.KV : head - ea.H;
+        uint16_t* cp = (isv ? ea.vc : ea.kc) + (int64_t(gi) * ea.rows.pool + crow) * kDh;
+        qkv_pair(v0, v1, c, sg, col, ea.H, ea.KV, ea.qkv + int64_t(row) * g.N + head * kDh, cp);
+      }
+    }
   }
 }
 
@@ -420,26 +482,13 @@ __global__ __launch_bounds__(256) void mx_qkv_fin(const float* part, int splits,
       sv.z += pv[z].z;
       sv.w += pv[z].w;
     }
-  const int head = col / kDh, rr = col % kDh;
-  const bool rot = head < H + KV;   // q and k get RoPE, v is stored as projected
+  const int head = col / kDh;
   float* q = qkv + int64_t(m) * nq + head * kDh;
   const bool isv = head >= H + KV;
   const int g = isv ? head - H - KV : head - H;
   uint16_t* cp = (isv ? vc : kc) + (int64_t(g) * rows.pool + crow) * kDh;
-#pragma unroll
-  for (int e = 0; e < 2; ++e) {
-    const float s0 = e ? sv.z : sv.x, s1 = e ? sv.w : sv.y;
-    const float c = e ? cs.y : cs.x, sg = e ? sn.y : sn.x;
-    const float r0 = s0 * c - s1 * sg, r1 = s0 * sg + s1 * c;
-    const float o0 = rot ? r0 : s0, o1 = rot ? r1 : s1;
-    const int d0 = rot ? ri + e : rr + 2 * e, d1 = rot ? ri + e + kDh / 2 : rr + 2 * e + 1;
-    q[d0] = o0;
-    q[d1] = o1;
-    if (head >= H) {
-      cp[d0] = f2bf(o0);
-      cp[d1] = f2bf(o1);
-    }
-  }
+  qkv_pair(sv.x, sv.y, cs.x, sn.x, col, H, KV, q, cp);
+  qkv_pair(sv.z, sv.w, cs.y, sn.y, col + 2, H, KV, q, cp);
 }
 
 // Row blockIdx.x: act_f = silu(gate_f) * up_f over the summed partials (gate/up are the packed
@@ -461,8 +510,8 @@ __global__ __launch_bounds__(256) void mx_swiglu_fin(const float* part, int spli
       g1 += pv[z].z;
       u1 += pv[z].w;
     }
-  put_split(act + act_index(m, perm_pos(f, F), F, ldx), plane, (g0 * (1.f / (1.f + expf(-g0)))) * u0);
-  put_split(act + act_index(m, perm_pos(f + 1, F), F, ldx), plane, (g1 * (1.f / (1.f + expf(-g1)))) * u1);
+  put_split(act + act_index(m, perm_pos(f, F), F, ldx), plane, swiglu(g0, u0));
+  put_split(act + act_index(m, perm_pos(f + 1, F), F, ldx), plane, swiglu(g1, u1));
 }
 
 // Prefill: causal GQA attention of query block blockIdx.y (16 rows) for head blockIdx.x.
@@ -818,15 +867,15 @@ static bool mx_config_ok(const msd_config* c) {
   return true;
 }
 
-template <bool TA, bool TW>
+template <bool TA, bool TW, int EPI = kEpiStore>
 static void launch_rows(int ct, dim3 grid, hipStream_t s, const GemmArgs& g) {
   switch (ct) {
-    case 8: hipLaunchKernelGGL((mx_gemm_rows<8, 3, TA, TW>), grid, dim3(256), 0, s, g); break;
-    case 6: hipLaunchKernelGGL((mx_gemm_rows<6, 3, TA, TW>), grid, dim3(256), 0, s, g); break;
-    case 4: hipLaunchKernelGGL((mx_gemm_rows<4, 4, TA, TW>), grid, dim3(256), 0, s, g); break;
-    case 3: hipLaunchKernelGGL((mx_gemm_rows<3, 4, TA, TW>), grid, dim3(256), 0, s, g); break;
-    case 2: hipLaunchKernelGGL((mx_gemm_rows<2, 4, TA, TW>), grid, dim3(256), 0, s, g); break;
-    default: hipLaunchKernelGGL((mx_gemm_rows<1, 4, TA, TW>), grid, dim3(256), 0, s, g); break;
+    case 8: hipLaunchKernelGGL((mx_gemm_rows<8, 3, TA, TW, EPI>), grid, dim3(256), 0, s, g); break;
+    case 6: hipLaunchKernelGGL((mx_gemm_rows<6, 3, TA, TW, EPI>), grid, dim3(256), 0, s, g); break;
+    case 4: hipLaunchKernelGGL((mx_gemm_rows<4, 4, TA, TW, EPI>), grid, dim3(256), 0, s, g); break;
+    case 3: hipLaunchKernelGGL((mx_gemm_rows<3, 4, TA, TW, EPI>), grid, dim3(256), 0, s, g); break;
+    case 2: hipLaunchKernelGGL((mx_gemm_rows<2, 4, TA, TW, EPI>), grid, dim3(256), 0, s, g); break;
+    default: hipLaunchKernelGGL((mx_gemm_rows<1, 4, TA, TW, EPI>), grid, dim3(256), 0, s, g); break;
   }
 }
 
@@ -842,15 +891,23 @@ static void launch_splitk(int bm, dim3 grid, hipStream_t s, const GemmArgs& g) {
 // rows_ok: mx_gemm_rows may run (single split only).  The tied logits pass false: one row and
 // every row then come from the same kernel and summation order, so the last row's logits are
 // bitwise the same either way.
+// fused(): whether a projection's epilogue can run in the GEMM (mx_gemm_rows over tile-order
+// operands); `epi` then selects it and `ea` carries its operands.
+static bool fused(int M, int N, int K, bool tw) { return tw && rows_ct(M, N, K, true) > 0; }
+
 static hipError_t gemm(const uint16_t* A, int64_t a_plane, int lda, const uint16_t* W, bool tw, int M, int N, int K,
-                       float* out, int ldo, int splits, hipStream_t s, bool rows_ok = true) {
-  GemmArgs g{A, a_plane, W, out, M, N, K, lda, ldo, splits};
+                       float* out, int ldo, int splits, hipStream_t s, bool rows_ok = true, int epi = kEpiStore,
+                       const EpiArgs* ea = nullptr) {
+  GemmArgs g{A, a_plane, W, out, M, N, K, lda, ldo, splits, ea ? *ea : EpiArgs{}};
   const bool ta = lda == 0;
   const int ct = splits == 1 && rows_ok ? rows_ct(M, N, K, tw) : 0;
+  if (epi != kEpiStore && !(ct > 0 && ta && tw && ea)) return hipErrorInvalidValue;
   if (ct > 0) {
     const int T = (M + 15) / 16, C = N / (16 * ct);
     const dim3 grid(8 * ((C + 7) / 8) * T);
-    if (ta && tw) launch_rows<true, true>(ct, grid, s, g);
+    if (epi == kEpiSwiglu) launch_rows<true, true, kEpiSwiglu>(ct, grid, s, g);
+    else if (epi == kEpiQkv) launch_rows<true, true, kEpiQkv>(ct, grid, s, g);
+    else if (ta && tw) launch_rows<true, true>(ct, grid, s, g);
     else if (ta) launch_rows<true, false>(ct, grid, s, g);
     else launch_rows<false, false>(ct, grid, s, g);
     return hipGetLastError();
@@ -914,9 +971,21 @@ static int run_layers(const msd_config* cfg, const Weights& wt, const Rows& rows
     // activation planes in tile order (ldx 0), the lo planes after the hi planes
     const int64_t pd = int64_t(pad16(M)) * d, pf = int64_t(pad16(M)) * ff;
     hipLaunchKernelGGL(mx_norm, dim3(M), dim3(kNormThreads), 0, s, h, part, pending, M, d, Wl, xn, pd, 0, 0);
-    if ((err = gemm(xn, pd, 0, Wqkv, tw, M, nqkv, d, part, nqkv, sq, s)) != hipSuccess) break;
-    hipLaunchKernelGGL(mx_qkv_fin, dim3(M, (nqkv / 4 + 255) / 256), dim3(256), 0, s, part, sq, M, H, KV, wt.rope, rows,
-                       kc, vc, qkv);
+    if (fused(M, nqkv, d, tw)) {   // RoPE, q/k/v and the cache rows in the GEMM's epilogue
+      EpiArgs ea{};
+      ea.rope = wt.rope;
+      ea.rows = rows;
+      ea.kc = kc;
+      ea.vc = vc;
+      ea.qkv = qkv;
+      ea.H = H;
+      ea.KV = KV;
+      if ((err = gemm(xn, pd, 0, Wqkv, tw, M, nqkv, d, part, nqkv, 1, s, true, kEpiQkv, &ea)) != hipSuccess) break;
+    } else {
+      if ((err = gemm(xn, pd, 0, Wqkv, tw, M, nqkv, d, part, nqkv, sq, s)) != hipSuccess) break;
+      hipLaunchKernelGGL(mx_qkv_fin, dim3(M, (nqkv / 4 + 255) / 256), dim3(256), 0, s, part, sq, M, H, KV, wt.rope,
+                         rows, kc, vc, qkv);
+    }
     if (prefill)
       hipLaunchKernelGGL(mx_attention_prefill, dim3(H, (M + kAttnQ - 1) / kAttnQ), dim3(256), 0, s, qkv, M, H, KV,
                          att, pd, 0);
@@ -925,8 +994,16 @@ static int run_layers(const msd_config* cfg, const Weights& wt, const Rows& rows
                          pd, 0);
     if ((err = gemm(att, pd, 0, Wo, tw, M, d, d, part, d, so, s)) != hipSuccess) break;
     hipLaunchKernelGGL(mx_norm, dim3(M), dim3(kNormThreads), 0, s, h, part, so, M, d, Wl + off_ln2, xn, pd, 0, 0);
-    if ((err = gemm(xn, pd, 0, Wgu, tw, M, 2 * ff, d, part, 2 * ff, sg, s)) != hipSuccess) break;
-    hipLaunchKernelGGL(mx_swiglu_fin, dim3(M, (ff / 2 + 255) / 256), dim3(256), 0, s, part, sg, M, ff, act, pf, 0);
+    if (fused(M, 2 * ff, d, tw)) {   // SwiGLU in the GEMM's epilogue
+      EpiArgs ea{};
+      ea.act = act;
+      ea.act_plane = pf;
+      if ((err = gemm(xn, pd, 0, Wgu, tw, M, 2 * ff, d, part, 2 * ff, 1, s, true, kEpiSwiglu, &ea)) != hipSuccess)
+        break;
+    } else {
+      if ((err = gemm(xn, pd, 0, Wgu, tw, M, 2 * ff, d, part, 2 * ff, sg, s)) != hipSuccess) break;
+      hipLaunchKernelGGL(mx_swiglu_fin, dim3(M, (ff / 2 + 255) / 256), dim3(256), 0, s, part, sg, M, ff, act, pf, 0);
+    }
     if ((err = gemm(act, pf, 0, Wdn, tw, M, d, ff, part, d, sd, s)) != hipSuccess) break;
     pending = sd;
   }
