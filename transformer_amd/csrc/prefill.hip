@@ -58,10 +58,7 @@ constexpr int kPage = 16;     // positions per KV page
 constexpr int kBN = 64;       // GEMM tile columns
 constexpr int kBK = 32;       // K per MFMA step
 constexpr int kNormThreads = 256;
-constexpr int kAttnQ = 16;    // queries per prefill attention workgroup (4 per wave)
-constexpr int kQW = kAttnQ / 4;
 constexpr int kMaxSplitK = 16;  // largest K split (partials summed by the consumers)
-constexpr int kKStride = kDh + 4;
 constexpr int kMaxRows = 1024;
 
 __device__ __forceinline__ float bf2f(uint16_t b) { return __uint_as_float(uint32_t(b) << 16); }
@@ -514,102 +511,181 @@ __global__ __launch_bounds__(256) void mx_swiglu_fin(const float* part, int spli
   put_split(act + act_index(m, perm_pos(f + 1, F), F, ldx), plane, swiglu(g1, u1));
 }
 
-// Prefill: causal GQA attention of query block blockIdx.y (16 rows) for head blockIdx.x.
-// Each wave owns 4 queries; key chunks of 64 rows go through LDS, with an online softmax per
-// query (scores: lane = key; output: lane = dimension).  Scale 1/sqrt(64) (model.py:98).
+// Eight f32 values as hi/lo bf16 parts (hi = bf16(x), lo = bf16(x - hi)), packed as MFMA operands.
+__device__ __forceinline__ void split8(const float (&x)[8], uint4& hi, uint4& lo) {
+  uint32_t h[4], l[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint16_t h0 = f2bf(x[2 * i]), h1 = f2bf(x[2 * i + 1]);
+    h[i] = uint32_t(h0) | (uint32_t(h1) << 16);
+    l[i] = uint32_t(f2bf(x[2 * i] - bf2f(h0))) | (uint32_t(f2bf(x[2 * i + 1] - bf2f(h1))) << 16);
+  }
+  hi = make_uint4(h[0], h[1], h[2], h[3]);
+  lo = make_uint4(l[0], l[1], l[2], l[3]);
+}
+
+// f32 operands as hi/lo parts on the matrix cores: a b ~ ah bh + ah bl + al bh (the lo lo term,
+// ~2^-16 of the product, is left out).
+__device__ __forceinline__ f32x4 mfma3(uint4 ah, uint4 al, uint4 bh, uint4 bl, f32x4 c) {
+  c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(ah), as_bf16x8(bh), c, 0, 0, 0);
+  c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(ah), as_bf16x8(bl), c, 0, 0, 0);
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(al), as_bf16x8(bh), c, 0, 0, 0);
+}
+
+// Reductions over the 16 lanes of a DPP row, every lane receiving the result (rotations by 1, 2,
+// 4, 8).  The sum's rounding may differ between the lanes of a row; callers read one lane.
+template <int CTRL>
+__device__ __forceinline__ float dpp_ror(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp_ror<0x121>(v));
+  v = fmaxf(v, dpp_ror<0x122>(v));
+  v = fmaxf(v, dpp_ror<0x124>(v));
+  return fmaxf(v, dpp_ror<0x128>(v));
+}
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp_ror<0x121>(v);
+  v += dpp_ror<0x122>(v);
+  v += dpp_ror<0x124>(v);
+  return v + dpp_ror<0x128>(v);
+}
+
+// Prefill: causal GQA attention of query block blockIdx.y (16 rows) for head blockIdx.x on the
+// matrix cores.  The key range 0..q0+15 is cut into 32-key chunks, wave w taking chunks w, w + 4,
+// ...: S = Q K^T (16 x 32) and O += P V (16 x 64) run on v_mfma_f32_16x16x32_bf16 with every f32
+// operand as hi/lo bf16 parts (mfma3), the softmax is online per query row in f32, and the four
+// waves' (max, sum, O) are merged by log-sum-exp at the end.  Scale 1/sqrt(64) (model.py:98).
+// MFMA operand lanes: A[i][8 (l / 16) ..] = row i = l % 16; B[8 (l / 16) ..][n] with n = l % 16;
+// D: rows 4 (l / 16) + r of column l % 16.
 __global__ __launch_bounds__(256) void mx_attention_prefill(const float* qkv, int M, int H, int KV, uint16_t* att,
                                                             int64_t plane, int ldx) {
-  __shared__ float sk[64 * kKStride];
-  __shared__ float sv[64 * kDh];
-  __shared__ float sq[kAttnQ * kDh];
-  __shared__ float sp[4][kQW][64];
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  constexpr int PS = 36;   // row stride (floats) of a wave's P tile in LDS: 16-byte reads of 16 rows spread over banks
+  __shared__ __align__(16) float sp[4][16 * PS];
+  __shared__ float sm[4][16], sl[4][16];
+  __shared__ float so[4][16][kDh + 4];
+  const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r16 = lane & 15, kq = lane >> 4;
   const int h = blockIdx.x, g = h / (H / KV);
   const int nqkv = (H + 2 * KV) * kDh, d = H * kDh;
-  const int q0 = blockIdx.y * kAttnQ;
-  // all loads of a staging step are issued from clamped rows before the LDS stores (a load
-  // under a branch is waited for at the join)
-  constexpr int kQLoads = kAttnQ * kDh / 256, kKVLoads = 64 * kDh / 256;
+  const int q0 = blockIdx.y * 16;
+  const int nk = min(q0 + 16, M), nch = (nk + 31) / 32;
+  // Q fragments (rows past M read row M - 1: their outputs are not stored)
+  uint4 qh[2], ql[2];
   {
-    float qv[kQLoads];
+    const float* qr = qkv + int64_t(min(q0 + r16, M - 1)) * nqkv + h * kDh + 8 * kq;
 #pragma unroll
-    for (int u = 0; u < kQLoads; ++u) {
-      const int t = threadIdx.x + 256 * u;
-      qv[u] = qkv[int64_t(min(q0 + t / kDh, M - 1)) * nqkv + h * kDh + (t % kDh)];
-    }
-#pragma unroll
-    for (int u = 0; u < kQLoads; ++u) {
-      const int t = threadIdx.x + 256 * u;
-      sq[t] = q0 + t / kDh < M ? qv[u] : 0.f;
+    for (int ks = 0; ks < 2; ++ks) {
+      const float4 a = *reinterpret_cast<const float4*>(qr + 32 * ks);
+      const float4 b = *reinterpret_cast<const float4*>(qr + 32 * ks + 4);
+      const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+      split8(x, qh[ks], ql[ks]);
     }
   }
-  float mx[kQW], ls[kQW], o[kQW];
+  float m[4], l[4];   // rows 4 kq + r: running max and sum (alike in the 16 lanes of the row)
+  f32x4 o[4];         // O columns 16 dt + r16
 #pragma unroll
-  for (int t = 0; t < kQW; ++t) {
-    mx[t] = -INFINITY;
-    ls[t] = 0.f;
-    o[t] = 0.f;
+  for (int r = 0; r < 4; ++r) {
+    m[r] = -INFINITY;
+    l[r] = 0.f;
+    o[r] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
-  const int nchunk = min((q0 + kAttnQ + 63) / 64, (M + 63) / 64);
-  for (int c = 0; c < nchunk; ++c) {
-    float kb[kKVLoads], vb[kKVLoads];
+  float* P = sp[wv];
+  for (int c = wv; c < nch; c += 4) {
+    const int kb = 32 * c;
+    // K rows (B of S: key kb + 16 t + r16, dims 32 ks + 8 kq ..) and V values (B of P V: keys
+    // kb + 8 kq + e, dim 16 dt + r16), all requested before the first MFMA; keys past M read
+    // row M - 1 and are masked
+    float kf[2][2][8], vf[4][8];
 #pragma unroll
-    for (int u = 0; u < kKVLoads; ++u) {
-      const int t = threadIdx.x + 256 * u;
-      const int64_t row = int64_t(min(64 * c + t / kDh, M - 1)) * nqkv;
-      kb[u] = qkv[row + (H + g) * kDh + t % kDh];
-      vb[u] = qkv[row + (H + KV + g) * kDh + t % kDh];
-    }
-    __syncthreads();
+    for (int t = 0; t < 2; ++t) {
+      const float* kr = qkv + int64_t(min(kb + 16 * t + r16, M - 1)) * nqkv + (H + g) * kDh + 8 * kq;
 #pragma unroll
-    for (int u = 0; u < kKVLoads; ++u) {
-      const int t = threadIdx.x + 256 * u;
-      const bool ok = 64 * c + t / kDh < M;
-      sk[(t / kDh) * kKStride + t % kDh] = ok ? kb[u] : 0.f;
-      sv[t] = ok ? vb[u] : 0.f;
-    }
-    __syncthreads();
-    const int j = 64 * c + lane;
-    float s[kQW];
-#pragma unroll
-    for (int t = 0; t < kQW; ++t) s[t] = 0.f;
-    const float4* kr = reinterpret_cast<const float4*>(sk + lane * kKStride);
-#pragma unroll
-    for (int e4 = 0; e4 < kDh / 4; ++e4) {
-      const float4 kk = kr[e4];
-#pragma unroll
-      for (int t = 0; t < kQW; ++t) {
-        const float4 qq = *reinterpret_cast<const float4*>(sq + (kQW * wv + t) * kDh + 4 * e4);
-        s[t] += qq.x * kk.x + qq.y * kk.y + qq.z * kk.z + qq.w * kk.w;
+      for (int ks = 0; ks < 2; ++ks) {
+        const float4 a = *reinterpret_cast<const float4*>(kr + 32 * ks);
+        const float4 b = *reinterpret_cast<const float4*>(kr + 32 * ks + 4);
+        kf[t][ks][0] = a.x; kf[t][ks][1] = a.y; kf[t][ks][2] = a.z; kf[t][ks][3] = a.w;
+        kf[t][ks][4] = b.x; kf[t][ks][5] = b.y; kf[t][ks][6] = b.z; kf[t][ks][7] = b.w;
       }
     }
 #pragma unroll
-    for (int t = 0; t < kQW; ++t) {
-      const int i = q0 + kQW * wv + t;
-      const float sc = (j <= i && j < M) ? s[t] * 0.125f : -INFINITY;
-      const float mn = fmaxf(mx[t], wave_max(sc));
-      const float p = (mn == -INFINITY) ? 0.f : expf(sc - mn);
-      const float ps = wave_sum(p);
-      const float alpha = (mx[t] == -INFINITY) ? 0.f : expf(mx[t] - mn);
-      ls[t] = ls[t] * alpha + ps;
-      o[t] *= alpha;
-      mx[t] = mn;
-      sp[wv][t][lane] = p;
+    for (int e = 0; e < 8; ++e) {
+      const float* vr = qkv + int64_t(min(kb + 8 * kq + e, M - 1)) * nqkv + (H + KV + g) * kDh + r16;
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) vf[dt][e] = vr[16 * dt];
+    }
+    f32x4 s[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      s[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        uint4 kh, kl;
+        split8(kf[t][ks], kh, kl);
+        s[t] = mfma3(qh[ks], ql[ks], kh, kl, s[t]);
+      }
+    }
+    // scale, causal mask, online softmax of rows 4 kq + r over keys kb + 16 t + r16
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int i = q0 + 4 * kq + r;
+      const int j0 = kb + r16, j1 = kb + 16 + r16;
+      const float v0 = (j0 <= i && j0 < M) ? s[0][r] * 0.125f : -INFINITY;
+      const float v1 = (j1 <= i && j1 < M) ? s[1][r] * 0.125f : -INFINITY;
+      const float mn = fmaxf(m[r], row16_max(fmaxf(v0, v1)));
+      const float p0 = mn == -INFINITY ? 0.f : expf(v0 - mn), p1 = mn == -INFINITY ? 0.f : expf(v1 - mn);
+      const float alpha = m[r] == -INFINITY ? 0.f : expf(m[r] - mn);
+      l[r] = l[r] * alpha + row16_sum(p0 + p1);
+      m[r] = mn;
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) o[dt][r] *= alpha;
+      P[(4 * kq + r) * PS + r16] = p0;
+      P[(4 * kq + r) * PS + 16 + r16] = p1;
     }
     __builtin_amdgcn_wave_barrier();
-#pragma unroll 8
-    for (int jj = 0; jj < 64; ++jj) {
-      const float vv = sv[jj * kDh + lane];
+    uint4 ph, pl;
+    {
+      const float4 a = *reinterpret_cast<const float4*>(P + r16 * PS + 8 * kq);
+      const float4 b = *reinterpret_cast<const float4*>(P + r16 * PS + 8 * kq + 4);
+      const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+      split8(x, ph, pl);
+    }
 #pragma unroll
-      for (int t = 0; t < kQW; ++t) o[t] += sp[wv][t][jj] * vv;
+    for (int dt = 0; dt < 4; ++dt) {
+      uint4 vh, vl;
+      split8(vf[dt], vh, vl);
+      o[dt] = mfma3(ph, pl, vh, vl, o[dt]);
     }
     __builtin_amdgcn_wave_barrier();
   }
+  // merge the waves by log-sum-exp
+  if (r16 == 0)
 #pragma unroll
-  for (int t = 0; t < kQW; ++t) {
-    const int i = q0 + kQW * wv + t;
-    if (i < M) put_split(att + act_index(i, perm_pos(h * kDh + lane, d), d, ldx), plane, o[t] / ls[t]);
+    for (int r = 0; r < 4; ++r) {
+      sm[wv][4 * kq + r] = m[r];
+      sl[wv][4 * kq + r] = l[r];
+    }
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) so[wv][4 * kq + r][16 * dt + r16] = o[dt][r];
+  __syncthreads();
+  const int qi = threadIdx.x >> 4, d4 = 4 * (threadIdx.x & 15);
+  float mx = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) mx = fmaxf(mx, sm[w][qi]);
+  float L = 0.f, O[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const float wt = sm[w][qi] == -INFINITY ? 0.f : expf(sm[w][qi] - mx);
+    L += sl[w][qi] * wt;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) O[e] += so[w][qi][d4 + e] * wt;
   }
+  const int i = q0 + qi;
+  if (i < M)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) put_split(att + act_index(i, perm_pos(h * kDh + d4 + e, d), d, ldx), plane, O[e] / L);
 }
 
 // Batched decode: row m (one sequence at position p = pos(m)) and head blockIdx.y attend over
@@ -987,7 +1063,7 @@ static int run_layers(const msd_config* cfg, const Weights& wt, const Rows& rows
                          rows, kc, vc, qkv);
     }
     if (prefill)
-      hipLaunchKernelGGL(mx_attention_prefill, dim3(H, (M + kAttnQ - 1) / kAttnQ), dim3(256), 0, s, qkv, M, H, KV,
+      hipLaunchKernelGGL(mx_attention_prefill, dim3(H, (M + 15) / 16), dim3(256), 0, s, qkv, M, H, KV,
                          att, pd, 0);
     else
       hipLaunchKernelGGL(mx_attention_decode, dim3(M, H), dim3(64 * kAttnWaves), 0, s, qkv, rows, H, KV, kc, vc, att,
