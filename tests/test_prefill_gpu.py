@@ -10,7 +10,7 @@ import torch
 
 from oracle import model as om
 from transformer_amd.configs import M306, TINY
-from transformer_amd.fused_decode_nlayer import (new_kv_packed, prepare_decode_weights_nlayer,
+from transformer_amd.fused_decode_nlayer import (kernel_perm, new_kv_packed, prepare_decode_weights_nlayer,
                                                  unpack_kv_caches, weight_tiles)
 from transformer_amd.multi_sm_decode import Decoder
 from transformer_amd.prefill import Prefiller, prefill_with_kv
@@ -74,21 +74,29 @@ def test_tiny_prefill_matches_oracle(tiny, T, tiles):
 def test_pack_tiles_layout(tiny):
     """msd_pack_tiles against a numpy re-tiling of every projection matrix of every layer: tile
     (n / 16, k / 32) holds rows 16 (n / 16) .. + 16 x columns 32 (k / 32) .. + 32, lane
-    r + 16 q = row r, columns 8 q .. 8 q + 8."""
+    r + 16 q = row r, columns 8 q .. 8 q + 8.  The O and down matrices take their rows in packed
+    order (row n of the copy = row kernel_perm(d)[n]), so their outputs land in the residual's
+    packed order; each layer ends with its two RMSNorm scales in packed order."""
     params, w = tiny
     cfg = TINY
     d, ff, L = cfg["d_model"], cfg["d_ff"], cfg["n_layers"]
     nqkv = (cfg["n_heads"] + 2 * cfg["n_kv_heads"]) * cfg["d_head"]
     got = weight_tiles(w, cfg).view(torch.int16).cpu().numpy()
     packed = w["packed_w"].view(torch.int16).cpu().numpy()
+    perm = kernel_perm(d).cpu().numpy()
     layer = 2 * d + nqkv * d + d * d + 2 * ff * d + d * ff
     want = []
     for l in range(L):
-        off = l * layer + 2 * d
-        for N, K in ((nqkv, d), (d, d), (2 * ff, d), (d, ff)):
-            W = packed[off:off + N * K].reshape(N // 16, 16, K // 32, 4, 8)
-            want.append(W.transpose(0, 2, 3, 1, 4).reshape(-1))
+        base = l * layer
+        off = base + 2 * d
+        for N, K, permuted in ((nqkv, d, False), (d, d, True), (2 * ff, d, False), (d, ff, True)):
+            W = packed[off:off + N * K].reshape(N, K)
+            if permuted:
+                W = W[perm]
+            want.append(W.reshape(N // 16, 16, K // 32, 4, 8).transpose(0, 2, 3, 1, 4).reshape(-1))
             off += N * K
+        want.append(packed[base:base + d][perm])
+        want.append(packed[base + d:base + 2 * d][perm])
     want = np.concatenate(want)
     assert got.shape == want.shape and np.array_equal(got, want)
 

@@ -147,7 +147,7 @@ __device__ __forceinline__ int64_t cache_row(const Rows& r, int m, int p) {
 }
 
 // What mx_gemm_rows does with its final outputs.
-enum Epi { kEpiStore = 0, kEpiSwiglu = 1, kEpiQkv = 2 };
+enum Epi { kEpiStore = 0, kEpiSwiglu = 1, kEpiQkv = 2, kEpiResid = 3 };
 // Operands of the fused epilogues.
 struct EpiArgs {
   uint16_t* act;       // SwiGLU: the down projection's input planes (tile order), lo plane act_plane further
@@ -167,9 +167,33 @@ struct GemmArgs {
   float* out;          // partials [splits][M][N] f32, or [M][ldo] (single split)
   int M, N, K, lda, ldo, splits;
   EpiArgs e;
+  const float* h;          // mx_gemm_rows with the norm folded in: f32 rows (packed order, stride lda)
+  const uint16_t* scale;   // and the norm's scales in packed order
 };
 
 __device__ __forceinline__ bf16x8 as_bf16x8(uint4 u) { return __builtin_bit_cast(bf16x8, u); }
+
+// Eight f32 values as hi/lo bf16 parts (hi = bf16(x), lo = bf16(x - hi)), packed as MFMA operands.
+__device__ __forceinline__ void split8(const float (&x)[8], uint4& hi, uint4& lo) {
+  uint32_t h[4], l[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint16_t h0 = f2bf(x[2 * i]), h1 = f2bf(x[2 * i + 1]);
+    h[i] = uint32_t(h0) | (uint32_t(h1) << 16);
+    l[i] = uint32_t(f2bf(x[2 * i] - bf2f(h0))) | (uint32_t(f2bf(x[2 * i + 1] - bf2f(h1))) << 16);
+  }
+  hi = make_uint4(h[0], h[1], h[2], h[3]);
+  lo = make_uint4(l[0], l[1], l[2], l[3]);
+}
+
+// f32 operands as hi/lo parts on the matrix cores: a b ~ ah bh + ah bl + al bh (the lo lo term,
+// ~2^-16 of the product, is left out).
+__device__ __forceinline__ f32x4 mfma3(uint4 ah, uint4 al, uint4 bh, uint4 bl, f32x4 c) {
+  c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(ah), as_bf16x8(bh), c, 0, 0, 0);
+  c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(ah), as_bf16x8(bl), c, 0, 0, 0);
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(al), as_bf16x8(bh), c, 0, 0, 0);
+}
+
 
 // Four waves as WM x (4 / WM); a wave covers RB 16-row blocks and (WM) 16-column blocks.  TA / TW:
 // the activations / weights in tile order (one 1 KB piece per operand load).
@@ -280,11 +304,17 @@ __device__ __forceinline__ void qkv_pair(float s0, float s1, float c, float sg, 
 // ...) with P steps of loads in flight, and add their tiles through LDS in wave order, so the
 // result is deterministic.  Tiles are dealt XCD-aware: every row tile of a column tile runs on
 // one XCD (workgroup b on XCD b mod 8), which then fetches that column tile's weights into its L2
-// once.  TA / TW as for mx_gemm.  EPI: store the outputs, or finish them in place of
-// mx_swiglu_fin / mx_qkv_fin (column pairs per thread, the same arithmetic, so the same values).
-template <int CT, int P, bool TA, bool TW, int EPI>
+// once.  AM: the A operand as bf16 hi/lo rows (0) or tiles (1) as for mx_gemm, or (2) RMSNorm
+// folded in (model.py:94-98): A = scale * h from the f32 residual rows, split into hi/lo parts in
+// registers, the sum of h^2 of each row taken over the same loads, and every output divided by
+// sqrt(mean(h^2) + 1e-5) in the epilogue.  TW as for mx_gemm.  EPI: store the outputs, add them to
+// out (the residual), or finish them in place of mx_swiglu_fin / mx_qkv_fin (column pairs per
+// thread, the same arithmetic).
+template <int CT, int P, int AM, bool TW, int EPI>
 __global__ __launch_bounds__(256) void mx_gemm_rows(GemmArgs g) {
   __shared__ f32x4 red[4][CT][64];
+  __shared__ float rss[AM == 2 ? 4 : 1][64];   // per-lane sums of h^2, then each row's rms
+  __shared__ float rrms[16];
   // wave-uniform wave index: the step count and its loop stay scalar (a per-lane loop would copy
   // the accumulators out of and back into the AGPRs around every step)
   const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -297,22 +327,32 @@ __global__ __launch_bounds__(256) void mx_gemm_rows(GemmArgs g) {
   const int S = g.K / kBK;
   // rows past M read row M - 1 (row layout) or whatever their tile holds: an MFMA row only
   // feeds its own output row, which is not stored
-  const uint16_t* ar = TA ? g.A + (int64_t(t) * S * 64 + lane) * 8 : g.A + int64_t(min(m0 + r16, g.M - 1)) * g.lda + kq;
+  const uint16_t* ar = AM == 1 ? g.A + (int64_t(t) * S * 64 + lane) * 8 : g.A + int64_t(min(m0 + r16, g.M - 1)) * g.lda + kq;
+  const float* hr = AM == 2 ? g.h + int64_t(min(m0 + r16, g.M - 1)) * g.lda + kq : nullptr;
+  const uint16_t* sr = AM == 2 ? g.scale + kq : nullptr;
   const uint16_t* wr = TW ? g.W + (int64_t(n0 >> 4) * S * 64 + lane) * 8 : g.W + int64_t(n0 + r16) * g.K + kq;
   // element offsets of step ks and of column tile ct
-  const int64_t astep = TA ? 512 : kBK, wstep = TW ? 512 : kBK;
+  const int64_t astep = AM == 1 ? 512 : kBK, wstep = TW ? 512 : kBK;
   const int64_t wtile = TW ? int64_t(S) * 512 : int64_t(16) * g.K;
   const int ns = (S - wv + 3) / 4;   // K steps of this wave (S >= 4: every wave has one)
   f32x4 acc[CT];
 #pragma unroll
   for (int ct = 0; ct < CT; ++ct) acc[ct] = f32x4{0.f, 0.f, 0.f, 0.f};
-  uint4 a[P], al[P], w[P][CT];
+  uint4 a[P], al[P], w[P][CT], sx[P];
+  float4 hx[P][2];
+  float ss = 0.f;
   // step i of this wave, clamped to its last: loads stay unconditional, so no wait lands at a
   // branch join
   auto load = [&](int p, int i) {
     const int ks = wv + 4 * min(i, ns - 1);
-    a[p] = *reinterpret_cast<const uint4*>(ar + ks * astep);
-    al[p] = *reinterpret_cast<const uint4*>(ar + g.a_plane + ks * astep);
+    if constexpr (AM == 2) {
+      hx[p][0] = *reinterpret_cast<const float4*>(hr + ks * kBK);
+      hx[p][1] = *reinterpret_cast<const float4*>(hr + ks * kBK + 4);
+      sx[p] = *reinterpret_cast<const uint4*>(sr + ks * kBK);
+    } else {
+      a[p] = *reinterpret_cast<const uint4*>(ar + ks * astep);
+      al[p] = *reinterpret_cast<const uint4*>(ar + g.a_plane + ks * astep);
+    }
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) w[p][ct] = *reinterpret_cast<const uint4*>(wr + ct * wtile + ks * wstep);
   };
@@ -324,7 +364,24 @@ __global__ __launch_bounds__(256) void mx_gemm_rows(GemmArgs g) {
 #pragma unroll
     for (int p = 0; p < P; ++p) {
       const bool live = i0 + p < ns;
-      const uint4 x = live ? a[p] : make_uint4(0, 0, 0, 0), xl = live ? al[p] : make_uint4(0, 0, 0, 0);
+      uint4 x, xl;
+      if constexpr (AM == 2) {
+        const float hv[8] = {hx[p][0].x, hx[p][0].y, hx[p][0].z, hx[p][0].w,
+                             hx[p][1].x, hx[p][1].y, hx[p][1].z, hx[p][1].w};
+        const uint32_t sw[4] = {sx[p].x, sx[p].y, sx[p].z, sx[p].w};
+        float xs[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const uint32_t u = sw[e >> 1];
+          xs[e] = __uint_as_float((e & 1) ? (u & 0xffff0000u) : (u << 16)) * hv[e];
+          ss += live ? hv[e] * hv[e] : 0.f;
+        }
+        split8(xs, x, xl);
+      } else {
+        x = a[p];
+        xl = al[p];
+      }
+      if (!live) x = xl = make_uint4(0, 0, 0, 0);
 #pragma unroll
       for (int ct = 0; ct < CT; ++ct) {
         acc[ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(x), as_bf16x8(w[p][ct]), acc[ct], 0, 0, 0);
@@ -335,21 +392,42 @@ __global__ __launch_bounds__(256) void mx_gemm_rows(GemmArgs g) {
   }
 #pragma unroll
   for (int ct = 0; ct < CT; ++ct) red[wv][ct][lane] = acc[ct];
+  if constexpr (AM == 2) rss[wv][lane] = ss;
   __syncthreads();
+  if constexpr (AM == 2) {   // row r's sum of h^2: lanes r + 16 q of every wave, in a fixed order
+    if (threadIdx.x < 16) {
+      float sum = 0.f;
+#pragma unroll
+      for (int w2 = 0; w2 < 4; ++w2)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) sum += rss[w2][threadIdx.x + 16 * q];
+      rrms[threadIdx.x] = sqrtf(sum / float(g.K) + 1e-5f);
+    }
+    __syncthreads();
+  }
   // D layout of a 16 x 16 tile: lane holds rows 4 (lane / 16) + r of column lane % 16
-  if constexpr (EPI == kEpiStore) {
+  if constexpr (EPI == kEpiStore || EPI == kEpiResid) {
     for (int idx = threadIdx.x; idx < CT * 256; idx += 256) {
       const int ct = idx >> 8, e = idx & 255, r = e >> 6, l = e & 63;
-      const float v = ((red[0][ct][l][r] + red[1][ct][l][r]) + red[2][ct][l][r]) + red[3][ct][l][r];
+      float v = ((red[0][ct][l][r] + red[1][ct][l][r]) + red[2][ct][l][r]) + red[3][ct][l][r];
+      if constexpr (AM == 2) v = v / rrms[4 * (l >> 4) + r];
       const int row = m0 + 4 * (l >> 4) + r;
-      if (row < g.M) g.out[int64_t(row) * g.ldo + n0 + 16 * ct + (l & 15)] = v;
+      float* o = g.out + int64_t(row) * g.ldo + n0 + 16 * ct + (l & 15);
+      if (row < g.M) {
+        if constexpr (EPI == kEpiResid) *o += v;
+        else *o = v;
+      }
     }
   } else {
     // one column pair (lanes l, l + 1 of a row) per thread
     for (int idx = threadIdx.x; idx < CT * 128; idx += 256) {
       const int ct = idx >> 7, e = idx & 127, r = e >> 5, l = 16 * ((e >> 3) & 3) + 2 * (e & 7);
-      const float v0 = ((red[0][ct][l][r] + red[1][ct][l][r]) + red[2][ct][l][r]) + red[3][ct][l][r];
-      const float v1 = ((red[0][ct][l + 1][r] + red[1][ct][l + 1][r]) + red[2][ct][l + 1][r]) + red[3][ct][l + 1][r];
+      float v0 = ((red[0][ct][l][r] + red[1][ct][l][r]) + red[2][ct][l][r]) + red[3][ct][l][r];
+      float v1 = ((red[0][ct][l + 1][r] + red[1][ct][l + 1][r]) + red[2][ct][l + 1][r]) + red[3][ct][l + 1][r];
+      if constexpr (AM == 2) {
+        v0 = v0 / rrms[4 * (l >> 4) + r];
+        v1 = v1 / rrms[4 * (l >> 4) + r];
+      }
       const int row = m0 + 4 * (l >> 4) + r, col = n0 + 16 * ct + (l & 15);
       if (row >= g.M) continue;
       const EpiArgs& ea = g.e;
@@ -382,10 +460,11 @@ __device__ __forceinline__ float block_sum256(float v, float* red) {
 // Row blockIdx.x + row0: h += sum_z part[z] (z in order), then
 // xn[j] = scale[i] * (h[i] / sqrt(mean(h^2) + 1e-5)) as hi/lo bf16 parts (planes `plane` apart),
 // with i the input element at position j of the packed row layout (model.py:94-98).  Every partial is requested before
-// the first is added, so the sum costs one memory round trip.
+// the first is added, so the sum costs one memory round trip.  With packed, h holds the row in
+// packed order (element i at position perm_pos(i)) and no partials are added.
 __global__ __launch_bounds__(kNormThreads) void mx_norm(float* h, const float* part, int splits, int M, int d,
                                                         const uint16_t* scale, uint16_t* xn, int64_t plane,
-                                                        int row0, int ldx) {
+                                                        int row0, int ldx, int packed) {
   constexpr int NE = kMaxRows / kNormThreads;
   __shared__ float red[4];
   __shared__ __align__(16) float hs[kMaxRows];
@@ -426,12 +505,15 @@ __global__ __launch_bounds__(kNormThreads) void mx_norm(float* h, const float* p
 #pragma unroll
   for (int q = 0; q < NE; ++q) {
     const int j = threadIdx.x + kNormThreads * q;
-    if (j < d) put_split(xn + act_index(blockIdx.x, j, d, ldx), plane, bf2f(sc[q]) * (hs[perm_elem(j, d)] / r));
+    if (j < d)
+      put_split(xn + act_index(blockIdx.x, j, d, ldx), plane, bf2f(sc[q]) * (hs[packed ? j : perm_elem(j, d)] / r));
   }
 }
 
+// Row m of the residual stream: the embedding of tokens[m] (element n at n, or with packed at its
+// packed position perm_pos(n)).
 __global__ __launch_bounds__(256) void mx_embed(const uint16_t* emb, const int32_t* tokens, int d, float* h,
-                                                int32_t* status, int V) {
+                                                int32_t* status, int V, int packed) {
   const int m = blockIdx.x;
   int t = tokens[m];
   if (t < 0 || t >= V) {
@@ -445,7 +527,7 @@ __global__ __launch_bounds__(256) void mx_embed(const uint16_t* emb, const int32
 #pragma unroll
   for (int i = 0; i < NE; ++i) {
     const int n = threadIdx.x + 256 * i;
-    if (n < d) h[int64_t(m) * d + n] = bf2f(e[i]);
+    if (n < d) h[int64_t(m) * d + (packed ? perm_pos(n, d) : n)] = bf2f(e[i]);
   }
 }
 
@@ -509,27 +591,6 @@ __global__ __launch_bounds__(256) void mx_swiglu_fin(const float* part, int spli
     }
   put_split(act + act_index(m, perm_pos(f, F), F, ldx), plane, swiglu(g0, u0));
   put_split(act + act_index(m, perm_pos(f + 1, F), F, ldx), plane, swiglu(g1, u1));
-}
-
-// Eight f32 values as hi/lo bf16 parts (hi = bf16(x), lo = bf16(x - hi)), packed as MFMA operands.
-__device__ __forceinline__ void split8(const float (&x)[8], uint4& hi, uint4& lo) {
-  uint32_t h[4], l[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint16_t h0 = f2bf(x[2 * i]), h1 = f2bf(x[2 * i + 1]);
-    h[i] = uint32_t(h0) | (uint32_t(h1) << 16);
-    l[i] = uint32_t(f2bf(x[2 * i] - bf2f(h0))) | (uint32_t(f2bf(x[2 * i + 1] - bf2f(h1))) << 16);
-  }
-  hi = make_uint4(h[0], h[1], h[2], h[3]);
-  lo = make_uint4(l[0], l[1], l[2], l[3]);
-}
-
-// f32 operands as hi/lo parts on the matrix cores: a b ~ ah bh + ah bl + al bh (the lo lo term,
-// ~2^-16 of the product, is left out).
-__device__ __forceinline__ f32x4 mfma3(uint4 ah, uint4 al, uint4 bh, uint4 bl, f32x4 c) {
-  c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(ah), as_bf16x8(bh), c, 0, 0, 0);
-  c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(ah), as_bf16x8(bl), c, 0, 0, 0);
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(al), as_bf16x8(bh), c, 0, 0, 0);
 }
 
 // Reductions over the 16 lanes of a DPP row, every lane receiving the result (rotations by 1, 2,
@@ -853,17 +914,28 @@ __global__ void mx_sanitize_rows(const int32_t* pos, int fixed_pos, const int32_
 }
 
 // One 16-byte piece per thread of the tile copy of an N x K matrix W (rows in packed order): piece
-// p is lane p % 64 of tile p / 64 = (n / 16) (K / 32) + k / 32, i.e. row 16 (tile / (K / 32)) + lane % 16
-// at positions 32 (tile % (K / 32)) + 8 (lane / 16) .. + 8.
-__global__ __launch_bounds__(256) void mx_pack_tiles(const uint16_t* W, int N, int K, uint16_t* T) {
+// p is lane p % 64 of tile p / 64 = (n / 16) (K / 32) + k / 32, i.e. row n = 16 (tile / (K / 32)) +
+// lane % 16 at positions 32 (tile % (K / 32)) + 8 (lane / 16) .. + 8.  With perm, row n of the copy
+// is row perm_elem(n, N) of W: output column n is then element perm_elem(n) of an N-long vector,
+// i.e. its packed position n (the O and down projections, whose outputs add to the residual).
+__global__ __launch_bounds__(256) void mx_pack_tiles(const uint16_t* W, int N, int K, int perm, uint16_t* T) {
   const int64_t p = int64_t(blockIdx.x) * 256 + threadIdx.x;
   const int S = K / kBK;
   if (p >= int64_t(N) * S * 64) return;
   const int lane = int(p & 63);
   const int64_t tile = p >> 6;
-  const int64_t n = 16 * (tile / S) + (lane & 15);
+  const int n = int(16 * (tile / S)) + (lane & 15);
+  const int64_t src = perm ? perm_elem(n, N) : n;
   const int k = kBK * int(tile % S) + 8 * (lane >> 4);
-  *reinterpret_cast<uint4*>(T + p * 8) = *reinterpret_cast<const uint4*>(W + n * K + k);
+  *reinterpret_cast<uint4*>(T + p * 8) = *reinterpret_cast<const uint4*>(W + src * K + k);
+}
+
+// A layer's two RMSNorm scales in packed order: out[j] = scale[perm_elem(j, d)] for [ln1 | ln2].
+__global__ __launch_bounds__(256) void mx_pack_scales(const uint16_t* ln, int d, uint16_t* out) {
+  const int j = blockIdx.x * 256 + threadIdx.x;
+  if (j >= 2 * d) return;
+  const int half = j >= d ? d : 0;
+  out[j] = ln[half + perm_elem(j - half, d)];
 }
 
 // ---------------------------------------------------------------- host side
@@ -882,12 +954,15 @@ constexpr int kRowsMaxN = 4096;
 // Column tiles (of 16) per workgroup of mx_gemm_rows: the widest that still gives about one
 // workgroup per compute unit; 0 when the projection has too few output tiles for it (few rows),
 // or too short a K for every wave to take a step, and the split-K kernel runs instead.
+// With the weights in tile order (tw) every projection takes it (the fused epilogues and the
+// folded norms live there): the widest that gives about one workgroup per compute unit, else 1.
 static int rows_ct(int M, int N, int K, bool tw) {
   const int T = (M + 15) / 16, n16 = N / 16;
-  if (K / kBK < 4 || M < 48 || (N > kRowsMaxN && !tw)) return 0;
+  if (K / kBK < 4) return 0;
+  if (!tw && (M < 48 || N > kRowsMaxN)) return 0;
   for (int ct : {8, 6, 4, 3, 2, 1})
     if (n16 % ct == 0 && T * (n16 / ct) >= 224) return ct;
-  return 0;
+  return tw ? 1 : 0;
 }
 
 // K splits of a projection: 1 for mx_gemm_rows, else enough split-K workgroups to occupy every
@@ -943,15 +1018,15 @@ static bool mx_config_ok(const msd_config* c) {
   return true;
 }
 
-template <bool TA, bool TW, int EPI = kEpiStore>
+template <int AM, bool TW, int EPI = kEpiStore>
 static void launch_rows(int ct, dim3 grid, hipStream_t s, const GemmArgs& g) {
   switch (ct) {
-    case 8: hipLaunchKernelGGL((mx_gemm_rows<8, 3, TA, TW, EPI>), grid, dim3(256), 0, s, g); break;
-    case 6: hipLaunchKernelGGL((mx_gemm_rows<6, 3, TA, TW, EPI>), grid, dim3(256), 0, s, g); break;
-    case 4: hipLaunchKernelGGL((mx_gemm_rows<4, 4, TA, TW, EPI>), grid, dim3(256), 0, s, g); break;
-    case 3: hipLaunchKernelGGL((mx_gemm_rows<3, 4, TA, TW, EPI>), grid, dim3(256), 0, s, g); break;
-    case 2: hipLaunchKernelGGL((mx_gemm_rows<2, 4, TA, TW, EPI>), grid, dim3(256), 0, s, g); break;
-    default: hipLaunchKernelGGL((mx_gemm_rows<1, 4, TA, TW, EPI>), grid, dim3(256), 0, s, g); break;
+    case 8: hipLaunchKernelGGL((mx_gemm_rows<8, 3, AM, TW, EPI>), grid, dim3(256), 0, s, g); break;
+    case 6: hipLaunchKernelGGL((mx_gemm_rows<6, 3, AM, TW, EPI>), grid, dim3(256), 0, s, g); break;
+    case 4: hipLaunchKernelGGL((mx_gemm_rows<4, 4, AM, TW, EPI>), grid, dim3(256), 0, s, g); break;
+    case 3: hipLaunchKernelGGL((mx_gemm_rows<3, 4, AM, TW, EPI>), grid, dim3(256), 0, s, g); break;
+    case 2: hipLaunchKernelGGL((mx_gemm_rows<2, 4, AM, TW, EPI>), grid, dim3(256), 0, s, g); break;
+    default: hipLaunchKernelGGL((mx_gemm_rows<1, 4, AM, TW, EPI>), grid, dim3(256), 0, s, g); break;
   }
 }
 
@@ -967,31 +1042,34 @@ static void launch_splitk(int bm, dim3 grid, hipStream_t s, const GemmArgs& g) {
 // rows_ok: mx_gemm_rows may run (single split only).  The tied logits pass false: one row and
 // every row then come from the same kernel and summation order, so the last row's logits are
 // bitwise the same either way.
-// fused(): whether a projection's epilogue can run in the GEMM (mx_gemm_rows over tile-order
-// operands); `epi` then selects it and `ea` carries its operands.
-static bool fused(int M, int N, int K, bool tw) { return tw && rows_ct(M, N, K, true) > 0; }
-
+// C = A W^T split over K: partials [splits][M][N] (pass ldo = N), or with splits == 1 rows
+// of stride ldo.  lda == 0: A in tile order (act_index); tw: W in tile order (msd_pack_tiles).
+// hn: A is RMSNorm(h) folded into mx_gemm_rows (f32 rows hn of stride lda, packed-order scales
+// `scale`).  epi / ea: the epilogue of mx_gemm_rows (tile-order weights only).
+// rows_ok: mx_gemm_rows may run (single split only).  The tied logits pass false: one row and
+// every row then come from the same kernel and summation order, so the last row's logits are
+// bitwise the same either way.
 static hipError_t gemm(const uint16_t* A, int64_t a_plane, int lda, const uint16_t* W, bool tw, int M, int N, int K,
                        float* out, int ldo, int splits, hipStream_t s, bool rows_ok = true, int epi = kEpiStore,
-                       const EpiArgs* ea = nullptr) {
-  GemmArgs g{A, a_plane, W, out, M, N, K, lda, ldo, splits, ea ? *ea : EpiArgs{}};
-  const bool ta = lda == 0;
-  const int ct = splits == 1 && rows_ok ? rows_ct(M, N, K, tw) : 0;
-  if (epi != kEpiStore && !(ct > 0 && ta && tw && ea)) return hipErrorInvalidValue;
+                       const EpiArgs* ea = nullptr, const float* hn = nullptr, const uint16_t* scale = nullptr) {
+  GemmArgs g{A, a_plane, W, out, M, N, K, lda, ldo, splits, ea ? *ea : EpiArgs{}, hn, scale};
+  const int am = hn ? 2 : (lda == 0 ? 1 : 0);
+  const int ct = splits == 1 && rows_ok && am > 0 ? rows_ct(M, N, K, tw) : 0;
+  if ((epi != kEpiStore || am == 2) && !(ct > 0 && tw)) return hipErrorInvalidValue;
+  if ((epi == kEpiQkv || epi == kEpiSwiglu) && !ea) return hipErrorInvalidValue;
   if (ct > 0) {
     const int T = (M + 15) / 16, C = N / (16 * ct);
     const dim3 grid(8 * ((C + 7) / 8) * T);
-    if (epi == kEpiSwiglu) launch_rows<true, true, kEpiSwiglu>(ct, grid, s, g);
-    else if (epi == kEpiQkv) launch_rows<true, true, kEpiQkv>(ct, grid, s, g);
-    else if (ta && tw) launch_rows<true, true>(ct, grid, s, g);
-    else if (ta) launch_rows<true, false>(ct, grid, s, g);
-    else launch_rows<false, false>(ct, grid, s, g);
+    if (am == 2 && epi == kEpiQkv) launch_rows<2, true, kEpiQkv>(ct, grid, s, g);
+    else if (am == 2 && epi == kEpiSwiglu) launch_rows<2, true, kEpiSwiglu>(ct, grid, s, g);
+    else if (am == 1 && tw && epi == kEpiResid) launch_rows<1, true, kEpiResid>(ct, grid, s, g);
+    else if (am == 1 && !tw && epi == kEpiStore) launch_rows<1, false>(ct, grid, s, g);
+    else return hipErrorInvalidValue;
     return hipGetLastError();
   }
   const int bm = bm_for(M);
   const dim3 grid(N / kBN, (M + bm - 1) / bm, splits);
-  if (ta && tw) launch_splitk<true, true>(bm, grid, s, g);
-  else if (ta) launch_splitk<true, false>(bm, grid, s, g);
+  if (am == 1) launch_splitk<true, false>(bm, grid, s, g);
   else launch_splitk<false, false>(bm, grid, s, g);
   return hipGetLastError();
 }
@@ -1005,11 +1083,12 @@ struct Weights {
   const uint16_t* tiles;   // the projections in tile order (msd_pack_tiles), or NULL
 };
 
-// Elements of one layer's projections in the tile copy: QKV, O, gate/up, down, each N x K in
-// tile order, layer after layer.
+// Elements of one layer in the tile copy: QKV, O, gate/up, down, each N x K in tile order (the
+// O and down rows permuted so that their outputs come in packed order), then the two RMSNorm
+// scales in packed order; layer after layer.
 static int64_t tile_layer_elems(const msd_config* c) {
   const int64_t d = c->d_model, ff = c->d_ff, nqkv = int64_t(c->n_heads + 2 * c->n_kv_heads) * kDh;
-  return nqkv * d + d * d + 2 * ff * d + d * ff;
+  return nqkv * d + d * d + 2 * ff * d + d * ff + 2 * d;
 }
 
 // The layer stack over M rows whose residual stream is already in h; leaves the last
@@ -1031,56 +1110,62 @@ static int run_layers(const msd_config* cfg, const Weights& wt, const Rows& rows
   const bool tw = wt.tiles != nullptr;
   const int sq = splits_for(M, nqkv, d, bm, tw), so = splits_for(M, d, d, bm, tw),
             sg = splits_for(M, 2 * ff, d, bm, tw), sd = splits_for(M, d, ff, bm, tw);
-  // the projections' weights: tile order when the tile copy is given, else the packed rows
-  const int64_t toff_o = int64_t(nqkv) * d, toff_gu = toff_o + int64_t(d) * d, toff_dn = toff_gu + 2 * int64_t(ff) * d;
+  // the tile copy's per-layer offsets
+  const int64_t toff_o = int64_t(nqkv) * d, toff_gu = toff_o + int64_t(d) * d, toff_dn = toff_gu + 2 * int64_t(ff) * d,
+                toff_sc = toff_dn + int64_t(d) * ff;
   int pending = 0;
   err = hipSuccess;
   for (int l = 0; l < cfg->n_layers && err == hipSuccess; ++l) {
     const uint16_t* Wl = wt.w + int64_t(l) * layer;
-    const uint16_t* Tl = tw ? wt.tiles + int64_t(l) * tile_layer_elems(cfg) : nullptr;
-    const uint16_t* Wqkv = tw ? Tl : Wl + off_qkv;
-    const uint16_t* Wo = tw ? Tl + toff_o : Wl + off_o;
-    const uint16_t* Wgu = tw ? Tl + toff_gu : Wl + off_gu;
-    const uint16_t* Wdn = tw ? Tl + toff_dn : Wl + off_dn;
     uint16_t* kc = kv + int64_t(l) * 2 * KV * rows.pool * kDh;
     uint16_t* vc = kc + int64_t(KV) * rows.pool * kDh;
     // activation planes in tile order (ldx 0), the lo planes after the hi planes
     const int64_t pd = int64_t(pad16(M)) * d, pf = int64_t(pad16(M)) * ff;
-    hipLaunchKernelGGL(mx_norm, dim3(M), dim3(kNormThreads), 0, s, h, part, pending, M, d, Wl, xn, pd, 0, 0);
-    if (fused(M, nqkv, d, tw)) {   // RoPE, q/k/v and the cache rows in the GEMM's epilogue
-      EpiArgs ea{};
-      ea.rope = wt.rope;
-      ea.rows = rows;
-      ea.kc = kc;
-      ea.vc = vc;
-      ea.qkv = qkv;
-      ea.H = H;
-      ea.KV = KV;
-      if ((err = gemm(xn, pd, 0, Wqkv, tw, M, nqkv, d, part, nqkv, 1, s, true, kEpiQkv, &ea)) != hipSuccess) break;
-    } else {
-      if ((err = gemm(xn, pd, 0, Wqkv, tw, M, nqkv, d, part, nqkv, sq, s)) != hipSuccess) break;
-      hipLaunchKernelGGL(mx_qkv_fin, dim3(M, (nqkv / 4 + 255) / 256), dim3(256), 0, s, part, sq, M, H, KV, wt.rope,
-                         rows, kc, vc, qkv);
+    if (tw) {
+      // Five kernels per layer over the tile copy, h in packed order: QKV with RMSNorm1 folded in
+      // and q/k/v, RoPE and the cache rows in its epilogue; attention; O adding to h; gate/up with
+      // RMSNorm2 folded in and SwiGLU in its epilogue; down adding to h.
+      const uint16_t* Tl = wt.tiles + int64_t(l) * tile_layer_elems(cfg);
+      EpiArgs eq{};
+      eq.rope = wt.rope;
+      eq.rows = rows;
+      eq.kc = kc;
+      eq.vc = vc;
+      eq.qkv = qkv;
+      eq.H = H;
+      eq.KV = KV;
+      if ((err = gemm(nullptr, 0, d, Tl, true, M, nqkv, d, nullptr, 0, 1, s, true, kEpiQkv, &eq, h, Tl + toff_sc)) !=
+          hipSuccess)
+        break;
+      if (prefill)
+        hipLaunchKernelGGL(mx_attention_prefill, dim3(H, (M + 15) / 16), dim3(256), 0, s, qkv, M, H, KV, att, pd, 0);
+      else
+        hipLaunchKernelGGL(mx_attention_decode, dim3(M, H), dim3(64 * kAttnWaves), 0, s, qkv, rows, H, KV, kc, vc,
+                           att, pd, 0);
+      if ((err = gemm(att, pd, 0, Tl + toff_o, true, M, d, d, h, d, 1, s, true, kEpiResid)) != hipSuccess) break;
+      EpiArgs eg{};
+      eg.act = act;
+      eg.act_plane = pf;
+      if ((err = gemm(nullptr, 0, d, Tl + toff_gu, true, M, 2 * ff, d, nullptr, 0, 1, s, true, kEpiSwiglu, &eg, h,
+                      Tl + toff_sc + d)) != hipSuccess)
+        break;
+      if ((err = gemm(act, pf, 0, Tl + toff_dn, true, M, d, ff, h, d, 1, s, true, kEpiResid)) != hipSuccess) break;
+      continue;
     }
+    hipLaunchKernelGGL(mx_norm, dim3(M), dim3(kNormThreads), 0, s, h, part, pending, M, d, Wl, xn, pd, 0, 0, 0);
+    if ((err = gemm(xn, pd, 0, Wl + off_qkv, false, M, nqkv, d, part, nqkv, sq, s)) != hipSuccess) break;
+    hipLaunchKernelGGL(mx_qkv_fin, dim3(M, (nqkv / 4 + 255) / 256), dim3(256), 0, s, part, sq, M, H, KV, wt.rope, rows,
+                       kc, vc, qkv);
     if (prefill)
-      hipLaunchKernelGGL(mx_attention_prefill, dim3(H, (M + 15) / 16), dim3(256), 0, s, qkv, M, H, KV,
-                         att, pd, 0);
+      hipLaunchKernelGGL(mx_attention_prefill, dim3(H, (M + 15) / 16), dim3(256), 0, s, qkv, M, H, KV, att, pd, 0);
     else
       hipLaunchKernelGGL(mx_attention_decode, dim3(M, H), dim3(64 * kAttnWaves), 0, s, qkv, rows, H, KV, kc, vc, att,
                          pd, 0);
-    if ((err = gemm(att, pd, 0, Wo, tw, M, d, d, part, d, so, s)) != hipSuccess) break;
-    hipLaunchKernelGGL(mx_norm, dim3(M), dim3(kNormThreads), 0, s, h, part, so, M, d, Wl + off_ln2, xn, pd, 0, 0);
-    if (fused(M, 2 * ff, d, tw)) {   // SwiGLU in the GEMM's epilogue
-      EpiArgs ea{};
-      ea.act = act;
-      ea.act_plane = pf;
-      if ((err = gemm(xn, pd, 0, Wgu, tw, M, 2 * ff, d, part, 2 * ff, 1, s, true, kEpiSwiglu, &ea)) != hipSuccess)
-        break;
-    } else {
-      if ((err = gemm(xn, pd, 0, Wgu, tw, M, 2 * ff, d, part, 2 * ff, sg, s)) != hipSuccess) break;
-      hipLaunchKernelGGL(mx_swiglu_fin, dim3(M, (ff / 2 + 255) / 256), dim3(256), 0, s, part, sg, M, ff, act, pf, 0);
-    }
-    if ((err = gemm(act, pf, 0, Wdn, tw, M, d, ff, part, d, sd, s)) != hipSuccess) break;
+    if ((err = gemm(att, pd, 0, Wl + off_o, false, M, d, d, part, d, so, s)) != hipSuccess) break;
+    hipLaunchKernelGGL(mx_norm, dim3(M), dim3(kNormThreads), 0, s, h, part, so, M, d, Wl + off_ln2, xn, pd, 0, 0, 0);
+    if ((err = gemm(xn, pd, 0, Wl + off_gu, false, M, 2 * ff, d, part, 2 * ff, sg, s)) != hipSuccess) break;
+    hipLaunchKernelGGL(mx_swiglu_fin, dim3(M, (ff / 2 + 255) / 256), dim3(256), 0, s, part, sg, M, ff, act, pf, 0);
+    if ((err = gemm(act, pf, 0, Wl + off_dn, false, M, d, ff, part, d, sd, s)) != hipSuccess) break;
     pending = sd;
   }
   if (err == hipSuccess) err = hipGetLastError();
@@ -1139,14 +1224,15 @@ static int32_t prefill_impl(const msd_config* cfg, const Weights& wt, const int3
                        cfg->context_len, pool_pages, nullptr, pages, status);
   Rows rows{M, nullptr, 0, page_table ? pages : nullptr, max_pages, page_table ? pool_pages * kPage : cfg->context_len,
             start};
-  hipLaunchKernelGGL(mx_embed, dim3(M), dim3(256), 0, s, wt.emb, tokens, d, h, status, V);
+  const int packed = wt.tiles != nullptr;   // the tile path keeps h in packed order
+  hipLaunchKernelGGL(mx_embed, dim3(M), dim3(256), 0, s, wt.emb, tokens, d, h, status, V, packed);
   hipError_t err;
   const int pending = run_layers(cfg, wt, rows, static_cast<uint16_t*>(kv), L, ws, start == 0, s, err);
   if (err != hipSuccess) return MSD_E_HIP;
   // final norm of the rows whose logits are wanted, then the tied output projection
   const int r0 = logits_all ? 0 : M - 1, nr = M - r0;
   hipLaunchKernelGGL(mx_norm, dim3(nr), dim3(kNormThreads), 0, s, h, part, pending, M, d, wt.lnf, xn,
-                     int64_t(nr) * d, r0, d);
+                     int64_t(nr) * d, r0, d, packed);
   if (gemm(xn, int64_t(nr) * d, d, wt.outp, false, nr, V, d, logits_all ? logits_all : logits_last, V, 1, s, false) !=
       hipSuccess)
     return MSD_E_HIP;
@@ -1173,19 +1259,21 @@ extern "C" int32_t msd_pack_tiles(const msd_config* cfg, const void* packed_w, v
   const int d = cfg->d_model, ff = cfg->d_ff, nqkv = (cfg->n_heads + 2 * cfg->n_kv_heads) * kDh;
   const int64_t off_qkv = 2 * int64_t(d), off_o = off_qkv + int64_t(nqkv) * d, off_gu = off_o + int64_t(d) * d,
                 off_dn = off_gu + 2 * int64_t(ff) * d, layer = off_dn + int64_t(d) * ff;
-  const struct { int64_t src, dst; int N, K; } mats[4] = {
-      {off_qkv, 0, nqkv, d},
-      {off_o, int64_t(nqkv) * d, d, d},
-      {off_gu, int64_t(nqkv) * d + int64_t(d) * d, 2 * ff, d},
-      {off_dn, int64_t(nqkv) * d + int64_t(d) * d + 2 * int64_t(ff) * d, d, ff}};
+  const int64_t dst_o = int64_t(nqkv) * d, dst_gu = dst_o + int64_t(d) * d, dst_dn = dst_gu + 2 * int64_t(ff) * d,
+                dst_sc = dst_dn + int64_t(d) * ff;
+  const struct { int64_t src, dst; int N, K, perm; } mats[4] = {
+      {off_qkv, 0, nqkv, d, 0}, {off_o, dst_o, d, d, 1}, {off_gu, dst_gu, 2 * ff, d, 0}, {off_dn, dst_dn, d, ff, 1}};
   const uint16_t* w = static_cast<const uint16_t*>(packed_w);
   uint16_t* t = static_cast<uint16_t*>(tiles);
-  for (int l = 0; l < cfg->n_layers; ++l)
+  for (int l = 0; l < cfg->n_layers; ++l) {
+    uint16_t* tl = t + l * tile_layer_elems(cfg);
     for (const auto& m : mats) {
       const int64_t pieces = int64_t(m.N) * m.K / 8;
-      hipLaunchKernelGGL(mx_pack_tiles, dim3(unsigned((pieces + 255) / 256)), dim3(256), 0, s,
-                         w + l * layer + m.src, m.N, m.K, t + l * tile_layer_elems(cfg) + m.dst);
+      hipLaunchKernelGGL(mx_pack_tiles, dim3(unsigned((pieces + 255) / 256)), dim3(256), 0, s, w + l * layer + m.src,
+                         m.N, m.K, m.perm, tl + m.dst);
     }
+    hipLaunchKernelGGL(mx_pack_scales, dim3((2 * d + 255) / 256), dim3(256), 0, s, w + l * layer, d, tl + dst_sc);
+  }
   return hipGetLastError() == hipSuccess ? MSD_OK : MSD_E_HIP;
 }
 
@@ -1283,12 +1371,13 @@ extern "C" int32_t msd_batch_decode_step(const msd_config* cfg, const void* toke
   hipLaunchKernelGGL(mx_sanitize_rows, dim3((M + 255) / 256), dim3(256), 0, s, positions, 0, page_tables, M, max_pages,
                      cfg->context_len, pool_pages, rowpos, pages, status);
   Rows rows{M, rowpos, 1, pages, max_pages, pool_pages * kPage, 0};
-  hipLaunchKernelGGL(mx_embed, dim3(M), dim3(256), 0, s, wt.emb, tokens, d, h, status, V);
+  const int packed = wt.tiles != nullptr;
+  hipLaunchKernelGGL(mx_embed, dim3(M), dim3(256), 0, s, wt.emb, tokens, d, h, status, V, packed);
   hipError_t err;
   const int pending = run_layers(cfg, wt, rows, static_cast<uint16_t*>(kv_pool), L, ws, false, s, err);
   if (err != hipSuccess) return MSD_E_HIP;
   hipLaunchKernelGGL(mx_norm, dim3(M), dim3(kNormThreads), 0, s, h, part, pending, M, d, wt.lnf, xn, int64_t(M) * d, 0,
-                     d);
+                     d, packed);
   if (gemm(xn, int64_t(M) * d, d, wt.outp, false, M, V, d, logits, V, 1, s, false) != hipSuccess) return MSD_E_HIP;
   hipLaunchKernelGGL(mx_argmax, dim3(M), dim3(1024), 0, s, logits, V, V, next_tokens, status);
   return hipGetLastError() == hipSuccess ? MSD_OK : MSD_E_HIP;
