@@ -167,8 +167,8 @@ struct GemmArgs {
   float* out;          // partials [splits][M][N] f32, or [M][ldo] (single split)
   int M, N, K, lda, ldo, splits;
   EpiArgs e;
-  const float* h;          // mx_gemm_rows with the norm folded in: f32 rows (packed order, stride lda)
-  const uint16_t* scale;   // and the norm's scales in packed order
+  const float* h;          // mx_gemm_rows with the norm folded in: the f32 residual (packed positions in
+  const uint16_t* scale;   // tile order, act_index) and the norm's scales in packed order
 };
 
 __device__ __forceinline__ bf16x8 as_bf16x8(uint4 u) { return __builtin_bit_cast(bf16x8, u); }
@@ -298,18 +298,18 @@ __device__ __forceinline__ void qkv_pair(float s0, float s1, float c, float sg, 
   }
 }
 
-// C = A W^T for many rows (M >= 48): a workgroup owns 16 rows x 16 CT columns over the whole of K,
-// so it streams CT * 16 complete weight rows (contiguous in memory) and writes final outputs (no
-// split-K partials).  The four waves take interleaved 32-wide K steps (wave w: steps w, w + 4,
+// C = A W^T for many rows: a workgroup owns 16 rows x 16 CT columns over the whole of K, so it
+// streams CT * 16 complete weight rows (contiguous in memory) and writes final outputs (no split-K
+// partials).  The four waves take interleaved 32-wide K steps (wave w: steps w, w + 4,
 // ...) with P steps of loads in flight, and add their tiles through LDS in wave order, so the
 // result is deterministic.  Tiles are dealt XCD-aware: every row tile of a column tile runs on
 // one XCD (workgroup b on XCD b mod 8), which then fetches that column tile's weights into its L2
 // once.  AM: the A operand as bf16 hi/lo rows (0) or tiles (1) as for mx_gemm, or (2) RMSNorm
-// folded in (model.py:94-98): A = scale * h from the f32 residual rows, split into hi/lo parts in
-// registers, the sum of h^2 of each row taken over the same loads, and every output divided by
-// sqrt(mean(h^2) + 1e-5) in the epilogue.  TW as for mx_gemm.  EPI: store the outputs, add them to
-// out (the residual), or finish them in place of mx_swiglu_fin / mx_qkv_fin (column pairs per
-// thread, the same arithmetic).
+// folded in (model.py:94-98): A = scale * h from the f32 residual (tile order, so a step reads one
+// 2 KB piece), split into hi/lo parts in registers, the sum of h^2 of each row taken over the same
+// loads, and every output divided by sqrt(mean(h^2) + 1e-5) in the epilogue.  TW as for mx_gemm.
+// EPI: store the outputs, add them to the residual out (tile order), or finish them in place of
+// mx_swiglu_fin / mx_qkv_fin (column pairs per thread, the same arithmetic).
 template <int CT, int P, int AM, bool TW, int EPI>
 __global__ __launch_bounds__(256) void mx_gemm_rows(GemmArgs g) {
   __shared__ f32x4 red[4][CT][64];
@@ -328,7 +328,7 @@ __global__ __launch_bounds__(256) void mx_gemm_rows(GemmArgs g) {
   // rows past M read row M - 1 (row layout) or whatever their tile holds: an MFMA row only
   // feeds its own output row, which is not stored
   const uint16_t* ar = AM == 1 ? g.A + (int64_t(t) * S * 64 + lane) * 8 : g.A + int64_t(min(m0 + r16, g.M - 1)) * g.lda + kq;
-  const float* hr = AM == 2 ? g.h + int64_t(min(m0 + r16, g.M - 1)) * g.lda + kq : nullptr;
+  const float* hr = AM == 2 ? g.h + (int64_t(t) * S * 64 + lane) * 8 : nullptr;
   const uint16_t* sr = AM == 2 ? g.scale + kq : nullptr;
   const uint16_t* wr = TW ? g.W + (int64_t(n0 >> 4) * S * 64 + lane) * 8 : g.W + int64_t(n0 + r16) * g.K + kq;
   // element offsets of step ks and of column tile ct
@@ -346,8 +346,8 @@ __global__ __launch_bounds__(256) void mx_gemm_rows(GemmArgs g) {
   auto load = [&](int p, int i) {
     const int ks = wv + 4 * min(i, ns - 1);
     if constexpr (AM == 2) {
-      hx[p][0] = *reinterpret_cast<const float4*>(hr + ks * kBK);
-      hx[p][1] = *reinterpret_cast<const float4*>(hr + ks * kBK + 4);
+      hx[p][0] = *reinterpret_cast<const float4*>(hr + int64_t(ks) * 512);
+      hx[p][1] = *reinterpret_cast<const float4*>(hr + int64_t(ks) * 512 + 4);
       sx[p] = *reinterpret_cast<const uint4*>(sr + ks * kBK);
     } else {
       a[p] = *reinterpret_cast<const uint4*>(ar + ks * astep);
@@ -411,8 +411,8 @@ __global__ __launch_bounds__(256) void mx_gemm_rows(GemmArgs g) {
       const int ct = idx >> 8, e = idx & 255, r = e >> 6, l = e & 63;
       float v = ((red[0][ct][l][r] + red[1][ct][l][r]) + red[2][ct][l][r]) + red[3][ct][l][r];
       if constexpr (AM == 2) v = v / rrms[4 * (l >> 4) + r];
-      const int row = m0 + 4 * (l >> 4) + r;
-      float* o = g.out + int64_t(row) * g.ldo + n0 + 16 * ct + (l & 15);
+      const int row = m0 + 4 * (l >> 4) + r, col = n0 + 16 * ct + (l & 15);
+      float* o = g.out + (EPI == kEpiResid ? act_index(row, col, g.N, 0) : int64_t(row) * g.ldo + col);
       if (row < g.M) {
         if constexpr (EPI == kEpiResid) *o += v;
         else *o = v;
@@ -461,7 +461,8 @@ __device__ __forceinline__ float block_sum256(float v, float* red) {
 // xn[j] = scale[i] * (h[i] / sqrt(mean(h^2) + 1e-5)) as hi/lo bf16 parts (planes `plane` apart),
 // with i the input element at position j of the packed row layout (model.py:94-98).  Every partial is requested before
 // the first is added, so the sum costs one memory round trip.  With packed, h holds the row in
-// packed order (element i at position perm_pos(i)) and no partials are added.
+// packed order (element i at position perm_pos(i)) in tile order (act_index), and no partials are
+// added.
 __global__ __launch_bounds__(kNormThreads) void mx_norm(float* h, const float* part, int splits, int M, int d,
                                                         const uint16_t* scale, uint16_t* xn, int64_t plane,
                                                         int row0, int ldx, int packed) {
@@ -479,7 +480,7 @@ __global__ __launch_bounds__(kNormThreads) void mx_norm(float* h, const float* p
   uint16_t sc[NE];
 #pragma unroll
   for (int i = 0; i < NE; ++i) sc[i] = scale[perm_elem(min(int(threadIdx.x) + kNormThreads * i, d - 1), d)];
-  float4 v = *reinterpret_cast<const float4*>(hr + n4c);
+  float4 v = *reinterpret_cast<const float4*>(packed ? h + act_index(m, n4c, d, 0) : hr + n4c);
   {   // partials (none when splits == 0: then split 0 is read and ignored)
     float4 pv[kMaxSplitK];
 #pragma unroll
@@ -511,7 +512,7 @@ __global__ __launch_bounds__(kNormThreads) void mx_norm(float* h, const float* p
 }
 
 // Row m of the residual stream: the embedding of tokens[m] (element n at n, or with packed at its
-// packed position perm_pos(n)).
+// packed position perm_pos(n) in tile order, act_index).
 __global__ __launch_bounds__(256) void mx_embed(const uint16_t* emb, const int32_t* tokens, int d, float* h,
                                                 int32_t* status, int V, int packed) {
   const int m = blockIdx.x;
@@ -527,7 +528,7 @@ __global__ __launch_bounds__(256) void mx_embed(const uint16_t* emb, const int32
 #pragma unroll
   for (int i = 0; i < NE; ++i) {
     const int n = threadIdx.x + 256 * i;
-    if (n < d) h[int64_t(m) * d + (packed ? perm_pos(n, d) : n)] = bf2f(e[i]);
+    if (n < d) h[packed ? act_index(m, perm_pos(n, d), d, 0) : int64_t(m) * d + n] = bf2f(e[i]);
   }
 }
 
@@ -956,6 +957,8 @@ constexpr int kRowsMaxN = 4096;
 // or too short a K for every wave to take a step, and the split-K kernel runs instead.
 // With the weights in tile order (tw) every projection takes it (the fused epilogues and the
 // folded norms live there): the widest that gives about one workgroup per compute unit, else 1.
+// (Workgroups owning 2 or 4 row tiles, which read each weight tile for 32 or 64 rows, measured
+// slower: 128-token prefill 1.16 -> 1.36 / 1.70 ms.)
 static int rows_ct(int M, int N, int K, bool tw) {
   const int T = (M + 15) / 16, n16 = N / 16;
   if (K / kBK < 4) return 0;
@@ -996,7 +999,7 @@ static Layout layout(const msd_config* c, int M) {
   const int d = c->d_model, ff = c->d_ff, nqkv = (c->n_heads + 2 * c->n_kv_heads) * kDh;
   Layout L;
   size_t o = 0;
-  L.h = o;      o += al256(size_t(M) * d * 4);
+  L.h = o;      o += al256(size_t(pad16(M)) * d * 4);   // rows padded to whole tiles (tile order)
   // activation planes (hi and lo) in tile order, rows padded to whole tiles
   L.xn = o;     o += al256(size_t(pad16(M)) * d * 2 * 2);
   L.qkv = o;    o += al256(size_t(M) * nqkv * 4);
@@ -1028,13 +1031,6 @@ static void launch_rows(int ct, dim3 grid, hipStream_t s, const GemmArgs& g) {
     case 2: hipLaunchKernelGGL((mx_gemm_rows<2, 4, AM, TW, EPI>), grid, dim3(256), 0, s, g); break;
     default: hipLaunchKernelGGL((mx_gemm_rows<1, 4, AM, TW, EPI>), grid, dim3(256), 0, s, g); break;
   }
-}
-
-template <bool TA, bool TW>
-static void launch_splitk(int bm, dim3 grid, hipStream_t s, const GemmArgs& g) {
-  if (bm == 16) hipLaunchKernelGGL((mx_gemm<1, 1, TA, TW>), grid, dim3(256), 0, s, g);
-  else if (bm == 64) hipLaunchKernelGGL((mx_gemm<2, 2, TA, TW>), grid, dim3(256), 0, s, g);
-  else hipLaunchKernelGGL((mx_gemm<4, 2, TA, TW>), grid, dim3(256), 0, s, g);
 }
 
 // C = A W^T split over K: partials [splits][M][N] (pass ldo = N), or with splits == 1 rows
