@@ -1033,11 +1033,13 @@ static void launch_rows(int ct, dim3 grid, hipStream_t s, const GemmArgs& g) {
   }
 }
 
-// C = A W^T split over K: partials [splits][M][N] (pass ldo = N), or with splits == 1 rows
-// of stride ldo.  lda == 0: A in tile order (act_index); tw: W in tile order (msd_pack_tiles).
-// rows_ok: mx_gemm_rows may run (single split only).  The tied logits pass false: one row and
-// every row then come from the same kernel and summation order, so the last row's logits are
-// bitwise the same either way.
+template <bool TA, bool TW>
+static void launch_splitk(int bm, dim3 grid, hipStream_t s, const GemmArgs& g) {
+  if (bm == 16) hipLaunchKernelGGL((mx_gemm<1, 1, TA, TW>), grid, dim3(256), 0, s, g);
+  else if (bm == 64) hipLaunchKernelGGL((mx_gemm<2, 2, TA, TW>), grid, dim3(256), 0, s, g);
+  else hipLaunchKernelGGL((mx_gemm<4, 2, TA, TW>), grid, dim3(256), 0, s, g);
+}
+
 // C = A W^T split over K: partials [splits][M][N] (pass ldo = N), or with splits == 1 rows
 // of stride ldo.  lda == 0: A in tile order (act_index); tw: W in tile order (msd_pack_tiles).
 // hn: A is RMSNorm(h) folded into mx_gemm_rows (f32 rows hn of stride lda, packed-order scales
