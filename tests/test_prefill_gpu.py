@@ -74,9 +74,11 @@ def test_tiny_prefill_matches_oracle(tiny, T, tiles):
 def test_pack_tiles_layout(tiny):
     """msd_pack_tiles against a numpy re-tiling of every projection matrix of every layer: tile
     (n / 16, k / 32) holds rows 16 (n / 16) .. + 16 x columns 32 (k / 32) .. + 32, lane
-    r + 16 q = row r, columns 8 q .. 8 q + 8.  The O and down matrices take their rows in packed
-    order (row n of the copy = row kernel_perm(d)[n]), so their outputs land in the residual's
-    packed order; each layer ends with its two RMSNorm scales in packed order."""
+    r + 16 q = row r, columns 8 q .. 8 q + 8.  Orders: the O and down rows in packed order (row n
+    of the copy = row kernel_perm(d)[n]), so their outputs land in the residual's packed order;
+    the gate/up row pairs in the down projection's input order (pair f = pair kernel_perm(d_ff)[f]);
+    the O columns in natural order (column k = packed column j with kernel_perm(d)[j] = k); each
+    layer ends with its two RMSNorm scales in packed order."""
     params, w = tiny
     cfg = TINY
     d, ff, L = cfg["d_model"], cfg["d_ff"], cfg["n_layers"]
@@ -84,15 +86,21 @@ def test_pack_tiles_layout(tiny):
     got = weight_tiles(w, cfg).view(torch.int16).cpu().numpy()
     packed = w["packed_w"].view(torch.int16).cpu().numpy()
     perm = kernel_perm(d).cpu().numpy()
+    fperm = kernel_perm(ff).cpu().numpy()
+    pairs = np.stack([2 * fperm, 2 * fperm + 1], axis=1).reshape(-1)
+    natural = np.argsort(perm)
     layer = 2 * d + nqkv * d + d * d + 2 * ff * d + d * ff
     want = []
     for l in range(L):
         base = l * layer
         off = base + 2 * d
-        for N, K, permuted in ((nqkv, d, False), (d, d, True), (2 * ff, d, False), (d, ff, True)):
+        for N, K, rows, cols in ((nqkv, d, None, None), (d, d, perm, natural), (2 * ff, d, pairs, None),
+                                 (d, ff, perm, None)):
             W = packed[off:off + N * K].reshape(N, K)
-            if permuted:
-                W = W[perm]
+            if rows is not None:
+                W = W[rows]
+            if cols is not None:
+                W = W[:, cols]
             want.append(W.reshape(N // 16, 16, K // 32, 4, 8).transpose(0, 2, 3, 1, 4).reshape(-1))
             off += N * K
         want.append(packed[base:base + d][perm])

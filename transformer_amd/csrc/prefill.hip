@@ -432,8 +432,9 @@ __global__ __launch_bounds__(256) void mx_gemm_rows(GemmArgs g) {
       if (row >= g.M) continue;
       const EpiArgs& ea = g.e;
       if constexpr (EPI == kEpiSwiglu) {
+        // (the tile copy orders the gate/up pairs by the down projection's input positions)
         const int F = g.N / 2, f = col >> 1;
-        put_split(ea.act + act_index(row, perm_pos(f, F), F, 0), ea.act_plane, swiglu(v0, v1));
+        put_split(ea.act + act_index(row, f, F, 0), ea.act_plane, swiglu(v0, v1));
       } else {
         const int p = row_pos(ea.rows, row);
         const int64_t crow = cache_row(ea.rows, row, p);
@@ -620,8 +621,10 @@ __device__ __forceinline__ float row16_sum(float v) {
 // waves' (max, sum, O) are merged by log-sum-exp at the end.  Scale 1/sqrt(64) (model.py:98).
 // MFMA operand lanes: A[i][8 (l / 16) ..] = row i = l % 16; B[8 (l / 16) ..][n] with n = l % 16;
 // D: rows 4 (l / 16) + r of column l % 16.
+// The head outputs go to the O projection's input planes at their packed positions, or with
+// natural at their element index (the tile copy's O columns are in natural order).
 __global__ __launch_bounds__(256) void mx_attention_prefill(const float* qkv, int M, int H, int KV, uint16_t* att,
-                                                            int64_t plane, int ldx) {
+                                                            int64_t plane, int ldx, int natural) {
   constexpr int PS = 36;   // row stride (floats) of a wave's P tile in LDS: 16-byte reads of 16 rows spread over banks
   __shared__ __align__(16) float sp[4][16 * PS];
   __shared__ float sm[4][16], sl[4][16];
@@ -747,7 +750,10 @@ __global__ __launch_bounds__(256) void mx_attention_prefill(const float* qkv, in
   const int i = q0 + qi;
   if (i < M)
 #pragma unroll
-    for (int e = 0; e < 4; ++e) put_split(att + act_index(i, perm_pos(h * kDh + d4 + e, d), d, ldx), plane, O[e] / L);
+    for (int e = 0; e < 4; ++e) {
+      const int el = h * kDh + d4 + e;
+      put_split(att + act_index(i, natural ? el : perm_pos(el, d), d, ldx), plane, O[e] / L);
+    }
 }
 
 // Batched decode: row m (one sequence at position p = pos(m)) and head blockIdx.y attend over
@@ -761,7 +767,8 @@ constexpr int kAttnWaves = 8;
 
 __global__ __launch_bounds__(64 * kAttnWaves) void mx_attention_decode(const float* qkv, Rows rows, int H, int KV,
                                                                        const uint16_t* kc, const uint16_t* vc,
-                                                                       uint16_t* att, int64_t plane, int ldx) {
+                                                                       uint16_t* att, int64_t plane, int ldx,
+                                                                       int natural) {
   __shared__ float sq[kDh], skc[kDh], svc[kDh];   // q, and the current position's f32 k and v
   __shared__ float sp[kAttnWaves][64];
   __shared__ int srow[kAttnWaves][64];
@@ -845,7 +852,7 @@ __global__ __launch_bounds__(64 * kAttnWaves) void mx_attention_decode(const flo
       num += a * so[w][lane];
       den += a * sml[w][1];
     }
-    put_split(att + act_index(m, perm_pos(h * kDh + lane, d), d, ldx), plane, num / den);
+    put_split(att + act_index(m, natural ? h * kDh + lane : perm_pos(h * kDh + lane, d), d, ldx), plane, num / den);
   }
 }
 
@@ -916,19 +923,32 @@ __global__ void mx_sanitize_rows(const int32_t* pos, int fixed_pos, const int32_
 
 // One 16-byte piece per thread of the tile copy of an N x K matrix W (rows in packed order): piece
 // p is lane p % 64 of tile p / 64 = (n / 16) (K / 32) + k / 32, i.e. row n = 16 (tile / (K / 32)) +
-// lane % 16 at positions 32 (tile % (K / 32)) + 8 (lane / 16) .. + 8.  With perm, row n of the copy
-// is row perm_elem(n, N) of W: output column n is then element perm_elem(n) of an N-long vector,
-// i.e. its packed position n (the O and down projections, whose outputs add to the residual).
-__global__ __launch_bounds__(256) void mx_pack_tiles(const uint16_t* W, int N, int K, int perm, uint16_t* T) {
+// lane % 16 at positions 32 (tile % (K / 32)) + 8 (lane / 16) .. + 8.  Row orders (rowperm): 1 = row
+// n of the copy is row perm_elem(n, N) of W, so output column n is element perm_elem(n) of an
+// N-long vector, i.e. its packed position n (the O and down projections, whose outputs add to the
+// residual); 2 = row pair n / 2 is pair perm_elem(n / 2, N / 2) (gate/up: output pair f is then the
+// down projection's input at its packed position f).  With natk, column k of the copy is input
+// element k (W's column perm_pos(k)): the O projection, whose input the attention writes in
+// natural order.  Either way an epilogue's consecutive outputs land on consecutive positions.
+__global__ __launch_bounds__(256) void mx_pack_tiles(const uint16_t* W, int N, int K, int rowperm, int natk,
+                                                     uint16_t* T) {
   const int64_t p = int64_t(blockIdx.x) * 256 + threadIdx.x;
   const int S = K / kBK;
   if (p >= int64_t(N) * S * 64) return;
   const int lane = int(p & 63);
   const int64_t tile = p >> 6;
   const int n = int(16 * (tile / S)) + (lane & 15);
-  const int64_t src = perm ? perm_elem(n, N) : n;
+  const int64_t src = rowperm == 1 ? perm_elem(n, N) : (rowperm == 2 ? 2 * perm_elem(n >> 1, N / 2) + (n & 1) : n);
   const int k = kBK * int(tile % S) + 8 * (lane >> 4);
-  *reinterpret_cast<uint4*>(T + p * 8) = *reinterpret_cast<const uint4*>(W + src * K + k);
+  if (natk) {
+    uint16_t v[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = W[src * K + perm_pos(k + e, K)];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) T[p * 8 + e] = v[e];
+  } else {
+    *reinterpret_cast<uint4*>(T + p * 8) = *reinterpret_cast<const uint4*>(W + src * K + k);
+  }
 }
 
 // A layer's two RMSNorm scales in packed order: out[j] = scale[perm_elem(j, d)] for [ln1 | ln2].
@@ -1136,10 +1156,10 @@ static int run_layers(const msd_config* cfg, const Weights& wt, const Rows& rows
           hipSuccess)
         break;
       if (prefill)
-        hipLaunchKernelGGL(mx_attention_prefill, dim3(H, (M + 15) / 16), dim3(256), 0, s, qkv, M, H, KV, att, pd, 0);
+        hipLaunchKernelGGL(mx_attention_prefill, dim3(H, (M + 15) / 16), dim3(256), 0, s, qkv, M, H, KV, att, pd, 0, 1);
       else
         hipLaunchKernelGGL(mx_attention_decode, dim3(M, H), dim3(64 * kAttnWaves), 0, s, qkv, rows, H, KV, kc, vc,
-                           att, pd, 0);
+                           att, pd, 0, 1);
       if ((err = gemm(att, pd, 0, Tl + toff_o, true, M, d, d, h, d, 1, s, true, kEpiResid)) != hipSuccess) break;
       EpiArgs eg{};
       eg.act = act;
@@ -1155,10 +1175,10 @@ static int run_layers(const msd_config* cfg, const Weights& wt, const Rows& rows
     hipLaunchKernelGGL(mx_qkv_fin, dim3(M, (nqkv / 4 + 255) / 256), dim3(256), 0, s, part, sq, M, H, KV, wt.rope, rows,
                        kc, vc, qkv);
     if (prefill)
-      hipLaunchKernelGGL(mx_attention_prefill, dim3(H, (M + 15) / 16), dim3(256), 0, s, qkv, M, H, KV, att, pd, 0);
+      hipLaunchKernelGGL(mx_attention_prefill, dim3(H, (M + 15) / 16), dim3(256), 0, s, qkv, M, H, KV, att, pd, 0, 0);
     else
       hipLaunchKernelGGL(mx_attention_decode, dim3(M, H), dim3(64 * kAttnWaves), 0, s, qkv, rows, H, KV, kc, vc, att,
-                         pd, 0);
+                         pd, 0, 0);
     if ((err = gemm(att, pd, 0, Wl + off_o, false, M, d, d, part, d, so, s)) != hipSuccess) break;
     hipLaunchKernelGGL(mx_norm, dim3(M), dim3(kNormThreads), 0, s, h, part, so, M, d, Wl + off_ln2, xn, pd, 0, 0, 0);
     if ((err = gemm(xn, pd, 0, Wl + off_gu, false, M, 2 * ff, d, part, 2 * ff, sg, s)) != hipSuccess) break;
@@ -1259,8 +1279,9 @@ extern "C" int32_t msd_pack_tiles(const msd_config* cfg, const void* packed_w, v
                 off_dn = off_gu + 2 * int64_t(ff) * d, layer = off_dn + int64_t(d) * ff;
   const int64_t dst_o = int64_t(nqkv) * d, dst_gu = dst_o + int64_t(d) * d, dst_dn = dst_gu + 2 * int64_t(ff) * d,
                 dst_sc = dst_dn + int64_t(d) * ff;
-  const struct { int64_t src, dst; int N, K, perm; } mats[4] = {
-      {off_qkv, 0, nqkv, d, 0}, {off_o, dst_o, d, d, 1}, {off_gu, dst_gu, 2 * ff, d, 0}, {off_dn, dst_dn, d, ff, 1}};
+  const struct { int64_t src, dst; int N, K, rowperm, natk; } mats[4] = {
+      {off_qkv, 0, nqkv, d, 0, 0}, {off_o, dst_o, d, d, 1, 1}, {off_gu, dst_gu, 2 * ff, d, 2, 0},
+      {off_dn, dst_dn, d, ff, 1, 0}};
   const uint16_t* w = static_cast<const uint16_t*>(packed_w);
   uint16_t* t = static_cast<uint16_t*>(tiles);
   for (int l = 0; l < cfg->n_layers; ++l) {
@@ -1268,7 +1289,7 @@ extern "C" int32_t msd_pack_tiles(const msd_config* cfg, const void* packed_w, v
     for (const auto& m : mats) {
       const int64_t pieces = int64_t(m.N) * m.K / 8;
       hipLaunchKernelGGL(mx_pack_tiles, dim3(unsigned((pieces + 255) / 256)), dim3(256), 0, s, w + l * layer + m.src,
-                         m.N, m.K, m.perm, tl + m.dst);
+                         m.N, m.K, m.rowperm, m.natk, tl + m.dst);
     }
     hipLaunchKernelGGL(mx_pack_scales, dim3((2 * d + 255) / 256), dim3(256), 0, s, w + l * layer, d, tl + dst_sc);
   }
