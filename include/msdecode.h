@@ -193,19 +193,22 @@ int32_t msd_sample_token_noalloc(const float* logits, int32_t vocab, double temp
 /* Bytes of device workspace msd_prefill needs for a prompt of n_tokens tokens. */
 int64_t msd_prefill_workspace_bytes(const msd_config* cfg, int32_t n_tokens);
 
-/* Bytes of the tile copy of the layer weights (the QKV, O, gate/up and down matrices of every
- * layer: the same bf16 values as packed_w's projection rows, 2 bytes each). */
+/* Bytes of the tile copy of the layer weights (the QKV, O, gate/up and down matrices and the two
+ * RMSNorm scales of every layer: the same bf16 values as packed_w's, 2 bytes each). */
 int64_t msd_tiles_bytes(const msd_config* cfg);
 
 /* Writes the tile copy of packed_w's projection matrices to `tiles` (msd_tiles_bytes bytes,
  * 16-byte aligned, device memory): every N x K matrix as 16-row x 32-column tiles of 1 KB in
  * matrix-core operand order (lane l of tile (n / 16, k / 32) holds row 16 (n / 16) + l % 16,
  * columns 32 (k / 32) + 8 (l / 16) .. + 8), tile (n / 16, k / 32) at ((n / 16) (K / 32) +
- * k / 32) * 512 elements, layer after layer.  The multi-row passes (msd_prefill, msd_prefill_paged,
+ * k / 32) * 512 elements, layer after layer, each layer followed by its two RMSNorm scales in
+ * packed order.  The O and down rows are in packed order, the gate/up row pairs in the down
+ * projection's input order and the O columns in natural order, so the passes' epilogues write
+ * contiguous runs.  The multi-row passes (msd_prefill, msd_prefill_paged,
  * msd_verify and the multi-kernel pass of msd_batch_decode_step) read their projection weights
  * from it when it is given: a fragment load is then one 1 KB piece instead of 16 row segments
- * (128-token prefill of the 306M model measured 1.79 -> 1.50 ms).  Rebuild it whenever packed_w
- * changes. */
+ * (with the fused epilogues and folded norms it allows, 128-token prefill of the 306M model
+ * measured 1.79 -> 1.09 ms).  Rebuild it whenever packed_w changes. */
 int32_t msd_pack_tiles(const msd_config* cfg, const void* packed_w, void* tiles, void* stream);
 
 /* Forward pass over a prompt: tokens[0..n_tokens) at positions 0..n_tokens-1 (device int32).
