@@ -147,11 +147,13 @@ __device__ __forceinline__ int64_t cache_row(const Rows& r, int m, int p) {
 }
 
 // What mx_gemm_rows does with its final outputs.
-enum Epi { kEpiStore = 0, kEpiSwiglu = 1, kEpiQkv = 2, kEpiResid = 3 };
+enum Epi { kEpiStore = 0, kEpiSwiglu = 1, kEpiQkv = 2, kEpiResid = 3, kEpiResidNorm = 4 };
 // Operands of the fused epilogues.
 struct EpiArgs {
-  uint16_t* act;       // SwiGLU: the down projection's input planes (tile order), lo plane act_plane further
-  int64_t act_plane;
+  uint16_t* act;       // SwiGLU: the down projection's input planes; ResidNorm: the next RMSNorm's
+  int64_t act_plane;   // input planes (scale * h); tile order, the lo plane act_plane further
+  const uint16_t* xscale;   // ResidNorm: the next RMSNorm's scales in packed order
+  float* ssq;               // ResidNorm: each row's partial sum of h^2 per column group, [M][N / (16 CT)]
   const float* rope;   // QKV: RoPE table, rows, cache and the f32 q/k/v rows (as mx_qkv_fin)
   Rows rows;
   uint16_t* kc;
@@ -167,8 +169,8 @@ struct GemmArgs {
   float* out;          // partials [splits][M][N] f32, or [M][ldo] (single split)
   int M, N, K, lda, ldo, splits;
   EpiArgs e;
-  const float* h;          // mx_gemm_rows with the norm folded in: the f32 residual (packed positions in
-  const uint16_t* scale;   // tile order, act_index) and the norm's scales in packed order
+  const float* ssq;   // mx_gemm_rows with the norm folded in (AM 2): each row's partial sums of h^2,
+  int nssq;           // [M][nssq], summed in a fixed order for the rms that divides the outputs
 };
 
 __device__ __forceinline__ bf16x8 as_bf16x8(uint4 u) { return __builtin_bit_cast(bf16x8, u); }
@@ -305,16 +307,16 @@ __device__ __forceinline__ void qkv_pair(float s0, float s1, float c, float sg, 
 // result is deterministic.  Tiles are dealt XCD-aware: every row tile of a column tile runs on
 // one XCD (workgroup b on XCD b mod 8), which then fetches that column tile's weights into its L2
 // once.  AM: the A operand as bf16 hi/lo rows (0) or tiles (1) as for mx_gemm, or (2) RMSNorm
-// folded in (model.py:94-98): A = scale * h from the f32 residual (tile order, so a step reads one
-// 2 KB piece), split into hi/lo parts in registers, the sum of h^2 of each row taken over the same
-// loads, and every output divided by sqrt(mean(h^2) + 1e-5) in the epilogue.  TW as for mx_gemm.
-// EPI: store the outputs, add them to the residual out (tile order), or finish them in place of
-// mx_swiglu_fin / mx_qkv_fin (column pairs per thread, the same arithmetic).
+// folded in (model.py:94-98): A = the hi/lo tiles of scale * h that the previous projection's
+// epilogue wrote (kEpiResidNorm), and every output divided by sqrt(mean(h^2) + 1e-5), the sum of
+// h^2 of each row added up from that epilogue's per-column-group partials.  TW as for mx_gemm.
+// EPI: store the outputs, add them to the residual out (tile order; with kEpiResidNorm also the
+// hi/lo tiles of scale * h and the row's partial sum of h^2 for the next RMSNorm), or finish them
+// in place of mx_swiglu_fin / mx_qkv_fin (column pairs per thread, the same arithmetic).
 template <int CT, int P, int AM, bool TW, int EPI>
 __global__ __launch_bounds__(256) void mx_gemm_rows(GemmArgs g) {
   __shared__ f32x4 red[4][CT][64];
-  __shared__ float rss[AM == 2 ? 4 : 1][64];   // per-lane sums of h^2, then each row's rms
-  __shared__ float rrms[16];
+  __shared__ float rrms[16];   // AM 2: each row's rms
   // wave-uniform wave index: the step count and its loop stay scalar (a per-lane loop would copy
   // the accumulators out of and back into the AGPRs around every step)
   const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -327,32 +329,34 @@ __global__ __launch_bounds__(256) void mx_gemm_rows(GemmArgs g) {
   const int S = g.K / kBK;
   // rows past M read row M - 1 (row layout) or whatever their tile holds: an MFMA row only
   // feeds its own output row, which is not stored
-  const uint16_t* ar = AM == 1 ? g.A + (int64_t(t) * S * 64 + lane) * 8 : g.A + int64_t(min(m0 + r16, g.M - 1)) * g.lda + kq;
-  const float* hr = AM == 2 ? g.h + (int64_t(t) * S * 64 + lane) * 8 : nullptr;
-  const uint16_t* sr = AM == 2 ? g.scale + kq : nullptr;
+  const uint16_t* ar = AM >= 1 ? g.A + (int64_t(t) * S * 64 + lane) * 8 : g.A + int64_t(min(m0 + r16, g.M - 1)) * g.lda + kq;
   const uint16_t* wr = TW ? g.W + (int64_t(n0 >> 4) * S * 64 + lane) * 8 : g.W + int64_t(n0 + r16) * g.K + kq;
   // element offsets of step ks and of column tile ct
-  const int64_t astep = AM == 1 ? 512 : kBK, wstep = TW ? 512 : kBK;
+  const int64_t astep = AM >= 1 ? 512 : kBK, wstep = TW ? 512 : kBK;
   const int64_t wtile = TW ? int64_t(S) * 512 : int64_t(16) * g.K;
   const int ns = (S - wv + 3) / 4;   // K steps of this wave (S >= 4: every wave has one)
   f32x4 acc[CT];
 #pragma unroll
   for (int ct = 0; ct < CT; ++ct) acc[ct] = f32x4{0.f, 0.f, 0.f, 0.f};
-  uint4 a[P], al[P], w[P][CT], sx[P];
-  float4 hx[P][2];
-  float ss = 0.f;
+  // AM 2: the partial sums of h^2 of row tid / 16 (columns groups tid % 16 + 16 j), requested
+  // now and added up after the K loop
+  constexpr int kSq = 4;
+  float sq[kSq];
+  if constexpr (AM == 2) {
+    const int64_t rrow = min(m0 + int(threadIdx.x >> 4), g.M - 1);
+#pragma unroll
+    for (int j = 0; j < kSq; ++j) {
+      const int cg = int(threadIdx.x & 15) + 16 * j;
+      sq[j] = g.ssq[rrow * g.nssq + min(cg, g.nssq - 1)];
+    }
+  }
+  uint4 a[P], al[P], w[P][CT];
   // step i of this wave, clamped to its last: loads stay unconditional, so no wait lands at a
   // branch join
   auto load = [&](int p, int i) {
     const int ks = wv + 4 * min(i, ns - 1);
-    if constexpr (AM == 2) {
-      hx[p][0] = *reinterpret_cast<const float4*>(hr + int64_t(ks) * 512);
-      hx[p][1] = *reinterpret_cast<const float4*>(hr + int64_t(ks) * 512 + 4);
-      sx[p] = *reinterpret_cast<const uint4*>(sr + ks * kBK);
-    } else {
-      a[p] = *reinterpret_cast<const uint4*>(ar + ks * astep);
-      al[p] = *reinterpret_cast<const uint4*>(ar + g.a_plane + ks * astep);
-    }
+    a[p] = *reinterpret_cast<const uint4*>(ar + ks * astep);
+    al[p] = *reinterpret_cast<const uint4*>(ar + g.a_plane + ks * astep);
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) w[p][ct] = *reinterpret_cast<const uint4*>(wr + ct * wtile + ks * wstep);
   };
@@ -364,23 +368,7 @@ __global__ __launch_bounds__(256) void mx_gemm_rows(GemmArgs g) {
 #pragma unroll
     for (int p = 0; p < P; ++p) {
       const bool live = i0 + p < ns;
-      uint4 x, xl;
-      if constexpr (AM == 2) {
-        const float hv[8] = {hx[p][0].x, hx[p][0].y, hx[p][0].z, hx[p][0].w,
-                             hx[p][1].x, hx[p][1].y, hx[p][1].z, hx[p][1].w};
-        const uint32_t sw[4] = {sx[p].x, sx[p].y, sx[p].z, sx[p].w};
-        float xs[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const uint32_t u = sw[e >> 1];
-          xs[e] = __uint_as_float((e & 1) ? (u & 0xffff0000u) : (u << 16)) * hv[e];
-          ss += live ? hv[e] * hv[e] : 0.f;
-        }
-        split8(xs, x, xl);
-      } else {
-        x = a[p];
-        xl = al[p];
-      }
+      uint4 x = a[p], xl = al[p];
       if (!live) x = xl = make_uint4(0, 0, 0, 0);
 #pragma unroll
       for (int ct = 0; ct < CT; ++ct) {
@@ -392,31 +380,47 @@ __global__ __launch_bounds__(256) void mx_gemm_rows(GemmArgs g) {
   }
 #pragma unroll
   for (int ct = 0; ct < CT; ++ct) red[wv][ct][lane] = acc[ct];
-  if constexpr (AM == 2) rss[wv][lane] = ss;
-  __syncthreads();
-  if constexpr (AM == 2) {   // row r's sum of h^2: lanes r + 16 q of every wave, in a fixed order
-    if (threadIdx.x < 16) {
-      float sum = 0.f;
+  if constexpr (AM == 2) {   // row tid / 16's sum of h^2 over its nssq <= 64 partials, in a fixed order
+    float sum = 0.f;
 #pragma unroll
-      for (int w2 = 0; w2 < 4; ++w2)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) sum += rss[w2][threadIdx.x + 16 * q];
-      rrms[threadIdx.x] = sqrtf(sum / float(g.K) + 1e-5f);
-    }
-    __syncthreads();
+    for (int j = 0; j < kSq; ++j) sum += int(threadIdx.x & 15) + 16 * j < g.nssq ? sq[j] : 0.f;
+    sum += __shfl_xor(sum, 1);
+    sum += __shfl_xor(sum, 2);
+    sum += __shfl_xor(sum, 4);
+    sum += __shfl_xor(sum, 8);
+    if ((threadIdx.x & 15) == 0) rrms[threadIdx.x >> 4] = sqrtf(sum / float(g.K) + 1e-5f);
   }
+  __syncthreads();
   // D layout of a 16 x 16 tile: lane holds rows 4 (lane / 16) + r of column lane % 16
-  if constexpr (EPI == kEpiStore || EPI == kEpiResid) {
+  if constexpr (EPI == kEpiStore || EPI == kEpiResid || EPI == kEpiResidNorm) {
+    // thread tid holds row 4 (lane / 16) + wave of the tile, columns 16 ct + lane % 16
+    float hsq = 0.f;
     for (int idx = threadIdx.x; idx < CT * 256; idx += 256) {
       const int ct = idx >> 8, e = idx & 255, r = e >> 6, l = e & 63;
       float v = ((red[0][ct][l][r] + red[1][ct][l][r]) + red[2][ct][l][r]) + red[3][ct][l][r];
       if constexpr (AM == 2) v = v / rrms[4 * (l >> 4) + r];
       const int row = m0 + 4 * (l >> 4) + r, col = n0 + 16 * ct + (l & 15);
-      float* o = g.out + (EPI == kEpiResid ? act_index(row, col, g.N, 0) : int64_t(row) * g.ldo + col);
+      float* o = g.out + (EPI == kEpiStore ? int64_t(row) * g.ldo + col : act_index(row, col, g.N, 0));
       if (row < g.M) {
-        if constexpr (EPI == kEpiResid) *o += v;
-        else *o = v;
+        if constexpr (EPI == kEpiStore) {
+          *o = v;
+        } else {
+          const float hv = *o + v;
+          *o = hv;
+          if constexpr (EPI == kEpiResidNorm) {
+            put_split(g.e.act + act_index(row, col, g.N, 0), g.e.act_plane, bf2f(g.e.xscale[col]) * hv);
+            hsq += hv * hv;
+          }
+        }
       }
+    }
+    if constexpr (EPI == kEpiResidNorm) {   // the row's 16 CT columns: 16 lanes, in a fixed order
+      hsq += __shfl_xor(hsq, 1);
+      hsq += __shfl_xor(hsq, 2);
+      hsq += __shfl_xor(hsq, 4);
+      hsq += __shfl_xor(hsq, 8);
+      const int row = m0 + 4 * (lane >> 4) + wv;
+      if ((lane & 15) == 0 && row < g.M) g.e.ssq[int64_t(row) * C + c] = hsq;
     }
   } else {
     // one column pair (lanes l, l + 1 of a row) per thread
@@ -513,9 +517,13 @@ __global__ __launch_bounds__(kNormThreads) void mx_norm(float* h, const float* p
 }
 
 // Row m of the residual stream: the embedding of tokens[m] (element n at n, or with packed at its
-// packed position perm_pos(n) in tile order, act_index).
+// packed position perm_pos(n) in tile order, act_index).  With xscale (packed only) also the first
+// RMSNorm's input planes, scale * h as hi/lo tiles (xn, lo plane `plane` further), and the row's
+// sum of h^2 in ssq[m].
 __global__ __launch_bounds__(256) void mx_embed(const uint16_t* emb, const int32_t* tokens, int d, float* h,
-                                                int32_t* status, int V, int packed) {
+                                                int32_t* status, int V, int packed, const uint16_t* xscale,
+                                                uint16_t* xn, int64_t plane, float* ssq) {
+  __shared__ float red[4];
   const int m = blockIdx.x;
   int t = tokens[m];
   if (t < 0 || t >= V) {
@@ -526,10 +534,25 @@ __global__ __launch_bounds__(256) void mx_embed(const uint16_t* emb, const int32
   uint16_t e[NE];
 #pragma unroll
   for (int i = 0; i < NE; ++i) e[i] = emb[int64_t(t) * d + min(int(threadIdx.x) + 256 * i, d - 1)];
+  float hsq = 0.f;
 #pragma unroll
   for (int i = 0; i < NE; ++i) {
     const int n = threadIdx.x + 256 * i;
-    if (n < d) h[packed ? act_index(m, perm_pos(n, d), d, 0) : int64_t(m) * d + n] = bf2f(e[i]);
+    if (n < d) {
+      const float hv = bf2f(e[i]);
+      if (packed) {
+        const int j = perm_pos(n, d);
+        h[act_index(m, j, d, 0)] = hv;
+        if (xscale) put_split(xn + act_index(m, j, d, 0), plane, bf2f(xscale[j]) * hv);
+      } else {
+        h[int64_t(m) * d + n] = hv;
+      }
+      hsq += hv * hv;
+    }
+  }
+  if (xscale) {
+    hsq = block_sum256(hsq, red);
+    if (threadIdx.x == 0) ssq[m] = hsq;
   }
 }
 
@@ -961,7 +984,7 @@ __global__ __launch_bounds__(256) void mx_pack_scales(const uint16_t* ln, int d,
 
 // ---------------------------------------------------------------- host side
 struct Layout {
-  size_t h, xn, qkv, att, act, part, status, rowpos, pages, bytes;
+  size_t h, xn, ssq, qkv, att, act, part, status, rowpos, pages, bytes;
 };
 
 static size_t al256(size_t x) { return (x + 255) & ~size_t(255); }
@@ -1022,6 +1045,7 @@ static Layout layout(const msd_config* c, int M) {
   L.h = o;      o += al256(size_t(pad16(M)) * d * 4);   // rows padded to whole tiles (tile order)
   // activation planes (hi and lo) in tile order, rows padded to whole tiles
   L.xn = o;     o += al256(size_t(pad16(M)) * d * 2 * 2);
+  L.ssq = o;    o += al256(size_t(M) * (d / 16) * 4);   // partial sums of h^2: at most d / 16 per row
   L.qkv = o;    o += al256(size_t(M) * nqkv * 4);
   L.att = o;    o += al256(size_t(pad16(M)) * d * 2 * 2);
   L.act = o;    o += al256(size_t(pad16(M)) * ff * 2 * 2);
@@ -1062,25 +1086,29 @@ static void launch_splitk(int bm, dim3 grid, hipStream_t s, const GemmArgs& g) {
 
 // C = A W^T split over K: partials [splits][M][N] (pass ldo = N), or with splits == 1 rows
 // of stride ldo.  lda == 0: A in tile order (act_index); tw: W in tile order (msd_pack_tiles).
-// hn: A is RMSNorm(h) folded into mx_gemm_rows (f32 rows hn of stride lda, packed-order scales
-// `scale`).  epi / ea: the epilogue of mx_gemm_rows (tile-order weights only).
+// ssq: A is the scale * h planes of an RMSNorm folded into mx_gemm_rows, whose rms comes from the
+// nssq partial sums of h^2 per row in ssq.  epi / ea: the epilogue of mx_gemm_rows (tile-order
+// weights only).
 // rows_ok: mx_gemm_rows may run (single split only).  The tied logits pass false: one row and
 // every row then come from the same kernel and summation order, so the last row's logits are
 // bitwise the same either way.
 static hipError_t gemm(const uint16_t* A, int64_t a_plane, int lda, const uint16_t* W, bool tw, int M, int N, int K,
                        float* out, int ldo, int splits, hipStream_t s, bool rows_ok = true, int epi = kEpiStore,
-                       const EpiArgs* ea = nullptr, const float* hn = nullptr, const uint16_t* scale = nullptr) {
-  GemmArgs g{A, a_plane, W, out, M, N, K, lda, ldo, splits, ea ? *ea : EpiArgs{}, hn, scale};
-  const int am = hn ? 2 : (lda == 0 ? 1 : 0);
+                       const EpiArgs* ea = nullptr, const float* ssq = nullptr, int nssq = 0) {
+  GemmArgs g{A, a_plane, W, out, M, N, K, lda, ldo, splits, ea ? *ea : EpiArgs{}, ssq, nssq};
+  const int am = ssq ? 2 : (lda == 0 ? 1 : 0);
   const int ct = splits == 1 && rows_ok && am > 0 ? rows_ct(M, N, K, tw) : 0;
   if ((epi != kEpiStore || am == 2) && !(ct > 0 && tw)) return hipErrorInvalidValue;
-  if ((epi == kEpiQkv || epi == kEpiSwiglu) && !ea) return hipErrorInvalidValue;
+  if ((epi == kEpiQkv || epi == kEpiSwiglu || epi == kEpiResidNorm) && !ea) return hipErrorInvalidValue;
+  if (am == 2 && (lda != 0 || nssq < 1 || nssq > 64)) return hipErrorInvalidValue;
+  if (epi == kEpiResidNorm && (!ea->act || !ea->xscale || !ea->ssq || N / (16 * ct) > 64)) return hipErrorInvalidValue;
   if (ct > 0) {
     const int T = (M + 15) / 16, C = N / (16 * ct);
     const dim3 grid(8 * ((C + 7) / 8) * T);
     if (am == 2 && epi == kEpiQkv) launch_rows<2, true, kEpiQkv>(ct, grid, s, g);
     else if (am == 2 && epi == kEpiSwiglu) launch_rows<2, true, kEpiSwiglu>(ct, grid, s, g);
     else if (am == 1 && tw && epi == kEpiResid) launch_rows<1, true, kEpiResid>(ct, grid, s, g);
+    else if (am == 1 && tw && epi == kEpiResidNorm) launch_rows<1, true, kEpiResidNorm>(ct, grid, s, g);
     else if (am == 1 && !tw && epi == kEpiStore) launch_rows<1, false>(ct, grid, s, g);
     else return hipErrorInvalidValue;
     return hipGetLastError();
@@ -1109,6 +1137,12 @@ static int64_t tile_layer_elems(const msd_config* c) {
   return nqkv * d + d * d + 2 * ff * d + d * ff + 2 * d;
 }
 
+// Element offset of the first layer's packed RMSNorm1 scales in the tile copy.
+static int64_t first_norm_scales(const msd_config* c) {
+  const int64_t d = c->d_model, ff = c->d_ff, nqkv = int64_t(c->n_heads + 2 * c->n_kv_heads) * kDh;
+  return nqkv * d + d * d + 2 * ff * d + d * ff;
+}
+
 // The layer stack over M rows whose residual stream is already in h; leaves the last
 // projection's partials pending (returned split count).
 static int run_layers(const msd_config* cfg, const Weights& wt, const Rows& rows, uint16_t* kv, const Layout& L,
@@ -1121,6 +1155,7 @@ static int run_layers(const msd_config* cfg, const Weights& wt, const Rows& rows
   uint16_t* att = reinterpret_cast<uint16_t*>(ws + L.att);
   uint16_t* act = reinterpret_cast<uint16_t*>(ws + L.act);
   float* part = reinterpret_cast<float*>(ws + L.part);
+  float* ssq = reinterpret_cast<float*>(ws + L.ssq);
   const int64_t off_ln2 = d, off_qkv = 2 * int64_t(d), off_o = off_qkv + int64_t(nqkv) * d,
                 off_gu = off_o + int64_t(d) * d, off_dn = off_gu + 2 * int64_t(ff) * d,
                 layer = off_dn + int64_t(d) * ff;
@@ -1131,6 +1166,9 @@ static int run_layers(const msd_config* cfg, const Weights& wt, const Rows& rows
   // the tile copy's per-layer offsets
   const int64_t toff_o = int64_t(nqkv) * d, toff_gu = toff_o + int64_t(d) * d, toff_dn = toff_gu + 2 * int64_t(ff) * d,
                 toff_sc = toff_dn + int64_t(d) * ff;
+  // partial sums of h^2 per row that the O and down epilogues leave (one per column group); the
+  // first layer's come from mx_embed (one per row)
+  const int cg_o = tw ? d / (16 * rows_ct(M, d, d, true)) : 0, cg_d = tw ? d / (16 * rows_ct(M, d, ff, true)) : 0;
   int pending = 0;
   err = hipSuccess;
   for (int l = 0; l < cfg->n_layers && err == hipSuccess; ++l) {
@@ -1141,9 +1179,11 @@ static int run_layers(const msd_config* cfg, const Weights& wt, const Rows& rows
     const int64_t pd = int64_t(pad16(M)) * d, pf = int64_t(pad16(M)) * ff;
     if (tw) {
       // Five kernels per layer over the tile copy, h in packed order: QKV with RMSNorm1 folded in
-      // and q/k/v, RoPE and the cache rows in its epilogue; attention; O adding to h; gate/up with
-      // RMSNorm2 folded in and SwiGLU in its epilogue; down adding to h.
+      // and q/k/v, RoPE and the cache rows in its epilogue; attention; O adding to h and writing
+      // RMSNorm2's input planes; gate/up with RMSNorm2 folded in and SwiGLU in its epilogue; down
+      // adding to h and writing the next layer's RMSNorm1 input planes.
       const uint16_t* Tl = wt.tiles + int64_t(l) * tile_layer_elems(cfg);
+      const bool last = l + 1 == cfg->n_layers;
       EpiArgs eq{};
       eq.rope = wt.rope;
       eq.rows = rows;
@@ -1152,7 +1192,7 @@ static int run_layers(const msd_config* cfg, const Weights& wt, const Rows& rows
       eq.qkv = qkv;
       eq.H = H;
       eq.KV = KV;
-      if ((err = gemm(nullptr, 0, d, Tl, true, M, nqkv, d, nullptr, 0, 1, s, true, kEpiQkv, &eq, h, Tl + toff_sc)) !=
+      if ((err = gemm(xn, pd, 0, Tl, true, M, nqkv, d, nullptr, 0, 1, s, true, kEpiQkv, &eq, ssq, l == 0 ? 1 : cg_d)) !=
           hipSuccess)
         break;
       if (prefill)
@@ -1160,14 +1200,23 @@ static int run_layers(const msd_config* cfg, const Weights& wt, const Rows& rows
       else
         hipLaunchKernelGGL(mx_attention_decode, dim3(M, H), dim3(64 * kAttnWaves), 0, s, qkv, rows, H, KV, kc, vc,
                            att, pd, 0, 1);
-      if ((err = gemm(att, pd, 0, Tl + toff_o, true, M, d, d, h, d, 1, s, true, kEpiResid)) != hipSuccess) break;
+      EpiArgs en{};   // the next RMSNorm's input planes and partial sums of h^2
+      en.act = xn;
+      en.act_plane = pd;
+      en.ssq = ssq;
+      en.xscale = Tl + toff_sc + d;
+      if ((err = gemm(att, pd, 0, Tl + toff_o, true, M, d, d, h, d, 1, s, true, kEpiResidNorm, &en)) != hipSuccess)
+        break;
       EpiArgs eg{};
       eg.act = act;
       eg.act_plane = pf;
-      if ((err = gemm(nullptr, 0, d, Tl + toff_gu, true, M, 2 * ff, d, nullptr, 0, 1, s, true, kEpiSwiglu, &eg, h,
-                      Tl + toff_sc + d)) != hipSuccess)
+      if ((err = gemm(xn, pd, 0, Tl + toff_gu, true, M, 2 * ff, d, nullptr, 0, 1, s, true, kEpiSwiglu, &eg, ssq, cg_o)) !=
+          hipSuccess)
         break;
-      if ((err = gemm(act, pf, 0, Tl + toff_dn, true, M, d, ff, h, d, 1, s, true, kEpiResid)) != hipSuccess) break;
+      if (!last) en.xscale = Tl + tile_layer_elems(cfg) + toff_sc;   // the next layer's RMSNorm1
+      if ((err = gemm(act, pf, 0, Tl + toff_dn, true, M, d, ff, h, d, 1, s, true, last ? kEpiResid : kEpiResidNorm,
+                      last ? nullptr : &en)) != hipSuccess)
+        break;
       continue;
     }
     hipLaunchKernelGGL(mx_norm, dim3(M), dim3(kNormThreads), 0, s, h, part, pending, M, d, Wl, xn, pd, 0, 0, 0);
@@ -1243,7 +1292,10 @@ static int32_t prefill_impl(const msd_config* cfg, const Weights& wt, const int3
   Rows rows{M, nullptr, 0, page_table ? pages : nullptr, max_pages, page_table ? pool_pages * kPage : cfg->context_len,
             start};
   const int packed = wt.tiles != nullptr;   // the tile path keeps h in packed order
-  hipLaunchKernelGGL(mx_embed, dim3(M), dim3(256), 0, s, wt.emb, tokens, d, h, status, V, packed);
+  // with the tile copy also the first layer's RMSNorm1 input planes and sums of h^2
+  hipLaunchKernelGGL(mx_embed, dim3(M), dim3(256), 0, s, wt.emb, tokens, d, h, status, V, packed,
+                     packed ? wt.tiles + first_norm_scales(cfg) : nullptr, xn, int64_t(pad16(M)) * d,
+                     reinterpret_cast<float*>(ws + L.ssq));
   hipError_t err;
   const int pending = run_layers(cfg, wt, rows, static_cast<uint16_t*>(kv), L, ws, start == 0, s, err);
   if (err != hipSuccess) return MSD_E_HIP;
@@ -1391,7 +1443,10 @@ extern "C" int32_t msd_batch_decode_step(const msd_config* cfg, const void* toke
                      cfg->context_len, pool_pages, rowpos, pages, status);
   Rows rows{M, rowpos, 1, pages, max_pages, pool_pages * kPage, 0};
   const int packed = wt.tiles != nullptr;
-  hipLaunchKernelGGL(mx_embed, dim3(M), dim3(256), 0, s, wt.emb, tokens, d, h, status, V, packed);
+  // with the tile copy also the first layer's RMSNorm1 input planes and sums of h^2
+  hipLaunchKernelGGL(mx_embed, dim3(M), dim3(256), 0, s, wt.emb, tokens, d, h, status, V, packed,
+                     packed ? wt.tiles + first_norm_scales(cfg) : nullptr, xn, int64_t(pad16(M)) * d,
+                     reinterpret_cast<float*>(ws + L.ssq));
   hipError_t err;
   const int pending = run_layers(cfg, wt, rows, static_cast<uint16_t*>(kv_pool), L, ws, false, s, err);
   if (err != hipSuccess) return MSD_E_HIP;
