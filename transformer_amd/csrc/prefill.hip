@@ -300,9 +300,10 @@ __device__ __forceinline__ void qkv_pair(float s0, float s1, float c, float sg, 
   }
 }
 
-// C = A W^T for many rows: a workgroup owns 16 rows x 16 CT columns over the whole of K, so it
+// C = A W^T for many rows: a workgroup owns 16 RT rows x 16 CT columns over the whole of K, so it
 // streams CT * 16 complete weight rows (contiguous in memory) and writes final outputs (no split-K
-// partials).  The four waves take interleaved 32-wide K steps (wave w: steps w, w + 4,
+// partials); with RT = 2 every weight tile it loads serves 32 rows, and the last column group may
+// be short (ragged: N / 16 need not be a multiple of CT).  The four waves take interleaved 32-wide K steps (wave w: steps w, w + 4,
 // ...) with P steps of loads in flight, and add their tiles through LDS in wave order, so the
 // result is deterministic.  Tiles are dealt XCD-aware: every row tile of a column tile runs on
 // one XCD (workgroup b on XCD b mod 8), which then fetches that column tile's weights into its L2
@@ -313,52 +314,67 @@ __device__ __forceinline__ void qkv_pair(float s0, float s1, float c, float sg, 
 // EPI: store the outputs, add them to the residual out (tile order; with kEpiResidNorm also the
 // hi/lo tiles of scale * h and the row's partial sum of h^2 for the next RMSNorm), or finish them
 // in place of mx_swiglu_fin / mx_qkv_fin (column pairs per thread, the same arithmetic).
-template <int CT, int P, int AM, bool TW, int EPI>
+template <int CT, int P, int AM, bool TW, int EPI, int RT = 1>
 __global__ __launch_bounds__(256) void mx_gemm_rows(GemmArgs g) {
-  __shared__ f32x4 red[4][CT][64];
-  __shared__ float rrms[16];   // AM 2: each row's rms
+  static_assert(RT == 1 || (AM >= 1 && TW && (EPI == kEpiSwiglu || EPI == kEpiQkv)),
+                "two row tiles per workgroup: tile-order operands and a pair epilogue");
+  __shared__ f32x4 red[4][RT][CT][64];
+  __shared__ float rrms[16 * RT];   // AM 2: each row's rms
   // wave-uniform wave index: the step count and its loop stay scalar (a per-lane loop would copy
   // the accumulators out of and back into the AGPRs around every step)
   const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int T = (g.M + 15) / 16, C = g.N / (16 * CT);
+  const int n16 = g.N / 16, T = (g.M + 15) / 16, TG = (T + RT - 1) / RT, C = (n16 + CT - 1) / CT;
   const int b = blockIdx.x, slot = b >> 3;
-  const int t = slot % T, c = (slot / T) * 8 + (b & 7);
+  const int t = slot % TG, c = (slot / TG) * 8 + (b & 7);
   if (c >= C) return;
-  const int m0 = 16 * t, n0 = 16 * CT * c;
+  const int m0 = 16 * RT * t, n0 = 16 * CT * c;
+  const int ctn = min(CT, n16 - CT * c);   // column tiles of this group (the last group may be short)
   const int r16 = lane & 15, kq = 8 * (lane >> 4);
   const int S = g.K / kBK;
-  // rows past M read row M - 1 (row layout) or whatever their tile holds: an MFMA row only
-  // feeds its own output row, which is not stored
-  const uint16_t* ar = AM >= 1 ? g.A + (int64_t(t) * S * 64 + lane) * 8 : g.A + int64_t(min(m0 + r16, g.M - 1)) * g.lda + kq;
+  // rows past M read row M - 1 (row layout) or whatever their tile holds (a row tile past the
+  // last reads the last): an MFMA row only feeds its own output row, which is not stored
+  const uint16_t* ar[RT];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt)
+    ar[rt] = AM >= 1 ? g.A + (int64_t(min(RT * t + rt, T - 1)) * S * 64 + lane) * 8
+                     : g.A + int64_t(min(m0 + r16, g.M - 1)) * g.lda + kq;
   const uint16_t* wr = TW ? g.W + (int64_t(n0 >> 4) * S * 64 + lane) * 8 : g.W + int64_t(n0 + r16) * g.K + kq;
   // element offsets of step ks and of column tile ct
   const int64_t astep = AM >= 1 ? 512 : kBK, wstep = TW ? 512 : kBK;
   const int64_t wtile = TW ? int64_t(S) * 512 : int64_t(16) * g.K;
   const int ns = (S - wv + 3) / 4;   // K steps of this wave (S >= 4: every wave has one)
-  f32x4 acc[CT];
+  f32x4 acc[RT][CT];
 #pragma unroll
-  for (int ct = 0; ct < CT; ++ct) acc[ct] = f32x4{0.f, 0.f, 0.f, 0.f};
-  // AM 2: the partial sums of h^2 of row tid / 16 (columns groups tid % 16 + 16 j), requested
-  // now and added up after the K loop
+  for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) acc[rt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // AM 2: the partial sums of h^2 of row 16 rt + tid / 16 (column groups tid % 16 + 16 j),
+  // requested now and added up after the K loop
   constexpr int kSq = 4;
-  float sq[kSq];
+  float sq[RT][kSq];
   if constexpr (AM == 2) {
-    const int64_t rrow = min(m0 + int(threadIdx.x >> 4), g.M - 1);
 #pragma unroll
-    for (int j = 0; j < kSq; ++j) {
-      const int cg = int(threadIdx.x & 15) + 16 * j;
-      sq[j] = g.ssq[rrow * g.nssq + min(cg, g.nssq - 1)];
+    for (int rt = 0; rt < RT; ++rt) {
+      const int64_t rrow = min(m0 + 16 * rt + int(threadIdx.x >> 4), g.M - 1);
+#pragma unroll
+      for (int j = 0; j < kSq; ++j) {
+        const int cg = int(threadIdx.x & 15) + 16 * j;
+        sq[rt][j] = g.ssq[rrow * g.nssq + min(cg, g.nssq - 1)];
+      }
     }
   }
-  uint4 a[P], al[P], w[P][CT];
+  uint4 a[P][RT], al[P][RT], w[P][CT];
   // step i of this wave, clamped to its last: loads stay unconditional, so no wait lands at a
-  // branch join
+  // branch join (a column tile past a short group's end reads its last tile)
   auto load = [&](int p, int i) {
     const int ks = wv + 4 * min(i, ns - 1);
-    a[p] = *reinterpret_cast<const uint4*>(ar + ks * astep);
-    al[p] = *reinterpret_cast<const uint4*>(ar + g.a_plane + ks * astep);
 #pragma unroll
-    for (int ct = 0; ct < CT; ++ct) w[p][ct] = *reinterpret_cast<const uint4*>(wr + ct * wtile + ks * wstep);
+    for (int rt = 0; rt < RT; ++rt) {
+      a[p][rt] = *reinterpret_cast<const uint4*>(ar[rt] + ks * astep);
+      al[p][rt] = *reinterpret_cast<const uint4*>(ar[rt] + g.a_plane + ks * astep);
+    }
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) w[p][ct] = *reinterpret_cast<const uint4*>(wr + min(ct, ctn - 1) * wtile + ks * wstep);
   };
 #pragma unroll
   for (int p = 0; p < P; ++p) load(p, p);
@@ -368,36 +384,45 @@ __global__ __launch_bounds__(256) void mx_gemm_rows(GemmArgs g) {
 #pragma unroll
     for (int p = 0; p < P; ++p) {
       const bool live = i0 + p < ns;
-      uint4 x = a[p], xl = al[p];
-      if (!live) x = xl = make_uint4(0, 0, 0, 0);
 #pragma unroll
-      for (int ct = 0; ct < CT; ++ct) {
-        acc[ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(x), as_bf16x8(w[p][ct]), acc[ct], 0, 0, 0);
-        acc[ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(xl), as_bf16x8(w[p][ct]), acc[ct], 0, 0, 0);
+      for (int rt = 0; rt < RT; ++rt) {
+        uint4 x = a[p][rt], xl = al[p][rt];
+        if (!live) x = xl = make_uint4(0, 0, 0, 0);
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) {
+          acc[rt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(x), as_bf16x8(w[p][ct]), acc[rt][ct], 0, 0, 0);
+          acc[rt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(xl), as_bf16x8(w[p][ct]), acc[rt][ct], 0, 0, 0);
+        }
       }
       load(p, i0 + p + P);
     }
   }
 #pragma unroll
-  for (int ct = 0; ct < CT; ++ct) red[wv][ct][lane] = acc[ct];
-  if constexpr (AM == 2) {   // row tid / 16's sum of h^2 over its nssq <= 64 partials, in a fixed order
-    float sum = 0.f;
+  for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-    for (int j = 0; j < kSq; ++j) sum += int(threadIdx.x & 15) + 16 * j < g.nssq ? sq[j] : 0.f;
-    sum += __shfl_xor(sum, 1);
-    sum += __shfl_xor(sum, 2);
-    sum += __shfl_xor(sum, 4);
-    sum += __shfl_xor(sum, 8);
-    if ((threadIdx.x & 15) == 0) rrms[threadIdx.x >> 4] = sqrtf(sum / float(g.K) + 1e-5f);
+    for (int ct = 0; ct < CT; ++ct) red[wv][rt][ct][lane] = acc[rt][ct];
+  if constexpr (AM == 2) {   // row 16 rt + tid / 16's sum of h^2 over its nssq <= 64 partials, in a fixed order
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      float sum = 0.f;
+#pragma unroll
+      for (int j = 0; j < kSq; ++j) sum += int(threadIdx.x & 15) + 16 * j < g.nssq ? sq[rt][j] : 0.f;
+      sum += __shfl_xor(sum, 1);
+      sum += __shfl_xor(sum, 2);
+      sum += __shfl_xor(sum, 4);
+      sum += __shfl_xor(sum, 8);
+      if ((threadIdx.x & 15) == 0) rrms[16 * rt + (threadIdx.x >> 4)] = sqrtf(sum / float(g.K) + 1e-5f);
+    }
   }
   __syncthreads();
   // D layout of a 16 x 16 tile: lane holds rows 4 (lane / 16) + r of column lane % 16
   if constexpr (EPI == kEpiStore || EPI == kEpiResid || EPI == kEpiResidNorm) {
-    // thread tid holds row 4 (lane / 16) + wave of the tile, columns 16 ct + lane % 16
+    // (one row tile, whole column groups) thread tid holds row 4 (lane / 16) + wave of the tile,
+    // columns 16 ct + lane % 16
     float hsq = 0.f;
     for (int idx = threadIdx.x; idx < CT * 256; idx += 256) {
       const int ct = idx >> 8, e = idx & 255, r = e >> 6, l = e & 63;
-      float v = ((red[0][ct][l][r] + red[1][ct][l][r]) + red[2][ct][l][r]) + red[3][ct][l][r];
+      float v = ((red[0][0][ct][l][r] + red[1][0][ct][l][r]) + red[2][0][ct][l][r]) + red[3][0][ct][l][r];
       if constexpr (AM == 2) v = v / rrms[4 * (l >> 4) + r];
       const int row = m0 + 4 * (l >> 4) + r, col = n0 + 16 * ct + (l & 15);
       float* o = g.out + (EPI == kEpiStore ? int64_t(row) * g.ldo + col : act_index(row, col, g.N, 0));
@@ -424,16 +449,18 @@ __global__ __launch_bounds__(256) void mx_gemm_rows(GemmArgs g) {
     }
   } else {
     // one column pair (lanes l, l + 1 of a row) per thread
-    for (int idx = threadIdx.x; idx < CT * 128; idx += 256) {
-      const int ct = idx >> 7, e = idx & 127, r = e >> 5, l = 16 * ((e >> 3) & 3) + 2 * (e & 7);
-      float v0 = ((red[0][ct][l][r] + red[1][ct][l][r]) + red[2][ct][l][r]) + red[3][ct][l][r];
-      float v1 = ((red[0][ct][l + 1][r] + red[1][ct][l + 1][r]) + red[2][ct][l + 1][r]) + red[3][ct][l + 1][r];
+    for (int idx = threadIdx.x; idx < RT * CT * 128; idx += 256) {
+      const int tc = idx >> 7, rt = tc / CT, ct = tc % CT, e = idx & 127, r = e >> 5,
+                l = 16 * ((e >> 3) & 3) + 2 * (e & 7);
+      float v0 = ((red[0][rt][ct][l][r] + red[1][rt][ct][l][r]) + red[2][rt][ct][l][r]) + red[3][rt][ct][l][r];
+      float v1 = ((red[0][rt][ct][l + 1][r] + red[1][rt][ct][l + 1][r]) + red[2][rt][ct][l + 1][r]) +
+                 red[3][rt][ct][l + 1][r];
       if constexpr (AM == 2) {
-        v0 = v0 / rrms[4 * (l >> 4) + r];
-        v1 = v1 / rrms[4 * (l >> 4) + r];
+        v0 = v0 / rrms[16 * rt + 4 * (l >> 4) + r];
+        v1 = v1 / rrms[16 * rt + 4 * (l >> 4) + r];
       }
-      const int row = m0 + 4 * (l >> 4) + r, col = n0 + 16 * ct + (l & 15);
-      if (row >= g.M) continue;
+      const int row = m0 + 16 * rt + 4 * (l >> 4) + r, col = n0 + 16 * ct + (l & 15);
+      if (row >= g.M || ct >= ctn) continue;
       const EpiArgs& ea = g.e;
       if constexpr (EPI == kEpiSwiglu) {
         // (the tile copy orders the gate/up pairs by the down projection's input positions)
@@ -1011,6 +1038,21 @@ static int rows_ct(int M, int N, int K, bool tw) {
   return tw ? 1 : 0;
 }
 
+// Workgroups owning two row tiles (tile-order weights, pair epilogues): when one row tile per
+// workgroup needs more workgroups than compute units, the column tiles (6, 8 or 4, the last group
+// ragged) of a grid of 224-256 workgroups, else 0.  Every weight tile then serves 32 rows, and one
+// pass over the CUs does the whole projection (128-token gate/up, 352 column tiles: 13.3 -> 9.2 us
+// in a microbenchmark with weights that miss the last-level cache).
+static int rows_ct2(int M, int N, int K, bool tw) {
+  const int ct1 = rows_ct(M, N, K, tw), T = (M + 15) / 16, n16 = N / 16;
+  if (!tw || ct1 <= 0 || T < 2 || T * (n16 / ct1) <= 256) return 0;
+  for (int ct : {6, 8, 4}) {
+    const int wg = ((T + 1) / 2) * ((n16 + ct - 1) / ct);
+    if (wg >= 224 && wg <= 256) return ct;
+  }
+  return 0;
+}
+
 // K splits of a projection: 1 for mx_gemm_rows, else enough split-K workgroups to occupy every
 // compute unit, at least 4 K steps each
 static int splits_for(int M, int N, int K, int bm, bool tw) {
@@ -1077,6 +1119,15 @@ static void launch_rows(int ct, dim3 grid, hipStream_t s, const GemmArgs& g) {
   }
 }
 
+template <int AM, int EPI>
+static void launch_rows2(int ct, dim3 grid, hipStream_t s, const GemmArgs& g) {
+  switch (ct) {
+    case 8: hipLaunchKernelGGL((mx_gemm_rows<8, 2, AM, true, EPI, 2>), grid, dim3(256), 0, s, g); break;
+    case 6: hipLaunchKernelGGL((mx_gemm_rows<6, 2, AM, true, EPI, 2>), grid, dim3(256), 0, s, g); break;
+    default: hipLaunchKernelGGL((mx_gemm_rows<4, 2, AM, true, EPI, 2>), grid, dim3(256), 0, s, g); break;
+  }
+}
+
 template <bool TA, bool TW>
 static void launch_splitk(int bm, dim3 grid, hipStream_t s, const GemmArgs& g) {
   if (bm == 16) hipLaunchKernelGGL((mx_gemm<1, 1, TA, TW>), grid, dim3(256), 0, s, g);
@@ -1102,6 +1153,15 @@ static hipError_t gemm(const uint16_t* A, int64_t a_plane, int lda, const uint16
   if ((epi == kEpiQkv || epi == kEpiSwiglu || epi == kEpiResidNorm) && !ea) return hipErrorInvalidValue;
   if (am == 2 && (lda != 0 || nssq < 1 || nssq > 64)) return hipErrorInvalidValue;
   if (epi == kEpiResidNorm && (!ea->act || !ea->xscale || !ea->ssq || N / (16 * ct) > 64)) return hipErrorInvalidValue;
+  const int ct2 = ct > 0 && (epi == kEpiSwiglu || epi == kEpiQkv) ? rows_ct2(M, N, K, tw) : 0;
+  if (ct2 > 0) {
+    const int TG = ((M + 15) / 16 + 1) / 2, C = (N / 16 + ct2 - 1) / ct2;
+    const dim3 grid(8 * ((C + 7) / 8) * TG);
+    if (am == 2 && epi == kEpiQkv) launch_rows2<2, kEpiQkv>(ct2, grid, s, g);
+    else if (am == 2 && epi == kEpiSwiglu) launch_rows2<2, kEpiSwiglu>(ct2, grid, s, g);
+    else return hipErrorInvalidValue;
+    return hipGetLastError();
+  }
   if (ct > 0) {
     const int T = (M + 15) / 16, C = N / (16 * ct);
     const dim3 grid(8 * ((C + 7) / 8) * T);
