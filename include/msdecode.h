@@ -208,7 +208,7 @@ int64_t msd_tiles_bytes(const msd_config* cfg);
  * msd_verify and the multi-kernel pass of msd_batch_decode_step) read their projection weights
  * from it when it is given: a fragment load is then one 1 KB piece instead of 16 row segments
  * (with the fused epilogues and folded norms it allows, 128-token prefill of the 306M model
- * measured 1.79 -> 1.09 ms).  Rebuild it whenever packed_w changes. */
+ * measured 1.79 -> 1.02 ms).  Rebuild it whenever packed_w changes. */
 int32_t msd_pack_tiles(const msd_config* cfg, const void* packed_w, void* tiles, void* stream);
 
 /* Forward pass over a prompt: tokens[0..n_tokens) at positions 0..n_tokens-1 (device int32).
