@@ -1147,6 +1147,19 @@ __device__ __forceinline__ void att_copy(DMA& d, const Args& a, const AttCtx& c,
   d.drain();
 }
 
+// One more cached row, row `r` of this split (whose rows 0 .. r - 1 att_copy has placed), to its
+// place after them: K at 144 r (lanes 0..8, one 16-byte slot each, the 9th repeating the 8th)
+// and V at 128 r (lanes 0..7).  Issued after att_copy's drain, so these writes land last.
+template <class DMA>
+__device__ __forceinline__ void att_copy_row(DMA& d, const Args& a, const AttCtx& c, int l, int lo, int r) {
+  const int lane = c.lane;
+  const uint16_t* kc = layer_k(a, l) + (int64_t(c.g) * a.ctx + lo + r) * kDh;
+  const uint16_t* vc = kc + int64_t(a.KV) * a.ctx * kDh;
+  if (lane < 9) d.issue(kc + min(lane, 7) * 8, c.K + 144 * r);
+  if (lane < 8) d.issue(vc + lane * 8, c.V + 128 * r);
+  d.drain();
+}
+
 // This workgroup's cached positions at position pos: [0, pos) is cut into nsplit equal ranges
 // (at most cap each); the last split also takes the current position.
 __device__ __forceinline__ void att_range(const Args& a, const AttCtx& c, int pos, int& lo, int& ncached) {
@@ -1169,13 +1182,19 @@ __device__ void att_loader(const Args& a, const AttCtx& c) {
   for (int st = 0; st < nsteps; ++st) {
     int lo, ncached;
     att_range(a, c, a.pos + st, lo, ncached);
-    // the previous step's cache rows are complete once its token is published (every row
-    // workgroup waits for its stores before arriving)
-    if (st > 0) poll_token(a, st - 1, c.item, lane, bad);
+    // The previous step's cache rows are complete once its token is published (every row
+    // workgroup waits for its stores before arriving).  Only its own row (position pos + st - 1)
+    // needs that token: the older rows were covered by the tokens already seen, so the first
+    // layer's older rows are copied before the poll, during the previous step's logits.
+    const int newest = st > 0 && a.pos + st - 1 >= lo && a.pos + st - 1 < lo + ncached ? 1 : 0;
     for (int l = 0; l < a.L; ++l) {
       const int gl = st * a.L + l;   // layers run on across the steps of a launch
       if (gl > 0) lds_wait(c.ctr + 2, kWavesA * gl, a.ctrl);
-      if (ncached > 0) {
+      if (MULTI && st > 0 && l == 0) {
+        if (ncached - newest > 0) att_copy(dd, a, c, l, lo, ncached - newest);
+        poll_token(a, st - 1, c.item, lane, bad);
+        if (newest) att_copy_row(dd, a, c, l, lo, ncached - 1);
+      } else if (ncached > 0) {
         if (MULTI) att_copy(dd, a, c, l, lo, ncached);
         else att_copy(d, a, c, l, lo, ncached);
       }
