@@ -123,6 +123,21 @@ def test_306m_prefill_128_matches_oracle(m306):
     assert np.max(np.abs(la - ref)) < 0.25 * np.max(np.abs(b16 - ref))
 
 
+def test_306m_prefill_odd_row_tiles(m306):
+    """A 100-token prompt: 7 row tiles of 16.  The gate/up projection then runs on workgroups of
+    two row tiles and six column tiles (7 x 44 one-tile workgroups would exceed the 256 compute
+    units), so one workgroup's second row tile lies past the prompt (read, never stored) and the
+    last column group is short (352 column tiles = 58 x 6 + 4)."""
+    params, w = m306
+    toks = make_prompt(100, M306["vocab_size"], seed=5)
+    la, last, out, kv = _run(w, M306, toks)
+    ref, kc, vc = om.prefill_with_kv(params, M306, toks)
+    print("306M 100-token prefill max |logit diff| vs f32 model.py:", float(np.max(np.abs(la - ref))))
+    np.testing.assert_allclose(la, ref, atol=ATOL, rtol=RTOL)
+    _check_kv(kv, M306, 100, kc, vc)
+    np.testing.assert_array_equal(last, la[-1])
+
+
 def _gpu_greedy_after_prefill(w, cfg, prompt, n):
     dec = Decoder(w, cfg)
     pf = Prefiller(w, cfg, max_tokens=len(prompt))
