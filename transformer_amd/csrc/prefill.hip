@@ -303,11 +303,11 @@ __device__ __forceinline__ void qkv_pair(float s0, float s1, float c, float sg, 
 // C = A W^T for many rows: a workgroup owns 16 RT rows x 16 CT columns over the whole of K, so it
 // streams CT * 16 complete weight rows (contiguous in memory) and writes final outputs (no split-K
 // partials); with RT = 2 every weight tile it loads serves 32 rows, and the last column group may
-// be short (ragged: N / 16 need not be a multiple of CT).  The four waves take interleaved 32-wide K steps (wave w: steps w, w + 4,
-// ...) with P steps of loads in flight, and add their tiles through LDS in wave order, so the
-// result is deterministic.  Tiles are dealt XCD-aware: every row tile of a column tile runs on
-// one XCD (workgroup b on XCD b mod 8), which then fetches that column tile's weights into its L2
-// once.  AM: the A operand as bf16 hi/lo rows (0) or tiles (1) as for mx_gemm, or (2) RMSNorm
+// be short (ragged: N / 16 need not be a multiple of CT).  The four waves take interleaved
+// 32-wide K steps (wave w: steps w, w + 4, ...) with P steps of loads in flight, and add their
+// tiles through LDS in wave order, so the result is deterministic.  Tiles are dealt XCD-aware:
+// every row tile of a column tile runs on one XCD (workgroup b on XCD b mod 8), which then fetches
+// that column tile's weights into its L2 once.  AM: the A operand as bf16 hi/lo rows (0) or tiles (1) as for mx_gemm, or (2) RMSNorm
 // folded in (model.py:94-98): A = the hi/lo tiles of scale * h that the previous projection's
 // epilogue wrote (kEpiResidNorm), and every output divided by sqrt(mean(h^2) + 1e-5), the sum of
 // h^2 of each row added up from that epilogue's per-column-group partials.  TW as for mx_gemm.
