@@ -430,6 +430,34 @@ def test_tiny_steps_in_one_launch_equal_single_steps(tiny):
     assert more == ref[33:41] and t2 == ref[41]
 
 
+def test_tiny_steps_in_one_launch_two_splits(tiny):
+    """Context 1024 (two attention workgroups per head): 24 greedy steps in one launch give the
+    logits of one launch per step bit for bit.  Each step's first layer copies its older cached
+    rows before the previous step's token is published and the newest row after it; the newest
+    row belongs to the last split."""
+    params, prompt, _ = tiny
+    cfg = dict(TINY, context_len=1024)
+    w = prepare_decode_weights_nlayer(params, cfg)
+    P = len(prompt)
+    single = Decoder(w, cfg)
+    for p, t in enumerate(prompt):
+        tok, _ = single.step(int(t), p)
+    first = tok
+    sl, st = [], []
+    for i in range(24):
+        tok, lg = single.step(tok, P + i)
+        st.append(tok)
+        sl.append(lg.cpu().numpy().copy())
+    multi = Decoder(w, cfg)
+    for p, t in enumerate(prompt):
+        multi.step(int(t), p)
+    toks, logits = multi.generate(first, P, 24, all_logits=True)
+    ml = logits.cpu().numpy()
+    assert toks == st
+    for i in range(24):
+        assert np.array_equal(ml[i], sl[i]), i
+
+
 def test_306m_whole_generation_in_one_launch(m306):
     """Config 2's 479 greedy steps (positions 32..510) in a single launch, token-exact."""
     params, w = m306
