@@ -227,6 +227,19 @@ int32_t msd_prefill(const msd_config* cfg, const void* token_emb, const void* ou
                     const int32_t* tokens, int32_t n_tokens, void* kv, void* workspace,
                     float* logits_last, float* logits_all, int32_t* next_token, void* stream);
 
+/* Launch mode of the multi-row passes (msd_prefill, msd_prefill_paged, msd_verify and the
+ * multi-kernel pass of msd_batch_decode_step).  With graphs on (off by default; the environment
+ * variable MSD_LAUNCH_GRAPHS=1 starts with them on) the ~130 dependent launches of a pass are
+ * captured once per argument set (shape, device pointers, sizes) into a HIP graph that is kept
+ * (at most 16 per process, the least recently used dropped) and replayed on the caller's stream.
+ * That cuts the host's enqueue time per pass from ~0.35 to ~0.07 ms (306M) but runs ~1 % slower
+ * on the device, so it is for callers whose host thread is the bottleneck.  Buffer contents are
+ * read when the kernels run, so a pass over new tokens in the same buffers replays the same
+ * graph.  A stream the caller is capturing gets the launches directly.  Results are bitwise the
+ * same either way.  Returns the previous setting.  No counterpart in the reference: a
+ * launch-mode switch of this library. */
+int32_t msd_set_launch_graphs(int32_t enabled);
+
 /* Bytes of device workspace msd_verify needs for n_tokens rows. */
 int64_t msd_verify_workspace_bytes(const msd_config* cfg, int32_t n_tokens);
 

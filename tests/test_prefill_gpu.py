@@ -197,3 +197,51 @@ def test_306m_prefill_full_context(m306):
     for l in (0, 11, 23):
         np.testing.assert_allclose(ks[l].float().cpu().numpy(), kc[l], atol=ATOL, rtol=RTOL)
         np.testing.assert_allclose(vs[l].float().cpu().numpy(), vc[l], atol=ATOL, rtol=RTOL)
+
+
+def _graph_vs_eager(w, cfg, prompts):
+    """Each prompt through the same buffers, eager launches then the cached graph's replay, with
+    eager torch work and synchronisations between the passes: every replay bitwise equal."""
+    from transformer_amd import _lib
+    L = _lib.lib()
+    T = len(prompts[0])
+    pf = Prefiller(w, cfg, max_tokens=T)
+    kv = new_kv_packed(cfg)
+    la = torch.empty((T, cfg["vocab_size"]), dtype=torch.float32, device="cuda")
+    before = L.msd_set_launch_graphs(0)
+    try:
+        for i, toks in enumerate(prompts):
+            got = {}
+            for mode in (0, 1, 1):   # eager, then the graph captured by the first pass, replayed
+                L.msd_set_launch_graphs(mode)
+                kv.fill_(SENTINEL + i)
+                la.fill_(-1.0)
+                out = pf.launch(toks, kv, logits_all=la)
+                torch.cuda.synchronize()
+                res = (la.cpu().numpy().copy(), pf.logits.cpu().numpy().copy(), out.cpu().numpy().copy(),
+                       kv.view(torch.int16).cpu().numpy().copy())
+                if mode == 0:
+                    got["eager"] = res
+                else:
+                    for a, b in zip(res, got["eager"]):
+                        assert np.array_equal(a, b), f"prompt {i}: graph replay differs from the eager launches"
+            assert int(got["eager"][2][1]) == 0
+    finally:
+        L.msd_set_launch_graphs(before)
+
+
+def test_tiny_graph_replays_equal_eager_launches(tiny):
+    """Three prompts of one length (one argument set: the same graph replayed over new tokens),
+    then a shorter one (a second graph)."""
+    _, w = tiny
+    rng = np.random.default_rng(11)
+    prompts = [rng.integers(0, TINY["vocab_size"], 40).tolist() for _ in range(3)]
+    _graph_vs_eager(w, TINY, prompts)
+    _graph_vs_eager(w, TINY, [rng.integers(0, TINY["vocab_size"], 23).tolist()])
+
+
+def test_306m_graph_replays_equal_eager_launches(m306):
+    """The 128-token prompt of the 306M model (the timed prefill workload), two prompts."""
+    _, w = m306
+    rng = np.random.default_rng(13)
+    _graph_vs_eager(w, M306, [rng.integers(0, M306["vocab_size"], 128).tolist() for _ in range(2)])

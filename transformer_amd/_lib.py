@@ -25,7 +25,7 @@ EXPORTS = ("msd_packed_weight_elems", "msd_workspace_bytes", "msd_default_workgr
            "msd_prefill_workspace_bytes", "msd_prefill", "msd_prefill_paged", "msd_batch_workspace_bytes",
            "msd_batch_decode_step", "msd_workspace_acquire", "msd_workspace_release",
            "msd_sample_token_noalloc", "msd_verify_workspace_bytes", "msd_verify",
-           "msd_decode_steps", "msd_tiles_bytes", "msd_pack_tiles")
+           "msd_decode_steps", "msd_tiles_bytes", "msd_pack_tiles", "msd_set_launch_graphs")
 
 
 class MsdConfig(ctypes.Structure):
@@ -109,6 +109,8 @@ def lib():
     L.msd_batch_workspace_bytes.restype = I64
     L.msd_batch_decode_step.argtypes = [CP, P, P, P, P, P, P, P, P, I32, P, I32, P, I32, P, P, P, P]
     L.msd_batch_decode_step.restype = I32
+    L.msd_set_launch_graphs.argtypes = [I32]
+    L.msd_set_launch_graphs.restype = I32
     L.msd_verify_workspace_bytes.argtypes = [CP, I32]
     L.msd_verify_workspace_bytes.restype = I64
     L.msd_verify.argtypes = [CP, P, P, P, P, P, P, P, I32, I32, P, P, P, P, P]

@@ -77,6 +77,10 @@ class PagedBatchDecoder:
         self.out = torch.zeros(2 * self.batch, dtype=torch.int32, device=self.device)
         self.last = torch.empty(config["vocab_size"], dtype=torch.float32, device=self.device)
         self.pf_out = torch.zeros(2, dtype=torch.int32, device=self.device)
+        # host prompts, tokens and positions are copied into these, so repeated calls keep their
+        # argument set (and replay the library's cached launch graph when launch graphs are on)
+        self._prompt = torch.empty(config["context_len"], dtype=torch.int32, device=self.device)
+        self._step_in = torch.empty((2, self.batch), dtype=torch.int32, device=self.device)
 
     def _w(self):
         w = self.w
@@ -95,8 +99,13 @@ class PagedBatchDecoder:
         """Prefill sequence b's prompt into its pages; returns the device int32[2] (argmax, status)."""
         if pages is not None:
             self.set_pages(b, pages)
-        toks = torch.as_tensor(np.asarray(prompt, dtype=np.int32)).to(self.device)
+        arr = np.asarray(prompt, dtype=np.int32).reshape(-1)
+        if not 1 <= arr.size <= self._prompt.numel():
+            raise ValueError(f"prompt length {arr.size} outside [1, {self._prompt.numel()}]")
         s = stream if stream is not None else torch.cuda.current_stream(self.device)
+        toks = self._prompt[:arr.size]
+        with torch.cuda.stream(s):
+            toks.copy_(torch.from_numpy(arr))
         rc = _lib.lib().msd_prefill_paged(
             ctypes.byref(self._cfg), *self._w(), toks.data_ptr(), toks.numel(), self.tables[b].data_ptr(),
             self.max_pages, self.pool.data.data_ptr(), self.pool.n_pages, self.pf_workspace.data_ptr(),
@@ -118,9 +127,9 @@ class PagedBatchDecoder:
 
     def step(self, tokens, positions):
         """One step from host lists; returns (next tokens (batch,) list, logits (batch, V) tensor)."""
-        t = torch.as_tensor(np.asarray(tokens, dtype=np.int32)).to(self.device)
-        p = torch.as_tensor(np.asarray(positions, dtype=np.int32)).to(self.device)
-        out = self.launch(t, p).cpu().numpy()
+        self._step_in.copy_(torch.from_numpy(np.stack([np.asarray(tokens, dtype=np.int32).reshape(self.batch),
+                                                        np.asarray(positions, dtype=np.int32).reshape(self.batch)])))
+        out = self.launch(self._step_in[0], self._step_in[1]).cpu().numpy()
         st = int(np.bitwise_or.reduce(out[1::2]))
         if st:
             raise _lib.MsdError(_lib.MSD_E_ARG, f"batched decode step (status {st:#x})")

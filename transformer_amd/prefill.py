@@ -37,6 +37,9 @@ class Prefiller:
         self.workspace = torch.empty(nbytes, dtype=torch.uint8, device=self.device)
         self.logits = torch.empty(self.config["vocab_size"], dtype=torch.float32, device=self.device)
         self.out = torch.zeros(2, dtype=torch.int32, device=self.device)   # [argmax, status]
+        # host prompts are copied here, so repeated passes keep their argument set (and replay
+        # the library's cached launch graph when launch graphs are on)
+        self._tok = torch.empty(self.max_tokens, dtype=torch.int32, device=self.device)
 
     def launch(self, tokens, kv, logits_all=None, out=None, stream=None):
         """Enqueue the prefill of ``tokens`` (host sequence or device int32 tensor) into ``kv``.
@@ -45,20 +48,24 @@ class Prefiller:
         position's logits are in ``self.logits``.
         """
         c = self.config
+        s = stream if stream is not None else torch.cuda.current_stream(self.device)
         if isinstance(tokens, torch.Tensor) and tokens.is_cuda:
             tok = tokens.to(torch.int32).contiguous()
+            T = tok.numel()
         else:
             arr = np.asarray(tokens, dtype=np.int64).reshape(-1)
             if arr.size and (arr.min() < 0 or arr.max() >= c["vocab_size"]):
                 raise ValueError("token id outside the vocabulary")
-            tok = torch.as_tensor(arr.astype(np.int32)).to(self.device)
-        T = tok.numel()
+            T = arr.size
         if not 1 <= T <= self.max_tokens:
             raise ValueError(f"prompt length {T} outside [1, {self.max_tokens}]")
+        if not (isinstance(tokens, torch.Tensor) and tokens.is_cuda):
+            tok = self._tok[:T]
+            with torch.cuda.stream(s):
+                tok.copy_(torch.from_numpy(arr.astype(np.int32)))
         if logits_all is not None and (logits_all.dtype != torch.float32 or logits_all.numel() != T * c["vocab_size"]):
             raise ValueError("logits_all must be a (T, V) f32 tensor")
         out = self.out if out is None else out
-        s = stream if stream is not None else torch.cuda.current_stream(self.device)
         w = self.w
         rc = _lib.lib().msd_prefill(
             ctypes.byref(self._cfg), w["token_emb"].data_ptr(), w["output_proj"].data_ptr(),
