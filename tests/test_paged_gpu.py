@@ -168,3 +168,37 @@ def test_persistent_step_epoch_wrap():
         assert na == nb
         ta, tb = na, nb
     assert int(bd2.workspace[:4].view(torch.int32).item()) == 3   # 0xFFFFFFFE, 1, 2, 3 after 0xFFFFFFFD
+
+
+def _paged_run(params, lens, steps):
+    """9 sequences (the multi-kernel step): prefills, then `steps` steps; every output on the host."""
+    bd, pool, tables, prompts, first = _setup(TINY, params, 9, lens, steps, 128, seed=12)
+    toks, outs = list(first), [list(first)]
+    for i in range(steps):
+        nxt, lg = bd.step(toks, [lens[b] + i for b in range(9)])
+        outs.append((list(nxt), lg.cpu().numpy().copy()))
+        toks = nxt
+    torch.cuda.synchronize()
+    return outs, pool.data.view(torch.int16).cpu().numpy().copy()
+
+
+def test_launch_graphs_equal_eager_paged_prefill_and_multi_kernel_step():
+    """Paged prefills and the multi-kernel batched step replayed from launch graphs (the later
+    steps replay the first step's graph over new tokens and positions in the same buffers):
+    tokens, logits and the page pool bitwise equal to eager launches."""
+    from transformer_amd import _lib
+    L = _lib.lib()
+    params = make_params(TINY, seed=0)
+    lens = [int(x) for x in np.random.default_rng(11).integers(16, 65, 9)]
+    before = L.msd_set_launch_graphs(0)
+    try:
+        eager = _paged_run(params, lens, 4)
+        L.msd_set_launch_graphs(1)
+        graphed = _paged_run(params, lens, 4)
+    finally:
+        L.msd_set_launch_graphs(before)
+    assert eager[0][0] == graphed[0][0]
+    for (ta, la), (tb, lb) in zip(eager[0][1:], graphed[0][1:]):
+        assert ta == tb
+        assert np.array_equal(la, lb)
+    assert np.array_equal(eager[1], graphed[1])

@@ -94,3 +94,37 @@ def test_verification_argument_checks():
         ver.launch([1, 2], TINY["context_len"] - 1, kv)   # past the context
     with pytest.raises(ValueError):
         ver.launch([1, 2, 3, 4, 5], 3, kv)               # more rows than the workspace holds
+
+
+def test_launch_graphs_equal_eager_verification():
+    """Two drafts verified at one position (the second replays the first's launch graph over new
+    tokens): logits, argmax pairs and the cache bitwise equal to eager launches."""
+    params = make_params(TINY, seed=0)
+    w = prepare_decode_weights_nlayer(params, TINY)
+    L = _lib.lib()
+    prompt = make_prompt(40, TINY["vocab_size"], seed=21)
+    rng = np.random.default_rng(5)
+    drafts = [rng.integers(0, TINY["vocab_size"], 4).tolist() for _ in range(2)]
+
+    def run():
+        kv = new_kv_packed(TINY)
+        Prefiller(w, TINY, max_tokens=40).launch(prompt, kv)
+        ver = Verifier(w, TINY, max_tokens=4)
+        res = []
+        for d in drafts:
+            logits, am = ver.launch(d, 40, kv)
+            torch.cuda.synchronize()
+            res.append((logits.cpu().numpy().copy(), am.cpu().numpy().copy()))
+        return res, kv.view(torch.int16).cpu().numpy().copy()
+
+    before = L.msd_set_launch_graphs(0)
+    try:
+        eager = run()
+        L.msd_set_launch_graphs(1)
+        graphed = run()
+    finally:
+        L.msd_set_launch_graphs(before)
+    for (la, aa), (lb, ab) in zip(eager[0], graphed[0]):
+        assert np.array_equal(la, lb) and np.array_equal(aa, ab)
+        assert np.all(aa[:, 1] == 0)
+    assert np.array_equal(eager[1], graphed[1])
