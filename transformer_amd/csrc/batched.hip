@@ -97,6 +97,11 @@ constexpr int kFlagReps = MBD_FLAG_REPS;
 #ifndef MBD_LDS_SLEEP
 #define MBD_LDS_SLEEP 1
 #endif
+// Wave priority (s_setprio) of the loader wave; the worker waves keep 0
+#ifndef MBD_LOADER_PRIO
+#define MBD_LOADER_PRIO 1
+#endif
+constexpr int kLoaderPrio = MBD_LOADER_PRIO;
 // the wave that polls the QKV barrier (the others request their first attention block meanwhile)
 #ifndef MBD_QKV_POLLER
 #define MBD_QKV_POLLER 6
@@ -817,6 +822,9 @@ __global__ __launch_bounds__(kThreads) void batch_step_kernel(Args a) {
   const int slot_par = int(epoch & 1u);
   Sync sy{&s_landed, &s_consumed, &s_wbar, a.ctrl + kCtlStatus + 16 * slot_par, 0};
   if (wv == kWorkers) {
+    // the loader wave issues ahead of the worker waves on its SIMD (measured: 0.792 -> 0.786 ms
+    // per step; the workers raised instead: 0.1-0.3 % slower)
+    if constexpr (kLoaderPrio > 0) __builtin_amdgcn_s_setprio(kLoaderPrio);
     loader(a, sy, slots, lane);
     return;
   }
