@@ -150,9 +150,12 @@ def secondary(w, cfg, dec, first_token):
     pos_end = cfg["context_len"] - 1
     tok0 = torch.tensor([int(first_token)], dtype=torch.int32, device="cuda")
     nsteps = pos_end - 32
-    one = lambda: dec.launch_steps(tok0, 32, nsteps)
+    one_out = torch.zeros((nsteps, 2), dtype=torch.int32, device="cuda")
+    one = lambda: dec.launch_steps(tok0, 32, nsteps, out=one_out)
     one()
     lms = _events_ms(one, 3)
+    if bool((one_out[:, 1] != 0).any()):
+        raise RuntimeError("status set in the one-launch generation")
     out["decode_one_launch"] = {"tok_s": round(nsteps / (lms / 1e3), 1), "us_per_token": round(lms / nsteps * 1e3, 2),
                                 "workload": f"306M, {nsteps} greedy steps at positions 32..{pos_end - 1} in one "
                                             "launch (each step's argmax fed to the next inside the kernel)"}

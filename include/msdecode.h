@@ -60,6 +60,27 @@ enum {
   MSD_E_TIMEOUT = -4,     /* a cross-workgroup wait exceeded its spin bound (reported by msd_check_status) */
 };
 
+/* Paths of the library (bits of msd_config_support). */
+enum {
+  MSD_PATH_DECODE = 1,    /* msd_decode_step / msd_decode_steps (the fused step) */
+  MSD_PATH_PREFILL = 2,   /* msd_prefill, msd_prefill_paged, msd_pack_tiles */
+  MSD_PATH_VERIFY = 4,    /* msd_verify */
+  MSD_PATH_BATCHED = 8,   /* msd_batch_decode_step (any batch; a persistent launch where it fits) */
+  MSD_PATH_SAMPLE = 16,   /* msd_sample_token (the vocabulary size) */
+};
+
+/* The paths that accept cfg, as MSD_PATH_* bits (0 = none), or MSD_E_ARG for a null cfg.
+ * n_workgroups is the decode grid the fused step would run on (msd_default_workgroups of the
+ * device; 0 or less: 256, one per compute unit of an MI355X).  Makes no HIP call, so a host
+ * can check a checkpoint's shape before touching the device.  Limits: d_head 64, n_heads a
+ * multiple of n_kv_heads; the fused step needs one of the instantiated (d_model, d_ff) pairs
+ * (see msd_decode_step) and context_len <= 2048; prefill d_model <= 1024 with d_model and
+ * vocab_size multiples of 64 and d_ff of 32; verification and batched decode also
+ * context_len <= 2048; the
+ * sampler vocab_size <= 32768.  No counterpart in the reference (its Triton kernel takes any
+ * shape through constexprs, kernels/multi_sm_decode.py:371-388): this library's shape query. */
+int32_t msd_config_support(const msd_config* cfg, int32_t n_workgroups);
+
 /* Kernel row layout: every row of K bf16 inputs is cut into blocks of 512 (the last block
  * holds the remaining S = 8*m values); within block b the value stored at offset
  * 512*b + 8*l + k (l < m, k < 8) is input element 512*b + k*m + l of the row.
@@ -99,7 +120,8 @@ int32_t msd_default_workgroups(int32_t device);
  * Supported shapes: d_head 64 and (d_model, d_ff) one of (256, 704), (256, 768), (512, 1408),
  * (768, 2048), (1024, 2816) -- the reference's d_ff = 8 d / 3 rounded up to 128 (model.py:13-20)
  * for d_model 256..1024, and the tiny benchmark shape -- with any n_heads = d_model / 64,
- * n_kv_heads dividing n_heads, context_len up to 1024 and n_workgroups no more than the device
+ * n_kv_heads dividing n_heads, context_len up to 2048 (above 512 the attention of each head is
+ * split over ceil(context_len / 512) workgroups) and n_workgroups no more than the device
  * holds at once (every workgroup waits on others; msd_default_workgroups is one per compute
  * unit).  Returns MSD_E_CONFIG otherwise.  Calls that share a workspace must be ordered on one
  * stream, and only one step may run on a device at a time (a concurrent kernel could keep some

@@ -267,6 +267,19 @@ def test_tiny_long_context_two_splits(tiny):
     assert not flips, flips
 
 
+def test_tiny_long_context_four_splits(tiny):
+    """Context 2048: each head's cached positions are split over four attention workgroups (the
+    row workgroups' merge buffer then shares LDS with vectors that are dead during the merge);
+    every position of a random stream over the whole context checked."""
+    params, _, _ = tiny
+    cfg = dict(TINY, context_len=2048)
+    w = prepare_decode_weights_nlayer(params, cfg)
+    seq = make_prompt(cfg["context_len"], cfg["vocab_size"], seed=8)
+    worst, flips = _teacher_forced(params, w, cfg, seq)
+    print("tiny ctx-2048 teacher-forced max |logit diff|:", worst)
+    assert not flips, flips
+
+
 @pytest.fixture(scope="module")
 def m306():
     params = make_params(M306, seed=0, resid_scaled=True)
@@ -471,3 +484,96 @@ def test_306m_whole_generation_in_one_launch(m306):
     lg = logits.cpu().numpy()
     for i in range(0, 479, 60):
         np.testing.assert_allclose(lg[i], rlogs[i + 1], atol=ATOL, rtol=RTOL)
+
+
+def _zeros_workspace_run(w, cfg, tokens_in, positions):
+    """Steps through msd_decode_step with an ordinary torch.zeros workspace (the integration
+    guide's ctypes path): one step per (token, pos), tokens from the host."""
+    from transformer_amd import _lib
+    from transformer_amd.fused_decode_nlayer import new_kv_packed
+    L = _lib.lib()
+    cfg_c = _lib.MsdConfig.from_dict(cfg)
+    G = _lib.check(L.msd_default_workgroups(torch.cuda.current_device()), "msd_default_workgroups")
+    ws = torch.zeros(_lib.check(L.msd_workspace_bytes(ctypes.byref(cfg_c), G), "msd_workspace_bytes"),
+                     dtype=torch.uint8, device="cuda")
+    kv = new_kv_packed(cfg)
+    logits = torch.empty(cfg["vocab_size"], dtype=torch.float32, device="cuda")
+    out = torch.zeros(2, dtype=torch.int32, device="cuda")
+    s = torch.cuda.current_stream()
+    res = []
+    for epoch, (t, p) in enumerate(zip(tokens_in, positions), start=1):
+        rc = L.msd_decode_step(ctypes.byref(cfg_c), w["token_emb"].data_ptr(), w["output_proj"].data_ptr(),
+                               w["packed_w"].data_ptr(), w["lnf_s"].data_ptr(), w["rope"].data_ptr(), int(t), None,
+                               int(p), kv.data_ptr(), ws.data_ptr(), epoch, logits.data_ptr(), out.data_ptr(), G,
+                               ctypes.c_void_p(s.cuda_stream))
+        assert rc == 0
+        o = out.cpu().numpy()
+        assert o[1] == 0
+        res.append((int(o[0]), logits.cpu().numpy().copy()))
+    return res, kv
+
+
+@pytest.mark.parametrize("shape", ["tiny", "306m"])
+def test_ordinary_zeroed_workspace_matches_pool_workspace(shape):
+    """The workspace may be any zero-filled device memory: torch.zeros memory gives the pooled
+    uncached workspace's tokens, logits and cache bitwise (tiny: the prompt fed step by step,
+    then greedy steps; 306M: a prompt of 8 and 12 greedy steps), and the tiny tokens equal the
+    oracle's greedy generation."""
+    cfg = TINY if shape == "tiny" else M306
+    params = make_params(TINY, seed=0) if shape == "tiny" else make_params(M306, seed=0, resid_scaled=True)
+    w = prepare_decode_weights_nlayer(params, cfg)
+    P, n_new = (16, 24) if shape == "tiny" else (8, 12)
+    prompt = make_prompt(P, cfg["vocab_size"], seed=1)
+    dec = Decoder(w, cfg)
+    toks_pool, logs_pool = [], []
+    inputs, positions = [int(t) for t in prompt], list(range(P))
+    for t, p in zip(inputs, positions):
+        tok, lg = dec.step(t, p)
+    toks_pool.append(tok)
+    logs_pool.append(lg.cpu().numpy().copy())
+    for i in range(n_new - 1):
+        tok, lg = dec.step(toks_pool[-1], P + i)
+        toks_pool.append(tok)
+        logs_pool.append(lg.cpu().numpy().copy())
+    # the same inputs through the ordinary workspace
+    all_in = inputs + toks_pool[:-1]
+    all_pos = positions + [P + i for i in range(n_new - 1)]
+    res, kv = _zeros_workspace_run(w, cfg, all_in, all_pos)
+    got = res[P - 1:]
+    assert [t for t, _ in got] == toks_pool
+    for (_, a), b in zip(got, logs_pool):
+        assert np.array_equal(a, b)
+    assert torch.equal(kv.view(torch.int16), dec.kv.view(torch.int16))
+    if shape == "tiny":
+        assert toks_pool == om.greedy_generate(params, TINY, prompt, n_new, prefill="step")
+
+
+def test_306m_context_2048_prefill_then_decode(m306):
+    """306M with a 2048-position context: a 1900-token prompt prefilled in one pass (last-row
+    logits against the oracle), then 24 decode steps at positions 1900..1923 on a random stream
+    (four context splits per head): argmax exact, logits within tolerance."""
+    from transformer_amd.fused_decode_nlayer import new_kv_packed
+    from transformer_amd.prefill import Prefiller
+    params, _ = m306
+    cfg = dict(M306, context_len=2048)
+    w = prepare_decode_weights_nlayer(params, cfg)
+    P = 1900
+    prompt = make_prompt(P, cfg["vocab_size"], seed=31)
+    dec = Decoder(w, cfg)
+    pf = Prefiller(w, cfg, max_tokens=P)
+    out = pf.launch(prompt, dec.kv).cpu().numpy()
+    assert out[1] == 0
+    ref_all, kc, vc = om.prefill_with_kv(params, cfg, prompt)
+    assert out[0] == int(np.argmax(ref_all[-1]))
+    np.testing.assert_allclose(pf.logits.cpu().numpy(), ref_all[-1], atol=ATOL, rtol=RTOL)
+    rope = om.precompute_rope_table(cfg["context_len"], cfg["d_head"])
+    seq = make_prompt(24, cfg["vocab_size"], seed=32)
+    worst = 0.0
+    for i, t in enumerate(seq):
+        tok, lg = dec.step(int(t), P + i)
+        ref, rtok = om.decode_step(params, cfg, int(t), P + i, kc, vc, rope=rope)
+        got = lg.cpu().numpy()
+        worst = max(worst, float(np.abs(got - ref).max()))
+        np.testing.assert_allclose(got, ref, atol=ATOL, rtol=RTOL)
+        assert tok == rtok, (P + i, tok, rtok)
+    print("306M ctx-2048 decode max |logit diff|:", worst)

@@ -27,7 +27,8 @@ _PARAMS = {}
 
 def _params(name):
     if name not in _PARAMS:
-        _PARAMS[name] = make_params(TINY, seed=0) if name == "tiny" else make_params(M306, seed=0, resid_scaled=True)
+        _PARAMS[name] = (make_params(TINY, seed=0) if name.startswith("tiny")
+                         else make_params(M306, seed=0, resid_scaled=True))
     return _PARAMS[name]
 
 
@@ -138,6 +139,14 @@ def test_306m_multi_kernel_step_9_sequences():
     lens = [int(x) for x in rng.integers(16, 257, 8)] + [200]
     worst, gap = _run_and_check("306m", M306, 9, lens, 64, 288, seed=5)
     print("306M multi-kernel: lens", lens, "max |logit diff|", worst, "smallest oracle top-2 gap", gap)
+
+
+def test_tiny_batched_context_2048():
+    """A 2048-position context (beyond the persistent step's reach: the multi-kernel step takes
+    it): 3 sequences with prompts of 700-1900 tokens, 8 free-running steps against the oracle."""
+    cfg = dict(TINY, context_len=2048)
+    worst, gap = _run_and_check("tiny2048", cfg, 3, [1900, 700, 1333], 8, 320, seed=14)
+    print("tiny ctx-2048 batched: max |logit diff|", worst, "smallest oracle top-2 gap", gap)
 
 
 def test_batched_step_matches_single_sequence_rows():

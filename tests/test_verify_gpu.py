@@ -57,6 +57,17 @@ def test_tiny_verification_rows_equal_sequential_decode_steps():
         print(f"tiny verify P={P} k={k} max |logit diff| {worst}")
 
 
+def test_tiny_verification_at_context_2048():
+    """A 2048-position context: 6 draft rows verified after a 1500-token prompt (each attention
+    wave takes up to four 64-position blocks)."""
+    params = make_params(TINY, seed=0)
+    cfg = dict(TINY, context_len=2048)
+    w = prepare_decode_weights_nlayer(params, cfg)
+    draft = make_prompt(6, cfg["vocab_size"], seed=33)
+    worst = _check_rows(params, cfg, w, 1500, draft)
+    print("tiny ctx-2048 verify max |logit diff|", worst)
+
+
 def test_306m_verification_rows_equal_sequential_decode_steps():
     params = make_params(M306, seed=0, resid_scaled=True)
     w = prepare_decode_weights_nlayer(params, M306)
@@ -81,6 +92,82 @@ def test_speculative_generation_is_the_target_greedy_generation(draft_kind):
     assert toks == ref
     if draft_kind == "same_model":
         assert stats["accepted_draft_tokens"] > 0
+
+
+class _ScriptedProposer:
+    """Draft proposals planted from the target's known greedy tokens: in cycle c the first
+    plan[c % len(plan)] proposals are the target's own next tokens and the one after is wrong,
+    so the verification must accept exactly that many (0 < j < k included)."""
+
+    def __init__(self, ref, P, vocab, plan):
+        self.ref, self.P, self.vocab, self.plan, self.cycle = ref, P, vocab, plan, 0
+        self.planned = []
+        self.buf = torch.empty(64, dtype=torch.int32, device="cuda")
+        self.stat = torch.zeros((64, 2), dtype=torch.int32, device="cuda")
+
+    def prefill(self, prompt_ids):
+        return None
+
+    def propose(self, x, n, k):
+        i0 = n - self.P                      # x is ref[i0]; the target's next tokens are ref[i0 + 1 ..]
+        j = min(self.plan[self.cycle % len(self.plan)], k)
+        self.cycle += 1
+        nxt = [self.ref[i0 + 1 + i] if i0 + 1 + i < len(self.ref) else 7 for i in range(k + 1)]
+        d = list(nxt)
+        if j < k:
+            d[j] = (nxt[j] + 1) % self.vocab   # the first wrong proposal
+            for i in range(j + 1, k + 1):
+                d[i] = (3 * i + 11) % self.vocab
+        self.planned.append(j)
+        self.buf[:k + 2].copy_(torch.tensor([x] + d, dtype=torch.int32))
+        self.stat[:k + 1, 0].copy_(torch.tensor(d, dtype=torch.int32))
+        return self.buf[:k + 2], self.stat[:k + 1]
+
+
+def test_speculative_partial_acceptance_follows_the_target():
+    """Planted agreement lengths 0..k: every cycle accepts exactly its planted prefix, the
+    rejected rows are rewritten by later cycles, and the output is the target's greedy
+    generation."""
+    params = make_params(TINY, seed=0)
+    w = prepare_decode_weights_nlayer(params, TINY)
+    prompt = make_prompt(16, TINY["vocab_size"], seed=1)
+    n_new, k = 60, 4
+    ref = om.greedy_generate(params, TINY, prompt, n_new + k + 2, prefill="full")
+    prop = _ScriptedProposer(ref, len(prompt), TINY["vocab_size"], plan=[1, 3, 2, 0, 4, 2, 1, 3])
+    toks, stats = speculative_generate(w, TINY, w, TINY, prompt, n_new, k=k, proposer=prop)
+    print(stats)
+    assert toks == ref[:n_new]
+    acc = stats["accepted_per_verification"]
+    assert acc == prop.planned[:len(acc)]
+    assert {1, 2, 3} <= set(acc) and 0 in acc and k in acc
+
+
+def test_verification_reads_device_tokens():
+    """The draft tokens as a device int32 tensor give the host list's results bitwise; a device
+    id outside the vocabulary is replaced by 0 and reported in its row's status."""
+    params = make_params(TINY, seed=0)
+    w = prepare_decode_weights_nlayer(params, TINY)
+    prompt = make_prompt(30, TINY["vocab_size"], seed=21)
+    draft = make_prompt(5, TINY["vocab_size"], seed=77).tolist()
+    res = []
+    for form in ("host", "device"):
+        kv = new_kv_packed(TINY)
+        Prefiller(w, TINY, max_tokens=30).launch(prompt, kv)
+        ver = Verifier(w, TINY, max_tokens=5)
+        toks = draft if form == "host" else torch.tensor(draft, dtype=torch.int32, device="cuda")
+        logits, am = ver.launch(toks, 30, kv)
+        res.append((logits.cpu().numpy().copy(), am.cpu().numpy().copy(), kv.view(torch.int16).cpu().numpy()))
+    assert np.array_equal(res[0][0], res[1][0]) and np.array_equal(res[0][1], res[1][1])
+    assert np.array_equal(res[0][2], res[1][2])
+    kv = new_kv_packed(TINY)
+    Prefiller(w, TINY, max_tokens=30).launch(prompt, kv)
+    ver = Verifier(w, TINY, max_tokens=5)
+    bad = torch.tensor([draft[0], TINY["vocab_size"] + 3, draft[2]], dtype=torch.int32, device="cuda")
+    _, am = ver.launch(bad, 30, kv)
+    a = am.cpu().numpy()
+    assert a[:, 1].any()
+    with pytest.raises(ValueError):
+        ver.launch(bad.to(torch.int64), 30, kv)
 
 
 def test_verification_argument_checks():

@@ -9,21 +9,41 @@ M306 = dict(vocab_size=32000, d_model=1024, n_heads=16, n_kv_heads=4, n_layers=2
             d_head=64, d_ff=2816, context_len=512)
 
 
-def check_config(config):
-    """Validate the shape relations the kernels rely on; raises ValueError."""
+def check_config(config, need=("decode", "prefill")):
+    """Validate a config against the library's paths; returns d_head, raises ValueError.
+
+    The shape relations come first (n_heads * d_head == d_model, GQA grouping); then every path
+    named in ``need`` (``"decode"``, ``"prefill"``, ``"verify"``, ``"batched"``, ``"sample"``) must
+    accept the config (``msd_config_support``, no device call), so an unsupported checkpoint is
+    refused before any weight reaches the device."""
     d, H, KV = config["d_model"], config["n_heads"], config["n_kv_heads"]
     dh = config.get("d_head", d // H)
     if H * dh != d:
         raise ValueError(f"n_heads*d_head ({H}*{dh}) != d_model ({d})")
     if H % KV != 0:
         raise ValueError(f"n_heads ({H}) not a multiple of n_kv_heads ({KV})")
-    if dh != 64:
-        raise ValueError(f"d_head must be 64 (got {dh})")
-    if d % 256 != 0 or d > 4096:
-        raise ValueError(f"d_model must be a multiple of 256 and <= 4096 (got {d})")
-    if config["d_ff"] % 16 != 0:
-        raise ValueError(f"d_ff must be a multiple of 16 (got {config['d_ff']})")
+    missing = [p for p in need if p not in supported_paths(config)]
+    if missing:
+        raise ValueError(f"config (d_model {d}, d_ff {config['d_ff']}, d_head {dh}, context_len "
+                         f"{config['context_len']}, vocab {config['vocab_size']}) is not supported by the "
+                         f"{', '.join(missing)} path(s): the fused decode step takes d_head 64, (d_model, d_ff) in "
+                         f"{DECODE_SHAPES} and context_len <= 2048; prefill takes d_model <= 1024")
     return dh
+
+
+# (d_model, d_ff) pairs the fused decode step is compiled for: the reference's
+# d_ff = 8 d / 3 rounded up to 128 (model.py:13-20) for d_model 256..1024, and d_ff 704 at 256
+DECODE_SHAPES = ((256, 704), (256, 768), (512, 1408), (768, 2048), (1024, 2816))
+
+
+def supported_paths(config, n_workgroups=0):
+    """Names of the library paths that accept ``config`` (``msd_config_support``)."""
+    import ctypes
+
+    from . import _lib
+    c = _lib.MsdConfig.from_dict(config)
+    bits = _lib.check(_lib.lib().msd_config_support(ctypes.byref(c), int(n_workgroups)), "msd_config_support")
+    return {name for name, b in _lib.PATHS.items() if bits & b}
 
 
 def bytes_per_token(config, pos):

@@ -56,6 +56,7 @@
 #include <vector>
 
 #include "batched.h"
+#include "internal.h"
 
 namespace mbd {
 
@@ -1147,7 +1148,6 @@ static bool same_cfg(const msd_config& a, const msd_config& b) {
 static Plan device_plan(const msd_config* c, hipError_t& err) {
   static std::mutex mu;
   static std::vector<Cached> cache;
-  static size_t attr_lds = 0;
   err = hipSuccess;
   int dev = 0;
   if ((err = hipGetDevice(&dev)) != hipSuccess) return Plan{};
@@ -1159,11 +1159,7 @@ static Plan device_plan(const msd_config* c, hipError_t& err) {
   Plan p = cus >= 8 && cus <= kMaxGrid ? make_plan(c, cus) : Plan{};
   if (p.ok) {
     const void* fn = reinterpret_cast<const void*>(&batch_step_kernel);
-    if (attr_lds < p.lds) {
-      if ((err = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, int(p.lds))) != hipSuccess)
-        return Plan{};
-      attr_lds = p.lds;
-    }
+    if ((err = msdc::ensure_dynamic_lds(fn, p.lds)) != hipSuccess) return Plan{};
     int per_cu = 0;
     if ((err = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kThreads, p.lds)) != hipSuccess)
       return Plan{};

@@ -47,6 +47,7 @@
 #include <vector>
 
 #include "../../include/msdecode.h"
+#include "internal.h"
 
 namespace msd {
 
@@ -86,6 +87,7 @@ __device__ uint64_t msd_trace_waves[4096 * 16 * 8];
 constexpr int kDh = 64;          // head dimension (fixed)
 constexpr int kPart = 66;        // per (head, split): m, l, o[64]
 constexpr int kAttCap = 512;     // cached positions an attention workgroup holds in LDS
+constexpr int kMaxCtx = 2048;    // context: at most 4 splits of kAttCap positions per head
 constexpr int kKRowB = 144;      // LDS bytes per cached K row: 128 + 16 padding, so 16-byte
                                  // reads of consecutive rows by consecutive lanes never conflict
 constexpr int kVRowB = 128;      // LDS bytes per cached V row
@@ -932,7 +934,11 @@ __device__ void row_worker(const Args& a, const RowCtx& c, int token) {
         gather_x<kWavesR, HPW, 0, kAttFirstPoll, D>(X + lay.x_att + myrep, D, c.xatt, tag, a.ctrl, wv, lane, bad);
         MSD_TRACE_POINT(wv == 0, l, 3);
       } else {
-        gather_x<kWavesR, NKA2, 0, kAttFirstPoll>(X + lay.x_att + myrep, natt * kPart, c.xa, tag, a.ctrl, wv, lane, bad);
+        // in pieces of at most two splits' words (four splits: two pieces)
+        const int nw = natt * kPart, piece = 2 * a.H * kPart;
+        for (int b = 0; b < nw; b += piece)
+          gather_x<kWavesR, NKA2, 0, kAttFirstPoll>(X + lay.x_att + myrep + b, min(piece, nw - b), c.xa + b, tag,
+                                                    a.ctrl, wv, lane, bad);
         MSD_TRACE_POINT(wv == 0, l, 3);
         bar();
         MSD_TRACE_POINT(wv == 0, l, 4);
@@ -1534,8 +1540,11 @@ __global__ __launch_bounds__(kThreadsWG, 1) void decode_step_kernel(Args a) {
   c.xhd1 = c.xatt + D;
   c.xhd2 = c.xhd1 + D;
   c.xact = c.xhd2 + D;
-  c.xa = c.xact + ((FF + 3) & ~3);
-  c.ctr = reinterpret_cast<int*>(c.xa + ((a.H * a.nsplit * kPart + 3) & ~3));
+  // the (head, split) partials: their own region with two splits; with more they share the
+  // O-output, down-output and activation vectors, none of which is live from the QKV stores'
+  // barrier to the O gather (the merge ends in a barrier before that gather writes xhd1)
+  c.xa = a.nsplit > 2 ? c.xhd1 : c.xact + ((FF + 3) & ~3);
+  c.ctr = reinterpret_cast<int*>(c.xact + ((FF + 3) & ~3) + (a.nsplit > 2 ? 0 : ((a.H * a.nsplit * kPart + 3) & ~3)));
   c.red_v = reinterpret_cast<float*>(c.ctr + 8);
   c.red_i = reinterpret_cast<int*>(c.red_v + kWavesR);
   if (threadIdx.x < 8) c.ctr[threadIdx.x] = 0;
@@ -1624,7 +1633,7 @@ static bool config_ok(const msd_config* c) {
   if (c->d_head != kDh || c->n_heads <= 0 || c->n_kv_heads <= 0 || c->n_layers <= 0) return false;
   if (c->n_heads * kDh != c->d_model || c->n_heads % c->n_kv_heads != 0) return false;
   if (c->d_ff <= 0 || c->d_ff % 16 != 0 || c->vocab_size <= 0 || c->context_len <= 0) return false;
-  if (c->context_len > 1024) return false;
+  if (c->context_len > kMaxCtx) return false;
   return find_shape(c->d_model, c->d_ff) != nullptr;
 }
 
@@ -1659,7 +1668,9 @@ static bool make_plan(const msd_config* c, int G, Plan* p) {
   ring = std::max(ring, 4 * D * 2);          // at least two logit rows per ring half
   ring = (ring + 2047) / 2048 * 2048;        // halves of whole KB
   const int natt = H * p->nsplit * kPart;
-  const int row_other = 4 * (3 * D + ((ff + 3) & ~3) + ((natt + 3) & ~3) + 8 + 2 * kWavesR);
+  // more than two splits: the partials alias xhd1 | xhd2 | xact (2 D + d_ff floats)
+  if (p->nsplit > 2 && natt > 2 * D + ff) return false;
+  const int row_other = 4 * (3 * D + ((ff + 3) & ~3) + (p->nsplit > 2 ? 0 : ((natt + 3) & ~3)) + 8 + 2 * kWavesR);
   const int att_lds = cdiv(p->cap * 9, 64) * 1024 + cdiv(p->cap, 8) * 1024 +
                       2 * 3 * kWavesA * kDh + 4 * (3 * kWavesA * kDh + 4 * kWavesA + 4);
   const int budget = std::max(std::max(att_lds, kMinLds), ring + row_other);
@@ -1695,13 +1706,8 @@ static int resident_capacity(const void* fn, size_t lds) {
 
 template <int D, int FF, int QPW, int ORW, int GPW, bool MULTI>
 static hipError_t launch_t(const Args& a, int grid, size_t lds, hipStream_t s, bool* not_resident) {
-  static size_t attr_lds = 0;
   const void* fn = reinterpret_cast<const void*>(&decode_step_kernel<D, FF, QPW, ORW, GPW, MULTI>);
-  if (attr_lds < lds) {
-    hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
-    if (e != hipSuccess) return e;
-    attr_lds = lds;
-  }
+  if (hipError_t e = msdc::ensure_dynamic_lds(fn, lds); e != hipSuccess) return e;
   const int cap = resident_capacity(fn, lds);
   if (cap < 0) return hipErrorInvalidValue;
   if (grid > cap) {
@@ -1729,6 +1735,35 @@ static hipError_t launch(const Args& a, int d, int ff, int grid, size_t lds, hip
 }
 
 }  // namespace msd
+
+hipError_t msdc::ensure_dynamic_lds(const void* fn, size_t lds) {
+  struct Entry {
+    const void* fn;
+    int dev;
+    size_t lds;
+  };
+  static std::mutex mu;
+  static std::vector<Entry> set;
+  int dev = 0;
+  if (hipError_t e = hipGetDevice(&dev); e != hipSuccess) return e;
+  std::lock_guard<std::mutex> lk(mu);
+  Entry* hit = nullptr;
+  for (Entry& x : set)
+    if (x.fn == fn && x.dev == dev) hit = &x;
+  if (hit && hit->lds >= lds) return hipSuccess;
+  if (hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, int(lds)); e != hipSuccess)
+    return e;
+  if (hit)
+    hit->lds = lds;
+  else
+    set.push_back({fn, dev, lds});
+  return hipSuccess;
+}
+
+bool msdc::decode_supported(const msd_config* cfg, int n_workgroups) {
+  msd::Plan p;
+  return msd::config_ok(cfg) && msd::make_plan(cfg, n_workgroups, &p) && msd::plan_instantiated(cfg, p);
+}
 
 using namespace msd;
 

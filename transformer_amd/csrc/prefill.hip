@@ -52,6 +52,7 @@
 
 #include "../../include/msdecode.h"
 #include "batched.h"
+#include "internal.h"
 
 namespace mpf {
 
@@ -819,7 +820,8 @@ __global__ __launch_bounds__(256) void mx_attention_prefill(const float* qkv, in
 // so the block costs two memory round trips; each wave keeps its own maximum and sum and the
 // waves' states are merged in LDS at the end.
 constexpr int kAttnWaves = 8;
-
+// Positions mx_attention_decode covers: wave w takes the 64-position blocks w, w + 8, ...
+constexpr int kAttnMaxCtx = 2048;
 __global__ __launch_bounds__(64 * kAttnWaves) void mx_attention_decode(const float* qkv, Rows rows, int H, int KV,
                                                                        const uint16_t* kc, const uint16_t* vc,
                                                                        uint16_t* att, int64_t plane, int ldx,
@@ -832,23 +834,27 @@ __global__ __launch_bounds__(64 * kAttnWaves) void mx_attention_decode(const flo
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int m = blockIdx.x, h = blockIdx.y, g = h / (H / KV);
   const int nqkv = (H + 2 * KV) * kDh, d = H * kDh;
-  const int j0 = 64 * wv, j = j0 + lane;
-  // q, the page-table entries and p are loaded together: the page-table load does not wait for
-  // p (every entry of a row is a sanitized page; p only selects which rows are cached
-  // positions), and no load sits under a branch (it would be waited for at the join)
+  // q, the page-table entries of the first block and p are loaded together: the page-table load
+  // does not wait for p (every entry of a row is a sanitized page; p only selects which rows are
+  // cached positions), and no load sits under a branch (it would be waited for at the join)
   const float* qr = qkv + int64_t(m) * nqkv;
   const int qsel = min(int(threadIdx.x) / kDh, 2);   // threads 0..63: q, 64..127: k, others: v
   const float qv = qr[(qsel == 0 ? h : (qsel == 1 ? H + g : H + KV + g)) * kDh + (threadIdx.x & (kDh - 1))];
-  const int64_t cr = cache_row(rows, m, rows.pages ? min(j, rows.max_pages * kPage - 1) : j);
+  auto row_of = [&](int j) { return cache_row(rows, m, rows.pages ? min(j, rows.max_pages * kPage - 1) : j); };
+  int64_t cr = row_of(64 * wv + lane);
   const int p = row_pos(rows, m);
   if (threadIdx.x < 3 * kDh) (qsel == 0 ? sq : (qsel == 1 ? skc : svc))[threadIdx.x & (kDh - 1)] = qv;
   const uint16_t* kg = kc + int64_t(g) * rows.pool * kDh;
   const uint16_t* vg = vc + int64_t(g) * rows.pool * kDh;
-  const int nj = max(0, min(64, p + 1 - j0));   // positions of this wave (the last one may be p)
-  srow[wv][lane] = j < p ? int(cr) : 0;
   __syncthreads();
   float mx = -INFINITY, ls = 0.f, o = 0.f;
-  if (nj > 0) {
+  // blocks wv, wv + 8, ... up to the one holding p (each holds at least one position <= p);
+  // the first is taken as it is, later ones merged by log-sum-exp
+  for (int blk = wv; 64 * blk <= p; blk += kAttnWaves) {
+    const int j0 = 64 * blk, j = j0 + lane;
+    if (blk != wv) cr = row_of(j);
+    srow[wv][lane] = j < p ? int(cr) : 0;
+    __builtin_amdgcn_wave_barrier();
     uint4 ku[kDh / 8];
     const uint4* kr = reinterpret_cast<const uint4*>(kg + int64_t(srow[wv][lane]) * kDh);
 #pragma unroll
@@ -877,9 +883,9 @@ __global__ __launch_bounds__(64 * kAttnWaves) void mx_attention_decode(const flo
       }
       s = (a0 + a1) * 0.125f;
     }
-    mx = wave_max(s);
-    const float e = (s == -INFINITY) ? 0.f : expf(s - mx);
-    ls = wave_sum(e);
+    const float bmx = wave_max(s);
+    const float e = (s == -INFINITY) ? 0.f : expf(s - bmx);
+    const float bls = wave_sum(e);
     sp[wv][lane] = e;
     __builtin_amdgcn_wave_barrier();
     const float vcur = svc[lane];
@@ -889,7 +895,19 @@ __global__ __launch_bounds__(64 * kAttnWaves) void mx_attention_decode(const flo
       const float v = j0 + jj < p ? bf2f(vv[jj]) : (j0 + jj == p ? vcur : 0.f);
       o4[jj & 3] += sp[wv][jj] * v;
     }
-    o = (o4[0] + o4[1]) + (o4[2] + o4[3]);
+    const float bo = (o4[0] + o4[1]) + (o4[2] + o4[3]);
+    if (blk == wv) {
+      mx = bmx;
+      ls = bls;
+      o = bo;
+    } else {
+      const float M = fmaxf(mx, bmx);
+      const float a0 = expf(mx - M), a1 = expf(bmx - M);
+      ls = ls * a0 + bls * a1;
+      o = o * a0 + bo * a1;
+      mx = M;
+    }
+    __builtin_amdgcn_wave_barrier();   // srow and sp are rewritten by the next block
   }
   so[wv][lane] = o;
   if (lane == 0) {
@@ -1439,7 +1457,7 @@ static int32_t prefill_impl(const msd_config* cfg, const Weights& wt, const int3
   if (!mx_config_ok(cfg)) return MSD_E_CONFIG;
   const int M = n_tokens;
   if (M <= 0 || start < 0 || start + M > cfg->context_len) return MSD_E_ARG;
-  if (start > 0 && cfg->context_len > 64 * kAttnWaves) return MSD_E_CONFIG;   // decode attention: 512 positions
+  if (start > 0 && cfg->context_len > kAttnMaxCtx) return MSD_E_CONFIG;   // decode attention
   if (argmax_all && !logits_all) return MSD_E_ARG;
   if (!wt.emb || !wt.outp || !wt.w || !wt.lnf || !wt.rope || !tokens || !kv || !workspace || !logits_last ||
       !next_token)
@@ -1593,7 +1611,7 @@ extern "C" int32_t msd_batch_decode_step(const msd_config* cfg, const void* toke
       !aligned16(workspace) || !aligned16(tiles))
     return MSD_E_ARG;
   if (max_pages <= 0 || max_pages > (cfg->context_len + kPage - 1) / kPage || pool_pages <= 0) return MSD_E_ARG;
-  if (cfg->context_len > 64 * kAttnWaves) return MSD_E_CONFIG;   // one 64-position block per attention wave
+  if (cfg->context_len > kAttnMaxCtx) return MSD_E_CONFIG;   // decode attention
   hipStream_t s = static_cast<hipStream_t>(stream);
   {   // up to 8 sequences: one persistent launch when the shape and the device allow it
     const mbd::StepArgs sa{cfg, static_cast<const uint16_t*>(token_emb), static_cast<const uint16_t*>(output_proj),
@@ -1637,6 +1655,19 @@ extern "C" int32_t msd_batch_decode_step(const msd_config* cfg, const void* toke
   hipLaunchKernelGGL(mx_argmax, dim3(M), dim3(1024), 0, s, logits, V, V, next_tokens, status);
   return hipGetLastError() == hipSuccess ? MSD_OK : MSD_E_HIP;
   });
+}
+
+extern "C" int32_t msd_config_support(const msd_config* cfg, int32_t n_workgroups) {
+  if (!cfg) return MSD_E_ARG;
+  const int G = n_workgroups > 0 ? n_workgroups : 256;
+  int32_t paths = 0;
+  if (msdc::decode_supported(cfg, G)) paths |= MSD_PATH_DECODE;
+  if (mx_config_ok(cfg)) {
+    paths |= MSD_PATH_PREFILL;
+    if (cfg->context_len <= kAttnMaxCtx) paths |= MSD_PATH_VERIFY | MSD_PATH_BATCHED;
+  }
+  if (msdc::sample_supported(cfg->vocab_size)) paths |= MSD_PATH_SAMPLE;
+  return paths;
 }
 
 extern "C" int32_t msd_set_launch_graphs(int32_t enabled) {

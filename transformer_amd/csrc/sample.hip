@@ -37,6 +37,7 @@
 #include <mutex>
 
 #include "../../include/msdecode.h"
+#include "internal.h"
 
 // Every float operation below is a separately rounded IEEE operation (no contraction).
 #pragma clang fp contract(off)
@@ -800,16 +801,11 @@ constexpr SLayout slayout(int V) {
   return s;
 }
 
-static hipError_t set_lds_once() {
-  static bool done = false;
-  if (done) return hipSuccess;
+static hipError_t set_big_lds() {
   const void* big[] = {reinterpret_cast<const void*>(&sample_full_kernel),
                        reinterpret_cast<const void*>(&sample_nucleus_kernel)};
-  for (const void* k : big) {
-    const hipError_t e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, int(kLdsBig));
-    if (e != hipSuccess) return e;
-  }
-  done = true;
+  for (const void* k : big)
+    if (const hipError_t e = msdc::ensure_dynamic_lds(k, kLdsBig); e != hipSuccess) return e;
   return hipSuccess;
 }
 
@@ -867,7 +863,7 @@ static int32_t sample_impl(const float* logits, int32_t vocab, double temperatur
   if (double(t32) < top_p) t32 = nextafterf(t32, INFINITY);
   a.t32 = t32;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (set_lds_once() != hipSuccess) return MSD_E_HIP;
+  if (set_big_lds() != hipSuccess) return MSD_E_HIP;
   if (a.mode == kGreedy) {
     hipLaunchKernelGGL(sample_greedy_kernel, dim3(1), dim3(kT), 0, s, a);
     return hipGetLastError() == hipSuccess ? MSD_OK : MSD_E_HIP;
@@ -898,6 +894,8 @@ static int32_t sample_impl(const float* logits, int32_t vocab, double temperatur
 }
 
 }  // namespace mss
+
+bool msdc::sample_supported(int vocab) { return vocab >= 1 && vocab <= kVMax; }
 
 extern "C" int32_t msd_sample_token(const float* logits, int32_t vocab, double temperature, double top_p,
                                     double rep_penalty, uint8_t* seen, const double* uniform,

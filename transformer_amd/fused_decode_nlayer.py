@@ -143,7 +143,7 @@ def prepare_decode_weights_nlayer(params, config, kv_splits=1, device=None):
     ``tiles`` (``weight_tiles``) on first use.
     """
     from .configs import check_config
-    dh = check_config(config)
+    dh = check_config(config, need=("decode",))
     dev = _dev(device)
     vocab = config["vocab_size"]
     align = 32 * config["n_heads"] * kv_splits

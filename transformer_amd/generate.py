@@ -248,6 +248,8 @@ def main(argv=None):
     args = parser.parse_args(argv)
 
     params, config = load_weights(args.weights)
+    from .configs import check_config
+    check_config(config, need=("decode", "prefill", "sample"))   # before any weight reaches the device
     tok_src = args.tokenizer or os.path.join(os.path.dirname(os.path.abspath(args.weights)), "data")
     bpe = load_bpe_vocab(tok_src)
     decode_fn, encode_fn = bpe["decode_fn"], bpe["encode_fn"]

@@ -132,5 +132,5 @@ class PagedBatchDecoder:
         out = self.launch(self._step_in[0], self._step_in[1]).cpu().numpy()
         st = int(np.bitwise_or.reduce(out[1::2]))
         if st:
-            raise _lib.MsdError(_lib.MSD_E_ARG, f"batched decode step (status {st:#x})")
+            raise _lib.status_error(st, "batched decode step")
         return [int(x) for x in out[0::2]], self.logits
