@@ -27,4 +27,11 @@ Pinning status of each function (what checks it, besides the HIP path):
   (the routine ``generate.py`` calls) on the same uniform draw, plus closed
   forms (temperature 0 = argmax, penalty sign rule).
 * ``bf16_round`` — pinned against torch's round-to-nearest-even cast.
+* ``xent.chunked_ce_fwd`` / ``xent.fused_ce_bwd`` (the training-side fused
+  cross-entropy, model.py:281-361) — pinned against torch's
+  ``cross_entropy`` and its autograd gradients in float64, repeated targets
+  included, and against closed forms (zero logits: loss = log V and grad_h
+  = (uniform - onehot) W / N; the logit gradient's rows sum to zero, so the
+  rows of grad_weight sum to zero; a dominant target logit gives loss 0);
+  independent of the chunk size.
 """

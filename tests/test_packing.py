@@ -12,10 +12,14 @@ from transformer_amd.synthetic import make_params
 
 
 def test_library_exports_every_declared_symbol():
-    L = _lib.lib()
-    hdr = open(_lib.os.path.join(_lib.HERE, "..", "include", "msdecode.h")).read()
+    """Every function the headers under include/ declare is exported by the library, and the
+    binding's list is exactly that set."""
+    import glob
     import re
-    declared = set(re.findall(r"\b(msd_[a-z_]+)\s*\(", hdr))
+    L = _lib.lib()
+    declared = set()
+    for h in sorted(glob.glob(_lib.os.path.join(_lib.HERE, "..", "include", "*.h"))):
+        declared |= set(re.findall(r"\b(msd_[a-z_]+)\s*\(", open(h).read()))
     assert declared == set(_lib.EXPORTS)
     for name in declared:
         assert getattr(L, name) is not None

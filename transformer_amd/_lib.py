@@ -26,7 +26,7 @@ EXPORTS = ("msd_packed_weight_elems", "msd_workspace_bytes", "msd_default_workgr
            "msd_batch_decode_step", "msd_workspace_acquire", "msd_workspace_release",
            "msd_sample_token_noalloc", "msd_verify_workspace_bytes", "msd_verify",
            "msd_decode_steps", "msd_tiles_bytes", "msd_pack_tiles", "msd_set_launch_graphs",
-           "msd_config_support")
+           "msd_config_support", "msd_xent_workspace_bytes", "msd_xent_forward", "msd_xent_backward")
 
 # Paths of the library (bits of msd_config_support)
 PATHS = {"decode": 1, "prefill": 2, "verify": 4, "batched": 8, "sample": 16}
@@ -121,6 +121,12 @@ def lib():
     L.msd_verify.restype = I32
     L.msd_config_support.argtypes = [CP, I32]
     L.msd_config_support.restype = I32
+    L.msd_xent_workspace_bytes.argtypes = [I32, I32, I32, I32]
+    L.msd_xent_workspace_bytes.restype = I64
+    L.msd_xent_forward.argtypes = [P, P, P, I32, I32, I32, P, P, P, P, P]
+    L.msd_xent_forward.restype = I32
+    L.msd_xent_backward.argtypes = [P, P, P, P, P, I32, I32, I32, I32, P, P, P, P, P]
+    L.msd_xent_backward.restype = I32
     _lib = L
     return L
 

@@ -17,7 +17,8 @@ HIPCC_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-shared", f"--offload-arch={ARCH}"
                "-Wno-unused-command-line-argument"]
 
 LIBS = {
-    "libmsdecode.so": ["csrc/msdecode.hip", "csrc/sample.hip", "csrc/prefill.hip", "csrc/batched.hip"],
+    "libmsdecode.so": ["csrc/msdecode.hip", "csrc/sample.hip", "csrc/prefill.hip", "csrc/batched.hip",
+                       "csrc/xent.hip"],
 }
 
 

@@ -1,0 +1,611 @@
+// Fused output projection + cross-entropy, forward and backward, on the matrix cores (gfx950).
+//
+// Reference: model.py:279-379 -- _chunked_ce_fwd (chunked online logsumexp, :281-302),
+// fused_cross_entropy (jax.custom_vjp, :305-312), _fused_ce_bwd (:320-361) and
+// fused_output_and_loss (:367-379).  h (N, d) and weight (V, d) are bf16 (train.py:113 casts the
+// parameters to bf16), targets int32 (N).  Every logit is a bf16 x bf16 dot product accumulated
+// in f32 (v_mfma_f32_32x32x16_bf16); softmax statistics are f32.
+//
+// Forward (msd_xent_forward): one GEMM S = h W^T over the whole vocabulary whose epilogue never
+// stores S: each 256 x 256 tile reduces its rows to a partial (max, sum of exp(s - max)) and
+// captures the target logits; xent_lse merges the partials of a row in vocabulary order
+// (lse = max + log sum, the online logsumexp of :293-301), xent_mean takes the mean of
+// lse - target logit in a fixed order (float64 sum).  The logits never exist in memory, as in the
+// reference, whose chunk loop materialises only one (N, chunk) block at a time.
+//
+// Backward (msd_xent_backward), per vocabulary chunk of `chunk` columns (the reference's
+// chunk loop, :344-353; the chunk bounds the probability buffers):
+//   1. xent_gemm<kEpiProb>: S = h W_c^T, then P' = (exp(S - lse) - onehot(target)) * g / N as bf16,
+//      stored as P (N x C) and its transpose PT (C x N) through LDS staging;
+//   2. xent_gemm<kEpiStoreBf16>: grad_W[c] = PT h   (A = PT, B = h^T: the whole reduction over
+//      N rows, so the chunk's rows of grad_W are final);
+//   3. xent_gemm<kEpiAccF32>: grad_h += P W_c   (A = P, B = W^T columns of the chunk), in f32
+//      across chunks in order; the last chunk also writes the bf16 result.
+// The target terms (:356-358) ride in P' (its -1 at the target column), so grad_h = (softmax -
+// onehot) W g/N and grad_W = (softmax - onehot)^T h g/N as in the reference.  The forward's lse
+// is reused instead of recomputing the logsumexp (:331-340); W^T and h^T are made once per call
+// (xent_transpose) so that every GEMM reads both operands along K.
+//
+// GEMM (xent_gemm<TM, TN, EPI>): C = A B^T with A (M x K) and B (Nn x K) both K-contiguous bf16.
+// A workgroup of 4 waves (2 x 2) owns a TM x TN tile, each wave a (TM/2) x (TN/2) block of
+// 32 x 32 MFMA tiles.  K advances 64 at a time through two LDS stages: every thread loads its
+// 16-byte pieces of the next stage into registers before the current stage's MFMAs and writes
+// them to LDS after, with one barrier per step.  A row of a stage is 128 bytes whose eight
+// 16-byte pieces are stored XOR-swizzled by the row (piece c of row r at c ^ (r & 7)), so the 32
+// rows an MFMA fragment reads hit all 32 banks.  Tiles are dealt to the 8 XCDs in contiguous
+// ranges (workgroup i runs on XCD i % 8), so the workgroups of one XCD share operand rows in
+// its L2.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <math.h>
+
+#include <algorithm>
+#include <utility>
+
+#include "../../include/msxent.h"
+#include "internal.h"
+
+namespace mxe {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));   // a native vector (HIP's uint4 is a struct)
+
+constexpr int kBK = 64;           // K per LDS stage
+constexpr int kThreads = 256;     // 4 waves, 2 x 2
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kStatusTarget = 4;  // a target id outside [0, V) (replaced by 0)
+
+__device__ __forceinline__ bf16x8 as_bf(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+// round to nearest even (finite inputs; NaN stays NaN)
+__device__ __forceinline__ uint16_t f2bf(float x) {
+  const uint32_t u = __float_as_uint(x);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return uint16_t((u >> 16) | 0x40);
+  return uint16_t((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+}
+
+// exp(x) for x <= 0 (x = -inf gives 0): the hardware base-2 exponential of x log2(e)
+__device__ __forceinline__ float exp_neg(float x) { return __builtin_amdgcn_exp2f(x * kLog2e); }
+
+// reductions over the 32 lanes of a half-wave (the lanes that hold one row of an MFMA tile)
+template <int X>
+__device__ __forceinline__ float swz(float v) {
+  return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), (X << 10) | 0x1f));
+}
+__device__ __forceinline__ float half_max(float v) {
+  v = fmaxf(v, swz<1>(v));
+  v = fmaxf(v, swz<2>(v));
+  v = fmaxf(v, swz<4>(v));
+  v = fmaxf(v, swz<8>(v));
+  return fmaxf(v, swz<16>(v));
+}
+__device__ __forceinline__ float half_sum(float v) {
+  v += swz<1>(v);
+  v += swz<2>(v);
+  v += swz<4>(v);
+  v += swz<8>(v);
+  return v + swz<16>(v);
+}
+
+enum Epi { kEpiLse = 0, kEpiProb = 1, kEpiAccF32 = 2, kEpiStoreBf16 = 3 };
+
+struct GemmArgs {
+  const uint16_t* A;   // M x K, row stride lda; rows >= a_valid read row a_valid - 1
+  int64_t lda;
+  int a_valid;
+  const uint16_t* B;   // Nn x K, row stride ldb; rows >= b_valid read row b_valid - 1
+  int64_t ldb;
+  int b_valid;
+  int K;               // multiple of kBK
+  int tiles_m, tiles_n;
+  int m_valid, n_valid;     // output rows / columns that exist (the rest are padding)
+  const int32_t* targets;   // kEpiLse, kEpiProb: sanitized target per row
+  int vcol0;                // kEpiProb: vocabulary index of output column 0
+  const float* lse;         // kEpiProb: per row
+  const float* grad;        // kEpiProb: the loss gradient g (device scalar)
+  float inv_n;              // kEpiProb: 1 / N
+  float* part;              // kEpiLse: (max, sum) per (column tile, row): [tiles_n][ldp][2]
+  int64_t ldp;
+  float* tgt;               // kEpiLse: target logit per row
+  uint16_t* P;              // kEpiProb: rows x ldP
+  int64_t ldP;
+  uint16_t* PT;             // kEpiProb: columns x ldPT
+  int64_t ldPT;
+  float* acc;               // kEpiAccF32: f32 rows x ldacc
+  int64_t ldacc;
+  int accumulate;           // kEpiAccF32: add to acc (else overwrite)
+  uint16_t* out;            // kEpiAccF32 (when not null: bf16 of the total), kEpiStoreBf16
+  int64_t ldout;
+};
+
+template <int TM, int TN>
+constexpr int stage_bytes() { return (TM + TN) * kBK * 2; }
+template <int TM, int TN>
+constexpr int staging_pitch() { return TN + 8; }   // bf16 per row of the epilogue's LDS tile
+template <int TM, int TN, int EPI>
+constexpr size_t lds_bytes() {
+  // kEpiProb: the bf16 staging tile (over the stage buffers) and the rows' lse and targets after it
+  return EPI == kEpiProb ? std::max<size_t>(2 * stage_bytes<TM, TN>(), size_t(TM) * staging_pitch<TM, TN>() * 2 + TM * 8)
+                         : size_t(2 * stage_bytes<TM, TN>());
+}
+
+// Tile (tm, tn) of workgroup b: XCD x = b % 8 takes tile ids [x * per, (x + 1) * per) in order,
+// ids running down a column of tiles first (the workgroups resident on one XCD share B rows and
+// stream the same A rows).
+__device__ __forceinline__ void tile_of(int b, int tiles_m, int tiles_n, int& tm, int& tn) {
+  const int total = tiles_m * tiles_n, per = (total + 7) / 8;
+  const int x = b & 7, k = b >> 3;
+  int t = x * per + k;
+  if (t >= total || per * 8 != total) t = b;   // uneven: the plain order
+  tm = t % tiles_m;
+  tn = t / tiles_m;
+}
+
+// the 16-byte pieces of one stage: global -> registers, registers -> LDS (piece u 4 KB apart);
+// the piece index is a constant of each expansion, so the arrays stay in registers
+template <int N, size_t... U>
+__device__ __forceinline__ void gload_(u32x4 (&r)[N], const uint16_t* base, const uint32_t (&off)[N], int kk,
+                                       std::index_sequence<U...>) {
+  ((r[U] = *reinterpret_cast<const u32x4*>(base + off[U] + kk)), ...);
+}
+template <int N>
+__device__ __forceinline__ void gload(u32x4 (&r)[N], const uint16_t* base, const uint32_t (&off)[N], int kk) {
+  gload_(r, base, off, kk, std::make_index_sequence<N>{});
+}
+template <int N, size_t... U>
+__device__ __forceinline__ void lstore_(uint8_t* dst, const u32x4 (&r)[N], std::index_sequence<U...>) {
+  ((*reinterpret_cast<u32x4*>(dst + 4096 * U) = r[U]), ...);
+}
+template <int N>
+__device__ __forceinline__ void lstore(uint8_t* dst, const u32x4 (&r)[N]) {
+  lstore_(dst, r, std::make_index_sequence<N>{});
+}
+template <int N, size_t... U>
+__device__ __forceinline__ void piece_offsets_(uint32_t (&off)[N], int row, int valid, int64_t ld, int col,
+                                               std::index_sequence<U...>) {
+  ((off[U] = uint32_t(min(row + 32 * int(U), valid - 1)) * uint32_t(ld) + col), ...);
+}
+
+template <int TM, int TN, int EPI>
+__global__ __launch_bounds__(kThreads) void xent_gemm(GemmArgs g) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  constexpr int WM = TM / 2, WN = TN / 2;   // wave tile
+  constexpr int RB = WM / 32, CB = WN / 32;
+  constexpr int STAGE = stage_bytes<TM, TN>();
+  constexpr int LA = TM * 8 / kThreads, LB = TN * 8 / kThreads;   // 16-byte pieces per thread per stage
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wv >> 1, wn = wv & 1;
+  int tm, tn;
+  tile_of(blockIdx.x, g.tiles_m, g.tiles_n, tm, tn);
+  const int row0 = tm * TM, col0 = tn * TN;
+
+  // this thread's pieces: piece q = tid + 256 u is row q / 8 = tid / 8 + 32 u at 16-byte column
+  // q % 8 = tid % 8, so its LDS offset is a fixed one plus 4 KB per u (the swizzle depends on
+  // the row only through row & 7 = (tid / 8) & 7)
+  const int pr = tid >> 3, pc = tid & 7;
+  const int poff = pr * 128 + ((pc ^ (pr & 7)) << 4);
+  uint32_t aof[LA], bof[LB];   // element offsets of the pieces (rows clamped to the valid ones)
+  piece_offsets_(aof, row0 + pr, g.a_valid, g.lda, 8 * pc, std::make_index_sequence<LA>{});
+  piece_offsets_(bof, col0 + pr, g.b_valid, g.ldb, 8 * pc, std::make_index_sequence<LB>{});
+  u32x4 ra[LA], rb[LB];
+
+  f32x16 acc[RB][CB];
+#pragma unroll
+  for (int i = 0; i < RB; ++i)
+#pragma unroll
+    for (int j = 0; j < CB; ++j) acc[i][j] = f32x16{};
+
+  const int KT = g.K / kBK;
+  gload(ra, g.A, aof, 0);
+  gload(rb, g.B, bof, 0);
+  lstore(smem + poff, ra);
+  lstore(smem + poff + TM * 128, rb);
+  __syncthreads();
+  // fragment rows of this lane: row (lane & 31) of each 32-row block; its 8 K values at 16-byte
+  // piece 2 ks + lane / 32 of the stage row
+  const int fr = lane & 31, fh = lane >> 5;
+  for (int kt = 0; kt < KT; ++kt) {
+    if (kt + 1 < KT) {
+      gload(ra, g.A, aof, (kt + 1) * kBK);
+      gload(rb, g.B, bof, (kt + 1) * kBK);
+    }
+    const uint8_t* As = smem + (kt & 1) * STAGE;
+    const uint8_t* Bs = As + TM * 128;
+#pragma unroll
+    for (int ks = 0; ks < kBK / 16; ++ks) {
+      const int sw = ((2 * ks + fh) ^ (fr & 7)) << 4;
+      u32x4 af[RB], bf[CB];
+#pragma unroll
+      for (int i = 0; i < RB; ++i)
+        af[i] = *reinterpret_cast<const u32x4*>(As + (wm * WM + i * 32 + fr) * 128 + sw);
+#pragma unroll
+      for (int j = 0; j < CB; ++j)
+        bf[j] = *reinterpret_cast<const u32x4*>(Bs + (wn * WN + j * 32 + fr) * 128 + sw);
+#pragma unroll
+      for (int i = 0; i < RB; ++i)
+#pragma unroll
+        for (int j = 0; j < CB; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf(af[i]), as_bf(bf[j]), acc[i][j], 0, 0, 0);
+    }
+    if (kt + 1 < KT) {
+      lstore(smem + ((kt + 1) & 1) * STAGE + poff, ra);
+      lstore(smem + ((kt + 1) & 1) * STAGE + poff + TM * 128, rb);
+    }
+    __syncthreads();
+  }
+
+  // Output element e of acc[i][j] (32 x 32 MFMA layout): row 8 (e / 4) + 4 (lane / 32) + e % 4,
+  // column lane % 32 of the block.
+  auto trow = [&](int i, int e) { return wm * WM + i * 32 + 8 * (e >> 2) + 4 * fh + (e & 3); };
+  auto tcol = [&](int j) { return wn * WN + j * 32 + fr; };
+
+  if constexpr (EPI == kEpiLse) {
+    float* smax = reinterpret_cast<float*>(smem);   // [2][TM]
+    float* ssum = smax + 2 * TM;                     // [2][TM]
+    int* stg = reinterpret_cast<int*>(ssum + 2 * TM);   // [TM]
+    for (int r = tid; r < TM; r += kThreads) stg[r] = g.targets[min(row0 + r, g.m_valid - 1)];
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < RB; ++i) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int r = trow(i, e);
+        const int t = stg[r] - col0;
+        float mx = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < CB; ++j) {
+          const int c = tcol(j);
+          const float v = col0 + c < g.n_valid ? acc[i][j][e] : -INFINITY;
+          mx = fmaxf(mx, v);
+          if (c == t && row0 + r < g.m_valid) g.tgt[row0 + r] = acc[i][j][e];
+        }
+        mx = half_max(mx);
+        float s = 0.f;
+        if (mx != -INFINITY) {
+#pragma unroll
+          for (int j = 0; j < CB; ++j)
+            if (col0 + tcol(j) < g.n_valid) s += exp_neg(acc[i][j][e] - mx);
+        }
+        s = half_sum(s);
+        if (fr == 0) {
+          smax[wn * TM + r] = mx;
+          ssum[wn * TM + r] = s;
+        }
+      }
+    }
+    __syncthreads();
+    for (int r = tid; r < TM; r += kThreads) {
+      const float m0 = smax[r], m1 = smax[TM + r];
+      const float m = fmaxf(m0, m1);
+      float s = 0.f;
+      if (m0 != -INFINITY) s += ssum[r] * exp_neg(m0 - m);
+      if (m1 != -INFINITY) s += ssum[TM + r] * exp_neg(m1 - m);
+      float2* p = reinterpret_cast<float2*>(g.part) + int64_t(tn) * g.ldp + row0 + r;
+      *p = make_float2(m, s);
+    }
+  } else if constexpr (EPI == kEpiProb) {
+    constexpr int PITCH = staging_pitch<TM, TN>(), PITCHT = TM + 8;
+    static_assert(TN * PITCHT <= TM * PITCH || TM == TN, "transposed staging fits");
+    uint16_t* st = reinterpret_cast<uint16_t*>(smem);   // the stage buffers are free now
+    float* slse = reinterpret_cast<float*>(smem + size_t(TM) * PITCH * 2);
+    int* stg = reinterpret_cast<int*>(slse + TM);
+    for (int r = tid; r < TM; r += kThreads) {
+      const int row = min(row0 + r, g.m_valid - 1);
+      slse[r] = g.lse[row];
+      stg[r] = g.targets[row] - g.vcol0;
+    }
+    __syncthreads();
+    const float scale = g.grad[0] * g.inv_n;
+    auto prob = [&](int i, int j, int e) -> uint32_t {
+      const int rt = trow(i, e), ct = tcol(j);
+      float p = 0.f;
+      if (row0 + rt < g.m_valid && col0 + ct < g.n_valid)
+        p = (exp_neg(acc[i][j][e] - slse[rt]) - (col0 + ct == stg[rt] ? 1.f : 0.f)) * scale;
+      return f2bf(p);
+    };
+    // row-major staging, then P rows as 16-byte pieces
+#pragma unroll
+    for (int i = 0; i < RB; ++i)
+#pragma unroll
+      for (int j = 0; j < CB; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) st[trow(i, e) * PITCH + tcol(j)] = uint16_t(prob(i, j, e));
+    __syncthreads();
+    for (int q = tid; q < TM * TN / 8; q += kThreads) {
+      const int r = q / (TN / 8), c8 = q % (TN / 8);
+      *reinterpret_cast<u32x4*>(g.P + int64_t(row0 + r) * g.ldP + col0 + 8 * c8) =
+          *reinterpret_cast<const u32x4*>(st + r * PITCH + 8 * c8);
+    }
+    __syncthreads();
+    // transposed staging (tile column c as a stage row; the 4 consecutive rows e4 of a lane in one
+    // 8-byte write, the values computed again), then PT rows as 16-byte pieces
+#pragma unroll
+    for (int i = 0; i < RB; ++i)
+#pragma unroll
+      for (int j = 0; j < CB; ++j)
+#pragma unroll
+        for (int e4 = 0; e4 < 4; ++e4) {
+          const uint32_t lo = prob(i, j, 4 * e4) | (prob(i, j, 4 * e4 + 1) << 16);
+          const uint32_t hi = prob(i, j, 4 * e4 + 2) | (prob(i, j, 4 * e4 + 3) << 16);
+          *reinterpret_cast<uint2*>(st + tcol(j) * PITCHT + trow(i, 4 * e4)) = make_uint2(lo, hi);
+        }
+    __syncthreads();
+    for (int q = tid; q < TN * TM / 8; q += kThreads) {
+      const int c = q / (TM / 8), r8 = q % (TM / 8);
+      *reinterpret_cast<u32x4*>(g.PT + int64_t(col0 + c) * g.ldPT + row0 + 8 * r8) =
+          *reinterpret_cast<const u32x4*>(st + c * PITCHT + 8 * r8);
+    }
+  } else if constexpr (EPI == kEpiAccF32) {
+#pragma unroll
+    for (int i = 0; i < RB; ++i)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int r = row0 + trow(i, e);
+#pragma unroll
+        for (int j = 0; j < CB; ++j) {
+          const int c = col0 + tcol(j);
+          float* p = g.acc + int64_t(r) * g.ldacc + c;
+          const float v = g.accumulate ? *p + acc[i][j][e] : acc[i][j][e];
+          *p = v;
+          if (g.out && r < g.m_valid && c < g.n_valid) g.out[int64_t(r) * g.ldout + c] = f2bf(v);
+        }
+      }
+  } else {   // kEpiStoreBf16
+#pragma unroll
+    for (int i = 0; i < RB; ++i)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int r = row0 + trow(i, e);
+        if (r >= g.m_valid) continue;
+#pragma unroll
+        for (int j = 0; j < CB; ++j) {
+          const int c = col0 + tcol(j);
+          if (c < g.n_valid) g.out[int64_t(r) * g.ldout + c] = f2bf(acc[i][j][e]);
+        }
+      }
+  }
+}
+
+// dst[c][r] = src[r][c] for r < rows, 0 for rows <= r < rows_pad (c < cols); 64 x 64 tiles.
+__global__ __launch_bounds__(256) void xent_transpose(const uint16_t* src, int rows, int cols, int64_t lds,
+                                                      uint16_t* dst, int rows_pad, int64_t ldd) {
+  __shared__ uint16_t t[64][66];
+  const int c0 = blockIdx.x * 64, r0 = blockIdx.y * 64;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  uint16_t v[16];
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {   // loads first, from clamped indices
+    const int r = r0 + ty + 4 * k, c = c0 + tx;
+    v[k] = src[int64_t(min(r, rows - 1)) * lds + min(c, cols - 1)];
+  }
+#pragma unroll
+  for (int k = 0; k < 16; ++k) t[ty + 4 * k][tx] = r0 + ty + 4 * k < rows ? v[k] : uint16_t(0);
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const int c = c0 + ty + 4 * k, r = r0 + tx;
+    if (c < cols && r < rows_pad) dst[int64_t(c) * ldd + r] = t[tx][ty + 4 * k];
+  }
+}
+
+// targets into [0, V): an id outside is replaced by 0 and reported
+__global__ void xent_targets(const int32_t* targets, int n, int V, int32_t* out, int32_t* status) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  int t = targets[i];
+  if (t < 0 || t >= V) {
+    atomicOr(status, kStatusTarget);
+    t = 0;
+  }
+  out[i] = t;
+}
+
+// lse of each row from its column tiles' (max, sum) in vocabulary order; loss term lse - target
+__global__ void xent_lse(const float2* part, int tiles, int64_t ldp, const float* tgt, int n, float* lse,
+                         float* lrow) {
+  const int r = blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= n) return;
+  float m = -INFINITY, s = 0.f;
+  for (int t = 0; t < tiles; ++t) {
+    const float2 p = part[int64_t(t) * ldp + r];
+    if (p.x == -INFINITY) continue;
+    const float nm = fmaxf(m, p.x);
+    s = s * exp_neg(m - nm) + p.y * exp_neg(p.x - nm);
+    m = nm;
+  }
+  const float l = m + logf(s);
+  lse[r] = l;
+  lrow[r] = l - tgt[r];
+}
+
+// mean of lrow[0..n) in a fixed order: float64 partial sums per thread, then a tree
+__global__ __launch_bounds__(1024) void xent_mean(const float* lrow, int n, float* loss) {
+  __shared__ double s[1024];
+  double a = 0.0;
+  for (int i = threadIdx.x; i < n; i += 1024) a += double(lrow[i]);
+  s[threadIdx.x] = a;
+  __syncthreads();
+  for (int w = 512; w > 0; w >>= 1) {
+    if (int(threadIdx.x) < w) s[threadIdx.x] += s[threadIdx.x + w];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) loss[0] = float(s[0] / double(n));
+}
+
+int64_t al256(int64_t b) { return (b + 255) / 256 * 256; }
+int rup(int x, int m) { return (x + m - 1) / m * m; }
+
+struct Layout {
+  int Np, Vp, C, Cp;
+  int64_t tgt_idx, part, tgt, lrow, wt, ht, P, PT, dh, bytes;
+};
+
+Layout layout(int n, int V, int d, int chunk) {
+  Layout L;
+  L.Np = rup(n, 256);
+  L.Vp = rup(V, 256);
+  L.C = std::min(rup(std::max(chunk, 1), 256), L.Vp);
+  L.Cp = L.C;
+  int64_t o = 0;
+  L.tgt_idx = o; o += al256(int64_t(L.Np) * 4);
+  L.part = o;    o += al256(int64_t(L.Vp / 256) * L.Np * 8);
+  L.tgt = o;     o += al256(int64_t(L.Np) * 4);
+  L.lrow = o;    o += al256(int64_t(L.Np) * 4);
+  L.wt = o;      o += al256(int64_t(d) * L.Vp * 2);
+  L.ht = o;      o += al256(int64_t(d) * L.Np * 2);
+  L.P = o;       o += al256(int64_t(L.Np) * L.Cp * 2);
+  L.PT = o;      o += al256(int64_t(L.Cp) * L.Np * 2);
+  L.dh = o;      o += al256(int64_t(L.Np) * d * 4);
+  L.bytes = o;
+  return L;
+}
+
+// d_model a multiple of 128 (the K step of the logits GEMM, the 128-column tiles of the gradients)
+// and every operand small enough for the GEMM's 32-bit element offsets (rows x row stride < 2^31)
+bool shape_ok(int n, int V, int d) {
+  if (n < 1 || V < 1 || d < 128 || d % 128 || d > 65536) return false;
+  const int64_t Np = rup(n, 256), Vp = rup(V, 256);
+  return Np * d < (int64_t(1) << 31) && Vp * d < (int64_t(1) << 31) && Np * Vp < (int64_t(1) << 31);
+}
+
+template <int TM, int TN, int EPI>
+hipError_t launch_gemm(const GemmArgs& g, hipStream_t s) {
+  const void* fn = reinterpret_cast<const void*>(&xent_gemm<TM, TN, EPI>);
+  const size_t lds = lds_bytes<TM, TN, EPI>();
+  if (hipError_t e = msdc::ensure_dynamic_lds(fn, lds); e != hipSuccess) return e;
+  hipLaunchKernelGGL((xent_gemm<TM, TN, EPI>), dim3(g.tiles_m * g.tiles_n), dim3(kThreads), lds, s, g);
+  return hipGetLastError();
+}
+
+}  // namespace mxe
+
+using namespace mxe;
+
+extern "C" int64_t msd_xent_workspace_bytes(int32_t n_rows, int32_t vocab, int32_t d_model, int32_t chunk) {
+  if (!shape_ok(n_rows, vocab, d_model)) return MSD_E_CONFIG;
+  return layout(n_rows, vocab, d_model, chunk).bytes;
+}
+
+extern "C" int32_t msd_xent_forward(const void* h, const void* weight, const int32_t* targets, int32_t n_rows,
+                                    int32_t vocab, int32_t d_model, void* workspace, float* loss, float* lse,
+                                    int32_t* status, void* stream) {
+  if (!shape_ok(n_rows, vocab, d_model)) return MSD_E_CONFIG;
+  if (!h || !weight || !targets || !workspace || !loss || !lse || !status) return MSD_E_ARG;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const Layout L = layout(n_rows, vocab, d_model, vocab);
+  char* ws = static_cast<char*>(workspace);
+  int32_t* tix = reinterpret_cast<int32_t*>(ws + L.tgt_idx);
+  hipLaunchKernelGGL(xent_targets, dim3((n_rows + 255) / 256), dim3(256), 0, s, targets, n_rows, vocab, tix, status);
+  GemmArgs g{};
+  g.A = static_cast<const uint16_t*>(h);
+  g.lda = d_model;
+  g.a_valid = n_rows;
+  g.B = static_cast<const uint16_t*>(weight);
+  g.ldb = d_model;
+  g.b_valid = vocab;
+  g.K = d_model;
+  g.tiles_m = L.Np / 256;
+  g.tiles_n = L.Vp / 256;
+  g.m_valid = n_rows;
+  g.n_valid = vocab;
+  g.targets = tix;
+  g.part = reinterpret_cast<float*>(ws + L.part);
+  g.ldp = L.Np;
+  g.tgt = reinterpret_cast<float*>(ws + L.tgt);
+  if (launch_gemm<256, 256, kEpiLse>(g, s) != hipSuccess) return MSD_E_HIP;
+  float* lrow = reinterpret_cast<float*>(ws + L.lrow);
+  hipLaunchKernelGGL(xent_lse, dim3((n_rows + 255) / 256), dim3(256), 0, s, reinterpret_cast<const float2*>(g.part),
+                     g.tiles_n, int64_t(L.Np), g.tgt, n_rows, lse, lrow);
+  hipLaunchKernelGGL(xent_mean, dim3(1), dim3(1024), 0, s, lrow, n_rows, loss);
+  return hipGetLastError() == hipSuccess ? MSD_OK : MSD_E_HIP;
+}
+
+extern "C" int32_t msd_xent_backward(const void* h, const void* weight, const int32_t* targets, const float* lse,
+                                     const float* grad_loss, int32_t n_rows, int32_t vocab, int32_t d_model,
+                                     int32_t chunk, void* workspace, void* grad_h, void* grad_weight,
+                                     int32_t* status, void* stream) {
+  if (!shape_ok(n_rows, vocab, d_model)) return MSD_E_CONFIG;
+  if (!h || !weight || !targets || !lse || !grad_loss || !workspace || !grad_h || !grad_weight || !status)
+    return MSD_E_ARG;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const Layout L = layout(n_rows, vocab, d_model, chunk);
+  char* ws = static_cast<char*>(workspace);
+  int32_t* tix = reinterpret_cast<int32_t*>(ws + L.tgt_idx);
+  uint16_t* wt = reinterpret_cast<uint16_t*>(ws + L.wt);
+  uint16_t* ht = reinterpret_cast<uint16_t*>(ws + L.ht);
+  uint16_t* P = reinterpret_cast<uint16_t*>(ws + L.P);
+  uint16_t* PT = reinterpret_cast<uint16_t*>(ws + L.PT);
+  float* dh = reinterpret_cast<float*>(ws + L.dh);
+  const uint16_t* W = static_cast<const uint16_t*>(weight);
+  const uint16_t* H = static_cast<const uint16_t*>(h);
+  hipLaunchKernelGGL(xent_targets, dim3((n_rows + 255) / 256), dim3(256), 0, s, targets, n_rows, vocab, tix, status);
+  // W^T (d x Vp) and h^T (d x Np), zero past V and N
+  hipLaunchKernelGGL(xent_transpose, dim3((d_model + 63) / 64, L.Vp / 64), dim3(256), 0, s, W, vocab, d_model,
+                     int64_t(d_model), wt, L.Vp, int64_t(L.Vp));
+  hipLaunchKernelGGL(xent_transpose, dim3((d_model + 63) / 64, L.Np / 64), dim3(256), 0, s, H, n_rows, d_model,
+                     int64_t(d_model), ht, L.Np, int64_t(L.Np));
+  for (int v0 = 0; v0 < vocab; v0 += L.C) {
+    const int cv = std::min(L.C, vocab - v0);   // valid columns of this chunk
+    const int cp = rup(cv, 256);                // padded
+    GemmArgs p{};
+    p.A = H;
+    p.lda = d_model;
+    p.a_valid = n_rows;
+    p.B = W + int64_t(v0) * d_model;
+    p.ldb = d_model;
+    p.b_valid = cv;
+    p.K = d_model;
+    p.tiles_m = L.Np / 256;
+    p.tiles_n = cp / 256;
+    p.m_valid = n_rows;
+    p.n_valid = cv;
+    p.targets = tix;
+    p.vcol0 = v0;
+    p.lse = lse;
+    p.grad = grad_loss;
+    p.inv_n = 1.0f / float(n_rows);
+    p.P = P;
+    p.ldP = L.Cp;
+    p.PT = PT;
+    p.ldPT = L.Np;
+    if (launch_gemm<256, 256, kEpiProb>(p, s) != hipSuccess) return MSD_E_HIP;
+    // grad_W rows of the chunk = PT (cp x Np) . (h^T)^T  (K = Np)
+    GemmArgs w{};
+    w.A = PT;
+    w.lda = L.Np;
+    w.a_valid = cp;
+    w.B = ht;
+    w.ldb = L.Np;
+    w.b_valid = d_model;
+    w.K = L.Np;
+    w.tiles_m = cp / 128;
+    w.tiles_n = (d_model + 127) / 128;
+    w.m_valid = cv;
+    w.n_valid = d_model;
+    w.out = static_cast<uint16_t*>(grad_weight) + int64_t(v0) * d_model;
+    w.ldout = d_model;
+    if (launch_gemm<128, 128, kEpiStoreBf16>(w, s) != hipSuccess) return MSD_E_HIP;
+    // grad_h (+)= P (Np x cp) . (W^T columns v0..v0+cp)^T  (K = cp)
+    GemmArgs a{};
+    a.A = P;
+    a.lda = L.Cp;
+    a.a_valid = L.Np;
+    a.B = wt + v0;
+    a.ldb = L.Vp;
+    a.b_valid = d_model;
+    a.K = cp;
+    a.tiles_m = L.Np / 128;
+    a.tiles_n = d_model / 128;
+    a.m_valid = n_rows;
+    a.n_valid = d_model;
+    a.acc = dh;
+    a.ldacc = d_model;
+    a.accumulate = v0 > 0;
+    a.out = v0 + L.C >= vocab ? static_cast<uint16_t*>(grad_h) : nullptr;
+    a.ldout = d_model;
+    if (launch_gemm<128, 128, kEpiAccF32>(a, s) != hipSuccess) return MSD_E_HIP;
+  }
+  return hipGetLastError() == hipSuccess ? MSD_OK : MSD_E_HIP;
+}
