@@ -21,6 +21,11 @@ Secondary figures on the same weights (not the headline value):
   sampled_decode  64-token prompt, then 256 tokens with temperature 0.7, top-p 0.95 and
                   repetition penalty 1.2 drawn on the device (decode + sampler chained, tok/s),
                   and the sampler alone per token (us)
+  decode_one_launch, batched_paged_decode
+                  the headline generation in one launch; 8 sequences over a paged cache
+  fused_cross_entropy
+                  the training-side fused output projection + cross-entropy (forward and
+                  backward) on 4096 rows of the 306M output layer, with its matrix-core roofline
 """
 import argparse
 import json
@@ -162,7 +167,40 @@ def secondary(w, cfg, dec, first_token):
     out["batched_paged_decode"] = {"tok_s": round(B * steps / (bms / 1e3), 1), "ms_per_step": round(bms / steps, 4),
                                    "workload": "306M, 8 sequences (prompts U[16,256]) x 128 steps, 16-token "
                                                "pages from a shuffled pool, all 8 stepped per call"}
+    out["fused_cross_entropy"] = cross_entropy_figure(cfg)
     return out
+
+
+PEAK_BF16_TFLOPS = 2500.0
+
+
+def cross_entropy_figure(cfg, n_rows=4096, chunk=4096):
+    """The training-side fused output projection + cross-entropy on the 306M output layer:
+    4096 token rows, the tied 32000 x 1024 embedding, chunk 4096.  Algorithmic work: the forward
+    is one (N x d) . (d x V) product, the backward three (logits again, grad_h, grad_weight)."""
+    import torch
+
+    from transformer_amd.xent import fused_cross_entropy
+    V, d = cfg["vocab_size"], cfg["d_model"]
+    g = torch.Generator().manual_seed(0)
+    h = torch.randn(n_rows, d, generator=g).to(torch.bfloat16).cuda().requires_grad_()
+    wt = (torch.randn(V, d, generator=g) * 0.02).to(torch.bfloat16).cuda().requires_grad_()
+    t = torch.randint(0, V, (n_rows,), generator=g).cuda()
+    loss = fused_cross_entropy(h, wt, t, chunk)          # checks the targets once
+    loss.backward()
+    fwd = lambda: fused_cross_entropy(h, wt, t, chunk, check_targets=False)
+    fms = _events_ms(fwd, 7)
+    saved = fwd()
+    bms = _events_ms(lambda: torch.autograd.grad(saved, (h, wt), retain_graph=True), 7)
+    flop = 2.0 * n_rows * V * d
+    f_tf, b_tf = flop / (fms * 1e9), 3 * flop / (bms * 1e9)
+    return {"forward_ms": round(fms, 4), "backward_ms": round(bms, 4), "forward_tflops": round(f_tf, 1),
+            "backward_tflops": round(b_tf, 1),
+            "roofline": {"bound": "mfma", "achieved": round(4 * flop / ((fms + bms) * 1e9), 1),
+                         "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(4 * flop / ((fms + bms) * 1e9) / PEAK_BF16_TFLOPS, 4)},
+            "workload": f"306M output layer: {n_rows} rows, vocab {V}, d {d}, chunk {chunk}; bf16 operands, "
+                        "f32 accumulation; forward + backward (4 products of 2 N V d flops)"}
 
 
 def main():

@@ -6,17 +6,18 @@
 // parameters to bf16), targets int32 (N).  Every logit is a bf16 x bf16 dot product accumulated
 // in f32 (v_mfma_f32_32x32x16_bf16); softmax statistics are f32.
 //
-// Forward (msd_xent_forward): one GEMM S = h W^T over the whole vocabulary whose epilogue never
-// stores S: each 256 x 256 tile reduces its rows to a partial (max, sum of exp(s - max)) and
-// captures the target logits; xent_lse merges the partials of a row in vocabulary order
-// (lse = max + log sum, the online logsumexp of :293-301), xent_mean takes the mean of
-// lse - target logit in a fixed order (float64 sum).  The logits never exist in memory, as in the
+// Forward (msd_xent_forward): one GEMM S^T = W h^T over the whole vocabulary whose epilogue never
+// stores it: each 256 x 256 tile (256 vocabulary ids x 256 tokens) reduces its token columns to a
+// partial (max, sum of exp(s - max)) and captures the target logits (the transposed product puts
+// one token's 64 values per tile in each lane's registers, so the reduction stays in registers);
+// xent_lse merges a token's partials in a fixed order (lse = max + log sum, the online logsumexp
+// of :293-301), xent_mean takes the mean of lse - target logit in a fixed order (float64 sum).  The logits never exist in memory, as in the
 // reference, whose chunk loop materialises only one (N, chunk) block at a time.
 //
 // Backward (msd_xent_backward), per vocabulary chunk of `chunk` columns (the reference's
 // chunk loop, :344-353; the chunk bounds the probability buffers):
-//   1. xent_gemm<kEpiProb>: S = h W_c^T, then P' = (exp(S - lse) - onehot(target)) * g / N as bf16,
-//      stored as P (N x C) and its transpose PT (C x N) through LDS staging;
+//   1. xent_gemm<kEpiProb>: S^T = W_c h^T, then P' = (exp(S - lse) - onehot(target)) * g / N as
+//      bf16, stored as PT (C x N) and P (N x C) through LDS staging;
 //   2. xent_gemm<kEpiStoreBf16>: grad_W[c] = PT h   (A = PT, B = h^T: the whole reduction over
 //      N rows, so the chunk's rows of grad_W are final);
 //   3. xent_gemm<kEpiAccF32>: grad_h += P W_c   (A = P, B = W^T columns of the chunk), in f32
@@ -52,7 +53,11 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));   // a native vector (HIP's uint4 is a struct)
 
 constexpr int kBK = 64;           // K per LDS stage
-constexpr int kThreads = 256;     // 4 waves, 2 x 2
+// Waves of the 256 x 256 GEMMs (the logits of the forward and the backward's probability block):
+// 4 (2 x 2, 128 x 128 per wave) or 8 (2 x 4, 128 x 64 per wave: two waves per SIMD)
+#ifndef XENT_BIG_WAVES
+#define XENT_BIG_WAVES 8
+#endif
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kStatusTarget = 4;  // a target id outside [0, V) (replaced by 0)
 
@@ -100,17 +105,17 @@ struct GemmArgs {
   int K;               // multiple of kBK
   int tiles_m, tiles_n;
   int m_valid, n_valid;     // output rows / columns that exist (the rest are padding)
-  const int32_t* targets;   // kEpiLse, kEpiProb: sanitized target per row
+  const int32_t* targets;   // kEpiLse, kEpiProb: sanitized target per token (output column)
   int vcol0;                // kEpiProb: vocabulary index of output column 0
-  const float* lse;         // kEpiProb: per row
+  const float* lse;         // kEpiProb: per token
   const float* grad;        // kEpiProb: the loss gradient g (device scalar)
   float inv_n;              // kEpiProb: 1 / N
-  float* part;              // kEpiLse: (max, sum) per (column tile, row): [tiles_n][ldp][2]
+  float* part;              // kEpiLse: (max, sum) per (vocabulary tile, token): [tiles_m][ldp][2]
   int64_t ldp;
-  float* tgt;               // kEpiLse: target logit per row
-  uint16_t* P;              // kEpiProb: rows x ldP
+  float* tgt;               // kEpiLse: target logit per token
+  uint16_t* P;              // kEpiProb: tokens x ldP
   int64_t ldP;
-  uint16_t* PT;             // kEpiProb: columns x ldPT
+  uint16_t* PT;             // kEpiProb: vocabulary ids x ldPT
   int64_t ldPT;
   float* acc;               // kEpiAccF32: f32 rows x ldacc
   int64_t ldacc;
@@ -126,24 +131,28 @@ constexpr int staging_pitch() { return TN + 8; }   // bf16 per row of the epilog
 template <int TM, int TN, int EPI>
 constexpr size_t lds_bytes() {
   // kEpiProb: the bf16 staging tile (over the stage buffers) and the rows' lse and targets after it
-  return EPI == kEpiProb ? std::max<size_t>(2 * stage_bytes<TM, TN>(), size_t(TM) * staging_pitch<TM, TN>() * 2 + TM * 8)
+  return EPI == kEpiProb ? std::max<size_t>(2 * stage_bytes<TM, TN>(), size_t(TM) * staging_pitch<TM, TN>() * 2 + TN * 8)
                          : size_t(2 * stage_bytes<TM, TN>());
 }
 
-// Tile (tm, tn) of workgroup b: XCD x = b % 8 takes tile ids [x * per, (x + 1) * per) in order,
-// ids running down a column of tiles first (the workgroups resident on one XCD share B rows and
-// stream the same A rows).
+// Tile (tm, tn) of workgroup b.  Workgroup b runs on XCD b % 8, which takes the tile ids
+// [x * per, (x + 1) * per) in order; ids then walk blocks of GB column tiles, row tile by row
+// tile, so the 32 workgroups an XCD holds at a time cover 4 row tiles x 8 column tiles and
+// share their operand rows in its L2.
 __device__ __forceinline__ void tile_of(int b, int tiles_m, int tiles_n, int& tm, int& tn) {
   const int total = tiles_m * tiles_n, per = (total + 7) / 8;
   const int x = b & 7, k = b >> 3;
   int t = x * per + k;
   if (t >= total || per * 8 != total) t = b;   // uneven: the plain order
-  tm = t % tiles_m;
-  tn = t / tiles_m;
+  const int GB = tiles_n % 8 == 0 ? 8 : (tiles_n % 4 == 0 ? 4 : 1);
+  const int blk = t / (GB * tiles_m), rem = t % (GB * tiles_m);
+  tm = rem / GB;
+  tn = blk * GB + rem % GB;
 }
 
-// the 16-byte pieces of one stage: global -> registers, registers -> LDS (piece u 4 KB apart);
-// the piece index is a constant of each expansion, so the arrays stay in registers
+// the 16-byte pieces of one stage: global -> registers, registers -> LDS (piece u is R rows
+// after piece u - 1, R = threads / 8); the piece index is a constant of each expansion, so the
+// arrays stay in registers
 template <int N, size_t... U>
 __device__ __forceinline__ void gload_(u32x4 (&r)[N], const uint16_t* base, const uint32_t (&off)[N], int kk,
                                        std::index_sequence<U...>) {
@@ -153,42 +162,65 @@ template <int N>
 __device__ __forceinline__ void gload(u32x4 (&r)[N], const uint16_t* base, const uint32_t (&off)[N], int kk) {
   gload_(r, base, off, kk, std::make_index_sequence<N>{});
 }
-template <int N, size_t... U>
+template <int R, int N, size_t... U>
 __device__ __forceinline__ void lstore_(uint8_t* dst, const u32x4 (&r)[N], std::index_sequence<U...>) {
-  ((*reinterpret_cast<u32x4*>(dst + 4096 * U) = r[U]), ...);
+  ((*reinterpret_cast<u32x4*>(dst + R * 128 * U) = r[U]), ...);
 }
-template <int N>
+template <int R, int N>
 __device__ __forceinline__ void lstore(uint8_t* dst, const u32x4 (&r)[N]) {
-  lstore_(dst, r, std::make_index_sequence<N>{});
+  lstore_<R>(dst, r, std::make_index_sequence<N>{});
 }
-template <int N, size_t... U>
+template <int R, int N, size_t... U>
 __device__ __forceinline__ void piece_offsets_(uint32_t (&off)[N], int row, int valid, int64_t ld, int col,
                                                std::index_sequence<U...>) {
-  ((off[U] = uint32_t(min(row + 32 * int(U), valid - 1)) * uint32_t(ld) + col), ...);
+  ((off[U] = uint32_t(min(row + R * int(U), valid - 1)) * uint32_t(ld) + col), ...);
 }
 
-template <int TM, int TN, int EPI>
-__global__ __launch_bounds__(kThreads) void xent_gemm(GemmArgs g) {
+// The MFMAs of one LDS stage (K = 64): 4 steps of 16, each reading this wave's RB A fragments and
+// CB B fragments (row fr of each 32-row block, 16-byte piece 2 ks + fh of the swizzled row).
+template <int TM, int WM, int WN, int RB, int CB>
+__device__ __forceinline__ void mma_stage(f32x16 (&acc)[RB][CB], const uint8_t* As, int wm, int wn, int fr, int fh) {
+  const uint8_t* Bs = As + TM * 128;
+#pragma unroll
+  for (int ks = 0; ks < kBK / 16; ++ks) {
+    const int sw = ((2 * ks + fh) ^ (fr & 7)) << 4;
+    u32x4 af[RB], bf[CB];
+#pragma unroll
+    for (int i = 0; i < RB; ++i) af[i] = *reinterpret_cast<const u32x4*>(As + (wm * WM + i * 32 + fr) * 128 + sw);
+#pragma unroll
+    for (int j = 0; j < CB; ++j) bf[j] = *reinterpret_cast<const u32x4*>(Bs + (wn * WN + j * 32 + fr) * 128 + sw);
+#pragma unroll
+    for (int i = 0; i < RB; ++i)
+#pragma unroll
+      for (int j = 0; j < CB; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf(af[i]), as_bf(bf[j]), acc[i][j], 0, 0, 0);
+  }
+}
+
+template <int TM, int TN, int GM, int GN, int EPI>
+__global__ __launch_bounds__(64 * GM * GN) void xent_gemm(GemmArgs g) {
   extern __shared__ __align__(16) uint8_t smem[];
-  constexpr int WM = TM / 2, WN = TN / 2;   // wave tile
+  constexpr int kThreads = 64 * GM * GN;    // GM x GN waves
+  constexpr int WM = TM / GM, WN = TN / GN;   // wave tile
   constexpr int RB = WM / 32, CB = WN / 32;
   constexpr int STAGE = stage_bytes<TM, TN>();
   constexpr int LA = TM * 8 / kThreads, LB = TN * 8 / kThreads;   // 16-byte pieces per thread per stage
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wv >> 1, wn = wv & 1;
+  const int wm = wv / GN, wn = wv % GN;
   int tm, tn;
   tile_of(blockIdx.x, g.tiles_m, g.tiles_n, tm, tn);
   const int row0 = tm * TM, col0 = tn * TN;
 
-  // this thread's pieces: piece q = tid + 256 u is row q / 8 = tid / 8 + 32 u at 16-byte column
-  // q % 8 = tid % 8, so its LDS offset is a fixed one plus 4 KB per u (the swizzle depends on
-  // the row only through row & 7 = (tid / 8) & 7)
+  // this thread's pieces: piece q = tid + T u (T threads) is row q / 8 = tid / 8 + (T / 8) u at
+  // 16-byte column q % 8 = tid % 8, so its LDS offset is a fixed one plus (T / 8) rows per u (the
+  // swizzle depends on the row only through row & 7 = (tid / 8) & 7)
   const int pr = tid >> 3, pc = tid & 7;
   const int poff = pr * 128 + ((pc ^ (pr & 7)) << 4);
   uint32_t aof[LA], bof[LB];   // element offsets of the pieces (rows clamped to the valid ones)
-  piece_offsets_(aof, row0 + pr, g.a_valid, g.lda, 8 * pc, std::make_index_sequence<LA>{});
-  piece_offsets_(bof, col0 + pr, g.b_valid, g.ldb, 8 * pc, std::make_index_sequence<LB>{});
+  constexpr int R = kThreads / 8;   // rows between a thread's pieces
+  piece_offsets_<R>(aof, row0 + pr, g.a_valid, g.lda, 8 * pc, std::make_index_sequence<LA>{});
+  piece_offsets_<R>(bof, col0 + pr, g.b_valid, g.ldb, 8 * pc, std::make_index_sequence<LB>{});
   u32x4 ra[LA], rb[LB];
 
   f32x16 acc[RB][CB];
@@ -200,8 +232,8 @@ __global__ __launch_bounds__(kThreads) void xent_gemm(GemmArgs g) {
   const int KT = g.K / kBK;
   gload(ra, g.A, aof, 0);
   gload(rb, g.B, bof, 0);
-  lstore(smem + poff, ra);
-  lstore(smem + poff + TM * 128, rb);
+  lstore<R>(smem + poff, ra);
+  lstore<R>(smem + poff + TM * 128, rb);
   __syncthreads();
   // fragment rows of this lane: row (lane & 31) of each 32-row block; its 8 K values at 16-byte
   // piece 2 ks + lane / 32 of the stage row
@@ -211,27 +243,10 @@ __global__ __launch_bounds__(kThreads) void xent_gemm(GemmArgs g) {
       gload(ra, g.A, aof, (kt + 1) * kBK);
       gload(rb, g.B, bof, (kt + 1) * kBK);
     }
-    const uint8_t* As = smem + (kt & 1) * STAGE;
-    const uint8_t* Bs = As + TM * 128;
-#pragma unroll
-    for (int ks = 0; ks < kBK / 16; ++ks) {
-      const int sw = ((2 * ks + fh) ^ (fr & 7)) << 4;
-      u32x4 af[RB], bf[CB];
-#pragma unroll
-      for (int i = 0; i < RB; ++i)
-        af[i] = *reinterpret_cast<const u32x4*>(As + (wm * WM + i * 32 + fr) * 128 + sw);
-#pragma unroll
-      for (int j = 0; j < CB; ++j)
-        bf[j] = *reinterpret_cast<const u32x4*>(Bs + (wn * WN + j * 32 + fr) * 128 + sw);
-#pragma unroll
-      for (int i = 0; i < RB; ++i)
-#pragma unroll
-        for (int j = 0; j < CB; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf(af[i]), as_bf(bf[j]), acc[i][j], 0, 0, 0);
-    }
+    mma_stage<TM, WM, WN, RB, CB>(acc, smem + (kt & 1) * STAGE, wm, wn, fr, fh);
     if (kt + 1 < KT) {
-      lstore(smem + ((kt + 1) & 1) * STAGE + poff, ra);
-      lstore(smem + ((kt + 1) & 1) * STAGE + poff + TM * 128, rb);
+      lstore<R>(smem + ((kt + 1) & 1) * STAGE + poff, ra);
+      lstore<R>(smem + ((kt + 1) & 1) * STAGE + poff + TM * 128, rb);
     }
     __syncthreads();
   }
@@ -242,59 +257,64 @@ __global__ __launch_bounds__(kThreads) void xent_gemm(GemmArgs g) {
   auto tcol = [&](int j) { return wn * WN + j * 32 + fr; };
 
   if constexpr (EPI == kEpiLse) {
-    float* smax = reinterpret_cast<float*>(smem);   // [2][TM]
-    float* ssum = smax + 2 * TM;                     // [2][TM]
-    int* stg = reinterpret_cast<int*>(ssum + 2 * TM);   // [TM]
-    for (int r = tid; r < TM; r += kThreads) stg[r] = g.targets[min(row0 + r, g.m_valid - 1)];
+    // rows are vocabulary ids, columns tokens: a lane holds one token per 32-column block and 16
+    // vocabulary rows per 32-row block, so a token's (max, sum) is a reduction in registers, one
+    // exchange with the other half-wave and a merge of the GM waves that share the column
+    float* smax = reinterpret_cast<float*>(smem);   // [GM][TN]
+    float* ssum = smax + GM * TN;                    // [GM][TN]
+    int* stg = reinterpret_cast<int*>(ssum + GM * TN);  // [TN] target of each token
+    for (int c = tid; c < TN; c += kThreads) stg[c] = g.targets[min(col0 + c, g.n_valid - 1)];
     __syncthreads();
 #pragma unroll
-    for (int i = 0; i < RB; ++i) {
+    for (int j = 0; j < CB; ++j) {
+      const int ct = tcol(j), t = stg[ct] - row0;
+      float mx = -INFINITY;
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int r = trow(i, e);
-        const int t = stg[r] - col0;
-        float mx = -INFINITY;
+      for (int i = 0; i < RB; ++i)
 #pragma unroll
-        for (int j = 0; j < CB; ++j) {
-          const int c = tcol(j);
-          const float v = col0 + c < g.n_valid ? acc[i][j][e] : -INFINITY;
-          mx = fmaxf(mx, v);
-          if (c == t && row0 + r < g.m_valid) g.tgt[row0 + r] = acc[i][j][e];
+        for (int e = 0; e < 16; ++e) {
+          const int rt = trow(i, e);
+          if (row0 + rt < g.m_valid) mx = fmaxf(mx, acc[i][j][e]);
+          if (rt == t && col0 + ct < g.n_valid) g.tgt[col0 + ct] = acc[i][j][e];
         }
-        mx = half_max(mx);
-        float s = 0.f;
-        if (mx != -INFINITY) {
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      float s = 0.f;
+      if (mx != -INFINITY) {
 #pragma unroll
-          for (int j = 0; j < CB; ++j)
-            if (col0 + tcol(j) < g.n_valid) s += exp_neg(acc[i][j][e] - mx);
-        }
-        s = half_sum(s);
-        if (fr == 0) {
-          smax[wn * TM + r] = mx;
-          ssum[wn * TM + r] = s;
-        }
+        for (int i = 0; i < RB; ++i)
+#pragma unroll
+          for (int e = 0; e < 16; ++e)
+            if (row0 + trow(i, e) < g.m_valid) s += exp_neg(acc[i][j][e] - mx);
+      }
+      s += __shfl_xor(s, 32);
+      if (fh == 0) {
+        smax[wm * TN + ct] = mx;
+        ssum[wm * TN + ct] = s;
       }
     }
     __syncthreads();
-    for (int r = tid; r < TM; r += kThreads) {
-      const float m0 = smax[r], m1 = smax[TM + r];
-      const float m = fmaxf(m0, m1);
+    for (int c = tid; c < TN; c += kThreads) {
+      float m = -INFINITY;
+#pragma unroll
+      for (int w = 0; w < GM; ++w) m = fmaxf(m, smax[w * TN + c]);
       float s = 0.f;
-      if (m0 != -INFINITY) s += ssum[r] * exp_neg(m0 - m);
-      if (m1 != -INFINITY) s += ssum[TM + r] * exp_neg(m1 - m);
-      float2* p = reinterpret_cast<float2*>(g.part) + int64_t(tn) * g.ldp + row0 + r;
+#pragma unroll
+      for (int w = 0; w < GM; ++w)
+        if (smax[w * TN + c] != -INFINITY) s += ssum[w * TN + c] * exp_neg(smax[w * TN + c] - m);
+      float2* p = reinterpret_cast<float2*>(g.part) + int64_t(tm) * g.ldp + col0 + c;
       *p = make_float2(m, s);
     }
   } else if constexpr (EPI == kEpiProb) {
+    // rows are the chunk's vocabulary ids, columns tokens
     constexpr int PITCH = staging_pitch<TM, TN>(), PITCHT = TM + 8;
     static_assert(TN * PITCHT <= TM * PITCH || TM == TN, "transposed staging fits");
     uint16_t* st = reinterpret_cast<uint16_t*>(smem);   // the stage buffers are free now
     float* slse = reinterpret_cast<float*>(smem + size_t(TM) * PITCH * 2);
-    int* stg = reinterpret_cast<int*>(slse + TM);
-    for (int r = tid; r < TM; r += kThreads) {
-      const int row = min(row0 + r, g.m_valid - 1);
-      slse[r] = g.lse[row];
-      stg[r] = g.targets[row] - g.vcol0;
+    int* stg = reinterpret_cast<int*>(slse + TN);
+    for (int c = tid; c < TN; c += kThreads) {
+      const int tok = min(col0 + c, g.n_valid - 1);
+      slse[c] = g.lse[tok];
+      stg[c] = g.targets[tok] - g.vcol0;
     }
     __syncthreads();
     const float scale = g.grad[0] * g.inv_n;
@@ -302,10 +322,10 @@ __global__ __launch_bounds__(kThreads) void xent_gemm(GemmArgs g) {
       const int rt = trow(i, e), ct = tcol(j);
       float p = 0.f;
       if (row0 + rt < g.m_valid && col0 + ct < g.n_valid)
-        p = (exp_neg(acc[i][j][e] - slse[rt]) - (col0 + ct == stg[rt] ? 1.f : 0.f)) * scale;
+        p = (exp_neg(acc[i][j][e] - slse[ct]) - (row0 + rt == stg[ct] ? 1.f : 0.f)) * scale;
       return f2bf(p);
     };
-    // row-major staging, then P rows as 16-byte pieces
+    // row-major staging (vocabulary rows), then PT rows as 16-byte pieces
 #pragma unroll
     for (int i = 0; i < RB; ++i)
 #pragma unroll
@@ -315,12 +335,12 @@ __global__ __launch_bounds__(kThreads) void xent_gemm(GemmArgs g) {
     __syncthreads();
     for (int q = tid; q < TM * TN / 8; q += kThreads) {
       const int r = q / (TN / 8), c8 = q % (TN / 8);
-      *reinterpret_cast<u32x4*>(g.P + int64_t(row0 + r) * g.ldP + col0 + 8 * c8) =
+      *reinterpret_cast<u32x4*>(g.PT + int64_t(row0 + r) * g.ldPT + col0 + 8 * c8) =
           *reinterpret_cast<const u32x4*>(st + r * PITCH + 8 * c8);
     }
     __syncthreads();
-    // transposed staging (tile column c as a stage row; the 4 consecutive rows e4 of a lane in one
-    // 8-byte write, the values computed again), then PT rows as 16-byte pieces
+    // transposed staging (token c as a stage row; the 4 consecutive vocabulary rows e4 of a lane
+    // in one 8-byte write, the values computed again), then P rows as 16-byte pieces
 #pragma unroll
     for (int i = 0; i < RB; ++i)
 #pragma unroll
@@ -334,7 +354,7 @@ __global__ __launch_bounds__(kThreads) void xent_gemm(GemmArgs g) {
     __syncthreads();
     for (int q = tid; q < TN * TM / 8; q += kThreads) {
       const int c = q / (TM / 8), r8 = q % (TM / 8);
-      *reinterpret_cast<u32x4*>(g.PT + int64_t(col0 + c) * g.ldPT + row0 + 8 * r8) =
+      *reinterpret_cast<u32x4*>(g.P + int64_t(col0 + c) * g.ldP + row0 + 8 * r8) =
           *reinterpret_cast<const u32x4*>(st + c * PITCHT + 8 * r8);
     }
   } else if constexpr (EPI == kEpiAccF32) {
@@ -402,22 +422,48 @@ __global__ void xent_targets(const int32_t* targets, int n, int V, int32_t* out,
   out[i] = t;
 }
 
-// lse of each row from its column tiles' (max, sum) in vocabulary order; loss term lse - target
-__global__ void xent_lse(const float2* part, int tiles, int64_t ldp, const float* tgt, int n, float* lse,
-                         float* lrow) {
-  const int r = blockIdx.x * blockDim.x + threadIdx.x;
-  if (r >= n) return;
-  float m = -INFINITY, s = 0.f;
-  for (int t = 0; t < tiles; ++t) {
-    const float2 p = part[int64_t(t) * ldp + r];
-    if (p.x == -INFINITY) continue;
-    const float nm = fmaxf(m, p.x);
-    s = s * exp_neg(m - nm) + p.y * exp_neg(p.x - nm);
-    m = nm;
+// lse of each token from its vocabulary tiles' (max, sum); loss term lse - target logit.  16 lanes
+// per token (a block of 256 threads takes 16 tokens): lane u merges tiles u, u + 16, ... in order,
+// then the 16 partials are merged pairwise in a fixed tree (lanes u, u ^ 1, u ^ 2, u ^ 4, u ^ 8)
+__device__ __forceinline__ void merge_ms(float& m, float& s, float m2, float s2) {
+  if (m2 == -INFINITY) return;
+  if (m == -INFINITY) {
+    m = m2;
+    s = s2;
+    return;
   }
-  const float l = m + logf(s);
-  lse[r] = l;
-  lrow[r] = l - tgt[r];
+  const float nm = fmaxf(m, m2);
+  s = s * exp_neg(m - nm) + s2 * exp_neg(m2 - nm);
+  m = nm;
+}
+__global__ __launch_bounds__(256) void xent_lse(const float2* part, int tiles, int64_t ldp, const float* tgt, int n,
+                                                float* lse, float* lrow) {
+  const int u = threadIdx.x & 15;
+  const int r = blockIdx.x * 16 + (threadIdx.x >> 4);
+  const int rr = min(r, n - 1);
+  float m = -INFINITY, s = 0.f;
+  for (int t = u; t < tiles; t += 16) {
+    const float2 p = part[int64_t(t) * ldp + rr];
+    merge_ms(m, s, p.x, p.y);
+  }
+#pragma unroll
+  for (int x = 1; x < 16; x <<= 1) {
+    const float m2 = __shfl_xor(m, x, 16), s2 = __shfl_xor(s, x, 16);
+    // both lanes of a pair merge in the same order (lower lane's partial first)
+    if (u & x) {
+      float mm = m2, ss = s2;
+      merge_ms(mm, ss, m, s);
+      m = mm;
+      s = ss;
+    } else {
+      merge_ms(m, s, m2, s2);
+    }
+  }
+  if (u == 0 && r < n) {
+    const float l = m + logf(s);
+    lse[r] = l;
+    lrow[r] = l - tgt[r];
+  }
 }
 
 // mean of lrow[0..n) in a fixed order: float64 partial sums per thread, then a tree
@@ -470,14 +516,15 @@ bool shape_ok(int n, int V, int d) {
   return Np * d < (int64_t(1) << 31) && Vp * d < (int64_t(1) << 31) && Np * Vp < (int64_t(1) << 31);
 }
 
-template <int TM, int TN, int EPI>
+template <int TM, int TN, int GM, int GN, int EPI>
 hipError_t launch_gemm(const GemmArgs& g, hipStream_t s) {
-  const void* fn = reinterpret_cast<const void*>(&xent_gemm<TM, TN, EPI>);
+  const void* fn = reinterpret_cast<const void*>(&xent_gemm<TM, TN, GM, GN, EPI>);
   const size_t lds = lds_bytes<TM, TN, EPI>();
   if (hipError_t e = msdc::ensure_dynamic_lds(fn, lds); e != hipSuccess) return e;
-  hipLaunchKernelGGL((xent_gemm<TM, TN, EPI>), dim3(g.tiles_m * g.tiles_n), dim3(kThreads), lds, s, g);
+  hipLaunchKernelGGL((xent_gemm<TM, TN, GM, GN, EPI>), dim3(g.tiles_m * g.tiles_n), dim3(64 * GM * GN), lds, s, g);
   return hipGetLastError();
 }
+constexpr int kBigGM = 2, kBigGN = XENT_BIG_WAVES / 2;
 
 }  // namespace mxe
 
@@ -499,25 +546,26 @@ extern "C" int32_t msd_xent_forward(const void* h, const void* weight, const int
   int32_t* tix = reinterpret_cast<int32_t*>(ws + L.tgt_idx);
   hipLaunchKernelGGL(xent_targets, dim3((n_rows + 255) / 256), dim3(256), 0, s, targets, n_rows, vocab, tix, status);
   GemmArgs g{};
-  g.A = static_cast<const uint16_t*>(h);
+  // S^T = W h^T: tile rows are vocabulary ids, columns tokens
+  g.A = static_cast<const uint16_t*>(weight);
   g.lda = d_model;
-  g.a_valid = n_rows;
-  g.B = static_cast<const uint16_t*>(weight);
+  g.a_valid = vocab;
+  g.B = static_cast<const uint16_t*>(h);
   g.ldb = d_model;
-  g.b_valid = vocab;
+  g.b_valid = n_rows;
   g.K = d_model;
-  g.tiles_m = L.Np / 256;
-  g.tiles_n = L.Vp / 256;
-  g.m_valid = n_rows;
-  g.n_valid = vocab;
+  g.tiles_m = L.Vp / 256;
+  g.tiles_n = L.Np / 256;
+  g.m_valid = vocab;
+  g.n_valid = n_rows;
   g.targets = tix;
   g.part = reinterpret_cast<float*>(ws + L.part);
   g.ldp = L.Np;
   g.tgt = reinterpret_cast<float*>(ws + L.tgt);
-  if (launch_gemm<256, 256, kEpiLse>(g, s) != hipSuccess) return MSD_E_HIP;
+  if (launch_gemm<256, 256, kBigGM, kBigGN, kEpiLse>(g, s) != hipSuccess) return MSD_E_HIP;
   float* lrow = reinterpret_cast<float*>(ws + L.lrow);
-  hipLaunchKernelGGL(xent_lse, dim3((n_rows + 255) / 256), dim3(256), 0, s, reinterpret_cast<const float2*>(g.part),
-                     g.tiles_n, int64_t(L.Np), g.tgt, n_rows, lse, lrow);
+  hipLaunchKernelGGL(xent_lse, dim3((n_rows + 15) / 16), dim3(256), 0, s, reinterpret_cast<const float2*>(g.part),
+                     g.tiles_m, int64_t(L.Np), g.tgt, n_rows, lse, lrow);
   hipLaunchKernelGGL(xent_mean, dim3(1), dim3(1024), 0, s, lrow, n_rows, loss);
   return hipGetLastError() == hipSuccess ? MSD_OK : MSD_E_HIP;
 }
@@ -550,17 +598,17 @@ extern "C" int32_t msd_xent_backward(const void* h, const void* weight, const in
     const int cv = std::min(L.C, vocab - v0);   // valid columns of this chunk
     const int cp = rup(cv, 256);                // padded
     GemmArgs p{};
-    p.A = H;
+    p.A = W + int64_t(v0) * d_model;   // S^T of the chunk: rows vocabulary ids, columns tokens
     p.lda = d_model;
-    p.a_valid = n_rows;
-    p.B = W + int64_t(v0) * d_model;
+    p.a_valid = cv;
+    p.B = H;
     p.ldb = d_model;
-    p.b_valid = cv;
+    p.b_valid = n_rows;
     p.K = d_model;
-    p.tiles_m = L.Np / 256;
-    p.tiles_n = cp / 256;
-    p.m_valid = n_rows;
-    p.n_valid = cv;
+    p.tiles_m = cp / 256;
+    p.tiles_n = L.Np / 256;
+    p.m_valid = cv;
+    p.n_valid = n_rows;
     p.targets = tix;
     p.vcol0 = v0;
     p.lse = lse;
@@ -570,7 +618,7 @@ extern "C" int32_t msd_xent_backward(const void* h, const void* weight, const in
     p.ldP = L.Cp;
     p.PT = PT;
     p.ldPT = L.Np;
-    if (launch_gemm<256, 256, kEpiProb>(p, s) != hipSuccess) return MSD_E_HIP;
+    if (launch_gemm<256, 256, kBigGM, kBigGN, kEpiProb>(p, s) != hipSuccess) return MSD_E_HIP;
     // grad_W rows of the chunk = PT (cp x Np) . (h^T)^T  (K = Np)
     GemmArgs w{};
     w.A = PT;
@@ -586,7 +634,7 @@ extern "C" int32_t msd_xent_backward(const void* h, const void* weight, const in
     w.n_valid = d_model;
     w.out = static_cast<uint16_t*>(grad_weight) + int64_t(v0) * d_model;
     w.ldout = d_model;
-    if (launch_gemm<128, 128, kEpiStoreBf16>(w, s) != hipSuccess) return MSD_E_HIP;
+    if (launch_gemm<128, 128, 2, 2, kEpiStoreBf16>(w, s) != hipSuccess) return MSD_E_HIP;
     // grad_h (+)= P (Np x cp) . (W^T columns v0..v0+cp)^T  (K = cp)
     GemmArgs a{};
     a.A = P;
@@ -605,7 +653,7 @@ extern "C" int32_t msd_xent_backward(const void* h, const void* weight, const in
     a.accumulate = v0 > 0;
     a.out = v0 + L.C >= vocab ? static_cast<uint16_t*>(grad_h) : nullptr;
     a.ldout = d_model;
-    if (launch_gemm<128, 128, kEpiAccF32>(a, s) != hipSuccess) return MSD_E_HIP;
+    if (launch_gemm<128, 128, 2, 2, kEpiAccF32>(a, s) != hipSuccess) return MSD_E_HIP;
   }
   return hipGetLastError() == hipSuccess ? MSD_OK : MSD_E_HIP;
 }
