@@ -124,12 +124,21 @@ struct GemmArgs {
   int64_t ldout;
 };
 
+// 1: operand tiles reach LDS by direct DMA (global_load_lds); 0: staged through registers
+#ifndef XENT_DMA
+#define XENT_DMA 1
+#endif
+
 template <int TM, int TN>
 constexpr int stage_bytes() { return (TM + TN) * kBK * 2; }
 template <int TM, int TN>
 constexpr int staging_pitch() { return TN + 8; }   // bf16 per row of the epilogue's LDS tile
 template <int TM, int TN, int EPI>
 constexpr size_t lds_bytes() {
+#if XENT_DMA
+  constexpr size_t ring = size_t(4) * (TM + TN) * 64;
+  return EPI == kEpiProb ? std::max<size_t>(ring, size_t(TM) * staging_pitch<TM, TN>() * 2 + TN * 8) : ring;
+#endif
   // kEpiProb: the bf16 staging tile (over the stage buffers) and the rows' lse and targets after it
   return EPI == kEpiProb ? std::max<size_t>(2 * stage_bytes<TM, TN>(), size_t(TM) * staging_pitch<TM, TN>() * 2 + TN * 8)
                          : size_t(2 * stage_bytes<TM, TN>());
@@ -176,6 +185,129 @@ __device__ __forceinline__ void piece_offsets_(uint32_t (&off)[N], int row, int 
   ((off[U] = uint32_t(min(row + R * int(U), valid - 1)) * uint32_t(ld) + col), ...);
 }
 
+// ---- direct-to-LDS pipeline (XENT_DMA): K advances 32 at a time through a ring of 4 LDS stages,
+// three in flight.  Each lane's global_load_lds writes 16 bytes at (stage base + 1 KB per
+// instruction + 16 lane); a stage row is 64 bytes (4 pieces of 8 K values) and holds piece c at
+// position c ^ ((row >> 1) & 3), so the 8 rows one read phase touches cover all 32 banks.  The
+// fragment reads are inline assembly with explicit waits: the compiler would otherwise wait for
+// every outstanding DMA (vmcnt(0)) before each LDS read, and __syncthreads' fence would too, so
+// the stage barrier is a bare s_barrier after this wave's own DMAs of the stage have landed.
+constexpr int kKD = 32;   // K per DMA stage
+constexpr int kStages = 4;
+typedef __attribute__((address_space(3))) uint8_t lds_u8;
+__device__ __forceinline__ uint32_t lds_addr(const void* p) { return uint32_t(reinterpret_cast<uintptr_t>((const lds_u8*)p)); }
+// (the host pass instantiates these templates along with the kernels but never emits them, and
+// an x86 compile rejects the vector-register constraints and the LDS builtin, so their bodies
+// are in the device pass only)
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+#if defined(__HIP_DEVICE_COMPILE__)
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+#endif
+}
+// The fragment reads of one DMA stage and the wait for them, as one assembly block: fa[ks][i] is
+// the A fragment of K step ks for row block i at a_ks + 2048 i (32 rows of 64 bytes apart), fb
+// likewise from b_ks.  The outputs exist only once the block has waited, so the compiler cannot
+// place a use (or a copy) of a fragment before its read has landed.
+__device__ __forceinline__ void stage_reads(u32x4 (&fa)[2][4], u32x4 (&fb)[2][2], uint32_t a0, uint32_t a1,
+                                            uint32_t b0, uint32_t b1) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  asm volatile(
+      "ds_read_b128 %0, %12 offset:0\n"
+      "ds_read_b128 %1, %12 offset:2048\n"
+      "ds_read_b128 %2, %12 offset:4096\n"
+      "ds_read_b128 %3, %12 offset:6144\n"
+      "ds_read_b128 %4, %14 offset:0\n"
+      "ds_read_b128 %5, %14 offset:2048\n"
+      "ds_read_b128 %6, %13 offset:0\n"
+      "ds_read_b128 %7, %13 offset:2048\n"
+      "ds_read_b128 %8, %13 offset:4096\n"
+      "ds_read_b128 %9, %13 offset:6144\n"
+      "ds_read_b128 %10, %15 offset:0\n"
+      "ds_read_b128 %11, %15 offset:2048\n"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(fa[0][0]), "=&v"(fa[0][1]), "=&v"(fa[0][2]), "=&v"(fa[0][3]), "=&v"(fb[0][0]), "=&v"(fb[0][1]),
+        "=&v"(fa[1][0]), "=&v"(fa[1][1]), "=&v"(fa[1][2]), "=&v"(fa[1][3]), "=&v"(fb[1][0]), "=&v"(fb[1][1])
+      : "v"(a0), "v"(a1), "v"(b0), "v"(b1));
+#endif
+}
+__device__ __forceinline__ void stage_reads(u32x4 (&fa)[2][2], u32x4 (&fb)[2][2], uint32_t a0, uint32_t a1,
+                                            uint32_t b0, uint32_t b1) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  asm volatile(
+      "ds_read_b128 %0, %8 offset:0\n"
+      "ds_read_b128 %1, %8 offset:2048\n"
+      "ds_read_b128 %2, %10 offset:0\n"
+      "ds_read_b128 %3, %10 offset:2048\n"
+      "ds_read_b128 %4, %9 offset:0\n"
+      "ds_read_b128 %5, %9 offset:2048\n"
+      "ds_read_b128 %6, %11 offset:0\n"
+      "ds_read_b128 %7, %11 offset:2048\n"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(fa[0][0]), "=&v"(fa[0][1]), "=&v"(fb[0][0]), "=&v"(fb[0][1]), "=&v"(fa[1][0]), "=&v"(fa[1][1]),
+        "=&v"(fb[1][0]), "=&v"(fb[1][1])
+      : "v"(a0), "v"(a1), "v"(b0), "v"(b1));
+#endif
+}
+__device__ __forceinline__ void stage_reads(u32x4 (&fa)[2][4], u32x4 (&fb)[2][4], uint32_t a0, uint32_t a1,
+                                            uint32_t b0, uint32_t b1) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  asm volatile(
+      "ds_read_b128 %0, %16 offset:0\n"
+      "ds_read_b128 %1, %16 offset:2048\n"
+      "ds_read_b128 %2, %16 offset:4096\n"
+      "ds_read_b128 %3, %16 offset:6144\n"
+      "ds_read_b128 %4, %18 offset:0\n"
+      "ds_read_b128 %5, %18 offset:2048\n"
+      "ds_read_b128 %6, %18 offset:4096\n"
+      "ds_read_b128 %7, %18 offset:6144\n"
+      "ds_read_b128 %8, %17 offset:0\n"
+      "ds_read_b128 %9, %17 offset:2048\n"
+      "ds_read_b128 %10, %17 offset:4096\n"
+      "ds_read_b128 %11, %17 offset:6144\n"
+      "ds_read_b128 %12, %19 offset:0\n"
+      "ds_read_b128 %13, %19 offset:2048\n"
+      "ds_read_b128 %14, %19 offset:4096\n"
+      "ds_read_b128 %15, %19 offset:6144\n"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(fa[0][0]), "=&v"(fa[0][1]), "=&v"(fa[0][2]), "=&v"(fa[0][3]), "=&v"(fb[0][0]), "=&v"(fb[0][1]),
+        "=&v"(fb[0][2]), "=&v"(fb[0][3]), "=&v"(fa[1][0]), "=&v"(fa[1][1]), "=&v"(fa[1][2]), "=&v"(fa[1][3]),
+        "=&v"(fb[1][0]), "=&v"(fb[1][1]), "=&v"(fb[1][2]), "=&v"(fb[1][3])
+      : "v"(a0), "v"(a1), "v"(b0), "v"(b1));
+#endif
+}
+template <int RB, int CB>
+__device__ __forceinline__ void stage_reads(u32x4 (&)[2][RB], u32x4 (&)[2][CB], uint32_t, uint32_t, uint32_t,
+                                            uint32_t) {
+  static_assert(RB < 0, "no fragment-read block for this wave tile");
+}
+// The NIW DMAs of one stage for this wave: instruction u fills the 1 KB at st + 1024 (wv + NW u)
+// from A (u < UA) or B, at K offset kt * kKD past this lane's element offset doff[u].
+template <int NIW, int UA, int NW>
+__device__ __forceinline__ void dma_stage(const uint16_t* A, const uint16_t* B, const uint32_t (&doff)[NIW], int kt,
+                                          uint8_t* st, int wv) {
+#if defined(__HIP_DEVICE_COMPILE__)
+#pragma unroll
+  for (int u = 0; u < NIW; ++u)
+    __builtin_amdgcn_global_load_lds((u < UA ? A : B) + doff[u] + kt * kKD,
+                                     (__attribute__((address_space(3))) void*)(st + 1024 * (wv + NW * u)), 16, 0, 0);
+#endif
+}
+// The MFMAs of one DMA stage (K = 32): both K steps' fragments read, then the RB x CB x 2 MFMAs.
+template <int TM, int RB, int CB>
+__device__ __forceinline__ void mma_stage_dma(f32x16 (&acc)[RB][CB], uint32_t a0, uint32_t a1, uint32_t b0,
+                                              uint32_t b1) {
+  u32x4 fa[2][RB], fb[2][CB];
+  stage_reads(fa, fb, a0, a1, b0, b1);
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+    for (int i = 0; i < RB; ++i)
+#pragma unroll
+      for (int j = 0; j < CB; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf(fa[ks][i]), as_bf(fb[ks][j]), acc[i][j], 0, 0, 0);
+}
+
 // The MFMAs of one LDS stage (K = 64): 4 steps of 16, each reading this wave's RB A fragments and
 // CB B fragments (row fr of each 32-row block, 16-byte piece 2 ks + fh of the swizzled row).
 template <int TM, int WM, int WN, int RB, int CB>
@@ -212,6 +344,48 @@ __global__ __launch_bounds__(64 * GM * GN) void xent_gemm(GemmArgs g) {
   tile_of(blockIdx.x, g.tiles_m, g.tiles_n, tm, tn);
   const int row0 = tm * TM, col0 = tn * TN;
 
+  f32x16 acc[RB][CB];
+#pragma unroll
+  for (int i = 0; i < RB; ++i)
+#pragma unroll
+    for (int j = 0; j < CB; ++j) acc[i][j] = f32x16{};
+  const int fr = lane & 31, fh = lane >> 5;
+#if XENT_DMA
+  {
+    constexpr int NW = GM * GN, SD = (TM + TN) * 64, NI = (TM + TN) / 16, NIW = NI / NW, UA = TM / (16 * NW);
+    static_assert(NI % NW == 0 && TM % (16 * NW) == 0, "whole DMA instructions per wave, A before B");
+    static_assert(kStages * SD <= 160 * 1024, "LDS ring");
+    // instruction u of this wave covers stage rows 16 (wv + NW u) .. + 16: A rows for u < UA, then
+    // B rows; this lane's row of it and the K piece it loads into position lane % 4
+    uint32_t doff[NIW];
+#pragma unroll
+    for (int u = 0; u < NIW; ++u) {
+      const int r = 16 * (wv + NW * u) + (lane >> 2) - (u < UA ? 0 : TM);
+      const int piece = (lane & 3) ^ ((r >> 1) & 3);
+      doff[u] = u < UA ? uint32_t(min(row0 + r, g.a_valid - 1)) * uint32_t(g.lda) + 8 * piece
+                       : uint32_t(min(col0 + r, g.b_valid - 1)) * uint32_t(g.ldb) + 8 * piece;
+    }
+    const int KT = g.K / kKD;
+    for (int s = 0; s < 3 && s < KT; ++s) dma_stage<NIW, UA, NW>(g.A, g.B, doff, s, smem + s * SD, wv);
+    // this lane's fragment rows and swizzled pieces (the swizzle depends only on fr)
+    const uint32_t base = lds_addr(smem);
+    const uint32_t sw0 = ((0 + fh) ^ ((fr >> 1) & 3)) << 4, sw1 = ((2 + fh) ^ ((fr >> 1) & 3)) << 4;
+    const uint32_t ar = (wm * WM + fr) * 64, br = TM * 64 + (wn * WN + fr) * 64;
+    for (int kt = 0; kt < KT; ++kt) {
+      if (kt + 2 < KT)
+        wait_vm<2 * NIW>();
+      else if (kt + 1 < KT)
+        wait_vm<NIW>();
+      else
+        wait_vm<0>();
+      __builtin_amdgcn_s_barrier();   // every wave's part of stage kt landed; stage kt - 1 read by all
+      if (kt + 3 < KT) dma_stage<NIW, UA, NW>(g.A, g.B, doff, kt + 3, smem + ((kt + 3) & (kStages - 1)) * SD, wv);
+      const uint32_t sb = base + (kt & (kStages - 1)) * SD;
+      mma_stage_dma<TM, RB, CB>(acc, sb + ar + sw0, sb + ar + sw1, sb + br + sw0, sb + br + sw1);
+    }
+    __builtin_amdgcn_s_barrier();   // the epilogue reuses the ring
+  }
+#else
   // this thread's pieces: piece q = tid + T u (T threads) is row q / 8 = tid / 8 + (T / 8) u at
   // 16-byte column q % 8 = tid % 8, so its LDS offset is a fixed one plus (T / 8) rows per u (the
   // swizzle depends on the row only through row & 7 = (tid / 8) & 7)
@@ -223,12 +397,6 @@ __global__ __launch_bounds__(64 * GM * GN) void xent_gemm(GemmArgs g) {
   piece_offsets_<R>(bof, col0 + pr, g.b_valid, g.ldb, 8 * pc, std::make_index_sequence<LB>{});
   u32x4 ra[LA], rb[LB];
 
-  f32x16 acc[RB][CB];
-#pragma unroll
-  for (int i = 0; i < RB; ++i)
-#pragma unroll
-    for (int j = 0; j < CB; ++j) acc[i][j] = f32x16{};
-
   const int KT = g.K / kBK;
   gload(ra, g.A, aof, 0);
   gload(rb, g.B, bof, 0);
@@ -237,7 +405,6 @@ __global__ __launch_bounds__(64 * GM * GN) void xent_gemm(GemmArgs g) {
   __syncthreads();
   // fragment rows of this lane: row (lane & 31) of each 32-row block; its 8 K values at 16-byte
   // piece 2 ks + lane / 32 of the stage row
-  const int fr = lane & 31, fh = lane >> 5;
   for (int kt = 0; kt < KT; ++kt) {
     if (kt + 1 < KT) {
       gload(ra, g.A, aof, (kt + 1) * kBK);
@@ -250,6 +417,8 @@ __global__ __launch_bounds__(64 * GM * GN) void xent_gemm(GemmArgs g) {
     }
     __syncthreads();
   }
+
+#endif
 
   // Output element e of acc[i][j] (32 x 32 MFMA layout): row 8 (e / 4) + 4 (lane / 32) + e % 4,
   // column lane % 32 of the block.
@@ -318,20 +487,33 @@ __global__ __launch_bounds__(64 * GM * GN) void xent_gemm(GemmArgs g) {
     }
     __syncthreads();
     const float scale = g.grad[0] * g.inv_n;
-    auto prob = [&](int i, int j, int e) -> uint32_t {
-      const int rt = trow(i, e), ct = tcol(j);
-      float p = 0.f;
-      if (row0 + rt < g.m_valid && col0 + ct < g.n_valid)
-        p = (exp_neg(acc[i][j][e] - slse[ct]) - (row0 + rt == stg[ct] ? 1.f : 0.f)) * scale;
-      return f2bf(p);
-    };
+    // every value once, as bf16 pairs of consecutive rows (elements 2 m, 2 m + 1 of a block)
+    uint32_t pk[RB][CB][8];
+#pragma unroll
+    for (int i = 0; i < RB; ++i)
+#pragma unroll
+      for (int j = 0; j < CB; ++j)
+#pragma unroll
+        for (int m = 0; m < 8; ++m) {
+          uint32_t h2[2];
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            const int e = 2 * m + u, rt = trow(i, e), ct = tcol(j);
+            float p = 0.f;
+            if (row0 + rt < g.m_valid && col0 + ct < g.n_valid)
+              p = (exp_neg(acc[i][j][e] - slse[ct]) - (row0 + rt == stg[ct] ? 1.f : 0.f)) * scale;
+            h2[u] = f2bf(p);
+          }
+          pk[i][j][m] = h2[0] | (h2[1] << 16);
+        }
     // row-major staging (vocabulary rows), then PT rows as 16-byte pieces
 #pragma unroll
     for (int i = 0; i < RB; ++i)
 #pragma unroll
       for (int j = 0; j < CB; ++j)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) st[trow(i, e) * PITCH + tcol(j)] = uint16_t(prob(i, j, e));
+        for (int e = 0; e < 16; ++e)
+          st[trow(i, e) * PITCH + tcol(j)] = uint16_t(pk[i][j][e >> 1] >> (16 * (e & 1)));
     __syncthreads();
     for (int q = tid; q < TM * TN / 8; q += kThreads) {
       const int r = q / (TN / 8), c8 = q % (TN / 8);
@@ -340,17 +522,15 @@ __global__ __launch_bounds__(64 * GM * GN) void xent_gemm(GemmArgs g) {
     }
     __syncthreads();
     // transposed staging (token c as a stage row; the 4 consecutive vocabulary rows e4 of a lane
-    // in one 8-byte write, the values computed again), then P rows as 16-byte pieces
+    // in one 8-byte write), then P rows as 16-byte pieces
 #pragma unroll
     for (int i = 0; i < RB; ++i)
 #pragma unroll
       for (int j = 0; j < CB; ++j)
 #pragma unroll
-        for (int e4 = 0; e4 < 4; ++e4) {
-          const uint32_t lo = prob(i, j, 4 * e4) | (prob(i, j, 4 * e4 + 1) << 16);
-          const uint32_t hi = prob(i, j, 4 * e4 + 2) | (prob(i, j, 4 * e4 + 3) << 16);
-          *reinterpret_cast<uint2*>(st + tcol(j) * PITCHT + trow(i, 4 * e4)) = make_uint2(lo, hi);
-        }
+        for (int e4 = 0; e4 < 4; ++e4)
+          *reinterpret_cast<uint2*>(st + tcol(j) * PITCHT + trow(i, 4 * e4)) =
+              make_uint2(pk[i][j][2 * e4], pk[i][j][2 * e4 + 1]);
     __syncthreads();
     for (int q = tid; q < TN * TM / 8; q += kThreads) {
       const int c = q / (TM / 8), r8 = q % (TM / 8);
@@ -388,12 +568,16 @@ __global__ __launch_bounds__(64 * GM * GN) void xent_gemm(GemmArgs g) {
   }
 }
 
-// dst[c][r] = src[r][c] for r < rows, 0 for rows <= r < rows_pad (c < cols); 64 x 64 tiles.
+// Transpose in blocks of `blk` rows (a multiple of 64): row r of src, column c goes to
+// dst[(r / blk) cols blk + c blk + r % blk] -- block k is the (cols x blk) transpose of rows
+// k blk .. -- with 0 for rows <= r < rows_pad (c < cols); 64 x 64 tiles.
 __global__ __launch_bounds__(256) void xent_transpose(const uint16_t* src, int rows, int cols, int64_t lds,
-                                                      uint16_t* dst, int rows_pad, int64_t ldd) {
+                                                      uint16_t* dst, int rows_pad, int blk) {
   __shared__ uint16_t t[64][66];
   const int c0 = blockIdx.x * 64, r0 = blockIdx.y * 64;
   const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  // a 64-row tile lies in one block (blk is a multiple of 64)
+  const int64_t dbase = int64_t(r0 / blk) * cols * blk + r0 % blk;
   uint16_t v[16];
 #pragma unroll
   for (int k = 0; k < 16; ++k) {   // loads first, from clamped indices
@@ -406,7 +590,7 @@ __global__ __launch_bounds__(256) void xent_transpose(const uint16_t* src, int r
 #pragma unroll
   for (int k = 0; k < 16; ++k) {
     const int c = c0 + ty + 4 * k, r = r0 + tx;
-    if (c < cols && r < rows_pad) dst[int64_t(c) * ldd + r] = t[tx][ty + 4 * k];
+    if (c < cols && r < rows_pad) dst[dbase + int64_t(c) * blk + tx] = t[tx][ty + 4 * k];
   }
 }
 
@@ -499,7 +683,7 @@ Layout layout(int n, int V, int d, int chunk) {
   L.part = o;    o += al256(int64_t(L.Vp / 256) * L.Np * 8);
   L.tgt = o;     o += al256(int64_t(L.Np) * 4);
   L.lrow = o;    o += al256(int64_t(L.Np) * 4);
-  L.wt = o;      o += al256(int64_t(d) * L.Vp * 2);
+  L.wt = o;      o += al256(int64_t((L.Vp + L.C - 1) / L.C) * d * L.C * 2);   // chunk-major W^T
   L.ht = o;      o += al256(int64_t(d) * L.Np * 2);
   L.P = o;       o += al256(int64_t(L.Np) * L.Cp * 2);
   L.PT = o;      o += al256(int64_t(L.Cp) * L.Np * 2);
@@ -589,11 +773,12 @@ extern "C" int32_t msd_xent_backward(const void* h, const void* weight, const in
   const uint16_t* W = static_cast<const uint16_t*>(weight);
   const uint16_t* H = static_cast<const uint16_t*>(h);
   hipLaunchKernelGGL(xent_targets, dim3((n_rows + 255) / 256), dim3(256), 0, s, targets, n_rows, vocab, tix, status);
-  // W^T (d x Vp) and h^T (d x Np), zero past V and N
+  // W^T (chunk-major: per chunk a d x C block, so a chunk's rows are C apart) and h^T (d x Np),
+  // zero past V and N
   hipLaunchKernelGGL(xent_transpose, dim3((d_model + 63) / 64, L.Vp / 64), dim3(256), 0, s, W, vocab, d_model,
-                     int64_t(d_model), wt, L.Vp, int64_t(L.Vp));
+                     int64_t(d_model), wt, L.Vp, L.C);
   hipLaunchKernelGGL(xent_transpose, dim3((d_model + 63) / 64, L.Np / 64), dim3(256), 0, s, H, n_rows, d_model,
-                     int64_t(d_model), ht, L.Np, int64_t(L.Np));
+                     int64_t(d_model), ht, L.Np, L.Np);
   for (int v0 = 0; v0 < vocab; v0 += L.C) {
     const int cv = std::min(L.C, vocab - v0);   // valid columns of this chunk
     const int cp = rup(cv, 256);                // padded
@@ -640,8 +825,8 @@ extern "C" int32_t msd_xent_backward(const void* h, const void* weight, const in
     a.A = P;
     a.lda = L.Cp;
     a.a_valid = L.Np;
-    a.B = wt + v0;
-    a.ldb = L.Vp;
+    a.B = wt + int64_t(v0 / L.C) * d_model * L.C;   // the chunk's block of W^T: d rows of C
+    a.ldb = L.C;
     a.b_valid = d_model;
     a.K = cp;
     a.tiles_m = L.Np / 128;
