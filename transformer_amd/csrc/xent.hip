@@ -11,8 +11,9 @@
 // partial (max, sum of exp(s - max)) and captures the target logits (the transposed product puts
 // one token's 64 values per tile in each lane's registers, so the reduction stays in registers);
 // xent_lse merges a token's partials in a fixed order (lse = max + log sum, the online logsumexp
-// of :293-301), xent_mean takes the mean of lse - target logit in a fixed order (float64 sum).  The logits never exist in memory, as in the
-// reference, whose chunk loop materialises only one (N, chunk) block at a time.
+// of :293-301), xent_mean takes the mean of lse - target logit in a fixed order (float64 sum).
+// The logits never exist in memory, as in the reference, whose chunk loop materialises only one
+// (N, chunk) block at a time.
 //
 // Backward (msd_xent_backward), per vocabulary chunk of `chunk` columns (the reference's
 // chunk loop, :344-353; the chunk bounds the probability buffers):
@@ -28,14 +29,15 @@
 // (xent_transpose) so that every GEMM reads both operands along K.
 //
 // GEMM (xent_gemm<TM, TN, EPI>): C = A B^T with A (M x K) and B (Nn x K) both K-contiguous bf16.
-// A workgroup of 4 waves (2 x 2) owns a TM x TN tile, each wave a (TM/2) x (TN/2) block of
-// 32 x 32 MFMA tiles.  K advances 64 at a time through two LDS stages: every thread loads its
-// 16-byte pieces of the next stage into registers before the current stage's MFMAs and writes
-// them to LDS after, with one barrier per step.  A row of a stage is 128 bytes whose eight
-// 16-byte pieces are stored XOR-swizzled by the row (piece c of row r at c ^ (r & 7)), so the 32
-// rows an MFMA fragment reads hit all 32 banks.  Tiles are dealt to the 8 XCDs in contiguous
-// ranges (workgroup i runs on XCD i % 8), so the workgroups of one XCD share operand rows in
-// its L2.
+// A workgroup of GM x GN waves owns a TM x TN tile (256 x 256 with 2 x 4 waves for the forward
+// logits and the backward's probability block, 128 x 128 with 2 x 2 waves for grad_W and grad_h),
+// each wave a block of 32 x 32 MFMA tiles.  K advances 32 at a time through a ring of 4 LDS
+// stages filled by direct DMA (global_load_lds, 16 bytes per lane), three stages in flight; a
+// stage row is 64 bytes whose four 16-byte pieces are stored XOR-swizzled by the row, so the rows
+// an MFMA fragment reads hit distinct banks.  Tiles are dealt to the 8 XCDs in contiguous ranges
+// (workgroup i runs on XCD i % 8), so the workgroups of one XCD share operand rows in its L2.
+// (XENT_DMA=0 builds the register-staged variant: two stages of K = 64, each thread's pieces
+// loaded into registers before the current stage's MFMAs and stored to LDS after.)
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <math.h>
