@@ -142,8 +142,9 @@ constexpr size_t lds_bytes() {
   return EPI == kEpiProb ? std::max<size_t>(ring, size_t(TM) * staging_pitch<TM, TN>() * 2 + TN * 8) : ring;
 #endif
   // kEpiProb: the bf16 staging tile (over the stage buffers) and the rows' lse and targets after it
-  return EPI == kEpiProb ? std::max<size_t>(2 * stage_bytes<TM, TN>(), size_t(TM) * staging_pitch<TM, TN>() * 2 + TN * 8)
-                         : size_t(2 * stage_bytes<TM, TN>());
+  return EPI == kEpiProb
+             ? std::max<size_t>(2 * stage_bytes<TM, TN>(), size_t(TM) * staging_pitch<TM, TN>() * 2 + TN * 8)
+             : size_t(2 * stage_bytes<TM, TN>());
 }
 
 // Tile (tm, tn) of workgroup b.  Workgroup b runs on XCD b % 8, which takes the tile ids
@@ -197,7 +198,9 @@ __device__ __forceinline__ void piece_offsets_(uint32_t (&off)[N], int row, int 
 constexpr int kKD = 32;   // K per DMA stage
 constexpr int kStages = 4;
 typedef __attribute__((address_space(3))) uint8_t lds_u8;
-__device__ __forceinline__ uint32_t lds_addr(const void* p) { return uint32_t(reinterpret_cast<uintptr_t>((const lds_u8*)p)); }
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return uint32_t(reinterpret_cast<uintptr_t>((const lds_u8*)p));
+}
 // (the host pass instantiates these templates along with the kernels but never emits them, and
 // an x86 compile rejects the vector-register constraints and the LDS builtin, so their bodies
 // are in the device pass only)
@@ -207,80 +210,75 @@ __device__ __forceinline__ void wait_vm() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 #endif
 }
-// The fragment reads of one DMA stage and the wait for them, as one assembly block: fa[ks][i] is
-// the A fragment of K step ks for row block i at a_ks + 2048 i (32 rows of 64 bytes apart), fb
-// likewise from b_ks.  The outputs exist only once the block has waited, so the compiler cannot
-// place a use (or a copy) of a fragment before its read has landed.
-__device__ __forceinline__ void stage_reads(u32x4 (&fa)[2][4], u32x4 (&fb)[2][2], uint32_t a0, uint32_t a1,
-                                            uint32_t b0, uint32_t b1) {
+// The fragment reads of one K step (16) of a DMA stage: fa[i] is the A fragment of row block i
+// at a + 2048 i (32 rows of 64 bytes apart), fb[j] the B fragment at b + 2048 j.  The reads are
+// issued by one assembly block and waited for by wait_frags, whose "+v" operands tie the
+// fragments to the wait: the compiler cannot place a use (or a copy) of a fragment before the
+// wait, while the MFMAs of the other K step may run between the two.
+__device__ __forceinline__ void step_reads(u32x4 (&fa)[4], u32x4 (&fb)[2], uint32_t a, uint32_t b) {
 #if defined(__HIP_DEVICE_COMPILE__)
   asm volatile(
-      "ds_read_b128 %0, %12 offset:0\n"
-      "ds_read_b128 %1, %12 offset:2048\n"
-      "ds_read_b128 %2, %12 offset:4096\n"
-      "ds_read_b128 %3, %12 offset:6144\n"
-      "ds_read_b128 %4, %14 offset:0\n"
-      "ds_read_b128 %5, %14 offset:2048\n"
-      "ds_read_b128 %6, %13 offset:0\n"
-      "ds_read_b128 %7, %13 offset:2048\n"
-      "ds_read_b128 %8, %13 offset:4096\n"
-      "ds_read_b128 %9, %13 offset:6144\n"
-      "ds_read_b128 %10, %15 offset:0\n"
-      "ds_read_b128 %11, %15 offset:2048\n"
-      "s_waitcnt lgkmcnt(0)"
-      : "=&v"(fa[0][0]), "=&v"(fa[0][1]), "=&v"(fa[0][2]), "=&v"(fa[0][3]), "=&v"(fb[0][0]), "=&v"(fb[0][1]),
-        "=&v"(fa[1][0]), "=&v"(fa[1][1]), "=&v"(fa[1][2]), "=&v"(fa[1][3]), "=&v"(fb[1][0]), "=&v"(fb[1][1])
-      : "v"(a0), "v"(a1), "v"(b0), "v"(b1));
+      "ds_read_b128 %0, %6 offset:0\n"
+      "ds_read_b128 %1, %6 offset:2048\n"
+      "ds_read_b128 %2, %6 offset:4096\n"
+      "ds_read_b128 %3, %6 offset:6144\n"
+      "ds_read_b128 %4, %7 offset:0\n"
+      "ds_read_b128 %5, %7 offset:2048"
+      : "=&v"(fa[0]), "=&v"(fa[1]), "=&v"(fa[2]), "=&v"(fa[3]), "=&v"(fb[0]), "=&v"(fb[1])
+      : "v"(a), "v"(b));
 #endif
 }
-__device__ __forceinline__ void stage_reads(u32x4 (&fa)[2][2], u32x4 (&fb)[2][2], uint32_t a0, uint32_t a1,
-                                            uint32_t b0, uint32_t b1) {
+template <int N>
+__device__ __forceinline__ void wait_frags(u32x4 (&fa)[4], u32x4 (&fb)[2]) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  asm volatile("s_waitcnt lgkmcnt(%6)"
+               : "+v"(fa[0]), "+v"(fa[1]), "+v"(fa[2]), "+v"(fa[3]), "+v"(fb[0]), "+v"(fb[1])
+               : "n"(N));
+#endif
+}
+__device__ __forceinline__ void step_reads(u32x4 (&fa)[2], u32x4 (&fb)[2], uint32_t a, uint32_t b) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  asm volatile(
+      "ds_read_b128 %0, %4 offset:0\n"
+      "ds_read_b128 %1, %4 offset:2048\n"
+      "ds_read_b128 %2, %5 offset:0\n"
+      "ds_read_b128 %3, %5 offset:2048"
+      : "=&v"(fa[0]), "=&v"(fa[1]), "=&v"(fb[0]), "=&v"(fb[1])
+      : "v"(a), "v"(b));
+#endif
+}
+template <int N>
+__device__ __forceinline__ void wait_frags(u32x4 (&fa)[2], u32x4 (&fb)[2]) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  asm volatile("s_waitcnt lgkmcnt(%4)" : "+v"(fa[0]), "+v"(fa[1]), "+v"(fb[0]), "+v"(fb[1]) : "n"(N));
+#endif
+}
+__device__ __forceinline__ void step_reads(u32x4 (&fa)[4], u32x4 (&fb)[4], uint32_t a, uint32_t b) {
 #if defined(__HIP_DEVICE_COMPILE__)
   asm volatile(
       "ds_read_b128 %0, %8 offset:0\n"
       "ds_read_b128 %1, %8 offset:2048\n"
-      "ds_read_b128 %2, %10 offset:0\n"
-      "ds_read_b128 %3, %10 offset:2048\n"
+      "ds_read_b128 %2, %8 offset:4096\n"
+      "ds_read_b128 %3, %8 offset:6144\n"
       "ds_read_b128 %4, %9 offset:0\n"
       "ds_read_b128 %5, %9 offset:2048\n"
-      "ds_read_b128 %6, %11 offset:0\n"
-      "ds_read_b128 %7, %11 offset:2048\n"
-      "s_waitcnt lgkmcnt(0)"
-      : "=&v"(fa[0][0]), "=&v"(fa[0][1]), "=&v"(fb[0][0]), "=&v"(fb[0][1]), "=&v"(fa[1][0]), "=&v"(fa[1][1]),
-        "=&v"(fb[1][0]), "=&v"(fb[1][1])
-      : "v"(a0), "v"(a1), "v"(b0), "v"(b1));
+      "ds_read_b128 %6, %9 offset:4096\n"
+      "ds_read_b128 %7, %9 offset:6144"
+      : "=&v"(fa[0]), "=&v"(fa[1]), "=&v"(fa[2]), "=&v"(fa[3]), "=&v"(fb[0]), "=&v"(fb[1]), "=&v"(fb[2]), "=&v"(fb[3])
+      : "v"(a), "v"(b));
 #endif
 }
-__device__ __forceinline__ void stage_reads(u32x4 (&fa)[2][4], u32x4 (&fb)[2][4], uint32_t a0, uint32_t a1,
-                                            uint32_t b0, uint32_t b1) {
+template <int N>
+__device__ __forceinline__ void wait_frags(u32x4 (&fa)[4], u32x4 (&fb)[4]) {
 #if defined(__HIP_DEVICE_COMPILE__)
-  asm volatile(
-      "ds_read_b128 %0, %16 offset:0\n"
-      "ds_read_b128 %1, %16 offset:2048\n"
-      "ds_read_b128 %2, %16 offset:4096\n"
-      "ds_read_b128 %3, %16 offset:6144\n"
-      "ds_read_b128 %4, %18 offset:0\n"
-      "ds_read_b128 %5, %18 offset:2048\n"
-      "ds_read_b128 %6, %18 offset:4096\n"
-      "ds_read_b128 %7, %18 offset:6144\n"
-      "ds_read_b128 %8, %17 offset:0\n"
-      "ds_read_b128 %9, %17 offset:2048\n"
-      "ds_read_b128 %10, %17 offset:4096\n"
-      "ds_read_b128 %11, %17 offset:6144\n"
-      "ds_read_b128 %12, %19 offset:0\n"
-      "ds_read_b128 %13, %19 offset:2048\n"
-      "ds_read_b128 %14, %19 offset:4096\n"
-      "ds_read_b128 %15, %19 offset:6144\n"
-      "s_waitcnt lgkmcnt(0)"
-      : "=&v"(fa[0][0]), "=&v"(fa[0][1]), "=&v"(fa[0][2]), "=&v"(fa[0][3]), "=&v"(fb[0][0]), "=&v"(fb[0][1]),
-        "=&v"(fb[0][2]), "=&v"(fb[0][3]), "=&v"(fa[1][0]), "=&v"(fa[1][1]), "=&v"(fa[1][2]), "=&v"(fa[1][3]),
-        "=&v"(fb[1][0]), "=&v"(fb[1][1]), "=&v"(fb[1][2]), "=&v"(fb[1][3])
-      : "v"(a0), "v"(a1), "v"(b0), "v"(b1));
+  asm volatile("s_waitcnt lgkmcnt(%8)"
+               : "+v"(fa[0]), "+v"(fa[1]), "+v"(fa[2]), "+v"(fa[3]), "+v"(fb[0]), "+v"(fb[1]), "+v"(fb[2]),
+                 "+v"(fb[3])
+               : "n"(N));
 #endif
 }
 template <int RB, int CB>
-__device__ __forceinline__ void stage_reads(u32x4 (&)[2][RB], u32x4 (&)[2][CB], uint32_t, uint32_t, uint32_t,
-                                            uint32_t) {
+__device__ __forceinline__ void step_reads(u32x4 (&)[RB], u32x4 (&)[CB], uint32_t, uint32_t) {
   static_assert(RB < 0, "no fragment-read block for this wave tile");
 }
 // The NIW DMAs of one stage for this wave: instruction u fills the 1 KB at st + 1024 (wv + NW u)
@@ -295,19 +293,29 @@ __device__ __forceinline__ void dma_stage(const uint16_t* A, const uint16_t* B, 
                                      (__attribute__((address_space(3))) void*)(st + 1024 * (wv + NW * u)), 16, 0, 0);
 #endif
 }
-// The MFMAs of one DMA stage (K = 32): both K steps' fragments read, then the RB x CB x 2 MFMAs.
+// The MFMAs of one DMA stage (K = 32): both K steps' fragment reads issued together, the first
+// step's MFMAs once its reads have landed (the second step's reads land meanwhile), then the
+// second step's.  The scheduling barrier keeps the compiler from moving the first step's MFMAs
+// past the second wait.
+template <int RB, int CB>
+__device__ __forceinline__ void mma_step(f32x16 (&acc)[RB][CB], const u32x4 (&fa)[RB], const u32x4 (&fb)[CB]) {
+#pragma unroll
+  for (int i = 0; i < RB; ++i)
+#pragma unroll
+    for (int j = 0; j < CB; ++j)
+      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf(fa[i]), as_bf(fb[j]), acc[i][j], 0, 0, 0);
+}
 template <int TM, int RB, int CB>
 __device__ __forceinline__ void mma_stage_dma(f32x16 (&acc)[RB][CB], uint32_t a0, uint32_t a1, uint32_t b0,
                                               uint32_t b1) {
-  u32x4 fa[2][RB], fb[2][CB];
-  stage_reads(fa, fb, a0, a1, b0, b1);
-#pragma unroll
-  for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-    for (int i = 0; i < RB; ++i)
-#pragma unroll
-      for (int j = 0; j < CB; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf(fa[ks][i]), as_bf(fb[ks][j]), acc[i][j], 0, 0, 0);
+  u32x4 fa[RB], fb[CB], ga[RB], gb[CB];
+  step_reads(fa, fb, a0, b0);
+  step_reads(ga, gb, a1, b1);
+  wait_frags<RB + CB>(fa, fb);
+  mma_step(acc, fa, fb);
+  __builtin_amdgcn_sched_barrier(0);
+  wait_frags<0>(ga, gb);
+  mma_step(acc, ga, gb);
 }
 
 // The MFMAs of one LDS stage (K = 64): 4 steps of 16, each reading this wave's RB A fragments and
