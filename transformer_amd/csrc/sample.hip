@@ -48,6 +48,7 @@ constexpr int kT = 1024;                    // threads of the single-workgroup k
 constexpr int kWaves = kT / 64;
 constexpr int kVMax = 32768;                // largest vocabulary: 32 entries per thread
 constexpr int kPer = kVMax / kT;
+static_assert(kPer == 32, "a thread of the single-workgroup kernels holds one 32-bit word of entry flags");
 constexpr int kTile = 512;                  // radix tile: entries per scatter workgroup
 constexpr int kTileThreads = 256;
 constexpr int kRounds = kTile / kTileThreads;
@@ -70,13 +71,22 @@ struct SArgs {
   int32_t* token_out;
   float* probs_out;       // optional [V]: normalised probabilities in id order
   int32_t* kept_out;      // optional: number of ids kept by the nucleus
-  uint32_t* keys[2];      // radix ping-pong: float bits of the probabilities
+  float* lg;              // [V] penalised, scaled logits in id order
+  float* ex;              // [V] exp(l - max) in id order
+  float* pr;              // [V] probabilities in id order
+  float* sp;              // [V] probabilities in sorted order (written by the last radix pass)
+  uint32_t* eqw;          // [kVMax / 32] bit i of word w: sorted entry 32w + i equals entry 32w + i + 1
+  float* pre;             // [kVMax / 128] numpy's pairwise leaf sums of the full 8192-entry buffers
+                          // of the sorted probabilities
+  uint32_t* keys[2];      // radix ping-pong: order-preserving bits of the penalised logits
   uint32_t* ids[2];
   uint32_t* hist;         // [kPasses][kMaxTiles][256]
   int* table;             // [3][kVMax / 64]: chunk totals, binades, odd-start changes
   float* tmax;            // [kVMax / 512]: maxima of the penalised, scaled logits per tile
   float* lsum;            // [kVMax / 8192][256]: numpy's pairwise leaf sums by buffer and heap slot
   int V;
+  int ntiles;             // tiles of kTile ids
+  int nleaf;              // workgroups of the pairwise-leaf role of sample_leaf_kernel
   int mode;
   int use_pen;
   float pen;
@@ -470,33 +480,75 @@ __global__ __launch_bounds__(kT) void sample_greedy_kernel(SArgs a) {
 }
 
 // Softmax, first step (generate.py:33-48): workgroup w takes ids [512w, 512w+512), stores the
-// penalised, scaled logits (to keys[1]) and their maximum (to tmax[w]).
+// penalised, scaled logits (to lg) and their maximum (to tmax[w]).  For the nucleus it also starts
+// the sort (generate.py:55): the sort keys are the order-preserving bits of those logits with the
+// ids in order, and this tile's counts of the first radix digit; the counts of the later passes
+// are cleared here for the scatters to fill.
 __global__ __launch_bounds__(kTile) void sample_max_kernel(SArgs a) {
   __shared__ float wm[kTile / 64];
-  const int t = threadIdx.x, j = blockIdx.x * kTile + t;
+  __shared__ uint32_t hl[256];
+  const int t = threadIdx.x, w = blockIdx.x, j = w * kTile + t;
+  const bool nuc = a.mode == kNucleus;
+  if (nuc && t < 256) hl[t] = 0;
   const int jc = min(j, a.V - 1);
   const float lv = a.logits[jc];
   const uint8_t sn = a.seen[jc];
   const float pv = penalised(a, lv, sn, true);
   const float l = j < a.V ? pv : -INFINITY;
-  if (j < a.V) reinterpret_cast<float*>(a.keys[1])[j] = l;
+  const uint32_t key = ordered(l);
+  if (j < a.V) {
+    a.lg[j] = l;
+    if (nuc) {
+      a.keys[0][j] = key;
+      a.ids[0][j] = uint32_t(j);
+    }
+  }
   const float m = wave_max(l);
   if (lane_id() == 0) wm[t >> 6] = m;
   __syncthreads();
+  if (nuc && j < a.V) atomicAdd(&hl[255u - (key & 255u)], 1u);
   if (t == 0) {
     float mm = wm[0];
     for (int i = 1; i < kTile / 64; ++i) mm = fmaxf(mm, wm[i]);
-    a.tmax[blockIdx.x] = mm;
+    a.tmax[w] = mm;
   }
+  __syncthreads();
+  if (nuc && t < 256) {
+    a.hist[w * 256 + t] = hl[t];
+    for (int p = 1; p < kPasses; ++p) a.hist[p * kHistWords + w * 256 + t] = 0;
+  }
+}
+
+// numpy's pairwise leaf of 128 entries held by one wave (x0: entry lane, x1: entry lane + 64):
+// accumulator r_k = e[k] + e[k + 8] + ... + e[k + 120] in order on lane k < 8, combined as
+// ((r0 + r1) + (r2 + r3)) + ((r4 + r5) + (r6 + r7)).  Wave-uniform result.
+__device__ float leaf128(float x0, float x1) {
+  const int lane = lane_id();
+  float r = x0;
+#pragma unroll
+  for (int q = 1; q < 16; ++q) {
+    const int idx = lane + 8 * q;
+    r += q < 8 ? __shfl(x0, idx & 63) : __shfl(x1, idx & 63);
+  }
+  return ((readlane_f(r, 0) + readlane_f(r, 1)) + (readlane_f(r, 2) + readlane_f(r, 3))) +
+         ((readlane_f(r, 4) + readlane_f(r, 5)) + (readlane_f(r, 6) + readlane_f(r, 7)));
 }
 
 // Softmax numerator (generate.py:49-50) and the leaves of numpy's float32 sum: wave g takes heap
 // slot g % 255 of reduction buffer g / 255 and, when that node is a leaf (<= 128 ids), writes
-// the correctly rounded exp(l - max) of its ids (to keys[0]) and the leaf's pairwise sum (to
+// the correctly rounded exp(l - max) of its ids (to ex) and the leaf's pairwise sum (to
 // lsum[256 * buffer + slot]).  The leaves of a buffer partition it, so every id is covered once.
+// For the nucleus, the workgroups after the first nleaf run the sort's first radix pass.
 constexpr int kLeafWaves = 4;
+static_assert(64 * kLeafWaves == kTileThreads, "the leaf launch also runs radix workgroups");
+
+__device__ void radix_pass(const SArgs& a, int pass, int w);
 
 __global__ __launch_bounds__(64 * kLeafWaves) void sample_leaf_kernel(SArgs a) {
+  if (int(blockIdx.x) >= a.nleaf) {   // the nucleus' first radix pass runs beside the leaves
+    radix_pass(a, 0, int(blockIdx.x) - a.nleaf);
+    return;
+  }
   const int lane = lane_id();
   const int g = blockIdx.x * kLeafWaves + (threadIdx.x >> 6);
   const int k = g / kSlots, slot = g - k * kSlots;
@@ -507,8 +559,8 @@ __global__ __launch_bounds__(64 * kLeafWaves) void sample_leaf_kernel(SArgs a) {
   if (!pw_node(bn, slot, start, len) || len > kPwBlock) return;
   const int ntiles = (V + kTile - 1) / kTile;
   const int j0 = k * kRedChunk + start;
-  const float* lg = reinterpret_cast<const float*>(a.keys[1]);
-  float* eo = reinterpret_cast<float*>(a.keys[0]);
+  const float* lg = a.lg;
+  float* eo = a.ex;
   const float l0 = lg[j0 + min(lane, len - 1)], l1 = lg[j0 + min(lane + 64, len - 1)];
   const float tm = a.tmax[min(lane, ntiles - 1)];
   const float m = wave_max(lane < ntiles ? tm : -INFINITY);
@@ -544,55 +596,57 @@ __global__ __launch_bounds__(64 * kLeafWaves) void sample_leaf_kernel(SArgs a) {
 // Normalisation (generate.py:51): p = e / sum with numpy's sum = the buffer sums added in order
 // to 0, each buffer's sum its pairwise tree over the leaf sums (inner nodes by decreasing
 // depth; every workgroup evaluates the tree identically).  Workgroup w takes ids
-// [512w, 512w+512): probabilities (optionally to probs_out), and for top_p < 1 the radix keys
-// in id order with this tile's counts of the first digit.
+// [512w, 512w+512), two per thread: the probabilities in id order (to pr, optionally to
+// probs_out).  For the nucleus, the workgroups after the first ntiles run the second radix pass.
 constexpr int kMaxBufs = kVMax / kRedChunk;
+constexpr int kNormThreads = 256;
+static_assert(kNormThreads == kTileThreads, "the normalisation launch also runs radix workgroups");
 
-__global__ __launch_bounds__(kTile) void sample_norm_kernel(SArgs a) {
-  __shared__ uint32_t hl[256];
+__global__ __launch_bounds__(kNormThreads) void sample_norm_kernel(SArgs a) {
+  if (int(blockIdx.x) >= a.ntiles) {
+    radix_pass(a, 1, int(blockIdx.x) - a.ntiles);
+    return;
+  }
   __shared__ float node[kMaxBufs * 256];
-  const int t = threadIdx.x, w = blockIdx.x, V = a.V, j = w * kTile + t;
+  const int t = threadIdx.x, w = blockIdx.x, V = a.V;
   const int nbuf = (V + kRedChunk - 1) / kRedChunk;
-  constexpr int kNodeRounds = kMaxBufs * 256 / kTile;
+  constexpr int kNodeRounds = kMaxBufs * 256 / kNormThreads;
+  constexpr int kIds = kTile / kNormThreads;
   int depth[kNodeRounds];
   bool inner[kNodeRounds];
-  const float e = reinterpret_cast<const float*>(a.keys[0])[min(j, V - 1)];
-  float ls[kNodeRounds];
+  float e[kIds], ls[kNodeRounds];
 #pragma unroll
-  for (int r = 0; r < kNodeRounds; ++r) ls[r] = a.lsum[t + kTile * r];
+  for (int r = 0; r < kIds; ++r) e[r] = a.ex[min(w * kTile + t + kNormThreads * r, V - 1)];
+#pragma unroll
+  for (int r = 0; r < kNodeRounds; ++r) ls[r] = a.lsum[t + kNormThreads * r];
 #pragma unroll
   for (int r = 0; r < kNodeRounds; ++r) {
-    const int q = t + kTile * r, k = q >> 8, slot = q & 255;
+    const int q = t + kNormThreads * r, k = q >> 8, slot = q & 255;
     int start = 0, len = 0;
     const bool valid = k < nbuf && slot < kSlots && pw_node(min(kRedChunk, V - k * kRedChunk), slot, start, len);
     inner[r] = valid && len > kPwBlock;
     depth[r] = 31 - __clz(slot + 1);
     if (valid && len <= kPwBlock) node[q] = ls[r];
   }
-  if (t < 256) hl[t] = 0;
   __syncthreads();
   for (int d = 6; d >= 0; --d) {
 #pragma unroll
     for (int r = 0; r < kNodeRounds; ++r) {
-      const int q = t + kTile * r, kb = q & ~255, slot = q & 255;
+      const int q = t + kNormThreads * r, kb = q & ~255, slot = q & 255;
       if (inner[r] && depth[r] == d) node[q] = node[kb + 2 * slot + 1] + node[kb + 2 * slot + 2];
     }
     __syncthreads();
   }
   float total = 0.f;
   for (int q = 0; q < nbuf; ++q) total += node[q << 8];
-  if (j < V) {
-    const float pj = e / total;
-    if (a.probs_out) a.probs_out[j] = pj;
-    const uint32_t key = __float_as_uint(pj);
-    a.keys[0][j] = key;
-    a.ids[0][j] = uint32_t(j);
-    if (a.mode == kNucleus) atomicAdd(&hl[255u - (key & 255u)], 1u);
-  }
-  __syncthreads();
-  if (a.mode == kNucleus && t < 256) {
-    a.hist[w * 256 + t] = hl[t];
-    for (int p = 1; p < kPasses; ++p) a.hist[p * kHistWords + w * 256 + t] = 0;
+#pragma unroll
+  for (int r = 0; r < kIds; ++r) {
+    const int j = w * kTile + t + kNormThreads * r;
+    if (j < V) {
+      const float pj = e[r] / total;
+      a.pr[j] = pj;
+      if (a.probs_out) a.probs_out[j] = pj;
+    }
   }
 }
 
@@ -603,7 +657,7 @@ __global__ __launch_bounds__(kT) void sample_full_kernel(SArgs a) {
   const int t = threadIdx.x, V = a.V;
   uint32_t kv[kPer];
 #pragma unroll
-  for (int i = 0; i < kPer; ++i) kv[i] = a.keys[0][min(t + kT * i, V - 1)];
+  for (int i = 0; i < kPer; ++i) kv[i] = __float_as_uint(a.pr[min(t + kT * i, V - 1)]);
 #pragma unroll
   for (int i = 0; i < kPer; ++i)
     if (t + kT * i < V) sh_p[pad(t + kT * i)] = __uint_as_float(kv[i]);
@@ -617,17 +671,19 @@ __global__ __launch_bounds__(kT) void sample_full_kernel(SArgs a) {
 // can move a sum).  table[c] = the chunk's increment in ulps for an even start value (-1: take
 // it entry by entry), table[kChunks + c] = E, table[2 kChunks + c] = the change for an odd
 // start value (only the first tie's adjustment flips).  Workgroup w takes chunks
-// [16w, 16w + 16), one wave per chunk.
+// [16w, 16w + 16), one wave per chunk (the last chunk may be partial: no table entry).  Each wave
+// also marks the entries equal to their successor (eqw) and, when its index g is a leaf of a full
+// 8192-entry buffer, stores numpy's pairwise leaf sum of entries [128 g, 128 g + 128) (pre): the
+// renormalising sum of the kept prefix reuses the leaves of its full buffers.
 constexpr int kTabChunks = kWaves;   // one chunk per wave
 
 __global__ __launch_bounds__(kT) void sample_table_kernel(SArgs a) {
   __shared__ double red[kWaves];
   __shared__ double csum[kTabChunks];
   const int t = threadIdx.x, lane = lane_id(), wv = t >> 6;
-  const int n = a.V, nch = n / 64;
+  const int n = a.V, nch = n / 64, nall = (n + 63) / 64;
   const int c0 = blockIdx.x * kTabChunks;
-  if (c0 >= nch) return;
-  const float* p = reinterpret_cast<const float*>(a.keys[kPasses & 1]);
+  const float* p = a.sp;
   // float64 sum of the entries before this workgroup's chunks (at most 31 per thread, all
   // requested at once; the order is irrelevant: only the binade with its margin is used)
   float pv[kPer];
@@ -636,17 +692,26 @@ __global__ __launch_bounds__(kT) void sample_table_kernel(SArgs a) {
     const float v = p[min(t + kT * i, n - 1)];
     pv[i] = t + kT * i < 64 * c0 ? v : 0.f;
   }
+  const int c = c0 + wv, g = blockIdx.x * kWaves + wv;
+  const float xl = p[min(64 * c + lane, n - 1)], xn = p[min(64 * c + lane + 1, n - 1)];
+  const float y0 = p[min(128 * g + lane, n - 1)], y1 = p[min(128 * g + 64 + lane, n - 1)];
   double pre = 0.0;
 #pragma unroll
   for (int i = 0; i < kPer; ++i) pre += double(pv[i]);
   for (int o = 32; o; o >>= 1) pre += __shfl_xor(pre, o);
   if (lane == 0) red[wv] = pre;
-  const int c = c0 + wv;
-  const float xl = p[min(64 * c + lane, n - 1)];
   const float x = c < nch ? xl : 0.f;
   double v = x;
   for (int o = 32; o; o >>= 1) v += __shfl_xor(v, o);
   if (lane == 0) csum[wv] = v;
+  if (c < nall) {
+    const uint64_t eq = __ballot(64 * c + lane + 1 < n && xl == xn);
+    if (lane < 2) a.eqw[2 * c + lane] = uint32_t(eq >> (32 * lane));
+  }
+  if (g < kVMax / kPwBlock && (g / (kRedChunk / kPwBlock) + 1) * kRedChunk <= n) {
+    const float s = leaf128(y0, y1);
+    if (lane == 0) a.pre[g] = s;
+  }
   __syncthreads();
   if (c >= nch) return;
   double ps = 0.0;
@@ -670,14 +735,16 @@ __global__ __launch_bounds__(kT) void sample_table_kernel(SArgs a) {
 }
 
 // One stable LSD pass over digit `pass` (bits 8*pass..8*pass+7, descending order) from
-// keys/ids[pass & 1] to keys/ids[(pass + 1) & 1].  Workgroup w moves entries
-// [512w, 512w+512) in order: an entry's destination is the number of entries with a larger
-// digit, plus those with the same digit in earlier tiles, earlier rounds of this tile, earlier
-// waves of this round and lower lanes of this wave.
-__global__ __launch_bounds__(kTileThreads) void sample_radix_kernel(SArgs a, int pass) {
+// keys/ids[pass & 1] to keys/ids[(pass + 1) & 1], by workgroup w (256 threads) of the launch that
+// runs it.  Tile w holds entries [512w, 512w+512), moved in order: an entry's destination is the
+// number of entries with a larger digit, plus those with the same digit in earlier tiles, earlier
+// rounds of this tile, earlier waves of this round and lower lanes of this wave.  The last pass
+// also writes each entry's probability to its sorted position (sp).
+__device__ void radix_pass(const SArgs& a, int pass, int w) {
   __shared__ uint32_t base[256], run[256], wcnt[kTileThreads / 64][256], wtot[kTileThreads / 64];
-  const int t = threadIdx.x, w = blockIdx.x, wv = t >> 6, lane = lane_id();
+  const int t = threadIdx.x, wv = t >> 6, lane = lane_id();
   const int V = a.V, ntiles = (V + kTile - 1) / kTile;
+  const bool last = pass == kPasses - 1;
   const uint32_t* kin = a.keys[pass & 1];
   const uint32_t* iin = a.ids[pass & 1];
   uint32_t key[kRounds], id[kRounds];   // this thread's entries, requested with the counts
@@ -686,6 +753,11 @@ __global__ __launch_bounds__(kTileThreads) void sample_radix_kernel(SArgs a, int
     const int e = w * kTile + r * kTileThreads + t;
     key[r] = kin[min(e, V - 1)];
     id[r] = iin[min(e, V - 1)];
+  }
+  float pv[kRounds] = {};
+  if (last) {
+#pragma unroll
+    for (int r = 0; r < kRounds; ++r) pv[r] = a.pr[min(id[r], uint32_t(V - 1))];
   }
   const uint32_t* H = a.hist + pass * kHistWords;
   uint32_t tot = 0, part = 0;
@@ -733,6 +805,7 @@ __global__ __launch_bounds__(kTileThreads) void sample_radix_kernel(SArgs a, int
     if (valid && pos < uint32_t(V)) {   // always true when the counts are consistent
       kout[pos] = key[r];
       iout[pos] = id[r];
+      if (last) a.sp[pos] = pv[r];
       if (pass + 1 < kPasses) {
         const uint32_t nd = 255u - ((key[r] >> (shift + 8)) & 255u);
         atomicAdd(&a.hist[(pass + 1) * kHistWords + (pos / kTile) * 256 + nd], 1u);
@@ -743,16 +816,102 @@ __global__ __launch_bounds__(kTileThreads) void sample_radix_kernel(SArgs a, int
   }
 }
 
+__global__ __launch_bounds__(kTileThreads) void sample_radix_kernel(SArgs a, int pass) {
+  radix_pass(a, pass, blockIdx.x);
+}
+
+// The id at sorted position pos in numpy's order.  The radix sort orders the ids by their
+// penalised logits, which gives the probabilities in the same sequence of values (a probability is
+// a nondecreasing function of its logit: rounding, exp and the division by the total all keep
+// order), so the cutoff, the sums and the drawn position are numpy's; but ids of equal probability
+// come out in the order of their logits, where numpy's stable sort has them in ascending id order.
+// So the answer is the (pos - ra)-th smallest id of the run [ra, rb) of entries equal to entry
+// pos.  eqw (LDS copy, kVMax / 32 words; bit n - 1 is clear: the last entry has no successor)
+// locates the run -- wave 0 scans 64 words per step outward from pos -- and is then reused as a
+// bitmap of the run's ids.
+__device__ int tie_fixup(const SArgs& a, uint32_t* eqw, int pos, BlockScratch& b) {
+  const int t = threadIdx.x, lane = lane_id();
+  const uint32_t* ids = a.ids[kPasses & 1];
+  if (t < 64) {
+    const int wp = pos >> 5, bp = pos & 31;
+    // ra = 1 + the largest i < pos with bit i clear (0 when there is none)
+    const uint32_t below = bp ? ~eqw[wp] & ((1u << bp) - 1u) : 0u;
+    int ra = -1;
+    if (below) {
+      ra = 32 * wp + 31 - __clz(below) + 1;
+    } else {
+      for (int w1 = wp - 1; w1 >= 0 && ra < 0; w1 -= 64) {
+        const int w = w1 - lane;
+        const uint32_t c = w >= 0 ? ~eqw[max(w, 0)] : 0u;
+        const uint64_t m = __ballot(c != 0u);
+        if (m) {
+          const int l = __ffsll(static_cast<unsigned long long>(m)) - 1;
+          const uint32_t cl = uint32_t(__builtin_amdgcn_readlane(int(c), l));
+          ra = 32 * (w1 - l) + 31 - __clz(cl) + 1;
+        }
+      }
+      if (ra < 0) ra = 0;
+    }
+    // rb = 1 + the smallest i >= pos with bit i clear
+    const uint32_t from = ~eqw[wp] & ~((1u << bp) - 1u);
+    int rb = -1;
+    if (from) {
+      rb = 32 * wp + __ffs(from) - 1 + 1;
+    } else {
+      for (int w1 = wp + 1; rb < 0 && w1 < kVMax / 32; w1 += 64) {   // bit n - 1 is clear
+        const int w = min(w1 + lane, kVMax / 32 - 1);
+        const uint32_t c = ~eqw[w];
+        const uint64_t m = __ballot(c != 0u);
+        if (m) {
+          const int l = __ffsll(static_cast<unsigned long long>(m)) - 1;
+          const uint32_t cl = uint32_t(__builtin_amdgcn_readlane(int(c), l));
+          rb = 32 * min(w1 + l, kVMax / 32 - 1) + __ffs(cl) - 1 + 1;
+        }
+      }
+    }
+    if (rb < 0) rb = a.V;
+    if (lane == 0) {
+      b.kw[0] = uint64_t(ra);
+      b.kw[1] = uint64_t(rb);
+    }
+  }
+  __syncthreads();
+  const int ra = int(b.kw[0]), rb = int(b.kw[1]);
+  __syncthreads();
+  if (rb - ra == 1) return int(ids[pos]);
+  eqw[t] = 0u;
+  __syncthreads();
+  for (int i = ra + t; i < rb; i += kT) {
+    const uint32_t id = ids[i];
+    atomicOr(&eqw[id >> 5], 1u << (id & 31u));
+  }
+  __syncthreads();
+  const uint32_t m0 = eqw[t];
+  const int c = __popc(m0), k = pos - ra;
+  const int ex = int(block_excl_scan_f64(double(c), b));
+  if (k >= ex && k < ex + c) {
+    uint32_t m = m0;
+    for (int q = 0; q < k - ex; ++q) m &= m - 1u;   // clear the lowest set bits
+    b.i0 = 32 * t + __ffs(m) - 1;
+  }
+  __syncthreads();
+  const int r = b.i0;
+  __syncthreads();
+  return r;
+}
+
 __global__ __launch_bounds__(kT) void sample_nucleus_kernel(SArgs a) {
   extern __shared__ float sh_p[];   // sorted probabilities, padded layout
   __shared__ BlockScratch b;
   __shared__ int ttot[kChunks], tex[kChunks], tdl[kChunks];
-  __shared__ float pre[kVMax / kPwBlock];   // leaf sums of the full 8192-id buffers
-  const int t = threadIdx.x, V = a.V;
-  const uint32_t* ks = a.keys[kPasses & 1];
+  __shared__ float pre[kVMax / kPwBlock];   // leaf sums of the full 8192-entry buffers
+  __shared__ uint32_t eqw[kVMax / 32];      // equal-successor bits of the sorted entries
+  const int t = threadIdx.x, V = a.V, nw = 2 * ((V + 63) / 64);
   uint32_t kv[kPer];   // every load issued before the first LDS store
 #pragma unroll
-  for (int i = 0; i < kPer; ++i) kv[i] = ks[min(t + kT * i, V - 1)];
+  for (int i = 0; i < kPer; ++i) kv[i] = __float_as_uint(a.sp[min(t + kT * i, V - 1)]);
+  const uint32_t ew = a.eqw[min(t, nw - 1)];
+  const float pl = a.pre[min(t, kVMax / kPwBlock - 1)];
   for (int c = t; c < V / 64; c += kT) {
     ttot[c] = a.table[c];
     tex[c] = a.table[kChunks + c];
@@ -761,27 +920,24 @@ __global__ __launch_bounds__(kT) void sample_nucleus_kernel(SArgs a) {
 #pragma unroll
   for (int i = 0; i < kPer; ++i)
     if (t + kT * i < V) sh_p[pad(t + kT * i)] = __uint_as_float(kv[i]);
+  eqw[t] = t < nw ? ew : 0u;
+  if (t < kVMax / kPwBlock) pre[t] = pl;
   __syncthreads();
   if (t < 64) {
     const int c = nucleus_cutoff(sh_p, V, a.t32, ttot, tex, tdl);
     if (t == 0) b.i0 = c;
-  } else if (t - 64 < kVMax / kPwBlock) {
-    // meanwhile the other waves sum the leaves of every full buffer: the renormalising sum
-    // of the kept prefix reuses those of its full buffers
-    const int li = t - 64, k = li / (kRedChunk / kPwBlock);
-    if ((k + 1) * kRedChunk <= V) pre[li] = pw_leaf(sh_p, li * kPwBlock, kPwBlock);
   }
   __syncthreads();
   const int kept = min(b.i0, V);
   const float fsum = np_sum(sh_p, kept, b, pre);
   const int pos = inverse_cdf(sh_p, kept, true, fsum, a.u[0], b);
   if (t == 0 && a.kept_out) a.kept_out[0] = kept;
-  finish(a, int(a.ids[kPasses & 1][pos]));
+  finish(a, tie_fixup(a, eqw, pos, b));
 }
 
 // ---------------------------------------------------------------- host side
 struct SLayout {
-  size_t keys0, keys1, ids0, ids1, hist, table, tmax, lsum, bytes;
+  size_t lg, ex, pr, sp, keys0, keys1, ids0, ids1, hist, table, tmax, lsum, eqw, pre, bytes;
 };
 
 constexpr size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
@@ -789,15 +945,21 @@ constexpr size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 constexpr SLayout slayout(int V) {
   SLayout s{};
   const size_t arr = align256(size_t(V) * sizeof(uint32_t));
-  s.keys0 = 0;
-  s.keys1 = arr;
-  s.ids0 = 2 * arr;
-  s.ids1 = 3 * arr;
-  s.hist = 4 * arr;
+  s.lg = 0;
+  s.ex = arr;
+  s.pr = 2 * arr;
+  s.sp = 3 * arr;
+  s.keys0 = 4 * arr;
+  s.keys1 = 5 * arr;
+  s.ids0 = 6 * arr;
+  s.ids1 = 7 * arr;
+  s.hist = 8 * arr;
   s.table = s.hist + align256(size_t(kPasses) * kHistWords * sizeof(uint32_t));
   s.tmax = s.table + align256(size_t(3) * (kVMax / 64) * sizeof(int));
   s.lsum = s.tmax + align256(size_t(kMaxTiles) * sizeof(float));
-  s.bytes = s.lsum + size_t(kVMax / kRedChunk) * 256 * sizeof(float);
+  s.eqw = s.lsum + align256(size_t(kVMax / kRedChunk) * 256 * sizeof(float));
+  s.pre = s.eqw + align256(size_t(kVMax / 32) * sizeof(uint32_t));
+  s.bytes = s.pre + size_t(kVMax / kPwBlock) * sizeof(float);
   return s;
 }
 
@@ -846,6 +1008,12 @@ static int32_t sample_impl(const float* logits, int32_t vocab, double temperatur
   a.token_out = token_out;
   a.probs_out = probs_out;
   a.kept_out = kept_out;
+  a.lg = reinterpret_cast<float*>(ws + L.lg);
+  a.ex = reinterpret_cast<float*>(ws + L.ex);
+  a.pr = reinterpret_cast<float*>(ws + L.pr);
+  a.sp = reinterpret_cast<float*>(ws + L.sp);
+  a.eqw = reinterpret_cast<uint32_t*>(ws + L.eqw);
+  a.pre = reinterpret_cast<float*>(ws + L.pre);
   a.keys[0] = reinterpret_cast<uint32_t*>(ws + L.keys0);
   a.keys[1] = reinterpret_cast<uint32_t*>(ws + L.keys1);
   a.ids[0] = reinterpret_cast<uint32_t*>(ws + L.ids0);
@@ -870,26 +1038,26 @@ static int32_t sample_impl(const float* logits, int32_t vocab, double temperatur
   }
   const int ntiles = (vocab + kTile - 1) / kTile;
   const int nbuf = (vocab + kRedChunk - 1) / kRedChunk;
+  const bool nuc = a.mode == kNucleus;
+  a.ntiles = ntiles;
+  a.nleaf = (nbuf * kSlots + kLeafWaves - 1) / kLeafWaves;
+  // the nucleus' first two radix passes ride in the leaf and normalisation launches
   hipLaunchKernelGGL(sample_max_kernel, dim3(ntiles), dim3(kTile), 0, s, a);
-  hipLaunchKernelGGL(sample_leaf_kernel, dim3((nbuf * kSlots + kLeafWaves - 1) / kLeafWaves), dim3(64 * kLeafWaves), 0, s,
-                     a);
-  hipLaunchKernelGGL(sample_norm_kernel, dim3(ntiles), dim3(kTile), 0, s, a);
+  hipLaunchKernelGGL(sample_leaf_kernel, dim3(a.nleaf + (nuc ? ntiles : 0)), dim3(64 * kLeafWaves), 0, s, a);
+  hipLaunchKernelGGL(sample_norm_kernel, dim3(nuc ? 2 * ntiles : ntiles), dim3(kNormThreads), 0, s, a);
   if (hipGetLastError() != hipSuccess) return MSD_E_HIP;
-  if (a.mode == kFull) {
+  if (!nuc) {
     hipLaunchKernelGGL(sample_full_kernel, dim3(1), dim3(kT), kLdsBig, s, a);
     return hipGetLastError() == hipSuccess ? MSD_OK : MSD_E_HIP;
   }
-  {
-    for (int p = 0; p < kPasses; ++p) {
-      hipLaunchKernelGGL(sample_radix_kernel, dim3(ntiles), dim3(kTileThreads), 0, s, a, p);
-      if (hipGetLastError() != hipSuccess) return MSD_E_HIP;
-    }
-    hipLaunchKernelGGL(sample_table_kernel, dim3(std::max(1, (vocab / 64 + kTabChunks - 1) / kTabChunks)), dim3(kT), 0, s,
-                       a);
-    if (hipGetLastError() != hipSuccess) return MSD_E_HIP;
-    hipLaunchKernelGGL(sample_nucleus_kernel, dim3(1), dim3(kT), kLdsBig, s, a);
+  for (int p = 2; p < kPasses; ++p) {
+    hipLaunchKernelGGL(sample_radix_kernel, dim3(ntiles), dim3(kTileThreads), 0, s, a, p);
     if (hipGetLastError() != hipSuccess) return MSD_E_HIP;
   }
+  hipLaunchKernelGGL(sample_table_kernel, dim3(((vocab + 63) / 64 + kTabChunks - 1) / kTabChunks), dim3(kT), 0, s, a);
+  if (hipGetLastError() != hipSuccess) return MSD_E_HIP;
+  hipLaunchKernelGGL(sample_nucleus_kernel, dim3(1), dim3(kT), kLdsBig, s, a);
+  if (hipGetLastError() != hipSuccess) return MSD_E_HIP;
   return MSD_OK;
 }
 
