@@ -200,7 +200,7 @@ int32_t msd_sample_token(const float* logits, int32_t vocab, double temperature,
                          void* workspace, void* stream);
 
 /* msd_sample_token without a workspace argument: the scratch lives in a static device array
- * of the library (one per device, 796,928 bytes, held until the process ends; sized for the
+ * of the library (one per device, 1,326,336 bytes, held until the process ends; sized for the
  * largest vocabulary, so vocab <= 32768 and MSD_E_CONFIG beyond).  No counterpart in the
  * reference: it is for callers that cannot allocate device memory (code under HIP graph
  * capture, tight serving loops, harnesses that forbid hipMalloc).  It calls no allocating

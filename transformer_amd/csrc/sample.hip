@@ -16,19 +16,29 @@
 //   * RandomState.choice(keep, p=filtered) on a supplied uniform u (generate.py:62-65):
 //     searchsorted(cdf / cdf[-1], u, 'right') with cdf the float64 cumulative sum.
 //
+// The sort runs on the penalised logits instead of the probabilities, so it can start in the
+// first kernel: a probability is a nondecreasing function of its logit, so the sorted sequence of
+// probability values (and with it the cutoff, the sums and the drawn position) is the same; only
+// ids of equal probability can come out in a different order, and the draw maps its position to
+// the right id of such a run afterwards (tie_fixup).
+//
 // Kernels, all on the caller's stream:
 //   sample_greedy_kernel   temperature 0: argmax of the penalised logits (1 workgroup)
-//   sample_max_kernel      512 ids per workgroup: penalised, scaled logits and their maxima
+//   sample_max_kernel      512 ids per workgroup: penalised, scaled logits and their maxima;
+//                          nucleus: the sort keys (logit order) and first digit counts
 //   sample_leaf_kernel     one wave per leaf of numpy's pairwise sum (<= 128 ids): correctly
-//                          rounded exponentials and the leaf's sum
-//   sample_norm_kernel     512 ids per workgroup: the pairwise trees over the leaf sums,
-//                          normalisation, radix keys, first digit counts
+//                          rounded exponentials and the leaf's sum; nucleus: radix pass 0 in
+//                          workgroups of its own
+//   sample_norm_kernel     512 ids per workgroup: the pairwise trees over the leaf sums and the
+//                          normalisation; nucleus: radix pass 1 in workgroups of its own
 //   sample_full_kernel     top_p >= 1: inverse CDF over all ids (1 workgroup)
-//   sample_radix_kernel    4 stable LSD passes of 8 bits over (probability bits, id), tiles of
-//                          512 entries per workgroup; each pass counts the next pass's digits
+//   sample_radix_kernel    passes 2 and 3 of the stable LSD sort (8 bits each) of (logit key, id),
+//                          tiles of 512 entries per workgroup; each pass counts the next pass's
+//                          digits, the last writes the probabilities in sorted order
 //   sample_table_kernel    per 64-entry chunk of the sorted probabilities: exact ulp totals for
-//                          the cumsum walk
-//   sample_nucleus_kernel  1 workgroup: the cumsum cutoff walk, renormalisation and draw
+//                          the cumsum walk, equal-neighbour bits, pairwise leaves of full buffers
+//   sample_nucleus_kernel  1 workgroup: the cumsum cutoff walk, renormalisation, draw and the
+//                          id of the drawn position
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <math.h>
