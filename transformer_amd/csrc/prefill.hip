@@ -1403,25 +1403,26 @@ static int32_t launch_graphed(const std::vector<char>& key, hipStream_t s, F&& b
     hipGraph_t g = nullptr;
     const hipError_t ec = hipStreamEndCapture(cap, &g);
     if (rc != MSD_OK || ec != hipSuccess) {
-      if (g) hipGraphDestroy(g);
+      if (g) (void)hipGraphDestroy(g);
       (void)hipGetLastError();
       return rc != MSD_OK ? rc : MSD_E_HIP;
     }
     hipGraphExec_t ex = nullptr;
     const hipError_t ei = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
-    hipGraphDestroy(g);
+    (void)hipGraphDestroy(g);
     if (ei != hipSuccess) return MSD_E_HIP;
     hipEvent_t ev = nullptr;
     if (hipEventCreateWithFlags(&ev, hipEventDisableTiming) != hipSuccess) {
-      hipGraphExecDestroy(ex);
+      (void)hipGraphExecDestroy(ex);
       return MSD_E_HIP;
     }
     if (cache.size() >= kGraphCache) {
       auto lru = std::min_element(cache.begin(), cache.end(),
                                   [](const GraphEntry& a, const GraphEntry& b) { return a.used < b.used; });
-      hipEventSynchronize(lru->done);
-      hipGraphExecDestroy(lru->exec);
-      hipEventDestroy(lru->done);
+      // cleanup of an evicted entry: its failures leave nothing to undo
+      (void)hipEventSynchronize(lru->done);
+      (void)hipGraphExecDestroy(lru->exec);
+      (void)hipEventDestroy(lru->done);
       cache.erase(lru);
     }
     cache.push_back(GraphEntry{key, dev, ex, ev, 0});
