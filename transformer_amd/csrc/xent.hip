@@ -191,7 +191,9 @@ __device__ __forceinline__ void piece_offsets_(uint32_t (&off)[N], int row, int 
 // ---- direct-to-LDS pipeline (XENT_DMA): K advances 32 at a time through a ring of 4 LDS stages,
 // three in flight.  Each lane's global_load_lds writes 16 bytes at (stage base + 1 KB per
 // instruction + 16 lane); a stage row is 64 bytes (4 pieces of 8 K values) and holds piece c at
-// position c ^ ((row >> 1) & 3), so the 8 rows one read phase touches cover all 32 banks.  The
+// position c ^ ((row >> 2) & 3).  Measured with a probe of ds_read_b128 address patterns
+// (SQ_LDS_BANK_CONFLICT): the fragment read of 32 rows x one piece is conflict-free with this
+// swizzle and takes twice the LDS cycles with c ^ ((row >> 1) & 3) or with no swizzle.  The
 // fragment reads are inline assembly with explicit waits: the compiler would otherwise wait for
 // every outstanding DMA (vmcnt(0)) before each LDS read, and __syncthreads' fence would too, so
 // the stage barrier is a bare s_barrier after this wave's own DMAs of the stage have landed.
@@ -371,7 +373,7 @@ __global__ __launch_bounds__(64 * GM * GN) void xent_gemm(GemmArgs g) {
 #pragma unroll
     for (int u = 0; u < NIW; ++u) {
       const int r = 16 * (wv + NW * u) + (lane >> 2) - (u < UA ? 0 : TM);
-      const int piece = (lane & 3) ^ ((r >> 1) & 3);
+      const int piece = (lane & 3) ^ ((r >> 2) & 3);
       doff[u] = u < UA ? uint32_t(min(row0 + r, g.a_valid - 1)) * uint32_t(g.lda) + 8 * piece
                        : uint32_t(min(col0 + r, g.b_valid - 1)) * uint32_t(g.ldb) + 8 * piece;
     }
@@ -379,7 +381,7 @@ __global__ __launch_bounds__(64 * GM * GN) void xent_gemm(GemmArgs g) {
     for (int s = 0; s < 3 && s < KT; ++s) dma_stage<NIW, UA, NW>(g.A, g.B, doff, s, smem + s * SD, wv);
     // this lane's fragment rows and swizzled pieces (the swizzle depends only on fr)
     const uint32_t base = lds_addr(smem);
-    const uint32_t sw0 = ((0 + fh) ^ ((fr >> 1) & 3)) << 4, sw1 = ((2 + fh) ^ ((fr >> 1) & 3)) << 4;
+    const uint32_t sw0 = ((0 + fh) ^ ((fr >> 2) & 3)) << 4, sw1 = ((2 + fh) ^ ((fr >> 2) & 3)) << 4;
     const uint32_t ar = (wm * WM + fr) * 64, br = TM * 64 + (wn * WN + fr) * 64;
     for (int kt = 0; kt < KT; ++kt) {
       if (kt + 2 < KT)
