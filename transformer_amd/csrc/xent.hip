@@ -131,6 +131,17 @@ struct GemmArgs {
 #define XENT_DMA 1
 #endif
 
+// Stages of the LDS ring: as many (TM + TN) x 64-byte stages as 160 KB holds, at most kMaxStages;
+// S - 1 stages are in flight while one is read.  (Measured: 5 stages for the 256 x 256 tiles and 8
+// for the 128 x 128 ones were no faster than 4 -- the operand latency is already covered.)
+#ifndef XENT_MAX_STAGES
+#define XENT_MAX_STAGES 4
+#endif
+constexpr int kMaxStages = XENT_MAX_STAGES;
+template <int TM, int TN>
+constexpr int ring_stages() {
+  return std::min(kMaxStages, (160 * 1024) / ((TM + TN) * 64));
+}
 template <int TM, int TN>
 constexpr int stage_bytes() { return (TM + TN) * kBK * 2; }
 template <int TM, int TN>
@@ -138,7 +149,7 @@ constexpr int staging_pitch() { return TN + 8; }   // bf16 per row of the epilog
 template <int TM, int TN, int EPI>
 constexpr size_t lds_bytes() {
 #if XENT_DMA
-  constexpr size_t ring = size_t(4) * (TM + TN) * 64;
+  constexpr size_t ring = size_t(ring_stages<TM, TN>()) * (TM + TN) * 64;
   return EPI == kEpiProb ? std::max<size_t>(ring, size_t(TM) * staging_pitch<TM, TN>() * 2 + TN * 8) : ring;
 #endif
   // kEpiProb: the bf16 staging tile (over the stage buffers) and the rows' lse and targets after it
@@ -188,8 +199,8 @@ __device__ __forceinline__ void piece_offsets_(uint32_t (&off)[N], int row, int 
   ((off[U] = uint32_t(min(row + R * int(U), valid - 1)) * uint32_t(ld) + col), ...);
 }
 
-// ---- direct-to-LDS pipeline (XENT_DMA): K advances 32 at a time through a ring of 4 LDS stages,
-// three in flight.  Each lane's global_load_lds writes 16 bytes at (stage base + 1 KB per
+// ---- direct-to-LDS pipeline (XENT_DMA): K advances 32 at a time through a ring of S LDS stages,
+// S - 1 in flight.  Each lane's global_load_lds writes 16 bytes at (stage base + 1 KB per
 // instruction + 16 lane); a stage row is 64 bytes (4 pieces of 8 K values) and holds piece c at
 // position c ^ ((row >> 2) & 3).  Measured with a probe of ds_read_b128 address patterns
 // (SQ_LDS_BANK_CONFLICT): the fragment read of 32 rows x one piece is conflict-free with this
@@ -198,7 +209,6 @@ __device__ __forceinline__ void piece_offsets_(uint32_t (&off)[N], int row, int 
 // every outstanding DMA (vmcnt(0)) before each LDS read, and __syncthreads' fence would too, so
 // the stage barrier is a bare s_barrier after this wave's own DMAs of the stage have landed.
 constexpr int kKD = 32;   // K per DMA stage
-constexpr int kStages = 4;
 typedef __attribute__((address_space(3))) uint8_t lds_u8;
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return uint32_t(reinterpret_cast<uintptr_t>((const lds_u8*)p));
@@ -211,6 +221,19 @@ __device__ __forceinline__ void wait_vm() {
 #if defined(__HIP_DEVICE_COMPILE__)
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 #endif
+}
+// Wait until at most n (< D, wave-uniform) stages of NIW DMA instructions are outstanding.
+template <int NIW, int D>
+__device__ __forceinline__ void wait_stages(int n) {
+  if constexpr (D > 1) {
+    if (n >= D - 1) {
+      wait_vm<(D - 1) * NIW>();
+      return;
+    }
+    wait_stages<NIW, D - 1>(n);
+  } else {
+    wait_vm<0>();
+  }
 }
 // The fragment reads of one K step (16) of a DMA stage: fa[i] is the A fragment of row block i
 // at a + 2048 i (32 rows of 64 bytes apart), fb[j] the B fragment at b + 2048 j.  The reads are
@@ -366,7 +389,8 @@ __global__ __launch_bounds__(64 * GM * GN) void xent_gemm(GemmArgs g) {
   {
     constexpr int NW = GM * GN, SD = (TM + TN) * 64, NI = (TM + TN) / 16, NIW = NI / NW, UA = TM / (16 * NW);
     static_assert(NI % NW == 0 && TM % (16 * NW) == 0, "whole DMA instructions per wave, A before B");
-    static_assert(kStages * SD <= 160 * 1024, "LDS ring");
+    constexpr int S = ring_stages<TM, TN>(), D = S - 1;
+    static_assert(S >= 2 && S * SD <= 160 * 1024, "LDS ring");
     // instruction u of this wave covers stage rows 16 (wv + NW u) .. + 16: A rows for u < UA, then
     // B rows; this lane's row of it and the K piece it loads into position lane % 4
     uint32_t doff[NIW];
@@ -378,22 +402,20 @@ __global__ __launch_bounds__(64 * GM * GN) void xent_gemm(GemmArgs g) {
                        : uint32_t(min(col0 + r, g.b_valid - 1)) * uint32_t(g.ldb) + 8 * piece;
     }
     const int KT = g.K / kKD;
-    for (int s = 0; s < 3 && s < KT; ++s) dma_stage<NIW, UA, NW>(g.A, g.B, doff, s, smem + s * SD, wv);
+    for (int s = 0; s < D && s < KT; ++s) dma_stage<NIW, UA, NW>(g.A, g.B, doff, s, smem + s * SD, wv);
     // this lane's fragment rows and swizzled pieces (the swizzle depends only on fr)
     const uint32_t base = lds_addr(smem);
     const uint32_t sw0 = ((0 + fh) ^ ((fr >> 2) & 3)) << 4, sw1 = ((2 + fh) ^ ((fr >> 2) & 3)) << 4;
     const uint32_t ar = (wm * WM + fr) * 64, br = TM * 64 + (wn * WN + fr) * 64;
+    int rd = 0;   // ring slot of stage kt; stage kt + D goes to the slot stage kt - 1 used
     for (int kt = 0; kt < KT; ++kt) {
-      if (kt + 2 < KT)
-        wait_vm<2 * NIW>();
-      else if (kt + 1 < KT)
-        wait_vm<NIW>();
-      else
-        wait_vm<0>();
+      wait_stages<NIW, D>(min(KT, kt + D) - kt - 1);   // stage kt landed
       __builtin_amdgcn_s_barrier();   // every wave's part of stage kt landed; stage kt - 1 read by all
-      if (kt + 3 < KT) dma_stage<NIW, UA, NW>(g.A, g.B, doff, kt + 3, smem + ((kt + 3) & (kStages - 1)) * SD, wv);
-      const uint32_t sb = base + (kt & (kStages - 1)) * SD;
+      const int is = rd == 0 ? S - 1 : rd - 1;
+      if (kt + D < KT) dma_stage<NIW, UA, NW>(g.A, g.B, doff, kt + D, smem + is * SD, wv);
+      const uint32_t sb = base + rd * SD;
       mma_stage_dma<TM, RB, CB>(acc, sb + ar + sw0, sb + ar + sw1, sb + br + sw0, sb + br + sw1);
+      rd = rd == S - 1 ? 0 : rd + 1;
     }
     __builtin_amdgcn_s_barrier();   // the epilogue reuses the ring
   }
