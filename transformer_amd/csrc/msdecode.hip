@@ -381,15 +381,20 @@ __device__ __forceinline__ void poll_words(const uint64_t* src, int n, uint32_t 
 
 // LDS position of element e of a K-long vector in the lane-major order of the row dot
 // products: in block b of 512 (the last block holds S = 8m elements, m lanes), element
-// 512b + q m + l sits at 512b + 8l + q, so lane l reads its 8 inputs of a block as two
-// 16-byte pieces (the order of the kernel row layout's packed weights).
+// 512b + q m + l sits in lane l's 32 bytes at 512b + 8l, so lane l reads its 8 inputs of a block
+// as two 16-byte pieces (the order of the kernel row layout's packed weights).  Lanes with bit 3
+// set keep their two halves swapped (q at 8l + (q ^ 4)) and read the upper one first: the first
+// read of lanes 0-7 then covers the even 16-byte bank groups and that of lanes 8-15 the odd ones.
+// Measured with a probe of ds_read_b128 patterns (SQ_LDS_BANK_CONFLICT): reading 32-byte lane
+// segments half by half takes twice the LDS cycles without the swap, none extra with it.
 template <int K>
 __device__ __forceinline__ int lane_major(int e) {
   const int b = e >> 9, r = e & 511;
   constexpr int mt = (K % 512) / 8;   // lanes of a short last block
   const int m = (mt > 0 && b == K / 512) ? mt : 64;
   const int q = m == 64 ? (r >> 6) : r / m;
-  return (b << 9) + 8 * (r - q * m) + q;
+  const int l = r - q * m;
+  return (b << 9) + 8 * l + (q ^ (((l >> 3) & 1) << 2));
 }
 
 // Gather n tagged words src[0..n) into dst (LDS floats), NW waves sharing the words; with
@@ -524,8 +529,9 @@ __device__ __forceinline__ void load_x(XV<NL>& xv, const float* x, int k, int la
 #pragma unroll
   for (int j = 0; j < NL; ++j) {
     const int m = block_lanes(k, j);
+    const int sw = (lane >> 3) & 1;   // this lane's halves are stored swapped (lane_major)
     const float4* p = reinterpret_cast<const float4*>(x + 512 * j + 8 * (lane < m ? lane : 0));
-    const float4 a = p[0], b = p[1];
+    const float4 a = p[sw], b = p[1 - sw];
     const bool on = lane < m;
     xv.v[j][0] = on ? a.x : 0.f;
     xv.v[j][1] = on ? a.y : 0.f;
