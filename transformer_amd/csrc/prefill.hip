@@ -324,7 +324,10 @@ template <int CT, int P, int AM, bool TW, int EPI, int RT = 1>
 __global__ __launch_bounds__(256) void mx_gemm_rows(GemmArgs g) {
   static_assert(RT == 1 || (AM >= 1 && TW && (EPI == kEpiSwiglu || EPI == kEpiQkv)),
                 "two row tiles per workgroup: tile-order operands and a pair epilogue");
-  __shared__ f32x4 red[4][RT][CT][64];
+  // the waves' partial tiles, element r of lane l's D registers at [r][l]: the epilogue reads
+  // them across lanes contiguously (read as [l][r], 16 bytes apart, they took 2-4 times the LDS
+  // cycles: SQ_LDS_BANK_CONFLICT)
+  __shared__ float red[4][RT][CT][4][64];
   __shared__ float rrms[16 * RT];   // AM 2: each row's rms
   // wave-uniform wave index: the step count and its loop stay scalar (a per-lane loop would copy
   // the accumulators out of and back into the AGPRs around every step)
@@ -406,7 +409,9 @@ __global__ __launch_bounds__(256) void mx_gemm_rows(GemmArgs g) {
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-    for (int ct = 0; ct < CT; ++ct) red[wv][rt][ct][lane] = acc[rt][ct];
+    for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) red[wv][rt][ct][r][lane] = acc[rt][ct][r];
   if constexpr (AM == 2) {   // row 16 rt + tid / 16's sum of h^2 over its nssq <= 64 partials, in a fixed order
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
@@ -428,7 +433,7 @@ __global__ __launch_bounds__(256) void mx_gemm_rows(GemmArgs g) {
     float hsq = 0.f;
     for (int idx = threadIdx.x; idx < CT * 256; idx += 256) {
       const int ct = idx >> 8, e = idx & 255, r = e >> 6, l = e & 63;
-      float v = ((red[0][0][ct][l][r] + red[1][0][ct][l][r]) + red[2][0][ct][l][r]) + red[3][0][ct][l][r];
+      float v = ((red[0][0][ct][r][l] + red[1][0][ct][r][l]) + red[2][0][ct][r][l]) + red[3][0][ct][r][l];
       if constexpr (AM == 2) v = v / rrms[4 * (l >> 4) + r];
       const int row = m0 + 4 * (l >> 4) + r, col = n0 + 16 * ct + (l & 15);
       float* o = g.out + (EPI == kEpiStore ? int64_t(row) * g.ldo + col : act_index(row, col, g.N, 0));
@@ -458,9 +463,9 @@ __global__ __launch_bounds__(256) void mx_gemm_rows(GemmArgs g) {
     for (int idx = threadIdx.x; idx < RT * CT * 128; idx += 256) {
       const int tc = idx >> 7, rt = tc / CT, ct = tc % CT, e = idx & 127, r = e >> 5,
                 l = 16 * ((e >> 3) & 3) + 2 * (e & 7);
-      float v0 = ((red[0][rt][ct][l][r] + red[1][rt][ct][l][r]) + red[2][rt][ct][l][r]) + red[3][rt][ct][l][r];
-      float v1 = ((red[0][rt][ct][l + 1][r] + red[1][rt][ct][l + 1][r]) + red[2][rt][ct][l + 1][r]) +
-                 red[3][rt][ct][l + 1][r];
+      float v0 = ((red[0][rt][ct][r][l] + red[1][rt][ct][r][l]) + red[2][rt][ct][r][l]) + red[3][rt][ct][r][l];
+      float v1 = ((red[0][rt][ct][r][l + 1] + red[1][rt][ct][r][l + 1]) + red[2][rt][ct][r][l + 1]) +
+                 red[3][rt][ct][r][l + 1];
       if constexpr (AM == 2) {
         v0 = v0 / rrms[16 * rt + 4 * (l >> 4) + r];
         v1 = v1 / rrms[16 * rt + 4 * (l >> 4) + r];
