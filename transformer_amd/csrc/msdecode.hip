@@ -88,8 +88,11 @@ constexpr int kDh = 64;          // head dimension (fixed)
 constexpr int kPart = 66;        // per (head, split): m, l, o[64]
 constexpr int kAttCap = 512;     // cached positions an attention workgroup holds in LDS
 constexpr int kMaxCtx = 2048;    // context: at most 4 splits of kAttCap positions per head
-constexpr int kKRowB = 144;      // LDS bytes per cached K row: 128 + 16 padding, so 16-byte
-                                 // reads of consecutive rows by consecutive lanes never conflict
+constexpr int kKRowB = 160;      // LDS bytes per cached K row: 128 + 32 padding.  The score tiles
+                                 // read 16 bytes of 16 consecutive rows per lane group: with a
+                                 // 144-byte pitch that took twice the LDS cycles (a probe of the
+                                 // pattern under SQ_LDS_BANK_CONFLICT), with 160 none extra
+constexpr int kKSlots = kKRowB / 16;   // 16-byte DMA slots per K row (those past 8 repeat the 8th)
 constexpr int kVRowB = 128;      // LDS bytes per cached V row
 constexpr uint32_t kSpinLimit = 1u << 20;
 
@@ -1145,17 +1148,17 @@ struct AttCtx {
 };
 
 // Loader wave of an attention workgroup: per layer, once every attention wave has
-// finished with the previous layer's rows, DMA this split's cached K rows (9 slots of
-// 16 bytes per row; the 9th is padding) and V rows (8 slots) into LDS.
+// finished with the previous layer's rows, DMA this split's cached K rows (kKSlots slots of
+// 16 bytes per row; those past the 8th are padding) and V rows (8 slots) into LDS.
 template <class DMA>
 __device__ __forceinline__ void att_copy(DMA& d, const Args& a, const AttCtx& c, int l, int lo, int ncached) {
   const int lane = c.lane;
   const uint16_t* kc = layer_k(a, l) + (int64_t(c.g) * a.ctx + lo) * kDh;
   const uint16_t* vc = kc + int64_t(a.KV) * a.ctx * kDh;
-  const int nk = cdiv(ncached * 9, 64);
+  const int nk = cdiv(ncached * kKSlots, 64);
   for (int t = 0; t < nk; ++t) {
     const int i = 64 * t + lane;
-    const int r = min(i / 9, ncached - 1), p = min(i % 9, 7);
+    const int r = min(i / kKSlots, ncached - 1), p = min(i % kKSlots, 7);
     d.issue(kc + r * kDh + p * 8, c.K + t * 1024);
   }
   const int nv = cdiv(ncached, 8);
@@ -1168,14 +1171,15 @@ __device__ __forceinline__ void att_copy(DMA& d, const Args& a, const AttCtx& c,
 }
 
 // One more cached row, row `r` of this split (whose rows 0 .. r - 1 att_copy has placed), to its
-// place after them: K at 144 r (lanes 0..8, one 16-byte slot each, the 9th repeating the 8th)
-// and V at 128 r (lanes 0..7).  Issued after att_copy's drain, so these writes land last.
+// place after them: K at kKRowB r (lanes 0..kKSlots-1, one 16-byte slot each, those past the 8th
+// repeating it) and V at 128 r (lanes 0..7).  Issued after att_copy's drain, so these writes land
+// last.
 template <class DMA>
 __device__ __forceinline__ void att_copy_row(DMA& d, const Args& a, const AttCtx& c, int l, int lo, int r) {
   const int lane = c.lane;
   const uint16_t* kc = layer_k(a, l) + (int64_t(c.g) * a.ctx + lo + r) * kDh;
   const uint16_t* vc = kc + int64_t(a.KV) * a.ctx * kDh;
-  if (lane < 9) d.issue(kc + min(lane, 7) * 8, c.K + 144 * r);
+  if (lane < kKSlots) d.issue(kc + min(lane, 7) * 8, c.K + kKRowB * r);
   if (lane < 8) d.issue(vc + lane * 8, c.V + 128 * r);
   d.drain();
 }
@@ -1516,7 +1520,7 @@ __global__ __launch_bounds__(kThreadsWG, 1) void decode_step_kernel(Args a) {
     c.wv = wv;
     c.part = a.nsplit == 1 ? int64_t(c.h) * kDh : int64_t(item) * kPart;
     c.K = smem;
-    c.V = c.K + cdiv(a.cap * 9, 64) * 1024;
+    c.V = c.K + cdiv(a.cap * kKSlots, 64) * 1024;
     c.apw = reinterpret_cast<uint16_t*>(c.V + cdiv(a.cap, 8) * 1024);
     c.pw = reinterpret_cast<float*>(c.apw + kWavesA * 3 * kDh);
     c.ow = c.pw + kWavesA * kDh;
@@ -1677,7 +1681,7 @@ static bool make_plan(const msd_config* c, int G, Plan* p) {
   // more than two splits: the partials alias xhd1 | xhd2 | xact (2 D + d_ff floats)
   if (p->nsplit > 2 && natt > 2 * D + ff) return false;
   const int row_other = 4 * (3 * D + ((ff + 3) & ~3) + (p->nsplit > 2 ? 0 : ((natt + 3) & ~3)) + 8 + 2 * kWavesR);
-  const int att_lds = cdiv(p->cap * 9, 64) * 1024 + cdiv(p->cap, 8) * 1024 +
+  const int att_lds = cdiv(p->cap * kKSlots, 64) * 1024 + cdiv(p->cap, 8) * 1024 +
                       2 * 3 * kWavesA * kDh + 4 * (3 * kWavesA * kDh + 4 * kWavesA + 4);
   const int budget = std::max(std::max(att_lds, kMinLds), ring + row_other);
   ring = std::max(ring, (budget - row_other) / 2048 * 2048);   // spare LDS widens the logit halves
