@@ -1144,7 +1144,10 @@ struct AttCtx {
   float* ow;        // [2][kWavesA][64] block outputs (double-buffered by layer parity)
   float* mw;        // [2][kWavesA] block maxima
   float* lw;        // [2][kWavesA] block sums
-  int* ctr;         // [0] wave sync, [1] KV layers loaded, [2] KV layers consumed (wave bumps)
+  float* kvl;       // [2][2][64] the current position's k and v (double-buffered by layer parity)
+  int* ctr;         // [0] wave sync, [1] KV layers loaded, [2] KV layers consumed (wave bumps),
+                    // [3] layers whose current k and v are in kvl, [4] layers whose q wave 0 has
+                    // received
 };
 
 // Loader wave of an attention workgroup: per layer, once every attention wave has
@@ -1224,6 +1227,27 @@ __device__ void att_loader(const Args& a, const AttCtx& c) {
       }
       lds_set(c.ctr + 1, gl + 1, lane);
       MSD_TRACE_POINT(true, l, 28);
+      if (c.has_cur) {
+        // the current position's k and v of layer l for the waves' merge, polled once q of the
+        // layer has arrived (they are posted with it) while the waves take the cached blocks
+        lds_wait(c.ctr + 4, gl + 1, a.ctrl);
+        const uint32_t tag = a.epoch + uint32_t(st);
+        const uint64_t* ks = layer_x(a, l) + a.lay.x_qkv + (a.H + c.g) * kDh + lane;
+        const uint64_t* vs = layer_x(a, l) + a.lay.x_qkv + (a.H + a.KV + c.g) * kDh + lane;
+        uint64_t kw = ld_tag(ks), vw = ld_tag(vs);
+        uint32_t spins = 0;
+        while (!bad) {
+          const bool kok = uint32_t(kw >> 32) == tag, vok = uint32_t(vw >> 32) == tag;
+          if (__all(kok && vok)) break;
+          if (!kok) kw = ld_tag(ks);
+          if (!vok) vw = ld_tag(vs);
+          spin_step(spins, a.ctrl, lane, bad);
+        }
+        float* kv = c.kvl + (gl & 1) * 2 * kDh;
+        kv[lane] = __uint_as_float(uint32_t(kw));
+        kv[kDh + lane] = __uint_as_float(uint32_t(vw));
+        lds_set(c.ctr + 3, gl + 1, lane);
+      }
     }
   }
 }
@@ -1298,6 +1322,7 @@ __device__ void att_waves(const Args& a, const AttCtx& c) {
     float* lw = c.lw + (gl & 1) * kWavesA;
     float qv[1];
     poll_words<1, 1>(X + lay.x_qkv + c.h * kDh, kDh, tag, qv, a.ctrl, 0, lane, bad);
+    if (wv == 0 && c.has_cur) lds_set(c.ctr + 4, gl + 1, lane);   // the loader polls k and v now
     MSD_TRACE_POINT(wv == 0, l, 24);
     MSD_TRACE_WAVE(l, 0);
     {   // q = hi + mid + lo exactly, three bf16 parts taken by truncation (each holds the next
@@ -1312,23 +1337,9 @@ __device__ void att_waves(const Args& a, const AttCtx& c) {
       apw[kDh + lane] = uint16_t(mb >> 16);
       apw[2 * kDh + lane] = uint16_t(lb >> 16);
     }
-    // new k and v of the KV head: first loads now (they land during the block work), the
-    // rest of the poll after it
-    const uint64_t* kvsrc[2] = {X + lay.x_qkv + (a.H + c.g) * kDh + lane, X + lay.x_qkv + (a.H + a.KV + c.g) * kDh + lane};
-    uint64_t kvw[2] = {uint64_t(tag) << 32, uint64_t(tag) << 32};
-    if (c.has_cur) {
-      kvw[0] = ld_tag(kvsrc[0]);
-      kvw[1] = ld_tag(kvsrc[1]);
-    }
     lds_wait(c.ctr + 1, gl + 1, a.ctrl);   // cached rows of layer l are in LDS
     MSD_TRACE_POINT(wv == 0, l, 25);
     MSD_TRACE_WAVE(l, 1);
-    // a second load of k and v issued before the block work, consumed after the scores
-    uint64_t kvx[2] = {0, 0};
-    if (c.has_cur) {
-      kvx[0] = ld_tag(kvsrc[0]);
-      kvx[1] = ld_tag(kvsrc[1]);
-    }
     // block of this wave: tiles [t0, t1) of 16 cached positions, the tiles split evenly over
     // the waves (at most 4 each: ncached <= 512); waves w and w + 4 share a SIMD, and the
     // even split keeps every SIMD's tile count within one of the others'
@@ -1383,14 +1394,6 @@ __device__ void att_waves(const Args& a, const AttCtx& c) {
       }
       MSD_TRACE_POINT(wv == 0, l, 29);
       MSD_TRACE_WAVE(l, 2);
-      // k or v not there at the first load: load again now, so the final check after P.V
-      // rarely needs another round trip
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-        if (uint32_t(kvw[i] >> 32) != tag) {
-          if (uint32_t(kvx[i] >> 32) == tag) kvw[i] = kvx[i];
-          else kvw[i] = ld_tag(kvsrc[i]);
-        }
       __builtin_amdgcn_s_waitcnt(0xc07f);
       __builtin_amdgcn_wave_barrier();
       const int g = kb, dq = m16;
@@ -1439,21 +1442,14 @@ __device__ void att_waves(const Args& a, const AttCtx& c) {
       mw[wv] = m;
       lw[wv] = lsum;
     }
-    {
-      uint32_t spins = 0;
-      bool ok = false;
-      while (!bad && !__all(ok)) {
-        ok = true;
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-          if (uint32_t(kvw[i] >> 32) != tag) {
-            ok = false;
-            kvw[i] = ld_tag(kvsrc[i]);
-          }
-        if (!__all(ok)) spin_step(spins, a.ctrl, lane, bad);
-      }
+    // the current position's k and v, polled by the loader wave
+    float kv2[2] = {0.f, 0.f};
+    if (c.has_cur) {
+      lds_wait(c.ctr + 3, gl + 1, a.ctrl);
+      const float* kv = c.kvl + (gl & 1) * 2 * kDh;
+      kv2[0] = kv[lane];
+      kv2[1] = kv[kDh + lane];
     }
-    const float kv2[2] = {__uint_as_float(uint32_t(kvw[0])), __uint_as_float(uint32_t(kvw[1]))};
     // score of the current position (un-rounded k), taken while the other waves finish
     const float scur = c.has_cur ? wave_sum(qv[0] * kv2[0]) * 0.125f : -INFINITY;
     MSD_TRACE_WAVE(l, 4);
@@ -1526,8 +1522,9 @@ __global__ __launch_bounds__(kThreadsWG, 1) void decode_step_kernel(Args a) {
     c.ow = c.pw + kWavesA * kDh;
     c.mw = c.ow + 2 * kWavesA * kDh;
     c.lw = c.mw + 2 * kWavesA;
-    c.ctr = reinterpret_cast<int*>(c.lw + 2 * kWavesA);
-    if (threadIdx.x < 4) c.ctr[threadIdx.x] = 0;
+    c.kvl = c.lw + 2 * kWavesA;
+    c.ctr = reinterpret_cast<int*>(c.kvl + 4 * kDh);
+    if (threadIdx.x < 8) c.ctr[threadIdx.x] = 0;
     __syncthreads();   // the only workgroup barrier; the roles below meet on LDS counters
     if (wv == kLoader) att_loader<MULTI>(a, c);
     else if (wv < kWavesA) att_waves<MULTI>(a, c);
@@ -1682,7 +1679,7 @@ static bool make_plan(const msd_config* c, int G, Plan* p) {
   if (p->nsplit > 2 && natt > 2 * D + ff) return false;
   const int row_other = 4 * (3 * D + ((ff + 3) & ~3) + (p->nsplit > 2 ? 0 : ((natt + 3) & ~3)) + 8 + 2 * kWavesR);
   const int att_lds = cdiv(p->cap * kKSlots, 64) * 1024 + cdiv(p->cap, 8) * 1024 +
-                      2 * 3 * kWavesA * kDh + 4 * (3 * kWavesA * kDh + 4 * kWavesA + 4);
+                      2 * 3 * kWavesA * kDh + 4 * (3 * kWavesA * kDh + 4 * kWavesA + 4 * kDh + 8);
   const int budget = std::max(std::max(att_lds, kMinLds), ring + row_other);
   ring = std::max(ring, (budget - row_other) / 2048 * 2048);   // spare LDS widens the logit halves
   p->ring_bytes = ring;
