@@ -12,11 +12,12 @@
 //     idle device), so workgroups may wait on each other.
 //   * two kinds of workgroups:
 //       - row workgroups (all but the last H * nsplit) own fixed output rows of every
-//         projection and of the tied logits.  A loader wave streams this workgroup's rows
-//         by DMA (global_load_lds) into an LDS ring one layer ahead; 8 worker waves, all
+//         projection and of the tied logits.  A loader wave streams this workgroup's layer
+//         rows by DMA (global_load_lds) into an LDS ring one layer ahead; 8 worker waves, all
 //         alike, keep the residual stream h in registers, take the RMSNorms, the dot
 //         products of their rows from LDS, store the outputs and gather an eighth of the
-//         next input vector each;
+//         next input vector each; at the end they stream the logit rows straight into
+//         registers;
 //       - attention workgroups (one per query head and context split of 512 positions)
 //         hold their KV head's cached rows in LDS (bf16, streamed in by their loader wave
 //         during the previous layer); 8 attention waves poll the head's q, take the scores
@@ -111,20 +112,17 @@ constexpr int kRep = MSD_REPLICAS;   // replicas of every vector all row workgro
 static_assert((kRep % kWavesA == 0 || kRep < kWavesA) && kRep <= 64, "attention waves store whole sets of replicas");
 // 1 KB DMA instructions a loader keeps in flight.  Fewer bytes in flight across the device
 // shorten the round trip of the exchange polls; the layer weights and KV rows need only a
-// few per CU to stay a layer ahead, the logit rows at the end stream with a wide window.
+// few per CU to stay a layer ahead.
 #ifndef MSD_DMA_LAYER
 #define MSD_DMA_LAYER 8
 #endif
 #ifndef MSD_DMA_KV
 #define MSD_DMA_KV 16
 #endif
-#ifndef MSD_DMA_LOGITS
-#define MSD_DMA_LOGITS 48
-#endif
 #ifndef MSD_DMA_FIRST
 #define MSD_DMA_FIRST 32
 #endif
-constexpr int kDmaLayer = MSD_DMA_LAYER, kDmaKV = MSD_DMA_KV, kDmaLogits = MSD_DMA_LOGITS;
+constexpr int kDmaLayer = MSD_DMA_LAYER, kDmaKV = MSD_DMA_KV;
 // the first layer's rows load before any exchange traffic: a wider window
 constexpr int kDmaFirst = MSD_DMA_FIRST;
 
@@ -197,8 +195,8 @@ struct Args {
   int H, KV, L, ff, V, ctx;
   int nsplit, cap, NA, GR;   // attention splits, positions per split, attention / row workgroups
   // row workgroups: LDS ring regions (bytes) of the QKV, O, gate/up and down rows, the
-  // ring size, and logit rows per ring half
-  int ring_q, ring_o, ring_g, ring_d, ring_bytes, log_rows;
+  // ring size
+  int ring_q, ring_o, ring_g, ring_d, ring_bytes;
   int keep;   // layers whose rows are read with the caching policy (the rest stream)
   Layout lay;
 };
@@ -547,17 +545,11 @@ __device__ __forceinline__ void load_x(XV<NL>& xv, const float* x, int k, int la
   }
 }
 
-// Dot products of R rows (in LDS) with the lane's inputs: every 16-byte piece of every row
-// is read before the first multiply, then the R wave sums run interleaved.  Lanes past a
-// short last block read in-bounds LDS bytes beyond the row and zero them.
+// Dot products of R rows with the lane's inputs from the rows' 16-byte pieces w (lanes past a
+// short last block hold bytes beyond the row, zeroed here); the R wave sums run interleaved.
 template <int NL, int R>
-__device__ __forceinline__ void dot_rows(const uint8_t* const (&rows)[R], const XV<NL>& xv, int k, int lane,
-                                         float (&out)[R]) {
-  uint4 w[R][NL];
-#pragma unroll
-  for (int i = 0; i < R; ++i)
-#pragma unroll
-    for (int j = 0; j < NL; ++j) w[i][j] = *reinterpret_cast<const uint4*>(rows[i] + 1024 * j + 16 * lane);
+__device__ __forceinline__ void dot_frags(const uint4 (&w)[R][NL], const XV<NL>& xv, int k, int lane,
+                                          float (&out)[R]) {
 #pragma unroll
   for (int i = 0; i < R; ++i) {
     float acc = 0.f;
@@ -577,6 +569,46 @@ __device__ __forceinline__ void dot_rows(const uint8_t* const (&rows)[R], const 
     out[i] = acc;
   }
   wave_sum_n<R>(out);
+}
+
+// Dot products of R rows (in LDS) with the lane's inputs: every 16-byte piece of every row
+// is read before the first multiply.  Lanes past a short last block read in-bounds LDS bytes
+// beyond the row.
+template <int NL, int R>
+__device__ __forceinline__ void dot_rows(const uint8_t* const (&rows)[R], const XV<NL>& xv, int k, int lane,
+                                         float (&out)[R]) {
+  uint4 w[R][NL];
+#pragma unroll
+  for (int i = 0; i < R; ++i)
+#pragma unroll
+    for (int j = 0; j < NL; ++j) w[i][j] = *reinterpret_cast<const uint4*>(rows[i] + 1024 * j + 16 * lane);
+  dot_frags<NL, R>(w, xv, k, lane, out);
+}
+
+// The value through an empty asm: the compiler can neither fold it nor hoist what depends on it
+// out of a loop (where it would hold registers for the whole loop).
+__device__ __forceinline__ int opaque(int v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+
+// Loads the 16-byte pieces of R rows of the output projection (rows r + S i, clamped to r1 - 1)
+// straight from memory, with the streaming policy; lanes past a short last block read the
+// row's first piece instead (zeroed by dot_frags).  The addresses are formed at the call.
+template <int NL, int R, int S>
+__device__ __forceinline__ void load_frags(const uint16_t* outp, int D, int r, int r1, int lane_, uint4 (&w)[R][NL]) {
+  const int lane = opaque(lane_);
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    const uint8_t* row = reinterpret_cast<const uint8_t*>(outp + int64_t(min(r + S * i, r1 - 1)) * D);
+#pragma unroll
+    for (int j = 0; j < NL; ++j) {
+      const int off = lane < block_lanes(D, j) ? 1024 * j + 16 * lane : 0;
+      typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+      const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(row + off));
+      w[i][j] = make_uint4(v[0], v[1], v[2], v[3]);
+    }
+  }
 }
 
 // dot_rows with one more wave sum taken in the same reduction chain: out[R] = sum over the
@@ -670,7 +702,6 @@ __device__ __forceinline__ int poll_token(const Args& a, int s, int rep, int lan
 struct RowCtx {
   int wr, lane, wv;
   int qp0, qp1, or0, or1, f0, f1, v0, v1;   // QKV pairs, O/down rows, gate/up pairs, vocabulary rows
-  int nlog;                                 // logit chunks
   uint8_t* ring;
   float* xatt;    // attention vector (input of the O rows)
   float* xhd1;    // O output (gathered)
@@ -685,11 +716,10 @@ struct RowCtx {
 enum { kCtrBar = 0, kCtrUsed = 4, kCtrLoaded = 5, kCtrTok = 6 };
 
 // Loader wave of a row workgroup.  Jobs in order, per step: per layer the QKV, O, gate/up and
-// down rows of this workgroup (into their fixed ring regions), then the logit rows in chunks
-// alternating between the two ring halves.  Job j may overwrite its region once the job that
-// last used it has been consumed by all compute waves (a step's first job: every job of the
-// previous step, whose logit chunks spread over the whole ring).  Job indices run on across the
-// steps of a launch, as do the LDS counters.
+// down rows of this workgroup, into their fixed ring regions (the worker waves stream the logit
+// rows themselves).  Job j may overwrite its region once the job that last used it has been
+// consumed by all compute waves (a step's first job: every job of the previous step).  Job
+// indices run on across the steps of a launch, as do the LDS counters.
 template <int D, int FF, bool MULTI>
 __device__ void row_loader(const Args& a, const RowCtx& c) {
   const Layout& lay = a.lay;
@@ -697,9 +727,7 @@ __device__ void row_loader(const Args& a, const RowCtx& c) {
   Dma<kDmaLayer, MSD_DMA_AUX> d;
   Dma<kDmaLayer, kAuxKeep> dk;
   Dma<kDmaFirst, kAuxKeep> d0;
-  Dma<kDmaLogits, MSD_DMA_AUX> dl;
-  const int half = a.ring_bytes / 2;
-  const int njobs = 4 * a.L + c.nlog;
+  const int njobs = 4 * a.L;
   const int nsteps = MULTI ? a.nsteps : 1;
   for (int st = 0; st < nsteps; ++st) {
     const int base = st * njobs;
@@ -707,7 +735,7 @@ __device__ void row_loader(const Args& a, const RowCtx& c) {
       const uint16_t* src;
       int64_t bytes;
       int off, need;
-      if (j < 4 * a.L) {
+      {
         const int l = j / 4, p = j % 4;
         const uint16_t* w = layer_w(a, l);
         if (p == 0) { src = w + lay.off_qkv + int64_t(2 * c.qp0) * D; bytes = int64_t(2 * (c.qp1 - c.qp0)) * D * 2; off = a.ring_q; }
@@ -717,14 +745,6 @@ __device__ void row_loader(const Args& a, const RowCtx& c) {
         // job j - 4 (same region, previous layer) consumed; a step's first layer: the whole
         // previous step
         need = l == 0 ? base : base + j - 3;
-      } else {
-        const int k = j - 4 * a.L;
-        const int r0 = c.v0 + k * a.log_rows;
-        const int r1 = min(c.v1, r0 + a.log_rows);
-        src = a.outp + int64_t(r0) * D;
-        bytes = int64_t(r1 - r0) * D * 2;
-        off = (k & 1) * half;
-        need = base + (k < 2 ? 4 * a.L : 4 * a.L + k - 1);   // every layer job, or logit chunk k - 2
       }
       if (need > 0 && lds_ld(c.ctr + kCtrUsed) < kWavesR * need) lds_wait(c.ctr + kCtrUsed, kWavesR * need, a.ctrl);
       if (bytes > 0) {
@@ -734,16 +754,13 @@ __device__ void row_loader(const Args& a, const RowCtx& c) {
         } else if (j < 4 * a.keep) {
           dma_copy(dk, reinterpret_cast<const uint8_t*>(src), c.ring + off, bytes, lane);
           dk.drain();
-        } else if (j < 4 * a.L) {
+        } else {
           dma_copy(d, reinterpret_cast<const uint8_t*>(src), c.ring + off, bytes, lane);
           d.drain();
-        } else {
-          dma_copy(dl, reinterpret_cast<const uint8_t*>(src), c.ring + off, bytes, lane);
-          dl.drain();
         }
       }
       lds_set(c.ctr + kCtrLoaded, base + j + 1, lane);
-      MSD_TRACE_POINT(st == 0 && j < 4 * a.L, j / 4, 28 + (j % 4));
+      MSD_TRACE_POINT(st == 0, j / 4, 28 + (j % 4));
     }
   }
 }
@@ -816,7 +833,7 @@ __device__ void row_worker(const Args& a, const RowCtx& c, int token) {
   auto count = [&](int n, int cap) {   // this wave's items among n (items w, w + 8, ...)
     return n > wv ? min(cap, (n - wv + kWavesR - 1) / kWavesR) : 0;
   };
-  const int njobs = 4 * a.L + c.nlog;
+  const int njobs = 4 * a.L;
   const int nsteps = MULTI ? a.nsteps : 1;
 
   for (int st = 0; st < nsteps; ++st) {
@@ -1056,7 +1073,15 @@ __device__ void row_worker(const Args& a, const RowCtx& c, int token) {
       MSD_TRACE_POINT(wv == 0, l, 23);
     }
     // ---- h += last down output; x = final rmsnorm(h); tied logits over this workgroup's
-    //      vocabulary rows (multi_sm_decode.py:314-337)
+    //      vocabulary rows (multi_sm_decode.py:314-337).  Each worker wave streams its rows
+    //      (v0 + w, v0 + w + 8, ...) from memory straight into registers, RB rows per batch with
+    //      the next batch in flight (two register sets taken in turn); the first batch is
+    //      requested before the last down vector is gathered, as it does not depend on it.  A
+    //      launch of several steps holds more state across the step loop: one row per batch.
+    constexpr int RB = MULTI ? 1 : 2;    // rows per batch
+    constexpr int SB = kWavesR * RB;     // rows between a wave's consecutive batches
+    uint4 wa[RB][NLD], wb[RB][NLD];
+    if (c.v0 + wv < c.v1) load_frags<NLD, RB, kWavesR>(a.outp, D, c.v0 + wv, c.v1, lane, wa);
     gather_x<kWavesR, HPW, 0, kFirstPoll, D>(layer_x(a, a.L - 1) + lay.x_hd2 + myrep, D, c.xhd2, tag, a.ctrl, wv, lane, bad);
     bar();
     MSD_TRACE_POINT(wv == 0, a.L - 1, 6);
@@ -1065,33 +1090,26 @@ __device__ void row_worker(const Args& a, const RowCtx& c, int token) {
     norm(xv);
     float best = -INFINITY;
     int besti = 0x7fffffff;
-    const int half = a.ring_bytes / 2;
-    constexpr int RB = 4;   // rows per batch of LDS reads
-    for (int k = 0; k < c.nlog; ++k) {
-      weights(jb + 4 * a.L + k);
-      const int r0 = c.v0 + k * a.log_rows;
-      const int n = min(c.v1, r0 + a.log_rows) - r0;
-      const uint8_t* base = c.ring + (k & 1) * half;
-      for (int b = wv; b < n; b += kWavesR * RB) {
-        const uint8_t* rows[RB];
+    auto take = [&](const uint4 (&w)[RB][NLD], int r) {   // rows r + kWavesR i
+      float y[RB];
+      dot_frags<NLD, RB>(w, xv, D, lane, y);
 #pragma unroll
-        for (int i = 0; i < RB; ++i) {
-          const int rel = b + kWavesR * i;
-          rows[i] = base + int64_t(rel < n ? rel : 0) * D * 2;
-        }
-        float y[RB];
-        dot_rows<NLD, RB>(rows, xv, D, lane, y);
-#pragma unroll
-        for (int i = 0; i < RB; ++i) {
-          const int rel = b + kWavesR * i;
-          if (rel < n) {
-            if (lane == 0) a.logits[st * a.logits_stride + r0 + rel] = y[i];
-            if (y[i] > best) { best = y[i]; besti = r0 + rel; }
-          }
+      for (int i = 0; i < RB; ++i) {
+        const int row = r + kWavesR * i;
+        if (row < c.v1) {
+          if (lane == 0) a.logits[st * a.logits_stride + row] = y[i];
+          if (y[i] > best) { best = y[i]; besti = row; }
         }
       }
-      release();
+    };
+    for (int r = c.v0 + wv; r < c.v1; r += 2 * SB) {
+      if (r + SB < c.v1) load_frags<NLD, RB, kWavesR>(a.outp, D, r + SB, c.v1, lane, wb);
+      take(wa, r);
+      if (r + SB >= c.v1) break;
+      if (r + 2 * SB < c.v1) load_frags<NLD, RB, kWavesR>(a.outp, D, r + 2 * SB, c.v1, lane, wa);
+      take(wb, r + SB);
     }
+    MSD_TRACE_POINT(wv == 0, a.L, 1);
     if (lane == 0) {
       c.red_v[wv] = best;
       c.red_i[wv] = besti;
@@ -1541,7 +1559,6 @@ __global__ __launch_bounds__(kThreadsWG, 1) void decode_step_kernel(Args a) {
   split(D, a.GR, wg, c.or0, c.or1);
   split(a.ff, a.GR, wg, c.f0, c.f1);
   split(a.V, a.GR, wg, c.v0, c.v1);
-  c.nlog = cdiv(c.v1 - c.v0, a.log_rows);
   c.ring = smem;
   c.xatt = reinterpret_cast<float*>(smem + a.ring_bytes);
   c.xhd1 = c.xatt + D;
@@ -1588,7 +1605,7 @@ __global__ __launch_bounds__(kThreadsWG, 1) void decode_step_kernel(Args a) {
 struct Plan {   // per-config launch parameters
   int nsplit, cap, NA, GR;
   int qpw, orw, gpw;   // QKV pairs, O/down rows and gate/up pairs per compute wave (at most)
-  int ring_q, ring_o, ring_g, ring_d, ring_bytes, log_rows;
+  int ring_q, ring_o, ring_g, ring_d, ring_bytes;
   size_t lds;
 };
 
@@ -1671,19 +1688,14 @@ static bool make_plan(const msd_config* c, int G, Plan* p) {
   p->ring_o = p->ring_q + kb(int64_t(2) * qpairs * D * 2);
   p->ring_g = p->ring_o + kb(int64_t(orows) * D * 2);
   p->ring_d = p->ring_g + kb(int64_t(2) * gpairs * D * 2);
-  int ring = p->ring_d + kb(int64_t(orows) * ff * 2);
-  ring = std::max(ring, 4 * D * 2);          // at least two logit rows per ring half
-  ring = (ring + 2047) / 2048 * 2048;        // halves of whole KB
+  const int ring = p->ring_d + kb(int64_t(orows) * ff * 2);
   const int natt = H * p->nsplit * kPart;
   // more than two splits: the partials alias xhd1 | xhd2 | xact (2 D + d_ff floats)
   if (p->nsplit > 2 && natt > 2 * D + ff) return false;
   const int row_other = 4 * (3 * D + ((ff + 3) & ~3) + (p->nsplit > 2 ? 0 : ((natt + 3) & ~3)) + 8 + 2 * kWavesR);
   const int att_lds = cdiv(p->cap * kKSlots, 64) * 1024 + cdiv(p->cap, 8) * 1024 +
                       2 * 3 * kWavesA * kDh + 4 * (3 * kWavesA * kDh + 4 * kWavesA + 4 * kDh + 8);
-  const int budget = std::max(std::max(att_lds, kMinLds), ring + row_other);
-  ring = std::max(ring, (budget - row_other) / 2048 * 2048);   // spare LDS widens the logit halves
   p->ring_bytes = ring;
-  p->log_rows = (ring / 2) / (D * 2);
   p->lds = size_t(std::max(std::max(att_lds, ring + row_other), kMinLds));
   return p->lds <= size_t(kMaxLds);
 }
@@ -1845,7 +1857,6 @@ static int32_t decode_impl(const msd_config* cfg, const void* token_emb, const v
   a.ring_g = p.ring_g;
   a.ring_d = p.ring_d;
   a.ring_bytes = p.ring_bytes;
-  a.log_rows = p.log_rows;
   a.keep = int(std::min<int64_t>(cfg->n_layers, kKeepBytes / (a.lay.layer_elems * 2)));
   bool not_resident = false;
   const hipError_t e = launch(a, cfg->d_model, cfg->d_ff, n_workgroups, p.lds, stream, &not_resident);

@@ -16,7 +16,8 @@ Row-workgroup slots: 16 QKV rows ready, 11 normed, 14 dots done, 17 QKV outputs 
 loader slots 28-31 the QKV / O / gate-up / down rows of the layer landed in LDS.
 Attention-workgroup slots: 28 cached K/V rows landed, 24 q gathered, 25 rows ready,
 29 scores done, 30 P.V done, 26 blocks merged, 27 head output published.
-Tail (layer index n_layers): 12 logits and argmax of the workgroup done.
+Tail (layer index n_layers): 1 worker wave 0's logit rows streamed, 12 logits and argmax of the
+workgroup done.
 """
 import argparse
 import ctypes
@@ -102,6 +103,13 @@ def run(pos, layers, n_prompt=32, trace_layer=10):
     print(f"  sum {lens.sum():.2f}; last down vector gathered -> logits done: "
           f"{_stats((t_logits - tr[nl - 1, :GR, 6].max()) / 100.0)}")
     print(f"  step span from the first QKV start: {(t_logits.max() - t_begin) / 100.0:.2f}")
+    t_dn = tr[nl - 1, :GR, 6].max()
+    print("  tail, us from the last down vector gathered (slowest workgroup):")
+    for slot, name in ((1, "logit rows streamed"), (12, "logits and argmax done")):
+        col = tr[nl, :GR, slot]
+        col = col[col > 0]
+        if len(col):
+            print(f"    {name:24s} {_stats((col - t_dn) / 100.0)}")
     for l in layers:
         t0 = starts[l]
         print(f"\n=== layer {l} (us from its first QKV start)")
