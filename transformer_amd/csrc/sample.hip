@@ -280,32 +280,33 @@ __device__ double cdf_threshold(double total, double u) {
 
 // RandomState.choice on one uniform: the number of i < n with cdf[i] / cdf[n-1] <= u, where
 // cdf is the float64 running sum of w[i] = (divide ? v[i] / div : v[i]) (float32 values,
-// padded LDS layout, read once into registers).  Thread t adds entries [32t, 32t+32) in order on
-// top of the sum of all earlier entries, so every partial sum equals the sequential one whenever
-// the float64 sums are exact (float32 terms spanning fewer than 29 binades below the total).
-// cdf is nondecreasing, so each thread tests its last entry against the threshold of
-// cdf_threshold and only the thread whose range crosses it tests its entries one by one.
+// padded LDS layout, read once into registers).  The float64 sums are exact whenever the float32
+// terms span fewer than 29 binades below the total, and then every partial sum equals the
+// sequential one in any order: thread t sums its entries [32t, 32t+32), a block scan gives the
+// sum of all earlier entries, and their sum is cdf at the thread's last entry.  cdf is
+// nondecreasing, so each thread tests its last entry against the threshold of cdf_threshold and
+// only the thread whose range crosses it adds its entries one by one.  Threads past n (whole
+// waves for a small nucleus) skip the divisions.
 __device__ __forceinline__ int inverse_cdf(const float* v, int n, bool divide, float div, double u,
                                            BlockScratch& b) {
   __shared__ uint8_t flag[kT];
   const int t = threadIdx.x, base = t * kPer;
   const int cnt = max(0, min(kPer, n - base));
   float w[kPer];
-#pragma unroll
-  for (int i = 0; i < kPer; ++i) w[i] = v[pad(min(base + i, kVMax - 1))];
-  if (divide) {
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) w[i] = w[i] / div;
-  }
   double tot = 0.0;
+  if (cnt > 0) {
 #pragma unroll
-  for (int i = 0; i < kPer; ++i)
-    if (i < cnt) tot += double(w[i]);
+    for (int i = 0; i < kPer; ++i) w[i] = v[pad(min(base + i, kVMax - 1))];
+    if (divide) {
+#pragma unroll
+      for (int i = 0; i < kPer; ++i) w[i] = w[i] / div;
+    }
+#pragma unroll
+    for (int i = 0; i < kPer; ++i)
+      if (i < cnt) tot += double(w[i]);
+  }
   const double excl = block_excl_scan_f64(tot, b);
-  double r = excl;
-#pragma unroll
-  for (int i = 0; i < kPer; ++i)
-    if (i < cnt) r += double(w[i]);
+  const double r = excl + tot;
   if (cnt > 0 && base + cnt == n) b.dthr = cdf_threshold(r, u);   // r = cdf[n-1] here
   if (t == 0) b.i0 = n;   // no range crosses: every entry is <= the threshold
   __syncthreads();
