@@ -93,15 +93,17 @@ def test_kernel_perm_layout():
 
 def test_config_support_query():
     """msd_config_support (no device call): the benchmark shapes take every path up to a
-    2048-position context; beyond it only prefill and the sampler; a d_model 2048 checkpoint is
-    refused by check_config and by the weight preparation before anything reaches a device."""
+    2048-position context (the persistent batched step up to 512); beyond it only prefill and the
+    sampler; a d_model 2048 checkpoint is refused by check_config and by the weight preparation
+    before anything reaches a device."""
     import pytest
     from transformer_amd.configs import M306, TINY, check_config, supported_paths
     from transformer_amd.fused_decode_nlayer import prepare_decode_weights_nlayer
     every = {"decode", "prefill", "verify", "batched", "sample"}
     for cfg in (TINY, M306):
         for ctx in (128, 512, 1024, 2048):
-            assert supported_paths(dict(cfg, context_len=ctx)) == every
+            step = {"batched_step"} if ctx <= 512 else set()
+            assert supported_paths(dict(cfg, context_len=ctx)) == every | step
         assert supported_paths(dict(cfg, context_len=4096)) == {"prefill", "sample"}
     big = dict(M306, d_model=2048, n_heads=32, d_ff=5504)
     assert supported_paths(big) == {"sample"}
@@ -110,4 +112,4 @@ def test_config_support_query():
     with pytest.raises(ValueError, match="decode"):
         prepare_decode_weights_nlayer({}, big, device="cpu")
     assert "decode" not in supported_paths(dict(M306, d_ff=2944))   # no instance for this d_ff
-    assert supported_paths(dict(TINY, vocab_size=40000)) == every - {"sample"}
+    assert supported_paths(dict(TINY, vocab_size=40000)) == (every | {"batched_step"}) - {"sample"}

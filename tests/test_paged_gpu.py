@@ -203,13 +203,15 @@ def test_persistent_step_matches_multi_kernel_step():
 
 def test_persistent_step_epoch_wrap():
     """The step's epoch (first word of its workspace) wraps from 0xFFFFFFFE to 1: steps across
-    the wrap give the same results as on a fresh workspace."""
+    the wrap, on an ordinary zero-filled tensor as the workspace, give the same results as on a
+    fresh workspace from the library's uncached pool (the decoder's default)."""
     params = make_params(TINY, seed=0)
     lens = [18, 40, 25]
     bd, pool, tables, prompts, first = _setup(TINY, params, 3, lens, 4, 64, seed=13)
     pool2 = PagePool(TINY, 64)
     pool2.data.copy_(pool.data)
-    bd2 = PagedBatchDecoder(bd.w, TINY, pool2, 3)
+    bd2 = PagedBatchDecoder(bd.w, TINY, pool2, 3, uncached=False)
+    assert bd.workspace is None and bd2.workspace is not None
     for b in range(3):
         bd2.set_pages(b, tables[b])
     bd2.workspace[:4].copy_(torch.tensor([0xFFFFFFFD], dtype=torch.int64).to(torch.int32).view(torch.uint8))

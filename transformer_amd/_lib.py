@@ -29,7 +29,7 @@ EXPORTS = ("msd_packed_weight_elems", "msd_workspace_bytes", "msd_default_workgr
            "msd_config_support", "msd_xent_workspace_bytes", "msd_xent_forward", "msd_xent_backward")
 
 # Paths of the library (bits of msd_config_support)
-PATHS = {"decode": 1, "prefill": 2, "verify": 4, "batched": 8, "sample": 16}
+PATHS = {"decode": 1, "prefill": 2, "verify": 4, "batched": 8, "sample": 16, "batched_step": 32}
 
 
 class MsdConfig(ctypes.Structure):

@@ -1671,6 +1671,7 @@ extern "C" int32_t msd_config_support(const msd_config* cfg, int32_t n_workgroup
   if (mx_config_ok(cfg)) {
     paths |= MSD_PATH_PREFILL;
     if (cfg->context_len <= kAttnMaxCtx) paths |= MSD_PATH_VERIFY | MSD_PATH_BATCHED;
+    if ((paths & MSD_PATH_BATCHED) && mbd::region_bytes(cfg) > 0) paths |= MSD_PATH_BATCHED_STEP;
   }
   if (msdc::sample_supported(cfg->vocab_size)) paths |= MSD_PATH_SAMPLE;
   return paths;

@@ -24,6 +24,7 @@ import torch
 from . import _lib
 
 PAGE = 16
+STEP_MAX_BATCH = 8   # sequences one persistent launch of msd_batch_decode_step takes
 
 
 class PagePool:
@@ -52,9 +53,12 @@ class PagePool:
 
 class PagedBatchDecoder:
     """Batched decode of ``batch`` sequences over ``pool``.  With ``tiles`` (default) the prompt
-    prefill and the multi-kernel step read the tile copy of the weights (``weight_tiles``)."""
+    prefill and the multi-kernel step read the tile copy of the weights (``weight_tiles``).
+    ``uncached`` places the step's workspace in the library's pool of uncached device memory
+    (default: when the step runs as one persistent launch, whose barrier polls are cheaper
+    there); otherwise it is an ordinary zero-filled tensor, ``self.workspace``."""
 
-    def __init__(self, w, config, pool, batch, max_pages=None, device=None, tiles=True):
+    def __init__(self, w, config, pool, batch, max_pages=None, device=None, tiles=True, uncached=None):
         from .fused_decode_nlayer import weight_tiles
         self.w = w
         self.tiles = weight_tiles(w, config) if tiles else None
@@ -70,7 +74,20 @@ class PagedBatchDecoder:
                          "msd_prefill_workspace_bytes")
         # the step's workspace holds its barrier flags and epoch: zero-filled once, used by no
         # other call (the prompt prefill has its own)
-        self.workspace = torch.zeros(nb, dtype=torch.uint8, device=self.device)
+        if uncached is None:
+            from .configs import supported_paths
+            uncached = self.batch <= STEP_MAX_BATCH and "batched_step" in supported_paths(self.config)
+        self.workspace = None
+        self._pooled = None
+        if uncached:   # zero-filled on acquire, returned to the pool by close()
+            ws = ctypes.c_void_p()
+            dev = self.device.index if self.device.index is not None else torch.cuda.current_device()
+            _lib.check(L.msd_workspace_acquire(dev, nb, ctypes.byref(ws)), "msd_workspace_acquire")
+            self._pooled = ws.value
+            self.workspace_ptr = ws.value
+        else:
+            self.workspace = torch.zeros(nb, dtype=torch.uint8, device=self.device)
+            self.workspace_ptr = self.workspace.data_ptr()
         self.pf_workspace = torch.empty(npf, dtype=torch.uint8, device=self.device)
         self.tables = torch.zeros((self.batch, self.max_pages), dtype=torch.int32, device=self.device)
         self.logits = torch.empty((self.batch, config["vocab_size"]), dtype=torch.float32, device=self.device)
@@ -121,9 +138,22 @@ class PagedBatchDecoder:
         rc = _lib.lib().msd_batch_decode_step(
             ctypes.byref(self._cfg), *self._w(), tokens.data_ptr(), positions.data_ptr(), self.batch,
             self.tables.data_ptr(), self.max_pages, self.pool.data.data_ptr(), self.pool.n_pages,
-            self.workspace.data_ptr(), self.logits.data_ptr(), out.data_ptr(), ctypes.c_void_p(s.cuda_stream))
+            self.workspace_ptr, self.logits.data_ptr(), out.data_ptr(), ctypes.c_void_p(s.cuda_stream))
         _lib.check(rc, "msd_batch_decode_step")
         return out
+
+    def close(self):
+        """Return a pooled workspace to the library (the decoder is unusable afterwards)."""
+        ptr, self._pooled = getattr(self, "_pooled", None), None
+        if ptr:
+            self.workspace_ptr = None
+            _lib.lib().msd_workspace_release(ptr)
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
     def step(self, tokens, positions):
         """One step from host lists; returns (next tokens (batch,) list, logits (batch, V) tensor)."""
