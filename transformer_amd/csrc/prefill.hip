@@ -372,6 +372,15 @@ __global__ __launch_bounds__(256) void mx_gemm_rows(GemmArgs g) {
       }
     }
   }
+  // the residual elements this thread's epilogue updates (one per column tile: row 4 (lane / 16)
+  // + wave of the tile, column 16 ct + lane % 16), requested before the K loop so that the
+  // epilogue does not wait a memory round trip for them (rows past M read row M - 1)
+  float hold[CT];
+  if constexpr (EPI == kEpiResid || EPI == kEpiResidNorm) {
+    const int row = min(m0 + 4 * (lane >> 4) + wv, g.M - 1);
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) hold[ct] = g.out[act_index(row, n0 + 16 * ct + (lane & 15), g.N, 0)];
+  }
   uint4 a[P][RT], al[P][RT], w[P][CT];
   // step i of this wave, clamped to its last: loads stay unconditional, so no wait lands at a
   // branch join (a column tile past a short group's end reads its last tile)
@@ -431,8 +440,9 @@ __global__ __launch_bounds__(256) void mx_gemm_rows(GemmArgs g) {
     // (one row tile, whole column groups) thread tid holds row 4 (lane / 16) + wave of the tile,
     // columns 16 ct + lane % 16
     float hsq = 0.f;
-    for (int idx = threadIdx.x; idx < CT * 256; idx += 256) {
-      const int ct = idx >> 8, e = idx & 255, r = e >> 6, l = e & 63;
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) {
+      const int r = wv, l = lane;
       float v = ((red[0][0][ct][r][l] + red[1][0][ct][r][l]) + red[2][0][ct][r][l]) + red[3][0][ct][r][l];
       if constexpr (AM == 2) v = v / rrms[4 * (l >> 4) + r];
       const int row = m0 + 4 * (l >> 4) + r, col = n0 + 16 * ct + (l & 15);
@@ -441,7 +451,7 @@ __global__ __launch_bounds__(256) void mx_gemm_rows(GemmArgs g) {
         if constexpr (EPI == kEpiStore) {
           *o = v;
         } else {
-          const float hv = *o + v;
+          const float hv = hold[ct] + v;
           *o = hv;
           if constexpr (EPI == kEpiResidNorm) {
             put_split(g.e.act + act_index(row, col, g.N, 0), g.e.act_plane, bf2f(g.e.xscale[col]) * hv);
