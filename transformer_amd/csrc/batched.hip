@@ -9,8 +9,9 @@
 // Grid: one workgroup per compute unit, all resident (checked with the occupancy API before
 // the launch).  A workgroup is 7 worker waves and one loader wave (two waves per SIMD).
 //
-// Phases, each ended by a grid barrier: the embedding rows, then per layer
-//   QKV   workgroups own groups of 8 packed q/k/v rows: raw projections -> qkv
+// Phases, each ended by a grid barrier except QKV: the embedding rows, then per layer
+//   QKV   workgroups own groups of 8 packed q/k/v rows: raw projections -> qkv (tagged words,
+//         which the attention items poll: no barrier)
 //   ATT   workgroups own (sequence, head) items: RoPE, K/V row of the current position to the
 //         cache, attention over the cached rows (bf16) and the current K/V (f32) -> att
 //   O     groups of 8 O rows: h += O att (each workgroup keeps its residual elements in LDS)
@@ -40,7 +41,9 @@
 // once per step with agent-scope (sc1) stores that go through to memory.  A buffer is read only
 // after the barrier that follows its writes, and nothing reads it earlier in the step, so no L2
 // holds a stale line of it (the L2s start every kernel invalidated): readers use ordinary cached
-// 16-byte loads, and each XCD fetches a vector from memory once.  A barrier is a flag word per
+// 16-byte loads, and each XCD fetches a vector from memory once.  The exception is qkv: its
+// words carry the step's epoch in their upper half and are polled with agent-scope loads.  A
+// barrier is a flag word per
 // workgroup set to the step's epoch after the workgroup's stores have completed
 // (s_waitcnt vmcnt(0)), polled by one wave of every workgroup with agent-scope loads.  Epochs
 // run 1..0xFFFFFFFE (the last one is kept in the workspace); every flag is rewritten each step,
@@ -103,11 +106,6 @@ constexpr int kFlagReps = MBD_FLAG_REPS;
 #define MBD_LOADER_PRIO 1
 #endif
 constexpr int kLoaderPrio = MBD_LOADER_PRIO;
-// the wave that polls the QKV barrier (the others request their first attention block meanwhile)
-#ifndef MBD_QKV_POLLER
-#define MBD_QKV_POLLER 6
-#endif
-constexpr int kQkvPoller = MBD_QKV_POLLER;
 constexpr uint32_t kLdsSpinLimit = 1u << 23;   // LDS-counter spins
 // control words (uint32 offsets in the control block)
 constexpr int kCtlEpoch = 0, kCtlStatus = 16;   // status slot k at kCtlStatus + 16 k
@@ -191,7 +189,8 @@ __device__ __forceinline__ void split(int total, int parts, int idx, int& lo, in
 }
 
 // Exchange block of layer l (block l + 1; block 0 holds the embedding rows as "layer -1"):
-//   qkv      f32 [kRows][nqkv]        raw q/k/v projections, packed row order
+//   qkv      u64 [kRows][nqkv]        raw q/k/v projections, packed row order, as tagged words
+//                                     (f32 bits | epoch << 32): the attention items poll them
 //   att      bf16 [2][kRows][ld(d)]   attention output as hi/lo planes, packed input order of O
 //   act      bf16 [2][kRows][ld(ff)]  SwiGLU output as hi/lo planes, packed input order of down
 //   hop, hdp bf16 [2][kRows][ld(d)]   the residual stream after O times ln2 and after down times
@@ -202,24 +201,24 @@ __device__ __forceinline__ void split(int total, int parts, int idx, int& lo, in
 // fragments an MFMA operand load touches sit at the same offset on one memory channel.
 __host__ __device__ __forceinline__ int plane_ld(int K) { return K + 8; }
 __device__ __forceinline__ float* x_blk(const Args& a, int l) { return a.x + int64_t(l + 1) * a.x_layer; }
-__device__ __forceinline__ float* x_qkv(const Args& a, int l) { return x_blk(a, l); }
+__device__ __forceinline__ uint64_t* x_qkv(const Args& a, int l) { return reinterpret_cast<uint64_t*>(x_blk(a, l)); }
 __device__ __forceinline__ uint16_t* x_att(const Args& a, int l) {
-  return reinterpret_cast<uint16_t*>(x_qkv(a, l) + int64_t(kRows) * a.nqkv);
+  return reinterpret_cast<uint16_t*>(x_blk(a, l) + int64_t(kRows) * 2 * a.nqkv);
 }
 __device__ __forceinline__ uint16_t* x_act(const Args& a, int l) {
-  return reinterpret_cast<uint16_t*>(x_qkv(a, l) + int64_t(kRows) * (a.nqkv + plane_ld(a.d)));
+  return reinterpret_cast<uint16_t*>(x_blk(a, l) + int64_t(kRows) * (2 * a.nqkv + plane_ld(a.d)));
 }
 __device__ __forceinline__ uint16_t* x_hop(const Args& a, int l) {
-  return reinterpret_cast<uint16_t*>(x_qkv(a, l) + int64_t(kRows) * (a.nqkv + plane_ld(a.d) + plane_ld(a.ff)));
+  return reinterpret_cast<uint16_t*>(x_blk(a, l) + int64_t(kRows) * (2 * a.nqkv + plane_ld(a.d) + plane_ld(a.ff)));
 }
 __device__ __forceinline__ uint16_t* x_hdp(const Args& a, int l) { return x_hop(a, l) + 2 * kRows * plane_ld(a.d); }
 __device__ __forceinline__ float* x_sso(const Args& a, int l) {
-  return x_qkv(a, l) + int64_t(kRows) * (a.nqkv + 3 * plane_ld(a.d) + plane_ld(a.ff));
+  return x_blk(a, l) + int64_t(kRows) * (2 * a.nqkv + 3 * plane_ld(a.d) + plane_ld(a.ff));
 }
 __device__ __forceinline__ float* x_ssd(const Args& a, int l) { return x_sso(a, l) + a.d; }
 // floats of one exchange block
 __host__ __device__ __forceinline__ int64_t x_block_floats(int d, int nqkv, int ff) {
-  return int64_t(kRows) * (3 * plane_ld(d) + nqkv + plane_ld(ff)) + 2 * d;
+  return int64_t(kRows) * (3 * plane_ld(d) + 2 * nqkv + plane_ld(ff)) + 2 * d;
 }
 
 __device__ __forceinline__ uint32_t ld_u32(const uint32_t* p) {
@@ -384,6 +383,23 @@ __device__ __forceinline__ void grid_wait(const Args& a, Sync& sy, int b, uint32
 __device__ __forceinline__ void grid_sync(const Args& a, Sync& sy, int b, uint32_t epoch, int wv, int lane) {
   grid_arrive(a, sy, b, epoch, wv, lane);
   grid_wait(a, sy, b, epoch, wv, lane);
+}
+// The f32 of a tagged word (f32 bits | epoch << 32) once its tag is the step's epoch: every lane
+// of the wave polls its word with agent-scope loads (a stale copy in an L2 is not read), bounded
+// like the grid barrier.
+__device__ __forceinline__ float poll_word(const uint64_t* p, uint32_t epoch, uint32_t* status) {
+  uint64_t w = ld_u64(p);
+  uint32_t spins = 0;
+  while (!__all(uint32_t(w >> 32) == epoch)) {
+    if constexpr (MBD_BAR_SLEEP > 0) __builtin_amdgcn_s_sleep(MBD_BAR_SLEEP);
+    if (uint32_t(w >> 32) != epoch) w = ld_u64(p);
+    if ((++spins & 255u) == 0 && (ld_u32(status) & kStTimeout)) break;
+    if (spins > kSpinLimit) {
+      if ((threadIdx.x & 63) == 0) atomicOr(status, kStTimeout);
+      break;
+    }
+  }
+  return __uint_as_float(uint32_t(w));
 }
 
 // ---------------------------------------------------------------- jobs (weight rows of a phase)
@@ -669,17 +685,16 @@ __device__ __forceinline__ void att_load(const Args& a, int l, const Item& it, i
 // The attention of item it in layer l (model.py:100-107 / multi_sm_decode.py:182-221).  Block wv
 // comes in P when `pre` (loaded before the barrier), later blocks are loaded here.
 __device__ __forceinline__ void att_compute(const Args& a, int l, const Item& it, AttPre& P, bool pre, AttLds& S,
-                                            Sync& sy, int wv, int lane) {
+                                            Sync& sy, uint32_t epoch, int wv, int lane) {
   const int tid = wv * 64 + lane;
   const int gs = a.H / a.KV, h = it.h, g = h / gs, m = it.m, p = it.p;
   const int pool = a.pool_pages * kPage;
   uint16_t* kc = a.kv + int64_t(l) * 2 * a.KV * pool * kDh + int64_t(g) * pool * kDh;
   uint16_t* vc = kc + int64_t(a.KV) * pool * kDh;
   if (!pre && 64 * wv <= p) att_load(a, l, it, wv, lane, P);
-  if (tid < 3 * kDh) {
-    const int sel = tid / kDh, c = tid % kDh;
-    const int head = sel == 0 ? h : (sel == 1 ? a.H + g : a.H + a.KV + g);
-    S.raw[sel][c] = x_qkv(a, l)[int64_t(m) * a.nqkv + head * kDh + c];
+  if (wv < 3) {   // wave 0 / 1 / 2 polls the item's q / k / v (posted by the QKV phase: no barrier)
+    const int head = wv == 0 ? h : (wv == 1 ? a.H + g : a.H + a.KV + g);
+    S.raw[wv][lane] = poll_word(x_qkv(a, l) + int64_t(m) * a.nqkv + head * kDh + lane, epoch, sy.status);
   }
   wsync(sy, lane);
   if (tid < kDh) {   // RoPE (model.py:110-117): packed pair (2i, 2i+1) = dims (i, i + 32)
@@ -888,17 +903,16 @@ __global__ __launch_bounds__(kThreads) void batch_step_kernel(Args a) {
           if (2 * t + (n >> 3) < jb.ng && m < M) {
             const float y = tile_out(red, tiles, t, m, n) * s_inv[m];
             const int row = 8 * (jb.g0 + 2 * t + (n >> 3)) + (n & 7);
-            st_f(x_qkv(a, l) + int64_t(m) * a.nqkv + row, y);
+            st_u64(x_qkv(a, l) + int64_t(m) * a.nqkv + row, (uint64_t(epoch) << 32) | __float_as_uint(y));
           }
         }
         MBD_T(wv == 0 && l == kTraceLayer, 4);
         lds_bump(sy.consumed, lane);
         ++j;
       }
-      grid_arrive(a, sy, bl, epoch, wv, lane);
-      // one wave polls; the others request their K/V block meanwhile (the poller after the barrier)
-      if (s_att.nitems > 0 && wv != kQkvPoller && 64 * wv <= s_att.it[0].p) att_load(a, l, s_att.it[0], wv, lane, pre);
-      grid_wait(a, sy, bl, epoch, wv, lane, kQkvPoller);
+      // no barrier: the attention items poll their q, k and v words; every wave requests its
+      // first K/V block meanwhile
+      if (s_att.nitems > 0 && 64 * wv <= s_att.it[0].p) att_load(a, l, s_att.it[0], wv, lane, pre);
       MBD_T(wv_ == 0, 40 + 5 * l + 0);
       MBD_T(wv_ == 0 && l == kTraceLayer, 5);
     }
@@ -907,7 +921,7 @@ __global__ __launch_bounds__(kThreads) void batch_step_kernel(Args a) {
       MBD_T(wv_ == 0 && l == kTraceLayer, 8);
       for (int n = 0; n < s_att.nitems; ++n) {
         const int lane = opaque(lane_), wv = opaque(wv_);
-        att_compute(a, l, s_att.it[n], pre, n == 0 && wv != kQkvPoller, s_att, sy, wv, lane);
+        att_compute(a, l, s_att.it[n], pre, n == 0, s_att, sy, epoch, wv, lane);
       }
       MBD_T(wv_ == 0 && l == kTraceLayer, 12);
       grid_sync(a, sy, bl + 1, epoch, wv, lane);
