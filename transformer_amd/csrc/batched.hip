@@ -141,7 +141,9 @@ struct Args {
 // Lane 0 of worker wave 0 of every workgroup stamps s_memrealtime (100 MHz) at phase
 // boundaries: slot 8 p + k of layer kTraceLayer's phase p (0 QKV .. 4 DN): k = 0 phase start,
 // 1 inputs ready, 2 weights landed, 3 summed, 4 outputs stored, 5 barrier passed; slot 40 + 5 l + p:
-// barrier p of layer l passed; slot 168: logits done; 169: final barrier.  The loader stamps slot
+// barrier p of layer l passed; slot 168: logits done; 169: final barrier.  Attention of layer
+// kTraceLayer (first item): slot 9 q/k/v polled, 14 the item's position (a value), 15 wave 1's
+// scores, 160 + w wave w's block done, 10 the waves met, 11 output stored.  The loader stamps slot
 // 176 + p when the weights of layer kTraceLayer's phase p are issued and 184 + p when they landed.
 constexpr int kTraceLayer = 10;
 #ifdef MBD_TRACE
@@ -152,9 +154,16 @@ __device__ uint64_t mbd_trace_buf[kMaxGrid * kTraceSlots];
     if ((cond) && (threadIdx.x & 63) == 0)                                                      \
       mbd_trace_buf[blockIdx.x * kTraceSlots + (slot)] = __builtin_amdgcn_s_memrealtime();      \
   } while (0)
+#define MBD_V(cond, slot, v)                                                                    \
+  do {                                                                                          \
+    if ((cond) && (threadIdx.x & 63) == 0) mbd_trace_buf[blockIdx.x * kTraceSlots + (slot)] = (v); \
+  } while (0)
 #else
 #define MBD_T(cond, slot) \
   do {                    \
+  } while (0)
+#define MBD_V(cond, slot, v) \
+  do {                       \
   } while (0)
 #endif
 
@@ -697,6 +706,8 @@ __device__ __forceinline__ void att_compute(const Args& a, int l, const Item& it
     S.raw[wv][lane] = poll_word(x_qkv(a, l) + int64_t(m) * a.nqkv + head * kDh + lane, epoch, sy.status);
   }
   wsync(sy, lane);
+  MBD_T(wv == 0 && l == kTraceLayer, 9);
+  MBD_V(wv == 0 && l == kTraceLayer, 14, uint64_t(p));
   if (tid < kDh) {   // RoPE (model.py:110-117): packed pair (2i, 2i+1) = dims (i, i + 32)
     const int sel = tid >> 5, i = tid & 31;
     const float c = it.cs[i], sn = it.cs[kDh / 2 + i];
@@ -723,6 +734,9 @@ __device__ __forceinline__ void att_compute(const Args& a, int l, const Item& it
       float4 qv[kDh / 4];   // q in registers (broadcast LDS reads, issued together)
 #pragma unroll
       for (int k = 0; k < kDh / 4; ++k) qv[k] = reinterpret_cast<const float4*>(S.q)[k];
+      // the current position's score (its f32 K) as one wave sum, by the wave whose block holds it
+      // (a sequential loop in its lane waited for an LDS round trip per pair of products)
+      const float scur = p < j0 + 64 ? wave_sum(S.q[lane] * S.k[lane]) * 0.125f : 0.f;
       float sc = -INFINITY;
       if (j < p) {
         float a0 = 0.f, a1 = 0.f;
@@ -738,15 +752,11 @@ __device__ __forceinline__ void att_compute(const Args& a, int l, const Item& it
           }
         }
         sc = (a0 + a1) * 0.125f;
-      } else if (j == p) {   // current position: its f32 K
-        float a0 = 0.f, a1 = 0.f;
-        for (int e = 0; e < kDh; e += 2) {
-          a0 += S.q[e] * S.k[e];
-          a1 += S.q[e + 1] * S.k[e + 1];
-        }
-        sc = (a0 + a1) * 0.125f;
+      } else if (j == p) {
+        sc = scur;
       }
       mx = wave_max(sc);
+      MBD_T(wv == 1 && b == wv && l == kTraceLayer, 15);
       const float e = (sc == -INFINITY) ? 0.f : expf(sc - mx);
       ls = wave_sum(e);
       S.p[b][lane] = e;
@@ -793,8 +803,10 @@ __device__ __forceinline__ void att_compute(const Args& a, int l, const Item& it
       S.ml[b][0] = mx;
       S.ml[b][1] = ls;
     }
+    MBD_T(b == wv && l == kTraceLayer, 160 + wv);
   }
   wsync(sy, lane);
+  MBD_T(wv == 0 && l == kTraceLayer, 10);
   if (wv == 0) {   // merge of the blocks: softmax over all positions
     float M = -INFINITY;
     for (int b = 0; b < kBlocks; ++b) M = fmaxf(M, S.ml[b][0]);
@@ -807,6 +819,7 @@ __device__ __forceinline__ void att_compute(const Args& a, int l, const Item& it
     }
     st_split(x_att(a, l) + int64_t(m) * plane_ld(a.d) + perm_pos(h * kDh + lane, a.d), int64_t(kRows) * plane_ld(a.d),
              num / den);
+    MBD_T(l == kTraceLayer, 11);
   }
   wsync(sy, lane);   // the LDS state is reused by the next item
 }
