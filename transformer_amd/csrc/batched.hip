@@ -106,6 +106,10 @@ constexpr int kFlagReps = MBD_FLAG_REPS;
 #define MBD_LOADER_PRIO 1
 #endif
 constexpr int kLoaderPrio = MBD_LOADER_PRIO;
+// the worker wave that polls an attention item's q, k and v; it requests its block of cached K/V
+// rows only afterwards (a wave's loads complete in order: polls issued behind ~40 K/V loads wait
+// for them), while the other waves request theirs at once
+constexpr int kQkvPoller = kWorkers - 1;
 constexpr uint32_t kLdsSpinLimit = 1u << 23;   // LDS-counter spins
 // control words (uint32 offsets in the control block)
 constexpr int kCtlEpoch = 0, kCtlStatus = 16;   // status slot k at kCtlStatus + 16 k
@@ -393,22 +397,33 @@ __device__ __forceinline__ void grid_sync(const Args& a, Sync& sy, int b, uint32
   grid_arrive(a, sy, b, epoch, wv, lane);
   grid_wait(a, sy, b, epoch, wv, lane);
 }
-// The f32 of a tagged word (f32 bits | epoch << 32) once its tag is the step's epoch: every lane
-// of the wave polls its word with agent-scope loads (a stale copy in an L2 is not read), bounded
-// like the grid barrier.
-__device__ __forceinline__ float poll_word(const uint64_t* p, uint32_t epoch, uint32_t* status) {
-  uint64_t w = ld_u64(p);
+// The f32s of N tagged words per lane (f32 bits | epoch << 32) once their tags are the step's
+// epoch: every lane of the wave polls its words with agent-scope loads (a stale copy in an L2 is
+// not read), bounded like the grid barrier.
+template <int N>
+__device__ __forceinline__ void poll_words(const uint64_t* const (&p)[N], uint32_t epoch, uint32_t* status,
+                                           float (&out)[N]) {
+  uint64_t w[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i) w[i] = ld_u64(p[i]);
   uint32_t spins = 0;
-  while (!__all(uint32_t(w >> 32) == epoch)) {
+  while (true) {
+    bool ok = true;
+#pragma unroll
+    for (int i = 0; i < N; ++i) ok = ok && uint32_t(w[i] >> 32) == epoch;
+    if (__all(ok)) break;
     if constexpr (MBD_BAR_SLEEP > 0) __builtin_amdgcn_s_sleep(MBD_BAR_SLEEP);
-    if (uint32_t(w >> 32) != epoch) w = ld_u64(p);
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+      if (uint32_t(w[i] >> 32) != epoch) w[i] = ld_u64(p[i]);
     if ((++spins & 255u) == 0 && (ld_u32(status) & kStTimeout)) break;
     if (spins > kSpinLimit) {
       if ((threadIdx.x & 63) == 0) atomicOr(status, kStTimeout);
       break;
     }
   }
-  return __uint_as_float(uint32_t(w));
+#pragma unroll
+  for (int i = 0; i < N; ++i) out[i] = __uint_as_float(uint32_t(w[i]));
 }
 
 // ---------------------------------------------------------------- jobs (weight rows of a phase)
@@ -700,10 +715,15 @@ __device__ __forceinline__ void att_compute(const Args& a, int l, const Item& it
   const int pool = a.pool_pages * kPage;
   uint16_t* kc = a.kv + int64_t(l) * 2 * a.KV * pool * kDh + int64_t(g) * pool * kDh;
   uint16_t* vc = kc + int64_t(a.KV) * pool * kDh;
-  if (!pre && 64 * wv <= p) att_load(a, l, it, wv, lane, P);
-  if (wv < 3) {   // wave 0 / 1 / 2 polls the item's q / k / v (posted by the QKV phase: no barrier)
-    const int head = wv == 0 ? h : (wv == 1 ? a.H + g : a.H + a.KV + g);
-    S.raw[wv][lane] = poll_word(x_qkv(a, l) + int64_t(m) * a.nqkv + head * kDh + lane, epoch, sy.status);
+  if (!pre && wv != kQkvPoller && 64 * wv <= p) att_load(a, l, it, wv, lane, P);
+  if (wv == kQkvPoller) {   // the item's q, k and v (posted by the QKV phase: no barrier)
+    const uint64_t* row = x_qkv(a, l) + int64_t(m) * a.nqkv + lane;
+    const uint64_t* const src[3] = {row + h * kDh, row + (a.H + g) * kDh, row + (a.H + a.KV + g) * kDh};
+    float v[3];
+    poll_words<3>(src, epoch, sy.status, v);
+#pragma unroll
+    for (int i = 0; i < 3; ++i) S.raw[i][lane] = v[i];
+    if (64 * wv <= p) att_load(a, l, it, wv, lane, P);   // this wave's block, after the poll
   }
   wsync(sy, lane);
   MBD_T(wv == 0 && l == kTraceLayer, 9);
@@ -923,9 +943,9 @@ __global__ __launch_bounds__(kThreads) void batch_step_kernel(Args a) {
         lds_bump(sy.consumed, lane);
         ++j;
       }
-      // no barrier: the attention items poll their q, k and v words; every wave requests its
-      // first K/V block meanwhile
-      if (s_att.nitems > 0 && 64 * wv <= s_att.it[0].p) att_load(a, l, s_att.it[0], wv, lane, pre);
+      // no barrier: the attention items poll their q, k and v words; the other waves request
+      // their first K/V block meanwhile
+      if (s_att.nitems > 0 && wv != kQkvPoller && 64 * wv <= s_att.it[0].p) att_load(a, l, s_att.it[0], wv, lane, pre);
       MBD_T(wv_ == 0, 40 + 5 * l + 0);
       MBD_T(wv_ == 0 && l == kTraceLayer, 5);
     }
