@@ -799,14 +799,19 @@ __device__ __forceinline__ void att_compute(const Args& a, int l, const Item& it
           o1[jj & 1] += pw[jj] * __uint_as_float(P.vv[jj] & 0xffff0000u);
         }
       } else {
+        // slots jj < lim hold cached positions; the others (their rows are not this sequence's)
+        // count as 0, and position p's f32 V is added after them with its weight
+        const int lim = p - j0 - 32 * half;
 #pragma unroll
         for (int jj = 0; jj < 32; ++jj) {
-          const int jp = j0 + 32 * half + jj;
-          const float pj = pw[jj];
-          const float v0 = jp < p ? __uint_as_float(P.vv[jj] << 16) : (jp == p ? vc0 : 0.f);
-          const float v1 = jp < p ? __uint_as_float(P.vv[jj] & 0xffff0000u) : (jp == p ? vc1 : 0.f);
-          o0[jj & 1] += pj * v0;
-          o1[jj & 1] += pj * v1;
+          const uint32_t vj = jj < lim ? P.vv[jj] : 0u;
+          o0[jj & 1] += pw[jj] * __uint_as_float(vj << 16);
+          o1[jj & 1] += pw[jj] * __uint_as_float(vj & 0xffff0000u);
+        }
+        const float ep = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), p - j0));
+        if (half == ((p - j0) >> 5)) {
+          o0[0] += ep * vc0;
+          o1[0] += ep * vc1;
         }
       }
       float a0 = o0[0] + o0[1], a1 = o1[0] + o1[1];
@@ -827,13 +832,15 @@ __device__ __forceinline__ void att_compute(const Args& a, int l, const Item& it
   }
   wsync(sy, lane);
   MBD_T(wv == 0 && l == kTraceLayer, 10);
-  if (wv == 0) {   // merge of the blocks: softmax over all positions
-    float M = -INFINITY;
-    for (int b = 0; b < kBlocks; ++b) M = fmaxf(M, S.ml[b][0]);
+  if (wv == 0) {   // merge of the blocks: softmax over all positions (lane b < 8: block b's weight)
+    const float mb = lane < kBlocks ? S.ml[lane][0] : -INFINITY;
+    const float M = wave_max(mb);
+    const float fb = mb == -INFINITY ? 0.f : expf(mb - M);
     float num = 0.f, den = 0.f;
+#pragma unroll
     for (int b = 0; b < kBlocks; ++b) {
-      if (S.ml[b][0] == -INFINITY) continue;
-      const float f = expf(S.ml[b][0] - M);
+      if (__int_as_float(__builtin_amdgcn_readlane(__float_as_int(mb), b)) == -INFINITY) continue;
+      const float f = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(fb), b));
       num += f * S.o[b][lane];
       den += f * S.ml[b][1];
     }
