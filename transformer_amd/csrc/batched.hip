@@ -131,7 +131,7 @@ struct Args {
   int32_t* out;
   uint32_t* ctrl;
   uint64_t* keys;   // [2][kRows]
-  uint32_t* flags;  // [5 L + 2][kMaxGrid]
+  uint32_t* flags;  // [5 L + 2][kMaxGrid] (barrier 1 + 5 l, after QKV, is no longer used)
   // exchange vectors, one block per layer (each written once per step):
   //   h after O [kRows][d], h after down [kRows][d] (residual stream, packed input order),
   //   qkv [kRows][nqkv] (raw projections, packed row order), att [kRows][d] (packed input
@@ -918,7 +918,7 @@ __global__ __launch_bounds__(kThreads) void batch_step_kernel(Args a) {
     }
     grid_sync(a, sy, 0, epoch, wv, lane);
   }
-  AttPre pre;   // the first item's block of K/V rows, loaded while the QKV barrier is awaited
+  AttPre pre;   // the first item's block of K/V rows, requested while the item's q/k/v are polled
   AOp<kStepsD> A;
   int s0, s1;
   for (int l = 0; l < a.L; ++l) {
