@@ -97,6 +97,10 @@ constexpr int kFlagReps = MBD_FLAG_REPS;
 #ifndef MBD_BAR_SLEEP
 #define MBD_BAR_SLEEP 1
 #endif
+// s_sleep units between the two rounds of an attention item's q/k/v poll kept in flight (0: one round)
+#ifndef MBD_QKV_STAGGER
+#define MBD_QKV_STAGGER 16
+#endif
 // s_sleep units between the polls of an LDS counter (0: spin)
 #ifndef MBD_LDS_SLEEP
 #define MBD_LDS_SLEEP 1
@@ -406,16 +410,40 @@ __device__ __forceinline__ void poll_words(const uint64_t* const (&p)[N], uint32
   uint64_t w[N];
 #pragma unroll
   for (int i = 0; i < N; ++i) w[i] = ld_u64(p[i]);
+#if MBD_QKV_STAGGER > 0
+  // a second round in flight, issued about half a memory round trip after the first
+  uint64_t w2[N];
+  __builtin_amdgcn_s_sleep(MBD_QKV_STAGGER);
+#pragma unroll
+  for (int i = 0; i < N; ++i) w2[i] = ld_u64(p[i]);
+#endif
   uint32_t spins = 0;
   while (true) {
     bool ok = true;
 #pragma unroll
     for (int i = 0; i < N; ++i) ok = ok && uint32_t(w[i] >> 32) == epoch;
     if (__all(ok)) break;
+#if MBD_QKV_STAGGER > 0
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+      if (uint32_t(w[i] >> 32) != epoch) w[i] = ld_u64(p[i]);
+    ok = true;
+#pragma unroll
+    for (int i = 0; i < N; ++i) ok = ok && uint32_t(w2[i] >> 32) == epoch;
+    if (__all(ok)) {
+#pragma unroll
+      for (int i = 0; i < N; ++i) w[i] = w2[i];
+      break;
+    }
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+      if (uint32_t(w2[i] >> 32) != epoch) w2[i] = ld_u64(p[i]);
+#else
     if constexpr (MBD_BAR_SLEEP > 0) __builtin_amdgcn_s_sleep(MBD_BAR_SLEEP);
 #pragma unroll
     for (int i = 0; i < N; ++i)
       if (uint32_t(w[i] >> 32) != epoch) w[i] = ld_u64(p[i]);
+#endif
     if ((++spins & 255u) == 0 && (ld_u32(status) & kStTimeout)) break;
     if (spins > kSpinLimit) {
       if ((threadIdx.x & 63) == 0) atomicOr(status, kStTimeout);
