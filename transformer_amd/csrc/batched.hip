@@ -656,7 +656,6 @@ struct Item {
   float cs[kDh];        // RoPE at p: cos (32) then sin (32)
 };
 struct AttLds {
-  float raw[3][kDh];    // q, k, v as projected (packed pair order for q and k)
   float q[kDh], k[kDh], v[kDh];
   float p[kBlocks][64];
   float o[kBlocks][kDh];
@@ -749,30 +748,31 @@ __device__ __forceinline__ void att_compute(const Args& a, int l, const Item& it
     const uint64_t* const src[3] = {row + h * kDh, row + (a.H + g) * kDh, row + (a.H + a.KV + g) * kDh};
     float v[3];
     poll_words<3>(src, epoch, sy.status, v);
-#pragma unroll
-    for (int i = 0; i < 3; ++i) S.raw[i][lane] = v[i];
+    // RoPE (model.py:110-117) in this wave: packed pair (2i, 2i+1) = dims (i, i + 32); lanes 0-31
+    // rotate q's pair i = lane, lanes 32-63 k's pair i = lane - 32
+    const int i = lane & 31;
+    const float qa = __shfl(v[0], 2 * i), qb = __shfl(v[0], 2 * i + 1);
+    const float ka = __shfl(v[1], 2 * i), kb = __shfl(v[1], 2 * i + 1);
+    const float x0 = lane < 32 ? qa : ka, x1 = lane < 32 ? qb : kb;
+    const float c = it.cs[i], sn = it.cs[kDh / 2 + i];
+    const float r0 = x0 * c - x1 * sn, r1 = x0 * sn + x1 * c;
+    float* dst = lane < 32 ? S.q : S.k;
+    dst[i] = r0;
+    dst[i + kDh / 2] = r1;
+    S.v[lane] = v[2];
+    if (h % gs == 0) {   // the current position's K/V row, bf16 (model.py:212-215)
+      const int64_t crow = it.prow * kDh;
+      if (lane >= 32) {
+        kc[crow + i] = f2bf(r0);
+        kc[crow + i + kDh / 2] = f2bf(r1);
+      }
+      vc[crow + lane] = f2bf(v[2]);
+    }
     if (64 * wv <= p) att_load(a, l, it, wv, lane, P);   // this wave's block, after the poll
   }
   wsync(sy, lane);
   MBD_T(wv == 0 && l == kTraceLayer, 9);
   MBD_V(wv == 0 && l == kTraceLayer, 14, uint64_t(p));
-  if (tid < kDh) {   // RoPE (model.py:110-117): packed pair (2i, 2i+1) = dims (i, i + 32)
-    const int sel = tid >> 5, i = tid & 31;
-    const float c = it.cs[i], sn = it.cs[kDh / 2 + i];
-    const float x0 = S.raw[sel][2 * i], x1 = S.raw[sel][2 * i + 1];
-    float* dst = sel == 0 ? S.q : S.k;
-    dst[i] = x0 * c - x1 * sn;
-    dst[i + kDh / 2] = x0 * sn + x1 * c;
-  } else if (tid < 2 * kDh) {
-    S.v[tid - kDh] = S.raw[2][tid - kDh];
-  }
-  wsync(sy, lane);
-  if (h % gs == 0 && tid < 2 * kDh) {   // the current position's K/V row, bf16 (model.py:212-215)
-    const int64_t row = it.prow;
-    const int c = tid & (kDh - 1);
-    if (tid < kDh) kc[row * kDh + c] = f2bf(S.k[c]);
-    else vc[row * kDh + c] = f2bf(S.v[c]);
-  }
   const int dp = lane & 31, half = lane >> 5;
   for (int b = wv; b < kBlocks; b += kWorkers) {
     const int j0 = 64 * b, j = j0 + lane;
@@ -861,6 +861,12 @@ __device__ __forceinline__ void att_compute(const Args& a, int l, const Item& it
   wsync(sy, lane);
   MBD_T(wv == 0 && l == kTraceLayer, 10);
   if (wv == 0) {   // merge of the blocks: softmax over all positions (lane b < 8: block b's weight)
+    float ob[kBlocks], lb[kBlocks];   // every LDS read first (blocks past p hold zeros)
+#pragma unroll
+    for (int b = 0; b < kBlocks; ++b) {
+      ob[b] = S.o[b][lane];
+      lb[b] = S.ml[b][1];
+    }
     const float mb = lane < kBlocks ? S.ml[lane][0] : -INFINITY;
     const float M = wave_max(mb);
     const float fb = mb == -INFINITY ? 0.f : expf(mb - M);
@@ -869,8 +875,8 @@ __device__ __forceinline__ void att_compute(const Args& a, int l, const Item& it
     for (int b = 0; b < kBlocks; ++b) {
       if (__int_as_float(__builtin_amdgcn_readlane(__float_as_int(mb), b)) == -INFINITY) continue;
       const float f = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(fb), b));
-      num += f * S.o[b][lane];
-      den += f * S.ml[b][1];
+      num += f * ob[b];
+      den += f * lb[b];
     }
     st_split(x_att(a, l) + int64_t(m) * plane_ld(a.d) + perm_pos(h * kDh + lane, a.d), int64_t(kRows) * plane_ld(a.d),
              num / den);
