@@ -148,9 +148,10 @@ struct Args {
 // ---------------------------------------------------------------- profiling build (-DMBD_TRACE)
 // Lane 0 of worker wave 0 of every workgroup stamps s_memrealtime (100 MHz) at phase
 // boundaries: slot 8 p + k of layer kTraceLayer's phase p (0 QKV .. 4 DN): k = 0 phase start,
-// 1 inputs ready, 2 weights landed, 3 summed, 4 outputs stored, 5 barrier passed; slot 40 + 5 l + p:
+// 1 inputs ready, 2 weights landed, 3 summed, 4 outputs stored, 5 barrier passed, 6 own flag set
+// (after the workgroup's stores completed); slot 40 + 5 l + p:
 // barrier p of layer l passed; slot 168: logits done; 169: final barrier.  Attention of layer
-// kTraceLayer (first item): slot 9 q/k/v polled, 14 the item's position (a value), 15 wave 1's
+// kTraceLayer (first item): slot 9 q/k/v polled, 7 the item's position (a value), 15 wave 1's
 // scores, 160 + w wave w's block done, 10 the waves met, 11 output stored.  The loader stamps slot
 // 176 + p when the weights of layer kTraceLayer's phase p are issued and 184 + p when they landed.
 constexpr int kTraceLayer = 10;
@@ -359,6 +360,7 @@ __device__ __forceinline__ void grid_arrive(const Args& a, Sync& sy, int b, uint
   __builtin_amdgcn_s_waitcnt(0);
   wsync(sy, lane);
   if (wv == 0 && lane < kFlagReps) st_u32(a.flags + (int64_t(b) * kFlagReps + lane) * kMaxGrid + blockIdx.x, epoch);
+  MBD_T(wv == 0 && b >= 1 + 5 * kTraceLayer && b < 6 + 5 * kTraceLayer, 8 * (b - 1 - 5 * kTraceLayer) + 6);
 }
 // Four consecutive flags with one agent-scope 16-byte load (each 4-byte flag is read whole).
 __device__ __forceinline__ uint4 ld_flags4(const uint32_t* p) {
@@ -772,7 +774,7 @@ __device__ __forceinline__ void att_compute(const Args& a, int l, const Item& it
   }
   wsync(sy, lane);
   MBD_T(wv == 0 && l == kTraceLayer, 9);
-  MBD_V(wv == 0 && l == kTraceLayer, 14, uint64_t(p));
+  MBD_V(wv == 0 && l == kTraceLayer, 7, uint64_t(p));
   const int dp = lane & 31, half = lane >> 5;
   for (int b = wv; b < kBlocks; b += kWorkers) {
     const int j0 = 64 * b, j = j0 + lane;
