@@ -462,6 +462,14 @@ struct Job {
   int K, g0, ng;          // groups g0 .. g0 + ng - 1 of 8 rows, K inputs each
 };
 
+// Workgroups that run the QKV phase: the upper half of the grid when that keeps every job within
+// its tiles, so that the first half, where the attention items sit (items deal from workgroup
+// 0), has no QKV job and requests its items' cached K/V rows as soon as the layer starts.
+__host__ __device__ __forceinline__ int qkv_wgs(int groups, int G) {
+  const int h = G / 2;
+  return (h > 0 && (groups + h - 1) / h <= 2 * kTilesD) ? h : G;
+}
+
 // Layer phase ph (0 QKV, 1 O, 2 GU, 3 DN) of layer l for workgroup wg.
 __device__ __forceinline__ Job layer_job(const Args& a, int l, int ph, int wg, int G) {
   const uint16_t* wl = a.w + int64_t(l) * a.layer_elems;
@@ -477,7 +485,14 @@ __device__ __forceinline__ Job layer_job(const Args& a, int l, int ph, int wg, i
     j.base = wl + a.off_dn; j.K = a.ff; rows = a.d;
   }
   int g1;
-  split(rows / 8, G, wg, j.g0, g1);
+  const int nq = qkv_wgs(rows / 8, G);
+  if (ph == 0 && wg < G - nq) {   // QKV runs on the last nq workgroups only
+    j.g0 = 0;
+    j.ng = 0;
+    return j;
+  }
+  if (ph == 0) split(rows / 8, nq, wg - (G - nq), j.g0, g1);
+  else split(rows / 8, G, wg, j.g0, g1);
   j.ng = g1 - j.g0;
   return j;
 }
@@ -1206,7 +1221,8 @@ static Plan make_plan(const msd_config* c, int G) {
   Plan p;
   const int d = c->d_model, ff = c->d_ff, nqkv = (c->n_heads + 2 * c->n_kv_heads) * kDh;
   auto groups_per_wg = [&](int rows) { return (rows / 8 + G - 1) / G; };
-  const int gq = groups_per_wg(nqkv), go = groups_per_wg(d), ggu = groups_per_wg(2 * ff), gdn = groups_per_wg(d);
+  const int nqw = qkv_wgs(nqkv / 8, G);
+  const int gq = (nqkv / 8 + nqw - 1) / nqw, go = groups_per_wg(d), ggu = groups_per_wg(2 * ff), gdn = groups_per_wg(d);
   if (std::max(std::max(gq, go), ggu) > 2 * kTilesD || gdn > 2 * kTilesF) return p;
   {   // (sequence, head) item slots per workgroup (att_setup deals 8 gs ceil(M KV / 8) slots)
     const int gs = c->n_heads / c->n_kv_heads, ni = 8 * gs * ((kRows * c->n_kv_heads + 7) / 8);
