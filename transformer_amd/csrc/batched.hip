@@ -887,10 +887,10 @@ __device__ __forceinline__ void att_compute(const Args& a, int l, const Item& it
     const float mb = lane < kBlocks ? S.ml[lane][0] : -INFINITY;
     const float M = wave_max(mb);
     const float fb = mb == -INFINITY ? 0.f : expf(mb - M);
+    // blocks past p (max -inf) have weight 0 and hold zeros: adding their 0 changes no sum
     float num = 0.f, den = 0.f;
 #pragma unroll
     for (int b = 0; b < kBlocks; ++b) {
-      if (__int_as_float(__builtin_amdgcn_readlane(__float_as_int(mb), b)) == -INFINITY) continue;
       const float f = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(fb), b));
       num += f * ob[b];
       den += f * lb[b];
