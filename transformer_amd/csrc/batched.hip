@@ -110,6 +110,12 @@ constexpr int kFlagReps = MBD_FLAG_REPS;
 #define MBD_LOADER_PRIO 1
 #endif
 constexpr int kLoaderPrio = MBD_LOADER_PRIO;
+// The tied logits' weight rows: streamed by the worker waves straight into registers (1), or by
+// the loader through the LDS ring (0)
+#ifndef MBD_LOGITS_REG
+#define MBD_LOGITS_REG 1
+#endif
+constexpr bool kLogitsReg = MBD_LOGITS_REG != 0;
 // the worker wave that polls an attention item's q, k and v; it requests its block of cached K/V
 // rows only afterwards (a wave's loads complete in order: polls issued behind ~40 K/V loads wait
 // for them), while the other waves request theirs at once
@@ -547,9 +553,11 @@ __device__ __forceinline__ void loader(const Args& a, Sync& sy, uint8_t* slots, 
       const Job jb = layer_job(a, l, ph, wg, G);
       if (jb.ng > 0) load(jb, 4 * l + ph);
     }
-  int t0, t1;
-  split(a.V / 8, G, wg, t0, t1);
-  for (int c = t0; c < t1; c += a.tchunk) load(Job{a.outp, a.d, c, min(a.tchunk, t1 - c)}, -1);
+  if constexpr (!kLogitsReg) {
+    int t0, t1;
+    split(a.V / 8, G, wg, t0, t1);
+    for (int c = t0; c < t1; c += a.tchunk) load(Job{a.outp, a.d, c, min(a.tchunk, t1 - c)}, -1);
+  }
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
   landed(j);
 }
@@ -902,6 +910,24 @@ __device__ __forceinline__ void att_compute(const Args& a, int l, const Item& it
   wsync(sy, lane);   // the LDS state is reused by the next item
 }
 
+// The B fragments of vocabulary groups c .. c + 3 (two 16-column tiles) for one worker wave's K
+// steps s0 .. s0 + ns - 1, straight from the tied embedding rows (lane: row 8 g + (lane & 7) of
+// group g = c + 2 t + ((lane & 15) >> 3), inputs 32 s + 8 (lane >> 4) .. + 7); groups past t1
+// re-read the last one (the loads stay unconditional) and are never stored.
+__device__ __forceinline__ void logit_frags(const Args& a, int c, int t1, int s0, int ns, int lane,
+                                            uint4 (&b)[kStepsD][2]) {
+  const int r = lane & 7, gq = (lane & 15) >> 3, q = lane >> 4;
+#pragma unroll
+  for (int i = 0; i < kStepsD; ++i) {
+    const int st = s0 + min(i, ns - 1);
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int g = min(c + 2 * t + gq, t1 - 1);
+      b[i][t] = *reinterpret_cast<const uint4*>(a.outp + int64_t(8 * g + r) * a.d + 32 * st + 8 * q);
+    }
+  }
+}
+
 // ---------------------------------------------------------------- the step
 // Epilogue of a phase that updates the residual stream (O, down, and the embedding): element e
 // of sequence m becomes h1 (kept by the caller in its workgroup's LDS), h1 * scale goes to the
@@ -1119,6 +1145,7 @@ __global__ __launch_bounds__(kThreads) void batch_step_kernel(Args a) {
         lds_bump(sy.consumed, lane);
         ++j;
       }
+      if (kLogitsReg && l + 1 == a.L) break;   // the last barrier follows the loop
       grid_sync(a, sy, bl + 4, epoch, wv, lane);
       MBD_T(wv_ == 0, 40 + 5 * l + 4);
       MBD_T(wv_ == 0 && l == kTraceLayer, 37);
@@ -1127,6 +1154,17 @@ __global__ __launch_bounds__(kThreads) void batch_step_kernel(Args a) {
   // ---- final RMSNorm, tied logits and the argmax keys
   int t0, t1;
   split(a.V / 8, G, wg, t0, t1);
+  uint4 lfirst[kStepsD][2];   // the first logits chunk's B fragments
+  if constexpr (kLogitsReg) {
+    // the last layer's down barrier: every wave but the polling one requests its first chunk
+    // of logit rows before waiting
+    const int bl = 5 * a.L;
+    grid_arrive(a, sy, bl, epoch, wv_, lane_);
+    split(a.d / 32, kWorkers, wv_, s0, s1);
+    if (wv_ != 0 && t1 > t0) logit_frags(a, t0, t1, s0, s1 - s0, lane_, lfirst);
+    grid_wait(a, sy, bl, epoch, wv_, lane_);
+    MBD_T(wv_ == 0, 40 + 5 * (a.L - 1) + 4);
+  }
   if (t1 > t0) {
     const int lane = opaque(lane_), wv = opaque(wv_);
     split(a.d / 32, kWorkers, wv, s0, s1);
@@ -1134,7 +1172,52 @@ __global__ __launch_bounds__(kThreads) void batch_step_kernel(Args a) {
     if (wv == 0) row_inv(x_ssd(a, a.L - 1), a.d, s_inv, lane);
     const int m = ((wv * 64 + lane) >> 4) & 7;   // the same sequence for every output of this thread
     uint64_t best = 0;
-    for (int c = t0; c < t1; c += a.tchunk) {
+    if constexpr (kLogitsReg) {
+      // chunks of 4 groups (two 16-column tiles), each worker wave streaming the B fragments of
+      // its K steps into registers one chunk ahead (the first chunk requested before the last
+      // barrier by every wave but the polling one).  The partial tiles meet in slot 0 of the
+      // ring, which no DMA writes any more (every layer job has been consumed).
+      const int ns = s1 - s0;
+      f32x4* red = reinterpret_cast<f32x4*>(slots);
+      auto load_b = [&](int c, uint4 (&b)[kStepsD][2]) { logit_frags(a, c, t1, s0, ns, lane, b); };
+      auto take = [&](const uint4 (&b)[kStepsD][2], int c) {
+        f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+        for (int i = 0; i < kStepsD; ++i)
+          if (i < ns) {
+            const bf16x8 av = __builtin_bit_cast(bf16x8, A.f[i]);
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+              acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(bf16x8, b[i][t]), acc[t], 0, 0, 0);
+          }
+        wsync(sy, lane);   // every wave has read the previous chunk's tiles
+#pragma unroll
+        for (int t = 0; t < 2; ++t) red[(wv * 2 + t) * 64 + lane] = acc[t];
+        wsync(sy, lane);
+        const int ng = min(4, t1 - c);
+        for (int i = wv * 64 + lane; i < 256 && wv * 64 + lane < kEpi; i += kEpi) {
+          const int t = i >> 7, n = i & 15;
+          if (2 * t + (n >> 3) < ng && m < M) {
+            const float y = tile_out(red, 2, t, m, n) * s_inv[m];
+            const int v = 8 * (c + 2 * t + (n >> 3)) + (n & 7);
+            a.logits[int64_t(m) * a.V + v] = y;
+            const uint64_t key = argmax_key(y, v);
+            best = key > best ? key : best;
+          }
+        }
+      };
+      uint4 (&ba)[kStepsD][2] = lfirst;
+      uint4 bb[kStepsD][2];
+      if (wv == 0) load_b(t0, ba);
+      for (int c = t0; c < t1; c += 8) {
+        load_b(c + 4, bb);
+        take(ba, c);
+        if (c + 4 >= t1) break;
+        load_b(c + 8, ba);
+        take(bb, c + 4);
+      }
+    }
+    for (int c = t0; !kLogitsReg && c < t1; c += a.tchunk) {
       const Job jb{a.outp, a.d, c, min(a.tchunk, t1 - c)};
       int tiles;
       const f32x4* red = run_job(a, jb, j, slots, A, s0, s1 - s0, sy, wv, lane, tiles);
