@@ -303,6 +303,21 @@ __device__ __forceinline__ float wave_sum(float v) {
   v += dpp<0x143, 0xc>(v, 0.f);
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
+// The sum over each group of 8 consecutive lanes, in every lane of the group: the butterfly
+// (lane ^ 1, ^ 2, ^ 4) with DPP quad permutes and the half-row mirror instead of LDS permutes
+// (after the two quad steps the lanes of a quad hold the same value, so the mirror adds the
+// other quad's sum exactly as lane ^ 4 would)
+__device__ __forceinline__ float sum8_lanes(float v) {
+  v += dpp<0xB1, 0xf>(v, 0.f);    // quad_perm [1, 0, 3, 2]: lane ^ 1
+  v += dpp<0x4E, 0xf>(v, 0.f);    // quad_perm [2, 3, 0, 1]: lane ^ 2
+  v += dpp<0x141, 0xf>(v, 0.f);   // row_half_mirror: the other quad of the 8
+  return v;
+}
+// v of this lane plus v of lane ^ 32 (gfx950's row-swapping permute; no LDS traffic)
+__device__ __forceinline__ float add_halves(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
 __device__ __forceinline__ float wave_max(float v) {
   v = fmaxf(v, dpp<0x111, 0xf>(v, -INFINITY));
   v = fmaxf(v, dpp<0x112, 0xf>(v, -INFINITY));
@@ -597,9 +612,7 @@ __device__ __forceinline__ void row_inv(const float* ss, int K, float* inv, int 
 #pragma unroll
   for (int k = 0; k < kStepsD; ++k)
     if (k < nl) v += ((u[k].x + u[k].y) + (u[k].z + u[k].w));
-  v += __shfl_xor(v, 1);
-  v += __shfl_xor(v, 2);
-  v += __shfl_xor(v, 4);
+  v = sum8_lanes(v);
   if (c == 0) inv[r] = 1.f / sqrtf(v / float(K) + 1e-5f);
 }
 
@@ -868,8 +881,8 @@ __device__ __forceinline__ void att_compute(const Args& a, int l, const Item& it
         }
       }
       float a0 = o0[0] + o0[1], a1 = o1[0] + o1[1];
-      a0 += __shfl_xor(a0, 32);   // the two halves of the block
-      a1 += __shfl_xor(a1, 32);
+      a0 = add_halves(a0);   // the two halves of the block
+      a1 = add_halves(a1);
       if (half == 0) {
         S.o[b][2 * dp] = a0;
         S.o[b][2 * dp + 1] = a1;
@@ -939,9 +952,7 @@ __device__ __forceinline__ void put_residual(const Args& a, bool act, int m, int
   const int64_t o = int64_t(m) * plane_ld(a.d) + perm_pos(e, a.d);
   if (act) st_split(planes + o, int64_t(kRows) * plane_ld(a.d), h1 * scale);
   float v = act ? h1 * h1 : 0.f;
-  v += __shfl_xor(v, 1);
-  v += __shfl_xor(v, 2);
-  v += __shfl_xor(v, 4);
+  v = sum8_lanes(v);
   if (act && (n & 7) == 0) st_f(ss + m * (a.d / 8) + grp, v);
 }
 
