@@ -89,6 +89,17 @@ template <int CTRL, int ROWMASK>
 __device__ __forceinline__ float dpp(float v, float fill) {
   return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(fill), __float_as_int(v), CTRL, ROWMASK, 0xf, false));
 }
+// The sum over each row of 16 lanes, in every lane of the row: the butterfly lane ^ 1, ^ 2, ^ 4,
+// ^ 8 with DPP (quad permutes, then the half-row and row mirrors: after each step the lanes of a
+// group hold the same value, so a mirror adds the other group's sum exactly as the xor would)
+// instead of LDS permutes
+__device__ __forceinline__ float sum16_lanes(float v) {
+  v += dpp<0xB1, 0xf>(v, 0.f);    // quad_perm [1, 0, 3, 2]: lane ^ 1
+  v += dpp<0x4E, 0xf>(v, 0.f);    // quad_perm [2, 3, 0, 1]: lane ^ 2
+  v += dpp<0x141, 0xf>(v, 0.f);   // row_half_mirror: the other quad of the 8
+  v += dpp<0x140, 0xf>(v, 0.f);   // row_mirror: the other 8 of the row
+  return v;
+}
 __device__ __forceinline__ float wave_sum(float v) {
   v += dpp<0x111, 0xf>(v, 0.f);
   v += dpp<0x112, 0xf>(v, 0.f);
@@ -427,10 +438,7 @@ __global__ __launch_bounds__(256) void mx_gemm_rows(GemmArgs g) {
       float sum = 0.f;
 #pragma unroll
       for (int j = 0; j < kSq; ++j) sum += int(threadIdx.x & 15) + 16 * j < g.nssq ? sq[rt][j] : 0.f;
-      sum += __shfl_xor(sum, 1);
-      sum += __shfl_xor(sum, 2);
-      sum += __shfl_xor(sum, 4);
-      sum += __shfl_xor(sum, 8);
+      sum = sum16_lanes(sum);
       if ((threadIdx.x & 15) == 0) rrms[16 * rt + (threadIdx.x >> 4)] = sqrtf(sum / float(g.K) + 1e-5f);
     }
   }
@@ -461,10 +469,7 @@ __global__ __launch_bounds__(256) void mx_gemm_rows(GemmArgs g) {
       }
     }
     if constexpr (EPI == kEpiResidNorm) {   // the row's 16 CT columns: 16 lanes, in a fixed order
-      hsq += __shfl_xor(hsq, 1);
-      hsq += __shfl_xor(hsq, 2);
-      hsq += __shfl_xor(hsq, 4);
-      hsq += __shfl_xor(hsq, 8);
+      hsq = sum16_lanes(hsq);
       const int row = m0 + 4 * (lane >> 4) + wv;
       if ((lane & 15) == 0 && row < g.M) g.e.ssq[int64_t(row) * C + c] = hsq;
     }
